@@ -1,0 +1,124 @@
+"""ctypes binding of libbeam_engine_amd.so (the C ABI in include/beam_engine_amd.h).
+
+torch is imported first so that the library binds to the HIP runtime torch
+already loaded (same SONAME), i.e. one runtime per process.  There is no CPU
+fallback: if the library is missing every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the process's HIP runtime before the library)
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libbeam_engine_amd.so")
+
+BE_F32, BE_F16, BE_BF16 = 0, 1, 2
+BE_OK, BE_ERR_INVALID, BE_ERR_HIP, BE_ERR_CAPACITY, BE_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
+BE_PLAN_FORCE_VALU = 1
+
+_DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dt}; expected float32, float16 or bfloat16") from None
+
+
+class BeLevel(ctypes.Structure):
+    _fields_ = [
+        ("qo_indptr", ctypes.c_void_p),
+        ("kv_indptr", ctypes.c_void_p),
+        ("kv_indices", ctypes.c_void_p),
+        ("last_page_len", ctypes.c_void_p),
+        ("num_groups", ctypes.c_int32),
+    ]
+
+
+class BeAttnPlanInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "num_items", "num_part_rows", "num_merge", "num_queries", "num_qo_heads", "num_kv_heads",
+        "head_dim", "page_size", "num_pages", "dtype", "kernel", "tile_rows", "chunk_tokens",
+        "plan_ints", "off_items", "off_qindex", "off_pages", "off_merge_q", "off_merge_ptr",
+        "off_merge_rows")] + [
+        ("partial_bytes", ctypes.c_int64),
+        ("kv_bytes", ctypes.c_int64),
+        ("qo_bytes", ctypes.c_int64),
+        ("flops", ctypes.c_double),
+    ]
+
+
+EXPORTS = (
+    "be_version", "be_last_error", "be_kv_append", "be_page_copy", "be_attn_plan", "be_attn_run",
+    "be_merge_states", "be_beam_topk_workspace_bytes", "be_beam_topk",
+)
+
+_lib = None
+
+
+class HipLibraryMissing(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise HipLibraryMissing if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipLibraryMissing(
+            f"{LIB_PATH} is missing: build it with `python -m beam_engine_amd.build` "
+            "(beam_engine_amd has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.be_version.restype = i32
+    lib.be_last_error.restype = ctypes.c_char_p
+    lib.be_kv_append.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i64, i64, i32, vp, vp]
+    lib.be_page_copy.argtypes = [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp]
+    lib.be_attn_plan.argtypes = [ctypes.POINTER(BeLevel), i32, i32, i32, i32, i32, i32, i32, i32, i32, i32,
+                                 vp, i64, ctypes.POINTER(BeAttnPlanInfo)]
+    lib.be_attn_run.argtypes = [ctypes.POINTER(BeAttnPlanInfo), vp, vp, vp, i64, i64, vp, vp, i64, i64, vp,
+                                ctypes.c_float, vp]
+    lib.be_merge_states.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]
+    lib.be_beam_topk_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.be_beam_topk_workspace_bytes.restype = i64
+    lib.be_beam_topk.argtypes = [vp, i32, i32, i32, i64, ctypes.c_float, i32, vp, i32, vp, vp, vp, vp, vp,
+                                 vp, i64, vp]
+    for name in EXPORTS:
+        if name not in ("be_version", "be_last_error", "be_beam_topk_workspace_bytes"):
+            getattr(lib, name).restype = i32
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a be_status to the reference's exception types."""
+    if rc == BE_OK:
+        return
+    msg = load().be_last_error().decode(errors="replace")
+    text = f"{what}: {msg}"
+    if rc == BE_ERR_INVALID:
+        raise ValueError(text)
+    if rc == BE_ERR_CAPACITY:
+        raise MemoryError(text)
+    if rc == BE_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise RuntimeError(text)
+
+
+def ptr(t) -> int:
+    """Device (or host) address of a tensor, or 0 for None."""
+    return 0 if t is None else t.data_ptr()
+
+
+def stream_ptr(device=None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a HIP device tensor (got {t.device}); there is no CPU path")

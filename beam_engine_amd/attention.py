@@ -1,0 +1,306 @@
+"""Decode attention wrappers over the HIP work-list kernels.
+
+``MultiLevelCascadeAttentionWrapper`` keeps the interface the reference uses
+(flashinfer.cascade.MultiLevelCascadeAttentionWrapper: constructed per step
+with a workspace, ``plan(...)`` once per step, ``run(q, kv_layer)`` once per
+layer -- src/beam_engine/models/modeling_llama.py:732-755, 321-367).
+``BatchDecodeWithPagedKVCacheWrapper`` is the flat strategy: one level, one
+group per query.  Both share one plan format and the same kernels.
+
+Semantics (every level, every group): o = softmax(sm_scale * q K^T) V over the
+group's valid tokens, query head h reading KV head h // (Hq / Hkv); levels are
+merged by log-sum-exp.  ``run(..., return_lse=True)`` returns the natural-log
+lse (FlashInfer returns base 2; the reference never reads it).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+
+_WS_ALIGN = 256
+
+
+def _as_i32(x) -> np.ndarray:
+    if isinstance(x, torch.Tensor):
+        x = x.detach()
+        if x.is_cuda:
+            x = x.cpu()
+        x = x.numpy()
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+class _Staging:
+    """Pinned host staging for plans (one per device), reused across wrappers.
+
+    The buffer is only rewritten after the previous upload from it finished."""
+
+    _lock = threading.Lock()
+    _by_dev = {}
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.buf = torch.empty(1 << 16, dtype=torch.int32, pin_memory=True)
+        self.event: Optional[torch.cuda.Event] = None
+
+    @classmethod
+    def get(cls, device: torch.device) -> "_Staging":
+        key = (device.type, device.index)
+        with cls._lock:
+            st = cls._by_dev.get(key)
+            if st is None:
+                st = cls._by_dev[key] = _Staging(device)
+            return st
+
+    def acquire(self, ints: int) -> torch.Tensor:
+        if self.event is not None:
+            self.event.synchronize()
+            self.event = None
+        if self.buf.numel() < ints:
+            self.buf = torch.empty(max(ints, 2 * self.buf.numel()), dtype=torch.int32, pin_memory=True)
+        return self.buf
+
+
+def _num_cus(device: torch.device) -> int:
+    try:
+        return int(torch.cuda.get_device_properties(device).multi_processor_count)
+    except Exception:   # noqa: BLE001 - properties are a sizing hint only
+        return 256
+
+
+class PlanStats:
+    """Algorithmic work of a plan (for roofline reporting)."""
+
+    def __init__(self, info: _lib.BeAttnPlanInfo):
+        self.kv_bytes = int(info.kv_bytes)
+        self.qo_bytes = int(info.qo_bytes)
+        self.flops = float(info.flops)
+        self.num_items = int(info.num_items)
+        self.num_part_rows = int(info.num_part_rows)
+        self.num_merge = int(info.num_merge)
+        self.kernel = "mfma" if info.kernel == 1 else "valu"
+        self.chunk_tokens = int(info.chunk_tokens)
+
+    @property
+    def bytes(self) -> int:
+        return self.kv_bytes + self.qo_bytes
+
+
+class _PagedPlanner:
+    """Shared plan/run machinery for the cascade and flat wrappers."""
+
+    def __init__(self, workspace: torch.Tensor, kv_layout: str):
+        if kv_layout != "NHD":
+            raise ValueError(f"kv_layout {kv_layout!r}: only 'NHD' ([P, 2, page, Hkv, D]) is supported")
+        if not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8:
+            raise ValueError("workspace buffer must be a uint8 tensor")
+        _lib.require_device(workspace, "workspace buffer")
+        self._ws = workspace
+        self._info: Optional[_lib.BeAttnPlanInfo] = None
+        self._plan_dev: Optional[torch.Tensor] = None
+        self._partials: Optional[torch.Tensor] = None
+        self._max_page = -1
+        self._sm_scale = 1.0
+        self._dtype: Optional[torch.dtype] = None
+        self._force_valu = False
+
+    # ---------------------------------------------------------------- plan
+    def _plan_levels(self, qo: Sequence, kvp: Sequence, kvi: Sequence, lpl: Sequence, num_qo_heads: int,
+                     num_kv_heads: int, head_dim: int, page_size: int, sm_scale: Optional[float],
+                     q_data_type, num_queries: Optional[int] = None) -> None:
+        lib = _lib.load()
+        if not (len(qo) == len(kvp) == len(kvi) == len(lpl)):
+            raise ValueError("per-level index lists must have the same length")
+        qo = [_as_i32(x) for x in qo]
+        kvp = [_as_i32(x) for x in kvp]
+        kvi = [_as_i32(x) for x in kvi]
+        lpl = [_as_i32(x) for x in lpl]
+        levels = (_lib.BeLevel * max(1, len(qo)))()
+        max_page = -1
+        nq = 0
+        for i, (a, b, c, d) in enumerate(zip(qo, kvp, kvi, lpl)):
+            ng = len(a) - 1
+            if ng < 0 or len(b) != ng + 1 or len(d) != ng:
+                raise ValueError(f"level {i}: qo_indptr / kv_indptr / last_page_len lengths disagree")
+            if ng > 0 and len(c) < int(b[-1]):
+                raise ValueError(f"level {i}: kv_indices shorter than kv_indptr[-1]")
+            levels[i] = _lib.BeLevel(a.ctypes.data, b.ctypes.data, c.ctypes.data if len(c) else 0,
+                                     d.ctypes.data, ng)
+            if len(c):
+                if int(c.min()) < 0:
+                    raise ValueError(f"level {i}: negative page index")
+                max_page = max(max_page, int(c.max()))
+            if ng > 0:
+                nq = max(nq, int(a[-1]))
+        if num_queries is not None:
+            nq = max(nq, int(num_queries))
+        if isinstance(q_data_type, str):
+            q_data_type = getattr(torch, q_data_type)
+        dt = _lib.dtype_code(q_data_type)
+        flags = _lib.BE_PLAN_FORCE_VALU if self._force_valu else 0
+        staging = _Staging.get(self._ws.device)
+        info = _lib.BeAttnPlanInfo()
+        cap = staging.buf.numel()
+        while True:
+            buf = staging.acquire(cap)
+            rc = lib.be_attn_plan(levels, len(qo), nq, num_qo_heads, num_kv_heads, head_dim, page_size,
+                                  max(max_page + 1, 1), dt, flags, _num_cus(self._ws.device),
+                                  buf.data_ptr(), buf.numel(), ctypes.byref(info))
+            if rc == _lib.BE_ERR_CAPACITY:
+                cap = 2 * buf.numel()
+                continue
+            _lib.check(rc, "attention plan")
+            break
+        plan_bytes = int(info.plan_ints) * 4
+        part_off = (plan_bytes + _WS_ALIGN - 1) // _WS_ALIGN * _WS_ALIGN
+        need = part_off + int(info.partial_bytes)
+        if need > self._ws.numel():
+            raise MemoryError(f"attention plan needs {need} workspace bytes, buffer has {self._ws.numel()}")
+        ws_i32 = self._ws[:plan_bytes].view(torch.int32)
+        ws_i32.copy_(buf[: info.plan_ints], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        staging.event = ev
+        self._plan_dev = ws_i32
+        self._partials = self._ws[part_off:need] if info.partial_bytes else None
+        self._info = info
+        self._max_page = max_page
+        self._sm_scale = float(head_dim ** -0.5 if sm_scale is None else sm_scale)
+        self._dtype = q_data_type
+
+    # ---------------------------------------------------------------- run
+    def _run(self, q: torch.Tensor, kv: torch.Tensor, out: Optional[torch.Tensor], return_lse: bool):
+        info = self._info
+        if info is None:
+            raise RuntimeError("plan() must be called before run()")
+        lib = _lib.load()
+        _lib.require_device(q, "q")
+        _lib.require_device(kv, "paged_kv_cache")
+        hq, hkv, d, ps = info.num_qo_heads, info.num_kv_heads, info.head_dim, info.page_size
+        if q.dim() != 3 or q.shape[1] != hq or q.shape[2] != d:
+            raise ValueError(f"q must be [N, {hq}, {d}], got {tuple(q.shape)}")
+        if q.shape[0] < info.num_queries:
+            raise ValueError(f"q has {q.shape[0]} rows, plan covers {info.num_queries} queries")
+        if kv.dim() != 5 or kv.shape[1] != 2 or kv.shape[2] != ps or kv.shape[3] != hkv or kv.shape[4] != d:
+            raise ValueError(f"paged_kv_cache must be [P, 2, {ps}, {hkv}, {d}], got {tuple(kv.shape)}")
+        if not kv.is_contiguous():
+            raise ValueError("paged_kv_cache must be contiguous")
+        if kv.shape[0] <= self._max_page:
+            raise ValueError(f"plan references page {self._max_page}, cache has {kv.shape[0]} pages")
+        if q.dtype != self._dtype or kv.dtype != self._dtype:
+            raise ValueError(f"q ({q.dtype}) and cache ({kv.dtype}) must match the planned dtype {self._dtype}")
+        if q.stride(2) != 1 or (q.data_ptr() % 16) or (q.stride(0) * q.element_size()) % 16 or \
+                (q.stride(1) * q.element_size()) % 16:
+            q = q.contiguous()
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+            raise ValueError("out must match q's shape and dtype with a contiguous head_dim")
+        elif (out.data_ptr() % 16) or (out.stride(0) * out.element_size()) % 16 or \
+                (out.stride(1) * out.element_size()) % 16:
+            raise ValueError("out must be 16-byte aligned in every row (vector stores)")
+        lse = torch.empty((q.shape[0], hq), dtype=torch.float32, device=q.device) if return_lse else None
+        rc = lib.be_attn_run(ctypes.byref(info), self._plan_dev.data_ptr(), _lib.ptr(self._partials),
+                             q.data_ptr(), q.stride(0), q.stride(1), kv.data_ptr(), out.data_ptr(),
+                             out.stride(0), out.stride(1), _lib.ptr(lse), self._sm_scale,
+                             _lib.stream_ptr(q.device))
+        _lib.check(rc, "attention run")
+        return (out, lse) if return_lse else out
+
+    @property
+    def stats(self) -> PlanStats:
+        if self._info is None:
+            raise RuntimeError("no plan")
+        return PlanStats(self._info)
+
+
+class MultiLevelCascadeAttentionWrapper(_PagedPlanner):
+    """Cascade decode attention (drop-in for the FlashInfer wrapper the
+    reference builds per step, models/modeling_llama.py:732-755)."""
+
+    def __init__(self, num_levels: int, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD"):
+        super().__init__(float_workspace_buffer, kv_layout)
+        if num_levels < 1:
+            raise ValueError("num_levels must be >= 1")
+        self.num_levels = num_levels
+
+    def plan(self, qo_indptr_arr: List, paged_kv_indptr_arr: List, paged_kv_indices_arr: List,
+             paged_kv_last_page_len: List, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+             page_size: int, causal: bool = False, pos_encoding_mode: str = "NONE",
+             use_fp16_qk_reduction: bool = False, sm_scale: Optional[float] = None,
+             window_left: int = -1, logits_soft_cap: Optional[float] = None,
+             rope_scale: Optional[float] = None, rope_theta: Optional[float] = None,
+             q_data_type="float16", kv_data_type=None) -> None:
+        if len(qo_indptr_arr) != self.num_levels:
+            raise ValueError(f"wrapper has {self.num_levels} levels, plan got {len(qo_indptr_arr)}")
+        if pos_encoding_mode != "NONE":
+            raise NotImplementedError("RoPE is applied before attention (pos_encoding_mode='NONE' only)")
+        if window_left not in (-1, None) or logits_soft_cap not in (None, 0.0):
+            raise NotImplementedError("sliding window / soft cap are not part of the decode path")
+        if kv_data_type is not None and kv_data_type != q_data_type:
+            raise NotImplementedError("q and KV must share one dtype")
+        if causal:
+            # causal applies to the last level only; with one query per group
+            # there it masks nothing (each query is the newest position).
+            last = _as_i32(qo_indptr_arr[-1])
+            if len(last) > 1 and int(np.max(np.diff(last))) > 1:
+                raise NotImplementedError("causal masking of multi-query groups on the last level")
+        self._plan_levels(qo_indptr_arr, paged_kv_indptr_arr, paged_kv_indices_arr, paged_kv_last_page_len,
+                          num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, q_data_type)
+
+    def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
+            return_lse: bool = False):
+        return self._run(q, paged_kv_cache, out, return_lse)
+
+    forward = run
+
+
+class BatchDecodeWithPagedKVCacheWrapper(_PagedPlanner):
+    """Flat paged decode: query i attends to its own page list (the baseline
+    strategy the cascade and tree strategies are measured against)."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD"):
+        super().__init__(float_workspace_buffer, kv_layout)
+
+    def plan(self, indptr, indices, last_page_len, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+             page_size: int, pos_encoding_mode: str = "NONE", window_left: int = -1,
+             logits_soft_cap: Optional[float] = None, q_data_type="float16", kv_data_type=None,
+             sm_scale: Optional[float] = None, **_unused) -> None:
+        if pos_encoding_mode != "NONE":
+            raise NotImplementedError("RoPE is applied before attention (pos_encoding_mode='NONE' only)")
+        if kv_data_type is not None and kv_data_type != q_data_type:
+            raise NotImplementedError("q and KV must share one dtype")
+        n = len(_as_i32(last_page_len))
+        self._plan_levels([np.arange(n + 1, dtype=np.int32)], [indptr], [indices], [last_page_len],
+                          num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, q_data_type)
+
+    def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
+            return_lse: bool = False):
+        return self._run(q, paged_kv_cache, out, return_lse)
+
+    forward = run
+
+
+def merge_state(v_a: torch.Tensor, s_a: torch.Tensor, v_b: torch.Tensor, s_b: torch.Tensor):
+    """Merge two attention states (v [n, H, D] float32, s [n, H] natural-log lse)."""
+    lib = _lib.load()
+    for t, nm in ((v_a, "v_a"), (s_a, "s_a"), (v_b, "v_b"), (s_b, "s_b")):
+        _lib.require_device(t, nm)
+        if t.dtype != torch.float32:
+            raise ValueError(f"{nm} must be float32")
+    if v_a.shape != v_b.shape or s_a.shape != s_b.shape or v_a.shape[:2] != s_a.shape:
+        raise ValueError("state shapes disagree")
+    v_a, s_a, v_b, s_b = (t.contiguous() for t in (v_a, s_a, v_b, s_b))
+    v = torch.empty_like(v_a)
+    s = torch.empty_like(s_a)
+    n, h, d = v_a.shape
+    _lib.check(lib.be_merge_states(v_a.data_ptr(), s_a.data_ptr(), v_b.data_ptr(), s_b.data_ptr(),
+                                   v.data_ptr(), s.data_ptr(), n, h, d, _lib.stream_ptr(v_a.device)),
+               "merge_state")
+    return v, s

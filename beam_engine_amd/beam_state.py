@@ -1,0 +1,440 @@
+"""Beam trie over KV pages: drop-in for the reference's ``BeamState``
+(src/beam_engine/beam_state.py).
+
+Same data classes and methods with the same results (page ids, candidate
+order, cascade index arrays are identical).  Differences in how they are
+computed:
+
+* ``get_cascade_input`` makes one top-down pass over the live trie: every
+  node gets its cascade level, the page list of its level segment (a chain of
+  only-children shares one list) and the representative node of each lower
+  level.  Each candidate's groups then come from its leaf in O(levels) instead
+  of walking every root-to-leaf path (beam_state.py:267-306).
+* Several requests can share one state: ``add_root_sequence`` may be called
+  once per request; each root is a separate cascade group at level 0 and
+  every candidate carries its ``request_id``.
+* ``add_filtered_results`` defers the page fork copies of one step to a
+  single batched launch (page ids are allocated in the reference's order).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from .kv_tree_node import KVTreeNode
+from .page_table import PageTable
+
+
+class TrieNode:
+    """One page of tokens in the beam trie (beam_state.py:12-30)."""
+
+    __slots__ = ("tokens", "parent", "children", "page_id", "_lvl", "_seg", "_seglen", "_reps", "_pre",
+                 "_stamp")
+
+    def __init__(self, tokens: List[int], page_id: int, parent: Optional["TrieNode"] = None):
+        self.tokens = tokens
+        self.parent = parent
+        self.children: List["TrieNode"] = []
+        self.page_id = page_id
+        self._stamp = -1
+        if parent:
+            parent.children.append(self)
+
+    def __repr__(self):
+        return f"TrieNode(tokens={self.tokens}, page_id={self.page_id}, children={len(self.children)})"
+
+
+@dataclass
+class BeamCandidate:
+    """A live beam: its leaf node and accumulated log-probability (beam_state.py:33-38)."""
+    trie_node: TrieNode
+    score: float
+    finished: bool = False
+    request_id: int = 0
+
+
+@dataclass
+class BeamTokenCandidate:
+    token_id: int
+    log_prob: float
+
+
+@dataclass
+class BeamToken:
+    token_id: int
+    accumulated_score: float
+
+
+@dataclass
+class BeamGenerateInput:
+    candidate: BeamCandidate
+    children: List[BeamTokenCandidate]
+
+
+@dataclass
+class BeamGenerateResult:
+    candidate: BeamCandidate
+    children: List[BeamToken]
+
+
+class BeamState:
+    """Live candidates and their page trie (beam_state.py:62-683)."""
+
+    def __init__(self, beam_size: int, page_table: PageTable):
+        self.beam_size = beam_size
+        self.page_table = page_table
+        self.root: Optional[TrieNode] = None
+        self.roots: List[TrieNode] = []
+        self.candidates: List[BeamCandidate] = []
+        self.finished_candidates: List[BeamCandidate] = []
+        self._cached_write_batch_indices = None
+        self._cached_write_kv_indptr = None
+        self._stamp = 0
+
+    # ------------------------------------------------------------ building
+    def add_root_sequence(self, sequence: List[int], request_id: int = 0) -> List[TrieNode]:
+        """Allocate pages for a prompt and add its candidate (beam_state.py:76-98).
+        Returns the created nodes in creation order."""
+        ps = self.page_table.page_size
+        cur = None
+        created = []
+        for start in range(0, len(sequence), ps):
+            page = self.page_table.allocate_block()
+            node = TrieNode(list(sequence[start:start + ps]), page, cur)
+            created.append(node)
+            if cur is None:
+                self.roots.append(node)
+                if self.root is None:
+                    self.root = node
+            cur = node
+        self.candidates.append(BeamCandidate(cur, 0, False, request_id))
+        return created
+
+    def add_filtered_results(self, results: List[BeamGenerateResult]) -> None:
+        """Prune dead branches, then expand survivors with the reference's fork
+        rules (beam_state.py:101-209): a single child appends to a non-full
+        page or opens a new page; several children of a full page open one
+        page each; several children of a partial page copy it for every child
+        after the first (siblings under the same parent), then the first child
+        appends to the original page."""
+        pt = self.page_table
+        ps = pt.page_size
+
+        for r in results:
+            if not r.children:
+                node = r.candidate.trie_node
+                while node is not None and not node.children:
+                    pt.free_block(node.page_id)
+                    parent = node.parent
+                    if parent is not None:
+                        parent.children.remove(node)
+                    elif node in self.roots:
+                        self.roots.remove(node)
+                        if self.root is node:
+                            self.root = self.roots[0] if self.roots else None
+                    node = parent
+
+        new: List[BeamCandidate] = []
+        with pt.defer_copies():
+            for r in results:
+                children = r.children
+                if not children:
+                    continue
+                node = r.candidate.trie_node
+                rid = r.candidate.request_id
+                tokens = node.tokens
+                if len(children) == 1:
+                    child = children[0]
+                    if len(tokens) < ps:
+                        tokens.append(child.token_id)
+                        new.append(BeamCandidate(node, child.accumulated_score, False, rid))
+                    else:
+                        page = pt.allocate_block()
+                        new.append(BeamCandidate(TrieNode([child.token_id], page, node),
+                                                 child.accumulated_score, False, rid))
+                    continue
+                if len(tokens) == ps:
+                    for child in children:
+                        page = pt.allocate_block()
+                        new.append(BeamCandidate(TrieNode([child.token_id], page, node),
+                                                 child.accumulated_score, False, rid))
+                else:
+                    first, rest = children[0], children[1:]
+                    for child in rest:
+                        page = pt.copy_block(node.page_id, len(node.tokens))
+                        sib = TrieNode([*tokens, child.token_id], page, node.parent)
+                        if node.parent is None:          # forking a partial root page makes a new root
+                            self.roots.append(sib)
+                        new.append(BeamCandidate(sib, child.accumulated_score, False, rid))
+                    tokens.append(first.token_id)
+                    new.append(BeamCandidate(node, first.accumulated_score, False, rid))
+        self.candidates = new
+
+    # ------------------------------------------------------------ trie pass
+    def _annotate(self) -> None:
+        """Top-down pass over every tree holding a candidate: level, segment
+        page list, lower-level representatives and prefix token count."""
+        self._stamp += 1
+        stamp = self._stamp
+        roots = list(self.roots)
+        if self.root is not None and self.root not in roots:
+            roots.append(self.root)
+        self._dfs(roots, stamp)
+        for c in self.candidates:           # trees whose root was never registered (hand-built)
+            n = c.trie_node
+            if n._stamp == stamp:
+                continue
+            while n.parent is not None:
+                n = n.parent
+            self._dfs([n], stamp)
+
+    @staticmethod
+    def _dfs(roots: List[TrieNode], stamp: int) -> None:
+        stack = []
+        for r in roots:
+            r._lvl = 0
+            r._seg = [r.page_id]
+            r._seglen = 1
+            r._reps = ()
+            r._pre = 0
+            r._stamp = stamp
+            stack.append(r)
+        while stack:
+            p = stack.pop()
+            ch = p.children
+            if not ch:
+                continue
+            pre = p._pre + len(p.tokens)
+            if len(ch) > 1:
+                reps = p._reps + (p,)
+                lvl = p._lvl + 1
+                for n in ch:
+                    n._lvl = lvl
+                    n._seg = [n.page_id]
+                    n._seglen = 1
+                    n._reps = reps
+                    n._pre = pre
+                    n._stamp = stamp
+                    stack.append(n)
+            else:
+                n = ch[0]
+                seg = p._seg
+                if len(seg) > p._seglen:         # the list was extended past p before: fork a copy
+                    seg = seg[:p._seglen]
+                seg.append(n.page_id)
+                n._lvl = p._lvl
+                n._seg = seg
+                n._seglen = p._seglen + 1
+                n._reps = p._reps
+                n._pre = pre
+                n._stamp = stamp
+                stack.append(n)
+
+    @staticmethod
+    def _seg_pages(node: TrieNode) -> List[int]:
+        pages = node._seg[:node._seglen]
+        if len(pages) > 1 and len(set(pages)) != len(pages):
+            pages = list(dict.fromkeys(pages))
+        return pages
+
+    def get_cascade_input(self):
+        """Per-level FlashInfer cascade arrays (beam_state.py:211-412).
+
+        Returns ``(qo_indptr_arr, kv_indptr_arr, kv_indices_arr,
+        last_page_len_arr, query_token_ids, write_batch_indices,
+        write_kv_indptr)``; the index arrays are CPU int32 tensors, the rest
+        live on the page table's device.  An empty state returns the
+        reference's 5-tuple."""
+        if not self.candidates:
+            return ([], [], [], [], torch.empty(0, 0, 0))
+        levels = self._cascade_lists()
+        qo_arr = [torch.tensor(l[0], dtype=torch.int32) for l in levels]
+        kvp_arr = [torch.tensor(l[1], dtype=torch.int32) for l in levels]
+        kvi_arr = [torch.tensor(l[2], dtype=torch.int32) for l in levels]
+        lpl_arr = [torch.tensor(l[3], dtype=torch.int32) for l in levels]
+        dev = self.page_table.device
+        qids = torch.tensor(self.query_token_ids(), dtype=torch.long, device=dev)
+        n = len(self.candidates)
+        if self._cached_write_batch_indices is None or self._cached_write_batch_indices.shape[0] != n:
+            self._cached_write_batch_indices = torch.arange(n, dtype=torch.int32, device=dev)
+            self._cached_write_kv_indptr = torch.arange(n + 1, dtype=torch.int32, device=dev)
+        return (qo_arr, kvp_arr, kvi_arr, lpl_arr, qids, self._cached_write_batch_indices,
+                self._cached_write_kv_indptr)
+
+    def _cascade_lists(self):
+        """The cascade arrays as Python lists: [(qo, kv_indptr, kv_indices, last_page_len)] per level."""
+        self._annotate()
+        cands = self.candidates
+        max_level = max(c.trie_node._lvl for c in cands)
+        levels = []
+        for lv in range(max_level + 1):
+            groups: Dict[int, list] = {}
+            for c in cands:
+                leaf = c.trie_node
+                rep = leaf._reps[lv] if lv < leaf._lvl else leaf
+                key = id(rep)
+                g = groups.get(key)
+                if g is None:
+                    cnt = len(rep.tokens)
+                    groups[key] = [1, rep, (max(0, cnt - 1) if rep is leaf else cnt)]
+                else:
+                    g[0] += 1
+            qo, kvp, kvi, lpl = [0], [0], [], []
+            for cnt, rep, last in groups.values():
+                kvi.extend(self._seg_pages(rep))
+                kvp.append(len(kvi))
+                lpl.append(last)
+                qo.append(qo[-1] + cnt)
+            levels.append((qo, kvp, kvi, lpl))
+        return levels
+
+    def query_token_ids(self) -> List[int]:
+        return [c.trie_node.tokens[-1] if c.trie_node.tokens else 0 for c in self.candidates]
+
+    def write_locations(self) -> Tuple[List[int], List[int]]:
+        """(page, slot) each candidate's new K/V goes to (beam.py:180-189)."""
+        return ([c.trie_node.page_id for c in self.candidates],
+                [len(c.trie_node.tokens) - 1 for c in self.candidates])
+
+    def position_ids(self) -> List[int]:
+        """Total path tokens minus one per candidate (beam.py:208-221)."""
+        self._annotate()
+        return [c.trie_node._pre + len(c.trie_node.tokens) - 1 for c in self.candidates]
+
+    def path_pages(self, idx: int) -> List[int]:
+        out = []
+        n = self.candidates[idx].trie_node
+        while n is not None:
+            out.append(n.page_id)
+            n = n.parent
+        return out[::-1]
+
+    def flat_lists(self, include_self: bool = False):
+        """Flat strategy arrays: one group per candidate over its whole path.
+
+        ``include_self=False`` follows the cascade convention of the reference
+        (the query's own new token is not attended, beam_state.py:347-354);
+        True attends to it (FastTree / HF convention)."""
+        self._annotate()
+        kvp, kvi, lpl = [0], [], []
+        for c in self.candidates:
+            leaf = c.trie_node
+            pages: List[int] = []
+            for rep in leaf._reps:
+                pages.extend(rep._seg[:rep._seglen])
+            pages.extend(leaf._seg[:leaf._seglen])
+            kvi.extend(pages)
+            kvp.append(len(kvi))
+            n = len(leaf.tokens)
+            lpl.append(n if include_self else max(0, n - 1))
+        return kvp, kvi, lpl
+
+    # ------------------------------------------------------------ FastTree inputs
+    def _build_kv_tree_structure(self) -> Tuple[List[KVTreeNode], Dict[int, int]]:
+        """BFS numbering of the live trie for FastTree (beam_state.py:414-510).
+        ``seqlen`` is cumulative from the root, as in the reference."""
+        self._annotate()
+        roots = []
+        seen = set()
+        for c in self.candidates:
+            n = c.trie_node
+            while n.parent is not None:
+                n = n.parent
+            if id(n) not in seen:
+                seen.add(id(n))
+                roots.append(n)
+        users: Dict[int, List[int]] = {}
+        for ci, c in enumerate(self.candidates):
+            n = c.trie_node
+            while n is not None:
+                users.setdefault(id(n), []).append(ci)
+                n = n.parent
+        out: List[KVTreeNode] = []
+        ids: Dict[int, int] = {}
+        queue = list(roots)
+        head = 0
+        while head < len(queue):
+            t = queue[head]
+            head += 1
+            k = KVTreeNode()
+            k.id = len(out)
+            ids[id(t)] = k.id
+            k.parent = ids[id(t.parent)] if t.parent is not None else -1
+            k.seqlen = t._pre + len(t.tokens)
+            k.num_children = len(t.children)
+            k.requests = sorted(users.get(id(t), []))
+            out.append(k)
+            queue.extend(t.children)
+        return out, ids
+
+    def _build_req_to_token(self, tree_nodes=None) -> torch.Tensor:
+        """``[N, max_len]`` slot ids page * page_size + i (beam_state.py:512-564),
+        built on the host and copied once."""
+        self._annotate()
+        ps = self.page_table.page_size
+        rows = []
+        for c in self.candidates:
+            path = []
+            n = c.trie_node
+            while n is not None:
+                path.append(n)
+                n = n.parent
+            row = []
+            for node in reversed(path):
+                base = node.page_id * ps
+                row.extend(range(base, base + len(node.tokens)))
+            rows.append(row)
+        width = max((len(r) for r in rows), default=0)
+        out = torch.zeros((len(rows), width), dtype=torch.int32)
+        for i, r in enumerate(rows):
+            out[i, :len(r)] = torch.tensor(r, dtype=torch.int32)
+        return out.to(self.page_table.device)
+
+    def get_fasttree_input(self):
+        """(tree_nodes, req_to_token, query_ids, write_pages, write_positions) (beam_state.py:566-633)."""
+        tree_nodes, _ = self._build_kv_tree_structure()
+        req_to_token = self._build_req_to_token(tree_nodes)
+        dev = self.page_table.device
+        wp, wpos = self.write_locations()
+        return (tree_nodes, req_to_token,
+                torch.tensor(self.query_token_ids(), dtype=torch.long, device=dev),
+                torch.tensor(wp, dtype=torch.int32, device=dev),
+                torch.tensor(wpos, dtype=torch.int32, device=dev))
+
+    # ------------------------------------------------------------ results
+    def sequence(self, cand: BeamCandidate) -> List[int]:
+        seq: List[int] = []
+        n = cand.trie_node
+        parts = []
+        while n is not None:
+            parts.append(n.tokens)
+            n = n.parent
+        for p in reversed(parts):
+            seq.extend(p)
+        return seq
+
+    def get_best_finished(self, num_return: int) -> List[BeamCandidate]:
+        """Best candidates by score / sequence length.  (The reference reads a
+        missing ``length`` attribute here, beam_state.py:635-644; the length
+        used is the full sequence length.)"""
+        pool = self.finished_candidates or self.candidates
+        return sorted(pool, key=lambda c: c.score / max(1, len(self.sequence(c))), reverse=True)[:num_return]
+
+    def get_final_sequences(self, num_return: int, length_penalty: float = 1.0,
+                            request_id: Optional[int] = None) -> List[Tuple[List[int], float]]:
+        """(sequence, score / len^penalty) sorted by score (beam_state.py:646-682)."""
+        pool = self.finished_candidates + self.candidates
+        if request_id is not None:
+            pool = [c for c in pool if c.request_id == request_id]
+        out = []
+        for c in pool:
+            seq = self.sequence(c)
+            sc = c.score
+            if length_penalty != 0 and len(seq) > 1:
+                sc = sc / (len(seq) ** length_penalty)
+            out.append((seq, sc))
+        out.sort(key=lambda x: x[1], reverse=True)
+        return out[:num_return]

@@ -1,0 +1,836 @@
+// Paged decode attention for flat / cascade / tree work lists on gfx950.
+//
+// One work-list format serves every strategy.  A work item is a tile of
+// queries (a contiguous slice of q_index) attending to a contiguous token range
+// of one paged group (a slice of the plan's page list).  The attention kernel
+// runs one workgroup per (item, KV head) and writes either the final output
+// (a query with a single item) or a partial (o, lse) row that the merge kernel
+// combines by log-sum-exp.  The reference computes the same quantities with
+// FlashInfer's MultiLevelCascadeAttentionWrapper (models/modeling_llama.py:
+// 321-367, 732-755) and the FastTree Triton kernels
+// (attention/fasttree/kernel.py:5-285).
+
+#include <math.h>
+#include <stdarg.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "common.h"
+
+namespace be {
+
+// ------------------------------------------------------------------ plan layout
+// Device plan = int32 words:
+//   items      [num_items][8]   WorkItem
+//   q_index    [num_queries]     query ids referenced by items
+//   pages      [sum of level page lists]
+//   merge_q    [num_merge]       queries the merge kernel combines
+//   merge_ptr  [num_merge + 1]   CSR into merge_rows
+//   merge_rows [...]             partial rows of each merged query
+struct WorkItem {
+  int32_t q_begin;     // first entry of q_index
+  int32_t q_count;     // queries in the tile
+  int32_t page_begin;  // first entry of pages[] of the item's group
+  int32_t tok_begin;   // first group token covered (a multiple of 32)
+  int32_t tok_count;   // tokens covered, > 0
+  int32_t out_row;     // first partial row, or -1: write the final output
+  int32_t pad0, pad1;
+};
+static_assert(sizeof(WorkItem) == 32, "WorkItem is 8 int32 words");
+
+constexpr int kMaxRows = 32;   // queries x GQA group per workgroup tile
+
+struct AttnArgs {
+  const void* q;
+  int64_t q_sn, q_sh;
+  const void* kv;
+  void* out;
+  int64_t o_sn, o_sh;
+  float* out_lse;
+  float* part_o;      // [rows, Hq, D]
+  float* part_lse;    // [rows, Hq]
+  const WorkItem* items;
+  const int32_t* q_index;
+  const int32_t* pages;
+  int page_size, hkv, hq, g;
+  float scale_log2;   // sm_scale * log2(e)
+};
+
+struct MergeArgs {
+  const float* part_o;
+  const float* part_lse;
+  const int32_t* merge_q;
+  const int32_t* merge_ptr;
+  const int32_t* merge_rows;
+  void* out;
+  int64_t o_sn, o_sh;
+  float* out_lse;
+  int hq;
+};
+
+// Element offset of (page, kv, slot, head, 0) in a [P, 2, page, Hkv, D] layer.
+__device__ __forceinline__ int64_t kv_off(int page, int kvsel, int slot, int head, int page_size,
+                                          int hkv, int d) {
+  return ((((int64_t)page * 2 + kvsel) * page_size + slot) * hkv + head) * (int64_t)d;
+}
+
+// Writes the finished state of one row: o = acc / l, lse = (m + log2 l) ln 2.
+template <typename T>
+__device__ __forceinline__ void store_row_lse(const AttnArgs& a, const WorkItem& it, int j, int head,
+                                              float m2, float l) {
+  float lse = (l > 0.f) ? (m2 + log2f(l)) * 0.69314718055994531f : -INFINITY;
+  if (it.out_row < 0) {
+    if (a.out_lse) {
+      int qi = a.q_index[it.q_begin + j];
+      a.out_lse[(int64_t)qi * a.hq + head] = lse;
+    }
+  } else {
+    a.part_lse[(int64_t)(it.out_row + j) * a.hq + head] = lse;
+  }
+}
+
+// ================================================================== MFMA kernel
+// bf16/fp16 storage, D in {64, 128, 256}, up to 16*NT rows per tile.
+//
+// Per 32-token block a wave computes S^T = K Q^T with v_mfma_f32_16x16x32:
+// the A operand (K) is 8 consecutive head_dim elements of one token row, i.e.
+// one 16-byte load straight from the page.  The C layout of S^T gives each lane
+// 8 tokens of one row; that is exactly the B operand (P^T) of O^T = V^T P^T
+// once the token axis of the contraction is permuted consistently
+// (k = 8*lg + j  <->  token 4*lg + j for j < 4, 16 + 4*lg + j - 4 otherwise).
+// V^T's A operand needs 8 tokens of one head_dim column, so each wave stages
+// its V block transposed in a private LDS slab.  The four waves of a
+// workgroup take interleaved blocks (split-K inside the workgroup) and are
+// combined through LDS at the end.
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ v4f mfma16(v8s a, v8s b, v4f c);
+template <>
+__device__ __forceinline__ v4f mfma16<bf16_t>(v8s a, v8s b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ v4f mfma16<f16_t>(v8s a, v8s b, v4f c) {
+  typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b),
+                                                c, 0, 0, 0);
+}
+
+template <typename T> __device__ __forceinline__ uint16_t pack16(float x);
+template <> __device__ __forceinline__ uint16_t pack16<bf16_t>(float x) { return f32_to_bf16_bits(x); }
+template <> __device__ __forceinline__ uint16_t pack16<f16_t>(float x) {
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+#define LDS_FENCE() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
+
+template <typename T, int D, int NT>
+__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
+  constexpr int KS = D / 32;          // contraction steps of Q.K^T
+  constexpr int MT = D / 16;          // head_dim tiles of O^T
+  constexpr int VROW = 36;            // transposed V row: 32 tokens + pad (16-bit units)
+  constexpr int VCH = D / 8;          // 16-byte chunks per token row
+  constexpr int SLAB = D * VROW;      // per-wave V^T slab (16-bit units)
+  constexpr int COMB = (MT * NT * 64 * 4 + NT * 64 * 2);   // floats per combine slot
+  constexpr int LDS_BYTES = (4 * SLAB * 2 > 2 * COMB * 4) ? 4 * SLAB * 2 : 2 * COMB * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+  uint16_t* vt = reinterpret_cast<uint16_t*>(lds);
+
+  const WorkItem it = a.items[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
+  const int g = a.g;
+  const int R = it.q_count * g;
+  const T* qbase = reinterpret_cast<const T*>(a.q);
+  const T* kv = reinterpret_cast<const T*>(a.kv);
+
+  // Q^T as the B operand: lane holds Q[row = nt*16 + lc][d = ks*32 + 8*lg .. +7].
+  v8s qf[NT][KS];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = nt * 16 + lc;
+    if (row < R) {
+      const int j = row / g, hh = row - j * g;
+      const int qi = a.q_index[it.q_begin + j];
+      const T* qp = qbase + (int64_t)qi * a.q_sn + (int64_t)(kvh * g + hh) * a.q_sh;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = *reinterpret_cast<const v8s*>(qp + ks * 32 + lg * 8);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+
+  float m_run[NT], l_run[NT];
+  v4f o_acc[MT][NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) o_acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+
+  uint16_t* my_vt = vt + w * SLAB;
+  const int n_blocks = (it.tok_count + 31) >> 5;
+  const int ps = a.page_size;
+
+  for (int blk = w; blk < n_blocks; blk += 4) {
+    const int tl0 = blk * 32;   // item-relative first token of the block
+    // ---- K (A operand) straight from the pages
+    v8s kf[2][KS];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tl = tl0 + tt * 16 + lc;
+      if (tl < it.tok_count) {
+        const int tok = it.tok_begin + tl;
+        const int page = a.pages[it.page_begin + tok / ps];
+        const T* kr = kv + kv_off(page, 0, tok % ps, kvh, ps, a.hkv, D);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kf[tt][ks] = *reinterpret_cast<const v8s*>(kr + ks * 32 + lg * 8);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kf[tt][ks] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+    // ---- V block: 16-byte chunks, chunk c -> token c / VCH, column chunk c % VCH
+    v8s vr[VCH / 2];
+#pragma unroll
+    for (int i = 0; i < VCH / 2; ++i) {
+      const int c = i * 64 + lane;
+      const int tl = tl0 + c / VCH;
+      if (tl < it.tok_count) {
+        const int tok = it.tok_begin + tl;
+        const int page = a.pages[it.page_begin + tok / ps];
+        vr[i] = *reinterpret_cast<const v8s*>(kv + kv_off(page, 1, tok % ps, kvh, ps, a.hkv, D) + (c % VCH) * 8);
+      } else {
+        vr[i] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+    // ---- S^T = K Q^T
+    v4f s[2][NT];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) acc = mfma16<T>(kf[tt][ks], qf[nt][ks], acc);
+        s[tt][nt] = acc;
+      }
+    // ---- V^T into this wave's slab (previous block's reads are complete:
+    //      they fed the MFMAs of the last iteration)
+    LDS_FENCE();
+#pragma unroll
+    for (int i = 0; i < VCH / 2; ++i) {
+      const int c = i * 64 + lane;
+      const int t = c / VCH, d0 = (c % VCH) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) my_vt[(d0 + e) * VROW + t] = (uint16_t)vr[i][e];
+    }
+    // ---- online softmax (log2 domain) per row = lane column
+    v8s pf[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float x[8];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tl = tl0 + tt * 16 + 4 * lg + i;
+          x[tt * 4 + i] = (tl < it.tok_count) ? s[tt][nt][i] * a.scale_log2 : -INFINITY;
+        }
+      float mx = x[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[nt], mx);       // finite: the block has a valid token
+      const float alpha = exp2f(m_run[nt] - m_new);   // 0 when m_run == -inf
+      float psum = 0.f;
+      v8s pk;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = exp2f(x[e] - m_new);
+        psum += p;
+        pk[e] = (short)pack16<T>(p);
+      }
+      pf[nt] = pk;
+      l_run[nt] = l_run[nt] * alpha + psum;
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) o_acc[mt][nt] *= alpha;
+    }
+    LDS_FENCE();
+    // ---- O^T += V^T P^T
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint16_t* src = my_vt + (mt * 16 + lc) * VROW + 4 * lg;
+      const v4s lo = *reinterpret_cast<const v4s*>(src);
+      const v4s hi = *reinterpret_cast<const v4s*>(src + 16);
+      const v8s vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o_acc[mt][nt] = mfma16<T>(vf, pf[nt], o_acc[mt][nt]);
+    }
+  }
+
+  // row sums over the four lane groups
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    l_run[nt] += __shfl_xor(l_run[nt], 16, 64);
+    l_run[nt] += __shfl_xor(l_run[nt], 32, 64);
+  }
+
+  // ---- combine the four waves: 3 -> 1, 2 -> 0, then 1 -> 0
+  float* comb = reinterpret_cast<float*>(lds);
+  __syncthreads();   // every wave is done with its V slab
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    const int senders_lo = (round == 0) ? 2 : 1;   // waves [senders_lo, 2*senders_lo) send
+    if (w >= senders_lo && w < 2 * senders_lo) {
+      float* slot = comb + (w - senders_lo) * COMB;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          *reinterpret_cast<v4f*>(slot + ((mt * NT + nt) * 64 + lane) * 4) = o_acc[mt][nt];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        slot[MT * NT * 64 * 4 + nt * 64 + lane] = m_run[nt];
+        slot[MT * NT * 64 * 4 + NT * 64 + nt * 64 + lane] = l_run[nt];
+      }
+    }
+    __syncthreads();
+    if (w < senders_lo) {
+      const float* slot = comb + w * COMB;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const float mb = slot[MT * NT * 64 * 4 + nt * 64 + lane];
+        const float lb = slot[MT * NT * 64 * 4 + NT * 64 + nt * 64 + lane];
+        const float M = fmaxf(m_run[nt], mb);
+        const float ca = (M == -INFINITY) ? 0.f : exp2f(m_run[nt] - M);
+        const float cb = (M == -INFINITY) ? 0.f : exp2f(mb - M);
+        l_run[nt] = l_run[nt] * ca + lb * cb;
+        m_run[nt] = M;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const v4f ob = *reinterpret_cast<const v4f*>(slot + ((mt * NT + nt) * 64 + lane) * 4);
+          o_acc[mt][nt] = o_acc[mt][nt] * ca + ob * cb;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (w != 0) return;
+  // ---- wave 0 writes: lane holds O^T[d = mt*16 + 4*lg + i][row = nt*16 + lc]
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = nt * 16 + lc;
+    if (row >= R) continue;
+    const int j = row / g, hh = row - j * g, head = kvh * g + hh;
+    const float l = l_run[nt];
+    const float inv = (l > 0.f) ? 1.f / l : 0.f;
+    if (it.out_row < 0) {
+      const int qi = a.q_index[it.q_begin + j];
+      T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        v4s pk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = (short)pack16<T>(o_acc[mt][nt][i] * inv);
+        *reinterpret_cast<v4s*>(op + mt * 16 + 4 * lg) = pk;
+      }
+    } else {
+      float* op = a.part_o + ((int64_t)(it.out_row + j) * a.hq + head) * D;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<v4f*>(op + mt * 16 + 4 * lg) = o_acc[mt][nt] * inv;
+    }
+    if (lg == 0) store_row_lse<T>(a, it, j, head, m_run[nt], l);
+  }
+}
+
+// ================================================================== VALU kernel
+// Any storage dtype, D in {64, 128, 256}, up to 32 rows per tile.  K/V blocks
+// of 32 tokens are converted to fp32 in LDS; scores use one thread per
+// (token, row-group), P.V one thread per (head_dim column, row-group).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_valu_kernel(AttnArgs a) {
+  constexpr int BT = 32;
+  constexpr int NRG = 256 / D;           // row groups in the P.V phase
+  constexpr int RPT = kMaxRows / NRG;    // rows per thread in the P.V phase
+  constexpr int KST = D + 1;             // padded K row
+  __shared__ float qs[kMaxRows][D];
+  __shared__ float ks[BT * KST];
+  __shared__ float vs[BT][D];
+  __shared__ float psm[kMaxRows][BT];
+  __shared__ float alpha_s[kMaxRows], l_s[kMaxRows], m_s[kMaxRows];
+
+  const WorkItem it = a.items[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int g = a.g;
+  const int R = it.q_count * g;
+  const T* qbase = reinterpret_cast<const T*>(a.q);
+  const T* kv = reinterpret_cast<const T*>(a.kv);
+  const int ps = a.page_size;
+
+  for (int e = tid; e < kMaxRows * D; e += 256) {
+    const int r = e / D, d = e % D;
+    float val = 0.f;
+    if (r < R) {
+      const int j = r / g, hh = r - j * g;
+      const int qi = a.q_index[it.q_begin + j];
+      val = to_f32(qbase[(int64_t)qi * a.q_sn + (int64_t)(kvh * g + hh) * a.q_sh + d]);
+    }
+    qs[r][d] = val;
+  }
+
+  // score-phase ownership: token t = tid % 32, rows rg + 8k
+  const int t_own = tid & 31, rg = tid >> 5;
+  float m_row[4], l_row[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) { m_row[k] = -INFINITY; l_row[k] = 0.f; }
+  // P.V-phase ownership: column d = tid % D, rows rgp + NRG*k
+  const int d_own = tid % D, rgp = tid / D;
+  float acc[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) acc[k] = 0.f;
+
+  for (int tb = 0; tb < it.tok_count; tb += BT) {
+    __syncthreads();
+    for (int e = tid; e < BT * D; e += 256) {
+      const int t = e / D, d = e % D;
+      const int tl = tb + t;
+      float kx = 0.f, vx = 0.f;
+      if (tl < it.tok_count) {
+        const int tok = it.tok_begin + tl;
+        const int page = a.pages[it.page_begin + tok / ps];
+        kx = to_f32(kv[kv_off(page, 0, tok % ps, kvh, ps, a.hkv, D) + d]);
+        vx = to_f32(kv[kv_off(page, 1, tok % ps, kvh, ps, a.hkv, D) + d]);
+      }
+      ks[t * KST + d] = kx;
+      vs[t][d] = vx;
+    }
+    __syncthreads();
+    const bool tvalid = (tb + t_own) < it.tok_count;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = rg + 8 * k;
+      float sc = 0.f;
+#pragma unroll 8
+      for (int d = 0; d < D; ++d) sc += qs[r][d] * ks[t_own * KST + d];
+      const float x = tvalid ? sc * a.scale_log2 : -INFINITY;
+      float mx = x;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      const float m_new = fmaxf(m_row[k], mx);
+      const float p = exp2f(x - m_new);
+      float psum = p;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) psum += __shfl_xor(psum, o, 64);
+      const float al = exp2f(m_row[k] - m_new);
+      l_row[k] = l_row[k] * al + psum;
+      m_row[k] = m_new;
+      psm[r][t_own] = p;
+      if (t_own == 0) alpha_s[r] = al;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int r = rgp + NRG * k;
+      float sacc = acc[k] * alpha_s[r];
+#pragma unroll 8
+      for (int t = 0; t < BT; ++t) sacc += psm[r][t] * vs[t][d_own];
+      acc[k] = sacc;
+    }
+  }
+  if (t_own == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { l_s[rg + 8 * k] = l_row[k]; m_s[rg + 8 * k] = m_row[k]; }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int r = rgp + NRG * k;
+    if (r >= R) continue;
+    const int j = r / g, hh = r - j * g, head = kvh * g + hh;
+    const float l = l_s[r];
+    const float o = (l > 0.f) ? acc[k] / l : 0.f;
+    if (it.out_row < 0) {
+      const int qi = a.q_index[it.q_begin + j];
+      reinterpret_cast<T*>(a.out)[(int64_t)qi * a.o_sn + (int64_t)head * a.o_sh + d_own] = from_f32<T>(o);
+    } else {
+      a.part_o[((int64_t)(it.out_row + j) * a.hq + head) * D + d_own] = o;
+    }
+    if (d_own == 0) store_row_lse<T>(a, it, j, head, m_s[r], l);
+  }
+}
+
+// ================================================================== merge kernel
+// One wave per (merged query, head): o = sum_i e^(lse_i - M) o_i / sum_i e^(lse_i - M).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int head = blockIdx.y * 4 + w;
+  if (head >= a.hq) return;
+  const int qi = a.merge_q[blockIdx.x];
+  const int b = a.merge_ptr[blockIdx.x], e = a.merge_ptr[blockIdx.x + 1];
+  float M = -INFINITY;
+  for (int i = b; i < e; ++i) M = fmaxf(M, a.part_lse[(int64_t)a.merge_rows[i] * a.hq + head]);
+  constexpr int PER = D / 64;
+  float acc[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) acc[k] = 0.f;
+  float z = 0.f;
+  if (M != -INFINITY) {
+    for (int i = b; i < e; ++i) {
+      const int64_t row = (int64_t)a.merge_rows[i] * a.hq + head;
+      const float wgt = expf(a.part_lse[row] - M);
+      z += wgt;
+      const float* op = a.part_o + row * D;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) acc[k] += wgt * op[lane + 64 * k];
+    }
+  }
+  const float inv = (z > 0.f) ? 1.f / z : 0.f;
+  T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) op[lane + 64 * k] = from_f32<T>(acc[k] * inv);
+  if (a.out_lse && lane == 0) a.out_lse[(int64_t)qi * a.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
+}
+
+// One wave owns one row, so outputs may alias inputs (every lane reads the
+// row's lse before lane 0 overwrites it).
+__global__ __launch_bounds__(256) void merge2_kernel(const float* oa, const float* la, const float* ob,
+                                                    const float* lb, float* oo, float* lo, int rows,
+                                                    int d) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float x = la[r], y = lb[r];
+  const float M = fmaxf(x, y);
+  float ca = 0.f, cb = 0.f;
+  if (M != -INFINITY) { ca = expf(x - M); cb = expf(y - M); }
+  const float z = ca + cb;
+  const float inv = (z > 0.f) ? 1.f / z : 0.f;
+  for (int e = lane; e < d; e += 64) {
+    const int64_t i = r * d + e;
+    oo[i] = (ca * oa[i] + cb * ob[i]) * inv;
+  }
+  if (lane == 0) lo[r] = (z > 0.f) ? M + logf(z) : -INFINITY;
+}
+
+// ================================================================== host: planner
+namespace {
+
+struct Group {
+  int level, q0, q1, page_base, kv_len;
+};
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, int hkv, int d,
+              int page_size, int num_pages, int dtype, int flags, int num_cus, int32_t* out,
+              int64_t cap, be_attn_plan_info* info) {
+  BE_REQUIRE(info != nullptr && out != nullptr, "null plan buffer or info");
+  BE_REQUIRE(num_levels >= 0 && (num_levels == 0 || levels != nullptr), "bad levels");
+  BE_REQUIRE(num_queries >= 0, "num_queries must be >= 0");
+  BE_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
+  BE_REQUIRE(page_size > 0 && num_pages > 0, "page_size and num_pages must be positive");
+  BE_REQUIRE(dtype == BE_F32 || dtype == BE_F16 || dtype == BE_BF16, "unknown dtype %d", dtype);
+  const int g = hq / hkv;
+  if (d != 64 && d != 128 && d != 256) return fail(BE_ERR_UNSUPPORTED, "head_dim %d: kernels exist for 64, 128, 256", d);
+  if (g > kMaxRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d", g, kMaxRows);
+  if (num_cus <= 0) num_cus = 256;
+
+  // ---- validate levels, collect groups
+  std::vector<Group> groups;
+  int64_t total_pages = 0;
+  for (int lv = 0; lv < num_levels; ++lv) {
+    const be_level& L = levels[lv];
+    BE_REQUIRE(L.num_groups >= 0, "level %d: negative group count", lv);
+    BE_REQUIRE(L.num_groups == 0 || (L.qo_indptr && L.kv_indptr && L.last_page_len), "level %d: null index array", lv);
+    if (L.num_groups == 0) continue;
+    BE_REQUIRE(L.qo_indptr[0] == 0 && L.kv_indptr[0] == 0, "level %d: indptr must start at 0", lv);
+    for (int j = 0; j < L.num_groups; ++j) {
+      BE_REQUIRE(L.qo_indptr[j + 1] >= L.qo_indptr[j], "level %d: qo_indptr not monotone", lv);
+      BE_REQUIRE(L.kv_indptr[j + 1] >= L.kv_indptr[j], "level %d: kv_indptr not monotone", lv);
+      BE_REQUIRE(L.last_page_len[j] >= 0 && L.last_page_len[j] <= page_size,
+                 "level %d group %d: last_page_len %d outside [0, %d]", lv, j, L.last_page_len[j], page_size);
+    }
+    BE_REQUIRE(L.qo_indptr[L.num_groups] <= num_queries, "level %d: qo_indptr exceeds %d queries", lv, num_queries);
+    const int np = L.kv_indptr[L.num_groups];
+    BE_REQUIRE(np == 0 || L.kv_indices, "level %d: null kv_indices", lv);
+    for (int i = 0; i < np; ++i)
+      BE_REQUIRE(L.kv_indices[i] >= 0 && L.kv_indices[i] < num_pages, "level %d: page %d out of range [0, %d)", lv,
+                 L.kv_indices[i], num_pages);
+    for (int j = 0; j < L.num_groups; ++j) {
+      const int npg = L.kv_indptr[j + 1] - L.kv_indptr[j];
+      const int kv_len = npg == 0 ? 0 : (npg - 1) * page_size + L.last_page_len[j];
+      groups.push_back(Group{lv, L.qo_indptr[j], L.qo_indptr[j + 1], (int)(total_pages + L.kv_indptr[j]), kv_len});
+    }
+    total_pages += np;
+  }
+
+  bool mfma = (dtype != BE_F32) && !(flags & BE_PLAN_FORCE_VALU);
+  if (mfma && d == 256 && g > 16) mfma = false;          // the 32-row D=256 MFMA tile does not fit in VGPRs
+  const int rows_cap = (mfma && d == 256) ? 16 : kMaxRows;
+  const int q_tile = std::max(1, rows_cap / g);
+
+  // ---- split-K chunk: about two workgroups per CU over all (tile, chunk, head)
+  int64_t work = 0;   // token-tiles
+  for (const Group& gr : groups)
+    if (gr.q1 > gr.q0 && gr.kv_len > 0) work += ceil_div(gr.q1 - gr.q0, q_tile) * (int64_t)gr.kv_len;
+  const int64_t target = 2 * (int64_t)num_cus;
+  int64_t chunk = ceil_div(work * hkv, target);
+  chunk = std::max<int64_t>(128, ceil_div(chunk, 128) * 128);
+  if (chunk > (int64_t)1 << 30) chunk = (int64_t)1 << 30;
+
+  // ---- per-query partial counts
+  std::vector<int> cnt(num_queries, 0);
+  for (const Group& gr : groups) {
+    if (gr.kv_len <= 0) continue;
+    const int nch = (int)ceil_div(gr.kv_len, chunk);
+    for (int qi = gr.q0; qi < gr.q1; ++qi) cnt[qi] += nch;
+  }
+
+  // ---- items and partial rows
+  std::vector<WorkItem> items;
+  std::vector<std::vector<int>> rows_of(num_queries);
+  int rows = 0, max_r = 0;
+  double flops = 0.0;
+  for (const Group& gr : groups) {
+    if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
+    flops += 4.0 * d * hq * (double)gr.kv_len * (gr.q1 - gr.q0);
+    for (int t0 = 0; t0 < gr.kv_len; t0 += (int)chunk) {
+      const int tc = (int)std::min<int64_t>(chunk, gr.kv_len - t0);
+      for (int qa = gr.q0; qa < gr.q1; qa += q_tile) {
+        const int qn = std::min(q_tile, gr.q1 - qa);
+        bool direct = true;
+        for (int qi = qa; qi < qa + qn; ++qi) direct = direct && (cnt[qi] == 1);
+        WorkItem w{qa, qn, gr.page_base, t0, tc, -1, 0, 0};
+        if (!direct) {
+          w.out_row = rows;
+          for (int j = 0; j < qn; ++j) rows_of[qa + j].push_back(rows + j);
+          rows += qn;
+        }
+        max_r = std::max(max_r, qn * g);
+        items.push_back(w);
+      }
+    }
+  }
+
+  // ---- algorithmic bytes: distinct (page, head) valid tokens, plus Q and O
+  std::vector<int> valid(num_pages, 0);
+  {
+    int64_t pbase = 0;
+    for (int lv = 0; lv < num_levels; ++lv) {
+      const be_level& L = levels[lv];
+      for (int j = 0; j < L.num_groups; ++j) {
+        const int b = L.kv_indptr[j], e = L.kv_indptr[j + 1];
+        for (int i = b; i < e; ++i) {
+          const int v = (i + 1 < e) ? page_size : L.last_page_len[j];
+          int& slot = valid[L.kv_indices[i]];
+          slot = std::max(slot, v);
+        }
+      }
+      pbase += L.num_groups ? L.kv_indptr[L.num_groups] : 0;
+    }
+  }
+  int64_t valid_tokens = 0;
+  for (int v : valid) valid_tokens += v;
+  const int64_t es = (int64_t)dtype_size(dtype);
+
+  // ---- merge list
+  std::vector<int> merge_q, merge_ptr{0}, merge_rows;
+  for (int qi = 0; qi < num_queries; ++qi) {
+    if (cnt[qi] == 1) continue;
+    merge_q.push_back(qi);
+    for (int r : rows_of[qi]) merge_rows.push_back(r);
+    merge_ptr.push_back((int)merge_rows.size());
+  }
+
+  // ---- serialise
+  const int64_t n_items = (int64_t)items.size();
+  int64_t off = 0;
+  const int64_t off_items = off;    off += n_items * 8;
+  const int64_t off_qindex = off;   off += num_queries;
+  const int64_t off_pages = off;    off += total_pages;
+  const int64_t off_mq = off;       off += (int64_t)merge_q.size();
+  const int64_t off_mp = off;       off += (int64_t)merge_ptr.size();
+  const int64_t off_mr = off;       off += (int64_t)merge_rows.size();
+  off = ceil_div(off, 4) * 4;
+  if (off > cap || off > INT32_MAX) return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  memcpy(out + off_items, items.data(), n_items * sizeof(WorkItem));
+  for (int i = 0; i < num_queries; ++i) out[off_qindex + i] = i;
+  {
+    int64_t p = off_pages;
+    for (int lv = 0; lv < num_levels; ++lv) {
+      const be_level& L = levels[lv];
+      const int np = L.num_groups ? L.kv_indptr[L.num_groups] : 0;
+      if (np) memcpy(out + p, L.kv_indices, np * sizeof(int32_t));
+      p += np;
+    }
+  }
+  if (!merge_q.empty()) memcpy(out + off_mq, merge_q.data(), merge_q.size() * 4);
+  memcpy(out + off_mp, merge_ptr.data(), merge_ptr.size() * 4);
+  if (!merge_rows.empty()) memcpy(out + off_mr, merge_rows.data(), merge_rows.size() * 4);
+  for (int64_t i = off_mr + (int64_t)merge_rows.size(); i < off; ++i) out[i] = 0;
+
+  memset(info, 0, sizeof(*info));
+  info->num_items = (int32_t)n_items;
+  info->num_part_rows = rows;
+  info->num_merge = (int32_t)merge_q.size();
+  info->num_queries = num_queries;
+  info->num_qo_heads = hq;
+  info->num_kv_heads = hkv;
+  info->head_dim = d;
+  info->page_size = page_size;
+  info->num_pages = num_pages;
+  info->dtype = dtype;
+  info->kernel = mfma ? 1 : 0;
+  info->tile_rows = max_r <= 16 ? 16 : 32;
+  info->chunk_tokens = (int32_t)std::min<int64_t>(chunk, INT32_MAX);
+  info->plan_ints = (int32_t)off;
+  info->off_items = (int32_t)off_items;
+  info->off_qindex = (int32_t)off_qindex;
+  info->off_pages = (int32_t)off_pages;
+  info->off_merge_q = (int32_t)off_mq;
+  info->off_merge_ptr = (int32_t)off_mp;
+  info->off_merge_rows = (int32_t)off_mr;
+  info->partial_bytes = (int64_t)rows * hq * (d + 1) * 4;
+  info->kv_bytes = valid_tokens * hkv * d * es * 2;
+  info->qo_bytes = (int64_t)num_queries * hq * d * es * 2;
+  info->flops = flops;
+  return BE_OK;
+}
+
+// ================================================================== host: run
+template <typename T>
+static int launch_attn(const be_attn_plan_info* info, AttnArgs& a, hipStream_t st) {
+  const dim3 grid(info->num_items, info->num_kv_heads);
+  if (info->kernel == 1) {
+    if constexpr (sizeof(T) == 2) {
+      const bool one = info->tile_rows <= 16;
+      switch (info->head_dim) {
+        case 64:  one ? attn_mfma_kernel<T, 64, 1><<<grid, 256, 0, st>>>(a) : attn_mfma_kernel<T, 64, 2><<<grid, 256, 0, st>>>(a); break;
+        case 128: one ? attn_mfma_kernel<T, 128, 1><<<grid, 256, 0, st>>>(a) : attn_mfma_kernel<T, 128, 2><<<grid, 256, 0, st>>>(a); break;
+        case 256: one ? attn_mfma_kernel<T, 256, 1><<<grid, 256, 0, st>>>(a) : attn_mfma_kernel<T, 256, 2><<<grid, 256, 0, st>>>(a); break;
+        default: return fail(BE_ERR_UNSUPPORTED, "head_dim %d", info->head_dim);
+      }
+    } else {
+      return fail(BE_ERR_UNSUPPORTED, "MFMA kernel needs fp16/bf16 storage");
+    }
+  } else {
+    switch (info->head_dim) {
+      case 64: attn_valu_kernel<T, 64><<<grid, 256, 0, st>>>(a); break;
+      case 128: attn_valu_kernel<T, 128><<<grid, 256, 0, st>>>(a); break;
+      case 256: attn_valu_kernel<T, 256><<<grid, 256, 0, st>>>(a); break;
+      default: return fail(BE_ERR_UNSUPPORTED, "head_dim %d", info->head_dim);
+    }
+  }
+  BE_HIP_CHECK(hipGetLastError());
+  return BE_OK;
+}
+
+template <typename T>
+static int launch_merge(const be_attn_plan_info* info, MergeArgs& m, hipStream_t st) {
+  const dim3 grid(info->num_merge, (info->num_qo_heads + 3) / 4);
+  switch (info->head_dim) {
+    case 64: merge_kernel<T, 64><<<grid, 256, 0, st>>>(m); break;
+    case 128: merge_kernel<T, 128><<<grid, 256, 0, st>>>(m); break;
+    case 256: merge_kernel<T, 256><<<grid, 256, 0, st>>>(m); break;
+    default: return fail(BE_ERR_UNSUPPORTED, "head_dim %d", info->head_dim);
+  }
+  BE_HIP_CHECK(hipGetLastError());
+  return BE_OK;
+}
+
+int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials, const void* q,
+             int64_t q_sn, int64_t q_sh, const void* kv, void* out, int64_t o_sn, int64_t o_sh,
+             float* lse, float sm_scale, void* stream) {
+  BE_REQUIRE(info && plan, "null plan");
+  BE_REQUIRE(q && kv && out, "null q / kv / out");
+  BE_REQUIRE(info->num_part_rows == 0 || partials, "plan needs %lld bytes of partial scratch", (long long)info->partial_bytes);
+  BE_REQUIRE(info->num_qo_heads % info->num_kv_heads == 0, "corrupt plan info");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t rows = info->num_part_rows;
+  AttnArgs a;
+  a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;
+  a.kv = kv; a.out = out; a.o_sn = o_sn; a.o_sh = o_sh; a.out_lse = lse;
+  a.part_o = reinterpret_cast<float*>(partials);
+  a.part_lse = a.part_o + rows * info->num_qo_heads * info->head_dim;
+  a.items = reinterpret_cast<const WorkItem*>(plan + info->off_items);
+  a.q_index = plan + info->off_qindex;
+  a.pages = plan + info->off_pages;
+  a.page_size = info->page_size;
+  a.hkv = info->num_kv_heads;
+  a.hq = info->num_qo_heads;
+  a.g = info->num_qo_heads / info->num_kv_heads;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  int rc = BE_OK;
+  if (info->num_items > 0) {
+    switch (info->dtype) {
+      case BE_F32: rc = launch_attn<float>(info, a, st); break;
+      case BE_F16: rc = launch_attn<f16_t>(info, a, st); break;
+      case BE_BF16: rc = launch_attn<bf16_t>(info, a, st); break;
+      default: return fail(BE_ERR_INVALID, "dtype %d", info->dtype);
+    }
+    if (rc) return rc;
+  }
+  if (info->num_merge > 0) {
+    MergeArgs m;
+    m.part_o = a.part_o; m.part_lse = a.part_lse;
+    m.merge_q = plan + info->off_merge_q;
+    m.merge_ptr = plan + info->off_merge_ptr;
+    m.merge_rows = plan + info->off_merge_rows;
+    m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse; m.hq = info->num_qo_heads;
+    switch (info->dtype) {
+      case BE_F32: rc = launch_merge<float>(info, m, st); break;
+      case BE_F16: rc = launch_merge<f16_t>(info, m, st); break;
+      case BE_BF16: rc = launch_merge<bf16_t>(info, m, st); break;
+    }
+  }
+  return rc;
+}
+
+}  // namespace be
+
+extern "C" {
+
+int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int num_qo_heads,
+                 int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype, int flags,
+                 int num_cus, int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info) {
+  return be::attn_plan(levels, num_levels, num_queries, num_qo_heads, num_kv_heads, head_dim, page_size,
+                       num_pages, dtype, flags, num_cus, host_plan, host_plan_capacity, info);
+}
+
+int be_attn_run(const be_attn_plan_info* info, const int32_t* dev_plan, void* partials, const void* q,
+                int64_t q_stride_n, int64_t q_stride_h, const void* kv_layer, void* out, int64_t o_stride_n,
+                int64_t o_stride_h, float* lse, float sm_scale, void* stream) {
+  return be::attn_run(info, dev_plan, partials, q, q_stride_n, q_stride_h, kv_layer, out, o_stride_n,
+                      o_stride_h, lse, sm_scale, stream);
+}
+
+int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, const float* lse_b, float* o_out,
+                    float* lse_out, int n, int heads, int head_dim, void* stream) {
+  BE_REQUIRE(o_a && lse_a && o_b && lse_b && o_out && lse_out, "null pointer");
+  BE_REQUIRE(n >= 0 && heads > 0 && head_dim > 0, "bad shape");
+  const int64_t rows = (int64_t)n * heads;
+  const int64_t total = rows * head_dim;
+  if (total == 0) return BE_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  be::merge2_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(o_a, lse_a, o_b, lse_b, o_out, lse_out,
+                                                              (int)rows, head_dim);
+  BE_HIP_CHECK(hipGetLastError());
+  return BE_OK;
+}
+
+}  // extern "C"

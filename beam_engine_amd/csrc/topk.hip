@@ -1,0 +1,374 @@
+// Beam token selection for one decode step on gfx950.
+//
+// Reference: log_softmax + topk(2B) per row (beam.py:269-276) and the global
+// top-B of VanillaBeamSearchStrategy.select_candidates with float64 scores and
+// a stable sort (beam_strategy.py:433-488).  Floating-point contract (shared
+// with the CPU restatement used as test oracle):
+//   x'   = round_dtype(x * inv_temp)                   (only if inv_temp != 1)
+//   m    = max_i x'_i
+//   S    = sum_i exp(fl64(x'_i - m))                    (float64)
+//   L    = fl32(ln S)
+//   logp = round_dtype(fl32(fl32(x'_i - m) - L))
+// Order: within a row (logp desc, index asc); in the pool (total desc,
+// row*k + rank asc) with total = parent_score + (double)logp.
+//
+// Pass 1  grid (S, N): per segment max and float64 exp-sum.
+// Pass 2  grid (S, N): per segment, exact k best by radix select over the
+//         order-preserving uint32 key of logp, ties to the lowest index.
+// Pass 3  grid (N):    rank the row's S*k candidates -> sorted row top-k.
+// Pass 4  grid (1):    radix select the beam best of the N*k pool (uint64 key
+//         of the float64 total, ties to the lowest pool position), emitted in
+//         pool-position order = grouped by row, children in selection order.
+
+#include <math.h>
+
+#include "common.h"
+
+namespace be {
+
+constexpr int kTopkThreads = 256;
+constexpr int kMaxSegLen = 8192;     // keys staged in LDS per segment
+constexpr int kMaxSegs = 64;
+constexpr int kMaxRowCand = 4096;    // S * k bound for pass 3
+constexpr int kMaxPool = 8192;       // N * k bound for pass 4
+constexpr int kMaxK = 256;
+
+struct TopkGeom {
+  int segs, seg_len;
+};
+
+static TopkGeom topk_geom(int n_rows, int vocab, int k) {
+  int segs = (vocab + kMaxSegLen - 1) / kMaxSegLen;
+  const int want = (512 + n_rows - 1) / n_rows;          // about two workgroups per CU
+  if (want > segs) segs = want;
+  const int by_k = (vocab + k - 1) / k;                   // every segment holds >= k elements
+  if (segs > by_k) segs = by_k;
+  if (segs > kMaxSegs) segs = kMaxSegs;
+  if (segs * k > kMaxRowCand) segs = kMaxRowCand / k;
+  if (segs < 1) segs = 1;
+  int seg_len = (vocab + segs - 1) / segs;
+  segs = (vocab + seg_len - 1) / seg_len;
+  return TopkGeom{segs, seg_len};
+}
+
+template <typename T>
+__device__ __forceinline__ float load_logit(const T* p) { return to_f32(*p); }
+
+template <typename T>
+__device__ __forceinline__ float round_to(float x);
+template <> __device__ __forceinline__ float round_to<float>(float x) { return x; }
+template <> __device__ __forceinline__ float round_to<bf16_t>(float x) {
+  return __uint_as_float(((uint32_t)f32_to_bf16_bits(x)) << 16);
+}
+template <> __device__ __forceinline__ float round_to<f16_t>(float x) { return (float)(_Float16)x; }
+
+template <typename T>
+__device__ __forceinline__ float scaled(float x, float inv_temp) {
+  return (inv_temp == 1.0f) ? x : round_to<T>(__fmul_rn(x, inv_temp));
+}
+
+__device__ __forceinline__ uint32_t fkey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint64_t dkey(double f) {
+  const uint64_t u = (uint64_t)__double_as_longlong(f);
+  return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Exact block-wide selection of the k largest keys, ties broken by the lowest
+// position.  keys[0..n) live in LDS.  Writes min(k, n) positions (unordered)
+// to out_pos (LDS) and returns that count.  All 256 threads must call it.
+template <typename K>
+__device__ int block_select(const K* keys, int n, int k, int* out_pos, int* hist /*4*256*/,
+                            int* suf /*257*/, int* misc /*4*/) {
+  const int tid = threadIdx.x, w = tid >> 6;
+  if (n <= k) {
+    for (int i = tid; i < n; i += kTopkThreads) out_pos[i] = i;
+    __syncthreads();
+    return n;
+  }
+  K prefix = 0, mask = 0;
+  int krem = k;
+  for (int shift = (int)sizeof(K) * 8 - 8; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 4 * 256; i += kTopkThreads) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += kTopkThreads) {
+      const K key = keys[i];
+      if ((key & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((key >> shift) & 255)], 1);
+    }
+    __syncthreads();
+    suf[tid] = hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid];
+    if (tid == 0) suf[256] = 0;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {     // suffix sums: suf[d] = #digits >= d
+      const int v = suf[tid] + ((tid + off < 256) ? suf[tid + off] : 0);
+      __syncthreads();
+      suf[tid] = v;
+      __syncthreads();
+    }
+    if (suf[tid] >= krem && suf[tid + 1] < krem) {   // unique digit
+      misc[0] = tid;
+      misc[1] = suf[tid + 1];
+    }
+    __syncthreads();
+    const int digit = misc[0];
+    krem -= misc[1];
+    prefix |= ((K)digit) << shift;
+    mask |= ((K)255) << shift;
+    __syncthreads();
+  }
+  // keys > prefix: exactly k - krem of them; keys == prefix: the krem lowest positions
+  if (tid == 0) misc[2] = 0;
+  __syncthreads();
+  const int per = (n + kTopkThreads - 1) / kTopkThreads;
+  const int b = tid * per, e = min(n, b + per);
+  int eq = 0;
+  for (int i = b; i < e; ++i) {
+    const K key = keys[i];
+    if (key > prefix) out_pos[atomicAdd(&misc[2], 1)] = i;
+    else if (key == prefix) ++eq;
+  }
+  // exclusive scan of eq over threads (in position order)
+  suf[tid] = eq;
+  __syncthreads();
+  for (int off = 1; off < kTopkThreads; off <<= 1) {
+    const int v = suf[tid] + ((tid >= off) ? suf[tid - off] : 0);
+    __syncthreads();
+    suf[tid] = v;
+    __syncthreads();
+  }
+  int rank = suf[tid] - eq;
+  const int ngt = k - krem;
+  for (int i = b; i < e && rank < krem; ++i)
+    if (keys[i] == prefix) out_pos[ngt + rank++] = i;
+  __syncthreads();
+  return k;
+}
+
+// ---------------------------------------------------------------- pass 1
+template <typename T>
+__global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                 int seg_len, float inv_temp, float* seg_max,
+                                                                 double* seg_sum) {
+  __shared__ float redf[4];
+  __shared__ double redd[4];
+  const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
+  const T* row = logits + (int64_t)r * row_stride;
+  const int b = s * seg_len, e = min(vocab, b + seg_len);
+  float m = -INFINITY;
+  for (int i = b + threadIdx.x; i < e; i += kTopkThreads) m = fmaxf(m, scaled<T>(load_logit(row + i), inv_temp));
+  m = block_max(m, redf);
+  double acc = 0.0;
+  const double md = (double)m;
+  for (int i = b + threadIdx.x; i < e; i += kTopkThreads)
+    acc += exp((double)scaled<T>(load_logit(row + i), inv_temp) - md);
+  acc = block_sum_d(acc, redd);
+  if (threadIdx.x == 0) {
+    seg_max[(int64_t)r * segs + s] = m;
+    seg_sum[(int64_t)r * segs + s] = acc;
+  }
+}
+
+// Row max m and L = fl32(ln S) from the segment statistics (fixed order).
+__device__ __forceinline__ void row_norm(const float* seg_max, const double* seg_sum, int r, int segs, float& m,
+                                         float& L) {
+  float mm = -INFINITY;
+  for (int s = 0; s < segs; ++s) mm = fmaxf(mm, seg_max[(int64_t)r * segs + s]);
+  double S = 0.0;
+  for (int s = 0; s < segs; ++s)
+    S += seg_sum[(int64_t)r * segs + s] * exp((double)seg_max[(int64_t)r * segs + s] - (double)mm);
+  m = mm;
+  L = (float)log(S);
+}
+
+template <typename T>
+__device__ __forceinline__ float logp_of(float xs, float m, float L) {
+  return round_to<T>(__fsub_rn(__fsub_rn(xs, m), L));
+}
+
+// ---------------------------------------------------------------- pass 2
+template <typename T>
+__global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                   int seg_len, float inv_temp, int k,
+                                                                   const float* seg_max, const double* seg_sum,
+                                                                   float* cand_val, int32_t* cand_idx) {
+  __shared__ uint32_t keys[kMaxSegLen];
+  __shared__ int pos[kMaxK];
+  __shared__ int hist[4 * 256];
+  __shared__ int suf[257];
+  __shared__ int misc[4];
+  const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
+  float m, L;
+  row_norm(seg_max, seg_sum, r, segs, m, L);
+  const T* row = logits + (int64_t)r * row_stride;
+  const int b = s * seg_len, e = min(vocab, b + seg_len), n = e - b;
+  for (int i = threadIdx.x; i < n; i += kTopkThreads)
+    keys[i] = fkey(logp_of<T>(scaled<T>(load_logit(row + b + i), inv_temp), m, L));
+  __syncthreads();
+  const int cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
+  float* cv = cand_val + ((int64_t)r * segs + s) * k;
+  int32_t* ci = cand_idx + ((int64_t)r * segs + s) * k;
+  for (int j = threadIdx.x; j < k; j += kTopkThreads) {
+    if (j < cnt) {
+      const int p = pos[j];
+      const uint32_t key = keys[p];
+      const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+      cv[j] = __uint_as_float(u);
+      ci[j] = b + p;
+    } else {
+      cv[j] = -INFINITY;
+      ci[j] = -1;   // empty slot (segment shorter than k)
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pass 3
+__global__ __launch_bounds__(kTopkThreads) void topk_row_kernel(int segs, int k, const float* cand_val,
+                                                               const int32_t* cand_idx, float* row_vals,
+                                                               int32_t* row_idx) {
+  __shared__ uint64_t key[kMaxRowCand];
+  const int r = blockIdx.x;
+  const int c = segs * k;
+  const float* cv = cand_val + (int64_t)r * c;
+  const int32_t* ci = cand_idx + (int64_t)r * c;
+  for (int i = threadIdx.x; i < c; i += kTopkThreads) {
+    const int32_t idx = ci[i];
+    key[i] = (idx < 0) ? 0ull : (((uint64_t)fkey(cv[i])) << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < c; i += kTopkThreads) {
+    const uint64_t me = key[i];
+    if (me == 0ull) continue;
+    int rank = 0;
+    for (int j = 0; j < c; ++j) rank += (key[j] > me);
+    if (rank < k) {
+      row_vals[(int64_t)r * k + rank] = cv[i];
+      row_idx[(int64_t)r * k + rank] = ci[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pass 4
+__global__ __launch_bounds__(kTopkThreads) void topk_global_kernel(int n_rows, int k, int beam,
+                                                                  const double* parent, const float* row_vals,
+                                                                  const int32_t* row_idx, int32_t* out_parent,
+                                                                  int32_t* out_token, double* out_score) {
+  __shared__ uint64_t keys[kMaxPool];
+  __shared__ int pos[kMaxK];
+  __shared__ int hist[4 * 256];
+  __shared__ int suf[257];
+  __shared__ int misc[4];
+  const int n = n_rows * k;
+  for (int i = threadIdx.x; i < n; i += kTopkThreads) {
+    const int r = i / k;
+    keys[i] = dkey(parent[r] + (double)row_vals[i]);
+  }
+  __syncthreads();
+  const int cnt = block_select<uint64_t>(keys, n, beam, pos, hist, suf, misc);
+  // emit in pool-position order
+  for (int i = threadIdx.x; i < cnt; i += kTopkThreads) {
+    const int p = pos[i];
+    int rank = 0;
+    for (int j = 0; j < cnt; ++j) rank += (pos[j] < p);
+    const int r = p / k;
+    out_parent[rank] = r;
+    out_token[rank] = row_idx[p];
+    out_score[rank] = parent[r] + (double)row_vals[p];
+  }
+  for (int i = cnt + threadIdx.x; i < beam; i += kTopkThreads) {
+    out_parent[i] = -1;
+    out_token[i] = -1;
+    out_score[i] = -INFINITY;
+  }
+}
+
+}  // namespace be
+
+extern "C" {
+
+int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k) {
+  if (n_rows <= 0 || vocab <= 0 || k <= 0) return 0;
+  const be::TopkGeom geo = be::topk_geom(n_rows, vocab, k);
+  const int64_t ns = (int64_t)n_rows * geo.segs;
+  return ns * 4 + ns * 8 + ns * k * 4 + ns * k * 4 + 256;
+}
+
+int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, float inv_temp, int k,
+                 const double* parent_scores, int beam, float* row_vals, int32_t* row_idx, int32_t* out_parent,
+                 int32_t* out_token, double* out_score, void* workspace, int64_t workspace_bytes, void* stream) {
+  BE_REQUIRE(logits && row_vals && row_idx, "null pointer");
+  BE_REQUIRE(dtype == BE_F32 || dtype == BE_F16 || dtype == BE_BF16, "unknown dtype %d", dtype);
+  BE_REQUIRE(n_rows > 0 && vocab > 0, "empty logits");
+  BE_REQUIRE(k >= 1 && k <= vocab, "k = %d outside [1, vocab = %d]", k, vocab);
+  if (k > be::kMaxK) return be::fail(BE_ERR_UNSUPPORTED, "k = %d exceeds %d", k, be::kMaxK);
+  BE_REQUIRE(row_stride >= vocab, "row stride %lld < vocab %d", (long long)row_stride, vocab);
+  BE_REQUIRE(inv_temp > 0.f && isfinite(inv_temp), "inverse temperature must be positive and finite");
+  BE_REQUIRE(beam >= 0, "beam must be >= 0");
+  if (beam > 0) {
+    BE_REQUIRE(parent_scores && out_parent && out_token && out_score, "null selection output");
+    if (beam > be::kMaxK) return be::fail(BE_ERR_UNSUPPORTED, "beam = %d exceeds %d", beam, be::kMaxK);
+    if ((int64_t)n_rows * k > be::kMaxPool)
+      return be::fail(BE_ERR_UNSUPPORTED, "pool %d x %d exceeds %d entries", n_rows, k, be::kMaxPool);
+  }
+  const int64_t need = be_beam_topk_workspace_bytes(n_rows, vocab, k);
+  if (!workspace || workspace_bytes < need)
+    return be::fail(BE_ERR_CAPACITY, "top-k workspace needs %lld bytes", (long long)need);
+  if (n_rows > 65535) return be::fail(BE_ERR_UNSUPPORTED, "n_rows %d exceeds 65535", n_rows);
+  const be::TopkGeom geo = be::topk_geom(n_rows, vocab, k);
+  if (geo.seg_len > be::kMaxSegLen || geo.segs * k > be::kMaxRowCand)
+    return be::fail(BE_ERR_UNSUPPORTED, "vocab %d with k %d needs segments of %d > %d logits", vocab, k, geo.seg_len,
+                    be::kMaxSegLen);
+  const int64_t ns = (int64_t)n_rows * geo.segs;
+  char* ws = reinterpret_cast<char*>(workspace);
+  double* seg_sum = reinterpret_cast<double*>(ws);
+  float* seg_max = reinterpret_cast<float*>(ws + ns * 8);
+  float* cand_val = reinterpret_cast<float*>(ws + ns * 12);
+  int32_t* cand_idx = reinterpret_cast<int32_t*>(ws + ns * 12 + ns * k * 4);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(geo.segs, n_rows);
+  switch (dtype) {
+#define BE_TOPK_CASE(DT, TY)                                                                                   \
+  case DT:                                                                                                     \
+    be::topk_stats_kernel<TY><<<grid, be::kTopkThreads, 0, st>>>(reinterpret_cast<const TY*>(logits), row_stride, \
+                                                                 vocab, geo.seg_len, inv_temp, seg_max, seg_sum); \
+    be::topk_segment_kernel<TY><<<grid, be::kTopkThreads, 0, st>>>(reinterpret_cast<const TY*>(logits),        \
+                                                                   row_stride, vocab, geo.seg_len, inv_temp, k,   \
+                                                                   seg_max, seg_sum, cand_val, cand_idx);       \
+    break;
+    BE_TOPK_CASE(BE_F32, float)
+    BE_TOPK_CASE(BE_F16, be::f16_t)
+    BE_TOPK_CASE(BE_BF16, be::bf16_t)
+#undef BE_TOPK_CASE
+  }
+  BE_HIP_CHECK(hipGetLastError());
+  be::topk_row_kernel<<<n_rows, be::kTopkThreads, 0, st>>>(geo.segs, k, cand_val, cand_idx, row_vals, row_idx);
+  BE_HIP_CHECK(hipGetLastError());
+  if (beam > 0) {
+    be::topk_global_kernel<<<1, be::kTopkThreads, 0, st>>>(n_rows, k, beam, parent_scores, row_vals, row_idx,
+                                                          out_parent, out_token, out_score);
+    BE_HIP_CHECK(hipGetLastError());
+  }
+  return BE_OK;
+}
+
+}  // extern "C"

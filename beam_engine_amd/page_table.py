@@ -1,0 +1,202 @@
+"""Paged KV cache: drop-in for the reference's ``PageTable`` (src/beam_engine/page_table.py).
+
+Same constructor, attributes and methods.  MI355X-first differences:
+
+* All layers live in one HBM allocation ``kv_pool`` of shape
+  ``[L, P, 2, page_size, Hkv, D]``; ``kv_cache_at_layer[l]`` is the
+  contiguous per-layer view with the reference's layout (page_table.py:62-72).
+  A fork copy of every layer is then one kernel launch (``be_page_copy``).
+* The FIFO free list is a deque (O(1) ``pop(0)``) with the same order.
+* Pages carry a reference count: ``allocate_block`` sets it to 1,
+  ``share_block`` adds a holder, ``free_block`` drops one and returns the page
+  to the free list at zero.  With one holder per page (the reference's trie)
+  this is exactly the reference's allocate / free behaviour.
+* ``write_blocks_vectorized`` calls the HIP append kernel instead of
+  FlashInfer's ``append_paged_kv_cache``.
+* ``copy_block`` can defer the data copy (``defer_copies()`` context) so that
+  all forks of a decode step are copied in a single launch; page ids are
+  allocated immediately, in the reference's order.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import logging
+from collections import deque
+from typing import List, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+
+logger = logging.getLogger(__name__)
+
+
+class PageCopyError(ValueError, TypeError):
+    """Bad ``copy_block`` arguments.  The reference raises a bare string there
+    (page_table.py:97-100), which Python 3 turns into a TypeError; this error
+    is both a ValueError and a TypeError so either handler catches it."""
+
+
+class PageTable:
+    def __init__(self, layer_num: int, page_size: int = 8, max_num_pages: int = 1024, head_num: int = 32,
+                 head_dim: int = 128, v_head_dim: Optional[int] = None, device: torch.device = None,
+                 store_dtype: torch.dtype = torch.float16):
+        if v_head_dim is not None and v_head_dim != head_dim:
+            raise ValueError("the paged layout stores K and V with one head_dim")
+        self.layer_num = layer_num
+        self.page_size = page_size
+        self.max_num_pages = max_num_pages
+        self.head_num = head_num
+        self.head_dim = head_dim
+        self.v_head_dim = v_head_dim or head_dim
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self.store_dtype = store_dtype
+
+        self.free_pages = deque(range(max_num_pages))
+        self.allocated_pages = set()
+        self._refs = {}
+        self._pending: List[Tuple[int, int, int]] = []
+        self._defer = 0
+
+        self.kv_pool = torch.zeros((layer_num, max_num_pages, 2, page_size, head_num, head_dim),
+                                   dtype=store_dtype, device=self.device)
+        self.kv_cache_at_layer: List[torch.Tensor] = [self.kv_pool[l] for l in range(layer_num)]
+        self.layer_stride_bytes = self.kv_pool.stride(0) * self.kv_pool.element_size()
+        logger.info("Initialized PageTable: %d layers, %d pages of size %d", layer_num, max_num_pages, page_size)
+
+    # ------------------------------------------------------------ allocator
+    def allocate_block(self) -> int:
+        """Pop the oldest free page (page_table.py:77-94)."""
+        if not self.free_pages:
+            raise MemoryError("No free pages available")
+        page = self.free_pages.popleft()
+        self.allocated_pages.add(page)
+        self._refs[page] = 1
+        return page
+
+    def share_block(self, page_idx: int) -> int:
+        """Add a holder to an allocated page; returns the new count."""
+        if page_idx not in self.allocated_pages:
+            raise ValueError(f"Page {page_idx} is not allocated")
+        self._refs[page_idx] += 1
+        return self._refs[page_idx]
+
+    def ref_count(self, page_idx: int) -> int:
+        return self._refs.get(page_idx, 0)
+
+    def free_block(self, page_idx: int) -> None:
+        """Drop one holder; at zero the page goes to the back of the free list
+        (page_table.py:110-124).  Freeing an unallocated page only warns."""
+        if page_idx not in self.allocated_pages:
+            logger.warning("Page %s is not allocated", page_idx)
+            return
+        self._refs[page_idx] -= 1
+        if self._refs[page_idx] > 0:
+            return
+        del self._refs[page_idx]
+        self.allocated_pages.remove(page_idx)
+        self.free_pages.append(page_idx)
+
+    def num_free_pages(self) -> int:
+        return len(self.free_pages)
+
+    # ------------------------------------------------------------ copies
+    def copy_block(self, page_idx: int, length: int) -> int:
+        """Allocate a page and copy the first ``length`` slots of K and V of
+        ``page_idx`` into it on every layer (page_table.py:96-106)."""
+        if length > self.page_size or length < 0:
+            raise PageCopyError("length cannot be larger than page size")
+        if page_idx < 0 or page_idx >= self.max_num_pages:
+            raise PageCopyError("page idx out of bound")
+        new_page = self.allocate_block()
+        self._pending.append((page_idx, new_page, length))
+        if not self._defer:
+            self.flush_copies()
+        return new_page
+
+    @contextlib.contextmanager
+    def defer_copies(self):
+        """Collect copy_block data copies and issue them in one launch on exit."""
+        self._defer += 1
+        try:
+            yield self
+        finally:
+            self._defer -= 1
+            if not self._defer:
+                self.flush_copies()
+
+    def flush_copies(self) -> int:
+        """Issue every pending fork copy in one be_page_copy launch."""
+        if not self._pending:
+            return 0
+        todo, self._pending = self._pending, []
+        arr = torch.tensor(np.asarray(todo, dtype=np.int32).T.copy(), dtype=torch.int32)
+        dev = arr.to(self.device, non_blocking=False)
+        lib = _lib.load()
+        rc = lib.be_page_copy(self.kv_pool.data_ptr(), self.layer_stride_bytes, self.layer_num,
+                              _lib.dtype_code(self.store_dtype), self.max_num_pages, self.page_size,
+                              self.head_num, self.head_dim, dev[0].data_ptr(), dev[1].data_ptr(),
+                              dev[2].data_ptr(), len(todo), None, _lib.stream_ptr(self.device))
+        _lib.check(rc, "page copy")
+        return len(todo)
+
+    # ------------------------------------------------------------ writes
+    def write_block(self, layer: int, page_idx: int, key: torch.Tensor, value: torch.Tensor, index: int) -> None:
+        """Prefill write of ``key``/``value`` ``[n, Hkv, D]`` at slots
+        index..index+n of one page (page_table.py:126-165)."""
+        assert key.shape == value.shape
+        assert key.shape[0] + index <= self.page_size, \
+            f"Cannot fit {key.shape[0]} tokens at index {index} in page size {self.page_size}"
+        if layer >= self.layer_num:
+            raise ValueError(f"Layer {layer} out of range (max: {self.layer_num - 1})")
+        if page_idx not in self.allocated_pages:
+            raise ValueError(f"Page {page_idx} is not allocated")
+        if index > self.page_size:
+            raise ValueError(f"Index {index} exceeds page size {self.page_size}")
+        n = key.shape[0]
+        if n > 0:
+            self.kv_cache_at_layer[layer][page_idx, 0, index:index + n] = key
+            self.kv_cache_at_layer[layer][page_idx, 1, index:index + n] = value
+
+    def write_blocks_vectorized(self, layer: int, page_indices: torch.Tensor, keys: torch.Tensor,
+                                values: torch.Tensor, indices: torch.Tensor,
+                                batch_indices: Optional[torch.Tensor] = None,
+                                kv_indptr: Optional[torch.Tensor] = None) -> None:
+        """Append one token per candidate: ``kv[page_indices[i], :, indices[i]] = (keys[i], values[i])``
+        (page_table.py:167-209).  ``batch_indices``/``kv_indptr`` are accepted
+        for signature compatibility (the reference passes the identity layout)."""
+        if layer < 0 or layer >= self.layer_num:
+            raise ValueError(f"Layer {layer} out of range (max: {self.layer_num - 1})")
+        n = keys.shape[0]
+        if keys.shape != values.shape or keys.dim() != 3 or keys.shape[1:] != (self.head_num, self.head_dim):
+            raise ValueError(f"keys/values must be [N, {self.head_num}, {self.head_dim}]")
+        if keys.dtype != self.store_dtype or values.dtype != self.store_dtype:
+            raise ValueError(f"keys/values must be {self.store_dtype}")
+        if keys.stride(2) != 1 or values.stride(2) != 1:
+            keys, values = keys.contiguous(), values.contiguous()
+        for t, nm in ((page_indices, "page_indices"), (indices, "indices"), (keys, "keys")):
+            _lib.require_device(t, nm)
+        page_indices = page_indices.to(torch.int32)
+        indices = indices.to(torch.int32)
+        if page_indices.numel() < n or indices.numel() < n:
+            raise ValueError("page_indices / indices shorter than keys")
+        lib = _lib.load()
+        rc = lib.be_kv_append(self.kv_cache_at_layer[layer].data_ptr(), _lib.dtype_code(self.store_dtype),
+                              self.max_num_pages, self.page_size, self.head_num, self.head_dim,
+                              page_indices.data_ptr(), indices.data_ptr(), keys.data_ptr(), keys.stride(0),
+                              keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1), n, None,
+                              _lib.stream_ptr(self.device))
+        _lib.check(rc, "kv append")
+
+    # ------------------------------------------------------------ flat views
+    def get_k_buffer(self, layer: int) -> torch.Tensor:
+        """K of every slot as ``[P * page, Hkv, D]`` (a copy, as in the reference,
+        page_table.py:211-226; the HIP attention path never needs it)."""
+        return self.kv_cache_at_layer[layer][:, 0].reshape(self.max_num_pages * self.page_size,
+                                                           self.head_num, self.head_dim)
+
+    def get_v_buffer(self, layer: int) -> torch.Tensor:
+        return self.kv_cache_at_layer[layer][:, 1].reshape(self.max_num_pages * self.page_size,
+                                                           self.head_num, self.head_dim)

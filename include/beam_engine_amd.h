@@ -1,0 +1,170 @@
+/*
+ * beam_engine_amd -- C ABI of the MI355X (gfx950) beam-decode hot path.
+ *
+ * Plain C: no C++ types, no exceptions, no torch types.  Device pointers are
+ * passed as void* / typed pointers, streams as void* (a hipStream_t, NULL for
+ * the default stream).  Every function returns a be_status; on failure
+ * be_last_error() returns a message for the calling thread.  The library
+ * never allocates or frees device memory: the caller owns every buffer,
+ * including the workspace.
+ *
+ * Reference interfaces replaced (paths relative to brian030128/beam_engine):
+ *   be_kv_append      flashinfer.page.append_paged_kv_cache as called by
+ *                     PageTable.write_blocks_vectorized (src/beam_engine/page_table.py:167-209)
+ *   be_page_copy      PageTable.copy_block's per-layer copy loop
+ *                     (src/beam_engine/page_table.py:96-106), batched over forks and layers
+ *   be_attn_plan      MultiLevelCascadeAttentionWrapper.plan
+ *                     (src/beam_engine/models/modeling_llama.py:732-755) and the FastTree
+ *                     host metadata pass (src/beam_engine/attention/fasttree/preparation.py:11-225)
+ *   be_attn_run       MultiLevelCascadeAttentionWrapper.run (models/modeling_llama.py:362) and
+ *                     fasttree_decode (src/beam_engine/attention/fasttree/kernel.py:288-348)
+ *   be_merge_states   the log-sum-exp merge inside the cascade wrapper and FastTree stage 2
+ *                     (src/beam_engine/attention/fasttree/kernel.py:188-285)
+ *   be_beam_topk      log_softmax + per-row topk (src/beam_engine/beam.py:269-276, prefill
+ *                     :105-141) and VanillaBeamSearchStrategy.select_candidates
+ *                     (src/beam_engine/beam_strategy.py:433-488)
+ */
+#ifndef BEAM_ENGINE_AMD_H
+#define BEAM_ENGINE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage dtypes of K/V, queries, outputs and logits. */
+enum be_dtype { BE_F32 = 0, BE_F16 = 1, BE_BF16 = 2 };
+
+enum be_status {
+  BE_OK = 0,
+  BE_ERR_INVALID = 1,     /* bad argument or inconsistent indices (ValueError) */
+  BE_ERR_HIP = 2,         /* a HIP runtime call failed (RuntimeError)          */
+  BE_ERR_CAPACITY = 3,    /* caller buffer / workspace too small               */
+  BE_ERR_UNSUPPORTED = 4  /* shape or dtype this build has no kernel for       */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int be_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* be_last_error(void);
+
+/* ------------------------------------------------------------------ KV cache
+ * Per-layer cache layout (the reference's FlashInfer "NHD" layout,
+ * page_table.py:62-72):  [num_pages, 2, page_size, num_kv_heads, head_dim],
+ * K at index 0, V at index 1, head_dim contiguous.
+ *
+ * be_kv_append: for i < n, writes k[i] and v[i] ([num_kv_heads, head_dim] each,
+ * element strides k_stride_n/k_stride_h, v_stride_n/v_stride_h, head_dim
+ * contiguous) into slot pos[i] of page page_idx[i] of kv_layer.
+ * Replaces append_paged_kv_cache (page_table.py:199-209).  num_pages bounds
+ * the page ids (checked on the device: out-of-range entries are skipped and
+ * counted in *err_count when err_count is non-NULL, a device int32).
+ */
+int be_kv_append(void* kv_layer, int dtype, int num_pages, int page_size, int num_kv_heads,
+                 int head_dim, const int32_t* page_idx, const int32_t* pos, const void* k,
+                 int64_t k_stride_n, int64_t k_stride_h, const void* v, int64_t v_stride_n,
+                 int64_t v_stride_h, int n, int32_t* err_count, void* stream);
+
+/* be_page_copy: for every c < n and every layer l < num_layers, copies the
+ * first len[c] slots of K and of V of page src[c] into page dst[c].  Layer l's
+ * cache starts at (char*)kv_pool + l * layer_stride_bytes.  src/dst/len are
+ * device int32 arrays.  Replaces copy_block's loop over layers
+ * (page_table.py:96-106) with one launch for all forks of a step.
+ * Bounds (page ids < num_pages, 0 <= len <= page_size) are checked on the
+ * device; offending entries are skipped and counted in *err_count. */
+int be_page_copy(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int dtype,
+                 int num_pages, int page_size, int num_kv_heads, int head_dim,
+                 const int32_t* src, const int32_t* dst, const int32_t* len, int n,
+                 int32_t* err_count, void* stream);
+
+/* ------------------------------------------------------------------ attention
+ * One level of a cascade (FlashInfer's per-level index arrays as built by
+ * BeamState.get_cascade_input, src/beam_engine/beam_state.py:211-412): group
+ * j owns queries qo_indptr[j]..qo_indptr[j+1] and pages
+ * kv_indices[kv_indptr[j]..kv_indptr[j+1]]; every page but the last is full
+ * and the last holds last_page_len[j] tokens (0..page_size).  Host pointers.
+ */
+typedef struct be_level {
+  const int32_t* qo_indptr;      /* num_groups + 1 */
+  const int32_t* kv_indptr;      /* num_groups + 1 */
+  const int32_t* kv_indices;     /* kv_indptr[num_groups] */
+  const int32_t* last_page_len;  /* num_groups */
+  int32_t num_groups;
+} be_level;
+
+/* Plan flags. */
+#define BE_PLAN_FORCE_VALU 1     /* use the VALU kernel even where MFMA applies */
+
+/* Filled by be_attn_plan; passed back to be_attn_run unchanged. */
+typedef struct be_attn_plan_info {
+  int32_t num_items;       /* work items (grid.x of the attention kernel)      */
+  int32_t num_part_rows;   /* partial rows, each [Hq, D] fp32 + [Hq] fp32 lse  */
+  int32_t num_merge;       /* queries merged by the merge kernel               */
+  int32_t num_queries;
+  int32_t num_qo_heads, num_kv_heads, head_dim, page_size, num_pages, dtype;
+  int32_t kernel;          /* 0 = VALU, 1 = MFMA                               */
+  int32_t tile_rows;       /* rows (queries x GQA group) per MFMA tile: 16/32  */
+  int32_t chunk_tokens;    /* split-K chunk length                             */
+  int32_t plan_ints;       /* int32 words of the device plan                    */
+  int32_t off_items, off_qindex, off_pages, off_merge_q, off_merge_ptr, off_merge_rows;
+  int64_t partial_bytes;   /* device bytes needed for partial o + lse          */
+  int64_t kv_bytes;        /* algorithmic K+V bytes: distinct (page, head) valid tokens */
+  int64_t qo_bytes;        /* Q + O bytes                                       */
+  double flops;            /* 4 * D * sum_q sum_h kv_len(q)                     */
+} be_attn_plan_info;
+
+/* be_attn_plan (host only): validates the levels against num_queries,
+ * num_pages and page_size, splits every group into work items (query tiles x
+ * KV chunks) and writes the device plan into host_plan[0..info->plan_ints).
+ * The caller copies that prefix to device memory (stream-ordered before
+ * be_attn_run) and provides info->partial_bytes of device scratch.
+ * num_cus sizes the split-K chunking (pass the device's CU count). */
+int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int num_qo_heads,
+                 int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype,
+                 int flags, int num_cus, int32_t* host_plan, int64_t host_plan_capacity,
+                 be_attn_plan_info* info);
+
+/* be_attn_run: o[i, h] = softmax(sm_scale * q[i, h] . K^T) V over query i's
+ * groups on every level, merged by log-sum-exp; query head h reads KV head
+ * h / (Hq / Hkv).  q and out are [num_queries, Hq, D] with element strides
+ * (n, h) and D contiguous; out has the plan's dtype.  lse (optional, device
+ * float [num_queries, Hq]) receives the natural-log log-sum-exp; a query with
+ * no keys gets o = 0 and lse = -inf.  dev_plan is the device copy of the plan,
+ * partials points at info->partial_bytes of device scratch. */
+int be_attn_run(const be_attn_plan_info* info, const int32_t* dev_plan, void* partials,
+                const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* kv_layer,
+                void* out, int64_t o_stride_n, int64_t o_stride_h, float* lse, float sm_scale,
+                void* stream);
+
+/* be_merge_states: (o, lse) <- merge((o_a, lse_a), (o_b, lse_b)) for n x heads
+ * rows of head_dim; o_* are float [n, heads, D] contiguous, lse natural log.
+ * o_out/lse_out may alias o_a/lse_a. */
+int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, const float* lse_b,
+                    float* o_out, float* lse_out, int n, int heads, int head_dim, void* stream);
+
+/* ------------------------------------------------------------------ beam top-k
+ * be_beam_topk: one decode-step selection over logits [n_rows, vocab]
+ * (dtype, row stride in elements):
+ *   x' = round_dtype(x * inv_temp)   (skipped when inv_temp == 1)
+ *   logp = round_dtype(fl32(fl32(x' - max) - fl32(ln sum exp(x' - max))))
+ *          with the exponential sum accumulated in float64;
+ *   per row the k best (logp desc, index asc) -> row_vals/row_idx [n_rows, k];
+ *   when beam > 0: the beam best of the pool total = parent_scores[r] +
+ *   (double)row_vals[r, j] by (total desc, r*k + j asc), emitted grouped by
+ *   row ascending and, within a row, in selection order, into
+ *   out_parent/out_token (int32) and out_score (double) [beam].
+ * All pointers are device pointers.  workspace must hold
+ * be_beam_topk_workspace_bytes(n_rows, vocab, k) bytes. */
+int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k);
+int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride,
+                 float inv_temp, int k, const double* parent_scores, int beam,
+                 float* row_vals, int32_t* row_idx, int32_t* out_parent, int32_t* out_token,
+                 double* out_score, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BEAM_ENGINE_AMD_H */

@@ -1,0 +1,149 @@
+"""Host-side checks of the C ABI (no GPU needed): the library loads and
+exports every function include/beam_engine_amd.h declares, and the attention
+planner (host code) validates its inputs and produces a consistent work list."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "beam_engine_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(be_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    from beam_engine_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("HIP library not built (run __graft_entry__.build())")
+    return _lib, _lib.load()
+
+
+def test_library_exports_every_declared_symbol():
+    _lib, L = lib()
+    names = declared_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(_lib.EXPORTS)
+    assert L.be_version() >= 100
+
+
+def plan(levels, nq=None, hq=8, hkv=2, d=128, page=4, num_pages=64, dtype=2, flags=0, cus=256):
+    _lib, L = lib()
+    keep = []
+    arr = (_lib.BeLevel * len(levels))()
+    for i, (qo, kvp, kvi, lpl) in enumerate(levels):
+        a = [np.asarray(x, dtype=np.int32) for x in (qo, kvp, kvi, lpl)]
+        keep.append(a)
+        arr[i] = _lib.BeLevel(a[0].ctypes.data, a[1].ctypes.data, a[2].ctypes.data if len(a[2]) else 0,
+                              a[3].ctypes.data, len(a[0]) - 1)
+    if nq is None:
+        nq = max(int(l[0][-1]) for l in levels)
+    buf = np.zeros(1 << 20, dtype=np.int32)
+    info = _lib.BeAttnPlanInfo()
+    rc = L.be_attn_plan(arr, len(levels), nq, hq, hkv, d, page, num_pages, dtype, flags, cus,
+                        buf.ctypes.data, buf.size, ctypes.byref(info))
+    return rc, info, buf, _lib, L
+
+
+def decode_items(info, buf):
+    it = buf[info.off_items: info.off_items + 8 * info.num_items].reshape(-1, 8)
+    return it
+
+
+def test_plan_covers_every_token_once_per_query():
+    # A.1-shaped cascade (page 4), bf16
+    levels = [([0, 8], [0, 4], [0, 1, 2, 3], [1]),
+              ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1]),
+              ([0, 1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 3, 4, 5, 6, 7, 8, 9],
+               [10, 11, 12, 13, 14, 15, 16, 17, 18], [1, 1, 1, 0, 0, 3, 3, 3])]
+    rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, num_pages=19)
+    assert rc == 0, L.be_last_error()
+    items = decode_items(info, buf)
+    # every query sees exactly the tokens of its groups
+    cover = {q: 0 for q in range(8)}
+    for q0, qn, pb, t0, tc, orow, _, _ in items:
+        assert tc > 0 and qn > 0
+        for q in range(q0, q0 + qn):
+            cover[q] += tc
+    expect = {}
+    for qo, kvp, kvi, lpl in levels:
+        for g in range(len(qo) - 1):
+            npg = kvp[g + 1] - kvp[g]
+            n = 0 if npg == 0 else (npg - 1) * 4 + lpl[g]
+            for q in range(qo[g], qo[g + 1]):
+                expect[q] = expect.get(q, 0) + n
+    assert cover == expect
+    # merge CSR lists one partial row per (item, query) of merged queries
+    mq = buf[info.off_merge_q: info.off_merge_q + info.num_merge]
+    mp = buf[info.off_merge_ptr: info.off_merge_ptr + info.num_merge + 1]
+    mr = buf[info.off_merge_rows: info.off_merge_rows + mp[-1]]
+    assert sorted(mr.tolist()) == list(range(info.num_part_rows))
+    assert set(mq.tolist()) == set(range(8))
+    # algorithmic bytes: distinct valid tokens x Hkv x D x 2 bytes x (K, V)
+    valid = 3 * 4 + 1 + 3 * (4 + 1) + (1 + 4 + 1 + 1 + 0 + 0 + 3 + 3 + 3)
+    assert info.kv_bytes == valid * 2 * 128 * 2 * 2
+    assert info.kernel == 1
+
+
+def test_plan_direct_output_for_single_partial_queries():
+    # flat: each query one group of 3 pages -> a single item, written directly
+    levels = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
+    rc, info, buf, *_ = plan(levels, num_pages=6)
+    assert rc == 0
+    assert info.num_part_rows == 0 and info.num_merge == 0
+    assert (decode_items(info, buf)[:, 5] == -1).all()
+
+
+def test_plan_split_k_when_few_groups():
+    # one group, long sequence -> chunked into several items sharing partial rows
+    n_pages = 512
+    levels = [([0, 4], [0, n_pages], list(range(n_pages)), [16])]
+    rc, info, buf, *_ = plan(levels, hq=32, hkv=8, page=16, num_pages=n_pages, cus=256)
+    assert rc == 0
+    items = decode_items(info, buf)
+    assert len(items) > 1
+    assert items[:, 4].sum() == n_pages * 16 * 1   # tokens x query tiles (4 queries x g 4 = 16 rows -> one tile)
+    assert (items[:, 3] % 32 == 0).all()
+    assert info.chunk_tokens % 128 == 0
+
+
+@pytest.mark.parametrize("bad,exc_code", [
+    (([0, 1], [0, 1], [7], [2]), 1),          # page 7 >= num_pages 4
+    (([0, 1], [0, 1], [1], [5]), 1),          # last_page_len > page_size
+    (([0, 2], [0, 1], [1], [2]), 1),          # qo beyond num_queries (1)
+    (([0, 1], [1, 1], [1], [2]), 1),          # indptr not starting at 0
+    (([0, 1], [0, 1], [-1], [2]), 1),         # negative page
+])
+def test_plan_rejects_bad_indices(bad, exc_code):
+    rc, info, buf, _lib, L = plan([bad], nq=1, num_pages=4)
+    assert rc == exc_code
+    assert L.be_last_error()
+
+
+def test_plan_unsupported_head_dim():
+    rc, info, buf, _lib, L = plan([([0, 1], [0, 1], [0], [2])], nq=1, d=96, num_pages=4)
+    assert rc == 4
+
+
+def test_status_codes_map_to_reference_exceptions():
+    _lib, L = lib()
+    rc, *_ = plan([([0, 1], [0, 1], [9], [2])], nq=1, num_pages=4)     # invalid page -> ValueError
+    with pytest.raises(ValueError, match="out of range"):
+        _lib.check(rc, "plan")
+    with pytest.raises(MemoryError):
+        _lib.check(_lib.BE_ERR_CAPACITY, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.BE_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.BE_ERR_HIP, "x")
+    _lib.check(_lib.BE_OK, "x")

@@ -1,0 +1,269 @@
+"""GPU parity of the HIP attention path against the CPU oracle.
+
+Tolerances: fp32 storage within 1e-5 max-abs of
+the float64 oracle; bf16/fp16 storage within 2e-2 relative / 1e-2 absolute of
+the oracle evaluated on the same (rounded) inputs.  Each case prints its name
+before touching the GPU."""
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from tests.conftest import load_fixtures
+
+pytestmark = pytest.mark.gpu
+FX = load_fixtures()
+
+TOL = {torch.float32: dict(rtol=0.0, atol=1e-5), torch.bfloat16: dict(rtol=2e-2, atol=1e-2),
+       torch.float16: dict(rtol=2e-2, atol=1e-2)}
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ws():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    return torch.empty(128 << 20, dtype=torch.uint8, device="cuda")
+
+
+def make_pool(num_pages, page, hkv, d, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    kv = torch.randn((num_pages, 2, page, hkv, d), generator=g, dtype=torch.float32) * scale
+    return kv.to(dtype)
+
+
+def make_q(n, hq, d, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn((n, hq, d), generator=g, dtype=torch.float32) * scale).to(dtype)
+
+
+def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True):
+    from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+    w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
+    w._force_valu = force_valu
+    hq, d = q.shape[1], q.shape[2]
+    w.plan(levels[0], levels[1], levels[2], levels[3], hq, kv.shape[3], d, page, causal=True,
+           pos_encoding_mode="NONE", q_data_type=q.dtype)
+    out = w.run(q.cuda(), kv.cuda(), return_lse=return_lse)
+    torch.cuda.synchronize()
+    return out, w
+
+
+def check(out, lse, ref_o, ref_lse, dtype):
+    o = out.float().cpu().numpy()
+    np.testing.assert_allclose(o, ref_o, **TOL[dtype])
+    if lse is not None:
+        l = lse.cpu().numpy()
+        fin = np.isfinite(ref_lse)
+        assert np.array_equal(np.isfinite(l), fin)
+        np.testing.assert_allclose(l[fin], ref_lse[fin], rtol=1e-5 if dtype == torch.float32 else 2e-3,
+                                   atol=1e-5 if dtype == torch.float32 else 2e-3)
+
+
+def tree_levels(name):
+    e = FX["trees"][name]["expected"]
+    return e["qo_indptr"], e["kv_indptr"], e["kv_indices"], e["last_page_len"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("name", ["cascade_md", "swapped", "uneven"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_reference_trees(ws, dtype, name, d):
+    say(f"reference tree {name} d={d} {dtype}")
+    page, hq, hkv = 4, 8, 2
+    levels = tree_levels(name)
+    n = levels[0][0][-1]
+    kv = make_pool(20, page, hkv, d, dtype, 1)
+    q = make_q(n, hq, d, dtype, 2)
+    (out, lse), _ = run_cascade(ws, q, kv, levels, page)
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, dtype)
+
+
+@pytest.mark.parametrize("force_valu", [False, True])
+def test_mfma_and_valu_agree_on_bf16(ws, force_valu):
+    say(f"mfma/valu bf16 force_valu={force_valu}")
+    levels = tree_levels("cascade_md")
+    kv = make_pool(20, 4, 2, 128, torch.bfloat16, 3)
+    q = make_q(8, 8, 128, torch.bfloat16, 4)
+    (out, lse), w = run_cascade(ws, q, kv, levels, 4, force_valu=force_valu)
+    assert w.stats.kernel == ("valu" if force_valu else "mfma")
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 4, 128 ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+def shared_prefix_levels(n_req, beams, prefix, suffixes, page):
+    """Two levels: per-request prefix pages, per-beam suffix pages."""
+    pp = -(-prefix // page)
+    pages = 0
+    qo0, kvp0, kvi0, lpl0 = [0], [0], [], []
+    qo1, kvp1, kvi1, lpl1 = [0], [0], [], []
+    for r in range(n_req):
+        kvi0.extend(range(pages, pages + pp))
+        pages += pp
+        kvp0.append(len(kvi0))
+        lpl0.append(prefix - (pp - 1) * page)
+        qo0.append(qo0[-1] + beams)
+        for b in range(beams):
+            s = suffixes[r * beams + b]
+            sp = max(1, -(-s // page))
+            kvi1.extend(range(pages, pages + sp))
+            pages += sp
+            kvp1.append(len(kvi1))
+            lpl1.append(s - (sp - 1) * page)
+            qo1.append(qo1[-1] + 1)
+    return ([qo0, qo1], [kvp0, kvp1], [kvi0, kvi1], [lpl0, lpl1]), pages
+
+
+def test_config1_fp32(ws):
+    """Config 1: B=4, prefix 512, suffix 32, 8/8 heads, D=64, fp32, page 16."""
+    say("config 1 fp32 cascade")
+    levels, pages = shared_prefix_levels(1, 4, 512, [32] * 4, 16)
+    kv = make_pool(pages, 16, 8, 64, torch.float32, 5)
+    q = make_q(4, 8, 64, torch.float32, 6)
+    (out, lse), w = run_cascade(ws, q, kv, levels, 16)
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 16, 64 ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.float32)
+    assert np.abs(out.cpu().numpy() - ref_o).max() <= 1e-5
+
+
+def test_config2_bf16_and_flat(ws):
+    """Config 2: 4 req x 8 beams, 32/8 heads, D=128, bf16, prefix 2048, suffix 128."""
+    say("config 2 bf16 cascade + flat")
+    from beam_engine_amd import BatchDecodeWithPagedKVCacheWrapper
+    levels, pages = shared_prefix_levels(4, 8, 2048, [128] * 32, 16)
+    s = 1 / math.sqrt(128)
+    kv = make_pool(pages, 16, 8, 128, torch.bfloat16, 7, s)
+    q = make_q(32, 32, 128, torch.bfloat16, 8, s)
+    (out, lse), w = run_cascade(ws, q, kv, levels, 16)
+    assert w.stats.kv_bytes == 50331648
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 16, 128 ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
+    # flat over the same pages: one group per query with prefix + suffix pages
+    kvp, kvi, lpl = [0], [], []
+    for i in range(32):
+        r = i // 8
+        kvi.extend(levels[2][0][levels[1][0][r]:levels[1][0][r + 1]])
+        kvi.extend(levels[2][1][levels[1][1][i]:levels[1][1][i + 1]])
+        kvp.append(len(kvi))
+        lpl.append(levels[3][1][i])
+    f = BatchDecodeWithPagedKVCacheWrapper(ws)
+    f.plan(kvp, kvi, lpl, 32, 8, 128, 16, q_data_type=torch.bfloat16)
+    fo, fl = f.run(q.cuda(), kv.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    check(fo, fl, ref_o, ref_lse, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_run_py_shape_fixture(ws, dtype):
+    """run.py:18-41 shapes: 7 queries, 512 shared pages + ragged unique pages, 64/8 heads."""
+    say(f"run.py shape {dtype}")
+    fx = FX["run_py_shape"]
+    page, hq, hkv, d = fx["page_size"], fx["num_qo_heads"], fx["num_kv_heads"], fx["head_dim"]
+    shared = fx["shared_kv_num_pages"]
+    uptr = fx["unique_kv_page_indptr"]
+    levels = ([[0, 7], list(range(8))], [[0, shared], uptr],
+              [list(range(shared)), list(range(shared, shared + uptr[-1]))],
+              [[page], fx["unique_kv_last_page_len"]])
+    kv = make_pool(shared + uptr[-1], page, hkv, d, dtype, 9, 0.3)
+    q = make_q(7, hq, d, dtype, 10, 0.3)
+    (out, lse), _ = run_cascade(ws, q, kv, levels, page)
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ragged_edges(ws, dtype):
+    """Token counts around block edges, empty groups, a query without groups."""
+    say(f"ragged edges {dtype}")
+    page, hq, hkv, d = 16, 16, 4, 128
+    lens = [1, 15, 16, 17, 31, 32, 33, 127, 128, 129, 0, 300, 5]
+    kvp, kvi, lpl = [0], [], []
+    pages = 0
+    for L in lens:
+        npg = max(1, -(-L // page))
+        kvi.extend(range(pages, pages + npg))
+        pages += npg
+        kvp.append(len(kvi))
+        lpl.append(L - (npg - 1) * page)
+    n = len(lens) + 1      # the last query belongs to no group
+    levels = ([list(range(len(lens) + 1))], [kvp], [kvi], [lpl])
+    kv = make_pool(pages, page, hkv, d, dtype, 11)
+    q = make_q(n, hq, d, dtype, 12)
+    from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+    w = MultiLevelCascadeAttentionWrapper(1, ws)
+    w._plan_levels(*levels, hq, hkv, d, page, None, dtype, num_queries=n)
+    out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    ref_o, ref_lse = oa.cascade_attention(q[:len(lens)], kv, *levels, page, d ** -0.5)
+    ref_o = np.concatenate([ref_o, np.zeros((1, hq, d))])
+    ref_lse = np.concatenate([ref_lse, np.full((1, hq), -np.inf)])
+    check(out, lse, ref_o, ref_lse, dtype)
+    assert np.all(out[10].float().cpu().numpy() == 0)     # empty group
+
+
+def test_long_prefix_split_k_and_strided_q(ws):
+    """One 8192-token prefix shared by 16 queries (many split-K chunks), q a strided view."""
+    say("long prefix split-K strided q")
+    page, hq, hkv, d = 16, 32, 8, 128
+    levels, pages = shared_prefix_levels(1, 16, 8192, [40] * 16, page)
+    kv = make_pool(pages, page, hkv, d, torch.bfloat16, 13, 0.1)
+    big = make_q(16, hq * 2, d, torch.bfloat16, 14, 0.1)
+    q = big.cuda()[:, ::2]                                   # stride(1) = 2*D
+    (out, lse), w = run_cascade(ws, q, kv, levels, page)
+    assert w.stats.num_items > 8
+    ref_o, ref_lse = oa.cascade_attention(q.cpu(), kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+def test_deep_tree_config3_shape(ws):
+    """Config 3 tree (root 4096, fanout 2/4/4 with 256/128/64, leaf suffix 32), 32/8 heads, bf16:
+    every leaf attends its root-to-leaf path; cascade levels equal flat attention."""
+    say("config 3 tree as cascade")
+    page, hq, hkv, d = 16, 32, 8, 128
+    from beam_engine_amd import BatchDecodeWithPagedKVCacheWrapper
+    next_page = [0]
+
+    def alloc(tokens):
+        n = tokens // page
+        out = list(range(next_page[0], next_page[0] + n))
+        next_page[0] += n
+        return out
+    root = alloc(4096)
+    l1 = [alloc(256) for _ in range(2)]
+    l2 = [alloc(128) for _ in range(8)]
+    l3 = [alloc(64) + alloc(32) for _ in range(32)]
+    levels = ([[0, 32], [0, 16, 32], list(range(0, 33, 4)), list(range(33))],
+              [[0, len(root)], [0, 16, 32], list(range(0, 8 * 8 + 1, 8)), list(range(0, 32 * 6 + 1, 6))],
+              [root, sum(l1, []), sum(l2, []), sum(l3, [])],
+              [[16], [16, 16], [16] * 8, [16] * 32])
+    kv = make_pool(next_page[0], page, hkv, d, torch.bfloat16, 15, 1 / math.sqrt(128))
+    q = make_q(32, hq, d, torch.bfloat16, 16, 1 / math.sqrt(128))
+    (out, lse), w = run_cascade(ws, q, kv, levels, page)
+    assert w.stats.kv_bytes == 35651584
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+def test_merge_state(ws):
+    say("merge_state")
+    from beam_engine_amd import merge_state
+    g = torch.Generator().manual_seed(17)
+    va, vb = torch.randn(5, 8, 128, generator=g), torch.randn(5, 8, 128, generator=g)
+    sa, sb = torch.randn(5, 8, generator=g), torch.randn(5, 8, generator=g)
+    sa[0, :] = -math.inf
+    sb[0, :2] = -math.inf
+    v, s = merge_state(va.cuda(), sa.cuda(), vb.cuda(), sb.cuda())
+    ro, rl = oa.merge_states([va.numpy(), vb.numpy()], [sa.numpy(), sb.numpy()])
+    np.testing.assert_allclose(v.cpu().numpy(), ro, rtol=1e-5, atol=1e-6)
+    got = s.cpu().numpy()
+    assert np.array_equal(np.isfinite(got), np.isfinite(rl))
+    np.testing.assert_allclose(got[np.isfinite(rl)], rl[np.isfinite(rl)], rtol=1e-6, atol=1e-6)

@@ -1,0 +1,121 @@
+"""GPU checks of the KV-cache kernels (bit-exact against torch indexing) and of
+PageTable + BeamState driving them through the reference's fork trace."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from tests.conftest import load_fixtures
+
+pytestmark = pytest.mark.gpu
+FX = load_fixtures()
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_append_matches_indexing(dtype):
+    say(f"kv append {dtype}")
+    from beam_engine_amd import PageTable
+    pt = PageTable(3, page_size=16, max_num_pages=64, head_num=8, head_dim=128, device="cuda", store_dtype=dtype)
+    g = torch.Generator().manual_seed(1)
+    n = 37
+    pages = torch.randperm(64, generator=g)[:n].to(torch.int32)
+    pos = torch.randint(0, 16, (n,), generator=g, dtype=torch.int32)
+    # keys as a strided view of a projection output [N, Hkv, 2*D]
+    proj = torch.randn((n, 8, 256), generator=g).to(dtype).cuda()
+    k, v = proj[:, :, :128], proj[:, :, 128:]
+    ref = pt.kv_cache_at_layer[1].clone()
+    ref[pages.long(), 0, pos.long()] = k
+    ref[pages.long(), 1, pos.long()] = v
+    pt.write_blocks_vectorized(1, pages.cuda(), k, v, pos.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(pt.kv_cache_at_layer[1], ref)
+    assert torch.count_nonzero(pt.kv_cache_at_layer[0]) == 0 and torch.count_nonzero(pt.kv_cache_at_layer[2]) == 0
+
+
+def test_append_skips_out_of_range_entries():
+    say("kv append out-of-range entries")
+    from beam_engine_amd import _lib
+    kv = torch.zeros((4, 2, 8, 2, 64), dtype=torch.bfloat16, device="cuda")
+    k = torch.ones((3, 2, 64), dtype=torch.bfloat16, device="cuda")
+    pages = torch.tensor([1, 9, 2], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([0, 0, 8], dtype=torch.int32, device="cuda")      # 9 >= 4 pages, slot 8 >= page 8
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    L = _lib.load()
+    _lib.check(L.be_kv_append(kv.data_ptr(), _lib.BE_BF16, 4, 8, 2, 64, pages.data_ptr(), pos.data_ptr(),
+                              k.data_ptr(), 128, 64, k.data_ptr(), 128, 64, 3, err.data_ptr(),
+                              _lib.stream_ptr()), "append")
+    torch.cuda.synchronize()
+    assert int(err) == 2
+    assert torch.all(kv[1, :, 0] == 1) and torch.count_nonzero(kv) == 2 * 2 * 64
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_batched_page_copy_all_layers(dtype):
+    say(f"page copy {dtype}")
+    from beam_engine_amd import PageTable
+    pt = PageTable(4, page_size=8, max_num_pages=32, head_num=2, head_dim=64, device="cuda", store_dtype=dtype)
+    g = torch.Generator().manual_seed(2)
+    pt.kv_pool.copy_(torch.randn(pt.kv_pool.shape, generator=g).to(dtype))
+    for _ in range(10):
+        pt.allocate_block()
+    before = pt.kv_pool.clone()
+    with pt.defer_copies():
+        a = pt.copy_block(3, 5)
+        b = pt.copy_block(7, 8)
+        c = pt.copy_block(3, 0)
+    assert (a, b, c) == (10, 11, 12)
+    torch.cuda.synchronize()
+    ref = before.clone()
+    ref[:, a, :, :5] = before[:, 3, :, :5]
+    ref[:, b, :, :8] = before[:, 7, :, :8]
+    assert torch.equal(pt.kv_pool, ref)
+
+
+def test_copy_block_errors():
+    from beam_engine_amd import PageTable
+    from beam_engine_amd.page_table import PageCopyError
+    pt = PageTable(1, page_size=4, max_num_pages=4, head_num=1, head_dim=64, device="cuda")
+    with pytest.raises(TypeError):
+        pt.copy_block(0, 5)
+    with pytest.raises(ValueError):
+        pt.copy_block(4, 1)
+    for _ in range(4):
+        pt.allocate_block()
+    with pytest.raises(MemoryError):
+        pt.allocate_block()
+
+
+def test_fork_trace_moves_page_contents():
+    """Run the reference's fork trace on a real PageTable: after each fork the
+    copied page holds the source's first len slots on every layer."""
+    say("fork trace on device")
+    from beam_engine_amd import BeamGenerateResult, BeamState, BeamToken, PageTable
+    tr = FX["fork_trace"]
+    pt = PageTable(2, page_size=tr["page_size"], max_num_pages=tr["max_num_pages"], head_num=2, head_dim=64,
+                   device="cuda", store_dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(3)
+    pt.kv_pool.copy_(torch.randn(pt.kv_pool.shape, generator=g).to(torch.bfloat16))
+    st = BeamState(tr["beam_size"], pt)
+    st.add_root_sequence(tr["prompt"])
+    for step in tr["steps"]:
+        before = pt.kv_pool.clone()
+        res = [BeamGenerateResult(c, [BeamToken(t, s) for t, s in ch]) for c, ch in zip(st.candidates, step["select"])]
+        st.add_filtered_results(res)
+        torch.cuda.synchronize()
+        assert [c.trie_node.page_id for c in st.candidates] == [c["page"] for c in step["expect_candidates"]]
+        for src, dst, n in step["expect_copies"]:
+            assert torch.equal(pt.kv_pool[:, dst, :, :n], before[:, src, :, :n])
+        assert list(pt.free_pages) == step.get("expect_free_list", list(pt.free_pages))

@@ -1,0 +1,84 @@
+"""GPU beam selection (be_beam_topk) bit-exact against the oracle: row top-k
+values and indices, and the global top-B parents, tokens and float64 scores."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import topk as ot
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+DT = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
+
+
+def compare(logits, parents, beam, temperature=1.0):
+    from beam_engine_amd import beam_topk, decode_k
+    n, v = logits.shape
+    k = decode_k(beam, v)
+    x = logits.float().numpy()
+    logp = ot.log_softmax_rows(x, DT[logits.dtype], temperature)
+    vals, idx = ot.row_topk(logp, k)
+    _, flat = ot.select_global(parents, vals, idx, beam)
+    rv, ri, (par, tok, sc) = beam_topk(logits.cuda(), k, torch.tensor(parents, dtype=torch.float64), beam,
+                                       temperature)
+    torch.cuda.synchronize()
+    assert np.array_equal(ri.cpu().numpy(), idx), "row indices differ"
+    assert np.array_equal(rv.cpu().numpy().view(np.uint32), vals.view(np.uint32)), "row values differ"
+    got = list(zip(par.tolist(), tok.tolist(), sc.tolist()))
+    assert got == flat
+
+
+def test_config1_fp32():
+    say("topk config 1 [4, 32000] fp32 beam 4")
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn((4, 32000), generator=g)
+    compare(logits, [0.0, -0.5, -0.7, -1.25], 4)
+
+
+def test_config4_bf16():
+    say("topk config 4 [128, 128256] bf16 beam 16")
+    g = torch.Generator().manual_seed(2)
+    logits = (torch.randn((128, 128256), generator=g) * 3).to(torch.bfloat16)
+    parents = (-torch.rand(128, generator=g, dtype=torch.float64) * 5).tolist()
+    # the engine selects per request: 8 requests x 16 rows
+    for r in range(8):
+        compare(logits[16 * r:16 * (r + 1)], parents[16 * r:16 * (r + 1)], 16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_ties_and_temperature(dtype):
+    say(f"topk ties/temperature {dtype}")
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randint(-3, 4, (6, 5000), generator=g).to(torch.float32).to(dtype)   # massive ties
+    parents = [0.0, 0.0, -1.0, -1.0, -2.0, 0.0]                                        # tied parents too
+    compare(logits, parents, 4)
+    compare(logits, parents, 4, temperature=0.7)
+    compare(logits, parents, 1)
+
+
+def test_prefill_single_row_and_small_vocab():
+    say("topk prefill row / small vocab")
+    from beam_engine_amd import beam_topk
+    g = torch.Generator().manual_seed(4)
+    row = torch.randn((1, 128256), generator=g).to(torch.bfloat16)
+    rv, ri = beam_topk(row.cuda(), 32)
+    sel = ot.prefill_select(row[0].float().numpy(), 16, "bfloat16")
+    assert [int(t) for t in ri[0, :16].tolist()] == [t for t, _ in sel]
+    assert rv[0, :16].tolist() == [s for _, s in sel]
+    small = torch.randn((3, 7), generator=g)
+    compare(small, [0.0, -1.0, -2.0], 3)
