@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(_PKG, "libbeam_engine_amd.so")
 BE_F32, BE_F16, BE_BF16 = 0, 1, 2
 BE_OK, BE_ERR_INVALID, BE_ERR_HIP, BE_ERR_CAPACITY, BE_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 BE_PLAN_FORCE_VALU = 1
+BE_PLAN_FUSED_MERGE = 2
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
 
@@ -44,8 +45,10 @@ class BeAttnPlanInfo(ctypes.Structure):
         "num_items", "num_part_rows", "num_merge", "num_queries", "num_qo_heads", "num_kv_heads",
         "head_dim", "page_size", "num_pages", "dtype", "kernel", "tile_rows", "chunk_tokens",
         "plan_ints", "off_items", "off_qindex", "off_pages", "off_merge_q", "off_merge_ptr",
-        "off_merge_rows")] + [
+        "off_merge_rows", "off_q_merge", "fused_merge", "num_zero", "off_zero_q", "off_zero_ptr")] + [
         ("partial_bytes", ctypes.c_int64),
+        ("counter_offset", ctypes.c_int64),
+        ("counter_bytes", ctypes.c_int64),
         ("kv_bytes", ctypes.c_int64),
         ("qo_bytes", ctypes.c_int64),
         ("flops", ctypes.c_double),

@@ -109,6 +109,7 @@ class _PagedPlanner:
         self._sm_scale = 1.0
         self._dtype: Optional[torch.dtype] = None
         self._force_valu = False
+        self._fused_merge = False
 
     # ---------------------------------------------------------------- plan
     def _plan_levels(self, qo: Sequence, kvp: Sequence, kvi: Sequence, lpl: Sequence, num_qo_heads: int,
@@ -143,7 +144,8 @@ class _PagedPlanner:
         if isinstance(q_data_type, str):
             q_data_type = getattr(torch, q_data_type)
         dt = _lib.dtype_code(q_data_type)
-        flags = _lib.BE_PLAN_FORCE_VALU if self._force_valu else 0
+        flags = (_lib.BE_PLAN_FORCE_VALU if self._force_valu else 0) | \
+            (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()
@@ -169,6 +171,9 @@ class _PagedPlanner:
         staging.event = ev
         self._plan_dev = ws_i32
         self._partials = self._ws[part_off:need] if info.partial_bytes else None
+        if info.counter_bytes:
+            c0 = part_off + int(info.counter_offset)
+            self._ws[c0:c0 + int(info.counter_bytes)].zero_()
         self._info = info
         self._max_page = max_page
         self._sm_scale = float(head_dim ** -0.5 if sm_scale is None else sm_scale)

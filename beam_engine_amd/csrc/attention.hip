@@ -53,6 +53,11 @@ struct AttnArgs {
   const WorkItem* items;
   const int32_t* q_index;
   const int32_t* pages;
+  // fused merge (null counters: the separate merge kernel runs instead)
+  const int32_t* q_merge;      // per query: merge-list index or -1
+  const int32_t* merge_ptr;    // CSR of partial rows per merge-list entry
+  const int32_t* merge_rows;
+  int32_t* counters;           // [num_merge][hkv] arrivals, zero between runs
   int page_size, hkv, hq, g;
   float scale_log2;   // sm_scale * log2(e)
 };
@@ -87,6 +92,59 @@ __device__ __forceinline__ void store_row_lse(const AttnArgs& a, const WorkItem&
     }
   } else {
     a.part_lse[(int64_t)(it.out_row + j) * a.hq + head] = lse;
+  }
+}
+
+// Fused split-K merge.  Called by every thread of a workgroup after it wrote
+// its partial rows.  For each query of the item the workgroup counts its
+// arrival on (query, kv head); the workgroup that completes the count merges
+// the g heads of that query from every partial row by log-sum-exp, writes the
+// output and resets the counter for the next run.  The release fence makes
+// this workgroup's partial rows visible device-wide (all XCD L2s) before its
+// arrival is counted; the acquire fence orders the merger's reads after it.
+template <typename T, int D>
+__device__ void fused_merge_epilogue(const AttnArgs& a, const WorkItem& it, int kvh, int* s_last) {
+  __threadfence();
+  __syncthreads();
+  const int tid = threadIdx.x;
+  if (tid < it.q_count) {
+    const int qi = a.q_index[it.q_begin + tid];
+    const int mi = a.q_merge[qi];
+    const int expect = a.merge_ptr[mi + 1] - a.merge_ptr[mi];
+    const int old = __hip_atomic_fetch_add(&a.counters[(int64_t)mi * a.hkv + kvh], 1, __ATOMIC_ACQ_REL,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    s_last[tid] = (old == expect - 1) ? mi : -1;
+  }
+  __syncthreads();
+  bool fenced = false;
+  for (int j = 0; j < it.q_count; ++j) {
+    const int mi = s_last[j];
+    if (mi < 0) continue;
+    if (!fenced) {
+      __threadfence();
+      fenced = true;
+    }
+    const int qi = a.q_index[it.q_begin + j];
+    const int rb = a.merge_ptr[mi], re = a.merge_ptr[mi + 1];
+    // thread -> (head hh, column d); g * D elements over 256 threads
+    for (int e = tid; e < a.g * D; e += 256) {
+      const int hh = e / D, d = e - hh * D, head = kvh * a.g + hh;
+      float M = -INFINITY;
+      for (int r = rb; r < re; ++r) M = fmaxf(M, a.part_lse[(int64_t)a.merge_rows[r] * a.hq + head]);
+      float z = 0.f, acc = 0.f;
+      if (M != -INFINITY) {
+        for (int r = rb; r < re; ++r) {
+          const int64_t row = (int64_t)a.merge_rows[r] * a.hq + head;
+          const float wgt = expf(a.part_lse[row] - M);
+          z += wgt;
+          acc += wgt * a.part_o[row * D + d];
+        }
+      }
+      T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh;
+      op[d] = from_f32<T>(z > 0.f ? acc / z : 0.f);
+      if (d == 0 && a.out_lse) a.out_lse[(int64_t)qi * a.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
+    }
+    if (tid == 0) a.counters[(int64_t)mi * a.hkv + kvh] = 0;
   }
 }
 
@@ -326,7 +384,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  if (w != 0) return;
+  __shared__ int s_last[kMaxRows];
+  if (w == 0) {
   // ---- wave 0 writes: lane holds O^T[d = mt*16 + 4*lg + i][row = nt*16 + lc]
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -352,6 +411,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
     }
     if (lg == 0) store_row_lse<T>(a, it, j, head, m_run[nt], l);
   }
+  }
+  if (it.out_row >= 0 && a.counters) fused_merge_epilogue<T, D>(a, it, kvh, s_last);
 }
 
 // ================================================================== VALU kernel
@@ -469,6 +530,8 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnArgs a) {
     }
     if (d_own == 0) store_row_lse<T>(a, it, j, head, m_s[r], l);
   }
+  __shared__ int s_last[kMaxRows];
+  if (it.out_row >= 0 && a.counters) fused_merge_epilogue<T, D>(a, it, kvh, s_last);
 }
 
 // ================================================================== merge kernel
@@ -648,10 +711,14 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   for (int v : valid) valid_tokens += v;
   const int64_t es = (int64_t)dtype_size(dtype);
 
-  // ---- merge list
-  std::vector<int> merge_q, merge_ptr{0}, merge_rows;
+  // ---- merge list (queries with >= 2 partial rows) and zero list (no keys)
+  std::vector<int> merge_q, merge_ptr{0}, merge_rows, zero_q;
   for (int qi = 0; qi < num_queries; ++qi) {
     if (cnt[qi] == 1) continue;
+    if (cnt[qi] == 0) {
+      zero_q.push_back(qi);
+      continue;
+    }
     merge_q.push_back(qi);
     for (int r : rows_of[qi]) merge_rows.push_back(r);
     merge_ptr.push_back((int)merge_rows.size());
@@ -666,6 +733,9 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   const int64_t off_mq = off;       off += (int64_t)merge_q.size();
   const int64_t off_mp = off;       off += (int64_t)merge_ptr.size();
   const int64_t off_mr = off;       off += (int64_t)merge_rows.size();
+  const int64_t off_qm = off;       off += num_queries;
+  const int64_t off_zq = off;       off += (int64_t)zero_q.size();
+  const int64_t off_zp = off;       off += (int64_t)zero_q.size() + 1;
   off = ceil_div(off, 4) * 4;
   if (off > cap || off > INT32_MAX) return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
   memcpy(out + off_items, items.data(), n_items * sizeof(WorkItem));
@@ -682,7 +752,10 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   if (!merge_q.empty()) memcpy(out + off_mq, merge_q.data(), merge_q.size() * 4);
   memcpy(out + off_mp, merge_ptr.data(), merge_ptr.size() * 4);
   if (!merge_rows.empty()) memcpy(out + off_mr, merge_rows.data(), merge_rows.size() * 4);
-  for (int64_t i = off_mr + (int64_t)merge_rows.size(); i < off; ++i) out[i] = 0;
+  for (int qi = 0; qi < num_queries; ++qi) out[off_qm + qi] = -1;
+  for (size_t m = 0; m < merge_q.size(); ++m) out[off_qm + merge_q[m]] = (int32_t)m;
+  if (!zero_q.empty()) memcpy(out + off_zq, zero_q.data(), zero_q.size() * 4);
+  for (int64_t i = off_zp; i < off; ++i) out[i] = 0;     // zero_ptr: empty row ranges, then padding
 
   memset(info, 0, sizeof(*info));
   info->num_items = (int32_t)n_items;
@@ -705,7 +778,14 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   info->off_merge_q = (int32_t)off_mq;
   info->off_merge_ptr = (int32_t)off_mp;
   info->off_merge_rows = (int32_t)off_mr;
-  info->partial_bytes = (int64_t)rows * hq * (d + 1) * 4;
+  info->off_q_merge = (int32_t)off_qm;
+  info->fused_merge = (flags & BE_PLAN_FUSED_MERGE) ? 1 : 0;
+  info->num_zero = (int32_t)zero_q.size();
+  info->off_zero_q = (int32_t)off_zq;
+  info->off_zero_ptr = (int32_t)off_zp;
+  info->counter_offset = ceil_div((int64_t)rows * hq * (d + 1) * 4, 256) * 256;
+  info->counter_bytes = info->fused_merge ? (int64_t)merge_q.size() * hkv * 4 : 0;
+  info->partial_bytes = info->counter_offset + info->counter_bytes;
   info->kv_bytes = valid_tokens * hkv * d * es * 2;
   info->qo_bytes = (int64_t)num_queries * hq * d * es * 2;
   info->flops = flops;
@@ -741,8 +821,8 @@ static int launch_attn(const be_attn_plan_info* info, AttnArgs& a, hipStream_t s
 }
 
 template <typename T>
-static int launch_merge(const be_attn_plan_info* info, MergeArgs& m, hipStream_t st) {
-  const dim3 grid(info->num_merge, (info->num_qo_heads + 3) / 4);
+static int launch_merge(const be_attn_plan_info* info, MergeArgs& m, int count, hipStream_t st) {
+  const dim3 grid(count, (info->num_qo_heads + 3) / 4);
   switch (info->head_dim) {
     case 64: merge_kernel<T, 64><<<grid, 256, 0, st>>>(m); break;
     case 128: merge_kernel<T, 128><<<grid, 256, 0, st>>>(m); break;
@@ -775,6 +855,12 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
   a.hq = info->num_qo_heads;
   a.g = info->num_qo_heads / info->num_kv_heads;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.q_merge = plan + info->off_q_merge;
+  a.merge_ptr = plan + info->off_merge_ptr;
+  a.merge_rows = plan + info->off_merge_rows;
+  a.counters = (info->fused_merge && info->num_merge > 0)
+                   ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(partials) + info->counter_offset)
+                   : nullptr;
   int rc = BE_OK;
   if (info->num_items > 0) {
     switch (info->dtype) {
@@ -785,18 +871,22 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
     }
     if (rc) return rc;
   }
-  if (info->num_merge > 0) {
-    MergeArgs m;
-    m.part_o = a.part_o; m.part_lse = a.part_lse;
-    m.merge_q = plan + info->off_merge_q;
-    m.merge_ptr = plan + info->off_merge_ptr;
-    m.merge_rows = plan + info->off_merge_rows;
-    m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse; m.hq = info->num_qo_heads;
+  MergeArgs m;
+  m.part_o = a.part_o; m.part_lse = a.part_lse;
+  m.merge_rows = plan + info->off_merge_rows;
+  m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse; m.hq = info->num_qo_heads;
+  for (int pass = 0; pass < 2; ++pass) {
+    // pass 0: split-K merge (separate-merge plans); pass 1: queries without keys
+    const int count = pass == 0 ? (info->fused_merge ? 0 : info->num_merge) : info->num_zero;
+    if (count == 0) continue;
+    m.merge_q = plan + (pass == 0 ? info->off_merge_q : info->off_zero_q);
+    m.merge_ptr = plan + (pass == 0 ? info->off_merge_ptr : info->off_zero_ptr);
     switch (info->dtype) {
-      case BE_F32: rc = launch_merge<float>(info, m, st); break;
-      case BE_F16: rc = launch_merge<f16_t>(info, m, st); break;
-      case BE_BF16: rc = launch_merge<bf16_t>(info, m, st); break;
+      case BE_F32: rc = launch_merge<float>(info, m, count, st); break;
+      case BE_F16: rc = launch_merge<f16_t>(info, m, count, st); break;
+      case BE_BF16: rc = launch_merge<bf16_t>(info, m, count, st); break;
     }
+    if (rc) return rc;
   }
   return rc;
 }

@@ -1,0 +1,171 @@
+#!/usr/bin/env python3
+"""Benchmark driver (one JSON line on stdout).
+
+Default workload ``e2e``: end-to-end batched beam search on a random-init
+Llama-3-8B-shaped decoder; value = beam-decode tokens/s
+= sum over requests of beam width x decode steps / decode wall time.  A step
+is one decode step of all 8 requests x 16 beams.
+
+Attention workloads (``--workload attn-c2|attn-ns|attn-c3|attn-c5|attn-c1``)
+time one decode-attention layer at a BASELINE shape over 32 distinct per-layer
+KV caches (working set above the 256 MB Infinity Cache); value = algorithmic
+HBM GB/s of the attention kernel.  ``--strategy flat`` runs the flat paged
+strategy on the same pages.
+
+Every line carries ``roofline`` (the attention kernel: algorithmic bytes per
+launch / mean launch time from HIP events on the launch stream) and
+``cpu_baseline`` (the CPU oracle on a bounded sample, rank 0, N=1 only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (decode steps / attention reps)")
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="e2e",
+                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5"])
+    ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat"])
+    ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--verbose", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------- attention
+def attention_workload(args):
+    import torch
+    from beam_engine_amd import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAttentionWrapper
+    from beam_engine_amd.workloads import BUILDERS
+
+    wl = BUILDERS[args.workload.split("-", 1)[1]]()
+    dtype = torch.float32 if wl.name == "c1" else torch.bfloat16
+    es = 4 if dtype == torch.float32 else 2
+    steps = args.steps or 20
+    warmup = 5 if args.warmup is None else args.warmup
+    L = args.layers
+    dev = torch.device("cuda")
+    torch.manual_seed(0)
+    scale = 1.0 / math.sqrt(wl.d)
+    log(f"{wl.name}: {wl.note}; {wl.num_pages} pages x {L} layers")
+    kv = [torch.randn((wl.num_pages, 2, wl.page, wl.hkv, wl.d), device=dev, dtype=dtype).mul_(scale) for _ in range(L)]
+    qs = [torch.randn((wl.num_queries, wl.hq, wl.d), device=dev, dtype=dtype).mul_(scale) for _ in range(L)]
+    outs = [torch.empty_like(q) for q in qs]
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    if args.strategy == "cascade":
+        w = MultiLevelCascadeAttentionWrapper(len(wl.levels[0]), ws)
+        w._fused_merge = args.fused_merge
+        w.plan(*wl.levels, wl.hq, wl.hkv, wl.d, wl.page, q_data_type=dtype)
+        alg_kv = w.stats.kv_bytes
+    else:
+        w = BatchDecodeWithPagedKVCacheWrapper(ws)
+        w._fused_merge = args.fused_merge
+        w.plan(*wl.flat, wl.hq, wl.hkv, wl.d, wl.page, q_data_type=dtype)
+        alg_kv = sum(wl.tokens_per_query) * wl.hkv * wl.d * es * 2     # flat scored by its own path bytes
+    st = w.stats
+    alg = alg_kv + st.qo_bytes
+    for _ in range(warmup):
+        for l in range(L):
+            w.run(qs[l], kv[l], out=outs[l])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps * L)]
+    loop = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(steps):
+        loop[r][0].record(stream)
+        for l in range(L):
+            s, e = evs[r * L + l]
+            s.record(stream)
+            w.run(qs[l], kv[l], out=outs[l])
+            e.record(stream)
+        loop[r][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) * 1e3 for s, e in evs]            # us per launch
+    mean_us = sum(per) / len(per)
+    med_us = statistics.median(per)
+    layer_us = statistics.median([a.elapsed_time(b) * 1e3 / L for a, b in loop])
+    gbs = alg / (mean_us * 1e-6) / 1e9
+    tflops = st.flops / (mean_us * 1e-6) / 1e12
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": f"attn_{st.kernel}_kernel" + ("" if st.num_merge == 0 or args.fused_merge else " + merge_kernel"),
+            "bytes_per_launch": alg, "mean_launch_us": round(mean_us, 2), "median_launch_us": round(med_us, 2),
+            "tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+    result = {
+        "metric": "decode attention HBM GB/s (algorithmic bytes / kernel time)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(layer_us * L / 1e3, 4), "higher_is_better": True, "scaling": "strong",
+        "vs_baseline": None, "dtype": "f32" if es == 4 else "bf16", "data": "synthetic N(0,1)/sqrt(D)",
+        "config": {"workload": f"attention {wl.name} {args.strategy}", "shape": wl.note, "layers": L,
+                   "items": st.num_items, "chunk_tokens": st.chunk_tokens, "merge_rows": st.num_part_rows,
+                   "fused_merge": bool(args.fused_merge), "per_layer_us": round(layer_us, 2),
+                   "wall_s": round(wall, 3)},
+        "roofline": roof,
+    }
+    return result, wl
+
+
+# ---------------------------------------------------------------------- CPU baseline
+def cpu_baseline_attention(wl, alg_bytes):
+    """The oracle (numpy float64 cascade attention + log-sum-exp merge) on one
+    layer of the same workload, in GB/s of the same algorithmic bytes."""
+    import numpy as np
+    from oracle import attention as oa
+    threads = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    kv = rng.standard_normal((wl.num_pages, 2, wl.page, wl.hkv, wl.d)).astype(np.float32)
+    q = rng.standard_normal((wl.num_queries, wl.hq, wl.d)).astype(np.float32)
+    t0 = time.perf_counter()
+    oa.cascade_attention(q, kv, *wl.levels, wl.page, wl.d ** -0.5)
+    dt = time.perf_counter() - t0
+    gbs = alg_bytes / dt / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle cascade attention (numpy float64, BLAS threads = {threads}) over all "
+                      f"{wl.num_queries} queries of one layer: {dt:.2f} s; cpu {platform.processor() or platform.machine()}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: bench.py --gpus N with N > 1 is not "
+                                   "supported (multi-GPU sharding is described in DESIGN.md, not built)"}))
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        return 1
+    if args.workload.startswith("attn-"):
+        result, wl = attention_workload(args)
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = cpu_baseline_attention(wl, result["roofline"]["bytes_per_launch"])
+    else:
+        from beam_engine_amd.e2e import run_e2e_bench
+        result = run_e2e_bench(args)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

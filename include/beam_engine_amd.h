@@ -95,7 +95,11 @@ typedef struct be_level {
 } be_level;
 
 /* Plan flags. */
-#define BE_PLAN_FORCE_VALU 1     /* use the VALU kernel even where MFMA applies */
+#define BE_PLAN_FORCE_VALU 1     /* use the VALU kernel even where MFMA applies            */
+#define BE_PLAN_FUSED_MERGE 2    /* merge split-K partials in the attention kernel's last-
+                                    arriving workgroup instead of a second kernel (every
+                                    workgroup then pays a device-scope release fence, an
+                                    L2 writeback on gfx950, so this is off by default)    */
 
 /* Filled by be_attn_plan; passed back to be_attn_run unchanged. */
 typedef struct be_attn_plan_info {
@@ -109,7 +113,15 @@ typedef struct be_attn_plan_info {
   int32_t chunk_tokens;    /* split-K chunk length                             */
   int32_t plan_ints;       /* int32 words of the device plan                    */
   int32_t off_items, off_qindex, off_pages, off_merge_q, off_merge_ptr, off_merge_rows;
-  int64_t partial_bytes;   /* device bytes needed for partial o + lse          */
+  int32_t off_q_merge;     /* per query: index into the merge list, or -1      */
+  int32_t fused_merge;     /* 1: the attention kernel merges (no second kernel) */
+  int32_t num_zero;        /* queries with no keys at all: o = 0, lse = -inf   */
+  int32_t off_zero_q, off_zero_ptr;
+  int64_t partial_bytes;   /* device scratch: partial o + lse + merge counters */
+  int64_t counter_offset;  /* byte offset of the int32 merge counters in the scratch;
+                              the caller zeroes counter_bytes there once after planning
+                              (every run leaves them at zero again)            */
+  int64_t counter_bytes;
   int64_t kv_bytes;        /* algorithmic K+V bytes: distinct (page, head) valid tokens */
   int64_t qo_bytes;        /* Q + O bytes                                       */
   double flops;            /* 4 * D * sum_q sum_h kv_len(q)                     */
@@ -132,7 +144,8 @@ int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int nu
  * (n, h) and D contiguous; out has the plan's dtype.  lse (optional, device
  * float [num_queries, Hq]) receives the natural-log log-sum-exp; a query with
  * no keys gets o = 0 and lse = -inf.  dev_plan is the device copy of the plan,
- * partials points at info->partial_bytes of device scratch. */
+ * partials points at info->partial_bytes of device scratch.  Runs of one plan
+ * must be stream-ordered (they share the scratch and its merge counters). */
 int be_attn_run(const be_attn_plan_info* info, const int32_t* dev_plan, void* partials,
                 const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* kv_layer,
                 void* out, int64_t o_stride_n, int64_t o_stride_h, float* lse, float sm_scale,

@@ -147,3 +147,14 @@ def test_status_codes_map_to_reference_exceptions():
     with pytest.raises(RuntimeError):
         _lib.check(_lib.BE_ERR_HIP, "x")
     _lib.check(_lib.BE_OK, "x")
+
+
+def test_plan_lists_keyless_queries_for_zero_fill():
+    # query 1's group is empty (one page, 0 valid tokens); query 2 belongs to no group
+    levels = [([0, 1, 2], [0, 1, 2], [0, 1], [3, 0])]
+    rc, info, buf, *_ = plan(levels, nq=3, num_pages=2)
+    assert rc == 0
+    assert info.num_zero == 2
+    assert buf[info.off_zero_q: info.off_zero_q + 2].tolist() == [1, 2]
+    assert buf[info.off_zero_ptr: info.off_zero_ptr + 3].tolist() == [0, 0, 0]
+    assert info.num_items == 1 and info.num_merge == 0

@@ -45,10 +45,11 @@ def make_q(n, hq, d, dtype, seed, scale=1.0):
     return (torch.randn((n, hq, d), generator=g, dtype=torch.float32) * scale).to(dtype)
 
 
-def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True):
+def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True, fused_merge=False):
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
     w._force_valu = force_valu
+    w._fused_merge = fused_merge
     hq, d = q.shape[1], q.shape[2]
     w.plan(levels[0], levels[1], levels[2], levels[3], hq, kv.shape[3], d, page, causal=True,
            pos_encoding_mode="NONE", q_data_type=q.dtype)
@@ -88,13 +89,14 @@ def test_reference_trees(ws, dtype, name, d):
     check(out, lse, ref_o, ref_lse, dtype)
 
 
+@pytest.mark.parametrize("fused_merge", [False, True])
 @pytest.mark.parametrize("force_valu", [False, True])
-def test_mfma_and_valu_agree_on_bf16(ws, force_valu):
-    say(f"mfma/valu bf16 force_valu={force_valu}")
+def test_mfma_and_valu_agree_on_bf16(ws, force_valu, fused_merge):
+    say(f"mfma/valu bf16 force_valu={force_valu} fused_merge={fused_merge}")
     levels = tree_levels("cascade_md")
     kv = make_pool(20, 4, 2, 128, torch.bfloat16, 3)
     q = make_q(8, 8, 128, torch.bfloat16, 4)
-    (out, lse), w = run_cascade(ws, q, kv, levels, 4, force_valu=force_valu)
+    (out, lse), w = run_cascade(ws, q, kv, levels, 4, force_valu=force_valu, fused_merge=fused_merge)
     assert w.stats.kernel == ("valu" if force_valu else "mfma")
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 4, 128 ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
@@ -267,3 +269,23 @@ def test_merge_state(ws):
     got = s.cpu().numpy()
     assert np.array_equal(np.isfinite(got), np.isfinite(rl))
     np.testing.assert_allclose(got[np.isfinite(rl)], rl[np.isfinite(rl)], rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("fused_merge", [False, True])
+def test_repeated_runs_of_one_plan(ws, fused_merge):
+    """One plan, many runs (as over the layers of a step): every run matches
+    the oracle, so the fused-merge arrival counters return to zero each run."""
+    say(f"repeated runs fused_merge={fused_merge}")
+    from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+    levels, pages = shared_prefix_levels(2, 8, 1024, [64] * 16, 16)
+    kv = make_pool(pages, 16, 8, 128, torch.bfloat16, 21, 0.2).cuda()
+    w = MultiLevelCascadeAttentionWrapper(2, ws)
+    w._fused_merge = fused_merge
+    w.plan(*levels, 32, 8, 128, 16, q_data_type=torch.bfloat16)
+    assert w.stats.num_merge == 16
+    for rep in range(6):
+        q = make_q(16, 32, 128, torch.bfloat16, 100 + rep, 0.2)
+        out, lse = w.run(q.cuda(), kv, return_lse=True)
+        torch.cuda.synchronize()
+        ref_o, ref_lse = oa.cascade_attention(q, kv.cpu(), *levels, 16, 128 ** -0.5)
+        check(out, lse, ref_o, ref_lse, torch.bfloat16)
