@@ -39,7 +39,8 @@ struct WorkItem {
 };
 static_assert(sizeof(WorkItem) == 32, "WorkItem is 8 int32 words");
 
-constexpr int kMaxRows = 32;   // queries x GQA group per workgroup tile
+constexpr int kMaxRows = 32;       // rows (queries x GQA group) per VALU workgroup
+constexpr int kMaxTileRows = 128;  // rows per MFMA workgroup (8 row tiles of 16)
 
 struct AttnArgs {
   const void* q;
@@ -149,33 +150,47 @@ __device__ void fused_merge_epilogue(const AttnArgs& a, const WorkItem& it, int 
 }
 
 // ================================================================== MFMA kernel
-// bf16/fp16 storage, D in {64, 128, 256}, up to 16*NT rows per tile.
+// bf16/fp16 storage, D in {64, 128, 256}, up to 16*RT rows (queries x GQA
+// group) per workgroup.
 //
-// Per 32-token block a wave computes S^T = K Q^T with v_mfma_f32_16x16x32:
-// the A operand (K) is 8 consecutive head_dim elements of one token row, i.e.
-// one 16-byte load straight from the page.  The C layout of S^T gives each lane
-// 8 tokens of one row; that is exactly the B operand (P^T) of O^T = V^T P^T
-// once the token axis of the contraction is permuted consistently
-// (k = 8*lg + j  <->  token 4*lg + j for j < 4, 16 + 4*lg + j - 4 otherwise).
-// V^T's A operand needs 8 tokens of one head_dim column, so each wave stages
-// its V block transposed in a private LDS slab.  The four waves of a
-// workgroup take interleaved blocks (split-K inside the workgroup) and are
-// combined through LDS at the end.
+// The workgroup streams its token range in 64-token tiles through LDS: all
+// 256 threads load a tile with 16-byte loads (16 consecutive lanes read one
+// 256-byte K or V row of a page), the next tile's loads are issued before the
+// current tile is computed (register prefetch), and the page ids of the item
+// are staged in LDS once.  K is kept row-major with its 16-byte chunks
+// XOR-swizzled by token; V is stored transposed (head_dim-major) with its
+// tokens XOR-swizzled in groups of four, so the MFMA operand reads are
+// ds_read_b128 / ds_read_b64 with few bank conflicts.
+//
+// Waves own 16-row tiles of the query rows.  With RT <= 2 row tiles the four
+// waves also split the tile's tokens (4/RT ways) and are combined through LDS
+// at the end; with RT >= 4 every wave sees all tokens of its row tiles, so KV
+// is read from HBM once per workgroup however many rows it serves.
+//
+// Scores: S^T = K Q^T with v_mfma_f32_16x16x32 (A = 8 consecutive head_dim
+// elements of a token row, B = Q from registers).  The C layout of a 16-token
+// S^T tile gives lane (lg, lc) tokens 4*lg..4*lg+3 of row lc, which is exactly
+// the B operand (P^T) of v_mfma_f32_16x16x16 for O^T = V^T P^T, whose A
+// operand is 4 consecutive tokens of one head_dim row of the transposed V.
 typedef short v8s __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <typename T>
-__device__ __forceinline__ v4f mfma16(v8s a, v8s b, v4f c);
-template <>
-__device__ __forceinline__ v4f mfma16<bf16_t>(v8s a, v8s b, v4f c) {
+template <typename T> __device__ __forceinline__ v4f mfma_qk(v8s a, v8s b, v4f c);
+template <> __device__ __forceinline__ v4f mfma_qk<bf16_t>(v8s a, v8s b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-template <>
-__device__ __forceinline__ v4f mfma16<f16_t>(v8s a, v8s b, v4f c) {
+template <> __device__ __forceinline__ v4f mfma_qk<f16_t>(v8s a, v8s b, v4f c) {
   typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b),
-                                                c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+template <typename T> __device__ __forceinline__ v4f mfma_pv(v4s a, v4s b, v4f c);
+template <> __device__ __forceinline__ v4f mfma_pv<bf16_t>(v4s a, v4s b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ v4f mfma_pv<f16_t>(v4s a, v4s b, v4f c) {
+  typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, a), __builtin_bit_cast(v4h, b), c, 0, 0, 0);
 }
 
 template <typename T> __device__ __forceinline__ uint16_t pack16(float x);
@@ -184,37 +199,66 @@ template <> __device__ __forceinline__ uint16_t pack16<f16_t>(float x) {
   return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
-#define LDS_FENCE() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
+constexpr int kTile = 64;              // tokens per LDS tile
+constexpr int kMaxPagesLds = 1024;     // page ids of one item staged in LDS
 
-template <typename T, int D, int NT>
-__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
-  constexpr int KS = D / 32;          // contraction steps of Q.K^T
-  constexpr int MT = D / 16;          // head_dim tiles of O^T
-  constexpr int VROW = 36;            // transposed V row: 32 tokens + pad (16-bit units)
-  constexpr int VCH = D / 8;          // 16-byte chunks per token row
-  constexpr int SLAB = D * VROW;      // per-wave V^T slab (16-bit units)
-  constexpr int COMB = (MT * NT * 64 * 4 + NT * 64 * 2);   // floats per combine slot
-  constexpr int LDS_BYTES = (4 * SLAB * 2 > 2 * COMB * 4) ? 4 * SLAB * 2 : 2 * COMB * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
-  uint16_t* vt = reinterpret_cast<uint16_t*>(lds);
+template <int D>
+struct TileLds {
+  static constexpr int CPT = D / 8;                  // 16-byte chunks per token row
+  static constexpr int K_BYTES = kTile * D * 2;
+  static constexpr int V_BYTES = D * kTile * 2;
+};
+
+// V^T token swizzle: groups of four tokens are permuted per 8-row band of head_dim.
+__device__ __forceinline__ int vt_swz(int d) { return (4 * (d >> 3)) & (kTile - 4); }
+
+template <typename T, int D, int RT>
+__global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
+  constexpr int KS = D / 32;                         // QK contraction steps
+  constexpr int MT = D / 16;                         // O^T head_dim tiles
+  constexpr int CPT = D / 8;
+  constexpr int LCH = kTile * CPT / 256;             // 16-byte chunks per thread per tile (K and V each)
+  constexpr int NTW = RT <= 4 ? 1 : RT / 4;          // row tiles per wave
+  constexpr int TSPLIT = RT >= 4 ? 1 : 4 / RT;       // waves sharing a row tile (token split)
+  constexpr int STW = (kTile / 16) / TSPLIT;         // 16-token subtiles per wave per tile
+  constexpr int KV_BYTES = TileLds<D>::K_BYTES + TileLds<D>::V_BYTES;
+  constexpr int COMB_SLOT = (MT * 64 * 4 + 2 * 64) * 4;   // bytes: O^T frags + m + l of one wave
+  static_assert(TSPLIT == 1 || (TSPLIT - 1) * RT * COMB_SLOT <= KV_BYTES, "combine scratch must fit");
+  static_assert(LCH >= 1, "tile too small for the workgroup");
+
+  __shared__ __attribute__((aligned(16))) unsigned char kv_lds[KV_BYTES];
+  __shared__ int pg_lds[kMaxPagesLds];
+  uint16_t* kt = reinterpret_cast<uint16_t*>(kv_lds);
+  uint16_t* vt = reinterpret_cast<uint16_t*>(kv_lds + TileLds<D>::K_BYTES);
 
   const WorkItem it = a.items[blockIdx.x];
   const int kvh = blockIdx.y;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
-  const int g = a.g;
-  const int R = it.q_count * g;
-  const T* qbase = reinterpret_cast<const T*>(a.q);
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, lg = lane >> 4, lc = lane & 15;
+  const int g = a.g, R = it.q_count * g, ps = a.page_size;
   const T* kv = reinterpret_cast<const T*>(a.kv);
 
-  // Q^T as the B operand: lane holds Q[row = nt*16 + lc][d = ks*32 + 8*lg .. +7].
-  v8s qf[NT][KS];
+  // ---- page ids of the item
+  const int first_page = it.tok_begin / ps;
+  const int n_pages = (it.tok_begin + it.tok_count - 1) / ps - first_page + 1;
+  for (int i = tid; i < n_pages; i += 256) pg_lds[i] = a.pages[it.page_begin + first_page + i];
+
+  // ---- wave role
+  const int rt0 = (RT >= 4) ? w * NTW : (w % RT);
+  const int ts = (RT >= 4) ? 0 : (w / RT);
+  bool active[NTW];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int row = nt * 16 + lc;
+  for (int nt = 0; nt < NTW; ++nt) active[nt] = (rt0 + nt) * 16 < R;
+
+  // ---- Q as the B operand: lane holds Q[row = (rt0+nt)*16 + lc][d = ks*32 + 8*lg .. +7]
+  v8s qf[NTW][KS];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
+    const int row = (rt0 + nt) * 16 + lc;
     if (row < R) {
       const int j = row / g, hh = row - j * g;
       const int qi = a.q_index[it.q_begin + j];
-      const T* qp = qbase + (int64_t)qi * a.q_sn + (int64_t)(kvh * g + hh) * a.q_sh;
+      const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)qi * a.q_sn + (int64_t)(kvh * g + hh) * a.q_sh;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = *reinterpret_cast<const v8s*>(qp + ks * 32 + lg * 8);
     } else {
@@ -222,196 +266,181 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
       for (int ks = 0; ks < KS; ++ks) qf[nt][ks] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
+  __syncthreads();   // page ids staged
 
-  float m_run[NT], l_run[NT];
-  v4f o_acc[MT][NT];
+  // ---- tile loader: thread chunk c = i*256 + tid -> token c / CPT, column chunk c % CPT
+  v8s kp[LCH], vp[LCH];
+  auto load_tile = [&](int tile) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+    for (int i = 0; i < LCH; ++i) {
+      const int c = i * 256 + tid;
+      const int tl = tile * kTile + c / CPT;
+      if (tl < it.tok_count) {
+        const int tok = it.tok_begin + tl;
+        const int page = pg_lds[tok / ps - first_page];
+        const int64_t base = kv_off(page, 0, tok % ps, kvh, ps, a.hkv, D) + (c % CPT) * 8;
+        const int64_t vstep = (int64_t)ps * a.hkv * D;     // K plane -> V plane of the page
+        kp[i] = *reinterpret_cast<const v8s*>(kv + base);
+        vp[i] = *reinterpret_cast<const v8s*>(kv + base + vstep);
+      } else {
+        kp[i] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
+        vp[i] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+  };
+
+  float m_run[NTW], l_run[NTW];
+  v4f o_acc[NTW][MT];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
     m_run[nt] = -INFINITY;
     l_run[nt] = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) o_acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) o_acc[nt][mt] = v4f{0.f, 0.f, 0.f, 0.f};
   }
 
-  uint16_t* my_vt = vt + w * SLAB;
-  const int n_blocks = (it.tok_count + 31) >> 5;
-  const int ps = a.page_size;
-
-  for (int blk = w; blk < n_blocks; blk += 4) {
-    const int tl0 = blk * 32;   // item-relative first token of the block
-    // ---- K (A operand) straight from the pages
-    v8s kf[2][KS];
+  const int n_tiles = (it.tok_count + kTile - 1) / kTile;
+  load_tile(0);
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    __syncthreads();                                   // previous tile's LDS reads are done
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int tl = tl0 + tt * 16 + lc;
-      if (tl < it.tok_count) {
-        const int tok = it.tok_begin + tl;
-        const int page = a.pages[it.page_begin + tok / ps];
-        const T* kr = kv + kv_off(page, 0, tok % ps, kvh, ps, a.hkv, D);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kf[tt][ks] = *reinterpret_cast<const v8s*>(kr + ks * 32 + lg * 8);
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kf[tt][ks] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-    // ---- V block: 16-byte chunks, chunk c -> token c / VCH, column chunk c % VCH
-    v8s vr[VCH / 2];
-#pragma unroll
-    for (int i = 0; i < VCH / 2; ++i) {
-      const int c = i * 64 + lane;
-      const int tl = tl0 + c / VCH;
-      if (tl < it.tok_count) {
-        const int tok = it.tok_begin + tl;
-        const int page = a.pages[it.page_begin + tok / ps];
-        vr[i] = *reinterpret_cast<const v8s*>(kv + kv_off(page, 1, tok % ps, kvh, ps, a.hkv, D) + (c % VCH) * 8);
-      } else {
-        vr[i] = v8s{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-    // ---- S^T = K Q^T
-    v4f s[2][NT];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) acc = mfma16<T>(kf[tt][ks], qf[nt][ks], acc);
-        s[tt][nt] = acc;
-      }
-    // ---- V^T into this wave's slab (previous block's reads are complete:
-    //      they fed the MFMAs of the last iteration)
-    LDS_FENCE();
-#pragma unroll
-    for (int i = 0; i < VCH / 2; ++i) {
-      const int c = i * 64 + lane;
-      const int t = c / VCH, d0 = (c % VCH) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) my_vt[(d0 + e) * VROW + t] = (uint16_t)vr[i][e];
-    }
-    // ---- online softmax (log2 domain) per row = lane column
-    v8s pf[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float x[8];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tl = tl0 + tt * 16 + 4 * lg + i;
-          x[tt * 4 + i] = (tl < it.tok_count) ? s[tt][nt][i] * a.scale_log2 : -INFINITY;
-        }
-      float mx = x[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[nt], mx);       // finite: the block has a valid token
-      const float alpha = exp2f(m_run[nt] - m_new);   // 0 when m_run == -inf
-      float psum = 0.f;
-      v8s pk;
+    for (int i = 0; i < LCH; ++i) {
+      const int c = i * 256 + tid;
+      const int t = c / CPT, ch = c % CPT;
+      *reinterpret_cast<v8s*>(kt + (t * CPT + (ch ^ (t & (CPT - 1)))) * 8) = kp[i];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float p = exp2f(x[e] - m_new);
-        psum += p;
-        pk[e] = (short)pack16<T>(p);
+        const int d = ch * 8 + e;
+        vt[d * kTile + (t ^ vt_swz(d))] = (uint16_t)vp[i][e];
       }
-      pf[nt] = pk;
+    }
+    __syncthreads();                                   // tile staged
+    if (tile + 1 < n_tiles) load_tile(tile + 1);       // in flight during the compute below
+
+    const int tl0 = tile * kTile;
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) {
+      if (!active[nt]) continue;
+      // scores of the wave's subtiles (lane: tokens 16*sub + 4*lg + r, row lc)
+      float x[STW][4];
+#pragma unroll
+      for (int sb = 0; sb < STW; ++sb) {
+        const int sub = ts * STW + sb;
+        const int t = sub * 16 + lc;
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int ch = ks * 4 + lg;
+          const v8s kf = *reinterpret_cast<const v8s*>(kt + (t * CPT + (ch ^ (t & (CPT - 1)))) * 8);
+          acc = mfma_qk<T>(kf, qf[nt][ks], acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tl = tl0 + sub * 16 + 4 * lg + r;
+          x[sb][r] = (tl < it.tok_count) ? acc[r] * a.scale_log2 : -INFINITY;
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sb = 0; sb < STW; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[sb][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[nt], mx);
+      const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = exp2f(m_run[nt] - msafe);    // 0 while nothing was seen
+      float psum = 0.f;
+      v4s pf[STW];
+#pragma unroll
+      for (int sb = 0; sb < STW; ++sb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = exp2f(x[sb][r] - msafe);
+          psum += p;
+          pf[sb][r] = (short)pack16<T>(p);
+        }
       l_run[nt] = l_run[nt] * alpha + psum;
       m_run[nt] = m_new;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) o_acc[mt][nt] *= alpha;
-    }
-    LDS_FENCE();
-    // ---- O^T += V^T P^T
+      for (int mt = 0; mt < MT; ++mt) {
+        v4f o = o_acc[nt][mt] * alpha;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const uint16_t* src = my_vt + (mt * 16 + lc) * VROW + 4 * lg;
-      const v4s lo = *reinterpret_cast<const v4s*>(src);
-      const v4s hi = *reinterpret_cast<const v4s*>(src + 16);
-      const v8s vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) o_acc[mt][nt] = mfma16<T>(vf, pf[nt], o_acc[mt][nt]);
+        for (int sb = 0; sb < STW; ++sb) {
+          const int d = mt * 16 + lc;
+          const int tok = (ts * STW + sb) * 16 + 4 * lg;
+          const v4s vf = *reinterpret_cast<const v4s*>(vt + d * kTile + (tok ^ vt_swz(d)));
+          o = mfma_pv<T>(vf, pf[sb], o);
+        }
+        o_acc[nt][mt] = o;
+      }
     }
   }
 
   // row sums over the four lane groups
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     l_run[nt] += __shfl_xor(l_run[nt], 16, 64);
     l_run[nt] += __shfl_xor(l_run[nt], 32, 64);
   }
 
-  // ---- combine the four waves: 3 -> 1, 2 -> 0, then 1 -> 0
-  float* comb = reinterpret_cast<float*>(lds);
-  __syncthreads();   // every wave is done with its V slab
+  // ---- token-split waves (ts > 0) hand their state to the ts == 0 wave of the row tile
+  if constexpr (TSPLIT > 1) {
+    float* comb = reinterpret_cast<float*>(kv_lds);
+    __syncthreads();                                   // tiles no longer needed
+    if (ts > 0 && active[0]) {
+      float* slot = comb + ((ts - 1) * RT + rt0) * (COMB_SLOT / 4);
 #pragma unroll
-  for (int round = 0; round < 2; ++round) {
-    const int senders_lo = (round == 0) ? 2 : 1;   // waves [senders_lo, 2*senders_lo) send
-    if (w >= senders_lo && w < 2 * senders_lo) {
-      float* slot = comb + (w - senders_lo) * COMB;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          *reinterpret_cast<v4f*>(slot + ((mt * NT + nt) * 64 + lane) * 4) = o_acc[mt][nt];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        slot[MT * NT * 64 * 4 + nt * 64 + lane] = m_run[nt];
-        slot[MT * NT * 64 * 4 + NT * 64 + nt * 64 + lane] = l_run[nt];
-      }
+      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<v4f*>(slot + (mt * 64 + lane) * 4) = o_acc[0][mt];
+      slot[MT * 256 + lane] = m_run[0];
+      slot[MT * 256 + 64 + lane] = l_run[0];
     }
     __syncthreads();
-    if (w < senders_lo) {
-      const float* slot = comb + w * COMB;
+    if (ts == 0 && active[0]) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float mb = slot[MT * NT * 64 * 4 + nt * 64 + lane];
-        const float lb = slot[MT * NT * 64 * 4 + NT * 64 + nt * 64 + lane];
-        const float M = fmaxf(m_run[nt], mb);
-        const float ca = (M == -INFINITY) ? 0.f : exp2f(m_run[nt] - M);
+      for (int s2 = 1; s2 < TSPLIT; ++s2) {
+        const float* slot = comb + ((s2 - 1) * RT + rt0) * (COMB_SLOT / 4);
+        const float mb = slot[MT * 256 + lane], lb = slot[MT * 256 + 64 + lane];
+        const float M = fmaxf(m_run[0], mb);
+        const float ca = (M == -INFINITY) ? 0.f : exp2f(m_run[0] - M);
         const float cb = (M == -INFINITY) ? 0.f : exp2f(mb - M);
-        l_run[nt] = l_run[nt] * ca + lb * cb;
-        m_run[nt] = M;
+        l_run[0] = l_run[0] * ca + lb * cb;
+        m_run[0] = M;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const v4f ob = *reinterpret_cast<const v4f*>(slot + ((mt * NT + nt) * 64 + lane) * 4);
-          o_acc[mt][nt] = o_acc[mt][nt] * ca + ob * cb;
-        }
+        for (int mt = 0; mt < MT; ++mt)
+          o_acc[0][mt] = o_acc[0][mt] * ca + *reinterpret_cast<const v4f*>(slot + (mt * 64 + lane) * 4) * cb;
       }
     }
-    __syncthreads();
   }
 
-  __shared__ int s_last[kMaxRows];
-  if (w == 0) {
-  // ---- wave 0 writes: lane holds O^T[d = mt*16 + 4*lg + i][row = nt*16 + lc]
+  // ---- writes: lane holds O^T[d = mt*16 + 4*lg + i][row = (rt0+nt)*16 + lc]
+  if (ts == 0) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int row = nt * 16 + lc;
-    if (row >= R) continue;
-    const int j = row / g, hh = row - j * g, head = kvh * g + hh;
-    const float l = l_run[nt];
-    const float inv = (l > 0.f) ? 1.f / l : 0.f;
-    if (it.out_row < 0) {
-      const int qi = a.q_index[it.q_begin + j];
-      T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int row = (rt0 + nt) * 16 + lc;
+      if (!active[nt] || row >= R) continue;
+      const int j = row / g, hh = row - j * g, head = kvh * g + hh;
+      const float l = l_run[nt];
+      const float inv = (l > 0.f) ? 1.f / l : 0.f;
+      if (it.out_row < 0) {
+        const int qi = a.q_index[it.q_begin + j];
+        T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        v4s pk;
+        for (int mt = 0; mt < MT; ++mt) {
+          v4s pk;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pk[i] = (short)pack16<T>(o_acc[mt][nt][i] * inv);
-        *reinterpret_cast<v4s*>(op + mt * 16 + 4 * lg) = pk;
+          for (int i = 0; i < 4; ++i) pk[i] = (short)pack16<T>(o_acc[nt][mt][i] * inv);
+          *reinterpret_cast<v4s*>(op + mt * 16 + 4 * lg) = pk;
+        }
+      } else {
+        float* op = a.part_o + ((int64_t)(it.out_row + j) * a.hq + head) * D;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<v4f*>(op + mt * 16 + 4 * lg) = o_acc[nt][mt] * inv;
       }
-    } else {
-      float* op = a.part_o + ((int64_t)(it.out_row + j) * a.hq + head) * D;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<v4f*>(op + mt * 16 + 4 * lg) = o_acc[mt][nt] * inv;
+      if (lg == 0) store_row_lse<T>(a, it, j, head, m_run[nt], l);
     }
-    if (lg == 0) store_row_lse<T>(a, it, j, head, m_run[nt], l);
   }
-  }
+  __shared__ int s_last[kMaxTileRows];
   if (it.out_row >= 0 && a.counters) fused_merge_epilogue<T, D>(a, it, kvh, s_last);
 }
 
@@ -610,7 +639,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   BE_REQUIRE(dtype == BE_F32 || dtype == BE_F16 || dtype == BE_BF16, "unknown dtype %d", dtype);
   const int g = hq / hkv;
   if (d != 64 && d != 128 && d != 256) return fail(BE_ERR_UNSUPPORTED, "head_dim %d: kernels exist for 64, 128, 256", d);
-  if (g > kMaxRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d", g, kMaxRows);
+  if (g > kMaxTileRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d", g, kMaxTileRows);
   if (num_cus <= 0) num_cus = 256;
 
   // ---- validate levels, collect groups
@@ -643,18 +672,22 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   }
 
   bool mfma = (dtype != BE_F32) && !(flags & BE_PLAN_FORCE_VALU);
-  if (mfma && d == 256 && g > 16) mfma = false;          // the 32-row D=256 MFMA tile does not fit in VGPRs
-  const int rows_cap = (mfma && d == 256) ? 16 : kMaxRows;
+  if (!mfma && g > kMaxRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d (VALU kernel)", g, kMaxRows);
+  if (mfma && d == 256 && g > 64) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds 64 at head_dim 256", g);
+  // rows per workgroup: MFMA 8 row tiles (4 at head_dim 256, VGPR budget), VALU 32
+  const int rows_cap = mfma ? (d == 256 ? 64 : kMaxTileRows) : kMaxRows;
   const int q_tile = std::max(1, rows_cap / g);
 
   // ---- split-K chunk: about two workgroups per CU over all (tile, chunk, head)
   int64_t work = 0;   // token-tiles
   for (const Group& gr : groups)
     if (gr.q1 > gr.q0 && gr.kv_len > 0) work += ceil_div(gr.q1 - gr.q0, q_tile) * (int64_t)gr.kv_len;
-  const int64_t target = 2 * (int64_t)num_cus;
+  const int64_t target = 3 * (int64_t)num_cus;
   int64_t chunk = ceil_div(work * hkv, target);
-  chunk = std::max<int64_t>(128, ceil_div(chunk, 128) * 128);
-  if (chunk > (int64_t)1 << 30) chunk = (int64_t)1 << 30;
+  chunk = std::max<int64_t>(128, ceil_div(chunk, 64) * 64);
+  // an item's page ids are staged in LDS: at most kMaxPagesLds pages per item
+  const int64_t chunk_cap = std::max<int64_t>(64, ((int64_t)(kMaxPagesLds - 1) * page_size) / 64 * 64);
+  if (chunk > chunk_cap) chunk = chunk_cap;
 
   // ---- per-query partial counts
   std::vector<int> cnt(num_queries, 0);
@@ -769,7 +802,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   info->num_pages = num_pages;
   info->dtype = dtype;
   info->kernel = mfma ? 1 : 0;
-  info->tile_rows = max_r <= 16 ? 16 : 32;
+  info->tile_rows = max_r <= 16 ? 16 : max_r <= 32 ? 32 : max_r <= 64 ? 64 : 128;
   info->chunk_tokens = (int32_t)std::min<int64_t>(chunk, INT32_MAX);
   info->plan_ints = (int32_t)off;
   info->off_items = (int32_t)off_items;
@@ -798,13 +831,23 @@ static int launch_attn(const be_attn_plan_info* info, AttnArgs& a, hipStream_t s
   const dim3 grid(info->num_items, info->num_kv_heads);
   if (info->kernel == 1) {
     if constexpr (sizeof(T) == 2) {
-      const bool one = info->tile_rows <= 16;
+      const int rt = info->tile_rows / 16;
+#define BE_TILE_LAUNCH(DD)                                                                    \
+  switch (rt) {                                                                               \
+    case 1: attn_tile_kernel<T, DD, 1><<<grid, 256, 0, st>>>(a); break;                       \
+    case 2: attn_tile_kernel<T, DD, 2><<<grid, 256, 0, st>>>(a); break;                       \
+    case 4: attn_tile_kernel<T, DD, 4><<<grid, 256, 0, st>>>(a); break;                       \
+    case 8: if (DD == 256) return fail(BE_ERR_UNSUPPORTED, "128-row tiles at head_dim 256"); \
+            attn_tile_kernel<T, DD, (DD == 256 ? 4 : 8)><<<grid, 256, 0, st>>>(a); break;     \
+    default: return fail(BE_ERR_INVALID, "corrupt plan: tile_rows %d", info->tile_rows);      \
+  }
       switch (info->head_dim) {
-        case 64:  one ? attn_mfma_kernel<T, 64, 1><<<grid, 256, 0, st>>>(a) : attn_mfma_kernel<T, 64, 2><<<grid, 256, 0, st>>>(a); break;
-        case 128: one ? attn_mfma_kernel<T, 128, 1><<<grid, 256, 0, st>>>(a) : attn_mfma_kernel<T, 128, 2><<<grid, 256, 0, st>>>(a); break;
-        case 256: one ? attn_mfma_kernel<T, 256, 1><<<grid, 256, 0, st>>>(a) : attn_mfma_kernel<T, 256, 2><<<grid, 256, 0, st>>>(a); break;
+        case 64: BE_TILE_LAUNCH(64) break;
+        case 128: BE_TILE_LAUNCH(128) break;
+        case 256: BE_TILE_LAUNCH(256) break;
         default: return fail(BE_ERR_UNSUPPORTED, "head_dim %d", info->head_dim);
       }
+#undef BE_TILE_LAUNCH
     } else {
       return fail(BE_ERR_UNSUPPORTED, "MFMA kernel needs fp16/bf16 storage");
     }
