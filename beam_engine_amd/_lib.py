@@ -19,6 +19,7 @@ BE_F32, BE_F16, BE_BF16 = 0, 1, 2
 BE_OK, BE_ERR_INVALID, BE_ERR_HIP, BE_ERR_CAPACITY, BE_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
 BE_PLAN_FORCE_VALU = 1
 BE_PLAN_FUSED_MERGE = 2
+BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
 
@@ -85,7 +86,7 @@ def load() -> ctypes.CDLL:
     lib.be_attn_plan.argtypes = [ctypes.POINTER(BeLevel), i32, i32, i32, i32, i32, i32, i32, i32, i32, i32,
                                  vp, i64, ctypes.POINTER(BeAttnPlanInfo)]
     lib.be_attn_run.argtypes = [ctypes.POINTER(BeAttnPlanInfo), vp, vp, vp, i64, i64, vp, vp, i64, i64, vp,
-                                ctypes.c_float, vp]
+                                ctypes.c_float, i32, vp]
     lib.be_merge_states.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]
     lib.be_beam_topk_workspace_bytes.argtypes = [i32, i32, i32]
     lib.be_beam_topk_workspace_bytes.restype = i64

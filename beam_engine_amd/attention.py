@@ -180,7 +180,8 @@ class _PagedPlanner:
         self._dtype = q_data_type
 
     # ---------------------------------------------------------------- run
-    def _run(self, q: torch.Tensor, kv: torch.Tensor, out: Optional[torch.Tensor], return_lse: bool):
+    def _run(self, q: torch.Tensor, kv: torch.Tensor, out: Optional[torch.Tensor], return_lse: bool,
+             between=None):
         info = self._info
         if info is None:
             raise RuntimeError("plan() must be called before run()")
@@ -211,11 +212,16 @@ class _PagedPlanner:
                 (out.stride(1) * out.element_size()) % 16:
             raise ValueError("out must be 16-byte aligned in every row (vector stores)")
         lse = torch.empty((q.shape[0], hq), dtype=torch.float32, device=q.device) if return_lse else None
-        rc = lib.be_attn_run(ctypes.byref(info), self._plan_dev.data_ptr(), _lib.ptr(self._partials),
-                             q.data_ptr(), q.stride(0), q.stride(1), kv.data_ptr(), out.data_ptr(),
-                             out.stride(0), out.stride(1), _lib.ptr(lse), self._sm_scale,
-                             _lib.stream_ptr(q.device))
-        _lib.check(rc, "attention run")
+        args = (ctypes.byref(info), self._plan_dev.data_ptr(), _lib.ptr(self._partials), q.data_ptr(),
+                q.stride(0), q.stride(1), kv.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+                _lib.ptr(lse), self._sm_scale)
+        stream = _lib.stream_ptr(q.device)
+        if between is None:
+            _lib.check(lib.be_attn_run(*args, _lib.BE_RUN_ATTENTION | _lib.BE_RUN_MERGE, stream), "attention run")
+        else:   # e.g. an event recorded between the attention and the merge kernels
+            _lib.check(lib.be_attn_run(*args, _lib.BE_RUN_ATTENTION, stream), "attention run")
+            between()
+            _lib.check(lib.be_attn_run(*args, _lib.BE_RUN_MERGE, stream), "attention merge")
         return (out, lse) if return_lse else out
 
     @property
@@ -260,8 +266,8 @@ class MultiLevelCascadeAttentionWrapper(_PagedPlanner):
                           num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, q_data_type)
 
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
-            return_lse: bool = False):
-        return self._run(q, paged_kv_cache, out, return_lse)
+            return_lse: bool = False, between=None):
+        return self._run(q, paged_kv_cache, out, return_lse, between)
 
     forward = run
 
@@ -286,8 +292,8 @@ class BatchDecodeWithPagedKVCacheWrapper(_PagedPlanner):
                           num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, q_data_type)
 
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
-            return_lse: bool = False):
-        return self._run(q, paged_kv_cache, out, return_lse)
+            return_lse: bool = False, between=None):
+        return self._run(q, paged_kv_cache, out, return_lse, between)
 
     forward = run
 

@@ -878,7 +878,8 @@ static int launch_merge(const be_attn_plan_info* info, MergeArgs& m, int count, 
 
 int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials, const void* q,
              int64_t q_sn, int64_t q_sh, const void* kv, void* out, int64_t o_sn, int64_t o_sh,
-             float* lse, float sm_scale, void* stream) {
+             float* lse, float sm_scale, int phases, void* stream) {
+  BE_REQUIRE(phases >= 1 && phases <= 3, "phases must be a non-empty subset of attention | merge");
   BE_REQUIRE(info && plan, "null plan");
   BE_REQUIRE(q && kv && out, "null q / kv / out");
   BE_REQUIRE(info->num_part_rows == 0 || partials, "plan needs %lld bytes of partial scratch", (long long)info->partial_bytes);
@@ -905,7 +906,7 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
                    ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(partials) + info->counter_offset)
                    : nullptr;
   int rc = BE_OK;
-  if (info->num_items > 0) {
+  if ((phases & BE_RUN_ATTENTION) && info->num_items > 0) {
     switch (info->dtype) {
       case BE_F32: rc = launch_attn<float>(info, a, st); break;
       case BE_F16: rc = launch_attn<f16_t>(info, a, st); break;
@@ -914,6 +915,7 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
     }
     if (rc) return rc;
   }
+  if (!(phases & BE_RUN_MERGE)) return rc;
   MergeArgs m;
   m.part_o = a.part_o; m.part_lse = a.part_lse;
   m.merge_rows = plan + info->off_merge_rows;
@@ -947,9 +949,9 @@ int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int nu
 
 int be_attn_run(const be_attn_plan_info* info, const int32_t* dev_plan, void* partials, const void* q,
                 int64_t q_stride_n, int64_t q_stride_h, const void* kv_layer, void* out, int64_t o_stride_n,
-                int64_t o_stride_h, float* lse, float sm_scale, void* stream) {
+                int64_t o_stride_h, float* lse, float sm_scale, int phases, void* stream) {
   return be::attn_run(info, dev_plan, partials, q, q_stride_n, q_stride_h, kv_layer, out, o_stride_n,
-                      o_stride_h, lse, sm_scale, stream);
+                      o_stride_h, lse, sm_scale, phases, stream);
 }
 
 int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, const float* lse_b, float* o_out,

@@ -1,0 +1,159 @@
+"""Batched beam-search decode loop over the HIP path.
+
+Restates the reference's driver (src/beam_engine/beam.py:48-352) for several
+requests decoded together in one forward per step:
+
+* prefill: prompt pages allocated per request (``add_root_sequence``), one
+  batched prefill, then each request's first B tokens of top-2B of the last
+  position (beam.py:105-141) expand its root;
+* per step (beam.py:145-317): cascade (or flat) metadata from the trie, the
+  write location and position of every candidate, one decode forward with the
+  attention plan built once and reused by every layer (the reference builds a
+  FlashInfer wrapper per step, models/modeling_llama.py:732-755), GPU beam
+  selection per request (log_softmax + top-2B + global top-B), trie update
+  with the step's fork copies in one launch.
+
+``kernel_type``: "cascade" (per-level groups of the reference's
+get_cascade_input), "flat" (each candidate's whole path, the baseline) or
+"auto" (the cost-model picker chooses per step).  ``include_self`` False
+follows the reference's cascade convention (a query does not attend to the
+K/V it appends in the same step, beam_state.py:347-354).
+"""
+
+from __future__ import annotations
+
+import time
+from typing import List, Optional, Sequence
+
+import torch
+
+from .attention import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAttentionWrapper
+from .beam_state import BeamGenerateResult, BeamState, BeamToken
+from .beam_strategy import VanillaBeamSearchStrategy
+from .page_table import PageTable
+from .selection import beam_topk
+
+
+class BatchedBeamSearch:
+    def __init__(self, model, page_table: PageTable, beam_size: int,
+                 strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
+                 temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False):
+        if kernel_type not in ("cascade", "flat", "auto"):
+            raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat' or 'auto'.")
+        self.model = model
+        self.pt = page_table
+        self.beam_size = beam_size
+        self.strategy = strategy or VanillaBeamSearchStrategy()
+        self.kernel_type = kernel_type
+        self.temperature = temperature
+        self.include_self = include_self
+        self.device = page_table.device
+        self.state = BeamState(beam_size, page_table)
+        self.ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
+        self.cascade = MultiLevelCascadeAttentionWrapper(1, self.ws)
+        self.flat = BatchDecodeWithPagedKVCacheWrapper(self.ws)
+        self.last_attn = None
+        self.picker = None
+        self.step_log: List[dict] = []
+        self._staging = torch.empty(4 * 4096, dtype=torch.int64, pin_memory=True)
+        self.attn_timer = None          # optional callable(layer, fn) used by benchmarks
+
+    # ---------------------------------------------------------------- prefill
+    @torch.no_grad()
+    def prefill(self, prompts: Sequence[Sequence[int]]) -> torch.Tensor:
+        if len({len(p) for p in prompts}) != 1:
+            raise ValueError("batched prefill needs prompts of equal length")
+        page_ids = []
+        for r, p in enumerate(prompts):
+            nodes = self.state.add_root_sequence(list(p), request_id=r)
+            page_ids.append([n.page_id for n in nodes])
+        ids = torch.tensor([list(p) for p in prompts], dtype=torch.long, device=self.device)
+        logits = self.model.prefill(ids, self.pt, page_ids)
+        results = []
+        k = min(2 * self.beam_size, logits.shape[-1])
+        vals, idx = beam_topk(logits, k, temperature=self.temperature)
+        vals, idx = vals[:, : self.beam_size].tolist(), idx[:, : self.beam_size].tolist()
+        for r, cand in enumerate(self.state.candidates):
+            results.append(BeamGenerateResult(cand, [BeamToken(int(t), float(s)) for t, s in zip(idx[r], vals[r])]))
+        self.state.add_filtered_results(results)
+        return logits
+
+    # ---------------------------------------------------------------- decode
+    def _plan(self, kind: str):
+        m = self.model
+        cfg = m.cfg
+        st = self.state
+        if kind == "cascade":
+            levels = st._cascade_lists()
+            if self.include_self:
+                raise NotImplementedError("include_self with cascade levels")
+            w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
+            w.plan([l[0] for l in levels], [l[1] for l in levels], [l[2] for l in levels], [l[3] for l in levels],
+                   cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pt.page_size,
+                   causal=True, q_data_type=m.dtype)
+        else:
+            kvp, kvi, lpl = st.flat_lists(self.include_self)
+            w = self.flat
+            w.plan(kvp, kvi, lpl, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                   self.pt.page_size, q_data_type=m.dtype)
+        self.last_attn = w
+        return w
+
+    @torch.no_grad()
+    def step(self) -> None:
+        st = self.state
+        n = len(st.candidates)
+        kind = self.kernel_type
+        if kind == "auto":
+            kind = self.picker.choose(st) if self.picker is not None else "cascade"
+        w = self._plan(kind)
+        qids = st.query_token_ids()
+        wp, wpos = st.write_locations()
+        pos = st.position_ids()
+        if self._staging.numel() < 4 * n:
+            self._staging = torch.empty(8 * n, dtype=torch.int64, pin_memory=True)
+        stg = self._staging[: 4 * n].view(4, n)
+        stg[0] = torch.tensor(qids)
+        stg[1] = torch.tensor(wp)
+        stg[2] = torch.tensor(wpos)
+        stg[3] = torch.tensor(pos)
+        dev = stg.to(self.device, non_blocking=True)
+        tok, wpg, wps, psn = dev[0], dev[1].to(torch.int32), dev[2].to(torch.int32), dev[3]
+
+        if self.attn_timer is None:
+            def attn(li, q, kv):
+                return w.run(q, kv)
+        else:
+            def attn(li, q, kv):
+                return self.attn_timer(li, lambda between: w.run(q, kv, between=between), w)
+        logits = self.model.decode(tok, psn, wpg, wps, self.pt, attn)
+        self._select(logits)
+        self.step_log.append({"n": n, "kind": kind})
+
+    def _select(self, logits: torch.Tensor) -> None:
+        st = self.state
+        cands = st.candidates
+        results: List[BeamGenerateResult] = []
+        b = 0
+        while b < len(cands):
+            rid = cands[b].request_id
+            e = b
+            while e < len(cands) and cands[e].request_id == rid:
+                e += 1
+            results.extend(self.strategy.select_from_logits(st, logits[b:e], self.temperature, rows=(b, e)))
+            b = e
+        st.add_filtered_results(results)
+
+    # ---------------------------------------------------------------- results
+    def final_sequences(self, num_return: Optional[int] = None):
+        reqs = sorted({c.request_id for c in self.state.candidates})
+        return {r: self.strategy.get_final_sequences(self.state, num_return, r) for r in reqs}
+
+    @torch.no_grad()
+    def generate(self, prompts: Sequence[Sequence[int]], steps: int):
+        self.prefill(prompts)
+        for _ in range(steps):
+            if self.strategy.should_stop(self.state, 1 << 30, 0):
+                break
+            self.step()
+        return self.final_sequences()

@@ -1,0 +1,175 @@
+"""Random-init Llama-shaped decoder for the end-to-end beam-search harness.
+
+The model math around attention (embeddings, RMSNorm, RoPE, projections,
+SwiGLU MLP, LM head) is plain torch (hipBLASLt GEMMs); it is not part of the
+decode hot path.  The reference runs the same structure through its modified
+HF Llama (src/beam_engine/models/modeling_llama.py:428-562, 668-831): per
+layer q/k/v projection, RoPE, append of the new K/V to the paged cache
+(write_blocks_vectorized, :506-514), decode attention over the pages
+(:517-525), output projection, MLP.  Here the append is ``PageTable`` (HIP
+kernel) and attention is whatever ``attn(layer, q, kv_layer)`` the caller
+passes (the HIP cascade / flat wrappers).
+
+Prefill (prompt processing) is out of the hot path: causal attention is done
+in float32 with explicit matmuls (contiguous operands) and the prompt's K/V is
+scattered into its pages with one append per layer.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, List, Optional
+
+import torch
+import torch.nn.functional as F
+
+
+@dataclass
+class LlamaConfig:
+    num_hidden_layers: int = 32
+    hidden_size: int = 4096
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 14336
+    vocab_size: int = 128256
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    max_position_embeddings: int = 8192
+    init_std: float = 0.02
+
+    @staticmethod
+    def llama3_8b() -> "LlamaConfig":
+        return LlamaConfig()
+
+    @staticmethod
+    def tiny(layers: int = 2, vocab: int = 1000) -> "LlamaConfig":
+        return LlamaConfig(num_hidden_layers=layers, hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
+                           head_dim=32, intermediate_size=512, vocab_size=vocab, max_position_embeddings=4096)
+
+    def num_params(self) -> int:
+        h, kvd = self.hidden_size, self.num_key_value_heads * self.head_dim
+        per_layer = h * (h + 2 * kvd) + h * h + 3 * h * self.intermediate_size + 2 * h
+        return self.num_hidden_layers * per_layer + 2 * self.vocab_size * h + h
+
+
+class LlamaDecoder:
+    """Weights ~ N(0, init_std) in ``dtype``; norms at 1."""
+
+    def __init__(self, cfg: LlamaConfig, device="cuda", dtype=torch.bfloat16, seed: int = 0):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        gen = torch.Generator(device=self.device).manual_seed(seed)
+        h, hq, hkv, d = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+
+        def w(*shape):
+            t = torch.empty(shape, device=self.device, dtype=dtype)
+            t.normal_(0.0, cfg.init_std, generator=gen)
+            return t
+
+        self.embed = w(cfg.vocab_size, h)
+        self.layers = []
+        for _ in range(cfg.num_hidden_layers):
+            self.layers.append(dict(
+                ln1=torch.ones(h, device=self.device, dtype=dtype),
+                wqkv=w((hq + 2 * hkv) * d, h),
+                wo=w(h, hq * d),
+                ln2=torch.ones(h, device=self.device, dtype=dtype),
+                wgu=w(2 * cfg.intermediate_size, h),
+                wd=w(h, cfg.intermediate_size),
+            ))
+        self.norm = torch.ones(h, device=self.device, dtype=dtype)
+        self.lm_head = w(cfg.vocab_size, h)
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64, device=self.device) / d))
+        t = torch.arange(cfg.max_position_embeddings, dtype=torch.float64, device=self.device)
+        freqs = torch.outer(t, inv)
+        emb = torch.cat([freqs, freqs], dim=-1)
+        self.cos = emb.cos().to(dtype)
+        self.sin = emb.sin().to(dtype)
+
+    # ---------------------------------------------------------------- pieces
+    def _rms(self, x: torch.Tensor, wgt: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, (x.shape[-1],), wgt, self.cfg.rms_norm_eps)
+
+    @staticmethod
+    def _rotate_half(x):
+        x1, x2 = x.chunk(2, dim=-1)
+        return torch.cat((-x2, x1), dim=-1)
+
+    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """x [..., T, H, D], pos [..., T] -> HF-style rotary embedding."""
+        cos = self.cos[pos].unsqueeze(-2)
+        sin = self.sin[pos].unsqueeze(-2)
+        return x * cos + self._rotate_half(x) * sin
+
+    def _qkv(self, layer, h):
+        cfg = self.cfg
+        hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        qkv = F.linear(h, layer["wqkv"])
+        q = qkv[..., : hq * d].unflatten(-1, (hq, d))
+        k = qkv[..., hq * d: (hq + hkv) * d].unflatten(-1, (hkv, d))
+        v = qkv[..., (hq + hkv) * d:].unflatten(-1, (hkv, d))
+        return q, k, v
+
+    def _mlp(self, layer, x):
+        h = self._rms(x, layer["ln2"])
+        gu = F.linear(h, layer["wgu"])
+        g, u = gu.chunk(2, dim=-1)
+        return x + F.linear(F.silu(g) * u, layer["wd"])
+
+    # ---------------------------------------------------------------- prefill
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor, page_table, page_ids: List[List[int]]) -> torch.Tensor:
+        """Prompts ``input_ids [R, S]`` (equal lengths); writes every prompt
+        token's K/V into the request's pages; returns last-position logits [R, V]."""
+        cfg = self.cfg
+        r, s = input_ids.shape
+        hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        ps = page_table.page_size
+        pos = torch.arange(s, device=self.device).unsqueeze(0).expand(r, s)
+        pages = torch.tensor([[p[i // ps] for i in range(s)] for p in page_ids], dtype=torch.int32,
+                             device=self.device).reshape(-1)
+        slots = (torch.arange(s, device=self.device, dtype=torch.int32) % ps).repeat(r)
+        causal = torch.full((s, s), float("-inf"), device=self.device).triu(1)
+        x = F.embedding(input_ids, self.embed)
+        for li, layer in enumerate(self.layers):
+            h = self._rms(x, layer["ln1"])
+            q, k, v = self._qkv(layer, h)
+            q = self._rope(q, pos)
+            k = self._rope(k, pos)
+            page_table.write_blocks_vectorized(li, pages, k.reshape(r * s, hkv, d).contiguous(),
+                                               v.reshape(r * s, hkv, d).contiguous(), slots)
+            # causal GQA attention in float32 (contiguous operands)
+            qf = q.float().permute(0, 2, 1, 3).contiguous()                                  # [R, Hq, S, D]
+            kf = k.float().repeat_interleave(hq // hkv, dim=2).permute(0, 2, 3, 1).contiguous()  # [R, Hq, D, S]
+            vf = v.float().repeat_interleave(hq // hkv, dim=2).permute(0, 2, 1, 3).contiguous()  # [R, Hq, S, D]
+            sc = torch.matmul(qf, kf) * (d ** -0.5) + causal
+            o = torch.matmul(torch.softmax(sc, dim=-1), vf)                                 # [R, Hq, S, D]
+            o = o.permute(0, 2, 1, 3).reshape(r, s, hq * d).to(self.dtype)
+            x = x + F.linear(o, layer["wo"])
+            x = self._mlp(layer, x)
+        last = self._rms(x[:, -1], self.norm)
+        return F.linear(last, self.lm_head)
+
+    # ---------------------------------------------------------------- decode
+    @torch.no_grad()
+    def decode(self, token_ids: torch.Tensor, positions: torch.Tensor, write_pages: torch.Tensor,
+               write_pos: torch.Tensor, page_table, attn: Callable) -> torch.Tensor:
+        """One token per candidate: ``token_ids/positions/write_pages/write_pos [N]``
+        (device).  ``attn(layer, q [N, Hq, D], kv_layer) -> o [N, Hq, D]``.
+        Returns logits [N, V]."""
+        n = token_ids.shape[0]
+        cfg = self.cfg
+        x = F.embedding(token_ids, self.embed)
+        for li, layer in enumerate(self.layers):
+            h = self._rms(x, layer["ln1"])
+            q, k, v = self._qkv(layer, h)
+            q = self._rope(q, positions)
+            k = self._rope(k, positions)
+            page_table.write_blocks_vectorized(li, write_pages, k, v, write_pos)
+            o = attn(li, q, page_table.kv_cache_at_layer[li])
+            x = x + F.linear(o.reshape(n, -1), layer["wo"])
+            x = self._mlp(layer, x)
+        return F.linear(self._rms(x, self.norm), self.lm_head)

@@ -145,11 +145,15 @@ int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int nu
  * float [num_queries, Hq]) receives the natural-log log-sum-exp; a query with
  * no keys gets o = 0 and lse = -inf.  dev_plan is the device copy of the plan,
  * partials points at info->partial_bytes of device scratch.  Runs of one plan
- * must be stream-ordered (they share the scratch and its merge counters). */
+ * must be stream-ordered (they share the scratch and its merge counters).
+ * phases selects the kernels launched (BE_RUN_ATTENTION | BE_RUN_MERGE for a
+ * full run; the two halves may be issued separately, in that order). */
+#define BE_RUN_ATTENTION 1   /* phases: the attention kernel                     */
+#define BE_RUN_MERGE 2       /* phases: the split-K merge and zero-fill kernels   */
 int be_attn_run(const be_attn_plan_info* info, const int32_t* dev_plan, void* partials,
                 const void* q, int64_t q_stride_n, int64_t q_stride_h, const void* kv_layer,
                 void* out, int64_t o_stride_n, int64_t o_stride_h, float* lse, float sm_scale,
-                void* stream);
+                int phases, void* stream);
 
 /* be_merge_states: (o, lse) <- merge((o_a, lse_a), (o_b, lse_b)) for n x heads
  * rows of head_dim; o_* are float [n, heads, D] contiguous, lse natural log.
