@@ -564,36 +564,79 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnArgs a) {
 }
 
 // ================================================================== merge kernel
-// One wave per (merged query, head): o = sum_i e^(lse_i - M) o_i / sum_i e^(lse_i - M).
+// One workgroup per merged query: the lse of every (partial row, head) pair is
+// read in parallel and turned into normalised weights in LDS, then every
+// thread accumulates 4 consecutive head_dim columns of one head over the rows
+// (independent loads, no dependent chain).
+constexpr int kMergeMaxRows = 64;
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int head = blockIdx.y * 4 + w;
-  if (head >= a.hq) return;
+  __shared__ float wgt[kMergeMaxRows * kMaxTileRows];   // [row][head] weights
+  __shared__ int rows_s[kMergeMaxRows];
+  __shared__ float lse_h[kMaxTileRows];
+  const int tid = threadIdx.x;
   const int qi = a.merge_q[blockIdx.x];
   const int b = a.merge_ptr[blockIdx.x], e = a.merge_ptr[blockIdx.x + 1];
-  float M = -INFINITY;
-  for (int i = b; i < e; ++i) M = fmaxf(M, a.part_lse[(int64_t)a.merge_rows[i] * a.hq + head]);
-  constexpr int PER = D / 64;
-  float acc[PER];
+  const int hq = a.hq;
+  T* out = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn;
+  if (e - b > kMergeMaxRows || hq > kMaxTileRows) {
+    // long merges: one wave per head, sequential over rows
+    for (int head = tid >> 6; head < hq; head += 4) {
+      const int lane = tid & 63;
+      float M = -INFINITY;
+      for (int i = b; i < e; ++i) M = fmaxf(M, a.part_lse[(int64_t)a.merge_rows[i] * hq + head]);
+      float z = 0.f, acc[D / 64];
 #pragma unroll
-  for (int k = 0; k < PER; ++k) acc[k] = 0.f;
-  float z = 0.f;
-  if (M != -INFINITY) {
-    for (int i = b; i < e; ++i) {
-      const int64_t row = (int64_t)a.merge_rows[i] * a.hq + head;
-      const float wgt = expf(a.part_lse[row] - M);
-      z += wgt;
-      const float* op = a.part_o + row * D;
+      for (int k = 0; k < D / 64; ++k) acc[k] = 0.f;
+      if (M != -INFINITY)
+        for (int i = b; i < e; ++i) {
+          const int64_t row = (int64_t)a.merge_rows[i] * hq + head;
+          const float w = expf(a.part_lse[row] - M);
+          z += w;
 #pragma unroll
-      for (int k = 0; k < PER; ++k) acc[k] += wgt * op[lane + 64 * k];
+          for (int k = 0; k < D / 64; ++k) acc[k] += w * a.part_o[row * D + lane + 64 * k];
+        }
+      const float inv = (z > 0.f) ? 1.f / z : 0.f;
+#pragma unroll
+      for (int k = 0; k < D / 64; ++k) out[(int64_t)head * a.o_sh + lane + 64 * k] = from_f32<T>(acc[k] * inv);
+      if (a.out_lse && lane == 0) a.out_lse[(int64_t)qi * hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
     }
+    return;
   }
-  const float inv = (z > 0.f) ? 1.f / z : 0.f;
-  T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh;
+  const int nr = e - b;
+  for (int i = tid; i < nr; i += 256) rows_s[i] = a.merge_rows[b + i];
+  __syncthreads();
+  for (int i = tid; i < nr * hq; i += 256) {
+    const int r = i / hq, h = i - r * hq;
+    wgt[r * hq + h] = a.part_lse[(int64_t)rows_s[r] * hq + h];
+  }
+  __syncthreads();
+  for (int h = tid; h < hq; h += 256) {
+    float M = -INFINITY;
+    for (int r = 0; r < nr; ++r) M = fmaxf(M, wgt[r * hq + h]);
+    float z = 0.f;
+    if (M != -INFINITY)
+      for (int r = 0; r < nr; ++r) z += expf(wgt[r * hq + h] - M);
+    const float inv = (z > 0.f) ? 1.f / z : 0.f;
+    for (int r = 0; r < nr; ++r) wgt[r * hq + h] = (M != -INFINITY) ? expf(wgt[r * hq + h] - M) * inv : 0.f;
+    lse_h[h] = (z > 0.f) ? M + logf(z) : -INFINITY;
+  }
+  __syncthreads();
+  constexpr int C4 = D / 4;                       // float4 columns per head
+  for (int i = tid; i < hq * C4; i += 256) {
+    const int h = i / C4, c = i - h * C4;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < nr; ++r) {
+      const v4f o = *reinterpret_cast<const v4f*>(a.part_o + ((int64_t)rows_s[r] * hq + h) * D + 4 * c);
+      acc += o * wgt[r * hq + h];
+    }
+    T* op = out + (int64_t)h * a.o_sh + 4 * c;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) op[lane + 64 * k] = from_f32<T>(acc[k] * inv);
-  if (a.out_lse && lane == 0) a.out_lse[(int64_t)qi * a.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
+    for (int k = 0; k < 4; ++k) op[k] = from_f32<T>(acc[k]);
+  }
+  if (a.out_lse)
+    for (int h = tid; h < hq; h += 256) a.out_lse[(int64_t)qi * hq + h] = lse_h[h];
 }
 
 // One wave owns one row, so outputs may alias inputs (every lane reads the
@@ -689,11 +732,20 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   const int64_t chunk_cap = std::max<int64_t>(64, ((int64_t)(kMaxPagesLds - 1) * page_size) / 64 * 64);
   if (chunk > chunk_cap) chunk = chunk_cap;
 
+  // A chunk of a group writes rows x D x 4 bytes of partials per KV head while
+  // reading 4 x D bytes per token (bf16 K + V): keep chunks >= 4 x rows tokens
+  // so partial traffic stays under ~1/4 of the KV bytes it summarises.
+  auto group_chunk = [&](const Group& gr) -> int64_t {
+    const int64_t rows = (int64_t)std::min(q_tile, gr.q1 - gr.q0) * g;
+    int64_t c = std::max<int64_t>(chunk, ceil_div(4 * rows, 64) * 64);
+    return std::min(c, chunk_cap);
+  };
+
   // ---- per-query partial counts
   std::vector<int> cnt(num_queries, 0);
   for (const Group& gr : groups) {
     if (gr.kv_len <= 0) continue;
-    const int nch = (int)ceil_div(gr.kv_len, chunk);
+    const int nch = (int)ceil_div(gr.kv_len, group_chunk(gr));
     for (int qi = gr.q0; qi < gr.q1; ++qi) cnt[qi] += nch;
   }
 
@@ -705,8 +757,9 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   for (const Group& gr : groups) {
     if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
     flops += 4.0 * d * hq * (double)gr.kv_len * (gr.q1 - gr.q0);
-    for (int t0 = 0; t0 < gr.kv_len; t0 += (int)chunk) {
-      const int tc = (int)std::min<int64_t>(chunk, gr.kv_len - t0);
+    const int64_t gchunk = group_chunk(gr);
+    for (int t0 = 0; t0 < gr.kv_len; t0 += (int)gchunk) {
+      const int tc = (int)std::min<int64_t>(gchunk, gr.kv_len - t0);
       for (int qa = gr.q0; qa < gr.q1; qa += q_tile) {
         const int qn = std::min(q_tile, gr.q1 - qa);
         bool direct = true;
@@ -865,7 +918,7 @@ static int launch_attn(const be_attn_plan_info* info, AttnArgs& a, hipStream_t s
 
 template <typename T>
 static int launch_merge(const be_attn_plan_info* info, MergeArgs& m, int count, hipStream_t st) {
-  const dim3 grid(count, (info->num_qo_heads + 3) / 4);
+  const dim3 grid(count);
   switch (info->head_dim) {
     case 64: merge_kernel<T, 64><<<grid, 256, 0, st>>>(m); break;
     case 128: merge_kernel<T, 128><<<grid, 256, 0, st>>>(m); break;
