@@ -22,7 +22,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
-    # packed-fp32 VALU forms stay off on this pool (traps)
+    # packed fp32 VALU forms (v_pk_*_f32) are disabled: some of their forms have
+    # returned wrong results on this GPU pool without raising an error
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", f"-I{os.path.join(ROOT, 'include')}",
 ]

@@ -1,4 +1,4 @@
-"""End-to-end beam-search benchmark.
+"""End-to-end beam-search benchmark (the 8-request, beam-16 Llama-3-8B workload).
 
 Random-init Llama-3-8B-shaped decoder (32 layers, hidden 4096, 32/8 heads,
 head_dim 128, FFN 14336, vocab 128256, bf16 weights ~ N(0, 0.02)), 8 requests

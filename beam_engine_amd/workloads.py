@@ -1,4 +1,4 @@
-"""Synthetic decode-attention workloads at the BASELINE configurations.
+"""Synthetic decode-attention workloads at the benchmark configurations.
 
 Each builder returns a ``Workload``: cascade levels (per-level qo_indptr,
 kv_indptr, kv_indices, last_page_len), the flat arrays over the same pages
@@ -78,7 +78,7 @@ def shared_prefix(name, n_req, beams, prefix, suffixes, hq, hkv, d, page=16, not
 
 
 def config2():
-    """4 requests x beam 8, Llama-3-8B GQA 32/8, D 128, prefix 2048, suffix 128."""
+    """Kernel-level cascade shape: 4 requests x beam 8, Llama-3-8B GQA 32/8, D 128, prefix 2048, suffix 128."""
     return shared_prefix("c2", 4, 8, 2048, [128] * 32, 32, 8, 128,
                          note="4 req x beam 8, 32/8 heads, D128, bf16, page 16, prefix 2048, suffix 128")
 
@@ -91,7 +91,7 @@ def north_star():
 
 
 def config5(seed: int = 5):
-    """70B layer shape 64/8, 2 requests x beam 64, prefix 32768,
+    """Long-context stress shape: 70B layer shape 64/8, 2 requests x beam 64, prefix 32768,
     suffix ~ U[1, 512] per beam from ``seed``."""
     rng = np.random.default_rng(seed)
     suf = rng.integers(1, 513, size=128)
@@ -100,7 +100,7 @@ def config5(seed: int = 5):
 
 
 def config3():
-    """tree, beam 32, root 4096, fanout 2/4/4 with node lengths
+    """Multi-level tree, beam 32, root 4096, fanout 2/4/4 with node lengths
     256/128/64 and a 32-token leaf suffix (4 levels; the last chain and the
     suffix form one level)."""
     page = 16
@@ -123,7 +123,7 @@ def config3():
 
 
 def config1():
-    """1 request x beam 4, prefix 512, suffix 32, 8/8 heads, D 64, fp32, page 16."""
+    """CPU-path shape: 1 request x beam 4, prefix 512, suffix 32, 8/8 heads, D 64, fp32, page 16."""
     return shared_prefix("c1", 1, 4, 512, [32] * 4, 8, 8, 64,
                          note="1 req x beam 4, 8/8 heads, D64, fp32, page 16, prefix 512, suffix 32")
 

@@ -2,12 +2,12 @@
 """Benchmark driver (one JSON line on stdout).
 
 Default workload ``e2e``: end-to-end batched beam search on a random-init
-Llama-3-8B-shaped decoder; value = beam-decode tokens/s
+Llama-3-8B-shaped decoder (8 requests x beam 16, 1024-token prompts); value = beam-decode tokens/s
 = sum over requests of beam width x decode steps / decode wall time.  A step
 is one decode step of all 8 requests x 16 beams.
 
 Attention workloads (``--workload attn-c2|attn-ns|attn-c3|attn-c5|attn-c1``)
-time one decode-attention layer at a BASELINE shape over 32 distinct per-layer
+time one decode-attention layer at a benchmark shape over 32 distinct per-layer
 KV caches (working set above the 256 MB Infinity Cache); value = algorithmic
 HBM GB/s of the attention kernel.  ``--strategy flat`` runs the flat paged
 strategy on the same pages.
@@ -150,7 +150,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: bench.py --gpus N with N > 1 is not "
-                                   "supported (multi-GPU sharding is described in DESIGN.md, not built)"}))
+                                   "supported (sharding across GPUs is designed, not built)"}))
         return 2
     import torch
     if not torch.cuda.is_available():
