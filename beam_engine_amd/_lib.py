@@ -41,12 +41,18 @@ class BeLevel(ctypes.Structure):
     ]
 
 
+class BePlanCaps(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "max_items", "max_queries", "max_pages", "max_merge", "max_merge_rows", "max_zero", "tile_rows")]
+
+
 class BeAttnPlanInfo(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "num_items", "num_part_rows", "num_merge", "num_queries", "num_qo_heads", "num_kv_heads",
         "head_dim", "page_size", "num_pages", "dtype", "kernel", "tile_rows", "chunk_tokens",
         "plan_ints", "off_items", "off_qindex", "off_pages", "off_merge_q", "off_merge_ptr",
-        "off_merge_rows", "off_q_merge", "fused_merge", "num_zero", "off_zero_q", "off_zero_ptr")] + [
+        "off_merge_rows", "off_q_merge", "fused_merge", "num_zero", "off_zero_q", "off_zero_ptr",
+        "static_layout", "grid_items", "grid_merge", "grid_zero", "part_rows_cap")] + [
         ("partial_bytes", ctypes.c_int64),
         ("counter_offset", ctypes.c_int64),
         ("counter_bytes", ctypes.c_int64),
@@ -57,7 +63,8 @@ class BeAttnPlanInfo(ctypes.Structure):
 
 
 EXPORTS = (
-    "be_version", "be_last_error", "be_kv_append", "be_page_copy", "be_attn_plan", "be_attn_run",
+    "be_version", "be_last_error", "be_kv_append", "be_rope_qkv_append", "be_page_copy", "be_attn_plan",
+    "be_attn_run",
     "be_merge_states", "be_beam_topk_workspace_bytes", "be_beam_topk",
 )
 
@@ -82,16 +89,18 @@ def load() -> ctypes.CDLL:
     lib.be_version.restype = i32
     lib.be_last_error.restype = ctypes.c_char_p
     lib.be_kv_append.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i64, i64, i32, vp, vp]
+    lib.be_rope_qkv_append.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, i32, i32, vp, vp,
+                                       vp, vp]
     lib.be_page_copy.argtypes = [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp]
     lib.be_attn_plan.argtypes = [ctypes.POINTER(BeLevel), i32, i32, i32, i32, i32, i32, i32, i32, i32, i32,
-                                 vp, i64, ctypes.POINTER(BeAttnPlanInfo)]
+                                 ctypes.POINTER(BePlanCaps), vp, i64, ctypes.POINTER(BeAttnPlanInfo)]
     lib.be_attn_run.argtypes = [ctypes.POINTER(BeAttnPlanInfo), vp, vp, vp, i64, i64, vp, vp, i64, i64, vp,
                                 ctypes.c_float, i32, vp]
     lib.be_merge_states.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]
     lib.be_beam_topk_workspace_bytes.argtypes = [i32, i32, i32]
     lib.be_beam_topk_workspace_bytes.restype = i64
-    lib.be_beam_topk.argtypes = [vp, i32, i32, i32, i64, ctypes.c_float, i32, vp, i32, vp, vp, vp, vp, vp,
-                                 vp, i64, vp]
+    lib.be_beam_topk.argtypes = [vp, i32, i32, i32, i64, ctypes.c_float, i32, vp, i32, i32, vp, i32, vp, vp, vp,
+                                 vp, vp, vp, i64, vp]
     for name in EXPORTS:
         if name not in ("be_version", "be_last_error", "be_beam_topk_workspace_bytes"):
             getattr(lib, name).restype = i32

@@ -110,6 +110,7 @@ class _PagedPlanner:
         self._dtype: Optional[torch.dtype] = None
         self._force_valu = False
         self._fused_merge = False
+        self._caps: Optional[_lib.BePlanCaps] = None
 
     # ---------------------------------------------------------------- plan
     def _plan_levels(self, qo: Sequence, kvp: Sequence, kvi: Sequence, lpl: Sequence, num_qo_heads: int,
@@ -153,6 +154,7 @@ class _PagedPlanner:
             buf = staging.acquire(cap)
             rc = lib.be_attn_plan(levels, len(qo), nq, num_qo_heads, num_kv_heads, head_dim, page_size,
                                   max(max_page + 1, 1), dt, flags, _num_cus(self._ws.device),
+                                  ctypes.byref(self._caps) if self._caps is not None else None,
                                   buf.data_ptr(), buf.numel(), ctypes.byref(info))
             if rc == _lib.BE_ERR_CAPACITY:
                 cap = 2 * buf.numel()
@@ -223,6 +225,15 @@ class _PagedPlanner:
             between()
             _lib.check(lib.be_attn_run(*args, _lib.BE_RUN_MERGE, stream), "attention merge")
         return (out, lse) if return_lse else out
+
+    def use_fixed_layout(self, max_items: int, max_queries: int, max_pages: int, max_merge: int,
+                         max_merge_rows: int, max_zero: int, tile_rows: int) -> None:
+        """Plan into a fixed-capacity layout from now on: every plan has the
+        same device addresses and launch sizes (the live counts are read on
+        the device), so runs can be captured in a HIP graph and replayed with
+        later plans.  A plan beyond a capacity raises MemoryError."""
+        self._caps = _lib.BePlanCaps(max_items, max_queries, max_pages, max_merge, max_merge_rows, max_zero,
+                                     tile_rows)
 
     @property
     def stats(self) -> PlanStats:

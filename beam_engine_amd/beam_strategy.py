@@ -83,6 +83,28 @@ class VanillaBeamSearchStrategy(BeamStrategy):
                 per[p].append(BeamToken(token_id=t, accumulated_score=s))
         return [BeamGenerateResult(candidate=c, children=per[i]) for i, c in enumerate(sub)]
 
+    def select_batched(self, beam_state: BeamState, logits: torch.Tensor,
+                       temperature: float = 1.0) -> List[BeamGenerateResult]:
+        """GPU selection for every request of a multi-request state in one
+        call: candidates of one request are consecutive; ``logits [N, V]``."""
+        cands = beam_state.candidates
+        if not cands:
+            return []
+        rows = []
+        for i, c in enumerate(cands):
+            if i == 0 or c.request_id != cands[i - 1].request_id:
+                rows.append(0)
+            rows[-1] += 1
+        k = decode_k(beam_state.beam_size, logits.shape[-1])
+        parents = torch.tensor([c.score for c in cands], dtype=torch.float64)
+        b = beam_state.beam_size
+        _, _, (par, tok, sc) = beam_topk(logits, k, parents, b, temperature, request_rows=rows)
+        per: List[List[BeamToken]] = [[] for _ in cands]
+        for p, t, s_ in zip(par.tolist(), tok.tolist(), sc.tolist()):
+            if p >= 0:
+                per[p].append(BeamToken(token_id=t, accumulated_score=s_))
+        return [BeamGenerateResult(candidate=c, children=per[i]) for i, c in enumerate(cands)]
+
     def should_stop(self, beam_state: BeamState, max_length: int, step: int) -> bool:
         """beam_strategy.py:490-517."""
         if step >= max_length:

@@ -39,6 +39,8 @@ struct WorkItem {
 };
 static_assert(sizeof(WorkItem) == 32, "WorkItem is 8 int32 words");
 
+constexpr int kPlanHeader = 16;    // int32 words of live counts at the start of a plan
+constexpr int kHdrItems = 0, kHdrMerge = 1, kHdrZero = 2, kHdrRows = 3;
 constexpr int kMaxRows = 32;       // rows (queries x GQA group) per VALU workgroup
 constexpr int kMaxTileRows = 128;  // rows per MFMA workgroup (8 row tiles of 16)
 
@@ -59,6 +61,7 @@ struct AttnArgs {
   const int32_t* merge_ptr;    // CSR of partial rows per merge-list entry
   const int32_t* merge_rows;
   int32_t* counters;           // [num_merge][hkv] arrivals, zero between runs
+  const int32_t* live_items;   // fixed layout: live item count (surplus workgroups exit)
   int page_size, hkv, hq, g;
   float scale_log2;   // sm_scale * log2(e)
 };
@@ -72,6 +75,7 @@ struct MergeArgs {
   void* out;
   int64_t o_sn, o_sh;
   float* out_lse;
+  const int32_t* live;         // fixed layout: live entry count (surplus workgroups exit)
   int hq;
 };
 
@@ -226,6 +230,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
   static_assert(TSPLIT == 1 || (TSPLIT - 1) * RT * COMB_SLOT <= KV_BYTES, "combine scratch must fit");
   static_assert(LCH >= 1, "tile too small for the workgroup");
 
+  if (a.live_items && (int)blockIdx.x >= *a.live_items) return;
   __shared__ __attribute__((aligned(16))) unsigned char kv_lds[KV_BYTES];
   __shared__ int pg_lds[kMaxPagesLds];
   uint16_t* kt = reinterpret_cast<uint16_t*>(kv_lds);
@@ -459,6 +464,7 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnArgs a) {
   __shared__ float vs[BT][D];
   __shared__ float psm[kMaxRows][BT];
   __shared__ float alpha_s[kMaxRows], l_s[kMaxRows], m_s[kMaxRows];
+  if (a.live_items && (int)blockIdx.x >= *a.live_items) return;
 
   const WorkItem it = a.items[blockIdx.x];
   const int kvh = blockIdx.y;
@@ -575,6 +581,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   __shared__ float wgt[kMergeMaxRows * kMaxTileRows];   // [row][head] weights
   __shared__ int rows_s[kMergeMaxRows];
   __shared__ float lse_h[kMaxTileRows];
+  if (a.live && (int)blockIdx.x >= *a.live) return;
   const int tid = threadIdx.x;
   const int qi = a.merge_q[blockIdx.x];
   const int b = a.merge_ptr[blockIdx.x], e = a.merge_ptr[blockIdx.x + 1];
@@ -672,8 +679,8 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 }  // namespace
 
 int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, int hkv, int d,
-              int page_size, int num_pages, int dtype, int flags, int num_cus, int32_t* out,
-              int64_t cap, be_attn_plan_info* info) {
+              int page_size, int num_pages, int dtype, int flags, int num_cus, const be_plan_caps* caps,
+              int32_t* out, int64_t cap, be_attn_plan_info* info) {
   BE_REQUIRE(info != nullptr && out != nullptr, "null plan buffer or info");
   BE_REQUIRE(num_levels >= 0 && (num_levels == 0 || levels != nullptr), "bad levels");
   BE_REQUIRE(num_queries >= 0, "num_queries must be >= 0");
@@ -718,7 +725,17 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   if (!mfma && g > kMaxRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d (VALU kernel)", g, kMaxRows);
   if (mfma && d == 256 && g > 64) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds 64 at head_dim 256", g);
   // rows per workgroup: MFMA 8 row tiles (4 at head_dim 256, VGPR budget), VALU 32
-  const int rows_cap = mfma ? (d == 256 ? 64 : kMaxTileRows) : kMaxRows;
+  int rows_cap = mfma ? (d == 256 ? 64 : kMaxTileRows) : kMaxRows;
+  if (caps) {
+    BE_REQUIRE(!(flags & BE_PLAN_FUSED_MERGE), "the fused merge is not available with a fixed-capacity layout");
+    const int tr = caps->tile_rows;
+    BE_REQUIRE(tr == 16 || tr == 32 || tr == 64 || tr == 128, "caps.tile_rows must be 16, 32, 64 or 128");
+    BE_REQUIRE(tr >= g, "caps.tile_rows %d smaller than the GQA group %d", tr, g);
+    BE_REQUIRE(caps->max_items >= 0 && caps->max_queries >= num_queries && caps->max_pages >= 0 &&
+                   caps->max_merge >= 0 && caps->max_merge_rows >= 0 && caps->max_zero >= 0,
+               "bad plan capacities (max_queries %d < %d queries?)", caps->max_queries, num_queries);
+    if (mfma) rows_cap = std::min(rows_cap, tr);
+  }
   const int q_tile = std::max(1, rows_cap / g);
 
   // ---- split-K chunk: about two workgroups per CU over all (tile, chunk, head)
@@ -810,20 +827,40 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
     merge_ptr.push_back((int)merge_rows.size());
   }
 
-  // ---- serialise
+  // ---- serialise: header of live counts, then the regions (sized to this
+  //      plan, or to the capacities of a fixed layout)
   const int64_t n_items = (int64_t)items.size();
-  int64_t off = 0;
-  const int64_t off_items = off;    off += n_items * 8;
-  const int64_t off_qindex = off;   off += num_queries;
-  const int64_t off_pages = off;    off += total_pages;
-  const int64_t off_mq = off;       off += (int64_t)merge_q.size();
-  const int64_t off_mp = off;       off += (int64_t)merge_ptr.size();
-  const int64_t off_mr = off;       off += (int64_t)merge_rows.size();
-  const int64_t off_qm = off;       off += num_queries;
-  const int64_t off_zq = off;       off += (int64_t)zero_q.size();
-  const int64_t off_zp = off;       off += (int64_t)zero_q.size() + 1;
+  if (caps) {
+    if (n_items > caps->max_items || total_pages > caps->max_pages || (int64_t)merge_q.size() > caps->max_merge ||
+        rows > caps->max_merge_rows || (int64_t)zero_q.size() > caps->max_zero)
+      return fail(BE_ERR_CAPACITY,
+                  "plan exceeds its fixed capacities: items %lld/%d pages %lld/%d merge %zu/%d rows %d/%d zero %zu/%d",
+                  (long long)n_items, caps->max_items, (long long)total_pages, caps->max_pages, merge_q.size(),
+                  caps->max_merge, rows, caps->max_merge_rows, zero_q.size(), caps->max_zero);
+  }
+  const int64_t c_items = caps ? caps->max_items : n_items;
+  const int64_t c_q = caps ? caps->max_queries : num_queries;
+  const int64_t c_pages = caps ? caps->max_pages : total_pages;
+  const int64_t c_merge = caps ? caps->max_merge : (int64_t)merge_q.size();
+  const int64_t c_rows = caps ? caps->max_merge_rows : (int64_t)merge_rows.size();
+  const int64_t c_zero = caps ? caps->max_zero : (int64_t)zero_q.size();
+  int64_t off = kPlanHeader;
+  const int64_t off_items = off;    off += c_items * 8;
+  const int64_t off_qindex = off;   off += c_q;
+  const int64_t off_pages = off;    off += c_pages;
+  const int64_t off_mq = off;       off += c_merge;
+  const int64_t off_mp = off;       off += c_merge + 1;
+  const int64_t off_mr = off;       off += c_rows;
+  const int64_t off_qm = off;       off += c_q;
+  const int64_t off_zq = off;       off += c_zero;
+  const int64_t off_zp = off;       off += c_zero + 1;
   off = ceil_div(off, 4) * 4;
   if (off > cap || off > INT32_MAX) return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  for (int i = 0; i < kPlanHeader; ++i) out[i] = 0;
+  out[kHdrItems] = (int32_t)n_items;
+  out[kHdrMerge] = (int32_t)merge_q.size();
+  out[kHdrZero] = (int32_t)zero_q.size();
+  out[kHdrRows] = rows;
   memcpy(out + off_items, items.data(), n_items * sizeof(WorkItem));
   for (int i = 0; i < num_queries; ++i) out[off_qindex + i] = i;
   {
@@ -841,7 +878,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   for (int qi = 0; qi < num_queries; ++qi) out[off_qm + qi] = -1;
   for (size_t m = 0; m < merge_q.size(); ++m) out[off_qm + merge_q[m]] = (int32_t)m;
   if (!zero_q.empty()) memcpy(out + off_zq, zero_q.data(), zero_q.size() * 4);
-  for (int64_t i = off_zp; i < off; ++i) out[i] = 0;     // zero_ptr: empty row ranges, then padding
+  for (int64_t i = off_zp; i < off_zp + (int64_t)zero_q.size() + 1; ++i) out[i] = 0;   // zero_ptr: empty ranges
 
   memset(info, 0, sizeof(*info));
   info->num_items = (int32_t)n_items;
@@ -855,7 +892,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   info->num_pages = num_pages;
   info->dtype = dtype;
   info->kernel = mfma ? 1 : 0;
-  info->tile_rows = max_r <= 16 ? 16 : max_r <= 32 ? 32 : max_r <= 64 ? 64 : 128;
+  info->tile_rows = caps ? caps->tile_rows : (max_r <= 16 ? 16 : max_r <= 32 ? 32 : max_r <= 64 ? 64 : 128);
   info->chunk_tokens = (int32_t)std::min<int64_t>(chunk, INT32_MAX);
   info->plan_ints = (int32_t)off;
   info->off_items = (int32_t)off_items;
@@ -869,7 +906,12 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   info->num_zero = (int32_t)zero_q.size();
   info->off_zero_q = (int32_t)off_zq;
   info->off_zero_ptr = (int32_t)off_zp;
-  info->counter_offset = ceil_div((int64_t)rows * hq * (d + 1) * 4, 256) * 256;
+  info->static_layout = caps ? 1 : 0;
+  info->grid_items = (int32_t)c_items;
+  info->grid_merge = (int32_t)c_merge;
+  info->grid_zero = (int32_t)c_zero;
+  info->part_rows_cap = (int32_t)(caps ? caps->max_merge_rows : rows);
+  info->counter_offset = ceil_div((int64_t)info->part_rows_cap * hq * (d + 1) * 4, 256) * 256;
   info->counter_bytes = info->fused_merge ? (int64_t)merge_q.size() * hkv * 4 : 0;
   info->partial_bytes = info->counter_offset + info->counter_bytes;
   info->kv_bytes = valid_tokens * hkv * d * es * 2;
@@ -881,7 +923,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
 // ================================================================== host: run
 template <typename T>
 static int launch_attn(const be_attn_plan_info* info, AttnArgs& a, hipStream_t st) {
-  const dim3 grid(info->num_items, info->num_kv_heads);
+  const dim3 grid(info->grid_items, info->num_kv_heads);
   if (info->kernel == 1) {
     if constexpr (sizeof(T) == 2) {
       const int rt = info->tile_rows / 16;
@@ -935,10 +977,10 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
   BE_REQUIRE(phases >= 1 && phases <= 3, "phases must be a non-empty subset of attention | merge");
   BE_REQUIRE(info && plan, "null plan");
   BE_REQUIRE(q && kv && out, "null q / kv / out");
-  BE_REQUIRE(info->num_part_rows == 0 || partials, "plan needs %lld bytes of partial scratch", (long long)info->partial_bytes);
+  BE_REQUIRE(info->part_rows_cap == 0 || partials, "plan needs %lld bytes of partial scratch", (long long)info->partial_bytes);
   BE_REQUIRE(info->num_qo_heads % info->num_kv_heads == 0, "corrupt plan info");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int64_t rows = info->num_part_rows;
+  const int64_t rows = info->part_rows_cap;
   AttnArgs a;
   a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;
   a.kv = kv; a.out = out; a.o_sn = o_sn; a.o_sh = o_sh; a.out_lse = lse;
@@ -955,11 +997,12 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
   a.q_merge = plan + info->off_q_merge;
   a.merge_ptr = plan + info->off_merge_ptr;
   a.merge_rows = plan + info->off_merge_rows;
+  a.live_items = info->static_layout ? plan + kHdrItems : nullptr;
   a.counters = (info->fused_merge && info->num_merge > 0)
                    ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(partials) + info->counter_offset)
                    : nullptr;
   int rc = BE_OK;
-  if ((phases & BE_RUN_ATTENTION) && info->num_items > 0) {
+  if ((phases & BE_RUN_ATTENTION) && info->grid_items > 0) {
     switch (info->dtype) {
       case BE_F32: rc = launch_attn<float>(info, a, st); break;
       case BE_F16: rc = launch_attn<f16_t>(info, a, st); break;
@@ -975,8 +1018,9 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
   m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse; m.hq = info->num_qo_heads;
   for (int pass = 0; pass < 2; ++pass) {
     // pass 0: split-K merge (separate-merge plans); pass 1: queries without keys
-    const int count = pass == 0 ? (info->fused_merge ? 0 : info->num_merge) : info->num_zero;
+    const int count = pass == 0 ? (info->fused_merge ? 0 : info->grid_merge) : info->grid_zero;
     if (count == 0) continue;
+    m.live = info->static_layout ? plan + (pass == 0 ? kHdrMerge : kHdrZero) : nullptr;
     m.merge_q = plan + (pass == 0 ? info->off_merge_q : info->off_zero_q);
     m.merge_ptr = plan + (pass == 0 ? info->off_merge_ptr : info->off_zero_ptr);
     switch (info->dtype) {
@@ -995,9 +1039,10 @@ extern "C" {
 
 int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int num_qo_heads,
                  int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype, int flags,
-                 int num_cus, int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info) {
+                 int num_cus, const be_plan_caps* caps, int32_t* host_plan, int64_t host_plan_capacity,
+                 be_attn_plan_info* info) {
   return be::attn_plan(levels, num_levels, num_queries, num_qo_heads, num_kv_heads, head_dim, page_size,
-                       num_pages, dtype, flags, num_cus, host_plan, host_plan_capacity, info);
+                       num_pages, dtype, flags, num_cus, caps, host_plan, host_plan_capacity, info);
 }
 
 int be_attn_run(const be_attn_plan_info* info, const int32_t* dev_plan, void* partials, const void* q,

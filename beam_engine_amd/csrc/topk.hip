@@ -228,77 +228,96 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
   const int cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
   float* cv = cand_val + ((int64_t)r * segs + s) * k;
   int32_t* ci = cand_idx + ((int64_t)r * segs + s) * k;
-  for (int j = threadIdx.x; j < k; j += kTopkThreads) {
-    if (j < cnt) {
-      const int p = pos[j];
-      const uint32_t key = keys[p];
-      const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
-      cv[j] = __uint_as_float(u);
-      ci[j] = b + p;
-    } else {
-      cv[j] = -INFINITY;
-      ci[j] = -1;   // empty slot (segment shorter than k)
-    }
+  // emit in ascending vocabulary index, so that candidate order = index order
+  for (int j = threadIdx.x; j < cnt; j += kTopkThreads) {
+    const int p = pos[j];
+    int rank = 0;
+    for (int t = 0; t < cnt; ++t) rank += (pos[t] < p);
+    const uint32_t key = keys[p];
+    const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+    cv[rank] = __uint_as_float(u);
+    ci[rank] = b + p;
+  }
+  for (int j = cnt + threadIdx.x; j < k; j += kTopkThreads) {
+    cv[j] = -INFINITY;
+    ci[j] = -1;   // empty slot (segment shorter than k)
   }
 }
 
 // ---------------------------------------------------------------- pass 3
+// Candidates are segment-major and index-ascending inside a segment, so their
+// position order is vocabulary order: the radix select's lowest-position tie
+// rule is the lowest-index rule.  The k selected are then ranked among
+// themselves by (value desc, index asc).
 __global__ __launch_bounds__(kTopkThreads) void topk_row_kernel(int segs, int k, const float* cand_val,
                                                                const int32_t* cand_idx, float* row_vals,
                                                                int32_t* row_idx) {
-  __shared__ uint64_t key[kMaxRowCand];
+  __shared__ uint32_t keys[kMaxRowCand];
+  __shared__ int pos[kMaxK];
+  __shared__ int hist[4 * 256];
+  __shared__ int suf[257];
+  __shared__ int misc[4];
   const int r = blockIdx.x;
   const int c = segs * k;
   const float* cv = cand_val + (int64_t)r * c;
   const int32_t* ci = cand_idx + (int64_t)r * c;
-  for (int i = threadIdx.x; i < c; i += kTopkThreads) {
-    const int32_t idx = ci[i];
-    key[i] = (idx < 0) ? 0ull : (((uint64_t)fkey(cv[i])) << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
-  }
+  for (int i = threadIdx.x; i < c; i += kTopkThreads) keys[i] = (ci[i] < 0) ? 0u : fkey(cv[i]);
   __syncthreads();
-  for (int i = threadIdx.x; i < c; i += kTopkThreads) {
-    const uint64_t me = key[i];
-    if (me == 0ull) continue;
+  const int cnt = block_select<uint32_t>(keys, c, k, pos, hist, suf, misc);
+  for (int i = threadIdx.x; i < cnt; i += kTopkThreads) {
+    const int p = pos[i];
+    const uint32_t kp = keys[p];
     int rank = 0;
-    for (int j = 0; j < c; ++j) rank += (key[j] > me);
-    if (rank < k) {
-      row_vals[(int64_t)r * k + rank] = cv[i];
-      row_idx[(int64_t)r * k + rank] = ci[i];
+    for (int j = 0; j < cnt; ++j) {
+      const uint32_t kj = keys[pos[j]];
+      rank += (kj > kp) || (kj == kp && pos[j] < p);
     }
+    row_vals[(int64_t)r * k + rank] = cv[p];
+    row_idx[(int64_t)r * k + rank] = ci[p];
   }
 }
 
 // ---------------------------------------------------------------- pass 4
+// grid.x = request; its rows are [req_row_ptr[r], req_row_ptr[r+1]) (all rows
+// when req_row_ptr is null).  Parents are emitted as global row indices.
 __global__ __launch_bounds__(kTopkThreads) void topk_global_kernel(int n_rows, int k, int beam,
-                                                                  const double* parent, const float* row_vals,
-                                                                  const int32_t* row_idx, int32_t* out_parent,
-                                                                  int32_t* out_token, double* out_score) {
+                                                                  const int32_t* req_row_ptr, const double* parent,
+                                                                  const float* row_vals, const int32_t* row_idx,
+                                                                  int32_t* out_parent, int32_t* out_token,
+                                                                  double* out_score) {
   __shared__ uint64_t keys[kMaxPool];
   __shared__ int pos[kMaxK];
   __shared__ int hist[4 * 256];
   __shared__ int suf[257];
   __shared__ int misc[4];
-  const int n = n_rows * k;
+  const int req = blockIdx.x;
+  const int rb = req_row_ptr ? req_row_ptr[req] : 0;
+  const int re = req_row_ptr ? req_row_ptr[req + 1] : n_rows;
+  int32_t* op = out_parent + (int64_t)req * beam;
+  int32_t* ot = out_token + (int64_t)req * beam;
+  double* os = out_score + (int64_t)req * beam;
+  const bool ok = rb >= 0 && re <= n_rows && rb <= re && (int64_t)(re - rb) * k <= kMaxPool;
+  const int n = ok ? (re - rb) * k : 0;
   for (int i = threadIdx.x; i < n; i += kTopkThreads) {
-    const int r = i / k;
-    keys[i] = dkey(parent[r] + (double)row_vals[i]);
+    const int r = rb + i / k;
+    keys[i] = dkey(parent[r] + (double)row_vals[(int64_t)rb * k + i]);
   }
   __syncthreads();
   const int cnt = block_select<uint64_t>(keys, n, beam, pos, hist, suf, misc);
-  // emit in pool-position order
+  // emit in pool-position order: rows ascending, children in selection order
   for (int i = threadIdx.x; i < cnt; i += kTopkThreads) {
     const int p = pos[i];
     int rank = 0;
     for (int j = 0; j < cnt; ++j) rank += (pos[j] < p);
-    const int r = p / k;
-    out_parent[rank] = r;
-    out_token[rank] = row_idx[p];
-    out_score[rank] = parent[r] + (double)row_vals[p];
+    const int r = rb + p / k;
+    op[rank] = r;
+    ot[rank] = row_idx[(int64_t)rb * k + p];
+    os[rank] = parent[r] + (double)row_vals[(int64_t)rb * k + p];
   }
   for (int i = cnt + threadIdx.x; i < beam; i += kTopkThreads) {
-    out_parent[i] = -1;
-    out_token[i] = -1;
-    out_score[i] = -INFINITY;
+    op[i] = -1;
+    ot[i] = -1;
+    os[i] = -INFINITY;
   }
 }
 
@@ -314,8 +333,9 @@ int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k) {
 }
 
 int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, float inv_temp, int k,
-                 const double* parent_scores, int beam, float* row_vals, int32_t* row_idx, int32_t* out_parent,
-                 int32_t* out_token, double* out_score, void* workspace, int64_t workspace_bytes, void* stream) {
+                 const double* parent_scores, int beam, int n_req, const int32_t* req_row_ptr, int max_req_rows,
+                 float* row_vals, int32_t* row_idx, int32_t* out_parent, int32_t* out_token, double* out_score,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
   BE_REQUIRE(logits && row_vals && row_idx, "null pointer");
   BE_REQUIRE(dtype == BE_F32 || dtype == BE_F16 || dtype == BE_BF16, "unknown dtype %d", dtype);
   BE_REQUIRE(n_rows > 0 && vocab > 0, "empty logits");
@@ -326,9 +346,13 @@ int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t r
   BE_REQUIRE(beam >= 0, "beam must be >= 0");
   if (beam > 0) {
     BE_REQUIRE(parent_scores && out_parent && out_token && out_score, "null selection output");
+    BE_REQUIRE(n_req >= 1 && (req_row_ptr != nullptr || n_req == 1), "n_req > 1 needs req_row_ptr");
+    BE_REQUIRE(n_req <= 65535, "too many requests");
     if (beam > be::kMaxK) return be::fail(BE_ERR_UNSUPPORTED, "beam = %d exceeds %d", beam, be::kMaxK);
-    if ((int64_t)n_rows * k > be::kMaxPool)
-      return be::fail(BE_ERR_UNSUPPORTED, "pool %d x %d exceeds %d entries", n_rows, k, be::kMaxPool);
+    const int rows = req_row_ptr ? max_req_rows : n_rows;
+    BE_REQUIRE(rows >= 0 && rows <= n_rows, "max_req_rows outside [0, n_rows]");
+    if ((int64_t)rows * k > be::kMaxPool)
+      return be::fail(BE_ERR_UNSUPPORTED, "pool %d x %d exceeds %d entries", rows, k, be::kMaxPool);
   }
   const int64_t need = be_beam_topk_workspace_bytes(n_rows, vocab, k);
   if (!workspace || workspace_bytes < need)
@@ -364,8 +388,8 @@ int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t r
   be::topk_row_kernel<<<n_rows, be::kTopkThreads, 0, st>>>(geo.segs, k, cand_val, cand_idx, row_vals, row_idx);
   BE_HIP_CHECK(hipGetLastError());
   if (beam > 0) {
-    be::topk_global_kernel<<<1, be::kTopkThreads, 0, st>>>(n_rows, k, beam, parent_scores, row_vals, row_idx,
-                                                          out_parent, out_token, out_score);
+    be::topk_global_kernel<<<n_req, be::kTopkThreads, 0, st>>>(n_rows, k, beam, req_row_ptr, parent_scores,
+                                                              row_vals, row_idx, out_parent, out_token, out_score);
     BE_HIP_CHECK(hipGetLastError());
   }
   return BE_OK;

@@ -60,7 +60,7 @@ class AttnTimer:
 
 def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 8, beam: int = 16,
             prompt_len: int = 1024, cfg: LlamaConfig = None, seed: int = 0, time_attention: bool = True,
-            max_pages: int = 8192):
+            max_pages: int = 8192, graphs: bool = True):
     cfg = cfg or LlamaConfig.llama3_8b()
     dev = torch.device("cuda")
     t0 = time.perf_counter()
@@ -72,7 +72,7 @@ def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 
         f"ready in {time.perf_counter() - t0:.1f} s")
     rng = np.random.default_rng(seed)
     prompts = rng.integers(0, cfg.vocab_size, size=(n_req, prompt_len)).tolist()
-    gen = BatchedBeamSearch(model, pt, beam, kernel_type=kernel_type)
+    gen = BatchedBeamSearch(model, pt, beam, kernel_type=kernel_type, graphs=graphs)
     timer = AttnTimer(kernel_type, cfg.num_key_value_heads, cfg.head_dim, 2) if time_attention else None
     t0 = time.perf_counter()
     gen.prefill(prompts)
@@ -166,7 +166,7 @@ def run_e2e_bench(args):
     steps = args.steps if args.steps is not None else 250
     warmup = args.warmup if args.warmup is not None else 5
     kind = args.strategy
-    gen, timer, wall, model, pt = run_e2e(steps, warmup, kind)
+    gen, timer, wall, model, pt = run_e2e(steps, warmup, kind, graphs=not getattr(args, "no_graphs", False))
     n = len(gen.state.candidates)
     tok_s = n * steps / wall
     att = summarize_attention(timer)

@@ -37,7 +37,8 @@ from .selection import beam_topk
 class BatchedBeamSearch:
     def __init__(self, model, page_table: PageTable, beam_size: int,
                  strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
-                 temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False):
+                 temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False,
+                 graphs: bool = False):
         if kernel_type not in ("cascade", "flat", "auto"):
             raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat' or 'auto'.")
         self.model = model
@@ -57,6 +58,8 @@ class BatchedBeamSearch:
         self.step_log: List[dict] = []
         self._staging = torch.empty(4 * 4096, dtype=torch.int64, pin_memory=True)
         self.attn_timer = None          # optional callable(layer, fn) used by benchmarks
+        self.graphs = graphs            # capture the non-attention work of a step in HIP graphs
+        self._gd = None
 
     # ---------------------------------------------------------------- prefill
     @torch.no_grad()
@@ -120,29 +123,33 @@ class BatchedBeamSearch:
         dev = stg.to(self.device, non_blocking=True)
         tok, wpg, wps, psn = dev[0], dev[1].to(torch.int32), dev[2].to(torch.int32), dev[3]
 
-        if self.attn_timer is None:
-            def attn(li, q, kv):
-                return w.run(q, kv)
+        timer = self.attn_timer
+
+        def attn(li, q, kv, out=None):
+            if timer is None:
+                return w.run(q, kv, out=out)
+            return timer(li, lambda between: w.run(q, kv, out=out, between=between), w)
+
+        if self.graphs and hasattr(self.model, "decode") and self._graph_ready(n):
+            self._gd.load_inputs(tok, psn, wpg, wps)
+            logits = self._gd.run(attn)
         else:
-            def attn(li, q, kv):
-                return self.attn_timer(li, lambda between: w.run(q, kv, between=between), w)
-        logits = self.model.decode(tok, psn, wpg, wps, self.pt, attn)
+            logits = self.model.decode(tok, psn, wpg, wps, self.pt, attn)
         self._select(logits)
         self.step_log.append({"n": n, "kind": kind})
 
+    def _graph_ready(self, n: int) -> bool:
+        """Capture the segment graphs once the candidate count is known (it
+        stays B per request); a different count runs eagerly."""
+        from .llama import GraphedDecoder
+        if self._gd is None:
+            self._gd = GraphedDecoder(self.model, self.pt, n)
+            self._gd.capture()
+        return self._gd.n == n
+
     def _select(self, logits: torch.Tensor) -> None:
         st = self.state
-        cands = st.candidates
-        results: List[BeamGenerateResult] = []
-        b = 0
-        while b < len(cands):
-            rid = cands[b].request_id
-            e = b
-            while e < len(cands) and cands[e].request_id == rid:
-                e += 1
-            results.extend(self.strategy.select_from_logits(st, logits[b:e], self.temperature, rows=(b, e)))
-            b = e
-        st.add_filtered_results(results)
+        st.add_filtered_results(self.strategy.select_batched(st, logits, self.temperature))
 
     # ---------------------------------------------------------------- results
     def final_sequences(self, num_return: Optional[int] = None):

@@ -156,20 +156,115 @@ class LlamaDecoder:
     # ---------------------------------------------------------------- decode
     @torch.no_grad()
     def decode(self, token_ids: torch.Tensor, positions: torch.Tensor, write_pages: torch.Tensor,
-               write_pos: torch.Tensor, page_table, attn: Callable) -> torch.Tensor:
+               write_pos: torch.Tensor, page_table, attn: Callable, fused_rope: bool = True) -> torch.Tensor:
         """One token per candidate: ``token_ids/positions/write_pages/write_pos [N]``
-        (device).  ``attn(layer, q [N, Hq, D], kv_layer) -> o [N, Hq, D]``.
-        Returns logits [N, V]."""
+        (device; positions int64, pages/slots int32).  ``attn(layer, q [N, Hq, D],
+        kv_layer) -> o [N, Hq, D]``.  With ``fused_rope`` RoPE and the K/V append
+        are one HIP kernel (bit-identical to the eager tensor code).  Returns
+        logits [N, V]."""
         n = token_ids.shape[0]
         cfg = self.cfg
         x = F.embedding(token_ids, self.embed)
         for li, layer in enumerate(self.layers):
             h = self._rms(x, layer["ln1"])
-            q, k, v = self._qkv(layer, h)
-            q = self._rope(q, positions)
-            k = self._rope(k, positions)
-            page_table.write_blocks_vectorized(li, write_pages, k, v, write_pos)
+            if fused_rope:
+                qkv = F.linear(h, layer["wqkv"])
+                q = page_table.write_rope_qkv(li, qkv, cfg.num_attention_heads, positions, self.cos, self.sin,
+                                              write_pages, write_pos)
+            else:
+                q, k, v = self._qkv(layer, h)
+                q = self._rope(q, positions)
+                k = self._rope(k, positions)
+                page_table.write_blocks_vectorized(li, write_pages, k, v, write_pos)
             o = attn(li, q, page_table.kv_cache_at_layer[li])
             x = x + F.linear(o.reshape(n, -1), layer["wo"])
             x = self._mlp(layer, x)
         return F.linear(self._rms(x, self.norm), self.lm_head)
+
+
+class GraphedDecoder:
+    """Decode forward with the non-attention work captured as HIP graphs.
+
+    Segment 0 = embedding + layer 0 up to its attention input (RMSNorm, fused
+    q|k|v projection, fused RoPE + KV append); segment l = the rest of layer
+    l-1 (output projection, residual, MLP) and layer l up to its attention
+    input; the last segment ends with the final norm and the LM head.  The
+    attention of every layer runs eagerly between two replays, from the plan
+    of the current step, into a fixed output buffer.  Inputs (token ids,
+    positions, write pages / slots) are copied into fixed device buffers
+    before the replays; the graphs share one memory pool and are replayed in
+    capture order.
+    """
+
+    def __init__(self, model: LlamaDecoder, page_table, n: int):
+        cfg = model.cfg
+        self.model, self.pt, self.n = model, page_table, n
+        dev = model.device
+        self.tok = torch.zeros(n, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(n, dtype=torch.long, device=dev)
+        self.wpg = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.wps = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.o = torch.zeros((n, cfg.num_attention_heads, cfg.head_dim), dtype=model.dtype, device=dev)
+        self.graphs = []
+        self.q = []
+        self.logits = None
+        self._pool = None
+        # page writes of the capture run go to a reserved page no candidate owns
+        self._scratch_page = page_table.reserve_block(page_table.max_num_pages - 1)
+
+    def _segment(self, l: int, x: Optional[torch.Tensor]):
+        m, cfg = self.model, self.model.cfg
+        if l == 0:
+            x = F.embedding(self.tok, m.embed)
+        else:
+            prev = m.layers[l - 1]
+            x = x + F.linear(self.o.reshape(self.n, -1), prev["wo"])
+            x = m._mlp(prev, x)
+        if l == cfg.num_hidden_layers:
+            return x, None, F.linear(m._rms(x, m.norm), m.lm_head)
+        layer = m.layers[l]
+        h = m._rms(x, layer["ln1"])
+        qkv = F.linear(h, layer["wqkv"])
+        q = self.pt.write_rope_qkv(l, qkv, cfg.num_attention_heads, self.pos, m.cos, m.sin, self.wpg, self.wps)
+        return x, q, None
+
+    @torch.no_grad()
+    def capture(self) -> None:
+        L = self.model.cfg.num_hidden_layers
+        # capture-time writes land in a scratch slot; real steps overwrite the inputs
+        self.wpg.fill_(self._scratch_page)
+        self.wps.zero_()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):              # warm the libraries (hipBLASLt handles, workspaces)
+            x = None
+            for l in range(L + 1):
+                x, _, _ = self._segment(l, x)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self._pool = torch.cuda.graph_pool_handle()
+        x = None
+        for l in range(L + 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self._pool):
+                x, q, logits = self._segment(l, x)
+            self.graphs.append(g)
+            self.q.append(q)
+            if logits is not None:
+                self.logits = logits
+        torch.cuda.synchronize()
+
+    def load_inputs(self, tok, pos, wpg, wps) -> None:
+        self.tok.copy_(tok, non_blocking=True)
+        self.pos.copy_(pos, non_blocking=True)
+        self.wpg.copy_(wpg, non_blocking=True)
+        self.wps.copy_(wps, non_blocking=True)
+
+    def run(self, attn: Callable) -> torch.Tensor:
+        """``attn(layer, q, kv_layer, out)`` must write the layer's attention into ``out``."""
+        L = self.model.cfg.num_hidden_layers
+        self.graphs[0].replay()
+        for l in range(L):
+            attn(l, self.q[l], self.pt.kv_cache_at_layer[l], self.o)
+            self.graphs[l + 1].replay()
+        return self.logits

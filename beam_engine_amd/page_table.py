@@ -99,6 +99,16 @@ class PageTable:
         self.allocated_pages.remove(page_idx)
         self.free_pages.append(page_idx)
 
+    def reserve_block(self, page_idx: int) -> int:
+        """Take one specific free page out of the free list (e.g. the last one,
+        as a scratch slot) without changing the FIFO order of the others."""
+        if page_idx in self.allocated_pages:
+            raise ValueError(f"Page {page_idx} is already allocated")
+        self.free_pages.remove(page_idx)
+        self.allocated_pages.add(page_idx)
+        self._refs[page_idx] = 1
+        return page_idx
+
     def num_free_pages(self) -> int:
         return len(self.free_pages)
 
@@ -189,6 +199,43 @@ class PageTable:
                               keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1), n, None,
                               _lib.stream_ptr(self.device))
         _lib.check(rc, "kv append")
+
+    def write_rope_qkv(self, layer: int, qkv: torch.Tensor, num_qo_heads: int, positions: torch.Tensor,
+                       cos: torch.Tensor, sin: torch.Tensor, page_indices: torch.Tensor, indices: torch.Tensor,
+                       q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Decode-step RoPE fused with the append: ``qkv [N, (Hq + 2 Hkv) * D]``
+        (q | k | v heads), ``positions [N]`` int64, HF cos/sin tables ``[max_pos, D]``.
+        Writes RoPE(k) and v to ``(page_indices[i], indices[i])`` and returns
+        RoPE(q) as ``[N, Hq, D]``."""
+        if layer < 0 or layer >= self.layer_num:
+            raise ValueError(f"Layer {layer} out of range (max: {self.layer_num - 1})")
+        n = qkv.shape[0]
+        width = (num_qo_heads + 2 * self.head_num) * self.head_dim
+        if qkv.dim() != 2 or qkv.shape[1] != width or qkv.stride(1) != 1:
+            raise ValueError(f"qkv must be [N, {width}] with a contiguous last dim")
+        if qkv.dtype != self.store_dtype or cos.dtype != self.store_dtype or sin.dtype != self.store_dtype:
+            raise ValueError(f"qkv and cos/sin tables must be {self.store_dtype}")
+        if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != self.head_dim or not cos.is_contiguous() \
+                or not sin.is_contiguous():
+            raise ValueError("cos/sin must be contiguous [max_pos, head_dim]")
+        for t, nm in ((qkv, "qkv"), (positions, "positions"), (page_indices, "page_indices"), (indices, "indices")):
+            _lib.require_device(t, nm)
+        if positions.dtype != torch.int64 or page_indices.dtype != torch.int32 or indices.dtype != torch.int32:
+            raise ValueError("positions must be int64, page_indices / indices int32")
+        if positions.numel() < n or page_indices.numel() < n or indices.numel() < n:
+            raise ValueError("positions / page_indices / indices shorter than qkv")
+        if q_out is None:
+            q_out = torch.empty((n, num_qo_heads, self.head_dim), dtype=qkv.dtype, device=qkv.device)
+        elif q_out.shape != (n, num_qo_heads, self.head_dim) or not q_out.is_contiguous() or q_out.dtype != qkv.dtype:
+            raise ValueError("q_out must be a contiguous [N, Hq, D] tensor of the storage dtype")
+        lib = _lib.load()
+        rc = lib.be_rope_qkv_append(qkv.data_ptr(), qkv.stride(0), _lib.dtype_code(self.store_dtype), n, num_qo_heads,
+                                    self.head_num, self.head_dim, positions.data_ptr(), cos.data_ptr(),
+                                    sin.data_ptr(), cos.shape[0], q_out.data_ptr(),
+                                    self.kv_cache_at_layer[layer].data_ptr(), self.max_num_pages, self.page_size,
+                                    page_indices.data_ptr(), indices.data_ptr(), None, _lib.stream_ptr(self.device))
+        _lib.check(rc, "rope append")
+        return q_out
 
     # ------------------------------------------------------------ flat views
     def get_k_buffer(self, layer: int) -> torch.Tensor:

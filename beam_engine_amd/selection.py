@@ -9,7 +9,9 @@ and tie order: see ``include/beam_engine_amd.h`` (be_beam_topk).
 
 from __future__ import annotations
 
-from typing import Optional, Tuple
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
 
 import torch
 
@@ -38,13 +40,17 @@ def decode_k(beam_size: int, vocab: int) -> int:
 
 
 def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor] = None, beam: int = 0,
-              temperature: float = 1.0, workspace: Optional[TopkWorkspace] = None):
-    """Row top-k of log_softmax(logits / T) and, when ``beam > 0``, the global
-    top-``beam`` of ``parent_scores[r] + logp`` (float64).
+              temperature: float = 1.0, workspace: Optional[TopkWorkspace] = None,
+              request_rows: Optional[Sequence[int]] = None):
+    """Row top-k of log_softmax(logits / T) and, when ``beam > 0``, the top-``beam``
+    of ``parent_scores[r] + logp`` (float64) within every request.
 
-    Returns ``(row_vals [N, k] f32, row_idx [N, k] i32)`` and, if beam > 0,
-    ``(parent [beam] i32, token [beam] i32, score [beam] f64)`` in emission
-    order (rows ascending, children in selection order)."""
+    ``request_rows`` partitions the rows into consecutive requests (default:
+    one request).  Returns ``(row_vals [N, k] f32, row_idx [N, k] i32)`` and, if
+    beam > 0, ``(parent [R * beam] i32 global row, token [R * beam] i32,
+    score [R * beam] f64)``; request q's entries are ``[q * beam, (q + 1) * beam)``
+    in emission order (rows ascending, children in selection order), unused
+    entries have parent -1."""
     lib = _lib.load()
     _lib.require_device(logits, "logits")
     if logits.dim() != 2:
@@ -62,20 +68,27 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
     row_vals = torch.empty((n, k), dtype=torch.float32, device=dev)
     row_idx = torch.empty((n, k), dtype=torch.int32, device=dev)
     outs = (None, None, None)
+    ps = ptr_dev = None
+    n_req, max_rows = 1, n
     if beam > 0:
         if parent_scores is None:
             raise ValueError("parent_scores are required when beam > 0")
         ps = parent_scores.to(device=dev, dtype=torch.float64).contiguous()
         if ps.numel() != n:
             raise ValueError("parent_scores must have one entry per row")
-        outs = (torch.empty(beam, dtype=torch.int32, device=dev), torch.empty(beam, dtype=torch.int32, device=dev),
-                torch.empty(beam, dtype=torch.float64, device=dev))
-    else:
-        ps = None
+        if request_rows is not None:
+            rows = [int(x) for x in request_rows]
+            if sum(rows) != n or min(rows, default=0) < 0:
+                raise ValueError("request_rows must partition the rows")
+            n_req, max_rows = len(rows), max(rows)
+            ptr_dev = torch.tensor(np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)).to(dev)
+        outs = (torch.empty(n_req * beam, dtype=torch.int32, device=dev),
+                torch.empty(n_req * beam, dtype=torch.int32, device=dev),
+                torch.empty(n_req * beam, dtype=torch.float64, device=dev))
     rc = lib.be_beam_topk(logits.data_ptr(), _lib.dtype_code(logits.dtype), n, v, logits.stride(0), inv_t, k,
-                          _lib.ptr(ps), beam, row_vals.data_ptr(), row_idx.data_ptr(), _lib.ptr(outs[0]),
-                          _lib.ptr(outs[1]), _lib.ptr(outs[2]), buf.data_ptr(), buf.numel(),
-                          _lib.stream_ptr(dev))
+                          _lib.ptr(ps), beam, n_req, _lib.ptr(ptr_dev), max_rows, row_vals.data_ptr(),
+                          row_idx.data_ptr(), _lib.ptr(outs[0]), _lib.ptr(outs[1]), _lib.ptr(outs[2]),
+                          buf.data_ptr(), buf.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "beam top-k")
     if beam > 0:
         return row_vals, row_idx, outs

@@ -42,6 +42,7 @@ def parse():
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat"])
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-graphs", action="store_true", help="e2e: launch every op eagerly (no HIP graphs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verbose", action="store_true")
     return ap.parse_args()

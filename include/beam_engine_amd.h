@@ -11,6 +11,8 @@
  * Reference interfaces replaced (paths relative to brian030128/beam_engine):
  *   be_kv_append      flashinfer.page.append_paged_kv_cache as called by
  *                     PageTable.write_blocks_vectorized (src/beam_engine/page_table.py:167-209)
+ *   be_rope_qkv_append apply_rotary_pos_emb + write_blocks_vectorized of a decode layer
+ *                     (src/beam_engine/models/modeling_llama.py:460-465, 506-514)
  *   be_page_copy      PageTable.copy_block's per-layer copy loop
  *                     (src/beam_engine/page_table.py:96-106), batched over forks and layers
  *   be_attn_plan      MultiLevelCascadeAttentionWrapper.plan
@@ -79,6 +81,24 @@ int be_page_copy(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int 
                  const int32_t* src, const int32_t* dst, const int32_t* len, int n,
                  int32_t* err_count, void* stream);
 
+/* be_rope_qkv_append: decode-step rotary embedding fused with the append.
+ * qkv is the fused projection [n, (Hq + 2 Hkv) * head_dim] (row stride in
+ * elements; q heads, then k heads, then v heads).  For every candidate i:
+ * q_out[i] ([Hq, head_dim] contiguous) = RoPE(q, positions[i]); RoPE(k) and v
+ * go to slot slot[i] of page page_idx[i] of kv_layer.  RoPE is the HF
+ * rotate_half form with cos/sin tables [max_position, head_dim] in the storage
+ * dtype, rounded like the eager tensor code:
+ * round(round(x*cos) + round(rotate_half(x)*sin)).  Replaces
+ * apply_rotary_pos_emb + write_blocks_vectorized of the decode layer
+ * (src/beam_engine/models/modeling_llama.py:460-465, 506-514;
+ * page_table.py:167-209).  Out-of-range positions / pages / slots are
+ * skipped and counted in *err_count (device int32, may be NULL). */
+int be_rope_qkv_append(const void* qkv, int64_t qkv_stride_n, int dtype, int n, int num_qo_heads,
+                       int num_kv_heads, int head_dim, const int64_t* positions,
+                       const void* cos_table, const void* sin_table, int max_position, void* q_out,
+                       void* kv_layer, int num_pages, int page_size, const int32_t* page_idx,
+                       const int32_t* slot, int32_t* err_count, void* stream);
+
 /* ------------------------------------------------------------------ attention
  * One level of a cascade (FlashInfer's per-level index arrays as built by
  * BeamState.get_cascade_input, src/beam_engine/beam_state.py:211-412): group
@@ -101,6 +121,16 @@ typedef struct be_level {
                                     workgroup then pays a device-scope release fence, an
                                     L2 writeback on gfx950, so this is off by default)    */
 
+/* Fixed-capacity plan layout (for HIP-graph capture): every region of the
+ * device plan sits at an offset that depends only on these capacities, the
+ * live counts sit in a device header, and be_attn_run launches capacity-sized
+ * grids whose surplus workgroups exit at once.  A plan that exceeds a capacity
+ * fails with BE_ERR_CAPACITY. */
+typedef struct be_plan_caps {
+  int32_t max_items, max_queries, max_pages, max_merge, max_merge_rows, max_zero;
+  int32_t tile_rows;       /* fixed rows per workgroup tile: 16, 32, 64 or 128 */
+} be_plan_caps;
+
 /* Filled by be_attn_plan; passed back to be_attn_run unchanged. */
 typedef struct be_attn_plan_info {
   int32_t num_items;       /* work items (grid.x of the attention kernel)      */
@@ -117,6 +147,9 @@ typedef struct be_attn_plan_info {
   int32_t fused_merge;     /* 1: the attention kernel merges (no second kernel) */
   int32_t num_zero;        /* queries with no keys at all: o = 0, lse = -inf   */
   int32_t off_zero_q, off_zero_ptr;
+  int32_t static_layout;   /* 1: fixed-capacity layout, counts in the device header */
+  int32_t grid_items, grid_merge, grid_zero;   /* launch sizes (= counts, or capacities) */
+  int32_t part_rows_cap;   /* partial rows the scratch is laid out for          */
   int64_t partial_bytes;   /* device scratch: partial o + lse + merge counters */
   int64_t counter_offset;  /* byte offset of the int32 merge counters in the scratch;
                               the caller zeroes counter_bytes there once after planning
@@ -132,11 +165,13 @@ typedef struct be_attn_plan_info {
  * KV chunks) and writes the device plan into host_plan[0..info->plan_ints).
  * The caller copies that prefix to device memory (stream-ordered before
  * be_attn_run) and provides info->partial_bytes of device scratch.
- * num_cus sizes the split-K chunking (pass the device's CU count). */
+ * num_cus sizes the split-K chunking (pass the device's CU count).  caps
+ * NULL gives a compact layout sized to this plan; non-NULL the fixed layout
+ * above (the fused merge is not available with it). */
 int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int num_qo_heads,
                  int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype,
-                 int flags, int num_cus, int32_t* host_plan, int64_t host_plan_capacity,
-                 be_attn_plan_info* info);
+                 int flags, int num_cus, const be_plan_caps* caps, int32_t* host_plan,
+                 int64_t host_plan_capacity, be_attn_plan_info* info);
 
 /* be_attn_run: o[i, h] = softmax(sm_scale * q[i, h] . K^T) V over query i's
  * groups on every level, merged by log-sum-exp; query head h reads KV head
@@ -168,17 +203,22 @@ int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, cons
  *   logp = round_dtype(fl32(fl32(x' - max) - fl32(ln sum exp(x' - max))))
  *          with the exponential sum accumulated in float64;
  *   per row the k best (logp desc, index asc) -> row_vals/row_idx [n_rows, k];
- *   when beam > 0: the beam best of the pool total = parent_scores[r] +
- *   (double)row_vals[r, j] by (total desc, r*k + j asc), emitted grouped by
- *   row ascending and, within a row, in selection order, into
- *   out_parent/out_token (int32) and out_score (double) [beam].
+ *   when beam > 0, for every request q < n_req (its rows are
+ *   [req_row_ptr[q], req_row_ptr[q+1]), a device int32 array; NULL with
+ *   n_req = 1 means all rows): the beam best of the request's pool
+ *   total = parent_scores[r] + (double)row_vals[r, j] by (total desc,
+ *   r*k + j asc), emitted grouped by row ascending and, within a row, in
+ *   selection order, into out_parent (global row) / out_token (int32) and
+ *   out_score (double) [n_req * beam].  max_req_rows bounds the rows of any
+ *   request (host-side pool capacity check).
  * All pointers are device pointers.  workspace must hold
  * be_beam_topk_workspace_bytes(n_rows, vocab, k) bytes. */
 int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k);
 int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride,
-                 float inv_temp, int k, const double* parent_scores, int beam,
-                 float* row_vals, int32_t* row_idx, int32_t* out_parent, int32_t* out_token,
-                 double* out_score, void* workspace, int64_t workspace_bytes, void* stream);
+                 float inv_temp, int k, const double* parent_scores, int beam, int n_req,
+                 const int32_t* req_row_ptr, int max_req_rows, float* row_vals, int32_t* row_idx,
+                 int32_t* out_parent, int32_t* out_token, double* out_score, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     assert L.be_version() >= 100
 
 
-def plan(levels, nq=None, hq=8, hkv=2, d=128, page=4, num_pages=64, dtype=2, flags=0, cus=256):
+def plan(levels, nq=None, hq=8, hkv=2, d=128, page=4, num_pages=64, dtype=2, flags=0, cus=256, caps=None):
     _lib, L = lib()
     keep = []
     arr = (_lib.BeLevel * len(levels))()
@@ -51,7 +51,8 @@ def plan(levels, nq=None, hq=8, hkv=2, d=128, page=4, num_pages=64, dtype=2, fla
     buf = np.zeros(1 << 20, dtype=np.int32)
     info = _lib.BeAttnPlanInfo()
     rc = L.be_attn_plan(arr, len(levels), nq, hq, hkv, d, page, num_pages, dtype, flags, cus,
-                        buf.ctypes.data, buf.size, ctypes.byref(info))
+                        ctypes.byref(caps) if caps is not None else None, buf.ctypes.data, buf.size,
+                        ctypes.byref(info))
     return rc, info, buf, _lib, L
 
 
@@ -158,3 +159,23 @@ def test_plan_lists_keyless_queries_for_zero_fill():
     assert buf[info.off_zero_q: info.off_zero_q + 2].tolist() == [1, 2]
     assert buf[info.off_zero_ptr: info.off_zero_ptr + 3].tolist() == [0, 0, 0]
     assert info.num_items == 1 and info.num_merge == 0
+
+
+def test_fixed_layout_offsets_do_not_depend_on_the_plan():
+    _lib, L = lib()
+    caps = _lib.BePlanCaps(64, 16, 256, 16, 128, 16, 32)
+    a = [([0, 8], [0, 4], [0, 1, 2, 3], [1]), ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1])]
+    b = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
+    rc1, i1, buf1, *_ = plan(a, nq=8, num_pages=19, caps=caps)
+    rc2, i2, buf2, *_ = plan(b, nq=2, num_pages=19, caps=caps)
+    assert rc1 == 0 and rc2 == 0
+    fields = ["plan_ints", "off_items", "off_qindex", "off_pages", "off_merge_q", "off_merge_ptr", "off_merge_rows",
+              "off_zero_q", "off_zero_ptr", "grid_items", "grid_merge", "grid_zero", "part_rows_cap",
+              "partial_bytes", "tile_rows"]
+    assert [getattr(i1, f) for f in fields] == [getattr(i2, f) for f in fields]
+    assert i1.static_layout == 1 and i1.grid_items == 64 and i1.tile_rows == 32
+    assert buf1[0] == i1.num_items and buf2[0] == i2.num_items and buf2[1] == i2.num_merge
+    # exceeding a capacity is a capacity error
+    tiny = _lib.BePlanCaps(1, 16, 256, 16, 128, 16, 32)
+    rc3, *_ = plan(a, nq=8, num_pages=19, caps=tiny)
+    assert rc3 == _lib.BE_ERR_CAPACITY

@@ -112,3 +112,42 @@ def test_tiny_llama_beam_search_matches_oracle(kind):
         gen.step()
     assert checks["attn"] == 10 * cfg.num_hidden_layers
     assert o_alloc.copies, "the run should have forked partial pages"
+
+
+def test_graph_replays_match_eager_steps():
+    """The segment-graph decode (HIP graphs replayed every step, eager attention,
+    eager selection and trie updates in between) gives the same logits and the
+    same beams as the fully eager decode, step after step."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    say("graph replays vs eager")
+    from beam_engine_amd import PageTable
+    from beam_engine_amd.generator import BatchedBeamSearch
+    from beam_engine_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(num_hidden_layers=3, hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
+                      head_dim=128, intermediate_size=512, vocab_size=700, max_position_embeddings=512)
+    runs = []
+    for graphs in (False, True):
+        model = LlamaDecoder(cfg, "cuda", torch.bfloat16, seed=11)
+        pt = PageTable(3, page_size=8, max_num_pages=256, head_num=2, head_dim=128, device="cuda",
+                       store_dtype=torch.bfloat16)
+        gen = BatchedBeamSearch(model, pt, 4, kernel_type="cascade", graphs=graphs)
+        logs = []
+        real = gen._select
+
+        def sel(logits, real=real, logs=logs):
+            logs.append(logits.clone())
+            real(logits)
+        gen._select = sel
+        gen.prefill([list(range(3, 23)), list(range(40, 60))])
+        runs.append((gen, logs))
+    (ge, le), (gg, lg) = runs
+    for step in range(8):
+        ge.step()
+        gg.step()
+        torch.cuda.synchronize()
+        assert torch.equal(le[step], lg[step]), f"step {step} logits differ"
+        assert [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in ge.state.candidates] == \
+            [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in gg.state.candidates]
+    assert gg._gd is not None and len(gg._gd.graphs) == cfg.num_hidden_layers + 1

@@ -119,3 +119,32 @@ def test_fork_trace_moves_page_contents():
         for src, dst, n in step["expect_copies"]:
             assert torch.equal(pt.kv_pool[:, dst, :, :n], before[:, src, :, :n])
         assert list(pt.free_pages) == step.get("expect_free_list", list(pt.free_pages))
+
+
+def test_rope_append_matches_eager_tensor_code():
+    """be_rope_qkv_append is bit-identical to the eager HF-style RoPE + append."""
+    say("rope append vs eager")
+    from beam_engine_amd import PageTable
+    from beam_engine_amd.llama import LlamaConfig, LlamaDecoder
+    cfg = LlamaConfig(num_hidden_layers=1, hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
+                      head_dim=128, intermediate_size=256, vocab_size=64, max_position_embeddings=2048)
+    m = LlamaDecoder(cfg, "cuda", torch.bfloat16, seed=1)
+    g = torch.Generator().manual_seed(5)
+    n = 37
+    qkv = (torch.randn((n, (8 + 4) * 128), generator=g) * 2).to(torch.bfloat16).cuda()
+    pos = torch.randint(0, 2048, (n,), generator=g).cuda()
+    pages = torch.randperm(64, generator=g)[:n].to(torch.int32).cuda()
+    slots = torch.randint(0, 16, (n,), generator=g, dtype=torch.int32).cuda()
+    a = PageTable(1, page_size=16, max_num_pages=64, head_num=2, head_dim=128, device="cuda",
+                  store_dtype=torch.bfloat16)
+    b = PageTable(1, page_size=16, max_num_pages=64, head_num=2, head_dim=128, device="cuda",
+                  store_dtype=torch.bfloat16)
+    q_fused = a.write_rope_qkv(0, qkv, 8, pos, m.cos, m.sin, pages, slots)
+    q = qkv[:, :1024].unflatten(-1, (8, 128))
+    k = qkv[:, 1024:1280].unflatten(-1, (2, 128))
+    v = qkv[:, 1280:].unflatten(-1, (2, 128))
+    q_ref = m._rope(q, pos)
+    b.write_blocks_vectorized(0, pages, m._rope(k, pos), v, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(q_fused, q_ref)
+    assert torch.equal(a.kv_pool, b.kv_pool)

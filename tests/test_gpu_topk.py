@@ -82,3 +82,23 @@ def test_prefill_single_row_and_small_vocab():
     assert rv[0, :16].tolist() == [s for _, s in sel]
     small = torch.randn((3, 7), generator=g)
     compare(small, [0.0, -1.0, -2.0], 3)
+
+
+def test_batched_requests_in_one_call():
+    say("topk batched requests")
+    from beam_engine_amd import beam_topk
+    g = torch.Generator().manual_seed(6)
+    rows = [16, 16, 5, 16]
+    logits = (torch.randn((sum(rows), 50000), generator=g) * 2).to(torch.bfloat16)
+    parents = (-torch.rand(sum(rows), generator=g, dtype=torch.float64) * 3)
+    _, _, (par, tok, sc) = beam_topk(logits.cuda(), 32, parents, 16, request_rows=rows)
+    torch.cuda.synchronize()
+    par, tok, sc = par.tolist(), tok.tolist(), sc.tolist()
+    b = 0
+    for q, r in enumerate(rows):
+        x = logits[b:b + r].float().numpy()
+        _, _, _, _, flat = ot.beam_step(x, parents[b:b + r].tolist(), 16, "bfloat16")
+        got = [(p - b, t, s) for p, t, s in zip(par[q * 16:(q + 1) * 16], tok[q * 16:(q + 1) * 16],
+                                                 sc[q * 16:(q + 1) * 16]) if p >= 0]
+        assert got == flat, f"request {q}"
+        b += r
