@@ -84,7 +84,7 @@ class PlanStats:
         self.num_items = int(info.num_items)
         self.num_part_rows = int(info.num_part_rows)
         self.num_merge = int(info.num_merge)
-        self.kernel = "mfma" if info.kernel == 1 else "valu"
+        self.kernel = {0: "valu", 1: "tile", 2: "stream"}[int(info.kernel)]
         self.chunk_tokens = int(info.chunk_tokens)
 
     @property
@@ -110,6 +110,8 @@ class _PagedPlanner:
         self._dtype: Optional[torch.dtype] = None
         self._force_valu = False
         self._fused_merge = False
+        self._tile_kernel = False     # force the per-(item, head) tile kernel over the streaming kernel
+        self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
 
     # ---------------------------------------------------------------- plan
@@ -146,14 +148,15 @@ class _PagedPlanner:
             q_data_type = getattr(torch, q_data_type)
         dt = _lib.dtype_code(q_data_type)
         flags = (_lib.BE_PLAN_FORCE_VALU if self._force_valu else 0) | \
-            (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0)
+            (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0) | \
+            (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()
         while True:
             buf = staging.acquire(cap)
             rc = lib.be_attn_plan(levels, len(qo), nq, num_qo_heads, num_kv_heads, head_dim, page_size,
-                                  max(max_page + 1, 1), dt, flags, _num_cus(self._ws.device),
+                                  max(max_page + 1, 1), dt, flags, self._num_cus or _num_cus(self._ws.device),
                                   ctypes.byref(self._caps) if self._caps is not None else None,
                                   buf.data_ptr(), buf.numel(), ctypes.byref(info))
             if rc == _lib.BE_ERR_CAPACITY:

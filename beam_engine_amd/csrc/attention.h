@@ -1,0 +1,73 @@
+// Declarations shared by the decode attention sources (gfx950): the planner's
+// group list, MFMA operand helpers, and the persistent streaming kernel's plan
+// and run entry points (attn_stream.hip).
+#pragma once
+
+#include <vector>
+
+#include "common.h"
+
+namespace be {
+
+constexpr int kPlanHeader = 16;    // int32 words of live counts at the start of a plan
+constexpr int kHdrItems = 0, kHdrMerge = 1, kHdrZero = 2, kHdrRows = 3;
+
+// One paged group of one cascade level after validation: queries [q0, q1)
+// attend kv_len tokens whose pages start at page_base of the plan's
+// concatenated page list.
+struct Group {
+  int level, q0, q1, page_base, kv_len;
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// S^T tile: v_mfma_f32_16x16x32 on 16-bit operands.
+template <typename T> __device__ __forceinline__ v4f mfma_qk(v8s a, v8s b, v4f c);
+template <> __device__ __forceinline__ v4f mfma_qk<bf16_t>(v8s a, v8s b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ v4f mfma_qk<f16_t>(v8s a, v8s b, v4f c) {
+  typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+// O^T += V^T P^T: v_mfma_f32_16x16x16 on 16-bit operands.
+template <typename T> __device__ __forceinline__ v4f mfma_pv(v4s a, v4s b, v4f c);
+template <> __device__ __forceinline__ v4f mfma_pv<bf16_t>(v4s a, v4s b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ v4f mfma_pv<f16_t>(v4s a, v4s b, v4f c) {
+  typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, a), __builtin_bit_cast(v4h, b), c, 0, 0, 0);
+}
+
+template <typename T> __device__ __forceinline__ uint16_t pack16(float x);
+template <> __device__ __forceinline__ uint16_t pack16<bf16_t>(float x) { return f32_to_bf16_bits(x); }
+template <> __device__ __forceinline__ uint16_t pack16<f16_t>(float x) {
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// ---------------------------------------------------------------- streaming kernel
+// True when the streaming kernel serves this shape (16-bit storage, head_dim
+// 128, GQA group <= 64).
+bool stream_eligible(int dtype, int head_dim, int group, int flags);
+
+// Writes the streaming plan for `groups` (validated by attn_plan, pages
+// concatenated level by level into total_pages entries) into out[0..cap) and
+// fills the layout fields of info.  Returns BE_ERR_UNSUPPORTED (without
+// setting an error) when a workgroup would need more segments than its LDS
+// table holds; the caller then plans for the tile kernel instead.
+int stream_plan(const std::vector<Group>& groups, const be_level* levels, int num_levels, int64_t total_pages,
+                int num_queries, int hq, int hkv, int d, int page_size, int num_pages, int dtype, int num_cus,
+                const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info);
+
+// Launches the streaming attention kernel (phases & BE_RUN_ATTENTION) and the
+// slot merge kernel (phases & BE_RUN_MERGE) of a kernel == 2 plan.
+int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partials, const void* q, int64_t q_sn,
+               int64_t q_sh, const void* kv, void* out, int64_t o_sn, int64_t o_sh, float* lse, float sm_scale,
+               int phases, hipStream_t st);
+
+}  // namespace be

@@ -16,7 +16,7 @@
 #include <algorithm>
 #include <vector>
 
-#include "common.h"
+#include "attention.h"
 
 namespace be {
 
@@ -39,8 +39,6 @@ struct WorkItem {
 };
 static_assert(sizeof(WorkItem) == 32, "WorkItem is 8 int32 words");
 
-constexpr int kPlanHeader = 16;    // int32 words of live counts at the start of a plan
-constexpr int kHdrItems = 0, kHdrMerge = 1, kHdrZero = 2, kHdrRows = 3;
 constexpr int kMaxRows = 32;       // rows (queries x GQA group) per VALU workgroup
 constexpr int kMaxTileRows = 128;  // rows per MFMA workgroup (8 row tiles of 16)
 
@@ -176,33 +174,6 @@ __device__ void fused_merge_epilogue(const AttnArgs& a, const WorkItem& it, int 
 // S^T tile gives lane (lg, lc) tokens 4*lg..4*lg+3 of row lc, which is exactly
 // the B operand (P^T) of v_mfma_f32_16x16x16 for O^T = V^T P^T, whose A
 // operand is 4 consecutive tokens of one head_dim row of the transposed V.
-typedef short v8s __attribute__((ext_vector_type(8)));
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-template <typename T> __device__ __forceinline__ v4f mfma_qk(v8s a, v8s b, v4f c);
-template <> __device__ __forceinline__ v4f mfma_qk<bf16_t>(v8s a, v8s b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-template <> __device__ __forceinline__ v4f mfma_qk<f16_t>(v8s a, v8s b, v4f c) {
-  typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
-}
-template <typename T> __device__ __forceinline__ v4f mfma_pv(v4s a, v4s b, v4f c);
-template <> __device__ __forceinline__ v4f mfma_pv<bf16_t>(v4s a, v4s b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-template <> __device__ __forceinline__ v4f mfma_pv<f16_t>(v4s a, v4s b, v4f c) {
-  typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, a), __builtin_bit_cast(v4h, b), c, 0, 0, 0);
-}
-
-template <typename T> __device__ __forceinline__ uint16_t pack16(float x);
-template <> __device__ __forceinline__ uint16_t pack16<bf16_t>(float x) { return f32_to_bf16_bits(x); }
-template <> __device__ __forceinline__ uint16_t pack16<f16_t>(float x) {
-  return __builtin_bit_cast(uint16_t, (_Float16)x);
-}
-
 constexpr int kTile = 64;              // tokens per LDS tile
 constexpr int kMaxPagesLds = 1024;     // page ids of one item staged in LDS
 
@@ -668,16 +639,6 @@ __global__ __launch_bounds__(256) void merge2_kernel(const float* oa, const floa
 }
 
 // ================================================================== host: planner
-namespace {
-
-struct Group {
-  int level, q0, q1, page_base, kv_len;
-};
-
-int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
-}  // namespace
-
 int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, int hkv, int d,
               int page_size, int num_pages, int dtype, int flags, int num_cus, const be_plan_caps* caps,
               int32_t* out, int64_t cap, be_attn_plan_info* info) {
@@ -721,6 +682,26 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
     total_pages += np;
   }
 
+  // ---- algorithmic bytes: distinct (page, head) valid tokens, plus Q and O
+  std::vector<int> valid(num_pages, 0);
+  for (int lv = 0; lv < num_levels; ++lv) {
+    const be_level& L = levels[lv];
+    for (int j = 0; j < L.num_groups; ++j) {
+      const int b = L.kv_indptr[j], e = L.kv_indptr[j + 1];
+      for (int i = b; i < e; ++i) {
+        const int v = (i + 1 < e) ? page_size : L.last_page_len[j];
+        int& slot = valid[L.kv_indices[i]];
+        slot = std::max(slot, v);
+      }
+    }
+  }
+  int64_t valid_tokens = 0;
+  for (int v : valid) valid_tokens += v;
+  const int64_t es = (int64_t)dtype_size(dtype);
+  double flops = 0.0;
+  for (const Group& gr : groups)
+    if (gr.kv_len > 0 && gr.q1 > gr.q0) flops += 4.0 * d * hq * (double)gr.kv_len * (gr.q1 - gr.q0);
+
   bool mfma = (dtype != BE_F32) && !(flags & BE_PLAN_FORCE_VALU);
   if (!mfma && g > kMaxRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d (VALU kernel)", g, kMaxRows);
   if (mfma && d == 256 && g > 64) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds 64 at head_dim 256", g);
@@ -735,6 +716,25 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
                    caps->max_merge >= 0 && caps->max_merge_rows >= 0 && caps->max_zero >= 0,
                "bad plan capacities (max_queries %d < %d queries?)", caps->max_queries, num_queries);
     if (mfma) rows_cap = std::min(rows_cap, tr);
+  }
+  if (stream_eligible(dtype, d, g, flags) && (!caps || caps->tile_rows == 64)) {
+    memset(info, 0, sizeof(*info));
+    const int rc = stream_plan(groups, levels, num_levels, total_pages, num_queries, hq, hkv, d, page_size,
+                               num_pages, dtype, num_cus, caps, out, cap, info);
+    if (rc == BE_OK) {
+      info->num_qo_heads = hq;
+      info->num_kv_heads = hkv;
+      info->head_dim = d;
+      info->page_size = page_size;
+      info->num_pages = num_pages;
+      info->dtype = dtype;
+      info->kv_bytes = valid_tokens * hkv * d * es * 2;
+      info->qo_bytes = (int64_t)num_queries * hq * d * es * 2;
+      info->flops = flops;
+      return BE_OK;
+    }
+    if (rc != BE_ERR_UNSUPPORTED) return rc;
+    // a workgroup would need more segments than its table holds: tile kernel
   }
   const int q_tile = std::max(1, rows_cap / g);
 
@@ -770,10 +770,8 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   std::vector<WorkItem> items;
   std::vector<std::vector<int>> rows_of(num_queries);
   int rows = 0, max_r = 0;
-  double flops = 0.0;
   for (const Group& gr : groups) {
     if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
-    flops += 4.0 * d * hq * (double)gr.kv_len * (gr.q1 - gr.q0);
     const int64_t gchunk = group_chunk(gr);
     for (int t0 = 0; t0 < gr.kv_len; t0 += (int)gchunk) {
       const int tc = (int)std::min<int64_t>(gchunk, gr.kv_len - t0);
@@ -792,27 +790,6 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
       }
     }
   }
-
-  // ---- algorithmic bytes: distinct (page, head) valid tokens, plus Q and O
-  std::vector<int> valid(num_pages, 0);
-  {
-    int64_t pbase = 0;
-    for (int lv = 0; lv < num_levels; ++lv) {
-      const be_level& L = levels[lv];
-      for (int j = 0; j < L.num_groups; ++j) {
-        const int b = L.kv_indptr[j], e = L.kv_indptr[j + 1];
-        for (int i = b; i < e; ++i) {
-          const int v = (i + 1 < e) ? page_size : L.last_page_len[j];
-          int& slot = valid[L.kv_indices[i]];
-          slot = std::max(slot, v);
-        }
-      }
-      pbase += L.num_groups ? L.kv_indptr[L.num_groups] : 0;
-    }
-  }
-  int64_t valid_tokens = 0;
-  for (int v : valid) valid_tokens += v;
-  const int64_t es = (int64_t)dtype_size(dtype);
 
   // ---- merge list (queries with >= 2 partial rows) and zero list (no keys)
   std::vector<int> merge_q, merge_ptr{0}, merge_rows, zero_q;
@@ -980,6 +957,8 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
   BE_REQUIRE(info->part_rows_cap == 0 || partials, "plan needs %lld bytes of partial scratch", (long long)info->partial_bytes);
   BE_REQUIRE(info->num_qo_heads % info->num_kv_heads == 0, "corrupt plan info");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (info->kernel == 2)
+    return stream_run(info, plan, partials, q, q_sn, q_sh, kv, out, o_sn, o_sh, lse, sm_scale, phases, st);
   const int64_t rows = info->part_rows_cap;
   AttnArgs a;
   a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;

@@ -1,0 +1,840 @@
+// Persistent streaming decode attention for gfx950 (bf16 / fp16 KV, head_dim 128).
+//
+// The same quantities as the tile kernel in attention.hip — softmax(s q K^T) V
+// of every query over each of its cascade groups, merged by log-sum-exp — as
+// FlashInfer's MultiLevelCascadeAttentionWrapper computes them for the
+// reference (models/modeling_llama.py:321-367, 732-755), but scheduled for an
+// HBM-bound decode step on MI355X:
+//
+//  * One workgroup (4 waves) per CU.  The planner cuts the work — (query tile
+//    of <= 64 rows) x (KV head) x (64-token tiles) — into one contiguous run per
+//    workgroup with equal bytes, splitting work items at tile boundaries where
+//    a run ends.  A piece of a work item inside one run is a segment.
+//  * Every asynchronous transfer is a direct global->LDS load
+//    (global_load_lds_dwordx4 / _dword): K and V tiles, the Q rows of a
+//    segment and the page ids of a tile.  Nothing in the loop waits on a
+//    VGPR load, so the loads of the next two tiles stay in flight across
+//    segment boundaries; waits are explicit vmcnt counts (vmcnt retires in
+//    issue order) followed by a bare s_barrier.
+//  * Pipeline: 3 stages of {K tile 16 KB, V tile 16 KB, Q slot 16 KB}; page ids
+//    run four tiles ahead in a 4-slot LDS ring.  In iteration n: wait for tile
+//    n, barrier, issue K/V/Q of tile n + 2 and page ids of tile n + 4, compute n.
+//  * K, V and Q rows are 256-byte rows whose 16-byte chunks sit XOR-swizzled by
+//    row (the swizzle is applied by choosing each lane's global address, since
+//    a direct load writes lane l's 16 bytes at LDS base + 16 l).
+//  * S^T = K Q^T with v_mfma_f32_16x16x32 (A = K rows, B = Q from registers);
+//    the C layout of a 16-token S^T tile is the B operand (P^T) of
+//    v_mfma_f32_16x16x16 for O^T = V^T P^T.  Its A operand (4 consecutive
+//    tokens of one head_dim column) is read from the row-major V tile with
+//    ds_read_b64_tr_b16: in each 16-lane group, lane r supplies the address of
+//    V[t0 + r/4][d0 + 4 (r%4) .. +3] and receives V[t0 + j][d0 + r], j = 0..3.
+//  * Wave w owns rows 16w..16w+15 of a segment (query x GQA head); waves
+//    without rows only load.  Online softmax in the log2 domain, fp32
+//    accumulation, natural-log lse at the boundary.
+//  * A (query, KV head) covered by one segment is written as the final
+//    output; otherwise each segment writes a partial (o, lse) slot and a
+//    merge record combines the slots of the (query, KV head).
+
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "attention.h"
+
+namespace be {
+
+namespace stream {
+
+constexpr int kD = 128;                       // head_dim served
+constexpr int kTok = 64;                      // tokens per tile
+constexpr int kStages = 3;
+constexpr int kPageSlots = 4;                 // page ids run kPageSlots tiles ahead of compute
+constexpr int kSegRows = 64;                  // rows per segment: 4 waves x 16
+constexpr int kMaxSegs = 224;                 // segments per workgroup (LDS table)
+constexpr int kKvBytes = kTok * kD * 2;       // one K (or V) tile: 16 KB
+constexpr int kQBytes = kSegRows * kD * 2;    // one Q slot: 16 KB
+constexpr int kStageBytes = 2 * kKvBytes + kQBytes;
+constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
+constexpr int kThreads = 64 * kWaves;
+constexpr int kLoadsPerTile = 4;              // direct loads per wave per tile (2 K + 2 V row blocks)
+constexpr int kEpiStores = 4;                 // lower bound of store instructions of an epilogue
+constexpr int kSegCost = 1;                   // planner cost of a segment start, in quarter tiles
+
+struct StreamSeg {
+  int32_t q_begin;     // first query
+  int32_t q_count;     // queries; rows = q_count * group <= 64
+  int32_t page_begin;  // first entry of the plan's page list for the group
+  int32_t tok_begin;   // first group token of the segment (a multiple of 64)
+  int32_t tok_count;   // tokens, > 0
+  int32_t head;        // KV head
+  int32_t out_slot;    // first partial slot (one per query), or -1: final output
+  int32_t n_tiles;     // ceil(tok_count / 64)
+};
+static_assert(sizeof(StreamSeg) == 32, "segment record is 8 int32 words");
+
+struct StreamArgs {
+  const void* q;
+  int64_t q_sn, q_sh;
+  const void* kv;
+  void* out;
+  int64_t o_sn, o_sh;
+  float* out_lse;
+  float* part_o;      // [slots, g, D]
+  float* part_lse;    // [slots, g]
+  const int4* wg;     // per workgroup: first segment, segments, tiles
+  const StreamSeg* segs;
+  const int32_t* pages;
+  int page_size, page_shift, hkv, hq, g;
+  float scale_log2;
+};
+
+struct SlotMergeArgs {
+  const float* part_o;
+  const float* part_lse;
+  const int4* recs;          // query, KV head, first entry of rec_slots, slot count
+  const int32_t* rec_slots;
+  const int32_t* live;       // live record count (device), or null
+  void* out;
+  int64_t o_sn, o_sh;
+  float* out_lse;
+  int n_recs, g, hq;
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(3))) v4s* lds_v4s_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)p;
+}
+
+// Direct global->LDS loads: lane l's bytes land at LDS byte address m0 + size * l
+// (lds must be wave-uniform).  They are issued from inline asm so that the
+// compiler's wait insertion does not treat every later LDS read as dependent
+// on them (it would wait for all outstanding loads); completion is tracked by
+// the explicit vmcnt waits.  Wait states: an M0 write needs one before an
+// LDS-DMA instruction reads it; an SGPR written by a VALU instruction
+// (readfirstlane) needs five before a vector memory instruction reads it.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+// SGPR base (wave-uniform) + 32-bit unsigned VGPR byte offset
+__device__ __forceinline__ void dma16_sv(uint64_t base, uint32_t voff, uint32_t lds) {
+  // readfirstlane returns int: zero-extend each half through uint32_t
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  const uint64_t sbase = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14).
+// n is the number of newer vector memory operations that may stay
+// outstanding; vmcnt retires operations in issue order.  Dispatched by a
+// binary tree of scalar branches (n is wave-uniform).
+#define BE_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+template <int LO, int HI>
+__device__ __forceinline__ void wait_tree(int n) {
+  if constexpr (LO == HI) {
+    __builtin_amdgcn_s_waitcnt(BE_VMCNT(LO));
+  } else {
+    constexpr int MID = (LO + HI) / 2;
+    if (n <= MID) wait_tree<LO, MID>(n);
+    else wait_tree<MID + 1, HI>(n);
+  }
+}
+__device__ __forceinline__ void wait_vmcnt(int n) { wait_tree<0, 31>(n < 31 ? n : 31); }
+
+__device__ __forceinline__ void lds_fence() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Two floats -> two 16-bit values (round to nearest even) in one word.
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, bf2));
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
+}
+template <typename T> __device__ __forceinline__ v4s pack4(float a, float b, float c, float d) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(v4s, (u2){pack2<T>(a, b), pack2<T>(c, d)});
+}
+
+// A segment record held in wave-uniform registers.
+struct SegReg {
+  int q_begin, q_count, page_begin, tok_begin, tok_count, head, out_slot, n_tiles;
+};
+__device__ __forceinline__ SegReg seg_reg(const StreamSeg& x) {
+  return SegReg{rfl(x.q_begin), rfl(x.q_count), rfl(x.page_begin), rfl(x.tok_begin),
+                rfl(x.tok_count), rfl(x.head),   rfl(x.out_slot),   rfl(x.n_tiles)};
+}
+
+// One wave's share of a 64-token tile: rows 16 rt + (0..15) against NSUB
+// 16-token sub-tiles starting at kt / vt, for NMT head_dim tiles (voff).
+// Online softmax state (m_run, l_run over this wave's tokens, o_acc) is
+// updated in place; the rescale is skipped when no row's max rose.  dma(j),
+// j = 0..3, issues this wave's share of the loads of a later tile; the calls
+// are spread over the computation so that the loads of all waves do not queue
+// on the address unit at the same moment.
+template <typename T, int NSUB, int NMT, typename Dma>
+__device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsigned char* vt, const v8s (&qf)[4],
+                                             const uint32_t (&koff)[4], const uint32_t (&voff)[NMT], int tok_base,
+                                             int valid, int lg, float scale, float& m_run, float& l_run,
+                                             v4f (&o_acc)[8], Dma&& dma) {
+  float x[NSUB][4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k) {
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      acc = mfma_qk<T>(*reinterpret_cast<const v8s*>(kt + k * 4096 + koff[ks]), qf[ks], acc);
+    if (k == 0) dma(0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[k][r] = acc[r] * scale;
+      if (valid < kTok && tok_base + k * 16 + 4 * lg + r >= valid) x[k][r] = -INFINITY;
+      mx = fmaxf(mx, x[k][r]);
+    }
+  }
+  dma(1);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m_run, mx);
+  const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
+  if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
+    const float alpha = __builtin_amdgcn_exp2f(m_run - msafe);
+    l_run *= alpha;
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) o_acc[mt] *= alpha;
+  }
+  m_run = m_new;
+  v4s pf[NSUB];
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k) {
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = __builtin_amdgcn_exp2f(x[k][r] - msafe);
+      l_run += p[r];
+    }
+    pf[k] = pack4<T>(p[0], p[1], p[2], p[3]);
+  }
+  dma(2);
+  // O^T tiles: lane (lg, lc) supplies V[16 sub + 4 lg + lc/4][16 mt + 4 (lc%4) .. +3]
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt) {
+    v4f o = o_acc[mt];
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k)
+      o = mfma_pv<T>(__builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + k * 4096 + voff[mt])), pf[k], o);
+    o_acc[mt] = o;
+    if (mt == NMT / 2 - 1) dma(3);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char st_lds[kStages * kStageBytes];
+  __shared__ StreamSeg seg_lds[kMaxSegs];
+  __shared__ __attribute__((aligned(16))) int pg_lds[kPageSlots][64];
+
+  const int tid = threadIdx.x;
+  const int w = rfl(tid >> 6);                        // wave index (uniform)
+  const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
+  const int4 wi = a.wg[blockIdx.x];
+  const int n_segs = rfl(wi.y), n_tiles = rfl(wi.z);
+  if (n_tiles <= 0) return;
+  {
+    const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
+    int* dst = reinterpret_cast<int*>(seg_lds);
+    for (int i = tid; i < n_segs * 8; i += kThreads) dst[i] = src[i];
+  }
+  __syncthreads();
+
+  const int ps = a.page_size, g = a.g, hkv = a.hkv;
+  const int pshift = a.page_shift;
+  auto page_of = [&](int tok) { return pshift >= 0 ? (tok >> pshift) : (tok / ps); };
+  const T* kv = reinterpret_cast<const T*>(a.kv);
+  const int64_t plane = (int64_t)ps * hkv * kD;      // K plane -> V plane of a page (elements)
+  const uint32_t st0 = lds_addr(st_lds);
+  const bool fast_pages = (ps & 15) == 0;            // a wave's 8 rows of a full tile share a page
+  const float scale = a.scale_log2;
+
+  // per-lane LDS offsets (bytes) of the MFMA operand reads, within a 16-token
+  // sub-tile: K / Q rows, and V^T columns of all 8 head_dim tiles and of this
+  // wave's half (waves 4..7 take the upper half where head_dim is split)
+  uint32_t koff[4], voff8[8], voff4[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = lc * 256 + ((((ks << 2) | lg) ^ lc) << 4);
+  {
+    const int tl = 4 * lg + (lc >> 2), b1 = (lc >> 1) & 1, b0 = lc & 1;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) voff8[mt] = tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) voff4[mt] = voff8[4 * (w >> 2) + mt];
+  }
+  // this wave loads rows 8w..8w+7 of every tile (two 1 KB loads of 4 rows for
+  // K and for V); per-lane byte offsets inside the page for the fast path
+  uint32_t doff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 4 * i + lg;
+    doff[i] = (uint32_t)(((int64_t)r * hkv * kD + ((lc ^ (8 * (w & 1) + r)) << 3)) * 2);
+  }
+
+  // cursors: segment index, tile of the segment and the segment's record, for
+  // the page-id loads, the K/V/Q loads and the compute
+  int p_s = 0, p_t = 0, l_s = 0, l_t = 0, c_s = 0, c_t = 0;
+  SegReg p_sg = seg_reg(seg_lds[0]), l_sg = p_sg, c_sg = p_sg;
+  auto advance = [&](int& si, int& ti, SegReg& sg) {
+    if (++ti == sg.n_tiles) {
+      ti = 0;
+      if (++si < n_segs) sg = seg_reg(seg_lds[si]);
+    }
+  };
+
+  // page ids of tile m (page cursor) -> pg_lds[m % kPageSlots][0..]; wave 0
+  // loads them.  Returns this wave's number of loads.
+  auto issue_pages = [&](int m) -> int {
+    int ops = 0;
+    if (w == 0) {
+      const int tok0 = p_sg.tok_begin + p_t * kTok;
+      const int valid = min(kTok, p_sg.tok_count - p_t * kTok);
+      const int first = page_of(tok0);
+      const int span = page_of(tok0 + valid - 1) - first;
+      const int idx = p_sg.page_begin + first + min(lane, span);
+      dma4(a.pages + idx, lds_addr(&pg_lds[m & (kPageSlots - 1)][0]));
+      ops = 1;
+    }
+    advance(p_s, p_t, p_sg);
+    return ops;
+  };
+
+  // Loads of tile m (load cursor) into stage st: the Q rows now when the tile
+  // starts a segment; the K/V rows are prepared here and issued by dma(j).
+  bool kv_pending = false, kv_fast = false;
+  uint64_t kv_kbase = 0, kv_vbase = 0;
+  const T* kv_src[2] = {nullptr, nullptr};
+  uint32_t kv_lds = 0;
+  auto prep_tile = [&](int m, int st) -> int {
+    const SegReg& sg = l_sg;
+    const uint32_t stage = st0 + (uint32_t)(st * kStageBytes);
+    const int tok0 = sg.tok_begin + l_t * kTok;
+    const int valid = min(kTok, sg.tok_count - l_t * kTok);
+    const int first = page_of(tok0);
+    const int* pg = pg_lds[m & (kPageSlots - 1)];
+    kv_pending = true;
+    kv_lds = stage + (2 * w) * 1024;
+    kv_fast = fast_pages && valid == kTok;
+    if (kv_fast) {
+      // rows 8w..8w+7 lie in one page: SGPR page base + per-lane row offsets
+      const int t8 = tok0 + 8 * w;
+      const int pi = page_of(t8);
+      const int page = rfl(pg[pi - first]);
+      const int s0 = t8 - pi * ps;
+      kv_kbase = reinterpret_cast<uint64_t>(kv) +
+                 (uint64_t)(((((int64_t)page * 2) * ps + s0) * hkv + sg.head) * kD * 2);
+      kv_vbase = kv_kbase + (uint64_t)(plane * 2);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = 8 * w + 4 * i + lg;
+        const int tok = tok0 + (row < valid ? row : 0);  // rows past the end re-read a valid token
+        const int pi = page_of(tok);
+        const int page = pg[pi - first];
+        kv_src[i] = kv + ((((int64_t)page * 2) * ps + (tok - pi * ps)) * hkv + sg.head) * kD +
+                    ((lc ^ (row & 15)) << 3);
+      }
+    }
+    int ops = kLoadsPerTile;
+    if (l_t == 0) {
+      const int R = sg.q_count * g;
+      const int nq = (R + 3) >> 2;                    // 1 KB loads of 4 rows
+      for (int k = w; k < nq; k += kWaves) {
+        const int r = 4 * k + lg;
+        const int rc = min(r, R - 1);
+        const int j = rc / g, hh = rc - j * g;
+        const T* src = reinterpret_cast<const T*>(a.q) + (int64_t)(sg.q_begin + j) * a.q_sn +
+                       (int64_t)(sg.head * g + hh) * a.q_sh + ((lc ^ (r & 15)) << 3);
+        dma16(src, stage + 2 * kKvBytes + k * 1024);
+        ++ops;
+      }
+    }
+    advance(l_s, l_t, l_sg);
+    return ops;
+  };
+  // load j of the prepared tile: K rows 0..3 (j = 0), V rows 0..3, K rows 4..7, V rows 4..7
+  auto dma = [&](int j) {
+    if (!kv_pending) return;
+    const int i = j >> 1, v = j & 1;
+    const uint32_t dst = kv_lds + i * 1024 + v * kKvBytes;
+    if (kv_fast) dma16_sv(v ? kv_vbase : kv_kbase, doff[i], dst);
+    else dma16(kv_src[i] + (v ? plane : 0), dst);
+  };
+  auto dma_all = [&]() {
+    dma(0);
+    dma(1);
+    dma(2);
+    dma(3);
+  };
+
+  // ---- prologue.  Iteration i issues the loads of tile i + 2 and the page ids
+  // of tile i + 4, then computes tile i (its epilogue stores come last).
+  // Waiting until only the previous iteration's operations are outstanding
+  // therefore completes everything issued two iterations back: tile i's
+  // K/V/Q and the page ids of tile i + 2.
+  issue_pages(0);
+  if (n_tiles > 1) issue_pages(1);
+  wait_vmcnt(0);
+  __syncthreads();
+  prep_tile(0, 0);
+  dma_all();
+  if (n_tiles > 2) issue_pages(2);
+  int ops_prev = 0;                  // operations issued by the previous iteration
+  if (n_tiles > 1) {
+    ops_prev = prep_tile(1, 1);
+    dma_all();
+    if (n_tiles > 3) ops_prev += issue_pages(3);
+  }
+  kv_pending = false;
+
+  float m_run = -INFINITY, l_run = 0.f;
+  v4f o_acc[8];
+  v8s qf[4];
+  int st_c = 0, st_l = 2;            // stages of the computed and the next loaded tile
+
+  for (int n = 0; n < n_tiles; ++n) {
+    wait_vmcnt(rfl(ops_prev));
+    lds_fence();
+    int ops = 0;
+    if (n + 2 < n_tiles) {
+      ops += prep_tile(n + 2, st_l);
+      dma_all();
+    }
+    kv_pending = false;
+    if (n + kPageSlots < n_tiles) ops += issue_pages(n + kPageSlots);
+    st_l = st_l == kStages - 1 ? 0 : st_l + 1;
+
+    // ---- compute tile n.  Wave roles by the segment's row tiles (NT):
+    //   NT >= 3: row tile w & 3, token half w >> 2, all head_dim;
+    //   NT == 2: row tile w & 1, token half (w >> 1) & 1, head_dim half w >> 2;
+    //   NT == 1: token quarter w & 3, head_dim half w >> 2.
+    // The ts == 0 wave of each (row tile, head_dim part) collects the others.
+    const SegReg& sg = c_sg;
+    const int R = sg.q_count * g;
+    const int NT = (R + 15) >> 4;
+    const int rt = NT >= 3 ? (w & 3) : NT == 2 ? (w & 1) : 0;
+    const int ts = NT >= 3 ? (w >> 2) : NT == 2 ? ((w >> 1) & 1) : (w & 3);
+    const int nsub = NT == 1 ? 1 : 2;
+    const int sub0 = ts * nsub;
+    const bool act = 16 * rt < R;
+    const bool last = c_t == sg.n_tiles - 1;
+    unsigned char* stage = st_lds + st_c * kStageBytes;
+    if (c_t == 0) {
+      m_run = -INFINITY;
+      l_run = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (act) {
+        const unsigned char* qs = stage + 2 * kKvBytes + rt * 4096;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const v8s*>(qs + koff[ks]);
+      }
+    }
+    if (act) {
+      const int valid = min(kTok, sg.tok_count - c_t * kTok);
+      const unsigned char* kt = stage + sub0 * 4096;
+      const unsigned char* vt = stage + kKvBytes + sub0 * 4096;
+      if (NT >= 3)
+        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc, dma);
+      else if (NT == 2)
+        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc, dma);
+      else
+        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc, dma);
+    } else {
+      dma_all();
+    }
+    kv_pending = false;
+
+    if (last) {
+      float l = l_run;
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+      const int nmt = NT >= 3 ? 8 : 4;
+      const int mt0 = NT >= 3 ? 0 : 4 * (w >> 2);
+      // token-split waves hand their state to the ts == 0 wave of their (row
+      // tile, head_dim part) through this stage's LDS (no loads target it
+      // until the next iteration's barrier)
+      const int kslot = nmt * 1024 + 512;
+      lds_fence();
+      if (ts > 0 && act) {
+        unsigned char* slot = stage + (NT >= 3 ? w - 4 : w) * kslot;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+          if (mt < nmt) *reinterpret_cast<v4f*>(slot + (mt * 64 + lane) * 16) = o_acc[mt];
+        reinterpret_cast<float*>(slot + nmt * 1024)[lane] = m_run;
+        reinterpret_cast<float*>(slot + nmt * 1024 + 256)[lane] = l;
+      }
+      lds_fence();
+      if (ts == 0 && act) {
+        const int np = NT == 1 ? 4 : 2;                  // waves sharing the (row tile, head_dim part)
+        for (int p = 1; p < np; ++p) {
+          const int pw = NT >= 3 ? w + 4 : NT == 2 ? w + 2 : w + p;   // partner wave
+          const unsigned char* slot = stage + (NT >= 3 ? pw - 4 : pw) * kslot;
+          const float mb = reinterpret_cast<const float*>(slot + nmt * 1024)[lane];
+          const float lb = reinterpret_cast<const float*>(slot + nmt * 1024 + 256)[lane];
+          const float M = fmaxf(m_run, mb);
+          const float ca = (M == -INFINITY) ? 0.f : exp2f(m_run - M);
+          const float cb = (M == -INFINITY) ? 0.f : exp2f(mb - M);
+          l = l * ca + lb * cb;
+          m_run = M;
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt)
+            if (mt < nmt)
+              o_acc[mt] = o_acc[mt] * ca + *reinterpret_cast<const v4f*>(slot + (mt * 64 + lane) * 16) * cb;
+        }
+        // lane holds O^T[d = 16 (mt0 + mt) + 4 lg + i][row = 16 rt + lc]
+        const int row = 16 * rt + lc;
+        if (row < R) {
+          const int j = row / g, hh = row - j * g, head = sg.head * g + hh;
+          const int qi = sg.q_begin + j;
+          const float inv = (l > 0.f) ? 1.f / l : 0.f;
+          const float lse = (l > 0.f) ? (m_run + log2f(l)) * 0.69314718055994531f : -INFINITY;
+          const int d0 = 16 * mt0 + 4 * lg;
+          if (sg.out_slot < 0) {
+            T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh + d0;
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+              if (mt < nmt)
+                *reinterpret_cast<v4s*>(op + mt * 16) =
+                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv);
+            if (mt0 == 0 && lg == 0 && a.out_lse) a.out_lse[(int64_t)qi * a.hq + head] = lse;
+          } else {
+            const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
+            float* op = a.part_o + slot * kD + d0;
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+              if (mt < nmt) *reinterpret_cast<v4f*>(op + mt * 16) = o_acc[mt] * inv;
+            if (mt0 == 0 && lg == 0) a.part_lse[slot] = lse;
+          }
+        }
+        ops += kEpiStores;
+      }
+    }
+    ops_prev = ops;
+    st_c = st_c == kStages - 1 ? 0 : st_c + 1;
+    advance(c_s, c_t, c_sg);
+  }
+}
+
+// One wave per record: the log-sum-exp combination of the record's partial
+// slots for the g heads of one (query, KV head); a record without slots writes
+// o = 0 and lse = -inf.  The slot ids are read once, then the lse and partial
+// rows of up to 8 slots are loaded together and folded in with a running max.
+template <typename T>
+__global__ __launch_bounds__(256) void slot_merge_kernel(SlotMergeArgs m) {
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int live = m.live ? *m.live : m.n_recs;
+  if (e >= live) return;
+  const int4 r = m.recs[e];
+  const int g = m.g, n = r.w;
+  constexpr int C4 = kD / 4;
+  T* out = reinterpret_cast<T*>(m.out) + (int64_t)r.x * m.o_sn;
+  const int32_t* slots = m.rec_slots + r.z;
+#pragma unroll 2
+  for (int c = lane; c < g * C4; c += 64) {
+    const int hh = c / C4, d4 = c - hh * C4;
+    const int head = r.y * g + hh;
+    float M = -INFINITY, z = 0.f;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < n; k0 += 8) {
+      int sl[8];
+      float lv[8];
+      v4f ov[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sl[j] = (k0 + j < n) ? slots[k0 + j] : -1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (sl[j] >= 0) {
+          const int64_t s = (int64_t)sl[j] * g + hh;
+          lv[j] = m.part_lse[s];
+          ov[j] = *reinterpret_cast<const v4f*>(m.part_o + s * kD + 4 * d4);
+        } else {
+          lv[j] = -INFINITY;
+          ov[j] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      float mx = M;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lv[j]);
+      if (mx != -INFINITY) {
+        const float sc = (M == -INFINITY) ? 0.f : expf(M - mx);
+        z *= sc;
+        acc *= sc;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float wgt = (lv[j] == -INFINITY) ? 0.f : expf(lv[j] - mx);
+          z += wgt;
+          acc += ov[j] * wgt;
+        }
+        M = mx;
+      }
+    }
+    const float inv = (z > 0.f) ? 1.f / z : 0.f;
+    *reinterpret_cast<v4s*>(out + (int64_t)head * m.o_sh + 4 * d4) =
+        pack4<T>(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+    if (d4 == 0 && m.out_lse) m.out_lse[(int64_t)r.x * m.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
+  }
+}
+
+}  // namespace stream
+
+using namespace stream;
+
+// ================================================================== host: plan
+bool stream_eligible(int dtype, int head_dim, int group, int flags) {
+  return (dtype == BE_BF16 || dtype == BE_F16) && head_dim == kD && group <= kSegRows &&
+         !(flags & (BE_PLAN_FORCE_VALU | BE_PLAN_FUSED_MERGE | BE_PLAN_TILE_KERNEL));
+}
+
+int stream_plan(const std::vector<Group>& groups, const be_level* levels, int num_levels, int64_t total_pages,
+                int num_queries, int hq, int hkv, int d, int page_size, int num_pages, int dtype, int num_cus,
+                const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info) {
+  (void)d;
+  (void)num_pages;
+  (void)dtype;
+  const int g = hq / hkv;
+  const int q_tile = std::max(1, kSegRows / g);
+  const int W = std::max(1, num_cus);
+
+  // ---- tasks: (query tile of a group, KV head), in group order
+  struct Task { int q0, qn, page_base, kv_len, head, tiles; };
+  std::vector<Task> tasks;
+  int64_t total = 0;
+  for (const Group& gr : groups) {
+    if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
+    const int tiles = (int)ceil_div(gr.kv_len, kTok);
+    for (int qa = gr.q0; qa < gr.q1; qa += q_tile)
+      for (int h = 0; h < hkv; ++h) {
+        tasks.push_back(Task{qa, std::min(q_tile, gr.q1 - qa), gr.page_base, gr.kv_len, h, tiles});
+        total += 4 * (int64_t)tiles + kSegCost;
+      }
+  }
+
+  // ---- balanced contiguous runs: workgroup b covers cost [b C / W, (b + 1) C / W)
+  // of the total cost C.  Every cut inside a task adds a segment start, so C
+  // is re-estimated from the realised assignment until the schedule closes.
+  std::vector<StreamSeg> segs;
+  std::vector<int4> wg(W, int4{0, 0, 0, 0});
+  auto assign = [&](int64_t c_total) -> int64_t {
+    segs.clear();
+    std::fill(wg.begin(), wg.end(), int4{0, 0, 0, 0});
+    auto wg_end = [&](int b) { return (int64_t)(((__int128)c_total * (b + 1)) / W); };
+    int b = 0;
+    int64_t pos = 0;
+    for (size_t ti = 0; ti < tasks.size(); ++ti) {
+      const Task& t = tasks[ti];
+      int t0 = 0;
+      while (t0 < t.tiles) {
+        int take = t.tiles - t0;
+        if (b < W - 1) {
+          const int fit = (int)((wg_end(b) - pos - kSegCost + 2) / 4);   // tiles that fit, rounded
+          if (fit <= 0 || wg[b].y >= kMaxSegs) {
+            ++b;
+            continue;
+          }
+          take = std::min(take, fit);
+        } else if (wg[b].y >= kMaxSegs) {
+          return -1;
+        }
+        if (wg[b].y == 0) wg[b].x = (int)segs.size();
+        StreamSeg s;
+        s.q_begin = t.q0;
+        s.q_count = t.qn;
+        s.page_begin = t.page_base;
+        s.tok_begin = t0 * kTok;
+        s.tok_count = std::min(t.kv_len - t0 * kTok, take * kTok);
+        s.head = t.head;
+        s.out_slot = -1;
+        s.n_tiles = take;
+        segs.push_back(s);
+        wg[b].y += 1;
+        wg[b].z += take;
+        pos += kSegCost + 4 * (int64_t)take;
+        t0 += take;
+      }
+    }
+    return pos;
+  };
+  int64_t c_total = total + (int64_t)(W - 1) * kSegCost;
+  for (int iter = 0; iter < 4; ++iter) {
+    const int64_t realised = assign(c_total);
+    if (realised < 0) return BE_ERR_UNSUPPORTED;
+    if (std::llabs(realised - c_total) <= 2) break;
+    c_total = realised;
+  }
+
+  // ---- partial slots and merge records per (query, KV head)
+  std::vector<int> cnt((size_t)num_queries * hkv, 0);
+  for (const StreamSeg& s : segs)
+    for (int j = 0; j < s.q_count; ++j) cnt[(size_t)(s.q_begin + j) * hkv + s.head] += 1;
+  int n_slots = 0;
+  for (StreamSeg& s : segs) {
+    bool direct = true;
+    for (int j = 0; j < s.q_count; ++j) direct = direct && cnt[(size_t)(s.q_begin + j) * hkv + s.head] == 1;
+    if (!direct) {
+      s.out_slot = n_slots;
+      n_slots += s.q_count;
+    }
+  }
+  std::vector<std::vector<int>> slots_of((size_t)num_queries * hkv);
+  for (const StreamSeg& s : segs)
+    if (s.out_slot >= 0)
+      for (int j = 0; j < s.q_count; ++j) slots_of[(size_t)(s.q_begin + j) * hkv + s.head].push_back(s.out_slot + j);
+  std::vector<int4> recs;
+  std::vector<int> rec_slots;
+  for (int qi = 0; qi < num_queries; ++qi)
+    for (int h = 0; h < hkv; ++h) {
+      const size_t k = (size_t)qi * hkv + h;
+      if (cnt[k] == 1 && slots_of[k].empty()) continue;   // written directly
+      recs.push_back(int4{qi, h, (int)rec_slots.size(), (int)slots_of[k].size()});
+      rec_slots.insert(rec_slots.end(), slots_of[k].begin(), slots_of[k].end());
+    }
+
+  // ---- serialise: header, workgroup table, segments, pages, records, record slots
+  const int64_t n_segs = (int64_t)segs.size();
+  if (caps) {
+    if (n_segs > caps->max_items || total_pages > caps->max_pages || (int64_t)recs.size() > caps->max_merge ||
+        n_slots > caps->max_merge_rows)
+      return fail(BE_ERR_CAPACITY,
+                  "plan exceeds its fixed capacities: segments %lld/%d pages %lld/%d records %zu/%d slots %d/%d",
+                  (long long)n_segs, caps->max_items, (long long)total_pages, caps->max_pages, recs.size(),
+                  caps->max_merge, n_slots, caps->max_merge_rows);
+  }
+  const int64_t c_segs = caps ? caps->max_items : n_segs;
+  const int64_t c_pages = caps ? caps->max_pages : total_pages;
+  const int64_t c_recs = caps ? caps->max_merge : (int64_t)recs.size();
+  const int64_t c_slots = caps ? caps->max_merge_rows : n_slots;
+  int64_t off = kPlanHeader;
+  const int64_t off_wg = off;     off += 4 * (int64_t)W;
+  const int64_t off_segs = off;   off += 8 * c_segs;
+  const int64_t off_pages = off;  off += c_pages;
+  const int64_t off_recs = off;   off += 4 * c_recs;
+  const int64_t off_rslots = off; off += c_slots;
+  off = ceil_div(off, 4) * 4;
+  if (off > cap || off > INT32_MAX)
+    return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  for (int i = 0; i < kPlanHeader; ++i) out[i] = 0;
+  out[kHdrItems] = (int32_t)n_segs;
+  out[kHdrMerge] = (int32_t)recs.size();
+  out[kHdrRows] = n_slots;
+  memcpy(out + off_wg, wg.data(), wg.size() * sizeof(int4));
+  if (n_segs) memcpy(out + off_segs, segs.data(), n_segs * sizeof(StreamSeg));
+  {
+    int64_t p = off_pages;
+    for (int lv = 0; lv < num_levels; ++lv) {
+      const be_level& L = levels[lv];
+      const int np = L.num_groups ? L.kv_indptr[L.num_groups] : 0;
+      if (np) memcpy(out + p, L.kv_indices, np * sizeof(int32_t));
+      p += np;
+    }
+  }
+  if (!recs.empty()) memcpy(out + off_recs, recs.data(), recs.size() * sizeof(int4));
+  if (!rec_slots.empty()) memcpy(out + off_rslots, rec_slots.data(), rec_slots.size() * sizeof(int32_t));
+
+  info->num_items = (int32_t)n_segs;
+  info->num_part_rows = n_slots;
+  info->num_merge = (int32_t)recs.size();
+  info->num_queries = num_queries;
+  info->kernel = 2;
+  info->tile_rows = kSegRows;
+  info->chunk_tokens = (int32_t)std::min<int64_t>(INT32_MAX, ceil_div(total, 4 * (int64_t)W) * kTok);
+  info->plan_ints = (int32_t)off;
+  info->off_items = (int32_t)off_segs;
+  info->off_pages = (int32_t)off_pages;
+  info->off_merge_q = (int32_t)off_recs;
+  info->off_merge_rows = (int32_t)off_rslots;
+  info->static_layout = caps ? 1 : 0;
+  info->grid_items = W;
+  info->grid_merge = (int32_t)c_recs;
+  info->part_rows_cap = (int32_t)c_slots;
+  info->counter_offset = ceil_div(c_slots * g * (kD + 1) * 4, 256) * 256;
+  info->counter_bytes = 0;
+  info->partial_bytes = info->counter_offset;
+  info->num_wg = W;
+  info->off_wg = (int32_t)off_wg;
+  info->off_records = (int32_t)off_recs;
+  info->off_record_slots = (int32_t)off_rslots;
+  return BE_OK;
+}
+
+// ================================================================== host: run
+int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partials, const void* q, int64_t q_sn,
+               int64_t q_sh, const void* kv, void* out, int64_t o_sn, int64_t o_sh, float* lse, float sm_scale,
+               int phases, hipStream_t st) {
+  const int hq = info->num_qo_heads, hkv = info->num_kv_heads, g = hq / hkv;
+  BE_REQUIRE(info->head_dim == kD, "corrupt plan info: streaming kernel with head_dim %d", info->head_dim);
+  BE_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && q_sn % 8 == 0 && q_sh % 8 == 0,
+             "q must be 16-byte aligned with strides that are multiples of 8 elements");
+  BE_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_sn % 4 == 0 && o_sh % 4 == 0,
+             "out must be 8-byte aligned with strides that are multiples of 4 elements");
+  float* part_o = reinterpret_cast<float*>(partials);
+  float* part_lse = part_o ? part_o + (int64_t)info->part_rows_cap * g * kD : nullptr;
+  const int ps = info->page_size;
+  if ((phases & BE_RUN_ATTENTION) && info->num_wg > 0) {
+    StreamArgs a;
+    a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;
+    a.kv = kv;
+    a.out = out; a.o_sn = o_sn; a.o_sh = o_sh; a.out_lse = lse;
+    a.part_o = part_o; a.part_lse = part_lse;
+    a.wg = reinterpret_cast<const int4*>(plan + info->off_wg);
+    a.segs = reinterpret_cast<const StreamSeg*>(plan + info->off_items);
+    a.pages = plan + info->off_pages;
+    a.page_size = ps;
+    a.page_shift = (ps & (ps - 1)) == 0 ? __builtin_ctz((unsigned)ps) : -1;
+    a.hkv = hkv; a.hq = hq; a.g = g;
+    a.scale_log2 = sm_scale * 1.4426950408889634f;
+    if (info->dtype == BE_BF16) attn_stream_kernel<bf16_t><<<info->num_wg, kThreads, 0, st>>>(a);
+    else if (info->dtype == BE_F16) attn_stream_kernel<f16_t><<<info->num_wg, kThreads, 0, st>>>(a);
+    else return fail(BE_ERR_INVALID, "corrupt plan info: streaming kernel with dtype %d", info->dtype);
+    BE_HIP_CHECK(hipGetLastError());
+  }
+  if ((phases & BE_RUN_MERGE) && info->grid_merge > 0) {
+    SlotMergeArgs m;
+    m.part_o = part_o; m.part_lse = part_lse;
+    m.recs = reinterpret_cast<const int4*>(plan + info->off_records);
+    m.rec_slots = plan + info->off_record_slots;
+    m.live = info->static_layout ? plan + kHdrMerge : nullptr;
+    m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse;
+    m.n_recs = info->grid_merge; m.g = g; m.hq = hq;
+    const int grid = (int)ceil_div(info->grid_merge, 4);
+    if (info->dtype == BE_BF16) slot_merge_kernel<bf16_t><<<grid, 256, 0, st>>>(m);
+    else slot_merge_kernel<f16_t><<<grid, 256, 0, st>>>(m);
+    BE_HIP_CHECK(hipGetLastError());
+  }
+  return BE_OK;
+}
+
+}  // namespace be

@@ -120,6 +120,8 @@ typedef struct be_level {
                                     arriving workgroup instead of a second kernel (every
                                     workgroup then pays a device-scope release fence, an
                                     L2 writeback on gfx950, so this is off by default)    */
+#define BE_PLAN_TILE_KERNEL 4    /* one workgroup per (work item, KV head) tile kernel even
+                                    where the persistent streaming kernel applies         */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the
@@ -138,7 +140,7 @@ typedef struct be_attn_plan_info {
   int32_t num_merge;       /* queries merged by the merge kernel               */
   int32_t num_queries;
   int32_t num_qo_heads, num_kv_heads, head_dim, page_size, num_pages, dtype;
-  int32_t kernel;          /* 0 = VALU, 1 = MFMA                               */
+  int32_t kernel;          /* 0 = VALU, 1 = MFMA tile, 2 = MFMA streaming (persistent) */
   int32_t tile_rows;       /* rows (queries x GQA group) per MFMA tile: 16/32  */
   int32_t chunk_tokens;    /* split-K chunk length                             */
   int32_t plan_ints;       /* int32 words of the device plan                    */
@@ -158,6 +160,14 @@ typedef struct be_attn_plan_info {
   int64_t kv_bytes;        /* algorithmic K+V bytes: distinct (page, head) valid tokens */
   int64_t qo_bytes;        /* Q + O bytes                                       */
   double flops;            /* 4 * D * sum_q sum_h kv_len(q)                     */
+  /* streaming kernel (kernel == 2): one workgroup per CU walks a contiguous,
+   * byte-balanced run of (query tile, KV head, 64-token tile) segments;
+   * partial results go to per-(query, KV head) slots merged by records.
+   * num_items = segments, num_part_rows = slots, num_merge = records.   */
+  int32_t num_wg;          /* persistent workgroups (grid of the attention kernel) */
+  int32_t off_wg;          /* [num_wg][4]: first segment, segments, tiles, 0       */
+  int32_t off_records;     /* [grid_merge][4]: query, KV head, first slot entry, n */
+  int32_t off_record_slots;/* slot ids of every record                             */
 } be_attn_plan_info;
 
 /* be_attn_plan (host only): validates the levels against num_queries,

@@ -12,6 +12,7 @@ import pytest
 from tests.conftest import ROOT
 
 HEADER = os.path.join(ROOT, "include", "beam_engine_amd.h")
+TILE = 4      # BE_PLAN_TILE_KERNEL
 
 
 def declared_functions():
@@ -67,7 +68,7 @@ def test_plan_covers_every_token_once_per_query():
               ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1]),
               ([0, 1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 3, 4, 5, 6, 7, 8, 9],
                [10, 11, 12, 13, 14, 15, 16, 17, 18], [1, 1, 1, 0, 0, 3, 3, 3])]
-    rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, num_pages=19)
+    rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, num_pages=19, flags=TILE)
     assert rc == 0, L.be_last_error()
     items = decode_items(info, buf)
     # every query sees exactly the tokens of its groups
@@ -99,7 +100,7 @@ def test_plan_covers_every_token_once_per_query():
 def test_plan_direct_output_for_single_partial_queries():
     # flat: each query one group of 3 pages -> a single item, written directly
     levels = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
-    rc, info, buf, *_ = plan(levels, num_pages=6)
+    rc, info, buf, *_ = plan(levels, num_pages=6, flags=TILE)
     assert rc == 0
     assert info.num_part_rows == 0 and info.num_merge == 0
     assert (decode_items(info, buf)[:, 5] == -1).all()
@@ -109,7 +110,7 @@ def test_plan_split_k_when_few_groups():
     # one group, long sequence -> chunked into several items sharing partial rows
     n_pages = 512
     levels = [([0, 4], [0, n_pages], list(range(n_pages)), [16])]
-    rc, info, buf, *_ = plan(levels, hq=32, hkv=8, page=16, num_pages=n_pages, cus=256)
+    rc, info, buf, *_ = plan(levels, hq=32, hkv=8, page=16, num_pages=n_pages, cus=256, flags=TILE)
     assert rc == 0
     items = decode_items(info, buf)
     assert len(items) > 1
@@ -153,7 +154,7 @@ def test_status_codes_map_to_reference_exceptions():
 def test_plan_lists_keyless_queries_for_zero_fill():
     # query 1's group is empty (one page, 0 valid tokens); query 2 belongs to no group
     levels = [([0, 1, 2], [0, 1, 2], [0, 1], [3, 0])]
-    rc, info, buf, *_ = plan(levels, nq=3, num_pages=2)
+    rc, info, buf, *_ = plan(levels, nq=3, num_pages=2, flags=TILE)
     assert rc == 0
     assert info.num_zero == 2
     assert buf[info.off_zero_q: info.off_zero_q + 2].tolist() == [1, 2]
@@ -168,6 +169,7 @@ def test_fixed_layout_offsets_do_not_depend_on_the_plan():
     b = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
     rc1, i1, buf1, *_ = plan(a, nq=8, num_pages=19, caps=caps)
     rc2, i2, buf2, *_ = plan(b, nq=2, num_pages=19, caps=caps)
+    assert i1.kernel == 1 and i2.kernel == 1       # tile_rows 32: the tile kernel's layout
     assert rc1 == 0 and rc2 == 0
     fields = ["plan_ints", "off_items", "off_qindex", "off_pages", "off_merge_q", "off_merge_ptr", "off_merge_rows",
               "off_zero_q", "off_zero_ptr", "grid_items", "grid_merge", "grid_zero", "part_rows_cap",
@@ -179,3 +181,134 @@ def test_fixed_layout_offsets_do_not_depend_on_the_plan():
     tiny = _lib.BePlanCaps(1, 16, 256, 16, 128, 16, 32)
     rc3, *_ = plan(a, nq=8, num_pages=19, caps=tiny)
     assert rc3 == _lib.BE_ERR_CAPACITY
+
+
+# ---------------------------------------------------------------- streaming plan
+def decode_stream(info, buf):
+    wg = buf[info.off_wg: info.off_wg + 4 * info.num_wg].reshape(-1, 4)
+    segs = buf[info.off_items: info.off_items + 8 * info.num_items].reshape(-1, 8)
+    recs = buf[info.off_records: info.off_records + 4 * info.num_merge].reshape(-1, 4)
+    rslots = buf[info.off_record_slots: info.off_record_slots + info.num_part_rows]
+    return wg, segs, recs, rslots
+
+
+def expected_tokens(levels, page, nq, hkv):
+    exp = np.zeros((nq, hkv), dtype=np.int64)
+    for qo, kvp, kvi, lpl in levels:
+        for g in range(len(qo) - 1):
+            npg = kvp[g + 1] - kvp[g]
+            n = 0 if npg == 0 else (npg - 1) * page + lpl[g]
+            exp[qo[g]:qo[g + 1], :] += n
+    return exp
+
+
+def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
+    assert info.kernel == 2
+    wg, segs, recs, rslots = decode_stream(info, buf)
+    g = hq // hkv
+    # workgroup table: contiguous segment runs, tile totals
+    assert wg[:, 1].sum() == info.num_items
+    start = 0
+    for b, (s0, ns, tiles, _) in enumerate(wg):
+        if ns:
+            assert s0 == start
+            assert tiles == segs[s0:s0 + ns, 7].sum()
+        start += ns
+    # coverage: every (query, KV head) sees exactly its tokens, in whole tiles from a 64-aligned start
+    seen = np.zeros((nq, hkv), dtype=np.int64)
+    for q0, qn, pb, t0, tc, head, slot, nt in segs:
+        assert tc > 0 and qn > 0 and qn * g <= 64 and t0 % 64 == 0 and nt == -(-tc // 64)
+        seen[q0:q0 + qn, head] += tc
+    assert (seen == expected_tokens(levels, page, nq, hkv)).all()
+    # slots: each non-direct segment owns qn consecutive slots; every slot is in exactly one record
+    owned = []
+    cover = {}
+    for q0, qn, pb, t0, tc, head, slot, nt in segs:
+        for j in range(qn):
+            cover.setdefault((q0 + j, head), []).append(-1 if slot < 0 else slot + j)
+        if slot >= 0:
+            owned.extend(range(slot, slot + qn))
+    assert sorted(owned) == list(range(info.num_part_rows))
+    assert sorted(rslots.tolist()) == list(range(info.num_part_rows))
+    rec_keys = set()
+    for q, h, ptr, n in recs:
+        rec_keys.add((q, h))
+        assert sorted(rslots[ptr:ptr + n].tolist()) == sorted(cover.get((q, h), []))
+    for q in range(nq):
+        for h in range(hkv):
+            c = cover.get((q, h), [])
+            direct = len(c) == 1 and c[0] == -1
+            assert ((q, h) in rec_keys) != direct
+    return wg, segs, recs, rslots
+
+
+def test_stream_plan_cascade_coverage_and_records():
+    levels = [([0, 8], [0, 4], [0, 1, 2, 3], [1]),
+              ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1]),
+              ([0, 1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 3, 4, 5, 6, 7, 8, 9],
+               [10, 11, 12, 13, 14, 15, 16, 17, 18], [1, 1, 1, 0, 0, 3, 3, 3])]
+    rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, num_pages=19)
+    assert rc == 0, L.be_last_error()
+    check_stream_plan(levels, 8, 8, 2, 4, info, buf)
+    valid = 3 * 4 + 1 + 3 * (4 + 1) + (1 + 4 + 1 + 1 + 0 + 0 + 3 + 3 + 3)
+    assert info.kv_bytes == valid * 2 * 128 * 2 * 2
+
+
+@pytest.mark.parametrize("cus", [2, 7, 256])
+def test_stream_plan_balances_tiles_across_workgroups(cus):
+    # north-star-like shape: 2 requests x 16 beams, prefix 1024 tokens, suffix 128 per beam
+    hq, hkv, page = 32, 8, 16
+    pre, suf = 64, 8
+    qo0, kvp0, kvi0 = [0, 16, 32], [0, pre, 2 * pre], list(range(2 * pre))
+    qo1 = list(range(33))
+    kvp1 = [2 * pre + 0] + [0] * 32
+    kvp1 = list(range(0, 33 * suf, suf))
+    kvi1 = list(range(2 * pre, 2 * pre + 32 * suf))
+    levels = [(qo0, kvp0, kvi0, [16, 16]), (qo1, kvp1, kvi1, [16] * 32)]
+    rc, info, buf, _lib, L = plan(levels, nq=32, hq=hq, hkv=hkv, page=page, num_pages=2 * pre + 32 * suf, cus=cus)
+    assert rc == 0, L.be_last_error()
+    wg, segs, recs, rslots = check_stream_plan(levels, 32, hq, hkv, page, info, buf)
+    assert info.num_wg == cus
+    tiles = wg[:, 2]
+    total = (2 * 16 + 32 * 2) * hkv            # prefix 2 x 16 tiles, suffix 32 x 2 tiles, per KV head
+    assert tiles.sum() == total
+    if cus > 1:
+        # balanced in the planner's cost (4 per tile + 1 per segment start) up to the
+        # granularity of the cuts: within two tiles and two segment starts
+        cost = 4 * tiles + wg[:, 1]
+        assert cost.max() - cost.min() <= 10
+    assert info.num_merge == 32 * hkv           # every (query, head) merges prefix and suffix
+
+
+def test_stream_plan_zero_records_for_keyless_queries():
+    levels = [([0, 1, 2], [0, 1, 2], [0, 1], [3, 0])]
+    rc, info, buf, *_ = plan(levels, nq=3, num_pages=2)
+    assert rc == 0
+    wg, segs, recs, rslots = check_stream_plan(levels, 3, 8, 2, 4, info, buf)
+    zero = sorted((int(q), int(h)) for q, h, p, n in recs if n == 0)
+    assert zero == [(1, 0), (1, 1), (2, 0), (2, 1)]
+
+
+def test_stream_plan_fixed_layout_offsets():
+    _lib, L = lib()
+    caps = _lib.BePlanCaps(4096, 16, 256, 64, 4096, 0, 64)
+    a = [([0, 8], [0, 4], [0, 1, 2, 3], [1]), ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1])]
+    b = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
+    rc1, i1, buf1, *_ = plan(a, nq=8, num_pages=19, caps=caps)
+    rc2, i2, buf2, *_ = plan(b, nq=2, num_pages=19, caps=caps)
+    assert rc1 == 0 and rc2 == 0 and i1.kernel == 2 and i2.kernel == 2
+    fields = ["plan_ints", "off_items", "off_pages", "off_wg", "off_records", "off_record_slots", "num_wg",
+              "grid_merge", "part_rows_cap", "partial_bytes"]
+    assert [getattr(i1, f) for f in fields] == [getattr(i2, f) for f in fields]
+    assert buf1[0] == i1.num_items and buf1[1] == i1.num_merge and buf2[1] == i2.num_merge
+    tiny = _lib.BePlanCaps(1, 16, 256, 64, 4096, 0, 64)
+    rc3, *_ = plan(a, nq=8, num_pages=19, caps=tiny)
+    assert rc3 == _lib.BE_ERR_CAPACITY
+
+
+def test_stream_plan_falls_back_to_tile_kernel_when_a_workgroup_overflows():
+    # one workgroup, 300 groups x 2 heads = 600 segments > the per-workgroup table
+    n = 300
+    levels = [(list(range(n + 1)), list(range(n + 1)), list(range(n)), [4] * n)]
+    rc, info, buf, *_ = plan(levels, nq=n, num_pages=n, cus=1)
+    assert rc == 0 and info.kernel == 1

@@ -45,11 +45,14 @@ def make_q(n, hq, d, dtype, seed, scale=1.0):
     return (torch.randn((n, hq, d), generator=g, dtype=torch.float32) * scale).to(dtype)
 
 
-def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True, fused_merge=False):
+def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True, fused_merge=False, tile_kernel=False,
+                num_cus=None):
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
     w._force_valu = force_valu
     w._fused_merge = fused_merge
+    w._tile_kernel = tile_kernel
+    w._num_cus = num_cus
     hq, d = q.shape[1], q.shape[2]
     w.plan(levels[0], levels[1], levels[2], levels[3], hq, kv.shape[3], d, page, causal=True,
            pos_encoding_mode="NONE", q_data_type=q.dtype)
@@ -97,7 +100,7 @@ def test_mfma_and_valu_agree_on_bf16(ws, force_valu, fused_merge):
     kv = make_pool(20, 4, 2, 128, torch.bfloat16, 3)
     q = make_q(8, 8, 128, torch.bfloat16, 4)
     (out, lse), w = run_cascade(ws, q, kv, levels, 4, force_valu=force_valu, fused_merge=fused_merge)
-    assert w.stats.kernel == ("valu" if force_valu else "mfma")
+    assert w.stats.kernel == ("valu" if force_valu else "tile" if fused_merge else "stream")
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 4, 128 ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
 
@@ -282,10 +285,84 @@ def test_repeated_runs_of_one_plan(ws, fused_merge):
     w = MultiLevelCascadeAttentionWrapper(2, ws)
     w._fused_merge = fused_merge
     w.plan(*levels, 32, 8, 128, 16, q_data_type=torch.bfloat16)
-    assert w.stats.num_merge == 16
+    # merge entries: per query (tile kernel) or per (query, KV head) (streaming kernel)
+    assert w.stats.num_merge == (16 if fused_merge else 16 * 8)
     for rep in range(6):
         q = make_q(16, 32, 128, torch.bfloat16, 100 + rep, 0.2)
         out, lse = w.run(q.cuda(), kv, return_lse=True)
         torch.cuda.synchronize()
         ref_o, ref_lse = oa.cascade_attention(q, kv.cpu(), *levels, 16, 128 ** -0.5)
         check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+def config3_levels(page):
+    next_page = [0]
+
+    def alloc(tokens):
+        n = tokens // page
+        out = list(range(next_page[0], next_page[0] + n))
+        next_page[0] += n
+        return out
+    root = alloc(4096)
+    l1 = [alloc(256) for _ in range(2)]
+    l2 = [alloc(128) for _ in range(8)]
+    l3 = [alloc(64) + alloc(32) for _ in range(32)]
+    levels = ([[0, 32], [0, 16, 32], list(range(0, 33, 4)), list(range(33))],
+              [[0, len(root)], [0, 16, 32], list(range(0, 8 * 8 + 1, 8)), list(range(0, 32 * 6 + 1, 6))],
+              [root, sum(l1, []), sum(l2, []), sum(l3, [])],
+              [[16], [16, 16], [16] * 8, [16] * 32])
+    return levels, next_page[0]
+
+
+@pytest.mark.parametrize("shape", ["config2", "config3", "ragged_suffix"])
+@pytest.mark.parametrize("kernel,num_cus", [("tile", None), ("stream", None), ("stream", 4), ("stream", 7),
+                                            ("stream", 61)])
+def test_stream_and_tile_kernels(ws, shape, kernel, num_cus):
+    """Both MFMA kernels against the oracle; small CU counts make every
+    streaming workgroup walk many segments and cut work items mid-way."""
+    say(f"{kernel} kernel {shape} cus={num_cus}")
+    page, hq, hkv, d = 16, 32, 8, 128
+    s = 1 / math.sqrt(128)
+    if shape == "config2":
+        levels, pages = shared_prefix_levels(4, 8, 2048, [128] * 32, page)
+    elif shape == "config3":
+        levels, pages = config3_levels(page)
+    else:
+        g = torch.Generator().manual_seed(31)
+        suf = torch.randint(1, 300, (24,), generator=g).tolist()
+        levels, pages = shared_prefix_levels(3, 8, 1000, suf, page)
+    n = levels[0][0][-1] if shape != "config3" else 32
+    kv = make_pool(pages, page, hkv, d, torch.bfloat16, 41, s)
+    q = make_q(n, hq, d, torch.bfloat16, 42, s)
+    (out, lse), w = run_cascade(ws, q, kv, levels, page, tile_kernel=(kernel == "tile"), num_cus=num_cus)
+    assert w.stats.kernel == kernel
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_stream_kernel_flat_long_paths(ws, dtype):
+    """Flat decode (one group per query) with paths longer than a workgroup's
+    share: queries split across workgroups are merged from slots."""
+    say(f"stream flat long paths {dtype}")
+    from beam_engine_amd import BatchDecodeWithPagedKVCacheWrapper
+    page, hq, hkv, d = 16, 64, 8, 128
+    lens = [3000, 17, 1, 64, 65, 2048, 129, 700]
+    kvp, kvi, lpl, pages = [0], [], [], 0
+    for L in lens:
+        npg = -(-L // page)
+        kvi.extend(range(pages, pages + npg))
+        pages += npg
+        kvp.append(len(kvi))
+        lpl.append(L - (npg - 1) * page)
+    kv = make_pool(pages, page, hkv, d, dtype, 43, 0.2)
+    q = make_q(len(lens), hq, d, dtype, 44, 0.2)
+    f = BatchDecodeWithPagedKVCacheWrapper(ws)
+    f._num_cus = 13
+    f.plan(kvp, kvi, lpl, hq, hkv, d, page, q_data_type=dtype)
+    assert f.stats.kernel == "stream"
+    out, lse = f.run(q.cuda(), kv.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    levels = ([list(range(len(lens) + 1))], [kvp], [kvi], [lpl])
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, dtype)
