@@ -58,8 +58,8 @@ constexpr int kStageBytes = 2 * kKvBytes + kQBytes;
 constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
 constexpr int kThreads = 64 * kWaves;
 constexpr int kLoadsPerTile = 4;              // direct loads per wave per tile (2 K + 2 V row blocks)
-constexpr int kEpiStores = 4;                 // lower bound of store instructions of an epilogue
-constexpr int kSegCost = 1;                   // planner cost of a segment start, in quarter tiles
+constexpr int kSegCost = 4;                   // planner cost of a segment start, in quarter tiles
+constexpr int kQuarterTiles = 4;              // single-row-tile segments this long split tokens 4 ways
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -192,32 +192,50 @@ __device__ __forceinline__ SegReg seg_reg(const StreamSeg& x) {
 // One wave's share of a 64-token tile: rows 16 rt + (0..15) against NSUB
 // 16-token sub-tiles starting at kt / vt, for NMT head_dim tiles (voff).
 // Online softmax state (m_run, l_run over this wave's tokens, o_acc) is
-// updated in place; the rescale is skipped when no row's max rose.  dma(j),
-// j = 0..3, issues this wave's share of the loads of a later tile; the calls
-// are spread over the computation so that the loads of all waves do not queue
-// on the address unit at the same moment.
-template <typename T, int NSUB, int NMT, typename Dma>
+// updated in place; the rescale is skipped when no row's max rose.  P.V pairs
+// two sub-tiles per v_mfma_f32_16x16x32: lane group lg holds tokens 4 lg..+3
+// of both sub-tiles in the A (V^T) and B (P^T) operands alike, so the 32-wide
+// contraction pairs the same tokens.
+template <typename T, int NSUB, int NMT>
 __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsigned char* vt, const v8s (&qf)[4],
                                              const uint32_t (&koff)[4], const uint32_t (&voff)[NMT], int tok_base,
                                              int valid, int lg, float scale, float& m_run, float& l_run,
-                                             v4f (&o_acc)[8], Dma&& dma) {
+                                             v4f (&o_acc)[8]) {
+  // all LDS operand reads first: the K fragments, then the V^T fragments
+  // (independent of the scores, so their latency hides under the softmax)
+  v8s kf[NSUB][4];
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kf[k][ks] = *reinterpret_cast<const v8s*>(kt + k * 4096 + koff[ks]);
+  v4s vf[NMT][NSUB];
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k)
+      vf[mt][k] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + k * 4096 + voff[mt]));
+
   float x[NSUB][4];
-  float mx = -INFINITY;
 #pragma unroll
   for (int k = 0; k < NSUB; ++k) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      acc = mfma_qk<T>(*reinterpret_cast<const v8s*>(kt + k * 4096 + koff[ks]), qf[ks], acc);
-    if (k == 0) dma(0);
+    for (int ks = 0; ks < 4; ++ks) acc = mfma_qk<T>(kf[k][ks], qf[ks], acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x[k][r] = acc[r] * scale;
-      if (valid < kTok && tok_base + k * 16 + 4 * lg + r >= valid) x[k][r] = -INFINITY;
-      mx = fmaxf(mx, x[k][r]);
-    }
+    for (int r = 0; r < 4; ++r) x[k][r] = acc[r] * scale;
   }
-  dma(1);
+  if (valid < kTok) {
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (tok_base + k * 16 + 4 * lg + r >= valid) x[k][r] = -INFINITY;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[k][r]);
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
   const float m_new = fmaxf(m_run, mx);
@@ -240,16 +258,19 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
     }
     pf[k] = pack4<T>(p[0], p[1], p[2], p[3]);
   }
-  dma(2);
-  // O^T tiles: lane (lg, lc) supplies V[16 sub + 4 lg + lc/4][16 mt + 4 (lc%4) .. +3]
+  // O^T tiles: lane (lg, lc) supplied V[16 sub + 4 lg + lc/4][16 mt + 4 (lc%4) .. +3]
 #pragma unroll
   for (int mt = 0; mt < NMT; ++mt) {
     v4f o = o_acc[mt];
+    if constexpr (NSUB == 1) {
+      o = mfma_pv<T>(vf[mt][0], pf[0], o);
+    } else {
 #pragma unroll
-    for (int k = 0; k < NSUB; ++k)
-      o = mfma_pv<T>(__builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + k * 4096 + voff[mt])), pf[k], o);
+      for (int k = 0; k < NSUB; k += 2)
+        o = mfma_qk<T>(__builtin_shufflevector(vf[mt][k], vf[mt][k + 1], 0, 1, 2, 3, 4, 5, 6, 7),
+                       __builtin_shufflevector(pf[k], pf[k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
+    }
     o_acc[mt] = o;
-    if (mt == NMT / 2 - 1) dma(3);
   }
 }
 
@@ -282,17 +303,19 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   const float scale = a.scale_log2;
 
   // per-lane LDS offsets (bytes) of the MFMA operand reads, within a 16-token
-  // sub-tile: K / Q rows, and V^T columns of all 8 head_dim tiles and of this
-  // wave's half (waves 4..7 take the upper half where head_dim is split)
-  uint32_t koff[4], voff8[8], voff4[4];
+  // sub-tile: K / Q rows, and V^T columns of all 8 head_dim tiles, of this
+  // wave's half (waves 4..7 take the upper half) and of head_dim tile w
+  uint32_t koff[4], voff8[8], voff4[4], voff1[1];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) koff[ks] = lc * 256 + ((((ks << 2) | lg) ^ lc) << 4);
   {
     const int tl = 4 * lg + (lc >> 2), b1 = (lc >> 1) & 1, b0 = lc & 1;
+    auto vcol = [&](int mt) { return (uint32_t)(tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3)); };
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) voff8[mt] = tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3);
+    for (int mt = 0; mt < 8; ++mt) voff8[mt] = vcol(mt);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) voff4[mt] = voff8[4 * (w >> 2) + mt];
+    for (int mt = 0; mt < 4; ++mt) voff4[mt] = vcol(4 * (w >> 2) + mt);
+    voff1[0] = vcol(w);
   }
   // this wave loads rows 8w..8w+7 of every tile (two 1 KB loads of 4 rows for
   // K and for V); per-lane byte offsets inside the page for the fast path
@@ -437,17 +460,22 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
     st_l = st_l == kStages - 1 ? 0 : st_l + 1;
 
     // ---- compute tile n.  Wave roles by the segment's row tiles (NT):
-    //   NT >= 3: row tile w & 3, token half w >> 2, all head_dim;
-    //   NT == 2: row tile w & 1, token half (w >> 1) & 1, head_dim half w >> 2;
-    //   NT == 1: token quarter w & 3, head_dim half w >> 2.
-    // The ts == 0 wave of each (row tile, head_dim part) collects the others.
+    //   NT >= 3: row tile w & 3, token half w >> 2, all head_dim        (mode 0)
+    //   NT == 2: row tile w & 1, token half (w >> 1) & 1, head_dim half  (mode 1)
+    //   NT == 1, segment of >= kQuarterTiles tiles: token quarter w & 3,
+    //            head_dim half w >> 2                                     (mode 2)
+    //   NT == 1, shorter: all 64 tokens, head_dim tile w                  (mode 3)
+    // Where tokens are split, the ts == 0 wave of each (row tile, head_dim
+    // part) collects the others at the end of the segment; mode 3 recomputes
+    // the scores in every wave instead, which costs less than that exchange
+    // when the segment is short.
     const SegReg& sg = c_sg;
     const int R = sg.q_count * g;
     const int NT = (R + 15) >> 4;
-    const int rt = NT >= 3 ? (w & 3) : NT == 2 ? (w & 1) : 0;
-    const int ts = NT >= 3 ? (w >> 2) : NT == 2 ? ((w >> 1) & 1) : (w & 3);
-    const int nsub = NT == 1 ? 1 : 2;
-    const int sub0 = ts * nsub;
+    const int mode = NT >= 3 ? 0 : NT == 2 ? 1 : sg.n_tiles >= kQuarterTiles ? 2 : 3;
+    const int rt = mode == 0 ? (w & 3) : mode == 1 ? (w & 1) : 0;
+    const int ts = mode == 0 ? (w >> 2) : mode == 1 ? ((w >> 1) & 1) : mode == 2 ? (w & 3) : 0;
+    const int sub0 = mode == 2 ? ts : 2 * ts;
     const bool act = 16 * rt < R;
     const bool last = c_t == sg.n_tiles - 1;
     unsigned char* stage = st_lds + st_c * kStageBytes;
@@ -466,42 +494,41 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
       const int valid = min(kTok, sg.tok_count - c_t * kTok);
       const unsigned char* kt = stage + sub0 * 4096;
       const unsigned char* vt = stage + kKvBytes + sub0 * 4096;
-      if (NT >= 3)
-        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc, dma);
-      else if (NT == 2)
-        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc, dma);
+      if (mode == 0)
+        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+      else if (mode == 1)
+        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+      else if (mode == 2)
+        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
       else
-        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc, dma);
-    } else {
-      dma_all();
+        tile_compute<T, 4, 1>(kt, vt, qf, koff, voff1, 0, valid, lg, scale, m_run, l_run, o_acc);
     }
-    kv_pending = false;
 
     if (last) {
       float l = l_run;
       l += __shfl_xor(l, 16, 64);
       l += __shfl_xor(l, 32, 64);
-      const int nmt = NT >= 3 ? 8 : 4;
-      const int mt0 = NT >= 3 ? 0 : 4 * (w >> 2);
+      const int nmt = mode == 0 ? 8 : mode == 3 ? 1 : 4;
+      const int mt0 = mode == 0 ? 0 : mode == 3 ? w : 4 * (w >> 2);
       // token-split waves hand their state to the ts == 0 wave of their (row
       // tile, head_dim part) through this stage's LDS (no loads target it
       // until the next iteration's barrier)
       const int kslot = nmt * 1024 + 512;
-      lds_fence();
+      if (mode != 3) lds_fence();
       if (ts > 0 && act) {
-        unsigned char* slot = stage + (NT >= 3 ? w - 4 : w) * kslot;
+        unsigned char* slot = stage + (mode == 0 ? w - 4 : w) * kslot;
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt)
           if (mt < nmt) *reinterpret_cast<v4f*>(slot + (mt * 64 + lane) * 16) = o_acc[mt];
         reinterpret_cast<float*>(slot + nmt * 1024)[lane] = m_run;
         reinterpret_cast<float*>(slot + nmt * 1024 + 256)[lane] = l;
       }
-      lds_fence();
+      if (mode != 3) lds_fence();
       if (ts == 0 && act) {
-        const int np = NT == 1 ? 4 : 2;                  // waves sharing the (row tile, head_dim part)
+        const int np = mode == 2 ? 4 : mode == 3 ? 1 : 2;   // waves sharing the (row tile, head_dim part)
         for (int p = 1; p < np; ++p) {
-          const int pw = NT >= 3 ? w + 4 : NT == 2 ? w + 2 : w + p;   // partner wave
-          const unsigned char* slot = stage + (NT >= 3 ? pw - 4 : pw) * kslot;
+          const int pw = mode == 0 ? w + 4 : mode == 1 ? w + 2 : w + p;   // partner wave
+          const unsigned char* slot = stage + (mode == 0 ? pw - 4 : pw) * kslot;
           const float mb = reinterpret_cast<const float*>(slot + nmt * 1024)[lane];
           const float lb = reinterpret_cast<const float*>(slot + nmt * 1024 + 256)[lane];
           const float M = fmaxf(m_run, mb);
@@ -539,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
             if (mt0 == 0 && lg == 0) a.part_lse[slot] = lse;
           }
         }
-        ops += kEpiStores;
+        ops += nmt;                                      // store instructions (lse not counted)
       }
     }
     ops_prev = ops;
@@ -643,57 +670,65 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       }
   }
 
-  // ---- balanced contiguous runs: workgroup b covers cost [b C / W, (b + 1) C / W)
-  // of the total cost C.  Every cut inside a task adds a segment start, so C
-  // is re-estimated from the realised assignment until the schedule closes.
+  // ---- balanced contiguous runs.  Costs: 4 per tile, kSegCost per segment
+  // start.  When workgroup b opens, its share is the remaining cost (tiles,
+  // task starts, and one split per remaining workgroup boundary) over the
+  // remaining workgroups; a tile joins b unless it would overshoot that share
+  // by more than half its cost.
   std::vector<StreamSeg> segs;
   std::vector<int4> wg(W, int4{0, 0, 0, 0});
-  auto assign = [&](int64_t c_total) -> int64_t {
-    segs.clear();
-    std::fill(wg.begin(), wg.end(), int4{0, 0, 0, 0});
-    auto wg_end = [&](int b) { return (int64_t)(((__int128)c_total * (b + 1)) / W); };
+  std::vector<int64_t> suffix(tasks.size() + 1, 0);     // cost of tasks[i..] as whole segments
+  for (size_t i = tasks.size(); i-- > 0;) suffix[i] = suffix[i + 1] + 4 * (int64_t)tasks[i].tiles + kSegCost;
+  {
     int b = 0;
-    int64_t pos = 0;
+    int64_t used = 0, share = 0;
+    auto open_wg = [&](size_t ti, int tile) {
+      const int64_t rem = suffix[ti + 1] + 4 * (int64_t)(tasks[ti].tiles - tile) + kSegCost +
+                          (int64_t)(W - 1 - b) * kSegCost;
+      share = ceil_div(rem, W - b);
+      used = 0;
+    };
+    bool first = true;
     for (size_t ti = 0; ti < tasks.size(); ++ti) {
       const Task& t = tasks[ti];
-      int t0 = 0;
-      while (t0 < t.tiles) {
-        int take = t.tiles - t0;
-        if (b < W - 1) {
-          const int fit = (int)((wg_end(b) - pos - kSegCost + 2) / 4);   // tiles that fit, rounded
-          if (fit <= 0 || wg[b].y >= kMaxSegs) {
-            ++b;
-            continue;
-          }
-          take = std::min(take, fit);
-        } else if (wg[b].y >= kMaxSegs) {
-          return -1;
+      bool open = false;                 // a segment of this task is open in workgroup b
+      for (int tile = 0; tile < t.tiles; ++tile) {
+        if (first) {
+          open_wg(ti, tile);
+          first = false;
         }
-        if (wg[b].y == 0) wg[b].x = (int)segs.size();
-        StreamSeg s;
-        s.q_begin = t.q0;
-        s.q_count = t.qn;
-        s.page_begin = t.page_base;
-        s.tok_begin = t0 * kTok;
-        s.tok_count = std::min(t.kv_len - t0 * kTok, take * kTok);
-        s.head = t.head;
-        s.out_slot = -1;
-        s.n_tiles = take;
-        segs.push_back(s);
-        wg[b].y += 1;
-        wg[b].z += take;
-        pos += kSegCost + 4 * (int64_t)take;
-        t0 += take;
+        for (;;) {
+          const int64_t c = 4 + (open ? 0 : kSegCost);
+          const bool room = used + c / 2 <= share && (open || wg[b].y < kMaxSegs);
+          if (room || b == W - 1) break;
+          ++b;
+          open = false;
+          open_wg(ti, tile);
+        }
+        if (!open) {
+          if (wg[b].y >= kMaxSegs) return BE_ERR_UNSUPPORTED;
+          if (wg[b].y == 0) wg[b].x = (int)segs.size();
+          StreamSeg sgm;
+          sgm.q_begin = t.q0;
+          sgm.q_count = t.qn;
+          sgm.page_begin = t.page_base;
+          sgm.tok_begin = tile * kTok;
+          sgm.tok_count = 0;
+          sgm.head = t.head;
+          sgm.out_slot = -1;
+          sgm.n_tiles = 0;
+          segs.push_back(sgm);
+          wg[b].y += 1;
+          used += kSegCost;
+          open = true;
+        }
+        StreamSeg& cur = segs.back();
+        cur.n_tiles += 1;
+        cur.tok_count = std::min(t.kv_len - cur.tok_begin, cur.n_tiles * kTok);
+        wg[b].z += 1;
+        used += 4;
       }
     }
-    return pos;
-  };
-  int64_t c_total = total + (int64_t)(W - 1) * kSegCost;
-  for (int iter = 0; iter < 4; ++iter) {
-    const int64_t realised = assign(c_total);
-    if (realised < 0) return BE_ERR_UNSUPPORTED;
-    if (std::llabs(realised - c_total) <= 2) break;
-    c_total = realised;
   }
 
   // ---- partial slots and merge records per (query, KV head)
