@@ -14,6 +14,7 @@ own mean duration against the plan's algorithmic bytes.
 
 from __future__ import annotations
 
+import json
 import math
 import os
 import platform
@@ -40,10 +41,12 @@ class AttnTimer:
     def __init__(self, kind: str, hkv: int, d: int, es: int):
         self.records = []      # (start, mid, end, algorithmic bytes, flops)
         self.kind = kind
+        self.kernels = set()   # attention kernels the plans used
         self.hkv, self.d, self.es = hkv, d, es
 
     def __call__(self, layer, run_fn, wrapper):
         st = wrapper.stats
+        self.kernels.add(st.kernel)
         if self.kind == "flat":
             # the flat strategy is scored by its own traffic: every query's whole path
             hq = wrapper._info.num_qo_heads
@@ -162,6 +165,19 @@ def cpu_baseline_e2e(gen: BatchedBeamSearch, budget_s: float = 20.0):
                        f"{platform.processor() or platform.machine()}")}
 
 
+def profiled_traffic(kind: str, steps: int):
+    """HBM traffic per attention launch measured by rocprofv3 counter runs of
+    the default bench command (profiles/e2e_llama8b_beam16_cascade_traffic.*),
+    or None for a run that is not that command."""
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles",
+                        "e2e_llama8b_beam16_cascade_traffic.json")
+    if kind != "cascade" or steps != 250 or not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        data = json.load(f)
+    return int(data["traffic_bytes_per_launch"]), "profiles/e2e_llama8b_beam16_cascade_traffic.md"
+
+
 def run_e2e_bench(args):
     steps = args.steps if args.steps is not None else 250
     warmup = args.warmup if args.warmup is not None else 5
@@ -169,6 +185,7 @@ def run_e2e_bench(args):
     gen, timer, wall, model, pt = run_e2e(steps, warmup, kind, graphs=not getattr(args, "no_graphs", False))
     n = len(gen.state.candidates)
     tok_s = n * steps / wall
+    traffic, traffic_src = profiled_traffic(kind, steps)
     att = summarize_attention(timer)
     log(f"{kind}: {steps} steps in {wall:.2f} s -> {tok_s:.1f} tokens/s; attention {att['mean_attn_us']:.1f} us "
         f"+ merge {att['mean_merge_us']:.1f} us per layer, {att['gbs']:.0f} GB/s")
@@ -183,8 +200,10 @@ def run_e2e_bench(args):
                    "layers": model.cfg.num_hidden_layers, "page_size": 16, "length_penalty": 1.0,
                    "per_request_tokens_per_s": round(tok_s / 8, 2)},
         "roofline": {"bound": "hbm", "achieved": round(att["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(att["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "attn_tile_kernel (decode attention; merge kernel timed separately)",
+                     "frac": round(att["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": " / ".join(f"attn_{k}_kernel" for k in sorted(timer.kernels)) +
+                               " (decode attention; merge kernel timed separately)",
                      "launches": att["launches"], "bytes_per_launch": round(att["bytes_per_launch"]),
                      "mean_launch_us": round(att["mean_attn_us"], 2),
                      "mean_merge_us": round(att["mean_merge_us"], 2),
