@@ -20,6 +20,7 @@ BE_OK, BE_ERR_INVALID, BE_ERR_HIP, BE_ERR_CAPACITY, BE_ERR_UNSUPPORTED = 0, 1, 2
 BE_PLAN_FORCE_VALU = 1
 BE_PLAN_FUSED_MERGE = 2
 BE_PLAN_TILE_KERNEL = 4
+BE_PLAN_NO_TAIL = 8
 BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
@@ -44,7 +45,8 @@ class BeLevel(ctypes.Structure):
 
 class BePlanCaps(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
-        "max_items", "max_queries", "max_pages", "max_merge", "max_merge_rows", "max_zero", "tile_rows")]
+        "max_items", "max_queries", "max_pages", "max_merge", "max_merge_rows", "max_zero", "tile_rows",
+        "max_tails")]
 
 
 class BeAttnPlanInfo(ctypes.Structure):
@@ -60,7 +62,8 @@ class BeAttnPlanInfo(ctypes.Structure):
         ("kv_bytes", ctypes.c_int64),
         ("qo_bytes", ctypes.c_int64),
         ("flops", ctypes.c_double),
-    ] + [(n, ctypes.c_int32) for n in ("num_wg", "off_wg", "off_records", "off_record_slots")]
+    ] + [(n, ctypes.c_int32) for n in ("num_wg", "off_wg", "off_records", "off_record_slots",
+                                              "num_tails", "off_tails")]
 
 
 EXPORTS = (

@@ -85,6 +85,7 @@ class PlanStats:
         self.num_part_rows = int(info.num_part_rows)
         self.num_merge = int(info.num_merge)
         self.kernel = {0: "valu", 1: "tile", 2: "stream"}[int(info.kernel)]
+        self.num_tails = int(info.num_tails) if self.kernel == "stream" else 0
         self.chunk_tokens = int(info.chunk_tokens)
 
     @property
@@ -111,6 +112,7 @@ class _PagedPlanner:
         self._force_valu = False
         self._fused_merge = False
         self._tile_kernel = False     # force the per-(item, head) tile kernel over the streaming kernel
+        self._no_tail = False         # streaming kernel: keep short groups out of the tail-and-merge pass
         self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
 
@@ -149,7 +151,8 @@ class _PagedPlanner:
         dt = _lib.dtype_code(q_data_type)
         flags = (_lib.BE_PLAN_FORCE_VALU if self._force_valu else 0) | \
             (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0) | \
-            (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0)
+            (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0) | \
+            (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()
@@ -230,13 +233,13 @@ class _PagedPlanner:
         return (out, lse) if return_lse else out
 
     def use_fixed_layout(self, max_items: int, max_queries: int, max_pages: int, max_merge: int,
-                         max_merge_rows: int, max_zero: int, tile_rows: int) -> None:
+                         max_merge_rows: int, max_zero: int, tile_rows: int, max_tails: int = 0) -> None:
         """Plan into a fixed-capacity layout from now on: every plan has the
         same device addresses and launch sizes (the live counts are read on
         the device), so runs can be captured in a HIP graph and replayed with
         later plans.  A plan beyond a capacity raises MemoryError."""
         self._caps = _lib.BePlanCaps(max_items, max_queries, max_pages, max_merge, max_merge_rows, max_zero,
-                                     tile_rows)
+                                     tile_rows, max_tails)
 
     @property
     def stats(self) -> PlanStats:

@@ -62,10 +62,10 @@ bool stream_eligible(int dtype, int head_dim, int group, int flags);
 // table holds; the caller then plans for the tile kernel instead.
 int stream_plan(const std::vector<Group>& groups, const be_level* levels, int num_levels, int64_t total_pages,
                 int num_queries, int hq, int hkv, int d, int page_size, int num_pages, int dtype, int num_cus,
-                const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info);
+                int flags, const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info);
 
 // Launches the streaming attention kernel (phases & BE_RUN_ATTENTION) and the
-// slot merge kernel (phases & BE_RUN_MERGE) of a kernel == 2 plan.
+// tail-and-merge kernel (phases & BE_RUN_MERGE) of a kernel == 2 plan.
 int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partials, const void* q, int64_t q_sn,
                int64_t q_sh, const void* kv, void* out, int64_t o_sn, int64_t o_sh, float* lse, float sm_scale,
                int phases, hipStream_t st);

@@ -720,7 +720,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   if (stream_eligible(dtype, d, g, flags) && (!caps || caps->tile_rows == 64)) {
     memset(info, 0, sizeof(*info));
     const int rc = stream_plan(groups, levels, num_levels, total_pages, num_queries, hq, hkv, d, page_size,
-                               num_pages, dtype, num_cus, caps, out, cap, info);
+                               num_pages, dtype, num_cus, flags, caps, out, cap, info);
     if (rc == BE_OK) {
       info->num_qo_heads = hq;
       info->num_kv_heads = hkv;

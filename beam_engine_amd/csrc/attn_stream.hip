@@ -60,6 +60,10 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kLoadsPerTile = 4;              // direct loads per wave per tile (2 K + 2 V row blocks)
 constexpr int kSegCost = 4;                   // planner cost of a segment start, in quarter tiles
 constexpr int kQuarterTiles = 4;              // single-row-tile segments this long split tokens 4 ways
+constexpr int kTailTokens = 64;               // groups this short with few queries go to the tail pass
+constexpr int kTailQueries = 4;
+constexpr int kTailChunks = 64;               // 16-token tail chunks per query (one per lane)
+constexpr int kRecWords = 8;                  // int32 words per merge record
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -89,16 +93,21 @@ struct StreamArgs {
   float scale_log2;
 };
 
-struct SlotMergeArgs {
+struct TailMergeArgs {
   const float* part_o;
   const float* part_lse;
-  const int4* recs;          // query, KV head, first entry of rec_slots, slot count
+  const int32_t* recs;       // [n][8]: query, KV head, first rec_slots entry, slots, first tail, tails, 0, 0
   const int32_t* rec_slots;
+  const int2* tails;         // 16-token chunks: page id, in-page token offset | valid tokens << 16
   const int32_t* live;       // live record count (device), or null
+  const void* q;
+  int64_t q_sn, q_sh;
+  const void* kv;
   void* out;
   int64_t o_sn, o_sh;
   float* out_lse;
-  int n_recs, g, hq;
+  int n_recs, g, hq, hkv, page_size;
+  float scale_log2;
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -575,33 +584,116 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   }
 }
 
-// One wave per record: the log-sum-exp combination of the record's partial
-// slots for the g heads of one (query, KV head); a record without slots writes
-// o = 0 and lse = -inf.  The slot ids are read once, then the lse and partial
-// rows of up to 8 slots are loaded together and folded in with a running max.
+// One wave per record (query, KV head).  The tail pass first attends the
+// record's tail chunks — 16 tokens of one page each, from the query's short
+// groups — as one online softmax (a token in two groups counts twice, as two
+// separately merged groups would count it): K and V rows come straight from
+// global memory into this wave's LDS area, then the streaming kernel's tile
+// step (S^T = K Q^T on v_mfma_f32_16x16x32, P.V on 16x16x16, rows = the g
+// query heads).  Its normalised output and lse join the record's partial
+// slots in a log-sum-exp combination with a running max; a record with
+// neither writes o = 0 and lse = -inf.
 template <typename T>
-__global__ __launch_bounds__(256) void slot_merge_kernel(SlotMergeArgs m) {
-  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+__global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
+  constexpr int kArea = 2 * kKvBytes / 4 + 256;      // K + V chunk (8 KB), then lse of the tail
+  __shared__ __attribute__((aligned(16))) unsigned char tl_lds[4][kArea];
+  const int wv = rfl(threadIdx.x >> 6);
+  const int e = blockIdx.x * 4 + wv;
+  const int lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
   const int live = m.live ? *m.live : m.n_recs;
   if (e >= live) return;
-  const int4 r = m.recs[e];
-  const int g = m.g, n = r.w;
+  const int32_t* rp = m.recs + (int64_t)e * kRecWords;
+  const int qi = rfl(rp[0]), h = rfl(rp[1]), s0 = rfl(rp[2]), n = rfl(rp[3]), t0 = rfl(rp[4]), nt = rfl(rp[5]);
+  const int g = m.g;
   constexpr int C4 = kD / 4;
-  T* out = reinterpret_cast<T*>(m.out) + (int64_t)r.x * m.o_sn;
-  const int32_t* slots = m.rec_slots + r.z;
+  unsigned char* kt = tl_lds[wv];
+  unsigned char* vt = kt + 4096;
+  float* vs_o = reinterpret_cast<float*>(tl_lds[wv]);           // tail result [g][kD] (g <= 16)
+  float* vs_lse = reinterpret_cast<float*>(tl_lds[wv] + 8192);
+  const int32_t* slots = m.rec_slots + s0;
+  // lane k holds tail entry k and slot id k (both loads issued before anything waits)
+  const int2 ent = lane < nt ? m.tails[t0 + lane] : int2{0, 0};
+  const int sid = lane < n ? slots[lane] : -1;
+
+  if (nt > 0) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const T* kvp = reinterpret_cast<const T*>(m.kv);
+    const int ps = m.page_size, hkv = m.hkv;
+    const int64_t plane = (int64_t)ps * hkv * kD;
+    const T* qp = reinterpret_cast<const T*>(m.q) + (int64_t)qi * m.q_sn + (int64_t)(h * g + min(lc, g - 1)) * m.q_sh;
+    v8s qf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const v8s*>(qp + 8 * (4 * ks + lg));
+    uint32_t koff[4], voff8[8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) koff[ks] = lc * 256 + ((((ks << 2) | lg) ^ lc) << 4);
+    {
+      const int tl = 4 * lg + (lc >> 2), b1 = (lc >> 1) & 1, b0 = lc & 1;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) voff8[mt] = (uint32_t)(tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3));
+    }
+    // rows 4 i + lg of chunk c, 16-byte column slot lc holding global column lc ^ row
+    v4i kr[4], vr[4];
+    auto load = [&](int c) {
+      const int page = __builtin_amdgcn_readlane(ent.x, c);
+      const int ov = __builtin_amdgcn_readlane(ent.y, c);
+      const int off = ov & 0xffff, valid = ov >> 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + lg;
+        const int tok = off + min(r, valid - 1);
+        const T* src = kvp + (((int64_t)page * 2 * ps + tok) * hkv + h) * kD + ((lc ^ r) << 3);
+        kr[i] = *reinterpret_cast<const v4i*>(src);
+        vr[i] = *reinterpret_cast<const v4i*>(src + plane);
+      }
+    };
+    float m_run = -INFINITY, l_run = 0.f;
+    v4f o_acc[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    load(0);
+    for (int c = 0; c < nt; ++c) {
+      const int valid = __builtin_amdgcn_readlane(ent.y, c) >> 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + lg;
+        *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[i];
+        *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[i];
+      }
+      if (c + 1 < nt) load(c + 1);
+      tile_compute<T, 1, 8>(kt, vt, qf, koff, voff8, 0, valid, lg, m.scale_log2, m_run, l_run, o_acc);
+    }
+    float l = l_run;
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    // lane holds O^T[d = 16 mt + 4 lg + i][row lc]; every tail chunk has a valid token, so l > 0
+    if (lc < g) {
+      const float inv = 1.f / l;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4f*>(vs_o + lc * kD + 16 * mt + 4 * lg) = o_acc[mt] * inv;
+      if (lg == 0) vs_lse[lc] = (m_run + log2f(l)) * 0.69314718055994531f;
+    }
+  }
+
+  T* out = reinterpret_cast<T*>(m.out) + (int64_t)qi * m.o_sn;
 #pragma unroll 2
   for (int c = lane; c < g * C4; c += 64) {
     const int hh = c / C4, d4 = c - hh * C4;
-    const int head = r.y * g + hh;
+    const int head = h * g + hh;
     float M = -INFINITY, z = 0.f;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (nt > 0) {
+      M = vs_lse[hh];
+      z = 1.f;
+      acc = *reinterpret_cast<const v4f*>(vs_o + hh * kD + 4 * d4);
+    }
     for (int k0 = 0; k0 < n; k0 += 8) {
       int sl[8];
       float lv[8];
       v4f ov[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sl[j] = (k0 + j < n) ? slots[k0 + j] : -1;
+      for (int j = 0; j < 8; ++j)
+        sl[j] = (k0 + j >= n) ? -1 : (k0 + j < 64) ? __builtin_amdgcn_readlane(sid, k0 + j) : slots[k0 + j];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if (sl[j] >= 0) {
@@ -632,7 +724,7 @@ __global__ __launch_bounds__(256) void slot_merge_kernel(SlotMergeArgs m) {
     const float inv = (z > 0.f) ? 1.f / z : 0.f;
     *reinterpret_cast<v4s*>(out + (int64_t)head * m.o_sh + 4 * d4) =
         pack4<T>(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
-    if (d4 == 0 && m.out_lse) m.out_lse[(int64_t)r.x * m.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
+    if (d4 == 0 && m.out_lse) m.out_lse[(int64_t)qi * m.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
   }
 }
 
@@ -648,7 +740,7 @@ bool stream_eligible(int dtype, int head_dim, int group, int flags) {
 
 int stream_plan(const std::vector<Group>& groups, const be_level* levels, int num_levels, int64_t total_pages,
                 int num_queries, int hq, int hkv, int d, int page_size, int num_pages, int dtype, int num_cus,
-                const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info) {
+                int flags, const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info) {
   (void)d;
   (void)num_pages;
   (void)dtype;
@@ -656,12 +748,48 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   const int q_tile = std::max(1, kSegRows / g);
   const int W = std::max(1, num_cus);
 
+  std::vector<int32_t> all_pages((size_t)total_pages);
+  {
+    int64_t p = 0;
+    for (int lv = 0; lv < num_levels; ++lv) {
+      const be_level& L = levels[lv];
+      const int np = L.num_groups ? L.kv_indptr[L.num_groups] : 0;
+      if (np) memcpy(all_pages.data() + p, L.kv_indices, np * sizeof(int32_t));
+      p += np;
+    }
+  }
+
+  // ---- tail chunks: groups of <= kTailTokens tokens and <= kTailQueries
+  // queries are attended by the merge kernel, 16 tokens (one page) per chunk,
+  // while each query holds at most kTailChunks of them
+  std::vector<std::vector<int2>> tails_of((size_t)num_queries);
+  std::vector<char> is_tail(groups.size(), 0);
+  if (!(flags & BE_PLAN_NO_TAIL) && page_size % 16 == 0 && g <= 16) {
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+      const Group& gr = groups[gi];
+      if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || gr.kv_len > kTailTokens || gr.q1 - gr.q0 > kTailQueries) continue;
+      const int nch = (int)ceil_div(gr.kv_len, 16);
+      bool fits = true;
+      for (int qi = gr.q0; qi < gr.q1; ++qi) fits = fits && (int)tails_of[qi].size() + nch <= kTailChunks;
+      if (!fits) continue;
+      is_tail[gi] = 1;
+      for (int qi = gr.q0; qi < gr.q1; ++qi)
+        for (int c = 0; c < nch; ++c) {
+          const int tok0 = 16 * c;
+          const int page = all_pages[(size_t)gr.page_base + tok0 / page_size];
+          const int valid = std::min(16, gr.kv_len - tok0);
+          tails_of[qi].push_back(int2{page, (tok0 % page_size) | (valid << 16)});
+        }
+    }
+  }
+
   // ---- tasks: (query tile of a group, KV head), in group order
   struct Task { int q0, qn, page_base, kv_len, head, tiles; };
   std::vector<Task> tasks;
   int64_t total = 0;
-  for (const Group& gr : groups) {
-    if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const Group& gr = groups[gi];
+    if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || is_tail[gi]) continue;
     const int tiles = (int)ceil_div(gr.kv_len, kTok);
     for (int qa = gr.q0; qa < gr.q1; qa += q_tile)
       for (int h = 0; h < hkv; ++h) {
@@ -738,7 +866,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   int n_slots = 0;
   for (StreamSeg& s : segs) {
     bool direct = true;
-    for (int j = 0; j < s.q_count; ++j) direct = direct && cnt[(size_t)(s.q_begin + j) * hkv + s.head] == 1;
+    for (int j = 0; j < s.q_count; ++j)
+      direct = direct && cnt[(size_t)(s.q_begin + j) * hkv + s.head] == 1 && tails_of[s.q_begin + j].empty();
     if (!direct) {
       s.out_slot = n_slots;
       n_slots += s.q_count;
@@ -748,60 +877,65 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   for (const StreamSeg& s : segs)
     if (s.out_slot >= 0)
       for (int j = 0; j < s.q_count; ++j) slots_of[(size_t)(s.q_begin + j) * hkv + s.head].push_back(s.out_slot + j);
-  std::vector<int4> recs;
+  std::vector<int32_t> recs;
   std::vector<int> rec_slots;
-  for (int qi = 0; qi < num_queries; ++qi)
+  std::vector<int2> tails;
+  for (int qi = 0; qi < num_queries; ++qi) {
+    const int t0 = (int)tails.size(), nt = (int)tails_of[qi].size();
+    tails.insert(tails.end(), tails_of[qi].begin(), tails_of[qi].end());
     for (int h = 0; h < hkv; ++h) {
       const size_t k = (size_t)qi * hkv + h;
-      if (cnt[k] == 1 && slots_of[k].empty()) continue;   // written directly
-      recs.push_back(int4{qi, h, (int)rec_slots.size(), (int)slots_of[k].size()});
+      if (cnt[k] == 1 && nt == 0 && slots_of[k].empty()) continue;   // written directly
+      const int32_t r[kRecWords] = {qi, h, (int)rec_slots.size(), (int)slots_of[k].size(), t0, nt, 0, 0};
+      recs.insert(recs.end(), r, r + kRecWords);
       rec_slots.insert(rec_slots.end(), slots_of[k].begin(), slots_of[k].end());
     }
+  }
+  const int64_t n_recs = (int64_t)recs.size() / kRecWords;
+  const int64_t n_tails = (int64_t)tails.size();
 
-  // ---- serialise: header, workgroup table, segments, pages, records, record slots
+  // ---- serialise: header, workgroup table, segments, pages, records, record
+  // slots, tail chunks
   const int64_t n_segs = (int64_t)segs.size();
   if (caps) {
-    if (n_segs > caps->max_items || total_pages > caps->max_pages || (int64_t)recs.size() > caps->max_merge ||
-        n_slots > caps->max_merge_rows)
+    if (n_segs > caps->max_items || total_pages > caps->max_pages || n_recs > caps->max_merge ||
+        n_slots > caps->max_merge_rows || n_tails > caps->max_tails)
       return fail(BE_ERR_CAPACITY,
-                  "plan exceeds its fixed capacities: segments %lld/%d pages %lld/%d records %zu/%d slots %d/%d",
-                  (long long)n_segs, caps->max_items, (long long)total_pages, caps->max_pages, recs.size(),
-                  caps->max_merge, n_slots, caps->max_merge_rows);
+                  "plan exceeds its fixed capacities: segments %lld/%d pages %lld/%d records %lld/%d slots %d/%d "
+                  "tail chunks %lld/%d",
+                  (long long)n_segs, caps->max_items, (long long)total_pages, caps->max_pages, (long long)n_recs,
+                  caps->max_merge, n_slots, caps->max_merge_rows, (long long)n_tails, caps->max_tails);
   }
   const int64_t c_segs = caps ? caps->max_items : n_segs;
   const int64_t c_pages = caps ? caps->max_pages : total_pages;
-  const int64_t c_recs = caps ? caps->max_merge : (int64_t)recs.size();
+  const int64_t c_recs = caps ? caps->max_merge : n_recs;
   const int64_t c_slots = caps ? caps->max_merge_rows : n_slots;
+  const int64_t c_tails = caps ? caps->max_tails : n_tails;
   int64_t off = kPlanHeader;
   const int64_t off_wg = off;     off += 4 * (int64_t)W;
   const int64_t off_segs = off;   off += 8 * c_segs;
   const int64_t off_pages = off;  off += c_pages;
-  const int64_t off_recs = off;   off += 4 * c_recs;
+  const int64_t off_recs = off;   off += kRecWords * c_recs;
   const int64_t off_rslots = off; off += c_slots;
+  off = ceil_div(off, 2) * 2;
+  const int64_t off_tails = off;  off += 2 * c_tails;
   off = ceil_div(off, 4) * 4;
   if (off > cap || off > INT32_MAX)
     return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
   for (int i = 0; i < kPlanHeader; ++i) out[i] = 0;
   out[kHdrItems] = (int32_t)n_segs;
-  out[kHdrMerge] = (int32_t)recs.size();
+  out[kHdrMerge] = (int32_t)n_recs;
   out[kHdrRows] = n_slots;
   memcpy(out + off_wg, wg.data(), wg.size() * sizeof(int4));
   if (n_segs) memcpy(out + off_segs, segs.data(), n_segs * sizeof(StreamSeg));
-  {
-    int64_t p = off_pages;
-    for (int lv = 0; lv < num_levels; ++lv) {
-      const be_level& L = levels[lv];
-      const int np = L.num_groups ? L.kv_indptr[L.num_groups] : 0;
-      if (np) memcpy(out + p, L.kv_indices, np * sizeof(int32_t));
-      p += np;
-    }
-  }
-  if (!recs.empty()) memcpy(out + off_recs, recs.data(), recs.size() * sizeof(int4));
+  if (total_pages) memcpy(out + off_pages, all_pages.data(), total_pages * sizeof(int32_t));
+  if (!recs.empty()) memcpy(out + off_recs, recs.data(), recs.size() * sizeof(int32_t));
   if (!rec_slots.empty()) memcpy(out + off_rslots, rec_slots.data(), rec_slots.size() * sizeof(int32_t));
+  if (n_tails) memcpy(out + off_tails, tails.data(), n_tails * sizeof(int2));
 
   info->num_items = (int32_t)n_segs;
   info->num_part_rows = n_slots;
-  info->num_merge = (int32_t)recs.size();
+  info->num_merge = (int32_t)n_recs;
   info->num_queries = num_queries;
   info->kernel = 2;
   info->tile_rows = kSegRows;
@@ -822,6 +956,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->off_wg = (int32_t)off_wg;
   info->off_records = (int32_t)off_recs;
   info->off_record_slots = (int32_t)off_rslots;
+  info->num_tails = (int32_t)n_tails;
+  info->off_tails = (int32_t)off_tails;
   return BE_OK;
 }
 
@@ -838,7 +974,7 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
   float* part_o = reinterpret_cast<float*>(partials);
   float* part_lse = part_o ? part_o + (int64_t)info->part_rows_cap * g * kD : nullptr;
   const int ps = info->page_size;
-  if ((phases & BE_RUN_ATTENTION) && info->num_wg > 0) {
+  if ((phases & BE_RUN_ATTENTION) && info->num_wg > 0 && (info->static_layout || info->num_items > 0)) {
     StreamArgs a;
     a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;
     a.kv = kv;
@@ -857,16 +993,20 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
     BE_HIP_CHECK(hipGetLastError());
   }
   if ((phases & BE_RUN_MERGE) && info->grid_merge > 0) {
-    SlotMergeArgs m;
+    TailMergeArgs m;
     m.part_o = part_o; m.part_lse = part_lse;
-    m.recs = reinterpret_cast<const int4*>(plan + info->off_records);
+    m.recs = plan + info->off_records;
     m.rec_slots = plan + info->off_record_slots;
+    m.tails = reinterpret_cast<const int2*>(plan + info->off_tails);
     m.live = info->static_layout ? plan + kHdrMerge : nullptr;
+    m.q = q; m.q_sn = q_sn; m.q_sh = q_sh;
+    m.kv = kv;
     m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse;
-    m.n_recs = info->grid_merge; m.g = g; m.hq = hq;
+    m.n_recs = info->grid_merge; m.g = g; m.hq = hq; m.hkv = hkv; m.page_size = ps;
+    m.scale_log2 = sm_scale * 1.4426950408889634f;
     const int grid = (int)ceil_div(info->grid_merge, 4);
-    if (info->dtype == BE_BF16) slot_merge_kernel<bf16_t><<<grid, 256, 0, st>>>(m);
-    else slot_merge_kernel<f16_t><<<grid, 256, 0, st>>>(m);
+    if (info->dtype == BE_BF16) tail_merge_kernel<bf16_t><<<grid, 256, 0, st>>>(m);
+    else tail_merge_kernel<f16_t><<<grid, 256, 0, st>>>(m);
     BE_HIP_CHECK(hipGetLastError());
   }
   return BE_OK;

@@ -112,7 +112,7 @@ def attention_workload(args):
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": f"attn_{st.kernel}_kernel" + ("" if st.num_merge == 0 or args.fused_merge else
-                                                    " + slot_merge_kernel" if st.kernel == "stream" else " + merge_kernel"),
+                                                    " + tail_merge_kernel" if st.kernel == "stream" else " + merge_kernel"),
             "bytes_per_launch": alg, "mean_launch_us": round(mean_us, 2), "median_launch_us": round(med_us, 2),
             "tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
     result = {

@@ -122,6 +122,8 @@ typedef struct be_level {
                                     L2 writeback on gfx950, so this is off by default)    */
 #define BE_PLAN_TILE_KERNEL 4    /* one workgroup per (work item, KV head) tile kernel even
                                     where the persistent streaming kernel applies         */
+#define BE_PLAN_NO_TAIL 8        /* streaming kernel: keep short groups of few queries in the
+                                    persistent kernel instead of the tail-and-merge pass   */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the
@@ -131,6 +133,7 @@ typedef struct be_level {
 typedef struct be_plan_caps {
   int32_t max_items, max_queries, max_pages, max_merge, max_merge_rows, max_zero;
   int32_t tile_rows;       /* fixed rows per workgroup tile: 16, 32, 64 or 128 */
+  int32_t max_tails;       /* streaming kernel: tail chunk entries              */
 } be_plan_caps;
 
 /* Filled by be_attn_plan; passed back to be_attn_run unchanged. */
@@ -166,8 +169,15 @@ typedef struct be_attn_plan_info {
    * num_items = segments, num_part_rows = slots, num_merge = records.   */
   int32_t num_wg;          /* persistent workgroups (grid of the attention kernel) */
   int32_t off_wg;          /* [num_wg][4]: first segment, segments, tiles, 0       */
-  int32_t off_records;     /* [grid_merge][4]: query, KV head, first slot entry, n */
+  int32_t off_records;     /* [grid_merge][8]: query, KV head, first slot entry, slots,
+                              first tail entry, tail entries, 0, 0                  */
   int32_t off_record_slots;/* slot ids of every record                             */
+  /* Groups of at most 64 tokens and at most 4 queries (page_size a multiple of
+   * 16) skip the persistent kernel: the merge kernel attends them per (query,
+   * KV head) before it combines the slots.  Tail entries are 16-token chunks,
+   * [num_tails][2]: page id, in-page token offset | valid tokens << 16. */
+  int32_t num_tails;
+  int32_t off_tails;
 } be_attn_plan_info;
 
 /* be_attn_plan (host only): validates the levels against num_queries,

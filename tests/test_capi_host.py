@@ -187,9 +187,24 @@ def test_fixed_layout_offsets_do_not_depend_on_the_plan():
 def decode_stream(info, buf):
     wg = buf[info.off_wg: info.off_wg + 4 * info.num_wg].reshape(-1, 4)
     segs = buf[info.off_items: info.off_items + 8 * info.num_items].reshape(-1, 8)
-    recs = buf[info.off_records: info.off_records + 4 * info.num_merge].reshape(-1, 4)
+    recs = buf[info.off_records: info.off_records + 8 * info.num_merge].reshape(-1, 8)
     rslots = buf[info.off_record_slots: info.off_record_slots + info.num_part_rows]
-    return wg, segs, recs, rslots
+    tails = buf[info.off_tails: info.off_tails + 2 * info.num_tails].reshape(-1, 2)
+    return wg, segs, recs, rslots, tails
+
+
+def expected_keys(levels, page, nq):
+    """Per query: the multiset of (page id, in-page slot) of every token of every group it is in."""
+    from collections import Counter
+    exp = [Counter() for _ in range(nq)]
+    for qo, kvp, kvi, lpl in levels:
+        for g in range(len(qo) - 1):
+            npg = kvp[g + 1] - kvp[g]
+            n = 0 if npg == 0 else (npg - 1) * page + lpl[g]
+            keys = [(kvi[kvp[g] + t // page], t % page) for t in range(n)]
+            for q in range(qo[g], qo[g + 1]):
+                exp[q].update(keys)
+    return exp
 
 
 def expected_tokens(levels, page, nq, hkv):
@@ -203,8 +218,10 @@ def expected_tokens(levels, page, nq, hkv):
 
 
 def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
+    from collections import Counter
     assert info.kernel == 2
-    wg, segs, recs, rslots = decode_stream(info, buf)
+    wg, segs, recs, rslots, tails = decode_stream(info, buf)
+    pages = buf[info.off_pages:]
     g = hq // hkv
     # workgroup table: contiguous segment runs, tile totals
     assert wg[:, 1].sum() == info.num_items
@@ -214,12 +231,27 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             assert s0 == start
             assert tiles == segs[s0:s0 + ns, 7].sum()
         start += ns
-    # coverage: every (query, KV head) sees exactly its tokens, in whole tiles from a 64-aligned start
-    seen = np.zeros((nq, hkv), dtype=np.int64)
+    # coverage: every (query, KV head) sees exactly its tokens (segments: whole tiles from a
+    # 64-aligned start; tail chunks: up to 16 tokens of one page), page by page
+    seen = [[Counter() for _ in range(hkv)] for _ in range(nq)]
     for q0, qn, pb, t0, tc, head, slot, nt in segs:
         assert tc > 0 and qn > 0 and qn * g <= 64 and t0 % 64 == 0 and nt == -(-tc // 64)
-        seen[q0:q0 + qn, head] += tc
-    assert (seen == expected_tokens(levels, page, nq, hkv)).all()
+        keys = [(int(pages[pb + t // page]), t % page) for t in range(t0, t0 + tc)]
+        for q in range(q0, q0 + qn):
+            seen[q][head].update(keys)
+    tails_of = {}
+    for q, h, ptr, n, tb, tn, z0, z1 in recs:
+        assert z0 == 0 and z1 == 0
+        chunk = [tuple(int(v) for v in e) for e in tails[tb:tb + tn]]
+        assert tails_of.setdefault(int(q), chunk) == chunk       # every head of a query shares its chunks
+        for pg, ov in chunk:
+            off, valid = ov & 0xFFFF, ov >> 16
+            assert 1 <= valid <= 16 and off + valid <= page
+            seen[q][h].update((pg, off + t) for t in range(valid))
+    exp = expected_keys(levels, page, nq)
+    for q in range(nq):
+        for h in range(hkv):
+            assert seen[q][h] == exp[q], (q, h)
     # slots: each non-direct segment owns qn consecutive slots; every slot is in exactly one record
     owned = []
     cover = {}
@@ -231,13 +263,13 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
     assert sorted(owned) == list(range(info.num_part_rows))
     assert sorted(rslots.tolist()) == list(range(info.num_part_rows))
     rec_keys = set()
-    for q, h, ptr, n in recs:
+    for q, h, ptr, n, tb, tn, *_ in recs:
         rec_keys.add((q, h))
-        assert sorted(rslots[ptr:ptr + n].tolist()) == sorted(cover.get((q, h), []))
+        assert sorted(rslots[ptr:ptr + n].tolist()) == sorted(x for x in cover.get((q, h), []) if x >= 0)
     for q in range(nq):
         for h in range(hkv):
             c = cover.get((q, h), [])
-            direct = len(c) == 1 and c[0] == -1
+            direct = len(c) == 1 and c[0] == -1 and not tails_of.get(q)
             assert ((q, h) in rec_keys) != direct
     return wg, segs, recs, rslots
 
@@ -285,23 +317,23 @@ def test_stream_plan_zero_records_for_keyless_queries():
     rc, info, buf, *_ = plan(levels, nq=3, num_pages=2)
     assert rc == 0
     wg, segs, recs, rslots = check_stream_plan(levels, 3, 8, 2, 4, info, buf)
-    zero = sorted((int(q), int(h)) for q, h, p, n in recs if n == 0)
+    zero = sorted((int(q), int(h)) for q, h, p, n, tb, tn, *_ in recs if n == 0 and tn == 0)
     assert zero == [(1, 0), (1, 1), (2, 0), (2, 1)]
 
 
 def test_stream_plan_fixed_layout_offsets():
     _lib, L = lib()
-    caps = _lib.BePlanCaps(4096, 16, 256, 64, 4096, 0, 64)
+    caps = _lib.BePlanCaps(4096, 16, 256, 64, 4096, 0, 64, 64)
     a = [([0, 8], [0, 4], [0, 1, 2, 3], [1]), ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1])]
     b = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
     rc1, i1, buf1, *_ = plan(a, nq=8, num_pages=19, caps=caps)
     rc2, i2, buf2, *_ = plan(b, nq=2, num_pages=19, caps=caps)
     assert rc1 == 0 and rc2 == 0 and i1.kernel == 2 and i2.kernel == 2
-    fields = ["plan_ints", "off_items", "off_pages", "off_wg", "off_records", "off_record_slots", "num_wg",
-              "grid_merge", "part_rows_cap", "partial_bytes"]
+    fields = ["plan_ints", "off_items", "off_pages", "off_wg", "off_records", "off_record_slots", "off_tails",
+              "num_wg", "grid_merge", "part_rows_cap", "partial_bytes"]
     assert [getattr(i1, f) for f in fields] == [getattr(i2, f) for f in fields]
     assert buf1[0] == i1.num_items and buf1[1] == i1.num_merge and buf2[1] == i2.num_merge
-    tiny = _lib.BePlanCaps(1, 16, 256, 64, 4096, 0, 64)
+    tiny = _lib.BePlanCaps(1, 16, 256, 64, 4096, 0, 64, 64)
     rc3, *_ = plan(a, nq=8, num_pages=19, caps=tiny)
     assert rc3 == _lib.BE_ERR_CAPACITY
 
@@ -312,3 +344,59 @@ def test_stream_plan_falls_back_to_tile_kernel_when_a_workgroup_overflows():
     levels = [(list(range(n + 1)), list(range(n + 1)), list(range(n)), [4] * n)]
     rc, info, buf, *_ = plan(levels, nq=n, num_pages=n, cus=1)
     assert rc == 0 and info.kernel == 1
+
+
+def e2e_like_levels(nreq=2, beams=4, pre_pages=8, page=16, seed=0):
+    """Request prefixes shared by their beams, then single-query levels of a few tokens (the
+    shape of a beam trie that re-converges every step)."""
+    rng = np.random.default_rng(seed)
+    nq = nreq * beams
+    nxt = 0
+    kvi0 = list(range(nxt, nxt + nreq * pre_pages)); nxt += nreq * pre_pages
+    l0 = (list(range(0, nq + 1, beams)), list(range(0, nreq * pre_pages + 1, pre_pages)), kvi0, [page] * nreq)
+    levels = [l0]
+    for _ in range(2):
+        lens = rng.integers(1, 49, size=nq)                  # 1..48 tokens
+        kvp, kvi, lpl = [0], [], []
+        for n in lens:
+            npg = -(-int(n) // page)
+            kvi += list(range(nxt, nxt + npg)); nxt += npg
+            kvp.append(kvp[-1] + npg)
+            lpl.append(int(n) - (npg - 1) * page)
+        levels.append((list(range(nq + 1)), kvp, kvi, lpl))
+    return levels, nq, nxt
+
+
+@pytest.mark.parametrize("page", [16, 32])
+def test_stream_plan_routes_short_groups_to_tail_chunks(page):
+    levels, nq, npages = e2e_like_levels(page=page)
+    rc, info, buf, _lib, L = plan(levels, nq=nq, hq=32, hkv=8, page=page, num_pages=npages)
+    assert rc == 0, L.be_last_error()
+    check_stream_plan(levels, nq, 32, 8, page, info, buf)
+    lens = [(np.diff(kvp) - 1) * page + np.asarray(lpl) for _, kvp, _, lpl in levels[1:]]
+    assert info.num_tails == sum(int(-(-n // 16)) for l in lens for n in l)
+    # the prefix level stays in the streaming kernel; every (query, head) merges
+    assert info.num_items > 0 and info.num_merge == nq * 8
+    rc, info2, buf2, *_ = plan(levels, nq=nq, hq=32, hkv=8, page=page, num_pages=npages, flags=_lib.BE_PLAN_NO_TAIL)
+    assert rc == 0 and info2.num_tails == 0
+    check_stream_plan(levels, nq, 32, 8, page, info2, buf2)
+
+
+def test_stream_plan_tail_limits():
+    page = 16
+    # a 5-query group (more than the tail pass takes) and 70 single-token levels for query 0
+    # (more chunks than one query holds)
+    levels = [([0, 5], [0, 1], [0], [3])]
+    nxt = 1
+    for _ in range(70):
+        levels.append(([0, 1], [0, 1], [nxt], [1]))
+        nxt += 1
+    rc, info, buf, _lib, L = plan(levels, nq=5, hq=8, hkv=2, page=page, num_pages=nxt)
+    assert rc == 0, L.be_last_error()
+    check_stream_plan(levels, 5, 8, 2, page, info, buf)
+    wg, segs, recs, rslots, tails = decode_stream(info, buf)
+    assert info.num_tails == 64
+    assert any(q0 == 0 and qn == 5 for q0, qn, *_ in segs)    # the 5-query group is a segment
+    # page sizes that are not a multiple of 16 never use tail chunks
+    rc, info, buf, *_ = plan(levels, nq=5, hq=8, hkv=2, page=8, num_pages=nxt)
+    assert rc == 0 and info.num_tails == 0

@@ -366,3 +366,60 @@ def test_stream_kernel_flat_long_paths(ws, dtype):
     levels = ([list(range(len(lens) + 1))], [kvp], [kvi], [lpl])
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, dtype)
+
+
+def trie_levels(n_req, beams, prefix, page, seed, depth=2, max_tail=48, shared=True):
+    """A request prefix shared by its beams, then `depth` levels of short groups: mostly
+    single queries of 1..max_tail tokens, and (shared=True) a few groups of 2-4 beams — the
+    shape of a beam trie that re-converges every step."""
+    rng = np.random.default_rng(seed)
+    nq = n_req * beams
+    nxt = [0]
+
+    def alloc(n):
+        npg = -(-n // page)
+        out = list(range(nxt[0], nxt[0] + npg))
+        nxt[0] += npg
+        return out, n - (npg - 1) * page
+    qo, kvp, kvi, lpl = [[0]], [[0]], [[]], [[]]
+    for r in range(n_req):
+        pg, last = alloc(prefix)
+        qo[0].append(qo[0][-1] + beams); kvi[0] += pg; kvp[0].append(len(kvi[0])); lpl[0].append(last)
+    for lv in range(depth):
+        q, p, i, l = [0], [0], [], []
+        while q[-1] < nq:
+            size = int(rng.integers(2, 5)) if shared and rng.random() < 0.15 else 1
+            size = min(size, nq - q[-1])
+            pg, last = alloc(int(rng.integers(1, max_tail + 1)))
+            q.append(q[-1] + size); i += pg; p.append(len(i)); l.append(last)
+        qo.append(q); kvp.append(p); kvi.append(i); lpl.append(l)
+    return (qo, kvp, kvi, lpl), nxt[0], nq
+
+
+@pytest.mark.parametrize("case", ["bf16_p16", "f16_p16", "bf16_p32", "bf16_g8", "bf16_g16", "bf16_deep"])
+@pytest.mark.parametrize("tails", [True, False])
+def test_stream_tail_pass_on_trie_shapes(ws, case, tails):
+    """Short groups attended by the tail-and-merge kernel (and, with tails off,
+    by the persistent kernel) against the oracle, on beam-trie shapes."""
+    say(f"tail pass {case} tails={tails}")
+    dtype = torch.float16 if case.startswith("f16") else torch.bfloat16
+    page = 32 if case.endswith("p32") else 16
+    hq, hkv = {"bf16_g8": (64, 8), "bf16_g16": (64, 4)}.get(case, (32, 8))
+    depth = 5 if case == "bf16_deep" else 2
+    d = 128
+    levels, pages, nq = trie_levels(3, 8, 300, page, seed=len(case) + 7 * depth, depth=depth)
+    s = 1 / math.sqrt(d)
+    kv = make_pool(pages, page, hkv, d, dtype, 51, s)
+    q = make_q(nq, hq, d, dtype, 52, s)
+    from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+    w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
+    w._no_tail = not tails
+    w._num_cus = 7
+    w.plan(*levels, hq, hkv, d, page, q_data_type=dtype)
+    st = w.stats
+    assert st.kernel == "stream"
+    assert (st.num_tails > 0) == tails
+    out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, dtype)
