@@ -291,6 +291,128 @@ class BeamState:
             levels.append((qo, kvp, kvi, lpl))
         return levels
 
+    def segment_tree(self):
+        """The live trie's segments (the cascade's groups: unbranched page
+        chains between branch points), parents before children.
+
+        Returns ``(segs, paths)``: ``segs[i] = [pages, tokens, parent index or
+        -1, candidate indices below it, child indices]`` (a candidate's own
+        leaf segment excludes its newest token, the cascade convention) and
+        ``paths[q]`` = the segment indices of candidate q's path, top down."""
+        self._annotate()
+        ps = self.page_table.page_size
+        index: Dict[int, int] = {}
+        segs: List[list] = []
+        paths: List[List[int]] = []
+        for qi, c in enumerate(self.candidates):
+            leaf = c.trie_node
+            path = []
+            parent = -1
+            for rep in leaf._reps + (leaf,):
+                i = index.get(id(rep))
+                if i is None:
+                    pages = self._seg_pages(rep)
+                    last = max(0, len(rep.tokens) - 1) if rep is leaf else len(rep.tokens)
+                    i = index[id(rep)] = len(segs)
+                    segs.append([pages, (len(pages) - 1) * ps + last, parent, [], []])
+                    if parent >= 0:
+                        segs[parent][4].append(i)
+                segs[i][3].append(qi)
+                path.append(i)
+                parent = i
+            paths.append(path)
+        return segs, paths
+
+    @staticmethod
+    def absorb_edges(segs, absorb):
+        """Top-down edge decisions (preparation.py:69-88 over segments):
+        ``absorb(nq_cur, nq_child, len_parent, len_child)`` True makes the
+        child's pass also read its parent's (effective) tokens, and the
+        parent's pass serve nq_child fewer queries.  Returns the set of
+        absorbing segments and the effective token count of every segment."""
+        nq = [len(s[3]) for s in segs]
+        teff = [s[1] for s in segs]
+        absorbed = set()
+        for k, s in enumerate(segs):
+            for ch in s[4]:
+                nch = len(segs[ch][3])
+                if absorb(nq[k], nch, teff[k], segs[ch][1]):
+                    absorbed.add(ch)
+                    nq[k] -= nch
+                    teff[ch] = segs[ch][1] + teff[k]
+        return absorbed, teff
+
+    def tree_levels(self, segs, paths, absorbed):
+        """Level arrays of a decomposition: a segment's pass reads its own
+        pages after those of the ancestors it absorbed and serves the
+        candidates below it that no absorbing child covers; a candidate's
+        passes along its path are its levels 0, 1, ...  Candidates served at
+        a level by one segment but not contiguous in candidate order get one
+        group per run; candidates without a pass at a level get empty
+        groups."""
+        ps = self.page_table.page_size
+        pages_eff: Dict[int, List[int]] = {}
+
+        def eff(k):
+            p = pages_eff.get(k)
+            if p is None:
+                p = segs[k][0]
+                if k in absorbed:
+                    p = eff(segs[k][2]) + p
+                pages_eff[k] = p
+            return p
+        per_level: List[Dict[int, List[int]]] = []
+        for qi, keys in enumerate(paths):
+            lv = 0
+            for j, k in enumerate(keys):
+                if j + 1 < len(keys) and keys[j + 1] in absorbed:
+                    continue
+                if lv == len(per_level):
+                    per_level.append({})
+                per_level[lv].setdefault(k, []).append(qi)
+                lv += 1
+        n = len(paths)
+        levels = []
+        for groups in per_level:
+            runs = []
+            for k, qs in groups.items():
+                start = prev = qs[0]
+                for q in qs[1:]:
+                    if q != prev + 1:
+                        runs.append((start, prev + 1, k))
+                        start = q
+                    prev = q
+                runs.append((start, prev + 1, k))
+            runs.sort()
+            qo, kvp, kvi, lpl = [0], [0], [], []
+            for q0, q1, k in runs:
+                if q0 > qo[-1]:                      # candidates without a pass here
+                    qo.append(q0); kvp.append(len(kvi)); lpl.append(0)
+                pages = eff(k)
+                tok = len(pages) * ps - (ps * len(segs[k][0]) - segs[k][1])
+                kvi.extend(pages)
+                kvp.append(len(kvi))
+                lpl.append(tok - (len(pages) - 1) * ps if pages else 0)
+                qo.append(q1)
+            if qo[-1] < n:
+                qo.append(n); kvp.append(len(kvi)); lpl.append(0)
+            levels.append((qo, kvp, kvi, lpl))
+        return levels
+
+    def tree_lists(self, absorb):
+        """Exact path attention as levels of shared passes (the decomposition of
+        FastTree's preparation, attention/fasttree/preparation.py:60-105, over
+        the cascade's segments instead of single pages): every candidate
+        attends each token of its path once (the flat strategy's result, own
+        newest token excluded); ``absorb`` decides each edge (see
+        ``absorb_edges``).  Returns [(qo, kv_indptr, kv_indices,
+        last_page_len)] per level."""
+        if not self.candidates:
+            return []
+        segs, paths = self.segment_tree()
+        absorbed, _ = self.absorb_edges(segs, absorb)
+        return self.tree_levels(segs, paths, absorbed)
+
     def query_token_ids(self) -> List[int]:
         return [c.trie_node.tokens[-1] if c.trie_node.tokens else 0 for c in self.candidates]
 

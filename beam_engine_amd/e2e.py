@@ -202,7 +202,9 @@ def run_e2e_bench(args):
         "config": {"workload": f"e2e beam search, Llama-3-8B shape, {kind} attention",
                    "requests": 8, "beam": 16, "prompt_len": 1024, "decode_steps": warmup + steps,
                    "layers": model.cfg.num_hidden_layers, "page_size": 16, "length_penalty": 1.0,
-                   "per_request_tokens_per_s": round(tok_s / 8, 2)},
+                   "per_request_tokens_per_s": round(tok_s / 8, 2),
+                   **({"picker_choices": {k: gen.picker.history.count(k) for k in sorted(set(gen.picker.history))}}
+                      if kind == "auto" and gen.picker is not None else {})},
         "roofline": {"bound": "hbm", "achieved": round(att["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(att["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,

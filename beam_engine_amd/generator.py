@@ -14,10 +14,15 @@ requests decoded together in one forward per step:
   with the step's fork copies in one launch.
 
 ``kernel_type``: "cascade" (per-level groups of the reference's
-get_cascade_input), "flat" (each candidate's whole path, the baseline) or
-"auto" (the cost-model picker chooses per step).  ``include_self`` False
-follows the reference's cascade convention (a query does not attend to the
-K/V it appends in the same step, beam_state.py:347-354).
+get_cascade_input), "flat" (each candidate's whole path, the baseline),
+"tree" (the path attention as shared passes over trie segments, each edge
+absorbed or split by the MI355X cost model, as FastTree's preparation decides
+them, attention/fasttree/preparation.py:60-105) or "auto" (per step, the
+cheaper of flat, fully split and tree under that model).  "flat", "tree" and
+"auto" give every candidate its path tokens exactly once; "cascade" keeps the
+reference's repetition of a shallow candidate's leaf group on deeper levels.
+``include_self`` False follows the reference's cascade convention (a query
+does not attend to the K/V it appends in the same step, beam_state.py:347-354).
 """
 
 from __future__ import annotations
@@ -39,8 +44,8 @@ class BatchedBeamSearch:
                  strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
                  temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False,
                  graphs: bool = False):
-        if kernel_type not in ("cascade", "flat", "auto"):
-            raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat' or 'auto'.")
+        if kernel_type not in ("cascade", "flat", "tree", "auto"):
+            raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat', 'tree' or 'auto'.")
         self.model = model
         self.pt = page_table
         self.beam_size = beam_size
@@ -82,18 +87,26 @@ class BatchedBeamSearch:
         return logits
 
     # ---------------------------------------------------------------- decode
-    def _plan(self, kind: str):
+    def _get_picker(self):
+        if self.picker is None:
+            from .picker import StrategyPicker
+            cfg = self.model.cfg
+            self.picker = StrategyPicker(cfg.num_attention_heads, cfg.num_key_value_heads, self.pt.page_size)
+        return self.picker
+
+    def _plan(self, kind: str, levels=None):
         m = self.model
         cfg = m.cfg
         st = self.state
-        if kind == "cascade":
-            levels = st._cascade_lists()
+        if kind != "flat" or levels is not None:
+            if levels is None:
+                levels = st._cascade_lists()
             if self.include_self:
-                raise NotImplementedError("include_self with cascade levels")
+                raise NotImplementedError("include_self with cascade or tree levels")
             w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
             w.plan([l[0] for l in levels], [l[1] for l in levels], [l[2] for l in levels], [l[3] for l in levels],
                    cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pt.page_size,
-                   causal=True, q_data_type=m.dtype)
+                   causal=kind == "cascade", q_data_type=m.dtype)
         else:
             kvp, kvi, lpl = st.flat_lists(self.include_self)
             w = self.flat
@@ -107,9 +120,13 @@ class BatchedBeamSearch:
         st = self.state
         n = len(st.candidates)
         kind = self.kernel_type
-        if kind == "auto":
-            kind = self.picker.choose(st) if self.picker is not None else "cascade"
-        w = self._plan(kind)
+        levels = None
+        if kind == "tree":
+            levels = st.tree_lists(self._get_picker().model.absorb)
+        elif kind == "auto":
+            plan = self._get_picker().choose(st)
+            kind, levels = plan.kind, plan.levels
+        w = self._plan(kind, levels)
         qids = st.query_token_ids()
         wp, wpos = st.write_locations()
         pos = st.position_ids()

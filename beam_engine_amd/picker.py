@@ -1,0 +1,195 @@
+"""Per-step strategy picker: a cost model of this build's decode attention on MI355X.
+
+The reference decides the shape of tree attention in FastTree's preparation
+(src/beam_engine/attention/fasttree/preparation.py:34-88): walking the trie top
+down, each child node either absorbs its parent's KV into its own pass
+(SplitQ: the child's queries read the parent's tokens again, the parent's pass
+loses them) or keeps a separate pass whose result is merged (SplitK), whichever
+of the two costs less under a padded-tile model Cmm with alpha 0.6, beta 0.3,
+gamma 0.1 fitted to its Triton kernel (metadata.py:12-17).  The reference fixes
+the strategy per generator (beam.py:20, 168-206) and has no flat strategy.
+
+Here the same top-down edge decision runs over the trie's segments (the
+cascade's groups: unbranched page chains) with costs of this build's kernels:
+the persistent streaming kernel prices a group by its 64-token tiles — per
+tile, by how many 16-row MFMA tiles the group's queries x GQA heads fill —
+and by its segment starts; short groups of few queries go to the tail pass,
+priced per 16-token chunk; every extra pass of a query costs one partial slot
+and its merge.  ``StrategyPicker.choose`` then compares the whole-step costs
+of the flat plan (every edge absorbed), the fully split plan and the greedy
+edge decision, and returns the cheapest.  All three attend each query to
+exactly the tokens of its path (the flat strategy's result), so the choice
+changes the time, not the output.
+
+The constants are microseconds per layer on one MI355X, fitted by
+``python -m beam_engine_amd.picker_fit`` from timed plans of the streaming
+kernel (least squares over a sweep of group shapes).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+from .beam_state import BeamState
+
+TILE_TOKENS = 64          # tokens per streaming-kernel tile
+SEG_ROWS = 64             # rows (queries x GQA heads) per streaming segment
+TAIL_TOKENS = 64          # tail pass: groups of at most this many tokens ...
+TAIL_QUERIES = 4          # ... and at most this many queries
+TAIL_CHUNK = 16
+
+
+@dataclass(frozen=True)
+class KernelCosts:
+    """Machine time (us per layer, the whole GPU) of one unit of work."""
+    tile_nt: Tuple[float, float, float, float] = (0.005995, 0.006132, 0.006983, 0.007661)
+    """one 64-token tile of one KV head, by 16-row MFMA tiles filled (1, 2, 3, 4)"""
+    seg: float = 0.012804           # a segment start (Q rows, epilogue) of one KV head
+    slot: float = 0.003339          # a partial slot of one (query, KV head) and its merge
+    tail: float = 0.001222          # a 16-token tail chunk of one (query, KV head)
+    fixed: float = 8.559           # both launches, prologue and the merge of a step
+
+
+MI355X = KernelCosts()
+
+
+class CostModel:
+    """Cost of attention groups for one head configuration and page size."""
+
+    def __init__(self, num_qo_heads: int, num_kv_heads: int, page_size: int, costs: KernelCosts = MI355X):
+        self.hkv = num_kv_heads
+        self.g = num_qo_heads // num_kv_heads
+        self.tail_ok = page_size % 16 == 0 and self.g <= 16
+        self.c = costs
+        self._memo: Dict[Tuple[int, int], float] = {}
+
+    def group(self, nq: int, tokens: int) -> float:
+        """One group of nq queries over `tokens` tokens, all KV heads."""
+        if nq <= 0 or tokens <= 0:
+            return 0.0
+        key = (nq, tokens)
+        v = self._memo.get(key)
+        if v is None:
+            if len(self._memo) > 1 << 16:
+                self._memo.clear()
+            v = self._memo[key] = self._group(nq, tokens)
+        return v
+
+    def _group(self, nq: int, tokens: int) -> float:
+        c = self.c
+        if self.tail_ok and tokens <= TAIL_TOKENS and nq <= TAIL_QUERIES:
+            return nq * self.hkv * math.ceil(tokens / TAIL_CHUNK) * c.tail
+        tiles = math.ceil(tokens / TILE_TOKENS)
+        rows = nq * self.g
+        cost = 0.0
+        while rows > 0:
+            r = min(rows, SEG_ROWS)
+            cost += tiles * c.tile_nt[min(4, math.ceil(r / 16)) - 1] + c.seg
+            rows -= r
+        return cost * self.hkv
+
+    def slots(self, nq: int) -> float:
+        return nq * self.hkv * self.c.slot
+
+    def absorb(self, nq_cur: int, nq_child: int, len_parent: int, len_child: int) -> bool:
+        """Edge decision (preparation.py:80-85 with this model): True when the
+        child should read the parent's tokens in its own pass."""
+        split = self.group(nq_cur, len_parent) + self.group(nq_child, len_child) + self.slots(nq_child)
+        absorb = self.group(nq_cur - nq_child, len_parent) + self.group(nq_child, len_child + len_parent)
+        return absorb < split
+
+
+@dataclass
+class Plan:
+    kind: str                       # "flat", "split" or "tree"
+    levels: List[tuple]             # [(qo_indptr, kv_indptr, kv_indices, last_page_len)] per level
+    cost: float
+    costs: Dict[str, float] = field(default_factory=dict)   # every option's modelled cost
+
+
+def decomposition_cost(model: CostModel, segs, paths, absorbed, teff) -> float:
+    """Modelled cost of one decomposition of a segment tree: each segment's
+    pass over its effective tokens for the candidates it serves, plus a slot
+    for every pass of a candidate beyond its first."""
+    total = model.c.fixed
+    served = [len(s[3]) for s in segs]
+    for k in absorbed:
+        served[segs[k][2]] -= len(segs[k][3])
+    for k, s in enumerate(segs):
+        total += model.group(served[k], teff[k])
+    extra = 0
+    for p in paths:
+        passes = sum(1 for j, k in enumerate(p) if teff[k] > 0 and not (j + 1 < len(p) and p[j + 1] in absorbed))
+        extra += max(0, passes - 1)
+    return total + model.slots(extra)
+
+
+def plan_cost(model: CostModel, levels: List[tuple], page_size: int) -> Tuple[float, int]:
+    """Modelled cost of level arrays (any strategy): their groups, plus a slot
+    for every query pass beyond the first.  Returns (cost, groups)."""
+    total = model.c.fixed
+    passes: Dict[int, int] = {}
+    groups = 0
+    for qo, kvp, _, lpl in levels:
+        for j in range(len(qo) - 1):
+            npg = kvp[j + 1] - kvp[j]
+            n = 0 if npg == 0 else (npg - 1) * page_size + lpl[j]
+            if n <= 0 or qo[j + 1] <= qo[j]:
+                continue
+            groups += 1
+            total += model.group(qo[j + 1] - qo[j], n)
+            for q in range(qo[j], qo[j + 1]):
+                passes[q] = passes.get(q, 0) + 1
+    total += sum(model.slots(1) * (p - 1) for p in passes.values() if p > 1)
+    return total, groups
+
+
+class StrategyPicker:
+    """Chooses, per decode step, how the exact path attention of every
+    candidate is decomposed: flat (every edge absorbed: one pass per
+    candidate over its path), split (no edge absorbed: one pass per trie
+    segment, merged), or tree (each edge by ``CostModel.absorb``).  The
+    options are costed on the segment tree; only the chosen one is laid out
+    as level arrays."""
+
+    def __init__(self, num_qo_heads: int, num_kv_heads: int, page_size: int, costs: KernelCosts = MI355X,
+                 candidates=("flat", "split", "tree")):
+        self.model = CostModel(num_qo_heads, num_kv_heads, page_size, costs)
+        self.page_size = page_size
+        self.candidates = tuple(candidates)
+        self.last: Optional[Plan] = None
+        self.history: List[str] = []
+
+    def _options(self, state: BeamState):
+        segs, paths = state.segment_tree()
+        m = self.model
+        out = {}
+        for kind in self.candidates:
+            if kind == "flat":              # every edge absorbed: one pass per candidate over its path
+                absorbed = set(k for k, sg in enumerate(segs) if sg[2] >= 0)
+                cum = [0] * len(segs)
+                for k, sg in enumerate(segs):
+                    cum[k] = sg[1] + (cum[sg[2]] if sg[2] >= 0 else 0)
+                cost = m.c.fixed + sum(m.group(1, cum[p[-1]]) for p in paths)
+            elif kind == "split":           # no edge absorbed: one pass per segment
+                absorbed = set()
+                cost = decomposition_cost(m, segs, paths, absorbed, [sg[1] for sg in segs])
+            else:
+                absorbed, teff = state.absorb_edges(segs, m.absorb)
+                cost = decomposition_cost(m, segs, paths, absorbed, teff)
+            out[kind] = (cost, absorbed)
+        return segs, paths, out
+
+    def costs(self, state: BeamState) -> Dict[str, float]:
+        return {k: v[0] for k, v in self._options(state)[2].items()}
+
+    def choose(self, state: BeamState) -> Plan:
+        segs, paths, opts = self._options(state)
+        kind = min(opts, key=lambda k: opts[k][0])
+        plan = Plan(kind, state.tree_levels(segs, paths, opts[kind][1]), opts[kind][0],
+                    {k: v[0] for k, v in opts.items()})
+        self.last = plan
+        self.history.append(kind)
+        return plan

@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="e2e",
                     choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5"])
-    ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat"])
+    ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat", "tree", "auto"],
+                    help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true", help="e2e: launch every op eagerly (no HIP graphs)")
@@ -159,6 +160,9 @@ def main():
         print(json.dumps({"error": "no HIP device visible"}))
         return 1
     if args.workload.startswith("attn-"):
+        if args.strategy not in ("cascade", "flat"):
+            print(json.dumps({"error": "attention workloads take --strategy cascade or flat"}))
+            return 2
         result, wl = attention_workload(args)
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = cpu_baseline_attention(wl, result["roofline"]["bytes_per_launch"])

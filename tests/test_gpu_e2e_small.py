@@ -21,7 +21,7 @@ def say(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("kind", ["cascade", "flat"])
+@pytest.mark.parametrize("kind", ["cascade", "flat", "tree", "auto"])
 def test_tiny_llama_beam_search_matches_oracle(kind):
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
