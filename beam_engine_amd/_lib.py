@@ -63,7 +63,7 @@ class BeAttnPlanInfo(ctypes.Structure):
         ("qo_bytes", ctypes.c_int64),
         ("flops", ctypes.c_double),
     ] + [(n, ctypes.c_int32) for n in ("num_wg", "off_wg", "off_records", "off_record_slots",
-                                              "num_tails", "off_tails")]
+                                              "num_tails", "off_tails", "tail_waves")]
 
 
 EXPORTS = (

@@ -60,7 +60,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kLoadsPerTile = 4;              // direct loads per wave per tile (2 K + 2 V row blocks)
 constexpr int kSegCost = 4;                   // planner cost of a segment start, in quarter tiles
 constexpr int kQuarterTiles = 4;              // single-row-tile segments this long split tokens 4 ways
-constexpr int kTailTokens = 64;               // groups this short with few queries go to the tail pass
+constexpr int kTailTokens = 128;              // groups this short with few queries go to the tail pass
 constexpr int kTailQueries = 4;
 constexpr int kTailChunks = 64;               // 16-token tail chunks per query (one per lane)
 constexpr int kRecWords = 8;                  // int32 words per merge record
@@ -584,39 +584,73 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   }
 }
 
-// One wave per record (query, KV head).  The tail pass first attends the
-// record's tail chunks — 16 tokens of one page each, from the query's short
-// groups — as one online softmax (a token in two groups counts twice, as two
-// separately merged groups would count it): K and V rows come straight from
-// global memory into this wave's LDS area, then the streaming kernel's tile
-// step (S^T = K Q^T on v_mfma_f32_16x16x32, P.V on 16x16x16, rows = the g
-// query heads).  Its normalised output and lse join the record's partial
-// slots in a log-sum-exp combination with a running max; a record with
-// neither writes o = 0 and lse = -inf.
-template <typename T>
+// WPR waves per record (query, KV head), 4 / WPR records per workgroup.  The
+// tail pass first attends the record's tail chunks — 16 tokens of one page
+// each, from the query's short groups — as one online softmax (a token in two
+// groups counts twice, as two separately merged groups would count it): wave
+// w of a record takes chunks w, w + WPR, ...; K and V rows go from global
+// memory through the wave's LDS area into the streaming kernel's tile step
+// (S^T = K Q^T on v_mfma_f32_16x16x32, P.V on 16x16x16, rows = the g query
+// heads).  The record's waves' states and its partial slots are then combined
+// by log-sum-exp with a running max, one (head, 4 columns) entry per thread;
+// the first 8 slots of a thread's first entry are loaded before the tail pass
+// so that their latency hides under it.  A record with neither tail chunks nor
+// slots writes o = 0 and lse = -inf.
+template <typename T, int WPR>
 __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
-  constexpr int kArea = 2 * kKvBytes / 4 + 256;      // K + V chunk (8 KB), then lse of the tail
-  __shared__ __attribute__((aligned(16))) unsigned char tl_lds[4][kArea];
-  const int wv = rfl(threadIdx.x >> 6);
-  const int e = blockIdx.x * 4 + wv;
-  const int lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
-  const int live = m.live ? *m.live : m.n_recs;
-  if (e >= live) return;
-  const int32_t* rp = m.recs + (int64_t)e * kRecWords;
-  const int qi = rfl(rp[0]), h = rfl(rp[1]), s0 = rfl(rp[2]), n = rfl(rp[3]), t0 = rfl(rp[4]), nt = rfl(rp[5]);
-  const int g = m.g;
+  constexpr int RPB = 4 / WPR;                 // records per workgroup
+  constexpr int RT = 64 * WPR;                 // threads per record
   constexpr int C4 = kD / 4;
-  unsigned char* kt = tl_lds[wv];
-  unsigned char* vt = kt + 4096;
-  float* vs_o = reinterpret_cast<float*>(tl_lds[wv]);           // tail result [g][kD] (g <= 16)
-  float* vs_lse = reinterpret_cast<float*>(tl_lds[wv] + 8192);
+  __shared__ __attribute__((aligned(16))) unsigned char tl_lds[4][2 * 4096];   // per wave: K and V chunk
+  __shared__ float st_m[4][16], st_l[4][16];
+  const int tid = threadIdx.x, wv = rfl(tid >> 6);
+  const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
+  const int rb = wv / WPR, sw = wv - rb * WPR;  // record of the workgroup, wave within the record
+  const int rtid = tid - rb * RT;
+  const int e = blockIdx.x * RPB + rb;
+  const int live = m.live ? *m.live : m.n_recs;
+  if (WPR == 4 && e >= live) return;           // (one record per workgroup: uniform)
+  const bool act = e < live;
+  int qi = 0, h = 0, s0 = 0, n = 0, t0 = 0, nt = 0;
+  if (act) {
+    const int32_t* rp = m.recs + (int64_t)e * kRecWords;
+    qi = rfl(rp[0]); h = rfl(rp[1]); s0 = rfl(rp[2]); n = rfl(rp[3]); t0 = rfl(rp[4]);
+    nt = min(rfl(rp[5]), kTailChunks);
+  }
+  const int g = m.g;
   const int32_t* slots = m.rec_slots + s0;
-  // lane k holds tail entry k and slot id k (both loads issued before anything waits)
+  // every wave holds all tail entries and the first 64 slot ids, lane k entry k
   const int2 ent = lane < nt ? m.tails[t0 + lane] : int2{0, 0};
   const int sid = lane < n ? slots[lane] : -1;
 
+  auto load_batch = [&](int hh, int d4, int k0, int (&sl)[8], float (&lv)[8], v4f (&ov)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      sl[j] = (k0 + j >= n) ? -1 : (k0 + j < 64) ? __builtin_amdgcn_readlane(sid, k0 + j) : slots[k0 + j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (sl[j] >= 0) {
+        const int64_t s = (int64_t)sl[j] * g + hh;
+        lv[j] = m.part_lse[s];
+        ov[j] = *reinterpret_cast<const v4f*>(m.part_o + s * kD + 4 * d4);
+      } else {
+        lv[j] = -INFINITY;
+        ov[j] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  // prefetch: the first slot batch of this thread's first entry
+  const bool has0 = act && rtid < g * C4;
+  int sl0[8];
+  float lv0[8];
+  v4f ov0[8];
+  load_batch(has0 ? rtid / C4 : 0, has0 ? rtid % C4 : 0, has0 ? 0 : n, sl0, lv0, ov0);
+
+  float* part = reinterpret_cast<float*>(&tl_lds[0][0]);       // after the tail pass: [4][16][kD]
   if (nt > 0) {
     typedef int v4i __attribute__((ext_vector_type(4)));
+    unsigned char* kt = tl_lds[wv];
+    unsigned char* vt = kt + 4096;
     const T* kvp = reinterpret_cast<const T*>(m.kv);
     const int ps = m.page_size, hkv = m.hkv;
     const int64_t plane = (int64_t)ps * hkv * kD;
@@ -651,8 +685,8 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
     v4f o_acc[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-    load(0);
-    for (int c = 0; c < nt; ++c) {
+    if (sw < nt) load(sw);
+    for (int c = sw; c < nt; c += WPR) {
       const int valid = __builtin_amdgcn_readlane(ent.y, c) >> 16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -660,50 +694,68 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
         *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[i];
         *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[i];
       }
-      if (c + 1 < nt) load(c + 1);
+      if (c + WPR < nt) load(c + WPR);
       tile_compute<T, 1, 8>(kt, vt, qf, koff, voff8, 0, valid, lg, m.scale_log2, m_run, l_run, o_acc);
     }
     float l = l_run;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    // lane holds O^T[d = 16 mt + 4 lg + i][row lc]; every tail chunk has a valid token, so l > 0
+    if (WPR > 1) __syncthreads();          // every wave of the record is done with its K/V area
+    // lane holds O^T[d = 16 mt + 4 lg + i][row lc] (unnormalised, log2 domain); a wave's
+    // area is its own K/V area, so one wave per record needs no barrier
     if (lc < g) {
-      const float inv = 1.f / l;
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4f*>(vs_o + lc * kD + 16 * mt + 4 * lg) = o_acc[mt] * inv;
-      if (lg == 0) vs_lse[lc] = (m_run + log2f(l)) * 0.69314718055994531f;
+      for (int mt = 0; mt < 8; ++mt)
+        *reinterpret_cast<v4f*>(part + (wv * 16 + lc) * kD + 16 * mt + 4 * lg) = o_acc[mt];
+      if (lg == 0) {
+        st_m[wv][lc] = m_run;
+        st_l[wv][lc] = l;
+      }
     }
+    if (WPR > 1) __syncthreads();
   }
+  if (!act) return;
 
   T* out = reinterpret_cast<T*>(m.out) + (int64_t)qi * m.o_sn;
-#pragma unroll 2
-  for (int c = lane; c < g * C4; c += 64) {
+  for (int c = rtid; c < g * C4; c += RT) {
     const int hh = c / C4, d4 = c - hh * C4;
     const int head = h * g + hh;
     float M = -INFINITY, z = 0.f;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     if (nt > 0) {
-      M = vs_lse[hh];
+      float mw = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < WPR; ++w) mw = fmaxf(mw, st_m[rb * WPR + w][hh]);
+      float zt = 0.f;
+      v4f at = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < WPR; ++w) {
+        const int ww = rb * WPR + w;
+        const float mk = st_m[ww][hh];
+        if (mk != -INFINITY) {
+          const float sc = __builtin_amdgcn_exp2f(mk - mw);
+          zt += st_l[ww][hh] * sc;
+          at += *reinterpret_cast<const v4f*>(part + (ww * 16 + hh) * kD + 4 * d4) * sc;
+        }
+      }
+      // the tail chunks hold a valid token, so zt > 0
+      M = (mw + log2f(zt)) * 0.69314718055994531f;
       z = 1.f;
-      acc = *reinterpret_cast<const v4f*>(vs_o + hh * kD + 4 * d4);
+      acc = at * (1.f / zt);
     }
     for (int k0 = 0; k0 < n; k0 += 8) {
       int sl[8];
       float lv[8];
       v4f ov[8];
+      if (c == rtid && k0 == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        sl[j] = (k0 + j >= n) ? -1 : (k0 + j < 64) ? __builtin_amdgcn_readlane(sid, k0 + j) : slots[k0 + j];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (sl[j] >= 0) {
-          const int64_t s = (int64_t)sl[j] * g + hh;
-          lv[j] = m.part_lse[s];
-          ov[j] = *reinterpret_cast<const v4f*>(m.part_o + s * kD + 4 * d4);
-        } else {
-          lv[j] = -INFINITY;
-          ov[j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 8; ++j) {
+          sl[j] = sl0[j];
+          lv[j] = lv0[j];
+          ov[j] = ov0[j];
         }
+      } else {
+        load_batch(hh, d4, k0, sl, lv, ov);
       }
       float mx = M;
 #pragma unroll
@@ -958,6 +1010,13 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->off_record_slots = (int32_t)off_rslots;
   info->num_tails = (int32_t)n_tails;
   info->off_tails = (int32_t)off_tails;
+  {
+    // chunks per record: spread a record over four waves when there are fewer
+    // records than SIMDs and their tails take several chunks each
+    int64_t chunks = 0;
+    for (int64_t r = 0; r < n_recs; ++r) chunks += recs[r * kRecWords + 5];
+    info->tail_waves = (n_recs > 0 && n_recs <= 4 * (int64_t)W && chunks >= 4 * n_recs) ? 4 : 1;
+  }
   return BE_OK;
 }
 
@@ -1004,9 +1063,17 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
     m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse;
     m.n_recs = info->grid_merge; m.g = g; m.hq = hq; m.hkv = hkv; m.page_size = ps;
     m.scale_log2 = sm_scale * 1.4426950408889634f;
-    const int grid = (int)ceil_div(info->grid_merge, 4);
-    if (info->dtype == BE_BF16) tail_merge_kernel<bf16_t><<<grid, 256, 0, st>>>(m);
-    else tail_merge_kernel<f16_t><<<grid, 256, 0, st>>>(m);
+    // four waves per record where records are few and their tails long enough to
+    // share out; one wave per record (four records per workgroup) otherwise
+    const bool wide = info->tail_waves == 4;
+    const int grid = wide ? info->grid_merge : (int)ceil_div(info->grid_merge, 4);
+    if (info->dtype == BE_BF16) {
+      if (wide) tail_merge_kernel<bf16_t, 4><<<grid, 256, 0, st>>>(m);
+      else tail_merge_kernel<bf16_t, 1><<<grid, 256, 0, st>>>(m);
+    } else {
+      if (wide) tail_merge_kernel<f16_t, 4><<<grid, 256, 0, st>>>(m);
+      else tail_merge_kernel<f16_t, 1><<<grid, 256, 0, st>>>(m);
+    }
     BE_HIP_CHECK(hipGetLastError());
   }
   return BE_OK;

@@ -36,7 +36,7 @@ from .beam_state import BeamState
 
 TILE_TOKENS = 64          # tokens per streaming-kernel tile
 SEG_ROWS = 64             # rows (queries x GQA heads) per streaming segment
-TAIL_TOKENS = 64          # tail pass: groups of at most this many tokens ...
+TAIL_TOKENS = 128         # tail pass: groups of at most this many tokens ...
 TAIL_QUERIES = 4          # ... and at most this many queries
 TAIL_CHUNK = 16
 

@@ -172,12 +172,13 @@ typedef struct be_attn_plan_info {
   int32_t off_records;     /* [grid_merge][8]: query, KV head, first slot entry, slots,
                               first tail entry, tail entries, 0, 0                  */
   int32_t off_record_slots;/* slot ids of every record                             */
-  /* Groups of at most 64 tokens and at most 4 queries (page_size a multiple of
+  /* Groups of at most 128 tokens and at most 4 queries (page_size a multiple of
    * 16) skip the persistent kernel: the merge kernel attends them per (query,
    * KV head) before it combines the slots.  Tail entries are 16-token chunks,
    * [num_tails][2]: page id, in-page token offset | valid tokens << 16. */
   int32_t num_tails;
   int32_t off_tails;
+  int32_t tail_waves;      /* waves per record in the tail-and-merge kernel: 1 or 4 */
 } be_attn_plan_info;
 
 /* be_attn_plan (host only): validates the levels against num_queries,

@@ -297,7 +297,9 @@ def test_stream_plan_balances_tiles_across_workgroups(cus):
     kvp1 = list(range(0, 33 * suf, suf))
     kvi1 = list(range(2 * pre, 2 * pre + 32 * suf))
     levels = [(qo0, kvp0, kvi0, [16, 16]), (qo1, kvp1, kvi1, [16] * 32)]
-    rc, info, buf, _lib, L = plan(levels, nq=32, hq=hq, hkv=hkv, page=page, num_pages=2 * pre + 32 * suf, cus=cus)
+    # (tail pass off: the 128-token suffixes would otherwise leave the persistent kernel)
+    rc, info, buf, _lib, L = plan(levels, nq=32, hq=hq, hkv=hkv, page=page, num_pages=2 * pre + 32 * suf, cus=cus,
+                                  flags=8)
     assert rc == 0, L.be_last_error()
     wg, segs, recs, rslots = check_stream_plan(levels, 32, hq, hkv, page, info, buf)
     assert info.num_wg == cus
