@@ -348,7 +348,7 @@ def test_stream_plan_falls_back_to_tile_kernel_when_a_workgroup_overflows():
     assert rc == 0 and info.kernel == 1
 
 
-def e2e_like_levels(nreq=2, beams=4, pre_pages=8, page=16, seed=0):
+def e2e_like_levels(nreq=2, beams=4, pre_pages=16, page=16, seed=0):
     """Request prefixes shared by their beams, then single-query levels of a few tokens (the
     shape of a beam trie that re-converges every step)."""
     rng = np.random.default_rng(seed)

@@ -137,7 +137,9 @@ def test_cost_model_prices_tail_stream_and_rows():
     m = CostModel(32, 8, 16, c)
     assert m.group(0, 100) == 0 and m.group(3, 0) == 0
     assert m.group(2, 40) == 2 * 8 * 3 * 0.25                 # tail: 3 chunks x 2 queries x 8 heads
-    assert m.group(1, 65) == 8 * (2 * 1.0 + 10.0)             # 4 rows: one 16-row tile, 2 tiles
+    assert m.group(1, 65) == 8 * 5 * 0.25                     # 65 tokens, one query: 5 tail chunks
+    assert m.group(5, 65) == 8 * (2 * 2.0 + 10.0)             # 20 rows: two 16-row tiles, 2 tiles
+    assert m.group(1, 129) == 8 * (3 * 1.0 + 10.0)            # 4 rows: one 16-row tile, 3 tiles
     assert m.group(16, 64) == 8 * (4.0 + 10.0)                # 64 rows: a full segment
     assert m.group(20, 64) == 8 * (4.0 + 10.0 + 1.0 + 10.0)   # 80 rows: 64 + 16
     assert CostModel(32, 8, 8, c).group(2, 40) == 8 * (1.0 + 10.0)   # page 8: no tail pass
