@@ -52,8 +52,8 @@ template <> __device__ __forceinline__ uint16_t pack16<f16_t>(float x) {
 
 // ---------------------------------------------------------------- streaming kernel
 // True when the streaming kernel serves this shape (16-bit storage, head_dim
-// 128, GQA group <= 64).
-bool stream_eligible(int dtype, int head_dim, int group, int flags);
+// 128, GQA group <= 64, page size a multiple of 16).
+bool stream_eligible(int dtype, int head_dim, int group, int page_size, int flags);
 
 // Writes the streaming plan for `groups` (validated by attn_plan, pages
 // concatenated level by level into total_pages entries) into out[0..cap) and

@@ -6,19 +6,22 @@
 // reference (models/modeling_llama.py:321-367, 732-755), but scheduled for an
 // HBM-bound decode step on MI355X:
 //
-//  * One workgroup (4 waves) per CU.  The planner cuts the work — (query tile
+//  * One workgroup (8 waves) per CU.  The planner cuts the work — (query tile
 //    of <= 64 rows) x (KV head) x (64-token tiles) — into one contiguous run per
-//    workgroup with equal bytes, splitting work items at tile boundaries where
-//    a run ends.  A piece of a work item inside one run is a segment.
-//  * Every asynchronous transfer is a direct global->LDS load
-//    (global_load_lds_dwordx4 / _dword): K and V tiles, the Q rows of a
-//    segment and the page ids of a tile.  Nothing in the loop waits on a
-//    VGPR load, so the loads of the next two tiles stay in flight across
-//    segment boundaries; waits are explicit vmcnt counts (vmcnt retires in
-//    issue order) followed by a bare s_barrier.
-//  * Pipeline: 3 stages of {K tile 16 KB, V tile 16 KB, Q slot 16 KB}; page ids
-//    run four tiles ahead in a 4-slot LDS ring.  In iteration n: wait for tile
-//    n, barrier, issue K/V/Q of tile n + 2 and page ids of tile n + 4, compute n.
+//    workgroup with equal cost, splitting work items at tile boundaries where a
+//    run ends.  A piece of a work item inside one run is a segment.  Groups of
+//    at most 128 tokens and 4 queries skip this kernel: the tail-and-merge
+//    kernel attends them per (query, KV head).
+//  * K, V and the Q rows of a segment move by direct global->LDS loads
+//    (global_load_lds_dwordx4).  Nothing in the loop waits on a VGPR load, so
+//    the loads of the next two tiles stay in flight across segment
+//    boundaries; waits are explicit vmcnt counts (vmcnt retires in issue
+//    order) followed by a bare s_barrier.  The page size is a multiple of 16,
+//    so each wave's 8 rows of a tile lie in one page whose id is a scalar
+//    load, issued an iteration early.
+//  * Pipeline: 3 stages of {K tile 16 KB, V tile 16 KB, Q slot 16 KB}.  In
+//    iteration n: wait for tile n, barrier, issue K/V/Q of tile n + 2,
+//    compute n.
 //  * K, V and Q rows are 256-byte rows whose 16-byte chunks sit XOR-swizzled by
 //    row (the swizzle is applied by choosing each lane's global address, since
 //    a direct load writes lane l's 16 bytes at LDS base + 16 l).
@@ -28,9 +31,9 @@
 //    tokens of one head_dim column) is read from the row-major V tile with
 //    ds_read_b64_tr_b16: in each 16-lane group, lane r supplies the address of
 //    V[t0 + r/4][d0 + 4 (r%4) .. +3] and receives V[t0 + j][d0 + r], j = 0..3.
-//  * Wave w owns rows 16w..16w+15 of a segment (query x GQA head); waves
-//    without rows only load.  Online softmax in the log2 domain, fp32
-//    accumulation, natural-log lse at the boundary.
+//  * Waves split a segment's rows (16-row MFMA tiles), tokens and head_dim by
+//    the segment's row count (modes below); online softmax in the log2
+//    domain, fp32 accumulation, natural-log lse at the boundary.
 //  * A (query, KV head) covered by one segment is written as the final
 //    output; otherwise each segment writes a partial (o, lse) slot and a
 //    merge record combines the slots of the (query, KV head).
@@ -49,7 +52,6 @@ namespace stream {
 constexpr int kD = 128;                       // head_dim served
 constexpr int kTok = 64;                      // tokens per tile
 constexpr int kStages = 3;
-constexpr int kPageSlots = 4;                 // page ids run kPageSlots tiles ahead of compute
 constexpr int kSegRows = 64;                  // rows per segment: 4 waves x 16
 constexpr int kMaxSegs = 224;                 // segments per workgroup (LDS table)
 constexpr int kKvBytes = kTok * kD * 2;       // one K (or V) tile: 16 KB
@@ -283,32 +285,22 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char st_lds[kStages * kStageBytes];
-  __shared__ StreamSeg seg_lds[kMaxSegs];
-  __shared__ __attribute__((aligned(16))) int pg_lds[kPageSlots][64];
-
+// The loop of one workgroup over its segments' tiles.  FM >= 0: every segment
+// of the workgroup takes wave-role mode FM (the planner marks such
+// workgroups), so the per-tile mode dispatch folds away; FM < 0: mode per
+// segment.
+template <typename T, int FM>
+__device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
+                                            int n_segs, int n_tiles) {
   const int tid = threadIdx.x;
   const int w = rfl(tid >> 6);                        // wave index (uniform)
   const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
-  const int4 wi = a.wg[blockIdx.x];
-  const int n_segs = rfl(wi.y), n_tiles = rfl(wi.z);
-  if (n_tiles <= 0) return;
-  {
-    const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
-    int* dst = reinterpret_cast<int*>(seg_lds);
-    for (int i = tid; i < n_segs * 8; i += kThreads) dst[i] = src[i];
-  }
-  __syncthreads();
-
   const int ps = a.page_size, g = a.g, hkv = a.hkv;
   const int pshift = a.page_shift;
   auto page_of = [&](int tok) { return pshift >= 0 ? (tok >> pshift) : (tok / ps); };
   const T* kv = reinterpret_cast<const T*>(a.kv);
   const int64_t plane = (int64_t)ps * hkv * kD;      // K plane -> V plane of a page (elements)
   const uint32_t st0 = lds_addr(st_lds);
-  const bool fast_pages = (ps & 15) == 0;            // a wave's 8 rows of a full tile share a page
   const float scale = a.scale_log2;
 
   // per-lane LDS offsets (bytes) of the MFMA operand reads, within a 16-token
@@ -327,7 +319,9 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
     voff1[0] = vcol(w);
   }
   // this wave loads rows 8w..8w+7 of every tile (two 1 KB loads of 4 rows for
-  // K and for V); per-lane byte offsets inside the page for the fast path
+  // K and for V).  The page size is a multiple of 16 and tiles start at a
+  // multiple of 64 tokens, so the 8 rows lie in one page: one page id (a
+  // scalar load) and per-lane row offsets from the wave's first row.
   uint32_t doff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -336,67 +330,50 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   }
 
   // cursors: segment index, tile of the segment and the segment's record, for
-  // the page-id loads, the K/V/Q loads and the compute
-  int p_s = 0, p_t = 0, l_s = 0, l_t = 0, c_s = 0, c_t = 0;
-  SegReg p_sg = seg_reg(seg_lds[0]), l_sg = p_sg, c_sg = p_sg;
+  // the K/V/Q loads and for the compute
+  int l_s = 0, l_t = 0, c_s = 0, c_t = 0;
+  SegReg l_sg = seg_reg(seg_lds[0]), c_sg = l_sg;
   auto advance = [&](int& si, int& ti, SegReg& sg) {
     if (++ti == sg.n_tiles) {
       ti = 0;
       if (++si < n_segs) sg = seg_reg(seg_lds[si]);
     }
   };
-
-  // page ids of tile m (page cursor) -> pg_lds[m % kPageSlots][0..]; wave 0
-  // loads them.  Returns this wave's number of loads.
-  auto issue_pages = [&](int m) -> int {
-    int ops = 0;
-    if (w == 0) {
-      const int tok0 = p_sg.tok_begin + p_t * kTok;
-      const int valid = min(kTok, p_sg.tok_count - p_t * kTok);
-      const int first = page_of(tok0);
-      const int span = page_of(tok0 + valid - 1) - first;
-      const int idx = p_sg.page_begin + first + min(lane, span);
-      dma4(a.pages + idx, lds_addr(&pg_lds[m & (kPageSlots - 1)][0]));
-      ops = 1;
-    }
-    advance(p_s, p_t, p_sg);
-    return ops;
+  // the page id of this wave's rows of the next tile to load (load cursor);
+  // read before the wait of an iteration so that its latency hides there
+  auto page_id = [&]() -> int {
+    const int valid = min(kTok, l_sg.tok_count - l_t * kTok);
+    const int t8 = l_sg.tok_begin + l_t * kTok + min(8 * w, valid - 1);
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_t;   // scalar (constant) loads
+    return ((const_i32_t)(uintptr_t)a.pages)[rfl(l_sg.page_begin + page_of(t8))];
   };
 
-  // Loads of tile m (load cursor) into stage st: the Q rows now when the tile
-  // starts a segment; the K/V rows are prepared here and issued by dma(j).
-  bool kv_pending = false, kv_fast = false;
+  // Loads of the next tile (load cursor) into stage st: the Q rows now when the
+  // tile starts a segment; the K/V rows are prepared here and issued by dma(j).
+  bool kv_pending = false;
   uint64_t kv_kbase = 0, kv_vbase = 0;
-  const T* kv_src[2] = {nullptr, nullptr};
+  uint32_t kv_off[2] = {0, 0};
   uint32_t kv_lds = 0;
-  auto prep_tile = [&](int m, int st) -> int {
+  auto prep_tile = [&](int st, int page) -> int {
     const SegReg& sg = l_sg;
     const uint32_t stage = st0 + (uint32_t)(st * kStageBytes);
-    const int tok0 = sg.tok_begin + l_t * kTok;
     const int valid = min(kTok, sg.tok_count - l_t * kTok);
-    const int first = page_of(tok0);
-    const int* pg = pg_lds[m & (kPageSlots - 1)];
+    const int r0 = min(8 * w, valid - 1);             // rows past the end re-read the last token
+    const int t8 = sg.tok_begin + l_t * kTok + r0;
+    const int s0 = t8 - page_of(t8) * ps;
     kv_pending = true;
     kv_lds = stage + (2 * w) * 1024;
-    kv_fast = fast_pages && valid == kTok;
-    if (kv_fast) {
-      // rows 8w..8w+7 lie in one page: SGPR page base + per-lane row offsets
-      const int t8 = tok0 + 8 * w;
-      const int pi = page_of(t8);
-      const int page = rfl(pg[pi - first]);
-      const int s0 = t8 - pi * ps;
-      kv_kbase = reinterpret_cast<uint64_t>(kv) +
-                 (uint64_t)(((((int64_t)page * 2) * ps + s0) * hkv + sg.head) * kD * 2);
-      kv_vbase = kv_kbase + (uint64_t)(plane * 2);
+    kv_kbase = reinterpret_cast<uint64_t>(kv) + (uint64_t)(((((int64_t)page * 2) * ps + s0) * hkv + sg.head) * kD * 2);
+    kv_vbase = kv_kbase + (uint64_t)(plane * 2);
+    if (8 * w + 8 <= valid) {
+      kv_off[0] = doff[0];
+      kv_off[1] = doff[1];
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int row = 8 * w + 4 * i + lg;
-        const int tok = tok0 + (row < valid ? row : 0);  // rows past the end re-read a valid token
-        const int pi = page_of(tok);
-        const int page = pg[pi - first];
-        kv_src[i] = kv + ((((int64_t)page * 2) * ps + (tok - pi * ps)) * hkv + sg.head) * kD +
-                    ((lc ^ (row & 15)) << 3);
+        const int r = 4 * i + lg;
+        const int rel = min(8 * w + r, valid - 1) - r0;
+        kv_off[i] = (uint32_t)(((int64_t)rel * hkv * kD + ((lc ^ (8 * (w & 1) + r)) << 3)) * 2);
       }
     }
     int ops = kLoadsPerTile;
@@ -416,38 +393,25 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
     advance(l_s, l_t, l_sg);
     return ops;
   };
-  // load j of the prepared tile: K rows 0..3 (j = 0), V rows 0..3, K rows 4..7, V rows 4..7
-  auto dma = [&](int j) {
-    if (!kv_pending) return;
-    const int i = j >> 1, v = j & 1;
-    const uint32_t dst = kv_lds + i * 1024 + v * kKvBytes;
-    if (kv_fast) dma16_sv(v ? kv_vbase : kv_kbase, doff[i], dst);
-    else dma16(kv_src[i] + (v ? plane : 0), dst);
-  };
+  // the four loads of the prepared tile: K rows 0..3, V rows 0..3, K rows 4..7, V rows 4..7
   auto dma_all = [&]() {
-    dma(0);
-    dma(1);
-    dma(2);
-    dma(3);
+    if (!kv_pending) return;
+    dma16_sv(kv_kbase, kv_off[0], kv_lds);
+    dma16_sv(kv_vbase, kv_off[0], kv_lds + kKvBytes);
+    dma16_sv(kv_kbase, kv_off[1], kv_lds + 1024);
+    dma16_sv(kv_vbase, kv_off[1], kv_lds + kKvBytes + 1024);
   };
 
-  // ---- prologue.  Iteration i issues the loads of tile i + 2 and the page ids
-  // of tile i + 4, then computes tile i (its epilogue stores come last).
-  // Waiting until only the previous iteration's operations are outstanding
-  // therefore completes everything issued two iterations back: tile i's
-  // K/V/Q and the page ids of tile i + 2.
-  issue_pages(0);
-  if (n_tiles > 1) issue_pages(1);
-  wait_vmcnt(0);
-  __syncthreads();
-  prep_tile(0, 0);
+  // ---- prologue.  Iteration i issues the loads of tile i + 2, then computes
+  // tile i (its epilogue stores come last).  Waiting until only the previous
+  // iteration's operations are outstanding therefore completes everything
+  // issued two iterations back: tile i's K/V/Q.
+  prep_tile(0, page_id());
   dma_all();
-  if (n_tiles > 2) issue_pages(2);
   int ops_prev = 0;                  // operations issued by the previous iteration
   if (n_tiles > 1) {
-    ops_prev = prep_tile(1, 1);
+    ops_prev = prep_tile(1, page_id());
     dma_all();
-    if (n_tiles > 3) ops_prev += issue_pages(3);
   }
   kv_pending = false;
 
@@ -457,15 +421,15 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   int st_c = 0, st_l = 2;            // stages of the computed and the next loaded tile
 
   for (int n = 0; n < n_tiles; ++n) {
+    const int page = (n + 2 < n_tiles) ? page_id() : 0;
     wait_vmcnt(rfl(ops_prev));
     lds_fence();
     int ops = 0;
     if (n + 2 < n_tiles) {
-      ops += prep_tile(n + 2, st_l);
+      ops += prep_tile(st_l, page);
       dma_all();
     }
     kv_pending = false;
-    if (n + kPageSlots < n_tiles) ops += issue_pages(n + kPageSlots);
     st_l = st_l == kStages - 1 ? 0 : st_l + 1;
 
     // ---- compute tile n.  Wave roles by the segment's row tiles (NT):
@@ -481,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
     const SegReg& sg = c_sg;
     const int R = sg.q_count * g;
     const int NT = (R + 15) >> 4;
-    const int mode = NT >= 3 ? 0 : NT == 2 ? 1 : sg.n_tiles >= kQuarterTiles ? 2 : 3;
+    const int mode = FM >= 0 ? FM : NT >= 3 ? 0 : NT == 2 ? 1 : sg.n_tiles >= kQuarterTiles ? 2 : 3;
     const int rt = mode == 0 ? (w & 3) : mode == 1 ? (w & 1) : 0;
     const int ts = mode == 0 ? (w >> 2) : mode == 1 ? ((w >> 1) & 1) : mode == 2 ? (w & 3) : 0;
     const int sub0 = mode == 2 ? ts : 2 * ts;
@@ -584,6 +548,26 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   }
 }
 
+template <typename T>
+__global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char st_lds[kStages * kStageBytes];
+  __shared__ StreamSeg seg_lds[kMaxSegs];
+
+  const int tid = threadIdx.x;
+  const int4 wi = a.wg[blockIdx.x];
+  const int n_segs = rfl(wi.y), n_tiles = rfl(wi.z), cls = rfl(wi.w);
+  if (n_tiles <= 0) return;
+  {
+    const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
+    int* dst = reinterpret_cast<int*>(seg_lds);
+    for (int i = tid; i < n_segs * 8; i += kThreads) dst[i] = src[i];
+  }
+  __syncthreads();
+  if (cls == 0) stream_body<T, 0>(a, st_lds, seg_lds, n_segs, n_tiles);
+  else if (cls == 2) stream_body<T, 2>(a, st_lds, seg_lds, n_segs, n_tiles);
+  else stream_body<T, -1>(a, st_lds, seg_lds, n_segs, n_tiles);
+}
+
 // WPR waves per record (query, KV head), 4 / WPR records per workgroup.  The
 // tail pass first attends the record's tail chunks — 16 tokens of one page
 // each, from the query's short groups — as one online softmax (a token in two
@@ -592,10 +576,9 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
 // memory through the wave's LDS area into the streaming kernel's tile step
 // (S^T = K Q^T on v_mfma_f32_16x16x32, P.V on 16x16x16, rows = the g query
 // heads).  The record's waves' states and its partial slots are then combined
-// by log-sum-exp with a running max, one (head, 4 columns) entry per thread;
-// the first 8 slots of a thread's first entry are loaded before the tail pass
-// so that their latency hides under it.  A record with neither tail chunks nor
-// slots writes o = 0 and lse = -inf.
+// by log-sum-exp with a running max, one (head, 4 columns) entry per thread.
+// Each wave keeps the K/V rows of its next two chunks in flight.  A record
+// with neither tail chunks nor slots writes o = 0 and lse = -inf.
 template <typename T, int WPR>
 __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
   constexpr int RPB = 4 / WPR;                 // records per workgroup
@@ -639,14 +622,12 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
       }
     }
   };
-  // prefetch: the first slot batch of this thread's first entry
-  const bool has0 = act && rtid < g * C4;
-  int sl0[8];
-  float lv0[8];
-  v4f ov0[8];
-  load_batch(has0 ? rtid / C4 : 0, has0 ? rtid % C4 : 0, has0 ? 0 : n, sl0, lv0, ov0);
 
   float* part = reinterpret_cast<float*>(&tl_lds[0][0]);       // after the tail pass: [4][16][kD]
+  float m_run = -INFINITY, l_run = 0.f;
+  v4f o_acc[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
   if (nt > 0) {
     typedef int v4i __attribute__((ext_vector_type(4)));
     unsigned char* kt = tl_lds[wv];
@@ -666,9 +647,10 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) voff8[mt] = (uint32_t)(tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3));
     }
-    // rows 4 i + lg of chunk c, 16-byte column slot lc holding global column lc ^ row
-    v4i kr[4], vr[4];
-    auto load = [&](int c) {
+    // rows 4 i + lg of chunk c, 16-byte column slot lc holding global column lc ^ row,
+    // into register buffer b
+    v4i kr[2][4], vr[2][4];
+    auto load = [&](int c, int b) {
       const int page = __builtin_amdgcn_readlane(ent.x, c);
       const int ov = __builtin_amdgcn_readlane(ent.y, c);
       const int off = ov & 0xffff, valid = ov >> 16;
@@ -677,32 +659,33 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
         const int r = 4 * i + lg;
         const int tok = off + min(r, valid - 1);
         const T* src = kvp + (((int64_t)page * 2 * ps + tok) * hkv + h) * kD + ((lc ^ r) << 3);
-        kr[i] = *reinterpret_cast<const v4i*>(src);
-        vr[i] = *reinterpret_cast<const v4i*>(src + plane);
+        kr[b][i] = *reinterpret_cast<const v4i*>(src);
+        vr[b][i] = *reinterpret_cast<const v4i*>(src + plane);
       }
     };
-    float m_run = -INFINITY, l_run = 0.f;
-    v4f o_acc[8];
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (sw < nt) load(sw);
-    for (int c = sw; c < nt; c += WPR) {
+    // chunk c from buffer b to LDS, chunk c + 2 WPR into buffer b, then compute c
+    auto step = [&](int c, int b) {
       const int valid = __builtin_amdgcn_readlane(ent.y, c) >> 16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * i + lg;
-        *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[i];
-        *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[i];
+        *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[b][i];
+        *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[b][i];
       }
-      if (c + WPR < nt) load(c + WPR);
+      if (c + 2 * WPR < nt) load(c + 2 * WPR, b);
       tile_compute<T, 1, 8>(kt, vt, qf, koff, voff8, 0, valid, lg, m.scale_log2, m_run, l_run, o_acc);
+    };
+    if (sw < nt) load(sw, 0);
+    if (sw + WPR < nt) load(sw + WPR, 1);
+    for (int c = sw; c < nt; c += 2 * WPR) {
+      step(c, 0);
+      if (c + WPR < nt) step(c + WPR, 1);
     }
     float l = l_run;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    if (WPR > 1) __syncthreads();          // every wave of the record is done with its K/V area
-    // lane holds O^T[d = 16 mt + 4 lg + i][row lc] (unnormalised, log2 domain); a wave's
-    // area is its own K/V area, so one wave per record needs no barrier
+    // lane holds O^T[d = 16 mt + 4 lg + i][row lc] (unnormalised, log2 domain); the
+    // wave's state goes to its own K/V area
     if (lc < g) {
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt)
@@ -712,8 +695,10 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
         st_l[wv][lc] = l;
       }
     }
-    if (WPR > 1) __syncthreads();
   }
+  // the record's other waves read the states: every wave of the workgroup
+  // (including those of an inactive record) passes this barrier
+  if (WPR > 1) __syncthreads();
   if (!act) return;
 
   T* out = reinterpret_cast<T*>(m.out) + (int64_t)qi * m.o_sn;
@@ -747,16 +732,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
       int sl[8];
       float lv[8];
       v4f ov[8];
-      if (c == rtid && k0 == 0) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          sl[j] = sl0[j];
-          lv[j] = lv0[j];
-          ov[j] = ov0[j];
-        }
-      } else {
-        load_batch(hh, d4, k0, sl, lv, ov);
-      }
+      load_batch(hh, d4, k0, sl, lv, ov);
       float mx = M;
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lv[j]);
@@ -785,8 +761,8 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
 using namespace stream;
 
 // ================================================================== host: plan
-bool stream_eligible(int dtype, int head_dim, int group, int flags) {
-  return (dtype == BE_BF16 || dtype == BE_F16) && head_dim == kD && group <= kSegRows &&
+bool stream_eligible(int dtype, int head_dim, int group, int page_size, int flags) {
+  return (dtype == BE_BF16 || dtype == BE_F16) && head_dim == kD && group <= kSegRows && page_size % 16 == 0 &&
          !(flags & (BE_PLAN_FORCE_VALU | BE_PLAN_FUSED_MERGE | BE_PLAN_TILE_KERNEL));
 }
 
@@ -911,6 +887,19 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     }
   }
 
+  // ---- wave-role mode class per workgroup: the mode every segment of the
+  // workgroup takes (0 or 2, which have specialised loops), else -1
+  for (int b = 0; b < W; ++b) {
+    int cls = -2;
+    for (int i = wg[b].x; i < wg[b].x + wg[b].y; ++i) {
+      const StreamSeg& sgm = segs[i];
+      const int nt = (sgm.q_count * g + 15) / 16;
+      const int md = nt >= 3 ? 0 : nt == 2 ? 1 : sgm.n_tiles >= kQuarterTiles ? 2 : 3;
+      cls = cls == -2 ? md : cls == md ? cls : -1;
+    }
+    wg[b].w = (cls == 0 || cls == 2) ? cls : -1;
+  }
+
   // ---- partial slots and merge records per (query, KV head)
   std::vector<int> cnt((size_t)num_queries * hkv, 0);
   for (const StreamSeg& s : segs)
@@ -1011,11 +1000,15 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->num_tails = (int32_t)n_tails;
   info->off_tails = (int32_t)off_tails;
   {
-    // chunks per record: spread a record over four waves when there are fewer
-    // records than SIMDs and their tails take several chunks each
+    // waves per record of the tail-and-merge kernel: spread a record's chunks
+    // over 2 or 4 waves while all of them stay resident at once (two waves per
+    // SIMD, 8 per CU) and the records' tails are long enough to share out
     int64_t chunks = 0;
     for (int64_t r = 0; r < n_recs; ++r) chunks += recs[r * kRecWords + 5];
-    info->tail_waves = (n_recs > 0 && n_recs <= 4 * (int64_t)W && chunks >= 4 * n_recs) ? 4 : 1;
+    const int64_t slots8 = 8 * (int64_t)W;
+    info->tail_waves = (n_recs > 0 && 4 * n_recs <= slots8 && chunks >= 4 * n_recs)   ? 4
+                       : (n_recs > 0 && 2 * n_recs <= slots8 && chunks >= 2 * n_recs) ? 2
+                                                                                      : 1;
   }
   return BE_OK;
 }
@@ -1063,15 +1056,18 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
     m.out = out; m.o_sn = o_sn; m.o_sh = o_sh; m.out_lse = lse;
     m.n_recs = info->grid_merge; m.g = g; m.hq = hq; m.hkv = hkv; m.page_size = ps;
     m.scale_log2 = sm_scale * 1.4426950408889634f;
-    // four waves per record where records are few and their tails long enough to
-    // share out; one wave per record (four records per workgroup) otherwise
-    const bool wide = info->tail_waves == 4;
-    const int grid = wide ? info->grid_merge : (int)ceil_div(info->grid_merge, 4);
+    // several waves per record where records are few and their tails long enough
+    // to share out (tail_waves from the planner), four records per workgroup
+    // with one wave each otherwise
+    const int wpr = info->tail_waves;
+    const int grid = (int)ceil_div(info->grid_merge, 4 / wpr);
     if (info->dtype == BE_BF16) {
-      if (wide) tail_merge_kernel<bf16_t, 4><<<grid, 256, 0, st>>>(m);
+      if (wpr == 4) tail_merge_kernel<bf16_t, 4><<<grid, 256, 0, st>>>(m);
+      else if (wpr == 2) tail_merge_kernel<bf16_t, 2><<<grid, 256, 0, st>>>(m);
       else tail_merge_kernel<bf16_t, 1><<<grid, 256, 0, st>>>(m);
     } else {
-      if (wide) tail_merge_kernel<f16_t, 4><<<grid, 256, 0, st>>>(m);
+      if (wpr == 4) tail_merge_kernel<f16_t, 4><<<grid, 256, 0, st>>>(m);
+      else if (wpr == 2) tail_merge_kernel<f16_t, 2><<<grid, 256, 0, st>>>(m);
       else tail_merge_kernel<f16_t, 1><<<grid, 256, 0, st>>>(m);
     }
     BE_HIP_CHECK(hipGetLastError());

@@ -279,11 +279,16 @@ def test_stream_plan_cascade_coverage_and_records():
               ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1]),
               ([0, 1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 3, 4, 5, 6, 7, 8, 9],
                [10, 11, 12, 13, 14, 15, 16, 17, 18], [1, 1, 1, 0, 0, 3, 3, 3])]
-    rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, num_pages=19)
-    assert rc == 0, L.be_last_error()
-    check_stream_plan(levels, 8, 8, 2, 4, info, buf)
-    valid = 3 * 4 + 1 + 3 * (4 + 1) + (1 + 4 + 1 + 1 + 0 + 0 + 3 + 3 + 3)
-    assert info.kv_bytes == valid * 2 * 128 * 2 * 2
+    # (the streaming kernel takes page sizes that are multiples of 16)
+    for flags in (0, 8):
+        rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, page=16, num_pages=19, flags=flags)
+        assert rc == 0, L.be_last_error()
+        check_stream_plan(levels, 8, 8, 2, 16, info, buf)
+        valid = 3 * 16 + 1 + 3 * (16 + 1) + (1 + 16 + 1 + 1 + 0 + 0 + 3 + 3 + 3)
+        assert info.kv_bytes == valid * 2 * 128 * 2 * 2
+        assert (info.num_tails > 0) == (flags == 0)
+    rc, info, *_ = plan(levels, hq=8, hkv=2, page=4, num_pages=19)
+    assert rc == 0 and info.kernel == 1                 # page 4: the tile kernel
 
 
 @pytest.mark.parametrize("cus", [2, 7, 256])
@@ -316,9 +321,9 @@ def test_stream_plan_balances_tiles_across_workgroups(cus):
 
 def test_stream_plan_zero_records_for_keyless_queries():
     levels = [([0, 1, 2], [0, 1, 2], [0, 1], [3, 0])]
-    rc, info, buf, *_ = plan(levels, nq=3, num_pages=2)
+    rc, info, buf, *_ = plan(levels, nq=3, page=16, num_pages=2)
     assert rc == 0
-    wg, segs, recs, rslots = check_stream_plan(levels, 3, 8, 2, 4, info, buf)
+    wg, segs, recs, rslots = check_stream_plan(levels, 3, 8, 2, 16, info, buf)
     zero = sorted((int(q), int(h)) for q, h, p, n, tb, tn, *_ in recs if n == 0 and tn == 0)
     assert zero == [(1, 0), (1, 1), (2, 0), (2, 1)]
 
@@ -328,15 +333,15 @@ def test_stream_plan_fixed_layout_offsets():
     caps = _lib.BePlanCaps(4096, 16, 256, 64, 4096, 0, 64, 64)
     a = [([0, 8], [0, 4], [0, 1, 2, 3], [1]), ([0, 3, 5, 8], [0, 2, 4, 6], [4, 5, 6, 7, 8, 9], [1, 1, 1])]
     b = [([0, 1, 2], [0, 3, 6], [0, 1, 2, 3, 4, 5], [4, 2])]
-    rc1, i1, buf1, *_ = plan(a, nq=8, num_pages=19, caps=caps)
-    rc2, i2, buf2, *_ = plan(b, nq=2, num_pages=19, caps=caps)
+    rc1, i1, buf1, *_ = plan(a, nq=8, page=16, num_pages=19, caps=caps)
+    rc2, i2, buf2, *_ = plan(b, nq=2, page=16, num_pages=19, caps=caps)
     assert rc1 == 0 and rc2 == 0 and i1.kernel == 2 and i2.kernel == 2
     fields = ["plan_ints", "off_items", "off_pages", "off_wg", "off_records", "off_record_slots", "off_tails",
               "num_wg", "grid_merge", "part_rows_cap", "partial_bytes"]
     assert [getattr(i1, f) for f in fields] == [getattr(i2, f) for f in fields]
     assert buf1[0] == i1.num_items and buf1[1] == i1.num_merge and buf2[1] == i2.num_merge
     tiny = _lib.BePlanCaps(1, 16, 256, 64, 4096, 0, 64, 64)
-    rc3, *_ = plan(a, nq=8, num_pages=19, caps=tiny)
+    rc3, *_ = plan(a, nq=8, page=16, num_pages=19, caps=tiny)
     assert rc3 == _lib.BE_ERR_CAPACITY
 
 
@@ -344,7 +349,7 @@ def test_stream_plan_falls_back_to_tile_kernel_when_a_workgroup_overflows():
     # one workgroup, 300 groups x 2 heads = 600 segments > the per-workgroup table
     n = 300
     levels = [(list(range(n + 1)), list(range(n + 1)), list(range(n)), [4] * n)]
-    rc, info, buf, *_ = plan(levels, nq=n, num_pages=n, cus=1)
+    rc, info, buf, *_ = plan(levels, nq=n, page=16, num_pages=n, cus=1, flags=8)
     assert rc == 0 and info.kernel == 1
 
 

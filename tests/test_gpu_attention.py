@@ -100,7 +100,8 @@ def test_mfma_and_valu_agree_on_bf16(ws, force_valu, fused_merge):
     kv = make_pool(20, 4, 2, 128, torch.bfloat16, 3)
     q = make_q(8, 8, 128, torch.bfloat16, 4)
     (out, lse), w = run_cascade(ws, q, kv, levels, 4, force_valu=force_valu, fused_merge=fused_merge)
-    assert w.stats.kernel == ("valu" if force_valu else "tile" if fused_merge else "stream")
+    # page 4: the streaming kernel takes page sizes that are multiples of 16
+    assert w.stats.kernel == ("valu" if force_valu else "tile")
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 4, 128 ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
 
@@ -396,25 +397,30 @@ def trie_levels(n_req, beams, prefix, page, seed, depth=2, max_tail=48, shared=T
     return (qo, kvp, kvi, lpl), nxt[0], nq
 
 
-@pytest.mark.parametrize("case", ["bf16_p16", "f16_p16", "bf16_p32", "bf16_g8", "bf16_g16", "bf16_deep"])
-@pytest.mark.parametrize("tails", [True, False])
-def test_stream_tail_pass_on_trie_shapes(ws, case, tails):
+@pytest.mark.parametrize("case", ["bf16_p16", "f16_p16", "bf16_p32", "bf16_g8", "bf16_g16", "bf16_deep",
+                                  "bf16_mixed"])
+@pytest.mark.parametrize("tails,cus", [(True, 7), (True, 61), (True, None), (False, 7)])
+def test_stream_tail_pass_on_trie_shapes(ws, case, tails, cus):
     """Short groups attended by the tail-and-merge kernel (and, with tails off,
-    by the persistent kernel) against the oracle, on beam-trie shapes."""
-    say(f"tail pass {case} tails={tails}")
+    by the persistent kernel) against the oracle, on beam-trie shapes.  The
+    device's CU count gives few records per CU (several waves per record);
+    "mixed" has groups on both sides of the tail threshold, so records with
+    and without tail chunks share workgroups (61 CUs: two waves per record)."""
+    say(f"tail pass {case} tails={tails} cus={cus}")
     dtype = torch.float16 if case.startswith("f16") else torch.bfloat16
     page = 32 if case.endswith("p32") else 16
     hq, hkv = {"bf16_g8": (64, 8), "bf16_g16": (64, 4)}.get(case, (32, 8))
     depth = 5 if case == "bf16_deep" else 2
     d = 128
-    levels, pages, nq = trie_levels(3, 8, 300, page, seed=len(case) + 7 * depth, depth=depth)
+    levels, pages, nq = trie_levels(3, 8, 300, page, seed=len(case) + 7 * depth, depth=depth,
+                                    max_tail=200 if case == "bf16_mixed" else 48)
     s = 1 / math.sqrt(d)
     kv = make_pool(pages, page, hkv, d, dtype, 51, s)
     q = make_q(nq, hq, d, dtype, 52, s)
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
     w._no_tail = not tails
-    w._num_cus = 7
+    w._num_cus = cus
     w.plan(*levels, hq, hkv, d, page, q_data_type=dtype)
     st = w.stats
     assert st.kernel == "stream"
