@@ -63,11 +63,37 @@ class AttnTimer:
         return out
 
 
+def use_tuned_gemms(path: str = None) -> bool:
+    """Use the TunableOp results file written by ``beam_engine_amd.tune_gemms``
+    (the decode GEMMs' library solutions, timed on this GPU) with tuning off;
+    shapes not in the file keep the library's default choice.  Returns False
+    (and leaves TunableOp off) when the file is missing or was written for
+    another GPU or library version."""
+    from .tune_gemms import DEFAULT_FILE
+    path = path or DEFAULT_FILE
+    if not os.path.exists(path):
+        return False
+    tun = torch.cuda.tunable
+    try:
+        tun.enable(True)
+        tun.tuning_enable(False)
+        tun.record_untuned_enable(False)
+        ok = bool(tun.read_file(path))
+    except Exception as e:               # validator mismatch and the like
+        log(f"tuned GEMM file not used: {e}")
+        ok = False
+    if not ok:
+        tun.enable(False)
+    return ok
+
+
 def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 8, beam: int = 16,
             prompt_len: int = 1024, cfg: LlamaConfig = None, seed: int = 0, time_attention: bool = True,
-            max_pages: int = 8192, graphs: bool = True):
+            max_pages: int = 8192, graphs: bool = True, tuned_gemms: bool = True):
     cfg = cfg or LlamaConfig.llama3_8b()
     dev = torch.device("cuda")
+    tuned = use_tuned_gemms() if tuned_gemms else False
+    log(f"decode GEMMs: {'TunableOp results file' if tuned else 'library defaults'}")
     t0 = time.perf_counter()
     model = LlamaDecoder(cfg, dev, torch.bfloat16, seed)
     pt = PageTable(cfg.num_hidden_layers, page_size=16, max_num_pages=max_pages, head_num=cfg.num_key_value_heads,
