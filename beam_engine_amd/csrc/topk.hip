@@ -207,29 +207,117 @@ __device__ __forceinline__ float logp_of(float xs, float m, float L) {
 }
 
 // ---------------------------------------------------------------- pass 2
+// Block-wide bitonic sort, descending, of one value per thread (256 values):
+// partners closer than 64 lanes exchange by shuffle, farther ones through LDS.
+template <typename K>
+__device__ K block_sort_desc(K v, K* xch) {
+  const int tid = threadIdx.x;
+#pragma unroll 1
+  for (int size = 2; size <= kTopkThreads; size <<= 1) {
+#pragma unroll 1
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      K p;
+      if (j >= 64) {
+        xch[tid] = v;
+        __syncthreads();
+        p = xch[tid ^ j];
+        __syncthreads();
+      } else if constexpr (sizeof(K) == 8) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
+        p = ((K)hi << 32) | lo;
+      } else {
+        p = (K)__shfl_xor((int)v, j, 64);
+      }
+      const bool lower = (tid & j) == 0, first_half = (tid & size) == 0;
+      // descending blocks where first_half: the lower index keeps the larger value
+      v = (lower == first_half) ? (v > p ? v : p) : (v < p ? v : p);
+    }
+  }
+  return v;
+}
+
+// Per segment the exact k best logp (ties to the lowest index), emitted in
+// ascending index order.  The k-th largest of the 256 per-thread maxima is a
+// lower bound of the segment's k-th largest key (the maxima are k distinct
+// elements), so the elements at or above it hold the answer; when they fit
+// one per thread, a block sort of (key, position) composites finishes the
+// selection, otherwise the radix select over all keys does.
 template <typename T>
 __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* logits, int64_t row_stride, int vocab,
                                                                    int seg_len, float inv_temp, int k,
                                                                    const float* seg_max, const double* seg_sum,
                                                                    float* cand_val, int32_t* cand_idx) {
+  constexpr int kPer = kMaxSegLen / kTopkThreads;    // keys per thread
   __shared__ uint32_t keys[kMaxSegLen];
   __shared__ int pos[kMaxK];
   __shared__ int hist[4 * 256];
   __shared__ int suf[257];
   __shared__ int misc[4];
+  __shared__ uint64_t xch[kTopkThreads];
+  const int tid = threadIdx.x;
   const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
   float m, L;
   row_norm(seg_max, seg_sum, r, segs, m, L);
   const T* row = logits + (int64_t)r * row_stride;
   const int b = s * seg_len, e = min(vocab, b + seg_len), n = e - b;
-  for (int i = threadIdx.x; i < n; i += kTopkThreads)
-    keys[i] = fkey(logp_of<T>(scaled<T>(load_logit(row + b + i), inv_temp), m, L));
+  // this thread's keys: positions tid + 256 j
+  uint32_t kr[kPer];
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + j * kTopkThreads;
+    uint32_t key = 0;
+    if (i < n) {
+      key = fkey(logp_of<T>(scaled<T>(load_logit(row + b + i), inv_temp), m, L));
+      keys[i] = key;
+    }
+    kr[j] = key;
+    kmax = key > kmax ? key : kmax;
+  }
+  // the k-th largest thread maximum (keys are > 0 for real elements)
+  const uint32_t tau = block_sort_desc<uint32_t>(kmax, reinterpret_cast<uint32_t*>(xch));
+  if (tid == k - 1) misc[3] = (int)tau;
   __syncthreads();
-  const int cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
+  const uint32_t t0 = (uint32_t)misc[3];
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) mine += (tid + j * kTopkThreads < n && kr[j] >= t0);
+  // exclusive scan of the per-thread candidate counts
+  suf[tid] = mine;
+  __syncthreads();
+  for (int off = 1; off < kTopkThreads; off <<= 1) {
+    const int v = suf[tid] + ((tid >= off) ? suf[tid - off] : 0);
+    __syncthreads();
+    suf[tid] = v;
+    __syncthreads();
+  }
+  const int total = suf[kTopkThreads - 1];
+  int cnt;
+  if (total <= kTopkThreads && n > k) {
+    // composites (key, ~position): larger = better, unique; one per thread
+    uint64_t* comp = xch;
+    int at = suf[tid] - mine;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kTopkThreads;
+      if (i < n && kr[j] >= t0) comp[at++] = ((uint64_t)kr[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+    }
+    __syncthreads();
+    const uint64_t v = tid < total ? comp[tid] : 0ull;
+    __syncthreads();
+    const uint64_t sorted = block_sort_desc<uint64_t>(v, comp);
+    if (tid < k) pos[tid] = (int)(0xffffffffu - (uint32_t)sorted);
+    __syncthreads();
+    cnt = k;
+  } else {
+    cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
+  }
   float* cv = cand_val + ((int64_t)r * segs + s) * k;
   int32_t* ci = cand_idx + ((int64_t)r * segs + s) * k;
   // emit in ascending vocabulary index, so that candidate order = index order
-  for (int j = threadIdx.x; j < cnt; j += kTopkThreads) {
+  for (int j = tid; j < cnt; j += kTopkThreads) {
     const int p = pos[j];
     int rank = 0;
     for (int t = 0; t < cnt; ++t) rank += (pos[t] < p);
@@ -238,7 +326,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
     cv[rank] = __uint_as_float(u);
     ci[rank] = b + p;
   }
-  for (int j = cnt + threadIdx.x; j < k; j += kTopkThreads) {
+  for (int j = cnt + tid; j < k; j += kTopkThreads) {
     cv[j] = -INFINITY;
     ci[j] = -1;   // empty slot (segment shorter than k)
   }

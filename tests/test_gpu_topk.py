@@ -102,3 +102,29 @@ def test_batched_requests_in_one_call():
                                                  sc[q * 16:(q + 1) * 16]) if p >= 0]
         assert got == flat, f"request {q}"
         b += r
+
+
+@pytest.mark.parametrize("case", ["strided_best", "constant", "two_levels", "near_ties_bf16"])
+def test_segment_select_paths(case):
+    """Logits that stress the per-segment selection: the best values all in
+    one thread's stride (a single thread maximum among them), constant rows
+    (every key tied: more candidates than threads), two value levels, and
+    bf16 logp values tied after rounding."""
+    say(f"topk segment paths {case}")
+    g = torch.Generator().manual_seed(11)
+    v = 128256
+    if case == "strided_best":
+        x = torch.randn((4, v), generator=g)
+        x[:, ::256] += 8.0                       # every 256th token (one thread's stride per segment) is best
+        logits = x.to(torch.bfloat16)
+    elif case == "constant":
+        logits = torch.full((3, v), 0.5).to(torch.bfloat16)
+    elif case == "two_levels":
+        x = torch.zeros((3, v))
+        x[:, torch.randperm(v, generator=g)[:40]] = 1.0
+        logits = x.to(torch.float16)
+    else:
+        logits = (torch.randn((4, v), generator=g) * 0.05).to(torch.bfloat16)
+    parents = [0.0, -0.25, -0.5, -0.75][: logits.shape[0]]
+    compare(logits, parents, 16)
+    compare(logits, parents, 1)
