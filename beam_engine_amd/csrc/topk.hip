@@ -95,12 +95,42 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// Block-wide inclusive scans of one int per thread: shuffles inside each wave,
+// then the wave totals through LDS (two barriers instead of a barrier pair per
+// doubling step).  Suffix: sum over threads >= tid; prefix: threads <= tid.
+__device__ __forceinline__ int block_suffix_sum(int v, int* tot /*4*/) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_down(v, o, 64);
+    if (lane + o < 64) v += u;
+  }
+  if (lane == 0) tot[w] = v;
+  __syncthreads();
+  for (int x = w + 1; x < 4; ++x) v += tot[x];
+  __syncthreads();
+  return v;
+}
+__device__ __forceinline__ int block_prefix_sum(int v, int* tot /*4*/) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  if (lane == 63) tot[w] = v;
+  __syncthreads();
+  for (int x = 0; x < w; ++x) v += tot[x];
+  __syncthreads();
+  return v;
+}
+
 // Exact block-wide selection of the k largest keys, ties broken by the lowest
 // position.  keys[0..n) live in LDS.  Writes min(k, n) positions (unordered)
 // to out_pos (LDS) and returns that count.  All 256 threads must call it.
 template <typename K>
 __device__ int block_select(const K* keys, int n, int k, int* out_pos, int* hist /*4*256*/,
-                            int* suf /*257*/, int* misc /*4*/) {
+                            int* suf /*257*/, int* misc /*8*/) {
   const int tid = threadIdx.x, w = tid >> 6;
   if (n <= k) {
     for (int i = tid; i < n; i += kTopkThreads) out_pos[i] = i;
@@ -117,15 +147,10 @@ __device__ int block_select(const K* keys, int n, int k, int* out_pos, int* hist
       if ((key & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((key >> shift) & 255)], 1);
     }
     __syncthreads();
-    suf[tid] = hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid];
+    // suffix sums: suf[d] = #digits >= d
+    suf[tid] = block_suffix_sum(hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid], misc + 4);
     if (tid == 0) suf[256] = 0;
     __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {     // suffix sums: suf[d] = #digits >= d
-      const int v = suf[tid] + ((tid + off < 256) ? suf[tid + off] : 0);
-      __syncthreads();
-      suf[tid] = v;
-      __syncthreads();
-    }
     if (suf[tid] >= krem && suf[tid + 1] < krem) {   // unique digit
       misc[0] = tid;
       misc[1] = suf[tid + 1];
@@ -149,15 +174,7 @@ __device__ int block_select(const K* keys, int n, int k, int* out_pos, int* hist
     else if (key == prefix) ++eq;
   }
   // exclusive scan of eq over threads (in position order)
-  suf[tid] = eq;
-  __syncthreads();
-  for (int off = 1; off < kTopkThreads; off <<= 1) {
-    const int v = suf[tid] + ((tid >= off) ? suf[tid - off] : 0);
-    __syncthreads();
-    suf[tid] = v;
-    __syncthreads();
-  }
-  int rank = suf[tid] - eq;
+  int rank = block_prefix_sum(eq, misc + 4) - eq;
   const int ngt = k - krem;
   for (int i = b; i < e && rank < krem; ++i)
     if (keys[i] == prefix) out_pos[ngt + rank++] = i;
@@ -173,15 +190,23 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logit
   __shared__ float redf[4];
   __shared__ double redd[4];
   const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
+  constexpr int kPer = kMaxSegLen / kTopkThreads;    // logits per thread, read once
   const T* row = logits + (int64_t)r * row_stride;
   const int b = s * seg_len, e = min(vocab, b + seg_len);
+  float x[kPer];
   float m = -INFINITY;
-  for (int i = b + threadIdx.x; i < e; i += kTopkThreads) m = fmaxf(m, scaled<T>(load_logit(row + i), inv_temp));
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = b + threadIdx.x + j * kTopkThreads;
+    x[j] = i < e ? scaled<T>(load_logit(row + i), inv_temp) : -INFINITY;
+    m = fmaxf(m, x[j]);
+  }
   m = block_max(m, redf);
   double acc = 0.0;
   const double md = (double)m;
-  for (int i = b + threadIdx.x; i < e; i += kTopkThreads)
-    acc += exp((double)scaled<T>(load_logit(row + i), inv_temp) - md);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (b + threadIdx.x + j * kTopkThreads < e) acc += exp((double)x[j] - md);
   acc = block_sum_d(acc, redd);
   if (threadIdx.x == 0) {
     seg_max[(int64_t)r * segs + s] = m;
@@ -189,16 +214,26 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logit
   }
 }
 
-// Row max m and L = fl32(ln S) from the segment statistics (fixed order).
-__device__ __forceinline__ void row_norm(const float* seg_max, const double* seg_sum, int r, int segs, float& m,
-                                         float& L) {
-  float mm = -INFINITY;
-  for (int s = 0; s < segs; ++s) mm = fmaxf(mm, seg_max[(int64_t)r * segs + s]);
-  double S = 0.0;
-  for (int s = 0; s < segs; ++s)
-    S += seg_sum[(int64_t)r * segs + s] * exp((double)seg_max[(int64_t)r * segs + s] - (double)mm);
-  m = mm;
-  L = (float)log(S);
+// Row max m and L = fl32(ln S) from the segment statistics, once per
+// workgroup: wave 0 takes one segment per lane (S_s exp(m_s - m) in
+// parallel), lane 0 adds the terms in segment order (a fixed float64 sum).
+__device__ __forceinline__ void row_norm_block(const float* seg_max, const double* seg_sum, int r, int segs,
+                                               float& m, float& L, double* terms, float* mL) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const float ms = lane < segs ? seg_max[(int64_t)r * segs + lane] : -INFINITY;
+    const float mm = wave_max(ms);
+    terms[lane] = lane < segs ? seg_sum[(int64_t)r * segs + lane] * exp((double)ms - (double)mm) : 0.0;
+    if (lane == 0) {
+      double S = 0.0;
+      for (int s = 0; s < segs; ++s) S += terms[s];
+      mL[0] = mm;
+      mL[1] = (float)log(S);
+    }
+  }
+  __syncthreads();
+  m = mL[0];
+  L = mL[1];
 }
 
 template <typename T>
@@ -237,12 +272,37 @@ __device__ K block_sort_desc(K v, K* xch) {
   return v;
 }
 
+// Wave-wide bitonic sort, descending, of one value per lane (64 values).
+template <typename K>
+__device__ K wave_sort_desc(K v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      K p;
+      if constexpr (sizeof(K) == 8) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
+        p = ((K)hi << 32) | lo;
+      } else {
+        p = (K)__shfl_xor((int)v, j, 64);
+      }
+      const bool lower = (lane & j) == 0, first_half = (lane & size) == 0;
+      v = (lower == first_half) ? (v > p ? v : p) : (v < p ? v : p);
+    }
+  }
+  return v;
+}
+
 // Per segment the exact k best logp (ties to the lowest index), emitted in
-// ascending index order.  The k-th largest of the 256 per-thread maxima is a
-// lower bound of the segment's k-th largest key (the maxima are k distinct
-// elements), so the elements at or above it hold the answer; when they fit
-// one per thread, a block sort of (key, position) composites finishes the
-// selection, otherwise the radix select over all keys does.
+// ascending index order.  Each wave sorts its 64 per-thread maxima; the
+// ceil(k/4)-th largest of every wave are, with the larger ones above them,
+// at least k distinct elements, so the smallest of the four is a lower bound
+// of the segment's k-th largest key.  The elements at or above it are
+// collected as (key, position) composites; up to 64 of them are sorted by one
+// wave, up to 256 by the workgroup, more fall back to the radix select over
+// all keys.
 template <typename T>
 __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* logits, int64_t row_stride, int vocab,
                                                                    int seg_len, float inv_temp, int k,
@@ -253,15 +313,27 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
   __shared__ int pos[kMaxK];
   __shared__ int hist[4 * 256];
   __shared__ int suf[257];
-  __shared__ int misc[4];
-  __shared__ uint64_t xch[kTopkThreads];
-  const int tid = threadIdx.x;
+  __shared__ int misc[8];
+  __shared__ uint64_t comp[kTopkThreads];
+  __shared__ uint32_t wtau[4];
+  __shared__ double terms[64];
+  __shared__ float mL[2];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
-  float m, L;
-  row_norm(seg_max, seg_sum, r, segs, m, L);
   const T* row = logits + (int64_t)r * row_stride;
   const int b = s * seg_len, e = min(vocab, b + seg_len), n = e - b;
-  // this thread's keys: positions tid + 256 j
+  // this thread's logits (positions tid + 256 j), loaded before the row
+  // normaliser so that the two latencies overlap
+  float xs[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + j * kTopkThreads;
+    xs[j] = i < n ? scaled<T>(load_logit(row + b + i), inv_temp) : 0.f;
+  }
+  float m, L;
+  if (tid == 0) misc[3] = 0;                         // candidate count
+  row_norm_block(seg_max, seg_sum, r, segs, m, L, terms, mL);
+  // keys (real keys are > 0)
   uint32_t kr[kPer];
   uint32_t kmax = 0;
 #pragma unroll
@@ -269,50 +341,42 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
     const int i = tid + j * kTopkThreads;
     uint32_t key = 0;
     if (i < n) {
-      key = fkey(logp_of<T>(scaled<T>(load_logit(row + b + i), inv_temp), m, L));
+      key = fkey(logp_of<T>(xs[j], m, L));
       keys[i] = key;
     }
     kr[j] = key;
     kmax = key > kmax ? key : kmax;
   }
-  // the k-th largest thread maximum (keys are > 0 for real elements)
-  const uint32_t tau = block_sort_desc<uint32_t>(kmax, reinterpret_cast<uint32_t*>(xch));
-  if (tid == k - 1) misc[3] = (int)tau;
+  const int kw = (k + 3) >> 2;                       // <= 64
+  const uint32_t ws = wave_sort_desc<uint32_t>(kmax);
+  if (lane == kw - 1) wtau[w] = ws;
   __syncthreads();
-  const uint32_t t0 = (uint32_t)misc[3];
-  int mine = 0;
+  const uint32_t t0 = min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3]));
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) mine += (tid + j * kTopkThreads < n && kr[j] >= t0);
-  // exclusive scan of the per-thread candidate counts
-  suf[tid] = mine;
-  __syncthreads();
-  for (int off = 1; off < kTopkThreads; off <<= 1) {
-    const int v = suf[tid] + ((tid >= off) ? suf[tid - off] : 0);
-    __syncthreads();
-    suf[tid] = v;
-    __syncthreads();
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + j * kTopkThreads;
+    if (i < n && kr[j] >= t0) {
+      const int at = atomicAdd(&misc[3], 1);
+      if (at < kTopkThreads) comp[at] = ((uint64_t)kr[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+    }
   }
-  const int total = suf[kTopkThreads - 1];
-  int cnt;
-  if (total <= kTopkThreads && n > k) {
-    // composites (key, ~position): larger = better, unique; one per thread
-    uint64_t* comp = xch;
-    int at = suf[tid] - mine;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = tid + j * kTopkThreads;
-      if (i < n && kr[j] >= t0) comp[at++] = ((uint64_t)kr[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+  __syncthreads();
+  const int total = misc[3];
+  int cnt = k;
+  if (n <= k || total > kTopkThreads) {
+    cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
+  } else if (total <= 64) {
+    if (w == 0) {
+      const uint64_t v = wave_sort_desc<uint64_t>(lane < total ? comp[lane] : 0ull);
+      if (lane < k) pos[lane] = (int)(0xffffffffu - (uint32_t)v);
     }
     __syncthreads();
+  } else {
     const uint64_t v = tid < total ? comp[tid] : 0ull;
     __syncthreads();
     const uint64_t sorted = block_sort_desc<uint64_t>(v, comp);
     if (tid < k) pos[tid] = (int)(0xffffffffu - (uint32_t)sorted);
     __syncthreads();
-    cnt = k;
-  } else {
-    cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
   }
   float* cv = cand_val + ((int64_t)r * segs + s) * k;
   int32_t* ci = cand_idx + ((int64_t)r * segs + s) * k;
@@ -344,7 +408,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_row_kernel(int segs, int k,
   __shared__ int pos[kMaxK];
   __shared__ int hist[4 * 256];
   __shared__ int suf[257];
-  __shared__ int misc[4];
+  __shared__ int misc[8];
   const int r = blockIdx.x;
   const int c = segs * k;
   const float* cv = cand_val + (int64_t)r * c;
@@ -377,7 +441,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_global_kernel(int n_rows, i
   __shared__ int pos[kMaxK];
   __shared__ int hist[4 * 256];
   __shared__ int suf[257];
-  __shared__ int misc[4];
+  __shared__ int misc[8];
   const int req = blockIdx.x;
   const int rb = req_row_ptr ? req_row_ptr[req] : 0;
   const int re = req_row_ptr ? req_row_ptr[req + 1] : n_rows;
