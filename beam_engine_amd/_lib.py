@@ -21,6 +21,7 @@ BE_PLAN_FORCE_VALU = 1
 BE_PLAN_FUSED_MERGE = 2
 BE_PLAN_TILE_KERNEL = 4
 BE_PLAN_NO_TAIL = 8
+BE_PLAN_TAIL_ROLE = 16
 BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
@@ -63,7 +64,8 @@ class BeAttnPlanInfo(ctypes.Structure):
         ("qo_bytes", ctypes.c_int64),
         ("flops", ctypes.c_double),
     ] + [(n, ctypes.c_int32) for n in ("num_wg", "off_wg", "off_records", "off_record_slots",
-                                              "num_tails", "off_tails", "tail_waves")]
+                                              "num_tails", "off_tails", "tail_waves",
+                                              "num_tail_items", "off_tail_items")]
 
 
 EXPORTS = (

@@ -421,9 +421,12 @@ class BeamState:
         return ([c.trie_node.page_id for c in self.candidates],
                 [len(c.trie_node.tokens) - 1 for c in self.candidates])
 
-    def position_ids(self) -> List[int]:
-        """Total path tokens minus one per candidate (beam.py:208-221)."""
-        self._annotate()
+    def position_ids(self, reuse_annotation: bool = False) -> List[int]:
+        """Total path tokens minus one per candidate (beam.py:208-221).
+        ``reuse_annotation``: the caller has built this step's metadata since
+        the last change of the trie, so its top-down pass still holds."""
+        if not reuse_annotation:
+            self._annotate()
         return [c.trie_node._pre + len(c.trie_node.tokens) - 1 for c in self.candidates]
 
     def path_pages(self, idx: int) -> List[int]:

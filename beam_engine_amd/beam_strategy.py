@@ -98,7 +98,7 @@ class VanillaBeamSearchStrategy(BeamStrategy):
         k = decode_k(beam_state.beam_size, logits.shape[-1])
         parents = torch.tensor([c.score for c in cands], dtype=torch.float64)
         b = beam_state.beam_size
-        _, _, (par, tok, sc) = beam_topk(logits, k, parents, b, temperature, request_rows=rows)
+        _, _, (par, tok, sc) = beam_topk(logits, k, parents, b, temperature, request_rows=rows, to_host=True)
         per: List[List[BeamToken]] = [[] for _ in cands]
         for p, t, s_ in zip(par.tolist(), tok.tolist(), sc.tolist()):
             if p >= 0:

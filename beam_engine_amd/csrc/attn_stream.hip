@@ -65,7 +65,9 @@ constexpr int kQuarterTiles = 4;              // single-row-tile segments this l
 constexpr int kTailTokens = 128;              // groups this short with few queries go to the tail pass
 constexpr int kTailQueries = 4;
 constexpr int kTailChunks = 64;               // 16-token tail chunks per query (one per lane)
-constexpr int kRecWords = 8;                  // int32 words per merge record
+constexpr int kRecWords = 8;                  // int32 words per merge record (and per tail item)
+constexpr int kTailRole = 8;                  // workgroup-table class of a workgroup that runs tail items
+constexpr int kTailUnit = 1;                  // planner cost of one tail chunk of one KV head (a tile is 4)
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -88,8 +90,10 @@ struct StreamArgs {
   float* out_lse;
   float* part_o;      // [slots, g, D]
   float* part_lse;    // [slots, g]
-  const int4* wg;     // per workgroup: first segment, segments, tiles
+  const int4* wg;     // per workgroup: first segment (item), segments (items), tiles, class
   const StreamSeg* segs;
+  const int32_t* titems;   // tail items [n][8]: query, KV head, first tail chunk, chunks, slot
+  const int2* tails;
   const int32_t* pages;
   int page_size, page_shift, hkv, hq, g;
   float scale_log2;
@@ -282,6 +286,71 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
                        __builtin_shufflevector(pf[k], pf[k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
     }
     o_acc[mt] = o;
+  }
+}
+
+// Online softmax of one (query, KV head) over its tail chunks c = first,
+// first + stride, ... < nt (16 tokens of one page each; ent: lane k holds
+// chunk k's page id and in-page offset | valid << 16).  K and V rows go from
+// global memory through registers (two chunks in flight) into the wave's 8 KB
+// LDS area and the streaming tile step, rows = the g query heads of the KV
+// head.  A token in two groups counts twice, as two merged groups would count it.
+template <typename T>
+__device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t q_sh, const void* kv, int ps, int hkv,
+                                            int g, int qi, int h, int2 ent, int nt, int first, int stride,
+                                            unsigned char* area, float scale, float& m_run, float& l_run,
+                                            v4f (&o_acc)[8]) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
+  unsigned char* kt = area;
+  unsigned char* vt = area + 4096;
+  const T* kvp = reinterpret_cast<const T*>(kv);
+  const int64_t plane = (int64_t)ps * hkv * kD;
+  const T* qp = reinterpret_cast<const T*>(q) + (int64_t)qi * q_sn + (int64_t)(h * g + min(lc, g - 1)) * q_sh;
+  v8s qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const v8s*>(qp + 8 * (4 * ks + lg));
+  uint32_t koff[4], voff8[8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = lc * 256 + ((((ks << 2) | lg) ^ lc) << 4);
+  {
+    const int tl = 4 * lg + (lc >> 2), b1 = (lc >> 1) & 1, b0 = lc & 1;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) voff8[mt] = (uint32_t)(tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3));
+  }
+  // rows 4 i + lg of chunk c, 16-byte column slot lc holding global column lc ^ row,
+  // into register buffer b
+  v4i kr[2][4], vr[2][4];
+  auto load = [&](int c, int b) {
+    const int page = __builtin_amdgcn_readlane(ent.x, c);
+    const int ov = __builtin_amdgcn_readlane(ent.y, c);
+    const int off = ov & 0xffff, valid = ov >> 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * i + lg;
+      const int tok = off + min(r, valid - 1);
+      const T* src = kvp + (((int64_t)page * 2 * ps + tok) * hkv + h) * kD + ((lc ^ r) << 3);
+      kr[b][i] = *reinterpret_cast<const v4i*>(src);
+      vr[b][i] = *reinterpret_cast<const v4i*>(src + plane);
+    }
+  };
+  // chunk c from buffer b to LDS, chunk c + 2 stride into buffer b, then compute c
+  auto step = [&](int c, int b) {
+    const int valid = __builtin_amdgcn_readlane(ent.y, c) >> 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * i + lg;
+      *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[b][i];
+      *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[b][i];
+    }
+    if (c + 2 * stride < nt) load(c + 2 * stride, b);
+    tile_compute<T, 1, 8>(kt, vt, qf, koff, voff8, 0, valid, lg, scale, m_run, l_run, o_acc);
+  };
+  if (first < nt) load(first, 0);
+  if (first + stride < nt) load(first + stride, 1);
+  for (int c = first; c < nt; c += 2 * stride) {
+    step(c, 0);
+    if (c + stride < nt) step(c + stride, 1);
   }
 }
 
@@ -548,6 +617,42 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* 
   }
 }
 
+// A workgroup of the tail role: wave w attends tail items w, w + 8, ... (one
+// (query, KV head) each, its chunks in order) and writes the normalised
+// output and lse of the g heads to the item's partial slot.
+static_assert(kWaves * 2 * 4096 <= kStages * kStageBytes, "tail-role areas fit the stage buffers");
+
+template <typename T>
+__device__ __forceinline__ void tail_body(const StreamArgs& a, unsigned char* st_lds, int first, int count) {
+  const int w = rfl(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
+  const int g = a.g;
+  for (int it = w; it < count; it += kWaves) {
+    const int32_t* ip = a.titems + (int64_t)(first + it) * kRecWords;
+    const int qi = rfl(ip[0]), h = rfl(ip[1]), t0 = rfl(ip[2]), slot = rfl(ip[4]);
+    const int nt = min(rfl(ip[3]), kTailChunks);
+    const int2 ent = lane < nt ? a.tails[t0 + lane] : int2{0, 0};
+    float m_run = -INFINITY, l_run = 0.f;
+    v4f o_acc[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    tail_chunks<T>(a.q, a.q_sn, a.q_sh, a.kv, a.page_size, a.hkv, g, qi, h, ent, nt, 0, 1, st_lds + w * 8192,
+                   a.scale_log2, m_run, l_run, o_acc);
+    float l = l_run;
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    // lane holds O^T[d = 16 mt + 4 lg + i][row lc]; items have chunks, so l > 0
+    if (lc < g) {
+      const float inv = 1.f / l;
+      const int64_t sl = (int64_t)slot * g + lc;
+      float* op = a.part_o + sl * kD + 4 * lg;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4f*>(op + 16 * mt) = o_acc[mt] * inv;
+      if (lg == 0) a.part_lse[sl] = (m_run + log2f(l)) * 0.69314718055994531f;
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char st_lds[kStages * kStageBytes];
@@ -556,6 +661,10 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   const int tid = threadIdx.x;
   const int4 wi = a.wg[blockIdx.x];
   const int n_segs = rfl(wi.y), n_tiles = rfl(wi.z), cls = rfl(wi.w);
+  if (cls == kTailRole) {
+    tail_body<T>(a, st_lds, rfl(wi.x), n_segs);
+    return;
+  }
   if (n_tiles <= 0) return;
   {
     const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
@@ -629,58 +738,8 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
   if (nt > 0) {
-    typedef int v4i __attribute__((ext_vector_type(4)));
-    unsigned char* kt = tl_lds[wv];
-    unsigned char* vt = kt + 4096;
-    const T* kvp = reinterpret_cast<const T*>(m.kv);
-    const int ps = m.page_size, hkv = m.hkv;
-    const int64_t plane = (int64_t)ps * hkv * kD;
-    const T* qp = reinterpret_cast<const T*>(m.q) + (int64_t)qi * m.q_sn + (int64_t)(h * g + min(lc, g - 1)) * m.q_sh;
-    v8s qf[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const v8s*>(qp + 8 * (4 * ks + lg));
-    uint32_t koff[4], voff8[8];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) koff[ks] = lc * 256 + ((((ks << 2) | lg) ^ lc) << 4);
-    {
-      const int tl = 4 * lg + (lc >> 2), b1 = (lc >> 1) & 1, b0 = lc & 1;
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) voff8[mt] = (uint32_t)(tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3));
-    }
-    // rows 4 i + lg of chunk c, 16-byte column slot lc holding global column lc ^ row,
-    // into register buffer b
-    v4i kr[2][4], vr[2][4];
-    auto load = [&](int c, int b) {
-      const int page = __builtin_amdgcn_readlane(ent.x, c);
-      const int ov = __builtin_amdgcn_readlane(ent.y, c);
-      const int off = ov & 0xffff, valid = ov >> 16;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * i + lg;
-        const int tok = off + min(r, valid - 1);
-        const T* src = kvp + (((int64_t)page * 2 * ps + tok) * hkv + h) * kD + ((lc ^ r) << 3);
-        kr[b][i] = *reinterpret_cast<const v4i*>(src);
-        vr[b][i] = *reinterpret_cast<const v4i*>(src + plane);
-      }
-    };
-    // chunk c from buffer b to LDS, chunk c + 2 WPR into buffer b, then compute c
-    auto step = [&](int c, int b) {
-      const int valid = __builtin_amdgcn_readlane(ent.y, c) >> 16;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * i + lg;
-        *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[b][i];
-        *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[b][i];
-      }
-      if (c + 2 * WPR < nt) load(c + 2 * WPR, b);
-      tile_compute<T, 1, 8>(kt, vt, qf, koff, voff8, 0, valid, lg, m.scale_log2, m_run, l_run, o_acc);
-    };
-    if (sw < nt) load(sw, 0);
-    if (sw + WPR < nt) load(sw + WPR, 1);
-    for (int c = sw; c < nt; c += 2 * WPR) {
-      step(c, 0);
-      if (c + WPR < nt) step(c + WPR, 1);
-    }
+    tail_chunks<T>(m.q, m.q_sn, m.q_sh, m.kv, m.page_size, m.hkv, g, qi, h, ent, nt, sw, WPR, tl_lds[wv],
+                   m.scale_log2, m_run, l_run, o_acc);
     float l = l_run;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -826,11 +885,32 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       }
   }
 
-  // ---- balanced contiguous runs.  Costs: 4 per tile, kSegCost per segment
-  // start.  When workgroup b opens, its share is the remaining cost (tiles,
-  // task starts, and one split per remaining workgroup boundary) over the
-  // remaining workgroups; a tile joins b unless it would overshoot that share
-  // by more than half its cost.
+  // ---- roles: with BE_PLAN_TAIL_ROLE the tail chunks run in tail-role
+  // workgroups of this kernel (one wave per (query, KV head) item) while the
+  // other workgroups stream; the split follows the planner costs (4 per tile,
+  // kSegCost per segment start, kTailUnit per chunk of one KV head).  By
+  // default the merge kernel attends them: the streaming workgroups are
+  // bandwidth-bound on every CU, and a CU given to tail items costs them more
+  // than the overlap saves on the ns and e2e shapes (measured on MI355X).
+  int64_t tail_cost = 0;
+  for (int qi = 0; qi < num_queries; ++qi) tail_cost += (int64_t)tails_of[qi].size() * hkv * kTailUnit;
+  const bool tail_role = tail_cost > 0 && (flags & BE_PLAN_TAIL_ROLE) && (tasks.empty() || W >= 2);
+  int W_t = 0;
+  if (tail_role) {
+    if (tasks.empty()) {
+      W_t = W;
+    } else {
+      W_t = (int)((int64_t)W * tail_cost / (tail_cost + total));
+      W_t = std::min(std::max(W_t, 1), W - 1);
+    }
+  }
+  const int W_s = W - W_t;                              // streaming workgroups: [0, W_s)
+
+  // ---- balanced contiguous runs over the streaming workgroups.  Costs: 4 per
+  // tile, kSegCost per segment start.  When workgroup b opens, its share is the
+  // remaining cost (tiles, task starts, and one split per remaining workgroup
+  // boundary) over the remaining workgroups; a tile joins b unless it would
+  // overshoot that share by more than half its cost.
   std::vector<StreamSeg> segs;
   std::vector<int4> wg(W, int4{0, 0, 0, 0});
   std::vector<int64_t> suffix(tasks.size() + 1, 0);     // cost of tasks[i..] as whole segments
@@ -840,8 +920,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     int64_t used = 0, share = 0;
     auto open_wg = [&](size_t ti, int tile) {
       const int64_t rem = suffix[ti + 1] + 4 * (int64_t)(tasks[ti].tiles - tile) + kSegCost +
-                          (int64_t)(W - 1 - b) * kSegCost;
-      share = ceil_div(rem, W - b);
+                          (int64_t)(W_s - 1 - b) * kSegCost;
+      share = ceil_div(rem, W_s - b);
       used = 0;
     };
     bool first = true;
@@ -856,7 +936,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
         for (;;) {
           const int64_t c = 4 + (open ? 0 : kSegCost);
           const bool room = used + c / 2 <= share && (open || wg[b].y < kMaxSegs);
-          if (room || b == W - 1) break;
+          if (room || b == W_s - 1) break;
           ++b;
           open = false;
           open_wg(ti, tile);
@@ -889,7 +969,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
 
   // ---- wave-role mode class per workgroup: the mode every segment of the
   // workgroup takes (0 or 2, which have specialised loops), else -1
-  for (int b = 0; b < W; ++b) {
+  for (int b = 0; b < W_s; ++b) {
     int cls = -2;
     for (int i = wg[b].x; i < wg[b].x + wg[b].y; ++i) {
       const StreamSeg& sgm = segs[i];
@@ -914,33 +994,84 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       n_slots += s.q_count;
     }
   }
-  std::vector<std::vector<int>> slots_of((size_t)num_queries * hkv);
+  // tail items (tail role): one per (query with tail chunks, KV head), with a slot
+  std::vector<int32_t> titems;
+  std::vector<int> item_slot((size_t)num_queries * hkv, -1);
+  if (tail_role) {
+    int t0 = 0;
+    for (int qi = 0; qi < num_queries; ++qi) {
+      const int nt = (int)tails_of[qi].size();
+      for (int h = 0; h < hkv && nt > 0; ++h) {
+        item_slot[(size_t)qi * hkv + h] = n_slots;
+        const int32_t it[kRecWords] = {qi, h, t0, nt, n_slots, 0, 0, 0};
+        titems.insert(titems.end(), it, it + kRecWords);
+        ++n_slots;
+      }
+      t0 += nt;
+    }
+  }
+  // slot ids per (query, KV head) as CSR: count, prefix, fill in segment order
+  const size_t nqh = (size_t)num_queries * hkv;
+  std::vector<int> sbeg(nqh + 1, 0);
   for (const StreamSeg& s : segs)
     if (s.out_slot >= 0)
-      for (int j = 0; j < s.q_count; ++j) slots_of[(size_t)(s.q_begin + j) * hkv + s.head].push_back(s.out_slot + j);
+      for (int j = 0; j < s.q_count; ++j) sbeg[(size_t)(s.q_begin + j) * hkv + s.head + 1] += 1;
+  for (size_t k = 0; k < nqh; ++k) sbeg[k + 1] += (item_slot[k] >= 0);
+  for (size_t k = 0; k < nqh; ++k) sbeg[k + 1] += sbeg[k];
+  std::vector<int> slot_ids((size_t)sbeg[nqh]);
+  {
+    std::vector<int> fill(sbeg.begin(), sbeg.end() - 1);
+    for (const StreamSeg& s : segs)
+      if (s.out_slot >= 0)
+        for (int j = 0; j < s.q_count; ++j) slot_ids[fill[(size_t)(s.q_begin + j) * hkv + s.head]++] = s.out_slot + j;
+    for (size_t k = 0; k < nqh; ++k)
+      if (item_slot[k] >= 0) slot_ids[fill[k]++] = item_slot[k];
+  }
   std::vector<int32_t> recs;
   std::vector<int> rec_slots;
   std::vector<int2> tails;
+  recs.reserve(nqh * kRecWords);
+  rec_slots.reserve(slot_ids.size());
   for (int qi = 0; qi < num_queries; ++qi) {
-    const int t0 = (int)tails.size(), nt = (int)tails_of[qi].size();
+    const int t0 = (int)tails.size(), nt_q = (int)tails_of[qi].size();
+    const int nt = tail_role ? 0 : nt_q;                 // tail role: the chunks arrive as a slot
     tails.insert(tails.end(), tails_of[qi].begin(), tails_of[qi].end());
     for (int h = 0; h < hkv; ++h) {
       const size_t k = (size_t)qi * hkv + h;
-      if (cnt[k] == 1 && nt == 0 && slots_of[k].empty()) continue;   // written directly
-      const int32_t r[kRecWords] = {qi, h, (int)rec_slots.size(), (int)slots_of[k].size(), t0, nt, 0, 0};
+      const int ns = sbeg[k + 1] - sbeg[k];
+      if (cnt[k] == 1 && nt_q == 0 && ns == 0) continue;   // written directly
+      const int32_t r[kRecWords] = {qi, h, (int)rec_slots.size(), ns, t0, nt, 0, 0};
       recs.insert(recs.end(), r, r + kRecWords);
-      rec_slots.insert(rec_slots.end(), slots_of[k].begin(), slots_of[k].end());
+      rec_slots.insert(rec_slots.end(), slot_ids.begin() + sbeg[k], slot_ids.begin() + sbeg[k + 1]);
     }
   }
   const int64_t n_recs = (int64_t)recs.size() / kRecWords;
   const int64_t n_tails = (int64_t)tails.size();
+  const int64_t n_items = (int64_t)titems.size() / kRecWords;
+  if (tail_role) {
+    // contiguous item ranges over the tail workgroups, balanced by chunks
+    int64_t left = 0;
+    for (int64_t i = 0; i < n_items; ++i) left += titems[i * kRecWords + 3];
+    int64_t i = 0;
+    for (int b = W_s; b < W; ++b) {
+      const int64_t share = ceil_div(left, W - b);
+      int64_t got = 0;
+      wg[b] = int4{(int)i, 0, 0, kTailRole};
+      while (i < n_items && (got == 0 || got + titems[i * kRecWords + 3] / 2 <= share || b == W - 1)) {
+        got += titems[i * kRecWords + 3];
+        ++i;
+        wg[b].y += 1;
+      }
+      left -= got;
+    }
+  }
 
   // ---- serialise: header, workgroup table, segments, pages, records, record
   // slots, tail chunks
   const int64_t n_segs = (int64_t)segs.size();
   if (caps) {
     if (n_segs > caps->max_items || total_pages > caps->max_pages || n_recs > caps->max_merge ||
-        n_slots > caps->max_merge_rows || n_tails > caps->max_tails)
+        n_slots > caps->max_merge_rows || n_tails > caps->max_tails || n_items > caps->max_merge)
       return fail(BE_ERR_CAPACITY,
                   "plan exceeds its fixed capacities: segments %lld/%d pages %lld/%d records %lld/%d slots %d/%d "
                   "tail chunks %lld/%d",
@@ -960,6 +1091,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   const int64_t off_rslots = off; off += c_slots;
   off = ceil_div(off, 2) * 2;
   const int64_t off_tails = off;  off += 2 * c_tails;
+  const int64_t c_items = caps ? (int64_t)caps->max_merge : n_items;
+  const int64_t off_items = off;  off += kRecWords * c_items;
   off = ceil_div(off, 4) * 4;
   if (off > cap || off > INT32_MAX)
     return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
@@ -973,6 +1106,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   if (!recs.empty()) memcpy(out + off_recs, recs.data(), recs.size() * sizeof(int32_t));
   if (!rec_slots.empty()) memcpy(out + off_rslots, rec_slots.data(), rec_slots.size() * sizeof(int32_t));
   if (n_tails) memcpy(out + off_tails, tails.data(), n_tails * sizeof(int2));
+  if (n_items) memcpy(out + off_items, titems.data(), titems.size() * sizeof(int32_t));
 
   info->num_items = (int32_t)n_segs;
   info->num_part_rows = n_slots;
@@ -999,6 +1133,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->off_record_slots = (int32_t)off_rslots;
   info->num_tails = (int32_t)n_tails;
   info->off_tails = (int32_t)off_tails;
+  info->num_tail_items = (int32_t)n_items;
+  info->off_tail_items = (int32_t)off_items;
   {
     // waves per record of the tail-and-merge kernel: spread a record's chunks
     // over 2 or 4 waves while all of them stay resident at once (two waves per
@@ -1026,7 +1162,8 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
   float* part_o = reinterpret_cast<float*>(partials);
   float* part_lse = part_o ? part_o + (int64_t)info->part_rows_cap * g * kD : nullptr;
   const int ps = info->page_size;
-  if ((phases & BE_RUN_ATTENTION) && info->num_wg > 0 && (info->static_layout || info->num_items > 0)) {
+  if ((phases & BE_RUN_ATTENTION) && info->num_wg > 0 &&
+      (info->static_layout || info->num_items > 0 || info->num_tail_items > 0)) {
     StreamArgs a;
     a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;
     a.kv = kv;
@@ -1034,6 +1171,8 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
     a.part_o = part_o; a.part_lse = part_lse;
     a.wg = reinterpret_cast<const int4*>(plan + info->off_wg);
     a.segs = reinterpret_cast<const StreamSeg*>(plan + info->off_items);
+    a.titems = plan + info->off_tail_items;
+    a.tails = reinterpret_cast<const int2*>(plan + info->off_tails);
     a.pages = plan + info->off_pages;
     a.page_size = ps;
     a.page_shift = (ps & (ps - 1)) == 0 ? __builtin_ctz((unsigned)ps) : -1;

@@ -129,7 +129,7 @@ class BatchedBeamSearch:
         w = self._plan(kind, levels)
         qids = st.query_token_ids()
         wp, wpos = st.write_locations()
-        pos = st.position_ids()
+        pos = st.position_ids(reuse_annotation=True)     # _plan's metadata pass just ran
         if self._staging.numel() < 4 * n:
             self._staging = torch.empty(8 * n, dtype=torch.int64, pin_memory=True)
         stg = self._staging[: 4 * n].view(4, n)

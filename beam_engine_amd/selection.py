@@ -39,9 +39,21 @@ def decode_k(beam_size: int, vocab: int) -> int:
     return min(beam_size * 2, vocab) if beam_size != 1 else 1
 
 
+_row_ptrs = {}      # (device, request rows) -> device int32 row pointers
+_pinned = {}        # (device, name) -> pinned host staging tensor
+
+
+def _staging(dev, name, n, dtype):
+    key = (dev.type, dev.index, name)
+    t = _pinned.get(key)
+    if t is None or t.numel() < n or t.dtype != dtype:
+        t = _pinned[key] = torch.empty(max(n, 256), dtype=dtype, pin_memory=True)
+    return t[:n]
+
+
 def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor] = None, beam: int = 0,
               temperature: float = 1.0, workspace: Optional[TopkWorkspace] = None,
-              request_rows: Optional[Sequence[int]] = None):
+              request_rows: Optional[Sequence[int]] = None, to_host: bool = False):
     """Row top-k of log_softmax(logits / T) and, when ``beam > 0``, the top-``beam``
     of ``parent_scores[r] + logp`` (float64) within every request.
 
@@ -50,7 +62,9 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
     beam > 0, ``(parent [R * beam] i32 global row, token [R * beam] i32,
     score [R * beam] f64)``; request q's entries are ``[q * beam, (q + 1) * beam)``
     in emission order (rows ascending, children in selection order), unused
-    entries have parent -1."""
+    entries have parent -1.  ``to_host``: the selection outputs come back as
+    CPU tensors through pinned staging with one synchronisation (host
+    ``parent_scores`` go up the same way)."""
     lib = _lib.load()
     _lib.require_device(logits, "logits")
     if logits.dim() != 2:
@@ -73,15 +87,27 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
     if beam > 0:
         if parent_scores is None:
             raise ValueError("parent_scores are required when beam > 0")
-        ps = parent_scores.to(device=dev, dtype=torch.float64).contiguous()
+        if parent_scores.device.type == "cpu" and to_host:
+            # the staging buffer is free again once this call synchronises
+            host = _staging(dev, "parents", parent_scores.numel(), torch.float64)
+            host.copy_(parent_scores.reshape(-1))
+            ps = host.to(dev, non_blocking=True)
+        else:
+            ps = parent_scores.to(device=dev, dtype=torch.float64).contiguous()
         if ps.numel() != n:
             raise ValueError("parent_scores must have one entry per row")
         if request_rows is not None:
-            rows = [int(x) for x in request_rows]
+            rows = tuple(int(x) for x in request_rows)
             if sum(rows) != n or min(rows, default=0) < 0:
                 raise ValueError("request_rows must partition the rows")
             n_req, max_rows = len(rows), max(rows)
-            ptr_dev = torch.tensor(np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)).to(dev)
+            key = (dev.type, dev.index, rows)
+            ptr_dev = _row_ptrs.get(key)
+            if ptr_dev is None:
+                if len(_row_ptrs) > 64:
+                    _row_ptrs.clear()
+                ptr_dev = _row_ptrs[key] = torch.tensor(
+                    np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)).to(dev)
         outs = (torch.empty(n_req * beam, dtype=torch.int32, device=dev),
                 torch.empty(n_req * beam, dtype=torch.int32, device=dev),
                 torch.empty(n_req * beam, dtype=torch.float64, device=dev))
@@ -91,5 +117,15 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
                           buf.data_ptr(), buf.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "beam top-k")
     if beam > 0:
+        if to_host:
+            m = outs[0].numel()
+            hp = _staging(dev, "parent", m, torch.int32)
+            ht = _staging(dev, "token", m, torch.int32)
+            hs = _staging(dev, "score", m, torch.float64)
+            hp.copy_(outs[0], non_blocking=True)
+            ht.copy_(outs[1], non_blocking=True)
+            hs.copy_(outs[2], non_blocking=True)
+            torch.cuda.current_stream(dev).synchronize()
+            outs = (hp.clone(), ht.clone(), hs.clone())
         return row_vals, row_idx, outs
     return row_vals, row_idx

@@ -123,7 +123,10 @@ typedef struct be_level {
 #define BE_PLAN_TILE_KERNEL 4    /* one workgroup per (work item, KV head) tile kernel even
                                     where the persistent streaming kernel applies         */
 #define BE_PLAN_NO_TAIL 8        /* streaming kernel: keep short groups of few queries in the
-                                    persistent kernel instead of the tail-and-merge pass   */
+                                    persistent kernel's tiles instead of tail chunks       */
+#define BE_PLAN_TAIL_ROLE 16     /* streaming kernel: attend tail chunks in tail-role
+                                    workgroups of the persistent kernel rather than in the
+                                    merge kernel                                            */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the
@@ -178,7 +181,12 @@ typedef struct be_attn_plan_info {
    * [num_tails][2]: page id, in-page token offset | valid tokens << 16. */
   int32_t num_tails;
   int32_t off_tails;
-  int32_t tail_waves;      /* waves per record in the tail-and-merge kernel: 1 or 4 */
+  int32_t tail_waves;      /* waves per record in the tail-and-merge kernel: 1, 2 or 4 */
+  /* With BE_PLAN_TAIL_ROLE, the tail chunks are attended by tail-role
+   * workgroups of the streaming kernel instead: items [n][8] (query, KV head,
+   * first tail entry, entries, slot) whose results join the records as slots. */
+  int32_t num_tail_items;
+  int32_t off_tail_items;
 } be_attn_plan_info;
 
 /* be_attn_plan (host only): validates the levels against num_queries,

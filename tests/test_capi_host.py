@@ -193,6 +193,11 @@ def decode_stream(info, buf):
     return wg, segs, recs, rslots, tails
 
 
+def decode_tail_items(info, buf):
+    """Tail items of tail-role workgroups: [n][8] (query, KV head, first tail entry, entries, slot, 0, 0, 0)."""
+    return buf[info.off_tail_items: info.off_tail_items + 8 * info.num_tail_items].reshape(-1, 8)
+
+
 def expected_keys(levels, page, nq):
     """Per query: the multiset of (page id, in-page slot) of every token of every group it is in."""
     from collections import Counter
@@ -223,10 +228,21 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
     wg, segs, recs, rslots, tails = decode_stream(info, buf)
     pages = buf[info.off_pages:]
     g = hq // hkv
-    # workgroup table: contiguous segment runs, tile totals
-    assert wg[:, 1].sum() == info.num_items
-    start = 0
-    for b, (s0, ns, tiles, _) in enumerate(wg):
+    items = decode_tail_items(info, buf)
+    TAIL_ROLE = 8
+    # workgroup table: contiguous segment runs with their tile totals, then the tail-role
+    # workgroups' contiguous item runs
+    role = wg[:, 3] == TAIL_ROLE
+    assert wg[~role, 1].sum() == info.num_items and wg[role, 1].sum() == info.num_tail_items
+    if role.any():
+        first = int(np.argmax(role))
+        assert role[first:].all()                          # tail roles are the last workgroups
+    start = istart = 0
+    for b, (s0, ns, tiles, cls) in enumerate(wg):
+        if cls == TAIL_ROLE:
+            assert s0 == istart and tiles == 0
+            istart += ns
+            continue
         if ns:
             assert s0 == start
             assert tiles == segs[s0:s0 + ns, 7].sum()
@@ -240,8 +256,12 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
         for q in range(q0, q0 + qn):
             seen[q][head].update(keys)
     tails_of = {}
-    for q, h, ptr, n, tb, tn, z0, z1 in recs:
-        assert z0 == 0 and z1 == 0
+    chunks = [(q, h, tb, tn) for q, h, ptr, n, tb, tn, z0, z1 in recs if tn > 0]
+    chunks += [(q, h, tb, tn) for q, h, tb, tn, slot, *_ in items]
+    assert not (info.num_tail_items and (recs[:, 5] > 0).any())   # chunks go to items or to records
+    assert (recs[:, 6:] == 0).all() and (items[:, 5:] == 0).all()
+    for q, h, tb, tn in chunks:
+        assert tn > 0
         chunk = [tuple(int(v) for v in e) for e in tails[tb:tb + tn]]
         assert tails_of.setdefault(int(q), chunk) == chunk       # every head of a query shares its chunks
         for pg, ov in chunk:
@@ -260,6 +280,9 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             cover.setdefault((q0 + j, head), []).append(-1 if slot < 0 else slot + j)
         if slot >= 0:
             owned.extend(range(slot, slot + qn))
+    for q, h, tb, tn, slot, *_ in items:
+        cover.setdefault((q, h), []).append(slot)
+        owned.append(slot)
     assert sorted(owned) == list(range(info.num_part_rows))
     assert sorted(rslots.tolist()) == list(range(info.num_part_rows))
     rec_keys = set()
@@ -280,13 +303,14 @@ def test_stream_plan_cascade_coverage_and_records():
               ([0, 1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 3, 4, 5, 6, 7, 8, 9],
                [10, 11, 12, 13, 14, 15, 16, 17, 18], [1, 1, 1, 0, 0, 3, 3, 3])]
     # (the streaming kernel takes page sizes that are multiples of 16)
-    for flags in (0, 8):
+    for flags in (0, 8, 16):
         rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, page=16, num_pages=19, flags=flags)
         assert rc == 0, L.be_last_error()
         check_stream_plan(levels, 8, 8, 2, 16, info, buf)
         valid = 3 * 16 + 1 + 3 * (16 + 1) + (1 + 16 + 1 + 1 + 0 + 0 + 3 + 3 + 3)
         assert info.kv_bytes == valid * 2 * 128 * 2 * 2
-        assert (info.num_tails > 0) == (flags == 0)
+        assert (info.num_tails > 0) == (flags != 8)
+        assert (info.num_tail_items > 0) == (flags == 16)
     rc, info, *_ = plan(levels, hq=8, hkv=2, page=4, num_pages=19)
     assert rc == 0 and info.kernel == 1                 # page 4: the tile kernel
 

@@ -399,13 +399,16 @@ def trie_levels(n_req, beams, prefix, page, seed, depth=2, max_tail=48, shared=T
 
 @pytest.mark.parametrize("case", ["bf16_p16", "f16_p16", "bf16_p32", "bf16_g8", "bf16_g16", "bf16_deep",
                                   "bf16_mixed"])
-@pytest.mark.parametrize("tails,cus", [(True, 7), (True, 61), (True, None), (False, 7)])
+@pytest.mark.parametrize("tails,cus", [("role", 7), ("role", 61), ("role", None), ("merge", 7), ("merge", 61),
+                                       ("merge", None), ("off", 7)])
 def test_stream_tail_pass_on_trie_shapes(ws, case, tails, cus):
-    """Short groups attended by the tail-and-merge kernel (and, with tails off,
-    by the persistent kernel) against the oracle, on beam-trie shapes.  The
-    device's CU count gives few records per CU (several waves per record);
-    "mixed" has groups on both sides of the tail threshold, so records with
-    and without tail chunks share workgroups (61 CUs: two waves per record)."""
+    """Short groups attended as 16-token tail chunks — by tail-role workgroups
+    of the persistent kernel ("role"), or by the tail-and-merge kernel
+    ("merge") — or, with tails off, in the persistent kernel's tiles, against
+    the oracle on beam-trie shapes.  In the merge kernel the device's CU count
+    gives few records per CU (several waves per record); "mixed" has groups on
+    both sides of the tail threshold, so records with and without tail chunks
+    share workgroups (61 CUs: two waves per record)."""
     say(f"tail pass {case} tails={tails} cus={cus}")
     dtype = torch.float16 if case.startswith("f16") else torch.bfloat16
     page = 32 if case.endswith("p32") else 16
@@ -419,13 +422,50 @@ def test_stream_tail_pass_on_trie_shapes(ws, case, tails, cus):
     q = make_q(nq, hq, d, dtype, 52, s)
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
-    w._no_tail = not tails
+    w._no_tail = tails == "off"
+    w._tail_role = tails == "role"
     w._num_cus = cus
     w.plan(*levels, hq, hkv, d, page, q_data_type=dtype)
     st = w.stats
     assert st.kernel == "stream"
-    assert (st.num_tails > 0) == tails
+    assert (st.num_tails > 0) == (tails != "off")
+    assert (w._info.num_tail_items > 0) == (tails == "role")
     out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
     torch.cuda.synchronize()
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, dtype)
+
+
+@pytest.mark.parametrize("cus", [1, 5, None])
+def test_stream_tail_role_without_streamed_groups(ws, cus):
+    """Every group short enough for tail chunks, tail role on: every workgroup
+    takes the tail role (no segments), down to a single one."""
+    say(f"tail role only, cus={cus}")
+    page, hq, hkv, d = 16, 32, 8, 128
+    rng = np.random.default_rng(11)
+    nq = 24
+    levels = ([], [], [], [])
+    pg = 0
+    for _ in range(3):
+        qo, kvp, kvi, lpl = [0], [0], [], []
+        for _q in range(nq):
+            n = int(rng.integers(1, 49))
+            npg = -(-n // page)
+            kvi += list(range(pg, pg + npg)); pg += npg
+            kvp.append(len(kvi)); lpl.append(n - (npg - 1) * page); qo.append(qo[-1] + 1)
+        for i, x in enumerate((qo, kvp, kvi, lpl)):
+            levels[i].append(x)
+    s = 1 / math.sqrt(d)
+    kv = make_pool(pg, page, hkv, d, torch.bfloat16, 53, s)
+    q = make_q(nq, hq, d, torch.bfloat16, 54, s)
+    from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+    w = MultiLevelCascadeAttentionWrapper(3, ws)
+    w._num_cus = cus
+    w._tail_role = True
+    w.plan(*levels, hq, hkv, d, page, q_data_type=torch.bfloat16)
+    assert w.stats.kernel == "stream" and w.stats.num_items == 0
+    assert w._info.num_tail_items == nq * hkv
+    out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
