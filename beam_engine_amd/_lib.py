@@ -22,6 +22,7 @@ BE_PLAN_FUSED_MERGE = 2
 BE_PLAN_TILE_KERNEL = 4
 BE_PLAN_NO_TAIL = 8
 BE_PLAN_TAIL_ROLE = 16
+BE_PLAN_NO_REGS = 32
 BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
@@ -65,7 +66,7 @@ class BeAttnPlanInfo(ctypes.Structure):
         ("flops", ctypes.c_double),
     ] + [(n, ctypes.c_int32) for n in ("num_wg", "off_wg", "off_records", "off_record_slots",
                                               "num_tails", "off_tails", "tail_waves",
-                                              "num_tail_items", "off_tail_items")]
+                                              "num_tail_items", "off_tail_items", "stream_loop")]
 
 
 EXPORTS = (

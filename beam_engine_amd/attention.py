@@ -114,6 +114,7 @@ class _PagedPlanner:
         self._tile_kernel = False     # force the per-(item, head) tile kernel over the streaming kernel
         self._no_tail = False         # streaming kernel: keep short groups in whole tiles, no tail chunks
         self._tail_role = False       # streaming kernel: tail chunks in tail-role workgroups, not the merge kernel
+        self._no_regs = False         # streaming kernel: direct-load loop in every workgroup
         self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
 
@@ -154,7 +155,8 @@ class _PagedPlanner:
             (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0) | \
             (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0) | \
             (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0) | \
-            (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0)
+            (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
+            (_lib.BE_PLAN_NO_REGS if self._no_regs else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()

@@ -10,7 +10,7 @@
 namespace be {
 
 constexpr int kPlanHeader = 16;    // int32 words of live counts at the start of a plan
-constexpr int kHdrItems = 0, kHdrMerge = 1, kHdrZero = 2, kHdrRows = 3;
+constexpr int kHdrItems = 0, kHdrMerge = 1, kHdrZero = 2, kHdrRows = 3, kHdrTailItems = 4;
 
 // One paged group of one cascade level after validation: queries [q0, q1)
 // attend kv_len tokens whose pages start at page_base of the plan's

@@ -12,16 +12,18 @@
 //    run ends.  A piece of a work item inside one run is a segment.  Groups of
 //    at most 128 tokens and 4 queries skip this kernel: the tail-and-merge
 //    kernel attends them per (query, KV head).
-//  * K, V and the Q rows of a segment move by direct global->LDS loads
-//    (global_load_lds_dwordx4).  Nothing in the loop waits on a VGPR load, so
-//    the loads of the next two tiles stay in flight across segment
-//    boundaries; waits are explicit vmcnt counts (vmcnt retires in issue
-//    order) followed by a bare s_barrier.  The page size is a multiple of 16,
-//    so each wave's 8 rows of a tile lie in one page whose id is a scalar
-//    load, issued an iteration early.
-//  * Pipeline: 3 stages of {K tile 16 KB, V tile 16 KB, Q slot 16 KB}.  In
-//    iteration n: wait for tile n, barrier, issue K/V/Q of tile n + 2,
-//    compute n.
+//  * Two loops.  Workgroups of at least kRegsMinTiles tiles move K, V and Q
+//    rows global -> registers -> LDS: two register sets keep the loads of
+//    tiles n + 1 and n + 2 in flight (across segment boundaries) while tile n
+//    is computed from one of 2 LDS stages of {K 16 KB, V 16 KB, Q slot 16 KB};
+//    iteration n computes n, stores tile n + 1 into the other stage, loads
+//    tile n + 3.  (Direct global->LDS loads of the same 256-byte rows streamed
+//    at 4.8 TB/s on MI355X, 6.2 TB/s through registers.)  Shorter workgroups
+//    use direct global->LDS loads (global_load_lds_dwordx4, explicit vmcnt
+//    waits, 3 stages, tile n + 2 issued in iteration n): they reach their
+//    first tile sooner.  The page size is a multiple of 16, so each wave's 8
+//    rows of a tile lie in one page whose id is a scalar load, issued an
+//    iteration early.
 //  * K, V and Q rows are 256-byte rows whose 16-byte chunks sit XOR-swizzled by
 //    row (the swizzle is applied by choosing each lane's global address, since
 //    a direct load writes lane l's 16 bytes at LDS base + 16 l).
@@ -36,7 +38,10 @@
 //    domain, fp32 accumulation, natural-log lse at the boundary.
 //  * A (query, KV head) covered by one segment is written as the final
 //    output; otherwise each segment writes a partial (o, lse) slot and a
-//    merge record combines the slots of the (query, KV head).
+//    merge record combines the slots of the (query, KV head).  Outputs and
+//    slots are written with non-temporal stores: nothing in the launch reads
+//    them back, and the end-of-kernel write-back before the merge kernel then
+//    has little left to do (the gap between the two kernels halved on MI355X).
 
 #include <math.h>
 
@@ -51,15 +56,18 @@ namespace stream {
 
 constexpr int kD = 128;                       // head_dim served
 constexpr int kTok = 64;                      // tokens per tile
-constexpr int kStages = 3;
+constexpr int kDmaStages = 3;                 // LDS stages of the direct-load loop
+constexpr int kRegStages = 2;                 // LDS stages of the register-staged loop
+constexpr int kRegsMinTiles = 8;              // launches whose largest run has this many tiles stage through registers
 constexpr int kSegRows = 64;                  // rows per segment: 4 waves x 16
 constexpr int kMaxSegs = 224;                 // segments per workgroup (LDS table)
 constexpr int kKvBytes = kTok * kD * 2;       // one K (or V) tile: 16 KB
 constexpr int kQBytes = kSegRows * kD * 2;    // one Q slot: 16 KB
 constexpr int kStageBytes = 2 * kKvBytes + kQBytes;
+constexpr int kLdsStages = kRegStages * kStageBytes;   // the smaller of the two loops' stage buffers
+constexpr int kClassGeneric = 1;              // workgroup-table class: per-segment mode (else the mode 0 or 2)
 constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
 constexpr int kThreads = 64 * kWaves;
-constexpr int kLoadsPerTile = 4;              // direct loads per wave per tile (2 K + 2 V row blocks)
 constexpr int kSegCost = 4;                   // planner cost of a segment start, in quarter tiles
 constexpr int kQuarterTiles = 4;              // single-row-tile segments this long split tokens 4 ways
 constexpr int kTailTokens = 128;              // groups this short with few queries go to the tail pass
@@ -68,6 +76,7 @@ constexpr int kTailChunks = 64;               // 16-token tail chunks per query 
 constexpr int kRecWords = 8;                  // int32 words per merge record (and per tail item)
 constexpr int kTailRole = 8;                  // workgroup-table class of a workgroup that runs tail items
 constexpr int kTailUnit = 1;                  // planner cost of one tail chunk of one KV head (a tile is 4)
+constexpr int kItemChunks = 4;                // tail chunks per tail item (tail role and tail queue)
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -171,9 +180,16 @@ __device__ __forceinline__ void wait_tree(int n) {
 }
 __device__ __forceinline__ void wait_vmcnt(int n) { wait_tree<0, 31>(n < 31 ? n : 31); }
 
+// Bare workgroup barrier (after explicit vmcnt waits for direct loads).
 __device__ __forceinline__ void lds_fence() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// Workgroup barrier after this wave's LDS writes have completed (s_waitcnt
+// lgkmcnt(0), then s_barrier; vector memory loads stay in flight).
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -354,13 +370,14 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
   }
 }
 
-// The loop of one workgroup over its segments' tiles.  FM >= 0: every segment
-// of the workgroup takes wave-role mode FM (the planner marks such
-// workgroups), so the per-tile mode dispatch folds away; FM < 0: mode per
-// segment.
+// The loop of one workgroup over its segments' tiles, K, V and Q rows by
+// direct global->LDS loads (the planner's choice for workgroups of few tiles,
+// whose time is mostly the pipeline's fill and drain).  Three LDS stages;
+// iteration n waits for tile n, issues the loads of tile n + 2 and computes
+// tile n.  FM as for stream_body_regs.
 template <typename T, int FM>
-__device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
-                                            int n_segs, int n_tiles) {
+__device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
+                                                float* ml_lds, int n_segs, int n_tiles) {
   const int tid = threadIdx.x;
   const int w = rfl(tid >> 6);                        // wave index (uniform)
   const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
@@ -445,7 +462,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* 
         kv_off[i] = (uint32_t)(((int64_t)rel * hkv * kD + ((lc ^ (8 * (w & 1) + r)) << 3)) * 2);
       }
     }
-    int ops = kLoadsPerTile;
+    int ops = 4;                                      // K/V loads per wave per tile
     if (l_t == 0) {
       const int R = sg.q_count * g;
       const int nq = (R + 3) >> 2;                    // 1 KB loads of 4 rows
@@ -499,7 +516,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* 
       dma_all();
     }
     kv_pending = false;
-    st_l = st_l == kStages - 1 ? 0 : st_l + 1;
+    st_l = st_l == kDmaStages - 1 ? 0 : st_l + 1;
 
     // ---- compute tile n.  Wave roles by the segment's row tiles (NT):
     //   NT >= 3: row tile w & 3, token half w >> 2, all head_dim        (mode 0)
@@ -553,26 +570,27 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* 
       const int nmt = mode == 0 ? 8 : mode == 3 ? 1 : 4;
       const int mt0 = mode == 0 ? 0 : mode == 3 ? w : 4 * (w >> 2);
       // token-split waves hand their state to the ts == 0 wave of their (row
-      // tile, head_dim part) through this stage's LDS (no loads target it
-      // until the next iteration's barrier)
-      const int kslot = nmt * 1024 + 512;
-      if (mode != 3) lds_fence();
+      // tile, head_dim part): o through this stage's K/V area (no loads target
+      // it until the next iteration's barrier; at most 32 KB), m and l through
+      // ml_lds
+      const int kslot = nmt * 1024;
+      if (mode != 3) lds_sync();
       if (ts > 0 && act) {
         unsigned char* slot = stage + (mode == 0 ? w - 4 : w) * kslot;
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt)
           if (mt < nmt) *reinterpret_cast<v4f*>(slot + (mt * 64 + lane) * 16) = o_acc[mt];
-        reinterpret_cast<float*>(slot + nmt * 1024)[lane] = m_run;
-        reinterpret_cast<float*>(slot + nmt * 1024 + 256)[lane] = l;
+        ml_lds[w * 128 + lane] = m_run;
+        ml_lds[w * 128 + 64 + lane] = l;
       }
-      if (mode != 3) lds_fence();
+      if (mode != 3) lds_sync();
       if (ts == 0 && act) {
         const int np = mode == 2 ? 4 : mode == 3 ? 1 : 2;   // waves sharing the (row tile, head_dim part)
         for (int p = 1; p < np; ++p) {
           const int pw = mode == 0 ? w + 4 : mode == 1 ? w + 2 : w + p;   // partner wave
           const unsigned char* slot = stage + (mode == 0 ? pw - 4 : pw) * kslot;
-          const float mb = reinterpret_cast<const float*>(slot + nmt * 1024)[lane];
-          const float lb = reinterpret_cast<const float*>(slot + nmt * 1024 + 256)[lane];
+          const float mb = ml_lds[pw * 128 + lane];
+          const float lb = ml_lds[pw * 128 + 64 + lane];
           const float M = fmaxf(m_run, mb);
           const float ca = (M == -INFINITY) ? 0.f : exp2f(m_run - M);
           const float cb = (M == -INFINITY) ? 0.f : exp2f(mb - M);
@@ -596,85 +614,378 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, unsigned char* 
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt)
               if (mt < nmt)
-                *reinterpret_cast<v4s*>(op + mt * 16) =
-                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv);
-            if (mt0 == 0 && lg == 0 && a.out_lse) a.out_lse[(int64_t)qi * a.hq + head] = lse;
+                __builtin_nontemporal_store(
+                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
+                    reinterpret_cast<v4s*>(op + mt * 16));
+            if (mt0 == 0 && lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
           } else {
             const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
             float* op = a.part_o + slot * kD + d0;
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt)
-              if (mt < nmt) *reinterpret_cast<v4f*>(op + mt * 16) = o_acc[mt] * inv;
-            if (mt0 == 0 && lg == 0) a.part_lse[slot] = lse;
+              if (mt < nmt) __builtin_nontemporal_store(o_acc[mt] * inv, reinterpret_cast<v4f*>(op + mt * 16));
+            if (mt0 == 0 && lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
           }
         }
         ops += nmt;                                      // store instructions (lse not counted)
       }
     }
     ops_prev = ops;
-    st_c = st_c == kStages - 1 ? 0 : st_c + 1;
+    st_c = st_c == kDmaStages - 1 ? 0 : st_c + 1;
     advance(c_s, c_t, c_sg);
   }
 }
 
-// A workgroup of the tail role: wave w attends tail items w, w + 8, ... (one
-// (query, KV head) each, its chunks in order) and writes the normalised
-// output and lse of the g heads to the item's partial slot.
-static_assert(kWaves * 2 * 4096 <= kStages * kStageBytes, "tail-role areas fit the stage buffers");
+// The loop of one workgroup over its segments' tiles (the planner's choice
+// for workgroups of at least kRegsMinTiles tiles).  FM >= 0: every segment of
+// the workgroup takes wave-role mode FM (the planner marks such workgroups),
+// so the per-tile mode dispatch folds away; FM < 0: mode per segment.
+//
+// K, V and Q rows travel global memory -> registers -> LDS.  Two register
+// sets hold tiles n + 1 and n + 2 in flight while tile n is computed from one
+// of the two LDS stages; iteration n then stores tile n + 1 (loaded two
+// iterations earlier) into the other stage, reloads its register set with
+// tile n + 3 and ends on a barrier.  Even tiles use register set A, odd tiles
+// set B (the loop is unrolled by two so that the sets are static).
+template <typename T, int FM>
+__device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
+                                                 float* ml_lds, int n_segs, int n_tiles) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x;
+  const int w = rfl(tid >> 6);                        // wave index (uniform)
+  const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
+  const int ps = a.page_size, g = a.g, hkv = a.hkv;
+  const int pshift = a.page_shift;
+  auto page_of = [&](int tok) { return pshift >= 0 ? (tok >> pshift) : (tok / ps); };
+  const T* kv = reinterpret_cast<const T*>(a.kv);
+  const int64_t plane = (int64_t)ps * hkv * kD;      // K plane -> V plane of a page (elements)
+  const float scale = a.scale_log2;
+
+  // per-lane LDS offsets (bytes) of the MFMA operand reads, within a 16-token
+  // sub-tile: K / Q rows, and V^T columns of all 8 head_dim tiles, of this
+  // wave's half (waves 4..7 take the upper half) and of head_dim tile w
+  uint32_t koff[4], voff8[8], voff4[4], voff1[1];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) koff[ks] = lc * 256 + ((((ks << 2) | lg) ^ lc) << 4);
+  {
+    const int tl = 4 * lg + (lc >> 2), b1 = (lc >> 1) & 1, b0 = lc & 1;
+    auto vcol = [&](int mt) { return (uint32_t)(tl * 256 + ((((2 * mt) | b1) ^ tl) << 4) + (b0 << 3)); };
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) voff8[mt] = vcol(mt);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) voff4[mt] = vcol(4 * (w >> 2) + mt);
+    voff1[0] = vcol(w);
+  }
+  // this wave loads rows 8w..8w+7 of every tile (two 16-byte loads per lane
+  // for K and for V, 4 rows each).  The page size is a multiple of 16 and
+  // tiles start at a multiple of 64 tokens, so the 8 rows lie in one page: one
+  // page id (a scalar load) and per-lane row offsets from the wave's first row.
+  uint32_t doff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 4 * i + lg;
+    doff[i] = (uint32_t)(((int64_t)r * hkv * kD + ((lc ^ (8 * (w & 1) + r)) << 3)) * 2);
+  }
+
+  // cursors: segment index, tile of the segment and the segment's record, for
+  // the loads and for the compute
+  int l_s = 0, l_t = 0, c_s = 0, c_t = 0;
+  SegReg l_sg = seg_reg(seg_lds[0]), c_sg = l_sg;
+  auto advance = [&](int& si, int& ti, SegReg& sg) {
+    if (++ti == sg.n_tiles) {
+      ti = 0;
+      if (++si < n_segs) sg = seg_reg(seg_lds[si]);
+    }
+  };
+  // the page id of this wave's rows of the next tile to load (load cursor);
+  // read an iteration's compute ahead of its use so that its latency hides
+  auto page_id = [&]() -> int {
+    const int valid = min(kTok, l_sg.tok_count - l_t * kTok);
+    const int t8 = l_sg.tok_begin + l_t * kTok + min(8 * w, valid - 1);
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_t;   // scalar (constant) loads
+    return ((const_i32_t)(uintptr_t)a.pages)[rfl(l_sg.page_begin + page_of(t8))];
+  };
+
+  // One tile's rows in registers: K and V rows 8w + (0..3) and 8w + (4..7)
+  // (lane (lg, lc) holds row 4 i + lg, 16-byte column slot lc, which holds the
+  // global column lc ^ row), and, for the first tile of a segment, this wave's
+  // 1 KB blocks k = w and w + 8 of the segment's Q rows.  Every call issues
+  // the same six loads, each from one selected address — past the last tile
+  // (live false), K/V rows of page 0 of KV head 0, and Q rows of query 0
+  // head 0 where no Q block is due (cache hits, never stored) — so that the
+  // compiler neither copies a set between paths nor counts fewer loads on one
+  // of them when it places the waits before a set's stores.
+  struct Regs {
+    v4i k[2], v[2], q[2];
+    int nq;                                          // Q blocks to store (0..2)
+  };
+  auto load = [&](Regs& r, bool live, int page) {
+    const SegReg& sg = l_sg;
+    const int valid = min(kTok, sg.tok_count - l_t * kTok);
+    const int r0 = min(8 * w, valid - 1);             // rows past the end re-read the last token
+    const int t8 = sg.tok_begin + l_t * kTok + r0;
+    const int s0 = t8 - page_of(t8) * ps;
+    const int64_t kb_off = live ? ((((int64_t)page * 2) * ps + s0) * hkv * kD + (int64_t)sg.head * kD) * 2 : 0;
+    const char* kb = reinterpret_cast<const char*>(kv) + kb_off;
+    uint32_t off[2] = {doff[0], doff[1]};
+    if (live && 8 * w + 8 > valid) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int rr = 4 * i + lg;
+        const int rel = min(8 * w + rr, valid - 1) - r0;
+        off[i] = (uint32_t)(((int64_t)rel * hkv * kD + ((lc ^ (8 * (w & 1) + rr)) << 3)) * 2);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      r.k[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(kb + off[i]));
+      r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(kb + off[i] + plane * 2));
+    }
+    const int R = sg.q_count * g;
+    const int nblk = (live && l_t == 0) ? (R + 3) >> 2 : 0;   // 1 KB blocks of 4 rows due with this tile
+    r.nq = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int k = w + kWaves * j;
+      const int rr = 4 * k + lg;
+      const int rc = k < nblk ? min(rr, R - 1) : 0;
+      const int qj = rc / g, hh = rc - qj * g;
+      const int64_t qoff = k < nblk ? (int64_t)(sg.q_begin + qj) * a.q_sn + (int64_t)(sg.head * g + hh) * a.q_sh +
+                                          ((lc ^ (rr & 15)) << 3)
+                                    : (int64_t)(lc << 3);
+      r.q[j] = *reinterpret_cast<const v4i*>(reinterpret_cast<const T*>(a.q) + qoff);
+      if (k < nblk) r.nq = j + 1;
+    }
+    if (live) advance(l_s, l_t, l_sg);
+  };
+  // store a tile's registers into stage st (lane l's 16 bytes at block + 16 l)
+  auto store = [&](const Regs& r, int st) {
+    unsigned char* stage = st_lds + st * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<v4i*>(stage + (2 * w + i) * 1024 + lane * 16) = r.k[i];
+      *reinterpret_cast<v4i*>(stage + kKvBytes + (2 * w + i) * 1024 + lane * 16) = r.v[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (j < r.nq) *reinterpret_cast<v4i*>(stage + 2 * kKvBytes + (w + kWaves * j) * 1024 + lane * 16) = r.q[j];
+  };
+
+  // ---- prologue: tiles 0 and 1 into A and B, tile 0 stored, tile 2 into A
+  Regs ra, rb;
+  load(ra, true, page_id());
+  load(rb, n_tiles > 1, n_tiles > 1 ? page_id() : 0);
+  store(ra, 0);
+  load(ra, n_tiles > 2, n_tiles > 2 ? page_id() : 0);
+  lds_sync();
+
+  float m_run = -INFINITY, l_run = 0.f;
+  v4f o_acc[8];
+  v8s qf[4];
+
+  // iteration n: compute n, store tile n + 1 (set nx), reload nx with tile n + 3
+  auto iteration = [&](int n, Regs& nx) {
+    const int page = (n + 3 < n_tiles) ? page_id() : 0;
+
+    // ---- compute tile n.  Wave roles by the segment's row tiles (NT):
+    //   NT >= 3: row tile w & 3, token half w >> 2, all head_dim        (mode 0)
+    //   NT == 2: row tile w & 1, token half (w >> 1) & 1, head_dim half  (mode 1)
+    //   NT == 1, segment of >= kQuarterTiles tiles: token quarter w & 3,
+    //            head_dim half w >> 2                                     (mode 2)
+    //   NT == 1, shorter: all 64 tokens, head_dim tile w                  (mode 3)
+    // Where tokens are split, the ts == 0 wave of each (row tile, head_dim
+    // part) collects the others at the end of the segment; mode 3 recomputes
+    // the scores in every wave instead, which costs less than that exchange
+    // when the segment is short.
+    const SegReg& sg = c_sg;
+    const int R = sg.q_count * g;
+    const int NT = (R + 15) >> 4;
+    const int mode = FM >= 0 ? FM : NT >= 3 ? 0 : NT == 2 ? 1 : sg.n_tiles >= kQuarterTiles ? 2 : 3;
+    const int rt = mode == 0 ? (w & 3) : mode == 1 ? (w & 1) : 0;
+    const int ts = mode == 0 ? (w >> 2) : mode == 1 ? ((w >> 1) & 1) : mode == 2 ? (w & 3) : 0;
+    const int sub0 = mode == 2 ? ts : 2 * ts;
+    const bool act = 16 * rt < R;
+    const bool last = c_t == sg.n_tiles - 1;
+    unsigned char* stage = st_lds + (n & 1) * kStageBytes;
+    if (c_t == 0) {
+      m_run = -INFINITY;
+      l_run = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (act) {
+        const unsigned char* qs = stage + 2 * kKvBytes + rt * 4096;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const v8s*>(qs + koff[ks]);
+      }
+    }
+    if (act) {
+      const int valid = min(kTok, sg.tok_count - c_t * kTok);
+      const unsigned char* kt = stage + sub0 * 4096;
+      const unsigned char* vt = stage + kKvBytes + sub0 * 4096;
+      if (mode == 0)
+        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+      else if (mode == 1)
+        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+      else if (mode == 2)
+        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+      else
+        tile_compute<T, 4, 1>(kt, vt, qf, koff, voff1, 0, valid, lg, scale, m_run, l_run, o_acc);
+    }
+
+    if (last) {
+      float l = l_run;
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+      const int nmt = mode == 0 ? 8 : mode == 3 ? 1 : 4;
+      const int mt0 = mode == 0 ? 0 : mode == 3 ? w : 4 * (w >> 2);
+      // token-split waves hand their state to the ts == 0 wave of their (row
+      // tile, head_dim part): o through this stage's K/V area (no loads target
+      // it until the next iteration's barrier; at most 32 KB: 4 writers x 8 KB
+      // in mode 0, writer w at 4 KB x w otherwise), m and l through ml_lds
+      const int kslot = nmt * 1024;
+      if (mode != 3) lds_sync();
+      if (ts > 0 && act) {
+        unsigned char* slot = stage + (mode == 0 ? w - 4 : w) * kslot;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+          if (mt < nmt) *reinterpret_cast<v4f*>(slot + (mt * 64 + lane) * 16) = o_acc[mt];
+        ml_lds[w * 128 + lane] = m_run;
+        ml_lds[w * 128 + 64 + lane] = l;
+      }
+      if (mode != 3) lds_sync();
+      if (ts == 0 && act) {
+        const int np = mode == 2 ? 4 : mode == 3 ? 1 : 2;   // waves sharing the (row tile, head_dim part)
+        for (int p = 1; p < np; ++p) {
+          const int pw = mode == 0 ? w + 4 : mode == 1 ? w + 2 : w + p;   // partner wave
+          const unsigned char* slot = stage + (mode == 0 ? pw - 4 : pw) * kslot;
+          const float mb = ml_lds[pw * 128 + lane];
+          const float lb = ml_lds[pw * 128 + 64 + lane];
+          const float M = fmaxf(m_run, mb);
+          const float ca = (M == -INFINITY) ? 0.f : exp2f(m_run - M);
+          const float cb = (M == -INFINITY) ? 0.f : exp2f(mb - M);
+          l = l * ca + lb * cb;
+          m_run = M;
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt)
+            if (mt < nmt)
+              o_acc[mt] = o_acc[mt] * ca + *reinterpret_cast<const v4f*>(slot + (mt * 64 + lane) * 16) * cb;
+        }
+        // lane holds O^T[d = 16 (mt0 + mt) + 4 lg + i][row = 16 rt + lc]
+        const int row = 16 * rt + lc;
+        if (row < R) {
+          const int j = row / g, hh = row - j * g, head = sg.head * g + hh;
+          const int qi = sg.q_begin + j;
+          const float inv = (l > 0.f) ? 1.f / l : 0.f;
+          const float lse = (l > 0.f) ? (m_run + log2f(l)) * 0.69314718055994531f : -INFINITY;
+          const int d0 = 16 * mt0 + 4 * lg;
+          if (sg.out_slot < 0) {
+            T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh + d0;
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+              if (mt < nmt)
+                __builtin_nontemporal_store(
+                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
+                    reinterpret_cast<v4s*>(op + mt * 16));
+            if (mt0 == 0 && lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
+          } else {
+            const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
+            float* op = a.part_o + slot * kD + d0;
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+              if (mt < nmt) __builtin_nontemporal_store(o_acc[mt] * inv, reinterpret_cast<v4f*>(op + mt * 16));
+            if (mt0 == 0 && lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
+          }
+        }
+      }
+    }
+    advance(c_s, c_t, c_sg);
+    if (n + 1 < n_tiles) store(nx, (n + 1) & 1);
+    load(nx, n + 3 < n_tiles, page);
+    lds_sync();                                      // tile n + 1 stored; stage n & 1 free
+  };
+  // (both iterations of a trip unconditional: on every path from a set's loads
+  // to its stores the other set's loads come in between)
+  int n = 0;
+  for (; n + 1 < n_tiles; n += 2) {
+    iteration(n, rb);
+    iteration(n + 1, ra);
+  }
+  if (n < n_tiles) iteration(n, rb);
+}
+
+// One tail item — tail chunks of one (query, KV head) — attended by one wave in
+// its 8 KB LDS area; the normalised output and lse of the g heads go to the
+// item's partial slot.
+static_assert(kWaves * 2 * 4096 <= kLdsStages, "per-wave tail areas fit the stage buffers");
 
 template <typename T>
-__device__ __forceinline__ void tail_body(const StreamArgs& a, unsigned char* st_lds, int first, int count) {
-  const int w = rfl(threadIdx.x >> 6);
+__device__ __forceinline__ void tail_item(const StreamArgs& a, unsigned char* area, int idx) {
   const int lane = threadIdx.x & 63, lg = lane >> 4, lc = lane & 15;
   const int g = a.g;
-  for (int it = w; it < count; it += kWaves) {
-    const int32_t* ip = a.titems + (int64_t)(first + it) * kRecWords;
-    const int qi = rfl(ip[0]), h = rfl(ip[1]), t0 = rfl(ip[2]), slot = rfl(ip[4]);
-    const int nt = min(rfl(ip[3]), kTailChunks);
-    const int2 ent = lane < nt ? a.tails[t0 + lane] : int2{0, 0};
-    float m_run = -INFINITY, l_run = 0.f;
-    v4f o_acc[8];
+  const int32_t* ip = a.titems + (int64_t)idx * kRecWords;
+  const int qi = rfl(ip[0]), h = rfl(ip[1]), t0 = rfl(ip[2]), slot = rfl(ip[4]);
+  const int nt = min(rfl(ip[3]), kTailChunks);
+  const int2 ent = lane < nt ? a.tails[t0 + lane] : int2{0, 0};
+  float m_run = -INFINITY, l_run = 0.f;
+  v4f o_acc[8];
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-    tail_chunks<T>(a.q, a.q_sn, a.q_sh, a.kv, a.page_size, a.hkv, g, qi, h, ent, nt, 0, 1, st_lds + w * 8192,
-                   a.scale_log2, m_run, l_run, o_acc);
-    float l = l_run;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    // lane holds O^T[d = 16 mt + 4 lg + i][row lc]; items have chunks, so l > 0
-    if (lc < g) {
-      const float inv = 1.f / l;
-      const int64_t sl = (int64_t)slot * g + lc;
-      float* op = a.part_o + sl * kD + 4 * lg;
+  for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  tail_chunks<T>(a.q, a.q_sn, a.q_sh, a.kv, a.page_size, a.hkv, g, qi, h, ent, nt, 0, 1, area, a.scale_log2,
+                 m_run, l_run, o_acc);
+  float l = l_run;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  // lane holds O^T[d = 16 mt + 4 lg + i][row lc]; items have chunks, so l > 0
+  if (lc < g) {
+    const float inv = 1.f / l;
+    const int64_t sl = (int64_t)slot * g + lc;
+    float* op = a.part_o + sl * kD + 4 * lg;
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4f*>(op + 16 * mt) = o_acc[mt] * inv;
-      if (lg == 0) a.part_lse[sl] = (m_run + log2f(l)) * 0.69314718055994531f;
-    }
+    for (int mt = 0; mt < 8; ++mt) __builtin_nontemporal_store(o_acc[mt] * inv, reinterpret_cast<v4f*>(op + 16 * mt));
+    if (lg == 0) __builtin_nontemporal_store((m_run + log2f(l)) * 0.69314718055994531f, a.part_lse + sl);
   }
 }
 
+// A workgroup of the tail role: wave w attends tail items w, w + 8, ... of
+// its range.
 template <typename T>
+__device__ __forceinline__ void tail_body(const StreamArgs& a, unsigned char* st_lds, int first, int count) {
+  const int w = rfl(threadIdx.x >> 6);
+  for (int it = w; it < count; it += kWaves) tail_item<T>(a, st_lds + w * 8192, first + it);
+}
+
+// REGS: the register-staged loop (the planner's choice for launches whose
+// largest workgroup run has at least kRegsMinTiles tiles), else the
+// direct-load loop.  One loop per kernel keeps each kernel's registers to
+// what that loop needs.
+template <typename T, bool REGS>
 __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char st_lds[kStages * kStageBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char st_lds[(REGS ? kRegStages : kDmaStages) * kStageBytes];
   __shared__ StreamSeg seg_lds[kMaxSegs];
+  __shared__ float ml_lds[kWaves * 128];      // epilogue exchange of m and l
 
   const int tid = threadIdx.x;
   const int4 wi = a.wg[blockIdx.x];
   const int n_segs = rfl(wi.y), n_tiles = rfl(wi.z), cls = rfl(wi.w);
   if (cls == kTailRole) {
     tail_body<T>(a, st_lds, rfl(wi.x), n_segs);
-    return;
+  } else if (n_tiles > 0) {
+    {
+      const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
+      int* dst = reinterpret_cast<int*>(seg_lds);
+      for (int i = tid; i < n_segs * 8; i += kThreads) dst[i] = src[i];
+    }
+    __syncthreads();
+    if constexpr (REGS) {
+      if (cls == 0) stream_body_regs<T, 0>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == 2) stream_body_regs<T, 2>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      else stream_body_regs<T, -1>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+    } else {
+      if (cls == 0) stream_body_dma<T, 0>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == 2) stream_body_dma<T, 2>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      else stream_body_dma<T, -1>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+    }
   }
-  if (n_tiles <= 0) return;
-  {
-    const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
-    int* dst = reinterpret_cast<int*>(seg_lds);
-    for (int i = tid; i < n_segs * 8; i += kThreads) dst[i] = src[i];
-  }
-  __syncthreads();
-  if (cls == 0) stream_body<T, 0>(a, st_lds, seg_lds, n_segs, n_tiles);
-  else if (cls == 2) stream_body<T, 2>(a, st_lds, seg_lds, n_segs, n_tiles);
-  else stream_body<T, -1>(a, st_lds, seg_lds, n_segs, n_tiles);
 }
 
 // WPR waves per record (query, KV head), 4 / WPR records per workgroup.  The
@@ -809,9 +1120,10 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
       }
     }
     const float inv = (z > 0.f) ? 1.f / z : 0.f;
-    *reinterpret_cast<v4s*>(out + (int64_t)head * m.o_sh + 4 * d4) =
-        pack4<T>(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
-    if (d4 == 0 && m.out_lse) m.out_lse[(int64_t)qi * m.hq + head] = (z > 0.f) ? M + logf(z) : -INFINITY;
+    __builtin_nontemporal_store(pack4<T>(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv),
+                                reinterpret_cast<v4s*>(out + (int64_t)head * m.o_sh + 4 * d4));
+    if (d4 == 0 && m.out_lse)
+      __builtin_nontemporal_store((z > 0.f) ? M + logf(z) : -INFINITY, m.out_lse + (int64_t)qi * m.hq + head);
   }
 }
 
@@ -967,8 +1279,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     }
   }
 
-  // ---- wave-role mode class per workgroup: the mode every segment of the
-  // workgroup takes (0 or 2, which have specialised loops), else -1
+  // ---- class per workgroup: the wave-role mode every segment of the
+  // workgroup takes (0 or 2, which have specialised loops), else kClassGeneric
   for (int b = 0; b < W_s; ++b) {
     int cls = -2;
     for (int i = wg[b].x; i < wg[b].x + wg[b].y; ++i) {
@@ -977,7 +1289,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       const int md = nt >= 3 ? 0 : nt == 2 ? 1 : sgm.n_tiles >= kQuarterTiles ? 2 : 3;
       cls = cls == -2 ? md : cls == md ? cls : -1;
     }
-    wg[b].w = (cls == 0 || cls == 2) ? cls : -1;
+    wg[b].w = (cls == 0 || cls == 2) ? cls : kClassGeneric;
   }
 
   // ---- partial slots and merge records per (query, KV head)
@@ -994,19 +1306,19 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       n_slots += s.q_count;
     }
   }
-  // tail items (tail role): one per (query with tail chunks, KV head), with a slot
+  // tail items (tail role): up to kItemChunks tail chunks of one (query, KV
+  // head), each with a slot
   std::vector<int32_t> titems;
-  std::vector<int> item_slot((size_t)num_queries * hkv, -1);
   if (tail_role) {
     int t0 = 0;
     for (int qi = 0; qi < num_queries; ++qi) {
       const int nt = (int)tails_of[qi].size();
-      for (int h = 0; h < hkv && nt > 0; ++h) {
-        item_slot[(size_t)qi * hkv + h] = n_slots;
-        const int32_t it[kRecWords] = {qi, h, t0, nt, n_slots, 0, 0, 0};
-        titems.insert(titems.end(), it, it + kRecWords);
-        ++n_slots;
-      }
+      for (int h = 0; h < hkv; ++h)
+        for (int c = 0; c < nt; c += kItemChunks) {
+          const int32_t it[kRecWords] = {qi, h, t0 + c, std::min(kItemChunks, nt - c), n_slots, 0, 0, 0};
+          titems.insert(titems.end(), it, it + kRecWords);
+          ++n_slots;
+        }
       t0 += nt;
     }
   }
@@ -1016,7 +1328,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   for (const StreamSeg& s : segs)
     if (s.out_slot >= 0)
       for (int j = 0; j < s.q_count; ++j) sbeg[(size_t)(s.q_begin + j) * hkv + s.head + 1] += 1;
-  for (size_t k = 0; k < nqh; ++k) sbeg[k + 1] += (item_slot[k] >= 0);
+  for (size_t i = 0; i < titems.size(); i += kRecWords) sbeg[(size_t)titems[i] * hkv + titems[i + 1] + 1] += 1;
   for (size_t k = 0; k < nqh; ++k) sbeg[k + 1] += sbeg[k];
   std::vector<int> slot_ids((size_t)sbeg[nqh]);
   {
@@ -1024,8 +1336,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     for (const StreamSeg& s : segs)
       if (s.out_slot >= 0)
         for (int j = 0; j < s.q_count; ++j) slot_ids[fill[(size_t)(s.q_begin + j) * hkv + s.head]++] = s.out_slot + j;
-    for (size_t k = 0; k < nqh; ++k)
-      if (item_slot[k] >= 0) slot_ids[fill[k]++] = item_slot[k];
+    for (size_t i = 0; i < titems.size(); i += kRecWords)
+      slot_ids[fill[(size_t)titems[i] * hkv + titems[i + 1]]++] = titems[i + 4];
   }
   std::vector<int32_t> recs;
   std::vector<int> rec_slots;
@@ -1034,7 +1346,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   rec_slots.reserve(slot_ids.size());
   for (int qi = 0; qi < num_queries; ++qi) {
     const int t0 = (int)tails.size(), nt_q = (int)tails_of[qi].size();
-    const int nt = tail_role ? 0 : nt_q;                 // tail role: the chunks arrive as a slot
+    const int nt = tail_role ? 0 : nt_q;                 // tail role: the chunks arrive as slots
     tails.insert(tails.end(), tails_of[qi].begin(), tails_of[qi].end());
     for (int h = 0; h < hkv; ++h) {
       const size_t k = (size_t)qi * hkv + h;
@@ -1100,6 +1412,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   out[kHdrItems] = (int32_t)n_segs;
   out[kHdrMerge] = (int32_t)n_recs;
   out[kHdrRows] = n_slots;
+  out[kHdrTailItems] = (int32_t)n_items;
   memcpy(out + off_wg, wg.data(), wg.size() * sizeof(int4));
   if (n_segs) memcpy(out + off_segs, segs.data(), n_segs * sizeof(StreamSeg));
   if (total_pages) memcpy(out + off_pages, all_pages.data(), total_pages * sizeof(int32_t));
@@ -1135,6 +1448,13 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->off_tails = (int32_t)off_tails;
   info->num_tail_items = (int32_t)n_items;
   info->off_tail_items = (int32_t)off_items;
+  // the loop: register-staged once the largest workgroup run is long enough
+  // for its faster steady state to outweigh its slower fill and drain (fixed
+  // layouts, whose runs change between plans of one layout, keep the
+  // direct-load loop so that a captured launch stays valid)
+  int max_tiles = 0;
+  for (int b = 0; b < W; ++b) max_tiles = std::max(max_tiles, wg[b].w == kTailRole ? 0 : wg[b].z);
+  info->stream_loop = (!caps && !(flags & BE_PLAN_NO_REGS) && max_tiles >= kRegsMinTiles) ? 1 : 0;
   {
     // waves per record of the tail-and-merge kernel: spread a record's chunks
     // over 2 or 4 waves while all of them stay resident at once (two waves per
@@ -1178,8 +1498,14 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
     a.page_shift = (ps & (ps - 1)) == 0 ? __builtin_ctz((unsigned)ps) : -1;
     a.hkv = hkv; a.hq = hq; a.g = g;
     a.scale_log2 = sm_scale * 1.4426950408889634f;
-    if (info->dtype == BE_BF16) attn_stream_kernel<bf16_t><<<info->num_wg, kThreads, 0, st>>>(a);
-    else if (info->dtype == BE_F16) attn_stream_kernel<f16_t><<<info->num_wg, kThreads, 0, st>>>(a);
+    const bool regs = info->stream_loop == 1;
+    if (info->dtype == BE_BF16) {
+      if (regs) attn_stream_kernel<bf16_t, true><<<info->num_wg, kThreads, 0, st>>>(a);
+      else attn_stream_kernel<bf16_t, false><<<info->num_wg, kThreads, 0, st>>>(a);
+    } else if (info->dtype == BE_F16) {
+      if (regs) attn_stream_kernel<f16_t, true><<<info->num_wg, kThreads, 0, st>>>(a);
+      else attn_stream_kernel<f16_t, false><<<info->num_wg, kThreads, 0, st>>>(a);
+    }
     else return fail(BE_ERR_INVALID, "corrupt plan info: streaming kernel with dtype %d", info->dtype);
     BE_HIP_CHECK(hipGetLastError());
   }

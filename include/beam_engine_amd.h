@@ -127,6 +127,8 @@ typedef struct be_level {
 #define BE_PLAN_TAIL_ROLE 16     /* streaming kernel: attend tail chunks in tail-role
                                     workgroups of the persistent kernel rather than in the
                                     merge kernel                                            */
+#define BE_PLAN_NO_REGS 32       /* streaming kernel: the direct-load loop whatever the runs'
+                                    lengths (no register-staged loop)                       */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the
@@ -187,6 +189,7 @@ typedef struct be_attn_plan_info {
    * first tail entry, entries, slot) whose results join the records as slots. */
   int32_t num_tail_items;
   int32_t off_tail_items;
+  int32_t stream_loop;     /* streaming kernel's loop: 0 direct global->LDS loads, 1 register-staged */
 } be_attn_plan_info;
 
 /* be_attn_plan (host only): validates the levels against num_queries,

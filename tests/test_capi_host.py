@@ -243,6 +243,7 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             assert s0 == istart and tiles == 0
             istart += ns
             continue
+        assert cls in (0, 1, 2)                # wave-role mode 0 / 2, or per segment (1)
         if ns:
             assert s0 == start
             assert tiles == segs[s0:s0 + ns, 7].sum()
@@ -260,10 +261,13 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
     chunks += [(q, h, tb, tn) for q, h, tb, tn, slot, *_ in items]
     assert not (info.num_tail_items and (recs[:, 5] > 0).any())   # chunks go to items or to records
     assert (recs[:, 6:] == 0).all() and (items[:, 5:] == 0).all()
+    assert (items[:, 3] <= 4).all()                                 # an item holds at most 4 chunks
+    per_qh = {}
     for q, h, tb, tn in chunks:
         assert tn > 0
-        chunk = [tuple(int(v) for v in e) for e in tails[tb:tb + tn]]
-        assert tails_of.setdefault(int(q), chunk) == chunk       # every head of a query shares its chunks
+        per_qh.setdefault((int(q), int(h)), []).extend(tuple(int(v) for v in e) for e in tails[tb:tb + tn])
+    for (q, h), chunk in per_qh.items():
+        assert tails_of.setdefault(q, sorted(chunk)) == sorted(chunk)   # every head of a query has its chunks
         for pg, ov in chunk:
             off, valid = ov & 0xFFFF, ov >> 16
             assert 1 <= valid <= 16 and off + valid <= page
@@ -294,6 +298,9 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             c = cover.get((q, h), [])
             direct = len(c) == 1 and c[0] == -1 and not tails_of.get(q)
             assert ((q, h) in rec_keys) != direct
+    # the loop: register-staged when the longest run reaches 8 tiles (never for fixed layouts)
+    assert info.stream_loop == (1 if int(wg[wg[:, 3] != TAIL_ROLE, 2].max(initial=0)) >= 8
+                                and not info.static_layout else 0)
     return wg, segs, recs, rslots
 
 
@@ -311,6 +318,7 @@ def test_stream_plan_cascade_coverage_and_records():
         assert info.kv_bytes == valid * 2 * 128 * 2 * 2
         assert (info.num_tails > 0) == (flags != 8)
         assert (info.num_tail_items > 0) == (flags == 16)
+        assert buf[4] == info.num_tail_items                     # header: tail item count
     rc, info, *_ = plan(levels, hq=8, hkv=2, page=4, num_pages=19)
     assert rc == 0 and info.kernel == 1                 # page 4: the tile kernel
 

@@ -46,9 +46,10 @@ def make_q(n, hq, d, dtype, seed, scale=1.0):
 
 
 def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True, fused_merge=False, tile_kernel=False,
-                num_cus=None):
+                num_cus=None, no_regs=False):
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
+    w._no_regs = no_regs
     w._force_valu = force_valu
     w._fused_merge = fused_merge
     w._tile_kernel = tile_kernel
@@ -317,10 +318,12 @@ def config3_levels(page):
 
 @pytest.mark.parametrize("shape", ["config2", "config3", "ragged_suffix"])
 @pytest.mark.parametrize("kernel,num_cus", [("tile", None), ("stream", None), ("stream", 4), ("stream", 7),
-                                            ("stream", 61)])
+                                            ("stream", 61), ("stream-dma", 4), ("stream-dma", 7)])
 def test_stream_and_tile_kernels(ws, shape, kernel, num_cus):
     """Both MFMA kernels against the oracle; small CU counts make every
-    streaming workgroup walk many segments and cut work items mid-way."""
+    streaming workgroup walk many segments and cut work items mid-way.
+    Launches with long workgroup runs take the register-staged loop, others
+    the direct-load loop; "stream-dma" keeps the latter."""
     say(f"{kernel} kernel {shape} cus={num_cus}")
     page, hq, hkv, d = 16, 32, 8, 128
     s = 1 / math.sqrt(128)
@@ -335,8 +338,13 @@ def test_stream_and_tile_kernels(ws, shape, kernel, num_cus):
     n = levels[0][0][-1] if shape != "config3" else 32
     kv = make_pool(pages, page, hkv, d, torch.bfloat16, 41, s)
     q = make_q(n, hq, d, torch.bfloat16, 42, s)
-    (out, lse), w = run_cascade(ws, q, kv, levels, page, tile_kernel=(kernel == "tile"), num_cus=num_cus)
-    assert w.stats.kernel == kernel
+    (out, lse), w = run_cascade(ws, q, kv, levels, page, tile_kernel=(kernel == "tile"), num_cus=num_cus,
+                                no_regs=(kernel == "stream-dma"))
+    assert w.stats.kernel == kernel.split("-")[0]
+    if kernel != "tile":
+        info = w._info
+        wg = w._plan_dev[info.off_wg: info.off_wg + 4 * info.num_wg].view(-1, 4).cpu()
+        assert info.stream_loop == (1 if kernel == "stream" and int(wg[:, 2].max()) >= 8 else 0)
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
 
@@ -405,7 +413,7 @@ def test_stream_tail_pass_on_trie_shapes(ws, case, tails, cus):
     """Short groups attended as 16-token tail chunks — by tail-role workgroups
     of the persistent kernel ("role"), or by the tail-and-merge kernel
     ("merge") — or, with tails off, in the persistent kernel's tiles, against
-    the oracle on beam-trie shapes.  In the merge kernel the device's CU count
+    the oracle on beam-trie shapes (each plan run twice).  In the merge kernel the device's CU count
     gives few records per CU (several waves per record); "mixed" has groups on
     both sides of the tail threshold, so records with and without tail chunks
     share workgroups (61 CUs: two waves per record)."""
@@ -430,10 +438,12 @@ def test_stream_tail_pass_on_trie_shapes(ws, case, tails, cus):
     assert st.kernel == "stream"
     assert (st.num_tails > 0) == (tails != "off")
     assert (w._info.num_tail_items > 0) == (tails == "role")
-    out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
-    torch.cuda.synchronize()
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
-    check(out, lse, ref_o, ref_lse, dtype)
+    qd, kvd = q.cuda(), kv.cuda()
+    for _ in range(2):
+        out, lse = w.run(qd, kvd, return_lse=True)
+        torch.cuda.synchronize()
+        check(out, lse, ref_o, ref_lse, dtype)
 
 
 @pytest.mark.parametrize("cus", [1, 5, None])
@@ -464,7 +474,7 @@ def test_stream_tail_role_without_streamed_groups(ws, cus):
     w._tail_role = True
     w.plan(*levels, hq, hkv, d, page, q_data_type=torch.bfloat16)
     assert w.stats.kernel == "stream" and w.stats.num_items == 0
-    assert w._info.num_tail_items == nq * hkv
+    assert w._info.num_tail_items >= nq * hkv
     out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
     torch.cuda.synchronize()
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
