@@ -115,6 +115,7 @@ class _PagedPlanner:
         self._no_tail = False         # streaming kernel: keep short groups in whole tiles, no tail chunks
         self._tail_role = False       # streaming kernel: tail chunks in tail-role workgroups, not the merge kernel
         self._no_regs = False         # streaming kernel: direct-load loop in every workgroup
+        self._no_wide = False         # streaming kernel: no wide (32-row) wave roles, no 128-row segments
         self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
 
@@ -156,7 +157,8 @@ class _PagedPlanner:
             (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0) | \
             (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0) | \
             (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
-            (_lib.BE_PLAN_NO_REGS if self._no_regs else 0)
+            (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
+            (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()

@@ -25,6 +25,36 @@ typedef short v8s __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane
+// rows of a wave that hold one MFMA column), on the VALU: v_permlane16_swap
+// exchanges odd and even 16-lane rows of its two operands and
+// v_permlane32_swap the wave's halves, so with both operands equal to x, one
+// result is x and the other the partner lane's x in every lane.  (A
+// __shfl_xor is an LDS permute whose wait also waits for the wave's
+// outstanding LDS reads.)  Vector elements are copied out before the bit
+// casts: a bit cast of an element expression reads element 0.
+__device__ __forceinline__ float rows4_max(float x) {
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  const unsigned xb = __float_as_uint(x);
+  const u2 a = __builtin_amdgcn_permlane16_swap(xb, xb, false, false);
+  const unsigned a0 = a.x, a1 = a.y;
+  const unsigned yb = __float_as_uint(fmaxf(__uint_as_float(a0), __uint_as_float(a1)));
+  const u2 b = __builtin_amdgcn_permlane32_swap(yb, yb, false, false);
+  const unsigned b0 = b.x, b1 = b.y;
+  return fmaxf(__uint_as_float(b0), __uint_as_float(b1));
+}
+// The same lanes' sum; every lane gets the bit-identical (x0 + x1) + (x2 + x3).
+__device__ __forceinline__ float rows4_sum(float x) {
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  const unsigned xb = __float_as_uint(x);
+  const u2 a = __builtin_amdgcn_permlane16_swap(xb, xb, false, false);
+  const unsigned a0 = a.x, a1 = a.y;
+  const unsigned yb = __float_as_uint(__uint_as_float(a0) + __uint_as_float(a1));
+  const u2 b = __builtin_amdgcn_permlane32_swap(yb, yb, false, false);
+  const unsigned b0 = b.x, b1 = b.y;
+  return __uint_as_float(b0) + __uint_as_float(b1);
+}
+
 // S^T tile: v_mfma_f32_16x16x32 on 16-bit operands.
 template <typename T> __device__ __forceinline__ v4f mfma_qk(v8s a, v8s b, v4f c);
 template <> __device__ __forceinline__ v4f mfma_qk<bf16_t>(v8s a, v8s b, v4f c) {

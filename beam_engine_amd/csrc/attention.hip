@@ -321,8 +321,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
       for (int sb = 0; sb < STW; ++sb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[sb][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = rows4_max(mx);
       const float m_new = fmaxf(m_run[nt], mx);
       const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
       const float alpha = exp2f(m_run[nt] - msafe);    // 0 while nothing was seen
@@ -356,8 +355,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
   // row sums over the four lane groups
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
-    l_run[nt] += __shfl_xor(l_run[nt], 16, 64);
-    l_run[nt] += __shfl_xor(l_run[nt], 32, 64);
+    l_run[nt] = rows4_sum(l_run[nt]);
   }
 
   // ---- token-split waves (ts > 0) hand their state to the ts == 0 wave of the row tile

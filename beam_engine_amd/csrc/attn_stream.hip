@@ -34,7 +34,9 @@
 //    ds_read_b64_tr_b16: in each 16-lane group, lane r supplies the address of
 //    V[t0 + r/4][d0 + 4 (r%4) .. +3] and receives V[t0 + j][d0 + r], j = 0..3.
 //  * Waves split a segment's rows (16-row MFMA tiles), tokens and head_dim by
-//    the segment's row count (modes below); online softmax in the log2
+//    the segment's row count (modes below).  Long groups of more than 64 rows
+//    (many beams x GQA group) get 128-row segments whose waves hold 32 rows
+//    each, so a tile is read once per 128 rows; online softmax in the log2
 //    domain, fp32 accumulation, natural-log lse at the boundary.
 //  * A (query, KV head) covered by one segment is written as the final
 //    output; otherwise each segment writes a partial (o, lse) slot and a
@@ -66,6 +68,7 @@ constexpr int kQBytes = kSegRows * kD * 2;    // one Q slot: 16 KB
 constexpr int kStageBytes = 2 * kKvBytes + kQBytes;
 constexpr int kLdsStages = kRegStages * kStageBytes;   // the smaller of the two loops' stage buffers
 constexpr int kClassGeneric = 1;              // workgroup-table class: per-segment mode (else the mode 0 or 2)
+constexpr int kClassWide = 5;                 // workgroup-table class of the wide roles (32 rows per wave)
 constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
 constexpr int kThreads = 64 * kWaves;
 constexpr int kSegCost = 4;                   // planner cost of a segment start, in quarter tiles
@@ -77,6 +80,10 @@ constexpr int kRecWords = 8;                  // int32 words per merge record (a
 constexpr int kTailRole = 8;                  // workgroup-table class of a workgroup that runs tail items
 constexpr int kTailUnit = 1;                  // planner cost of one tail chunk of one KV head (a tile is 4)
 constexpr int kItemChunks = 4;                // tail chunks per tail item (tail role and tail queue)
+constexpr int kWideRows = 128;               // rows per segment of a long group's wide-128 tasks
+constexpr int kWideMinTiles = 8;              // 128-row tasks for groups of at least this many tiles
+constexpr int kWideMinRun = 64;               // ... when the launch has this many 64-row tiles per workgroup
+constexpr int kWideTileCost = 6;              // planner cost of a 128-row tile (a 64-row tile is 4)
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -267,8 +274,7 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
   for (int k = 0; k < NSUB; ++k)
 #pragma unroll
     for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[k][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = rows4_max(mx);
   const float m_new = fmaxf(m_run, mx);
   const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
   if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
@@ -303,6 +309,96 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
     }
     o_acc[mt] = o;
   }
+}
+
+// Wide wave roles: one wave's share of a 64-token tile for two 16-row MFMA
+// tiles (32 rows) at once, so that every K and V^T fragment read from LDS
+// feeds both (half the LDS reads per row of tile_compute).  qf[r], m_run[r],
+// l_run[r] and o_acc[r] belong to row tile r; NSUB 16-token sub-tiles start
+// at kt / vt (tokens tok_base ..); all 8 head_dim tiles.
+template <typename T, int NSUB>
+__device__ __forceinline__ void tile_compute_w(const unsigned char* kt, const unsigned char* vt,
+                                               const v8s (&qf)[2][4], const uint32_t (&koff)[4],
+                                               const uint32_t (&voff)[8], int tok_base, int valid, int lg,
+                                               float scale, float (&m_run)[2], float (&l_run)[2],
+                                               v4f (&o_acc)[2][8]) {
+  v8s kf[NSUB][4];
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kf[k][ks] = *reinterpret_cast<const v8s*>(kt + k * 4096 + koff[ks]);
+  v4s vf[8][NSUB];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k)
+      vf[mt][k] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + k * 4096 + voff[mt]));
+
+  float x[2][NSUB][4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k) {
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) acc = mfma_qk<T>(kf[k][ks], qf[r][ks], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[r][k][i] = acc[i] * scale;
+    }
+  if (valid < tok_base + 16 * NSUB) {
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (tok_base + k * 16 + 4 * lg + i >= valid) {
+          x[0][k][i] = -INFINITY;
+          x[1][k][i] = -INFINITY;
+        }
+  }
+  v4s pf[2][NSUB];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, x[r][k][i]);
+    mx = rows4_max(mx);
+    const float m_new = fmaxf(m_run[r], mx);
+    const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run[r]) != 0) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run[r] - msafe);
+      l_run[r] *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) o_acc[r][mt] *= alpha;
+    }
+    m_run[r] = m_new;
+#pragma unroll
+    for (int k = 0; k < NSUB; ++k) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(x[r][k][i] - msafe);
+        l_run[r] += p[i];
+      }
+      pf[r][k] = pack4<T>(p[0], p[1], p[2], p[3]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      v4f o = o_acc[r][mt];
+      if constexpr (NSUB == 1) {
+        o = mfma_pv<T>(vf[mt][0], pf[r][0], o);
+      } else {
+#pragma unroll
+        for (int k = 0; k < NSUB; k += 2)
+          o = mfma_qk<T>(__builtin_shufflevector(vf[mt][k], vf[mt][k + 1], 0, 1, 2, 3, 4, 5, 6, 7),
+                         __builtin_shufflevector(pf[r][k], pf[r][k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
+      }
+      o_acc[r][mt] = o;
+    }
 }
 
 // Online softmax of one (query, KV head) over its tail chunks c = first,
@@ -372,9 +468,10 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
 
 // The loop of one workgroup over its segments' tiles, K, V and Q rows by
 // direct global->LDS loads (the planner's choice for workgroups of few tiles,
-// whose time is mostly the pipeline's fill and drain).  Three LDS stages;
-// iteration n waits for tile n, issues the loads of tile n + 2 and computes
-// tile n.  FM as for stream_body_regs.
+// whose time is mostly the pipeline's fill and drain, and for the wide
+// roles).  Three LDS stages; iteration n waits for tile n, issues the loads
+// of tile n + 2 and computes tile n.  FM as for stream_body_regs, or
+// kClassWide: the wide roles (32 rows per wave, segments of up to 128 rows).
 template <typename T, int FM>
 __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
                                                 float* ml_lds, int n_segs, int n_tiles) {
@@ -463,7 +560,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
       }
     }
     int ops = 4;                                      // K/V loads per wave per tile
-    if (l_t == 0) {
+    if (FM != kClassWide && l_t == 0) {             // wide roles: Q rows go to registers
       const int R = sg.q_count * g;
       const int nq = (R + 3) >> 2;                    // 1 KB loads of 4 rows
       for (int k = w; k < nq; k += kWaves) {
@@ -504,6 +601,9 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
   float m_run = -INFINITY, l_run = 0.f;
   v4f o_acc[8];
   v8s qf[4];
+  float m2[2] = {-INFINITY, -INFINITY}, l2[2] = {0.f, 0.f};   // wide roles
+  v4f o2[2][8];
+  v8s qf2[2][4];
   int st_c = 0, st_l = 2;            // stages of the computed and the next loaded tile
 
   for (int n = 0; n < n_tiles; ++n) {
@@ -528,6 +628,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
     // part) collects the others at the end of the segment; mode 3 recomputes
     // the scores in every wave instead, which costs less than that exchange
     // when the segment is short.
+    if constexpr (FM != kClassWide) {
     const SegReg& sg = c_sg;
     const int R = sg.q_count * g;
     const int NT = (R + 15) >> 4;
@@ -565,8 +666,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
 
     if (last) {
       float l = l_run;
-      l += __shfl_xor(l, 16, 64);
-      l += __shfl_xor(l, 32, 64);
+      l = rows4_sum(l);
       const int nmt = mode == 0 ? 8 : mode == 3 ? 1 : 4;
       const int mt0 = mode == 0 ? 0 : mode == 3 ? w : 4 * (w >> 2);
       // token-split waves hand their state to the ts == 0 wave of their (row
@@ -629,6 +729,125 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
         }
         ops += nmt;                                      // store instructions (lse not counted)
       }
+    }
+    } else {
+    // ---- wide roles (FM == kClassWide, every segment of the workgroup; up to
+    // 128 rows): wave w takes rows 32 (w & 3) .. +31 as two 16-row MFMA tiles
+    // sharing each K / V^T fragment read, and tokens 32 (w >> 2) .. +31 of the
+    // tile.  The w < 4 wave of each row group collects its partner's (m, l, o)
+    // at the end of the segment, one row tile at a time through this stage.
+    // The segment's Q rows go global -> registers on its first tile (up to
+    // 32 KB, more than the stage's Q slot holds).
+    constexpr int TP = 2;                             // token parts
+    constexpr int RG = kWaves / TP;                   // 32-row groups
+    constexpr int NSUB = 4 / TP;                      // 16-token sub-tiles per part
+    const int rg = w % RG, tp = w / RG;
+    const SegReg& sg = c_sg;
+    const int R = sg.q_count * g;
+    const bool act = 32 * rg < R;
+    const bool last = c_t == sg.n_tiles - 1;
+    unsigned char* stage = st_lds + st_c * kStageBytes;
+    if (c_t == 0) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        m2[r] = -INFINITY;
+        l2[r] = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) o2[r][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+      if (act) {
+        {
+          // rows past the segment's last re-read it (their results are never stored)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = min(32 * rg + 16 * r + lc, R - 1);
+            const int j = row / g, hh = row - j * g;
+            const T* src = reinterpret_cast<const T*>(a.q) + (int64_t)(sg.q_begin + j) * a.q_sn +
+                           (int64_t)(sg.head * g + hh) * a.q_sh;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qf2[r][ks] = *reinterpret_cast<const v8s*>(src + 8 * (4 * ks + lg));
+          }
+        }
+      }
+    }
+    if (act) {
+      const int valid = min(kTok, sg.tok_count - c_t * kTok);
+      const int sub0 = tp * NSUB;
+      tile_compute_w<T, NSUB>(stage + sub0 * 4096, stage + kKvBytes + sub0 * 4096, qf2, koff, voff8, sub0 * 16,
+                              valid, lg, scale, m2, l2, o2);
+    }
+    if (last) {
+      float l[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        l[r] = l2[r];
+        l[r] = rows4_sum(l[r]);
+      }
+      // (TP - 1) * RG = 4 waves hand over 8 KB each per row tile (32 KB of the stage's 48)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        lds_sync();
+        if (tp > 0 && act) {
+          unsigned char* slot = stage + ((tp - 1) * RG + rg) * 8192;
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4f*>(slot + (mt * 64 + lane) * 16) = o2[r][mt];
+          ml_lds[w * 128 + lane] = m2[r];
+          ml_lds[w * 128 + 64 + lane] = l[r];
+        }
+        lds_sync();
+        if (tp == 0 && act) {
+#pragma unroll
+          for (int p = 1; p < TP; ++p) {
+            const int pw = p * RG + rg;
+            const unsigned char* slot = stage + ((p - 1) * RG + rg) * 8192;
+            const float mb = ml_lds[pw * 128 + lane];
+            const float lb = ml_lds[pw * 128 + 64 + lane];
+            const float M = fmaxf(m2[r], mb);
+            const float ca = (M == -INFINITY) ? 0.f : exp2f(m2[r] - M);
+            const float cb = (M == -INFINITY) ? 0.f : exp2f(mb - M);
+            l[r] = l[r] * ca + lb * cb;
+            m2[r] = M;
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+              o2[r][mt] = o2[r][mt] * ca + *reinterpret_cast<const v4f*>(slot + (mt * 64 + lane) * 16) * cb;
+          }
+        }
+      }
+      if (tp == 0 && act) {
+        // lane holds O^T[d = 16 mt + 4 lg + i][row = 32 rg + 16 r + lc]
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int row = 32 * rg + 16 * r + lc;
+          if (row < R) {
+            const int j = row / g, hh = row - j * g, head = sg.head * g + hh;
+            const int qi = sg.q_begin + j;
+            const float inv = (l[r] > 0.f) ? 1.f / l[r] : 0.f;
+            const float lse = (l[r] > 0.f) ? (m2[r] + log2f(l[r])) * 0.69314718055994531f : -INFINITY;
+            const int d0 = 4 * lg;
+            if (sg.out_slot < 0) {
+              T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh + d0;
+#pragma unroll
+              for (int mt = 0; mt < 8; ++mt)
+                __builtin_nontemporal_store(pack4<T>(o2[r][mt][0] * inv, o2[r][mt][1] * inv, o2[r][mt][2] * inv,
+                                                     o2[r][mt][3] * inv),
+                                            reinterpret_cast<v4s*>(op + mt * 16));
+              if (lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
+            } else {
+              const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
+              float* op = a.part_o + slot * kD + d0;
+#pragma unroll
+              for (int mt = 0; mt < 8; ++mt)
+                __builtin_nontemporal_store(o2[r][mt] * inv, reinterpret_cast<v4f*>(op + mt * 16));
+              if (lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
+            }
+          }
+        }
+        // row tile 2 rg always has a stored row (32 rg < R): its 8 stores are
+        // certain; the second tile's and the lse stores are not counted, which
+        // only makes the next wait stricter
+        ops += 8;
+      }
+    }
     }
     ops_prev = ops;
     st_c = st_c == kDmaStages - 1 ? 0 : st_c + 1;
@@ -834,8 +1053,7 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
 
     if (last) {
       float l = l_run;
-      l += __shfl_xor(l, 16, 64);
-      l += __shfl_xor(l, 32, 64);
+      l = rows4_sum(l);
       const int nmt = mode == 0 ? 8 : mode == 3 ? 1 : 4;
       const int mt0 = mode == 0 ? 0 : mode == 3 ? w : 4 * (w >> 2);
       // token-split waves hand their state to the ts == 0 wave of their (row
@@ -933,8 +1151,7 @@ __device__ __forceinline__ void tail_item(const StreamArgs& a, unsigned char* ar
   tail_chunks<T>(a.q, a.q_sn, a.q_sh, a.kv, a.page_size, a.hkv, g, qi, h, ent, nt, 0, 1, area, a.scale_log2,
                  m_run, l_run, o_acc);
   float l = l_run;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l = rows4_sum(l);
   // lane holds O^T[d = 16 mt + 4 lg + i][row lc]; items have chunks, so l > 0
   if (lc < g) {
     const float inv = 1.f / l;
@@ -983,6 +1200,7 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
     } else {
       if (cls == 0) stream_body_dma<T, 0>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
       else if (cls == 2) stream_body_dma<T, 2>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == kClassWide) stream_body_dma<T, kClassWide>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
       else stream_body_dma<T, -1>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
     }
   }
@@ -1052,8 +1270,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
     tail_chunks<T>(m.q, m.q_sn, m.q_sh, m.kv, m.page_size, m.hkv, g, qi, h, ent, nt, sw, WPR, tl_lds[wv],
                    m.scale_log2, m_run, l_run, o_acc);
     float l = l_run;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = rows4_sum(l);
     // lane holds O^T[d = 16 mt + 4 lg + i][row lc] (unnormalised, log2 domain); the
     // wave's state goes to its own K/V area
     if (lc < g) {
@@ -1072,7 +1289,10 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
   if (!act) return;
 
   T* out = reinterpret_cast<T*>(m.out) + (int64_t)qi * m.o_sn;
-  for (int c = rtid; c < g * C4; c += RT) {
+  // one (head, 4 columns) entry: the waves' tail states from LDS, then the
+  // partial slots in batches of 8 (the first batch loaded by the caller), then
+  // the normalised output and lse
+  auto merge_entry = [&](int c, float (&lv0)[8], v4f (&ov0)[8]) {
     const int hh = c / C4, d4 = c - hh * C4;
     const int head = h * g + hh;
     float M = -INFINITY, z = 0.f;
@@ -1098,11 +1318,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
       z = 1.f;
       acc = at * (1.f / zt);
     }
-    for (int k0 = 0; k0 < n; k0 += 8) {
-      int sl[8];
-      float lv[8];
-      v4f ov[8];
-      load_batch(hh, d4, k0, sl, lv, ov);
+    auto fold = [&](const float (&lv)[8], const v4f (&ov)[8]) {
       float mx = M;
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lv[j]);
@@ -1118,12 +1334,33 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
         }
         M = mx;
       }
+    };
+    fold(lv0, ov0);
+    for (int k0 = 8; k0 < n; k0 += 8) {
+      int sl[8];
+      float lv[8];
+      v4f ov[8];
+      load_batch(hh, d4, k0, sl, lv, ov);
+      fold(lv, ov);
     }
     const float inv = (z > 0.f) ? 1.f / z : 0.f;
     __builtin_nontemporal_store(pack4<T>(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv),
                                 reinterpret_cast<v4s*>(out + (int64_t)head * m.o_sh + 4 * d4));
     if (d4 == 0 && m.out_lse)
       __builtin_nontemporal_store((z > 0.f) ? M + logf(z) : -INFINITY, m.out_lse + (int64_t)qi * m.hq + head);
+  };
+  // a thread's entries two at a time: both first slot batches are loaded
+  // before either is folded, so their latencies overlap
+  const int ne = g * C4;
+  for (int c = rtid; c < ne; c += 2 * RT) {
+    const int c1 = c + RT;
+    int sl0[8], sl1[8];
+    float lv0[8], lv1[8];
+    v4f ov0[8], ov1[8];
+    load_batch(c / C4, c % C4, 0, sl0, lv0, ov0);
+    if (c1 < ne) load_batch(c1 / C4, c1 % C4, 0, sl1, lv1, ov1);
+    merge_entry(c, lv0, ov0);
+    if (c1 < ne) merge_entry(c1, lv1, ov1);
   }
 }
 
@@ -1182,18 +1419,39 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     }
   }
 
-  // ---- tasks: (query tile of a group, KV head), in group order
-  struct Task { int q0, qn, page_base, kv_len, head, tiles; };
+  // ---- tasks: (query tile of a group, KV head), in group order.  A long group
+  // of more than 64 rows takes query tiles of up to 128 rows (wide roles), so
+  // its tiles are read once per 128 rows instead of once per 64; such a tile
+  // costs kWideTileCost (twice the MFMA work of a 64-row tile for the same bytes).
+  // (Only where every workgroup's run is long: a wide segment loads its Q rows
+  // into registers, which drains the load pipeline once per segment, and the
+  // direct-load loop it runs in fills and drains slower than the
+  // register-staged one.)
+  const int q_tile_w = std::max(1, kWideRows / g);
+  bool wide = !(flags & BE_PLAN_NO_WIDE) && !caps;
+  if (wide) {
+    int64_t tiles64 = 0;
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+      const Group& gr = groups[gi];
+      if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || is_tail[gi]) continue;
+      tiles64 += ceil_div(gr.kv_len, kTok) * ceil_div(gr.q1 - gr.q0, q_tile) * hkv;
+    }
+    wide = tiles64 >= (int64_t)kWideMinRun * W;
+  }
+  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc; };
   std::vector<Task> tasks;
   int64_t total = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
     const Group& gr = groups[gi];
     if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || is_tail[gi]) continue;
     const int tiles = (int)ceil_div(gr.kv_len, kTok);
-    for (int qa = gr.q0; qa < gr.q1; qa += q_tile)
+    const bool w128 = wide && (gr.q1 - gr.q0) * g > kSegRows && tiles >= kWideMinTiles;
+    const int qt = w128 ? q_tile_w : q_tile;
+    const int tc = w128 ? kWideTileCost : 4;
+    for (int qa = gr.q0; qa < gr.q1; qa += qt)
       for (int h = 0; h < hkv; ++h) {
-        tasks.push_back(Task{qa, std::min(q_tile, gr.q1 - qa), gr.page_base, gr.kv_len, h, tiles});
-        total += 4 * (int64_t)tiles + kSegCost;
+        tasks.push_back(Task{qa, std::min(qt, gr.q1 - qa), gr.page_base, gr.kv_len, h, tiles, tc});
+        total += tc * (int64_t)tiles + kSegCost;
       }
   }
 
@@ -1226,12 +1484,13 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   std::vector<StreamSeg> segs;
   std::vector<int4> wg(W, int4{0, 0, 0, 0});
   std::vector<int64_t> suffix(tasks.size() + 1, 0);     // cost of tasks[i..] as whole segments
-  for (size_t i = tasks.size(); i-- > 0;) suffix[i] = suffix[i + 1] + 4 * (int64_t)tasks[i].tiles + kSegCost;
+  for (size_t i = tasks.size(); i-- > 0;)
+    suffix[i] = suffix[i + 1] + tasks[i].tc * (int64_t)tasks[i].tiles + kSegCost;
   {
     int b = 0;
     int64_t used = 0, share = 0;
     auto open_wg = [&](size_t ti, int tile) {
-      const int64_t rem = suffix[ti + 1] + 4 * (int64_t)(tasks[ti].tiles - tile) + kSegCost +
+      const int64_t rem = suffix[ti + 1] + tasks[ti].tc * (int64_t)(tasks[ti].tiles - tile) + kSegCost +
                           (int64_t)(W_s - 1 - b) * kSegCost;
       share = ceil_div(rem, W_s - b);
       used = 0;
@@ -1246,7 +1505,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
           first = false;
         }
         for (;;) {
-          const int64_t c = 4 + (open ? 0 : kSegCost);
+          const int64_t c = t.tc + (open ? 0 : kSegCost);
           const bool room = used + c / 2 <= share && (open || wg[b].y < kMaxSegs);
           if (room || b == W_s - 1) break;
           ++b;
@@ -1274,22 +1533,28 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
         cur.n_tiles += 1;
         cur.tok_count = std::min(t.kv_len - cur.tok_begin, cur.n_tiles * kTok);
         wg[b].z += 1;
-        used += 4;
+        used += t.tc;
       }
     }
   }
 
   // ---- class per workgroup: the wave-role mode every segment of the
-  // workgroup takes (0 or 2, which have specialised loops), else kClassGeneric
+  // workgroup takes (0 or 2, which have specialised loops), else kClassGeneric;
+  // a workgroup holding a segment of more than 64 rows runs all of its
+  // segments with the wide roles (class 5: 32 rows per wave).
+  bool any_wide = false;
   for (int b = 0; b < W_s; ++b) {
     int cls = -2;
+    bool big = false;
     for (int i = wg[b].x; i < wg[b].x + wg[b].y; ++i) {
       const StreamSeg& sgm = segs[i];
       const int nt = (sgm.q_count * g + 15) / 16;
+      big = big || sgm.q_count * g > kSegRows;
       const int md = nt >= 3 ? 0 : nt == 2 ? 1 : sgm.n_tiles >= kQuarterTiles ? 2 : 3;
       cls = cls == -2 ? md : cls == md ? cls : -1;
     }
-    wg[b].w = (cls == 0 || cls == 2) ? cls : kClassGeneric;
+    wg[b].w = big ? kClassWide : (cls == 0 || cls == 2) ? cls : kClassGeneric;
+    any_wide = any_wide || big;
   }
 
   // ---- partial slots and merge records per (query, KV head)
@@ -1454,7 +1719,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // direct-load loop so that a captured launch stays valid)
   int max_tiles = 0;
   for (int b = 0; b < W; ++b) max_tiles = std::max(max_tiles, wg[b].w == kTailRole ? 0 : wg[b].z);
-  info->stream_loop = (!caps && !(flags & BE_PLAN_NO_REGS) && max_tiles >= kRegsMinTiles) ? 1 : 0;
+  // (wide roles run in the direct-load loop only)
+  info->stream_loop = (!caps && !any_wide && !(flags & BE_PLAN_NO_REGS) && max_tiles >= kRegsMinTiles) ? 1 : 0;
   {
     // waves per record of the tail-and-merge kernel: spread a record's chunks
     // over 2 or 4 waves while all of them stay resident at once (two waves per

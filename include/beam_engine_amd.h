@@ -129,6 +129,8 @@ typedef struct be_level {
                                     merge kernel                                            */
 #define BE_PLAN_NO_REGS 32       /* streaming kernel: the direct-load loop whatever the runs'
                                     lengths (no register-staged loop)                       */
+#define BE_PLAN_NO_WIDE 64       /* streaming kernel: no wide wave roles (32 rows per wave)
+                                    and no 128-row segments for long many-query groups      */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the

@@ -238,21 +238,29 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
         first = int(np.argmax(role))
         assert role[first:].all()                          # tail roles are the last workgroups
     start = istart = 0
+    seg_cls = np.full(len(segs), -1)
     for b, (s0, ns, tiles, cls) in enumerate(wg):
         if cls == TAIL_ROLE:
             assert s0 == istart and tiles == 0
             istart += ns
             continue
-        assert cls in (0, 1, 2)                # wave-role mode 0 / 2, or per segment (1)
+        # wave-role mode 0 / 2, per segment (1), wide roles over up to 128 rows (5)
+        assert cls in (0, 1, 2, 5)
         if ns:
             assert s0 == start
             assert tiles == segs[s0:s0 + ns, 7].sum()
+            seg_cls[s0:s0 + ns] = cls
+            rows = segs[s0:s0 + ns, 1] * g
+            if cls == 5:
+                assert (rows > 64).any() and (rows <= 128).all()
+            else:
+                assert (rows <= 64).all()
         start += ns
     # coverage: every (query, KV head) sees exactly its tokens (segments: whole tiles from a
     # 64-aligned start; tail chunks: up to 16 tokens of one page), page by page
     seen = [[Counter() for _ in range(hkv)] for _ in range(nq)]
     for q0, qn, pb, t0, tc, head, slot, nt in segs:
-        assert tc > 0 and qn > 0 and qn * g <= 64 and t0 % 64 == 0 and nt == -(-tc // 64)
+        assert tc > 0 and qn > 0 and qn * g <= 128 and t0 % 64 == 0 and nt == -(-tc // 64)
         keys = [(int(pages[pb + t // page]), t % page) for t in range(t0, t0 + tc)]
         for q in range(q0, q0 + qn):
             seen[q][head].update(keys)
@@ -298,9 +306,10 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             c = cover.get((q, h), [])
             direct = len(c) == 1 and c[0] == -1 and not tails_of.get(q)
             assert ((q, h) in rec_keys) != direct
-    # the loop: register-staged when the longest run reaches 8 tiles (never for fixed layouts)
+    # the loop: register-staged when the longest run reaches 8 tiles (never for fixed layouts
+    # nor with wide-role workgroups, which run in the direct-load loop)
     assert info.stream_loop == (1 if int(wg[wg[:, 3] != TAIL_ROLE, 2].max(initial=0)) >= 8
-                                and not info.static_layout else 0)
+                                and not info.static_layout and not (wg[:, 3] == 5).any() else 0)
     return wg, segs, recs, rslots
 
 
@@ -349,6 +358,34 @@ def test_stream_plan_balances_tiles_across_workgroups(cus):
         cost = tiles + wg[:, 1]
         assert cost.max() - cost.min() <= 4
     assert info.num_merge == 32 * hkv           # every (query, head) merges prefix and suffix
+
+
+@pytest.mark.parametrize("beams,cus", [(32, 256), (32, 5), (18, 4), (64, 13), (64, 5), (10, 5)])
+def test_stream_plan_wide_roles(beams, cus):
+    """Long groups of more than 64 rows go to 128-row segments in wide-role
+    workgroups (class 5) when the launch gives every workgroup a long run (at
+    least 64 tiles of 64 rows each); BE_PLAN_NO_WIDE keeps 64-row segments;
+    every (query, KV head) still sees exactly its tokens."""
+    hq, hkv, page = 32, 8, 16
+    pre, suf = 96, 3                            # 1536-token prefix, 48-token suffixes
+    qo0, kvp0, kvi0 = [0, beams], [0, pre], list(range(pre))
+    qo1 = list(range(beams + 1))
+    kvp1 = list(range(0, (beams + 1) * suf, suf))
+    kvi1 = list(range(pre, pre + beams * suf))
+    levels = [(qo0, kvp0, kvi0, [16]), (qo1, kvp1, kvi1, [16] * beams)]
+    g = hq // hkv
+    tiles64 = (pre * page // 64) * -(-beams * g // 64) * hkv
+    expect = beams * g > 64 and tiles64 >= 64 * cus
+    for flags in (0, 64):
+        rc, info, buf, _lib, L = plan(levels, nq=beams, hq=hq, hkv=hkv, page=page, num_pages=pre + beams * suf,
+                                      cus=cus, flags=flags)
+        assert rc == 0, L.be_last_error()
+        wg, segs, recs, rslots = check_stream_plan(levels, beams, hq, hkv, page, info, buf)
+        rows = segs[:, 1] * g
+        if flags or not expect:
+            assert (rows <= 64).all() and not (wg[:, 3] == 5).any()
+        else:
+            assert rows.max() > 64 and (wg[:, 3] == 5).any() and info.stream_loop == 0
 
 
 def test_stream_plan_zero_records_for_keyless_queries():

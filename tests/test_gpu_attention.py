@@ -46,10 +46,11 @@ def make_q(n, hq, d, dtype, seed, scale=1.0):
 
 
 def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True, fused_merge=False, tile_kernel=False,
-                num_cus=None, no_regs=False):
+                num_cus=None, no_regs=False, no_wide=False):
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
     w._no_regs = no_regs
+    w._no_wide = no_wide
     w._force_valu = force_valu
     w._fused_merge = fused_merge
     w._tile_kernel = tile_kernel
@@ -344,9 +345,60 @@ def test_stream_and_tile_kernels(ws, shape, kernel, num_cus):
     if kernel != "tile":
         info = w._info
         wg = w._plan_dev[info.off_wg: info.off_wg + 4 * info.num_wg].view(-1, 4).cpu()
-        assert info.stream_loop == (1 if kernel == "stream" and int(wg[:, 2].max()) >= 8 else 0)
+        wide = bool(((wg[:, 3] == 4) | (wg[:, 3] == 5)).any())
+        assert info.stream_loop == (1 if kernel == "stream" and int(wg[:, 2].max()) >= 8 and not wide else 0)
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+@pytest.mark.parametrize("case", ["rows72", "rows100", "rows128", "rows256_g8", "mixed"])
+@pytest.mark.parametrize("cus", [None, 4, 7, 13])
+def test_stream_wide_roles(ws, case, cus):
+    """Wide wave roles (32 rows per wave, 128-row segments of long groups of
+    more than 64 rows) against the oracle and against the plan without them,
+    with ragged token counts (partial last tiles, split segments), row counts
+    that leave row groups empty, and shorter groups in the same launch.  They
+    apply when every workgroup's run is long (few CUs here); with all 256 CUs
+    the same shapes take 64-row segments."""
+    say(f"wide roles {case} cus={cus}")
+    page, hkv, d = 16, 8, 128
+    hq = 64 if case.endswith("g8") else 32
+    g = hq // hkv
+    s = 1 / math.sqrt(d)
+    gen = torch.Generator().manual_seed(sum(map(ord, case)))
+    if case == "mixed":
+        # requests of 10 / 32 / 18 beams (40 / 128 / 72 rows) over ragged prefixes
+        beams, prefixes = [10, 32, 18], [2000, 3100, 1613]
+    else:
+        beams = [int(case[4:].split("_")[0]) // g] * 2
+        prefixes = [3000, 1777]
+    # shared prefix per request, private ragged suffix per beam, all in one pool
+    pages = 0
+    lv0 = [[0], [0], [], []]
+    lv1 = [[0], [0], [], []]
+    for r, (b, pre) in enumerate(zip(beams, prefixes)):
+        pp = -(-pre // page)
+        lv0[2].extend(range(pages, pages + pp)); pages += pp
+        lv0[1].append(len(lv0[2])); lv0[3].append(pre - (pp - 1) * page); lv0[0].append(lv0[0][-1] + b)
+        for _ in range(b):
+            sfx = int(torch.randint(1, 200, (1,), generator=gen))
+            sp = -(-sfx // page)
+            lv1[2].extend(range(pages, pages + sp)); pages += sp
+            lv1[1].append(len(lv1[2])); lv1[3].append(sfx - (sp - 1) * page); lv1[0].append(lv1[0][-1] + 1)
+    levels = tuple([lv0[i], lv1[i]] for i in range(4))
+    n = lv0[0][-1]
+    kv = make_pool(pages, page, hkv, d, torch.bfloat16, 51, s)
+    q = make_q(n, hq, d, torch.bfloat16, 52, s)
+    (out, lse), w = run_cascade(ws, q, kv, levels, page, num_cus=cus)
+    info = w._info
+    wg = w._plan_dev[info.off_wg: info.off_wg + 4 * info.num_wg].view(-1, 4).cpu()
+    tiles64 = sum(-(-p // 64) * -(-b * g // 64) * hkv for b, p in zip(beams, prefixes))
+    expect = any(b * g > 64 for b in beams) and tiles64 >= 64 * info.num_wg
+    assert bool((wg[:, 3] == 5).any()) == expect
+    ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
+    check(out, lse, ref_o, ref_lse, torch.bfloat16)
+    (out2, lse2), _ = run_cascade(ws, q, kv, levels, page, num_cus=cus, no_wide=True)
+    torch.testing.assert_close(out.float(), out2.float(), rtol=2e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
