@@ -20,8 +20,10 @@ computed:
 from __future__ import annotations
 
 from dataclasses import dataclass
+import ctypes
 from typing import Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from .kv_tree_node import KVTreeNode
@@ -32,7 +34,7 @@ class TrieNode:
     """One page of tokens in the beam trie (beam_state.py:12-30)."""
 
     __slots__ = ("tokens", "parent", "children", "page_id", "_lvl", "_seg", "_seglen", "_reps", "_pre",
-                 "_stamp")
+                 "_stamp", "nid")
 
     def __init__(self, tokens: List[int], page_id: int, parent: Optional["TrieNode"] = None):
         self.tokens = tokens
@@ -40,6 +42,7 @@ class TrieNode:
         self.children: List["TrieNode"] = []
         self.page_id = page_id
         self._stamp = -1
+        self.nid = -1            # row in the owning state's node table (-1: not tracked)
         if parent:
             parent.children.append(self)
 
@@ -80,10 +83,52 @@ class BeamGenerateResult:
     children: List[BeamToken]
 
 
-class BeamState:
-    """Live candidates and their page trie (beam_state.py:62-683)."""
+class _NodeTable:
+    """Flat mirror of a trie for the native metadata builder: per node its
+    parent row (-1 for a root), page, token count, last token and liveness.
+    Rows follow creation order, so a parent's row is below its children's."""
 
-    def __init__(self, beam_size: int, page_table: PageTable):
+    def __init__(self, cap: int = 1024):
+        self.n = 0
+        self._alloc(cap)
+
+    def _alloc(self, cap):
+        old = getattr(self, "parent", None)
+        arrs = [np.full(cap, -1, np.int32), np.zeros(cap, np.int32), np.zeros(cap, np.int32),
+                np.zeros(cap, np.int32), np.zeros(cap, np.uint8)]
+        if old is not None:
+            for a, b in zip(arrs, (self.parent, self.page, self.ntok, self.last, self.alive)):
+                a[:self.n] = b[:self.n]
+        self.parent, self.page, self.ntok, self.last, self.alive = arrs
+
+    def add(self, node: "TrieNode") -> None:
+        if self.n == len(self.parent):
+            self._alloc(2 * len(self.parent))
+        i = self.n
+        self.n += 1
+        node.nid = i
+        self.parent[i] = node.parent.nid if node.parent is not None else -1
+        self.page[i] = node.page_id
+        self.ntok[i] = len(node.tokens)
+        self.last[i] = node.tokens[-1] if node.tokens else 0
+        self.alive[i] = 1
+
+    def append(self, node: "TrieNode", token: int) -> None:
+        i = node.nid
+        self.ntok[i] += 1
+        self.last[i] = token
+
+
+class BeamState:
+    """Live candidates and their page trie (beam_state.py:62-683).
+
+    ``fast_metadata``: keep a node table of the trie as it changes and build
+    each step's cascade arrays, write locations and positions natively
+    (``step_metadata``).  The table follows changes made through this class's
+    methods only, so it is for the engine's own states; a trie edited by hand
+    keeps the Python pass."""
+
+    def __init__(self, beam_size: int, page_table: PageTable, fast_metadata: bool = False):
         self.beam_size = beam_size
         self.page_table = page_table
         self.root: Optional[TrieNode] = None
@@ -93,6 +138,9 @@ class BeamState:
         self._cached_write_batch_indices = None
         self._cached_write_kv_indptr = None
         self._stamp = 0
+        self._tab: Optional[_NodeTable] = _NodeTable() if fast_metadata else None
+        self._meta_buf = np.zeros(1 << 16, np.int32)
+        self._meta_used = ctypes.c_int64(0)
 
     # ------------------------------------------------------------ building
     def add_root_sequence(self, sequence: List[int], request_id: int = 0) -> List[TrieNode]:
@@ -104,6 +152,8 @@ class BeamState:
         for start in range(0, len(sequence), ps):
             page = self.page_table.allocate_block()
             node = TrieNode(list(sequence[start:start + ps]), page, cur)
+            if self._tab is not None:
+                self._tab.add(node)
             created.append(node)
             if cur is None:
                 self.roots.append(node)
@@ -122,12 +172,15 @@ class BeamState:
         appends to the original page."""
         pt = self.page_table
         ps = pt.page_size
+        tab = self._tab
 
         for r in results:
             if not r.children:
                 node = r.candidate.trie_node
                 while node is not None and not node.children:
                     pt.free_block(node.page_id)
+                    if tab is not None:
+                        tab.alive[node.nid] = 0
                     parent = node.parent
                     if parent is not None:
                         parent.children.remove(node)
@@ -150,26 +203,36 @@ class BeamState:
                     child = children[0]
                     if len(tokens) < ps:
                         tokens.append(child.token_id)
+                        if tab is not None:
+                            tab.append(node, child.token_id)
                         new.append(BeamCandidate(node, child.accumulated_score, False, rid))
                     else:
                         page = pt.allocate_block()
-                        new.append(BeamCandidate(TrieNode([child.token_id], page, node),
-                                                 child.accumulated_score, False, rid))
+                        leaf = TrieNode([child.token_id], page, node)
+                        if tab is not None:
+                            tab.add(leaf)
+                        new.append(BeamCandidate(leaf, child.accumulated_score, False, rid))
                     continue
                 if len(tokens) == ps:
                     for child in children:
                         page = pt.allocate_block()
-                        new.append(BeamCandidate(TrieNode([child.token_id], page, node),
-                                                 child.accumulated_score, False, rid))
+                        leaf = TrieNode([child.token_id], page, node)
+                        if tab is not None:
+                            tab.add(leaf)
+                        new.append(BeamCandidate(leaf, child.accumulated_score, False, rid))
                 else:
                     first, rest = children[0], children[1:]
                     for child in rest:
                         page = pt.copy_block(node.page_id, len(node.tokens))
                         sib = TrieNode([*tokens, child.token_id], page, node.parent)
+                        if tab is not None:
+                            tab.add(sib)
                         if node.parent is None:          # forking a partial root page makes a new root
                             self.roots.append(sib)
                         new.append(BeamCandidate(sib, child.accumulated_score, False, rid))
                     tokens.append(first.token_id)
+                    if tab is not None:
+                        tab.append(node, first.token_id)
                     new.append(BeamCandidate(node, first.accumulated_score, False, rid))
         self.candidates = new
 
@@ -290,6 +353,44 @@ class BeamState:
                 qo.append(qo[-1] + cnt)
             levels.append((qo, kvp, kvi, lpl))
         return levels
+
+    def step_metadata(self):
+        """This step's cascade arrays and per-candidate inputs, built natively
+        from the node table (``fast_metadata`` states; else the Python pass).
+
+        Returns ``(levels, query_tokens, write_pages, write_slots, positions)``:
+        ``levels`` as ``_cascade_lists`` gives them (int32 arrays here), the
+        rest one int per candidate as ``query_token_ids``, ``write_locations``
+        and ``position_ids`` give them."""
+        tab = self._tab
+        cands = self.candidates
+        if tab is None or any(c.trie_node.nid < 0 for c in cands):
+            levels = self._cascade_lists()
+            wp, ws = self.write_locations()
+            return levels, self.query_token_ids(), wp, ws, self.position_ids(reuse_annotation=True)
+        from . import _lib
+        lib = _lib.load()
+        leaves = np.fromiter((c.trie_node.nid for c in cands), np.int32, len(cands))
+        while True:
+            buf = self._meta_buf
+            rc = lib.be_trie_cascade(tab.parent.ctypes.data, tab.page.ctypes.data, tab.ntok.ctypes.data,
+                                     tab.last.ctypes.data, tab.alive.ctypes.data, tab.n, leaves.ctypes.data,
+                                     len(cands), buf.ctypes.data, buf.size, ctypes.byref(self._meta_used))
+            if rc == _lib.BE_ERR_CAPACITY:
+                self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
+                continue
+            _lib.check(rc, "trie cascade metadata")
+            break
+        buf = self._meta_buf[: int(self._meta_used.value)].copy()
+        nl, oc = int(buf[0]), int(buf[1])
+        levels = []
+        for lv in range(nl):
+            ng, oq, op, oi, ol = (int(x) for x in buf[2 + 5 * lv: 7 + 5 * lv])
+            levels.append((buf[oq: oq + ng + 1], buf[op: op + ng + 1], buf[oi: oi + int(buf[op + ng])],
+                           buf[ol: ol + ng]))
+        n = len(cands)
+        return levels, buf[oc: oc + n], buf[oc + n: oc + 2 * n], buf[oc + 2 * n: oc + 3 * n], \
+            buf[oc + 3 * n: oc + 4 * n]
 
     def segment_tree(self):
         """The live trie's segments (the cascade's groups: unbranched page

@@ -6,12 +6,14 @@ with random 1024-token prompts, beam width 16, length penalty 1.0.  A bench
 step is one decode step of all 8 x 16 = 128 candidates; tokens/s = 128 x
 timed steps / timed wall time (prefill excluded).
 
-Every decode-attention launch in the run (warmup and timed) is bracketed by
-HIP events on the launch stream, with a third event between the attention
-kernel and the merge kernel.  The roofline reports the plan's algorithmic
-bytes against the mean duration of both kernels together: with the streaming
-kernel, short groups are attended inside the tail-and-merge kernel, so the
-pair is the unit that reads the plan's bytes.
+In every timed decode step one decode-attention launch -- that of layer
+(step mod 32), so every layer and every step of the run is sampled alike --
+is bracketed by two HIP events on the launch stream (events around all 32
+launches of a step cost about 4% of the step).  The roofline reports the plan's
+algorithmic bytes against the mean duration of both kernels of a launch
+together: with the streaming kernel, short groups are attended inside the
+tail-and-merge kernel, so the pair is the unit that reads the plan's bytes
+(each kernel's own share is in the rocprofv3 summaries).
 """
 
 from __future__ import annotations
@@ -38,15 +40,22 @@ def log(msg):
 
 
 class AttnTimer:
-    """Per-launch events: start -> attention kernel -> mid -> merge kernel -> end."""
+    """Events start -> attention kernel, merge kernel -> end around the launch
+    of layer (step mod layers) of every step."""
 
-    def __init__(self, kind: str, hkv: int, d: int, es: int):
-        self.records = []      # (start, mid, end, algorithmic bytes, flops)
+    def __init__(self, kind: str, hkv: int, d: int, es: int, layers: int):
+        self.records = []      # (start, end, algorithmic bytes, flops)
         self.kind = kind
         self.kernels = set()   # attention kernels the plans used
         self.hkv, self.d, self.es = hkv, d, es
+        self.layers = layers
+        self.step = -1
 
     def __call__(self, layer, run_fn, wrapper):
+        if layer == 0:
+            self.step += 1
+        if layer != self.step % self.layers:
+            return run_fn(None)
         st = wrapper.stats
         self.kernels.add(st.kernel)
         if self.kind == "flat":
@@ -55,11 +64,11 @@ class AttnTimer:
             kv = int(round(st.flops / (4.0 * self.d * hq))) * self.hkv * self.d * self.es * 2
         else:
             kv = st.kv_bytes
-        s, m, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        out = run_fn(lambda: m.record())
+        out = run_fn(None)
         e.record()
-        self.records.append((s, m, e, kv + st.qo_bytes, st.flops))
+        self.records.append((s, e, kv + st.qo_bytes, st.flops))
         return out
 
 
@@ -104,16 +113,17 @@ def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 
     rng = np.random.default_rng(seed)
     prompts = rng.integers(0, cfg.vocab_size, size=(n_req, prompt_len)).tolist()
     gen = BatchedBeamSearch(model, pt, beam, kernel_type=kernel_type, graphs=graphs)
-    timer = AttnTimer(kernel_type, cfg.num_key_value_heads, cfg.head_dim, 2) if time_attention else None
+    timer = AttnTimer(kernel_type, cfg.num_key_value_heads, cfg.head_dim, 2, cfg.num_hidden_layers) \
+        if time_attention else None
     t0 = time.perf_counter()
     gen.prefill(prompts)
     torch.cuda.synchronize()
     log(f"prefill {n_req} x {prompt_len} in {time.perf_counter() - t0:.1f} s")
-    gen.attn_timer = timer
     for _ in range(warmup):
         gen.step()
     torch.cuda.synchronize()
     log(f"{warmup} warmup steps done")
+    gen.attn_timer = timer
     t0 = time.perf_counter()
     for i in range(steps):
         gen.step()
@@ -125,18 +135,17 @@ def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 
 
 
 def summarize_attention(timer: AttnTimer):
-    attn_us, merge_us, byts, flops = [], [], 0, 0.0
-    for s, m, e, b, f in timer.records:
-        attn_us.append(s.elapsed_time(m) * 1e3)
-        merge_us.append(m.elapsed_time(e) * 1e3)
+    pair_us, byts, flops = [], 0, 0.0
+    for s, e, b, f in timer.records:
+        pair_us.append(s.elapsed_time(e) * 1e3)
         byts += b
         flops += f
-    n = len(attn_us)
-    tot = sum(attn_us) + sum(merge_us)
+    n = len(pair_us)
+    tot = sum(pair_us)
     gbs = byts / (tot * 1e-6) / 1e9
     return {
-        "launches": n, "mean_attn_us": sum(attn_us) / n, "mean_merge_us": sum(merge_us) / n,
-        "mean_pair_us": tot / n, "bytes_per_launch": byts / n, "gbs": gbs, "tflops": flops / (tot * 1e-6) / 1e12,
+        "launches": n, "mean_pair_us": tot / n, "bytes_per_launch": byts / n, "gbs": gbs,
+        "tflops": flops / (tot * 1e-6) / 1e12,
     }
 
 
@@ -217,8 +226,8 @@ def run_e2e_bench(args):
     tok_s = n * steps / wall
     traffic, traffic_src = profiled_traffic(kind, steps)
     att = summarize_attention(timer)
-    log(f"{kind}: {steps} steps in {wall:.2f} s -> {tok_s:.1f} tokens/s; attention {att['mean_attn_us']:.1f} us "
-        f"+ merge {att['mean_merge_us']:.1f} us per layer, {att['gbs']:.0f} GB/s over both")
+    log(f"{kind}: {steps} steps in {wall:.2f} s -> {tok_s:.1f} tokens/s; attention {att['mean_pair_us']:.1f} us "
+        f"per layer (both kernels), {att['gbs']:.0f} GB/s")
     result = {
         "metric": "beam-decode tokens/sec @ beam 16 (1 GPU)",
         "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -237,10 +246,10 @@ def run_e2e_bench(args):
                      "kernel": " / ".join(f"attn_{k}_kernel" for k in sorted(timer.kernels)) +
                                (" + tail_merge_kernel" if timer.kernels == {"stream"} else " + merge_kernel") +
                                " (decode attention: both kernels of a launch)",
-                     "launches": att["launches"], "bytes_per_launch": round(att["bytes_per_launch"]),
+                     "timed_launches": att["launches"],
+                     "timed_sample": "the launch of layer (step mod 32) in every timed step",
+                     "bytes_per_launch": round(att["bytes_per_launch"]),
                      "mean_launch_us": round(att["mean_pair_us"], 2),
-                     "mean_attention_kernel_us": round(att["mean_attn_us"], 2),
-                     "mean_merge_us": round(att["mean_merge_us"], 2),
                      "attention_tflops": round(att["tflops"], 2)},
     }
     if not getattr(args, "no_cpu_baseline", False):

@@ -30,6 +30,7 @@ from __future__ import annotations
 import time
 from typing import List, Optional, Sequence
 
+import numpy as np
 import torch
 
 from .attention import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAttentionWrapper
@@ -54,7 +55,7 @@ class BatchedBeamSearch:
         self.temperature = temperature
         self.include_self = include_self
         self.device = page_table.device
-        self.state = BeamState(beam_size, page_table)
+        self.state = BeamState(beam_size, page_table, fast_metadata=True)
         self.ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
         self.cascade = MultiLevelCascadeAttentionWrapper(1, self.ws)
         self.flat = BatchDecodeWithPagedKVCacheWrapper(self.ws)
@@ -121,22 +122,25 @@ class BatchedBeamSearch:
         n = len(st.candidates)
         kind = self.kernel_type
         levels = None
-        if kind == "tree":
-            levels = st.tree_lists(self._get_picker().model.absorb)
-        elif kind == "auto":
-            plan = self._get_picker().choose(st)
-            kind, levels = plan.kind, plan.levels
+        if kind == "cascade":
+            # the cascade arrays and the candidates' inputs from the native builder
+            levels, qids, wp, wpos, pos = st.step_metadata()
+        else:
+            if kind == "tree":
+                levels = st.tree_lists(self._get_picker().model.absorb)
+            elif kind == "auto":
+                plan = self._get_picker().choose(st)
+                kind, levels = plan.kind, plan.levels
         w = self._plan(kind, levels)
-        qids = st.query_token_ids()
-        wp, wpos = st.write_locations()
-        pos = st.position_ids(reuse_annotation=True)     # _plan's metadata pass just ran
+        if self.kernel_type != "cascade":
+            qids = st.query_token_ids()
+            wp, wpos = st.write_locations()
+            pos = st.position_ids(reuse_annotation=True)     # _plan's metadata pass just ran
         if self._staging.numel() < 4 * n:
             self._staging = torch.empty(8 * n, dtype=torch.int64, pin_memory=True)
         stg = self._staging[: 4 * n].view(4, n)
-        stg[0] = torch.tensor(qids)
-        stg[1] = torch.tensor(wp)
-        stg[2] = torch.tensor(wpos)
-        stg[3] = torch.tensor(pos)
+        for i, v in enumerate((qids, wp, wpos, pos)):
+            stg[i] = torch.from_numpy(v) if isinstance(v, np.ndarray) else torch.tensor(v)
         dev = stg.to(self.device, non_blocking=True)
         tok, wpg, wps, psn = dev[0], dev[1].to(torch.int32), dev[2].to(torch.int32), dev[3]
 

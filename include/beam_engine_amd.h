@@ -25,6 +25,8 @@
  *   be_beam_topk      log_softmax + per-row topk (src/beam_engine/beam.py:269-276, prefill
  *                     :105-141) and VanillaBeamSearchStrategy.select_candidates
  *                     (src/beam_engine/beam_strategy.py:433-488)
+ *   be_trie_cascade   BeamState.get_cascade_input (src/beam_engine/beam_state.py:211-412) and the
+ *                     per-step write locations / position ids (src/beam_engine/beam.py:180-221)
  */
 #ifndef BEAM_ENGINE_AMD_H
 #define BEAM_ENGINE_AMD_H
@@ -206,6 +208,23 @@ int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int nu
                  int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype,
                  int flags, int num_cus, const be_plan_caps* caps, int32_t* host_plan,
                  int64_t host_plan_capacity, be_attn_plan_info* info);
+
+/* ------------------------------------------------------------------ trie metadata
+ * be_trie_cascade (host only): the per-level cascade index arrays of a live
+ * beam trie -- what the reference's BeamState.get_cascade_input builds by
+ * walking every candidate's path in Python (beam_state.py:211-412), with its
+ * grouping, ordering and last_page_len rules -- plus each candidate's query
+ * token, write page / slot and position (beam.py:180-221).
+ * The trie is a node table: node n has parent[n] (-1 for a root, else an
+ * older live node), page[n], ntok[n] tokens, last_tok[n] (its last token)
+ * and alive[n]; leaves[c] is candidate c's node.  out receives int32 words:
+ * [num_levels L, off_cand], L records [groups, off_qo, off_kv_indptr,
+ * off_kv_indices, off_last_page_len] (word offsets into out), the arrays,
+ * and at off_cand four arrays of num_cands: query tokens, write pages, write
+ * slots, positions.  *out_used is the word count (also on BE_ERR_CAPACITY). */
+int be_trie_cascade(const int32_t* parent, const int32_t* page, const int32_t* ntok, const int32_t* last_tok,
+                    const uint8_t* alive, int num_nodes, const int32_t* leaves, int num_cands, int32_t* out,
+                    int64_t out_capacity, int64_t* out_used);
 
 /* be_attn_run: o[i, h] = softmax(sm_scale * q[i, h] . K^T) V over query i's
  * groups on every level, merged by log-sum-exp; query head h reads KV head

@@ -108,7 +108,7 @@ def test_product_random_runs_match_oracle(seed):
     o_alloc = OracleAllocator(20000, page)
     o = OracleBeamState(beam, o_alloc)
     pages = RecordingPages(20000, page)
-    p = BeamState(beam, pages)
+    p = BeamState(beam, pages, fast_metadata=True)
     o.add_root_sequence(prompt)
     p.add_root_sequence(prompt)
     first = [(1000 + j, -0.25 * j) for j in range(beam)]
@@ -137,7 +137,58 @@ def test_product_random_runs_match_oracle(seed):
         assert p.query_token_ids() == qids
         assert p.position_ids() == o.position_ids()
         assert p.write_locations() == o.write_locations()
+        # the native builder over the state's node table gives the same arrays
+        nlv, nq, nwp, nws, npos = p.step_metadata()
+        assert [l[0].tolist() for l in nlv] == qo and [l[1].tolist() for l in nlv] == kvp
+        assert [l[2].tolist() for l in nlv] == kvi and [l[3].tolist() for l in nlv] == lpl
+        assert nq.tolist() == qids and npos.tolist() == o.position_ids()
+        assert (nwp.tolist(), nws.tolist()) == tuple(o.write_locations())
     assert p.get_final_sequences(beam) == o.get_final_sequences(beam)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_native_metadata_on_random_forests(seed):
+    """Several requests in one state (forest), including partial root pages
+    forked into new roots and whole requests dying: the native builder equals
+    the Python pass at every step."""
+    rng = random.Random(100 + seed)
+    page = rng.choice([2, 4, 16])
+    beam = rng.choice([2, 4, 8])
+    pages = RecordingPages(50000, page)
+    st = BeamState(beam, pages, fast_metadata=True)
+    for r in range(rng.randint(1, 4)):
+        st.add_root_sequence(list(range(rng.randint(1, 3 * page))), request_id=r)
+    for step in range(30):
+        res = []
+        by_req = {}
+        for i, c in enumerate(st.candidates):
+            by_req.setdefault(c.request_id, []).append(i)
+        chosen = {}
+        for r, idx in by_req.items():
+            if step == 10 and r == 0 and len(by_req) > 1:
+                continue                              # request 0 dies: its whole tree is pruned
+            pool = [(i, rng.randrange(50), st.candidates[i].score - rng.random()) for i in idx
+                    for _ in range(2 * beam)]
+            pool.sort(key=lambda t: t[2], reverse=True)
+            for i, t, sc in pool[:beam]:
+                chosen.setdefault(i, []).append(BeamToken(t, sc))
+        res = [BeamGenerateResult(c, chosen.get(i, [])) for i, c in enumerate(st.candidates)]
+        st.add_filtered_results(res)
+        lv = st._cascade_lists()
+        nlv, nq, nwp, nws, npos = st.step_metadata()
+        assert [tuple(x.tolist() for x in l) for l in nlv] == [tuple(l) for l in lv]
+        assert nq.tolist() == st.query_token_ids()
+        assert (nwp.tolist(), nws.tolist()) == tuple(st.write_locations())
+        assert npos.tolist() == st.position_ids()
+
+
+def test_native_metadata_needs_tracked_nodes():
+    """A hand-built trie (nodes not made by the state) takes the Python pass."""
+    tree = FX["trees"]["uneven"]
+    st = build_product(tree)
+    st._tab = __import__("beam_engine_amd.beam_state", fromlist=["_NodeTable"])._NodeTable()
+    lv, q, wp, ws, pos = st.step_metadata()
+    assert lv == st._cascade_lists() and q == st.query_token_ids()
 
 
 def test_forest_of_requests_groups_by_root():
