@@ -11,7 +11,7 @@ from .attention import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAtte
 from .attention_mode import AttentionMode
 from .beam_state import (BeamCandidate, BeamGenerateInput, BeamGenerateResult, BeamState, BeamToken,
                          BeamTokenCandidate, TrieNode)
-from .beam_strategy import BeamStrategy, VanillaBeamSearchStrategy
+from .beam_strategy import BeamStrategy, DiverseBeamSearchStrategy, VanillaBeamSearchStrategy
 from .kv_tree_node import KVTreeNode
 from .page_table import PageTable
 from .selection import beam_topk, decode_k
@@ -19,7 +19,7 @@ from .selection import beam_topk, decode_k
 __all__ = [
     "AttentionMode", "BatchDecodeWithPagedKVCacheWrapper", "BeamCandidate", "BeamGenerateInput",
     "BeamGenerateResult", "BeamState", "BeamStrategy", "BeamToken", "BeamTokenCandidate", "KVTreeNode",
-    "MultiLevelCascadeAttentionWrapper", "PageTable", "TrieNode", "VanillaBeamSearchStrategy", "beam_topk",
+    "MultiLevelCascadeAttentionWrapper", "PageTable", "TrieNode", "VanillaBeamSearchStrategy", "DiverseBeamSearchStrategy", "beam_topk",
     "decode_k", "merge_state",
 ]
 

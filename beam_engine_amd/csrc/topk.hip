@@ -473,6 +473,113 @@ __global__ __launch_bounds__(kTopkThreads) void topk_global_kernel(int n_rows, i
   }
 }
 
+// ---------------------------------------------------------------- diverse selection
+// Diverse beam search with the Hamming penalty (beam_strategy.py:173-312),
+// one workgroup per request over its pool of row top-k choices (row-major:
+// choice i = (row rb + i / k, rank i % k)).  Groups pick in turn, each
+// max(1, beam / groups) choices not yet taken, by
+//   (log_prob - penalty * [token taken by an earlier group]) descending,
+// ties to the higher log_prob, then the lower pool position -- the order of the
+// reference's two stable sorts (by log_prob over the pool in row order, then by
+// the adjusted score; its length normalisation divides every choice of a step
+// by the same positive factor and leaves that order unchanged).  The picks are
+// emitted grouped by row (rows ascending, each row's children in pick order);
+// beyond beam entries the last ones are dropped.
+struct DivKey {
+  double adj;
+  float lp;
+  int pos;
+};
+__device__ __forceinline__ bool div_better(const DivKey& a, const DivKey& b) {
+  if (a.pos < 0) return false;
+  if (b.pos < 0) return true;
+  if (a.adj != b.adj) return a.adj > b.adj;
+  if (a.lp != b.lp) return a.lp > b.lp;
+  return a.pos < b.pos;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_diverse_kernel(int n_rows, int k, int beam, int groups,
+                                                                   double penalty, const int32_t* req_row_ptr,
+                                                                   const double* parent, const float* row_vals,
+                                                                   const int32_t* row_idx, int32_t* out_parent,
+                                                                   int32_t* out_token, double* out_score) {
+  __shared__ uint8_t state[kMaxPool];        // bit 0: taken; bit 1: token taken by an earlier group
+  __shared__ int picks[kMaxK];                // pool positions in pick order
+  __shared__ int pick_tok[kMaxK];
+  __shared__ DivKey red[kTopkThreads];
+  __shared__ int n_picks;
+  const int tid = threadIdx.x;
+  const int req = blockIdx.x;
+  const int rb = req_row_ptr ? req_row_ptr[req] : 0;
+  const int re = req_row_ptr ? req_row_ptr[req + 1] : n_rows;
+  int32_t* op = out_parent + (int64_t)req * beam;
+  int32_t* ot = out_token + (int64_t)req * beam;
+  double* os = out_score + (int64_t)req * beam;
+  const bool ok = rb >= 0 && re <= n_rows && rb <= re && (int64_t)(re - rb) * k <= kMaxPool;
+  const int n = ok ? (re - rb) * k : 0;
+  const float* vals = row_vals + (int64_t)rb * k;
+  const int32_t* toks = row_idx + (int64_t)rb * k;
+  const int per = max(1, beam / groups);
+  for (int i = tid; i < n; i += kTopkThreads) state[i] = 0;
+  if (tid == 0) n_picks = 0;
+  __syncthreads();
+  for (int g = 0; g < groups; ++g) {
+    const int n0 = n_picks;                   // tokens taken by earlier groups: pick_tok[0, n0)
+    for (int i = tid; i < n; i += kTopkThreads) {
+      bool hit = false;
+      const int t = toks[i];
+      for (int j = 0; j < n0; ++j) hit = hit || pick_tok[j] == t;
+      state[i] = (uint8_t)((state[i] & 1) | (hit ? 2 : 0));
+    }
+    __syncthreads();
+    for (int s = 0; s < per; ++s) {
+      DivKey best{0.0, 0.f, -1};
+      for (int i = tid; i < n; i += kTopkThreads) {
+        if (state[i] & 1) continue;
+        const DivKey c{(double)vals[i] - ((state[i] & 2) ? penalty : 0.0), vals[i], i};
+        if (div_better(c, best)) best = c;
+      }
+      red[tid] = best;
+      __syncthreads();
+      for (int w = kTopkThreads / 2; w > 0; w >>= 1) {
+        if (tid < w && div_better(red[tid + w], red[tid])) red[tid] = red[tid + w];
+        __syncthreads();
+      }
+      const int win = red[0].pos;
+      if (win < 0) break;                     // (uniform: every thread reads red[0])
+      if (tid == 0) {
+        state[win] |= 1;
+        picks[n_picks] = win;
+        pick_tok[n_picks] = toks[win];
+        n_picks += 1;
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  const int cnt = n_picks;
+  const int keep = min(cnt, beam);
+  // emission rank of pick q: picks of lower rows, then earlier picks of its own row
+  for (int q = tid; q < cnt; q += kTopkThreads) {
+    const int p = picks[q], row = p / k;
+    int rank = 0;
+    for (int j = 0; j < cnt; ++j) {
+      const int rj = picks[j] / k;
+      rank += (rj < row) || (rj == row && j < q);
+    }
+    if (rank < keep) {
+      op[rank] = rb + row;
+      ot[rank] = toks[p];
+      os[rank] = parent[rb + row] + (double)vals[p];
+    }
+  }
+  for (int i = keep + tid; i < beam; i += kTopkThreads) {
+    op[i] = -1;
+    ot[i] = -1;
+    os[i] = -INFINITY;
+  }
+}
+
 }  // namespace be
 
 extern "C" {
@@ -544,6 +651,29 @@ int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t r
                                                               row_vals, row_idx, out_parent, out_token, out_score);
     BE_HIP_CHECK(hipGetLastError());
   }
+  return BE_OK;
+}
+
+int be_diverse_select(const float* row_vals, const int32_t* row_idx, int n_rows, int k, const double* parent_scores,
+                      int n_req, const int32_t* req_row_ptr, int max_req_rows, int beam, int num_groups,
+                      double diversity_penalty, int32_t* out_parent, int32_t* out_token, double* out_score,
+                      void* stream) {
+  BE_REQUIRE(row_vals && row_idx && parent_scores && out_parent && out_token && out_score, "null pointer");
+  BE_REQUIRE(n_rows > 0 && k >= 1, "empty pool");
+  BE_REQUIRE(beam >= 1 && num_groups >= 1, "beam and num_groups must be positive");
+  if (beam > be::kMaxK || num_groups > be::kMaxK)
+    return be::fail(BE_ERR_UNSUPPORTED, "beam %d / groups %d exceed %d", beam, num_groups, be::kMaxK);
+  BE_REQUIRE(isfinite(diversity_penalty), "diversity penalty must be finite");
+  BE_REQUIRE(n_req >= 1 && n_req <= 65535 && (req_row_ptr != nullptr || n_req == 1), "bad request partition");
+  const int rows = req_row_ptr ? max_req_rows : n_rows;
+  BE_REQUIRE(rows >= 0 && rows <= n_rows, "max_req_rows outside [0, n_rows]");
+  if ((int64_t)rows * k > be::kMaxPool)
+    return be::fail(BE_ERR_UNSUPPORTED, "pool %d x %d exceeds %d entries", rows, k, be::kMaxPool);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  be::topk_diverse_kernel<<<n_req, be::kTopkThreads, 0, st>>>(n_rows, k, beam, num_groups, diversity_penalty,
+                                                             req_row_ptr, parent_scores, row_vals, row_idx,
+                                                             out_parent, out_token, out_score);
+  BE_HIP_CHECK(hipGetLastError());
   return BE_OK;
 }
 

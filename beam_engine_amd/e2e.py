@@ -98,7 +98,7 @@ def use_tuned_gemms(path: str = None) -> bool:
 
 def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 8, beam: int = 16,
             prompt_len: int = 1024, cfg: LlamaConfig = None, seed: int = 0, time_attention: bool = True,
-            max_pages: int = 8192, graphs: bool = True, tuned_gemms: bool = True):
+            max_pages: int = 8192, graphs: bool = True, tuned_gemms: bool = True, selection: str = "vanilla"):
     cfg = cfg or LlamaConfig.llama3_8b()
     dev = torch.device("cuda")
     tuned = use_tuned_gemms() if tuned_gemms else False
@@ -112,7 +112,11 @@ def run_e2e(steps: int, warmup: int, kernel_type: str = "cascade", n_req: int = 
         f"ready in {time.perf_counter() - t0:.1f} s")
     rng = np.random.default_rng(seed)
     prompts = rng.integers(0, cfg.vocab_size, size=(n_req, prompt_len)).tolist()
-    gen = BatchedBeamSearch(model, pt, beam, kernel_type=kernel_type, graphs=graphs)
+    strategy = None
+    if selection == "diverse":
+        from .beam_strategy import DiverseBeamSearchStrategy
+        strategy = DiverseBeamSearchStrategy(num_groups=4, diversity_penalty=0.5)
+    gen = BatchedBeamSearch(model, pt, beam, strategy=strategy, kernel_type=kernel_type, graphs=graphs)
     timer = AttnTimer(kernel_type, cfg.num_key_value_heads, cfg.head_dim, 2, cfg.num_hidden_layers) \
         if time_attention else None
     t0 = time.perf_counter()
@@ -221,10 +225,12 @@ def run_e2e_bench(args):
     steps = args.steps if args.steps is not None else 250
     warmup = args.warmup if args.warmup is not None else 5
     kind = args.strategy
-    gen, timer, wall, model, pt = run_e2e(steps, warmup, kind, graphs=not getattr(args, "no_graphs", False))
+    selection = getattr(args, "selection", "vanilla")
+    gen, timer, wall, model, pt = run_e2e(steps, warmup, kind, graphs=not getattr(args, "no_graphs", False),
+                                          selection=selection)
     n = len(gen.state.candidates)
     tok_s = n * steps / wall
-    traffic, traffic_src = profiled_traffic(kind, steps)
+    traffic, traffic_src = profiled_traffic(kind, steps) if selection == "vanilla" else (None, None)
     att = summarize_attention(timer)
     log(f"{kind}: {steps} steps in {wall:.2f} s -> {tok_s:.1f} tokens/s; attention {att['mean_pair_us']:.1f} us "
         f"per layer (both kernels), {att['gbs']:.0f} GB/s")
@@ -234,7 +240,8 @@ def run_e2e_bench(args):
         "ms_per_step": round(wall / steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: random-init weights N(0,0.02), random token-id prompts",
-        "config": {"workload": f"e2e beam search, Llama-3-8B shape, {kind} attention",
+        "config": {"workload": f"e2e beam search, Llama-3-8B shape, {kind} attention"
+                               + (", diverse beam search (4 groups, Hamming penalty 0.5)" if selection == "diverse" else ""),
                    "requests": 8, "beam": 16, "prompt_len": 1024, "decode_steps": warmup + steps,
                    "layers": model.cfg.num_hidden_layers, "page_size": 16, "length_penalty": 1.0,
                    "per_request_tokens_per_s": round(tok_s / 8, 2),

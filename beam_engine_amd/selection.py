@@ -129,3 +129,62 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
             outs = (hp.clone(), ht.clone(), hs.clone())
         return row_vals, row_idx, outs
     return row_vals, row_idx
+
+
+def diverse_select(row_vals: torch.Tensor, row_idx: torch.Tensor, parent_scores: torch.Tensor, beam: int,
+                   num_groups: int, diversity_penalty: float, request_rows: Optional[Sequence[int]] = None,
+                   to_host: bool = True):
+    """Diverse beam search with the Hamming penalty over a row top-k already on
+    the device (``row_vals [N, k]`` f32, ``row_idx [N, k]`` i32, as returned by
+    ``beam_topk``): ``be_diverse_select`` per request.  Returns ``(parent,
+    token, score)`` of ``R * beam`` entries (request q's at ``[q * beam, (q +
+    1) * beam)``, grouped by row, unused entries parent -1); on the host with
+    ``to_host`` (one synchronisation)."""
+    lib = _lib.load()
+    for t, nm in ((row_vals, "row_vals"), (row_idx, "row_idx")):
+        _lib.require_device(t, nm)
+    if row_vals.dim() != 2 or row_vals.shape != row_idx.shape:
+        raise ValueError("row_vals and row_idx must be [N, k] of the same shape")
+    if row_vals.dtype != torch.float32 or row_idx.dtype != torch.int32:
+        raise ValueError("row_vals must be float32 and row_idx int32")
+    n, k = row_vals.shape
+    dev = row_vals.device
+    row_vals, row_idx = row_vals.contiguous(), row_idx.contiguous()
+    if parent_scores.numel() != n:
+        raise ValueError("parent_scores must have one entry per row")
+    if parent_scores.device.type == "cpu":
+        host = _staging(dev, "dbs_parents", n, torch.float64)
+        host.copy_(parent_scores.reshape(-1))
+        ps = host.to(dev, non_blocking=True)
+    else:
+        ps = parent_scores.to(dtype=torch.float64).contiguous()
+    n_req, max_rows, ptr_dev = 1, n, None
+    if request_rows is not None:
+        rows = tuple(int(x) for x in request_rows)
+        if sum(rows) != n or min(rows, default=0) < 0:
+            raise ValueError("request_rows must partition the rows")
+        n_req, max_rows = len(rows), max(rows)
+        key = (dev.type, dev.index, rows)
+        ptr_dev = _row_ptrs.get(key)
+        if ptr_dev is None:
+            if len(_row_ptrs) > 64:
+                _row_ptrs.clear()
+            ptr_dev = _row_ptrs[key] = torch.tensor(np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)).to(dev)
+    outs = (torch.empty(n_req * beam, dtype=torch.int32, device=dev),
+            torch.empty(n_req * beam, dtype=torch.int32, device=dev),
+            torch.empty(n_req * beam, dtype=torch.float64, device=dev))
+    rc = lib.be_diverse_select(row_vals.data_ptr(), row_idx.data_ptr(), n, k, ps.data_ptr(), n_req,
+                               _lib.ptr(ptr_dev), max_rows, beam, num_groups, float(diversity_penalty),
+                               outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(rc, "diverse selection")
+    if not to_host:
+        return outs
+    m = outs[0].numel()
+    hp = _staging(dev, "dbs_parent", m, torch.int32)
+    ht = _staging(dev, "dbs_token", m, torch.int32)
+    hs = _staging(dev, "dbs_score", m, torch.float64)
+    hp.copy_(outs[0], non_blocking=True)
+    ht.copy_(outs[1], non_blocking=True)
+    hs.copy_(outs[2], non_blocking=True)
+    torch.cuda.current_stream(dev).synchronize()
+    return hp.clone(), ht.clone(), hs.clone()

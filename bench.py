@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
+    ap.add_argument("--selection", default="vanilla", choices=["vanilla", "diverse"],
+                    help="e2e: beam selection (vanilla, or diverse beam search with 4 groups)")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true", help="e2e: launch every op eagerly (no HIP graphs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")

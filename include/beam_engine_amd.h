@@ -25,6 +25,8 @@
  *   be_beam_topk      log_softmax + per-row topk (src/beam_engine/beam.py:269-276, prefill
  *                     :105-141) and VanillaBeamSearchStrategy.select_candidates
  *                     (src/beam_engine/beam_strategy.py:433-488)
+ *   be_diverse_select DiverseBeamSearchStrategy.select_candidates, Hamming diversity
+ *                     (src/beam_engine/beam_strategy.py:173-312)
  *   be_trie_cascade   BeamState.get_cascade_input (src/beam_engine/beam_state.py:211-412) and the
  *                     per-step write locations / position ids (src/beam_engine/beam.py:180-221)
  */
@@ -208,6 +210,21 @@ int be_attn_plan(const be_level* levels, int num_levels, int num_queries, int nu
                  int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype,
                  int flags, int num_cus, const be_plan_caps* caps, int32_t* host_plan,
                  int64_t host_plan_capacity, be_attn_plan_info* info);
+
+/* be_diverse_select: diverse beam search selection with the Hamming penalty
+ * (DiverseBeamSearchStrategy.select_candidates, src/beam_engine/beam_strategy.py:173-312)
+ * over the row top-k that be_beam_topk wrote (row_vals / row_idx, [n_rows, k],
+ * rows in candidate order).  Per request (rows [req_row_ptr[r], req_row_ptr[r+1]),
+ * or all rows when req_row_ptr is NULL and n_req == 1): num_groups groups pick
+ * max(1, beam / num_groups) choices each, by log_prob - diversity_penalty when
+ * an earlier group took the token, ties to the higher log_prob, then the
+ * earlier (row, rank); the picks come out grouped by row (children in pick
+ * order), at most beam of them: out_* [n_req * beam] as be_beam_topk's (parent
+ * = global row, -1 for unused entries; score = parent_scores[row] + log_prob). */
+int be_diverse_select(const float* row_vals, const int32_t* row_idx, int n_rows, int k, const double* parent_scores,
+                      int n_req, const int32_t* req_row_ptr, int max_req_rows, int beam, int num_groups,
+                      double diversity_penalty, int32_t* out_parent, int32_t* out_token, double* out_score,
+                      void* stream);
 
 /* ------------------------------------------------------------------ trie metadata
  * be_trie_cascade (host only): the per-level cascade index arrays of a live

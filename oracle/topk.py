@@ -127,3 +127,69 @@ def prefill_select(logits_row: np.ndarray, beam_size: int, dtype: str = "float32
     vals, idx = row_topk(logp, k)
     b = min(beam_size, k)
     return [(int(idx[0, j]), float(vals[0, j])) for j in range(b)]
+
+
+def diverse_select(parent_scores, top_vals: np.ndarray, top_idx: np.ndarray, beam_size: int, num_groups: int,
+                   diversity_penalty: float, diversity_type: str = "hamming", length_penalty: float = 1.0,
+                   parent_sequences=None):
+    """Diverse beam search selection (beam_strategy.py:173-312), restated step
+    by step: the pool of (row, token, log_prob) choices in (row, rank) order is
+    stably sorted by log_prob; group g (of ``num_groups``, ``max(1, B // G)``
+    slots each) scores every not yet selected choice as
+    ``(log_prob - penalty) / len ** length_penalty`` (``len`` = parent
+    sequence length + 1; no division when the penalty exponent is 0), where
+    the Hamming penalty applies to a token already chosen by an earlier group
+    this step and the cumulative one is the mean positional overlap with the
+    sequences chosen so far times the penalty; a stable sort picks the group's
+    slots.  Children are regrouped per row (selection order) with
+    ``parent_score + log_prob``; a total above B is cut from the last rows'
+    last children.  ``parent_sequences[r]`` (token lists) are needed for the
+    cumulative type and for ``len``; without them every parent has length 0.
+    Returns ``(per_row_children, flat)`` as ``select_global``."""
+    n, k = top_idx.shape
+    bpg = max(1, beam_size // num_groups)
+    seqs = parent_sequences if parent_sequences is not None else [[] for _ in range(n)]
+    choices = [(r, int(top_idx[r, j]), float(top_vals[r, j])) for r in range(n) for j in range(k)]
+    choices.sort(key=lambda c: c[2], reverse=True)                 # stable
+    selected = []                                                  # (row, token) in selection order
+    sel_keys = set()
+    sel_tokens = set()
+    sel_seqs = []
+    for _ in range(num_groups):
+        adjusted = []
+        for r, tok, lp in choices:
+            if (r, tok) in sel_keys:
+                continue
+            cand = list(seqs[r]) + [tok]
+            if diversity_type == "hamming":
+                pen = diversity_penalty if tok in sel_tokens else 0.0
+            else:
+                if sel_seqs:
+                    tot = 0.0
+                    for s in sel_seqs:
+                        tot += sum(1 for a, b in zip(cand, s) if a == b) * diversity_penalty
+                    pen = tot / len(sel_seqs)
+                else:
+                    pen = 0.0
+            adj = lp - pen
+            if length_penalty != 0:
+                adj = adj / (len(cand) ** length_penalty)
+            adjusted.append((r, tok, lp, adj))
+        adjusted.sort(key=lambda c: c[3], reverse=True)            # stable
+        for r, tok, lp, _ in adjusted[:bpg]:
+            selected.append((r, tok, lp))
+            sel_keys.add((r, tok))
+            sel_tokens.add(tok)
+            sel_seqs.append(list(seqs[r]) + [tok])
+    per_row: List[List[Tuple[int, float]]] = [[] for _ in range(n)]
+    for r, tok, lp in selected:
+        per_row[r].append((tok, float(parent_scores[r]) + lp))
+    extra = sum(len(c) for c in per_row) - beam_size
+    for r in range(n - 1, -1, -1):
+        while extra > 0 and per_row[r]:
+            per_row[r].pop()
+            extra -= 1
+        if extra <= 0:
+            break
+    flat = [(r, tok, sc) for r in range(n) for tok, sc in per_row[r]]
+    return per_row, flat
