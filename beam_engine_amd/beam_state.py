@@ -52,11 +52,15 @@ class TrieNode:
 
 @dataclass
 class BeamCandidate:
-    """A live beam: its leaf node and accumulated log-probability (beam_state.py:33-38)."""
+    """A live beam: its leaf node and accumulated log-probability (beam_state.py:33-38).
+    A beam finished by an end-of-sequence pick keeps its whole token sequence
+    (``sequence``, ending with the EOS token); its ``trie_node`` is the node it
+    was picked from."""
     trie_node: TrieNode
     score: float
     finished: bool = False
     request_id: int = 0
+    sequence: Optional[List[int]] = None
 
 
 @dataclass
@@ -163,13 +167,33 @@ class BeamState:
         self.candidates.append(BeamCandidate(cur, 0, False, request_id))
         return created
 
-    def add_filtered_results(self, results: List[BeamGenerateResult]) -> None:
+    def add_filtered_results(self, results: List[BeamGenerateResult], eos_token_id: Optional[int] = None) -> None:
         """Prune dead branches, then expand survivors with the reference's fork
         rules (beam_state.py:101-209): a single child appends to a non-full
         page or opens a new page; several children of a full page open one
         page each; several children of a partial page copy it for every child
         after the first (siblings under the same parent), then the first child
-        appends to the original page."""
+        appends to the original page.
+
+        ``eos_token_id`` (the reference resolves one but never finishes a beam,
+        beam.py:68-69): a child with that token finishes its beam instead --
+        it joins ``finished_candidates`` with its sequence and score and takes
+        no page; the remaining children expand as above, and a candidate left
+        without children is pruned."""
+        if eos_token_id is not None:
+            kept = []
+            for r in results:
+                live = []
+                for ch in r.children:
+                    if ch.token_id == eos_token_id:
+                        c = r.candidate
+                        self.finished_candidates.append(BeamCandidate(
+                            c.trie_node, ch.accumulated_score, True, c.request_id,
+                            self.sequence(c) + [ch.token_id]))
+                    else:
+                        live.append(ch)
+                kept.append(r if len(live) == len(r.children) else BeamGenerateResult(r.candidate, live))
+            results = kept
         pt = self.page_table
         ps = pt.page_size
         tab = self._tab
@@ -632,6 +656,8 @@ class BeamState:
 
     # ------------------------------------------------------------ results
     def sequence(self, cand: BeamCandidate) -> List[int]:
+        if cand.sequence is not None:
+            return list(cand.sequence)
         seq: List[int] = []
         n = cand.trie_node
         parts = []

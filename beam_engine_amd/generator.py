@@ -23,6 +23,10 @@ cheaper of flat, fully split and tree under that model).  "flat", "tree" and
 reference's repetition of a shallow candidate's leaf group on deeper levels.
 ``include_self`` False follows the reference's cascade convention (a query
 does not attend to the K/V it appends in the same step, beam_state.py:347-354).
+``eos_token_id`` (off by default, as in the reference, which never finishes a
+beam): a pick of that token finishes its beam (``state.finished_candidates``)
+and the request continues with its other beams; steps whose candidate count
+differs from the captured one run eagerly.
 """
 
 from __future__ import annotations
@@ -44,7 +48,7 @@ class BatchedBeamSearch:
     def __init__(self, model, page_table: PageTable, beam_size: int,
                  strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
                  temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False,
-                 graphs: bool = False):
+                 graphs: bool = False, eos_token_id: Optional[int] = None):
         if kernel_type not in ("cascade", "flat", "tree", "auto"):
             raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat', 'tree' or 'auto'.")
         self.model = model
@@ -54,6 +58,7 @@ class BatchedBeamSearch:
         self.kernel_type = kernel_type
         self.temperature = temperature
         self.include_self = include_self
+        self.eos_token_id = eos_token_id    # a pick of this token finishes its beam (off: None)
         self.device = page_table.device
         self.state = BeamState(beam_size, page_table, fast_metadata=True)
         self.ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
@@ -120,6 +125,8 @@ class BatchedBeamSearch:
     def step(self) -> None:
         st = self.state
         n = len(st.candidates)
+        if n == 0:                  # every beam finished
+            return
         kind = self.kernel_type
         levels = None
         if kind == "cascade":
@@ -170,7 +177,7 @@ class BatchedBeamSearch:
 
     def _select(self, logits: torch.Tensor) -> None:
         st = self.state
-        st.add_filtered_results(self.strategy.select_batched(st, logits, self.temperature))
+        st.add_filtered_results(self.strategy.select_batched(st, logits, self.temperature), self.eos_token_id)
 
     # ---------------------------------------------------------------- results
     def final_sequences(self, num_return: Optional[int] = None):
@@ -181,7 +188,7 @@ class BatchedBeamSearch:
     def generate(self, prompts: Sequence[Sequence[int]], steps: int):
         self.prefill(prompts)
         for _ in range(steps):
-            if self.strategy.should_stop(self.state, 1 << 30, 0):
+            if not self.state.candidates or self.strategy.should_stop(self.state, 1 << 30, 0):
                 break
             self.step()
         return self.final_sequences()

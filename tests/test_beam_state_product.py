@@ -220,3 +220,60 @@ def test_fasttree_structure_is_bfs_with_cumulative_seqlen():
     assert [n.seqlen for n in nodes] == [2, 4, 6, 5, 5, 7]
     assert [n.parent for n in nodes] == [-1, 0, 0, 1, 1, 2]
     assert nodes[0].requests == [0, 1, 2]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_eos_finishes_beams_without_pages(seed):
+    """With an end-of-sequence token, a pick of it finishes its beam (score,
+    whole sequence ending with the token, no page); the trie evolves exactly as
+    the oracle's with those picks removed, so page ids, copies and candidates
+    stay the reference's."""
+    rng = random.Random(200 + seed)
+    page, beam, eos = rng.choice([2, 4]), 4, 7
+    o_alloc = OracleAllocator(20000, page)
+    o = OracleBeamState(beam, o_alloc)
+    pages = RecordingPages(20000, page)
+    p = BeamState(beam, pages, fast_metadata=True)
+    prompt = list(range(20, 20 + rng.randint(1, 9)))
+    o.add_root_sequence(prompt)
+    p.add_root_sequence(prompt)
+    first = [(100 + j, -0.25 * j) for j in range(beam)]
+    o.add_filtered_results([OResult(o.candidates[0], first)])
+    p.add_filtered_results([BeamGenerateResult(p.candidates[0], [BeamToken(t, s) for t, s in first])], eos)
+    n_fin = 0
+    for step in range(25):
+        if not p.candidates:
+            break
+        pool = []
+        for ci, c in enumerate(p.candidates):
+            for j in range(2 * beam):
+                pool.append((ci, eos if rng.random() < 0.08 else rng.randrange(30), c.score - rng.random()))
+        pool.sort(key=lambda t: t[2], reverse=True)
+        chosen, seen = [], set()
+        for ci, t, s in pool:
+            if (ci, t) not in seen and len(chosen) < beam:
+                seen.add((ci, t))
+                chosen.append((ci, t, s))
+        p_res = [BeamGenerateResult(c, [BeamToken(t, s) for ci2, t, s in chosen if ci2 == ci])
+                 for ci, c in enumerate(p.candidates)]
+        # finished in result order (candidates in order, children in order)
+        expect_fin = [(p.sequence(r.candidate) + [eos], ch.accumulated_score) for r in p_res for ch in r.children
+                      if ch.token_id == eos]
+        o_res = [OResult(c, [(t, s) for ci2, t, s in chosen if ci2 == ci and t != eos])
+                 for ci, c in enumerate(o.candidates)]
+        p.add_filtered_results(p_res, eos)
+        o.add_filtered_results(o_res)
+        got_fin = [(c.sequence, c.score) for c in p.finished_candidates[n_fin:]]
+        assert got_fin == expect_fin and all(c.finished for c in p.finished_candidates)
+        n_fin = len(p.finished_candidates)
+        assert o_alloc.copies == pages.copies and list(o_alloc.free_pages) == list(pages.free_pages)
+        assert [(c.node.page_id, c.node.tokens, c.score) for c in o.candidates] == \
+            [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in p.candidates]
+        if p.candidates:
+            nlv, *_ = p.step_metadata()
+            assert [tuple(x.tolist() for x in l) for l in nlv] == [tuple(l) for l in p._cascade_lists()]
+    final = p.get_final_sequences(100)
+    assert len(final) == len(p.finished_candidates) + len(p.candidates)
+    # finished beams end with the token; live ones never carry it (an EOS pick never continues)
+    assert n_fin > 0 and sum(seq[-1] == eos for seq, _ in final) == n_fin
+    assert all(eos not in p.sequence(c) for c in p.candidates)

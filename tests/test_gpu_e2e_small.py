@@ -151,3 +151,62 @@ def test_graph_replays_match_eager_steps():
         assert [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in ge.state.candidates] == \
             [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in gg.state.candidates]
     assert gg._gd is not None and len(gg._gd.graphs) == cfg.num_hidden_layers + 1
+
+
+def test_eos_finishes_beams_and_decoding_continues():
+    """With eos_token_id set to a token the model picks, beams finish, requests
+    continue with fewer live beams (eager steps: the candidate count changes),
+    and every step's selection equals the oracle's on the same logits."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    say("tiny llama with an end-of-sequence token")
+    from beam_engine_amd import PageTable
+    from beam_engine_amd.generator import BatchedBeamSearch
+    from beam_engine_amd.llama import LlamaConfig, LlamaDecoder
+    from beam_engine_amd.selection import beam_topk
+
+    cfg = LlamaConfig(num_hidden_layers=2, hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
+                      head_dim=128, intermediate_size=512, vocab_size=512, max_position_embeddings=512)
+    prompts = [list(range(5, 23)), list(range(100, 118))]
+
+    def run(eos, steps, check=False):
+        model = LlamaDecoder(cfg, "cuda", torch.bfloat16, seed=3)
+        pt = PageTable(2, page_size=4, max_num_pages=512, head_num=2, head_dim=128, device="cuda",
+                       store_dtype=torch.bfloat16)
+        gen = BatchedBeamSearch(model, pt, 4, kernel_type="cascade", graphs=True, eos_token_id=eos)
+        gen.prefill(prompts)
+        counts = []
+        if check:
+            orig = gen._select
+
+            def sel(logits):
+                st = gen.state
+                cands = list(st.candidates)
+                vals, idx = beam_topk(logits, 8)
+                v, ix = vals.cpu().numpy(), idx.cpu().numpy().astype(np.int64)
+                exp, r0 = [], 0
+                while r0 < len(cands):
+                    r1 = r0
+                    while r1 < len(cands) and cands[r1].request_id == cands[r0].request_id:
+                        r1 += 1
+                    per_row, _ = ot.select_global([c.score for c in cands[r0:r1]], v[r0:r1], ix[r0:r1], 4)
+                    exp += per_row
+                    r0 = r1
+                res = gen.strategy.select_batched(st, logits)
+                assert [[(b.token_id, b.accumulated_score) for b in r.children] for r in res] == exp
+                counts.append(len(cands))
+                st.add_filtered_results(res, eos)
+            gen._select = sel
+        for _ in range(steps):
+            if not gen.state.candidates:
+                break
+            gen.step()
+        torch.cuda.synchronize()
+        return gen, counts
+
+    base, _ = run(None, 3)
+    eos = base.state.candidates[0].trie_node.tokens[-1]        # a token picked in step 3 of the plain run
+    gen, counts = run(eos, 8, check=True)
+    assert gen.state.finished_candidates and all(c.sequence[-1] == eos for c in gen.state.finished_candidates)
+    assert min(counts) < 8 and counts[0] == 8
+    assert all(eos not in gen.state.sequence(c)[18:] for c in gen.state.candidates)
