@@ -2,12 +2,14 @@
 
 Drop-in for the decode path of brian030128/beam_engine: paged KV cache and
 allocator (``PageTable``), beam trie (``BeamState``), flat / cascade decode
-attention wrappers, and GPU beam selection, all backed by hand-written gfx950
+and paged prefill attention wrappers, and GPU beam selection (vanilla and
+diverse), all backed by hand-written gfx950
 HIP kernels in ``libbeam_engine_amd.so`` (C ABI: include/beam_engine_amd.h).
 There is no CPU fallback: every compute call raises if the library is missing.
 """
 
-from .attention import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAttentionWrapper, merge_state
+from .attention import (BatchDecodeWithPagedKVCacheWrapper, BatchPrefillWithPagedKVCacheWrapper,
+                        MultiLevelCascadeAttentionWrapper, merge_state)
 from .attention_mode import AttentionMode
 from .beam_state import (BeamCandidate, BeamGenerateInput, BeamGenerateResult, BeamState, BeamToken,
                          BeamTokenCandidate, TrieNode)
@@ -17,9 +19,11 @@ from .page_table import PageTable
 from .selection import beam_topk, decode_k
 
 __all__ = [
-    "AttentionMode", "BatchDecodeWithPagedKVCacheWrapper", "BeamCandidate", "BeamGenerateInput",
+    "AttentionMode", "BatchDecodeWithPagedKVCacheWrapper", "BatchPrefillWithPagedKVCacheWrapper", "BeamCandidate",
+    "BeamGenerateInput",
     "BeamGenerateResult", "BeamState", "BeamStrategy", "BeamToken", "BeamTokenCandidate", "KVTreeNode",
-    "MultiLevelCascadeAttentionWrapper", "PageTable", "TrieNode", "VanillaBeamSearchStrategy", "DiverseBeamSearchStrategy", "beam_topk",
+    "MultiLevelCascadeAttentionWrapper", "PageTable", "TrieNode", "VanillaBeamSearchStrategy",
+    "DiverseBeamSearchStrategy", "beam_topk",
     "decode_k", "merge_state",
 ]
 

@@ -24,6 +24,7 @@ BE_PLAN_NO_TAIL = 8
 BE_PLAN_TAIL_ROLE = 16
 BE_PLAN_NO_REGS = 32
 BE_PLAN_NO_WIDE = 64
+BE_PLAN_CAUSAL = 128
 BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}

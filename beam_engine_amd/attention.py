@@ -122,7 +122,7 @@ class _PagedPlanner:
     # ---------------------------------------------------------------- plan
     def _plan_levels(self, qo: Sequence, kvp: Sequence, kvi: Sequence, lpl: Sequence, num_qo_heads: int,
                      num_kv_heads: int, head_dim: int, page_size: int, sm_scale: Optional[float],
-                     q_data_type, num_queries: Optional[int] = None) -> None:
+                     q_data_type, num_queries: Optional[int] = None, causal: bool = False) -> None:
         lib = _lib.load()
         if not (len(qo) == len(kvp) == len(kvi) == len(lpl)):
             raise ValueError("per-level index lists must have the same length")
@@ -158,7 +158,8 @@ class _PagedPlanner:
             (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0) | \
             (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
             (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
-            (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0)
+            (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0) | \
+            (_lib.BE_PLAN_CAUSAL if causal else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()
@@ -279,14 +280,15 @@ class MultiLevelCascadeAttentionWrapper(_PagedPlanner):
             raise NotImplementedError("sliding window / soft cap are not part of the decode path")
         if kv_data_type is not None and kv_data_type != q_data_type:
             raise NotImplementedError("q and KV must share one dtype")
+        # causal applies to the last level: query i of a group of n sees the
+        # group's first kv_len - n + i + 1 tokens; one query per group (the
+        # decode case) masks nothing and keeps the streaming kernel
+        mask = False
         if causal:
-            # causal applies to the last level only; with one query per group
-            # there it masks nothing (each query is the newest position).
             last = _as_i32(qo_indptr_arr[-1])
-            if len(last) > 1 and int(np.max(np.diff(last))) > 1:
-                raise NotImplementedError("causal masking of multi-query groups on the last level")
+            mask = len(last) > 1 and int(np.max(np.diff(last))) > 1
         self._plan_levels(qo_indptr_arr, paged_kv_indptr_arr, paged_kv_indices_arr, paged_kv_last_page_len,
-                          num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, q_data_type)
+                          num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, q_data_type, causal=mask)
 
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
             return_lse: bool = False, between=None):
@@ -317,6 +319,43 @@ class BatchDecodeWithPagedKVCacheWrapper(_PagedPlanner):
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
             return_lse: bool = False, between=None):
         return self._run(q, paged_kv_cache, out, return_lse, between)
+
+    forward = run
+
+
+class BatchPrefillWithPagedKVCacheWrapper(_PagedPlanner):
+    """Paged prefill attention (drop-in for the FlashInfer wrapper of the
+    reference's prefill, models/modeling_llama.py:213-283, 775-798): request
+    r's queries ``q[qo_indptr[r]:qo_indptr[r+1]]`` attend to its pages, whose
+    K/V the caller wrote first; ``causal=True`` gives query i of n the first
+    kv_len - n + i + 1 tokens.  Runs on the MFMA tile kernel (bf16 / fp16) or
+    the VALU kernel (fp32) with a per-row causal limit; query tiles stop at
+    the chunk holding their last visible token."""
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD"):
+        super().__init__(float_workspace_buffer, kv_layout)
+
+    def plan(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, num_qo_heads: int,
+             num_kv_heads: int, head_dim_qk: int, page_size: int, head_dim_vo: Optional[int] = None,
+             causal: bool = False, pos_encoding_mode: str = "NONE", use_fp16_qk_reduction: bool = False,
+             sm_scale: Optional[float] = None, window_left: int = -1, logits_soft_cap: Optional[float] = None,
+             q_data_type="float16", kv_data_type=None, **_unused) -> None:
+        if pos_encoding_mode != "NONE":
+            raise NotImplementedError("RoPE is applied before attention (pos_encoding_mode='NONE' only)")
+        if window_left not in (-1, None) or logits_soft_cap not in (None, 0.0):
+            raise NotImplementedError("sliding window / soft cap are not supported")
+        if head_dim_vo is not None and head_dim_vo != head_dim_qk:
+            raise NotImplementedError("head_dim_vo must equal head_dim_qk")
+        if kv_data_type is not None and kv_data_type != q_data_type:
+            raise NotImplementedError("q and KV must share one dtype")
+        qo = _as_i32(qo_indptr)
+        self._plan_levels([qo], [paged_kv_indptr], [paged_kv_indices], [paged_kv_last_page_len], num_qo_heads,
+                          num_kv_heads, head_dim_qk, page_size, sm_scale, q_data_type,
+                          causal=bool(causal) and len(qo) > 1 and int(np.max(np.diff(qo))) > 1)
+
+    def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, out: Optional[torch.Tensor] = None,
+            return_lse: bool = False):
+        return self._run(q, paged_kv_cache, out, return_lse)
 
     forward = run
 

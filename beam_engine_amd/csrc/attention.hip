@@ -35,8 +35,10 @@ struct WorkItem {
   int32_t tok_begin;   // first group token covered (a multiple of 32)
   int32_t tok_count;   // tokens covered, > 0
   int32_t out_row;     // first partial row, or -1: write the final output
-  int32_t pad0, pad1;
+  int32_t vis0;        // causal: group tokens its first query sees, unclamped (query j: vis0 + j); else kNoCausal
+  int32_t pad1;
 };
+constexpr int32_t kNoCausal = 0x3fffffff;
 static_assert(sizeof(WorkItem) == 32, "WorkItem is 8 int32 words");
 
 constexpr int kMaxRows = 32;       // rows (queries x GQA group) per VALU workgroup
@@ -223,8 +225,13 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
   const int rt0 = (RT >= 4) ? w * NTW : (w % RT);
   const int ts = (RT >= 4) ? 0 : (w / RT);
   bool active[NTW];
+  int lim[NTW];      // item tokens this lane's row sees (causal: its query's limit)
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) active[nt] = (rt0 + nt) * 16 < R;
+  for (int nt = 0; nt < NTW; ++nt) {
+    active[nt] = (rt0 + nt) * 16 < R;
+    const int64_t v = (int64_t)it.vis0 + ((rt0 + nt) * 16 + lc) / g - it.tok_begin;
+    lim[nt] = (int)std::min<int64_t>(it.tok_count, std::max<int64_t>(v, 0));
+  }
 
   // ---- Q as the B operand: lane holds Q[row = (rt0+nt)*16 + lc][d = ks*32 + 8*lg .. +7]
   v8s qf[NTW][KS];
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tl = tl0 + sub * 16 + 4 * lg + r;
-          x[sb][r] = (tl < it.tok_count) ? acc[r] * a.scale_log2 : -INFINITY;
+          x[sb][r] = (tl < lim[nt]) ? acc[r] * a.scale_log2 : -INFINITY;
         }
       }
       float mx = -INFINITY;
@@ -458,8 +465,14 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnArgs a) {
   // score-phase ownership: token t = tid % 32, rows rg + 8k
   const int t_own = tid & 31, rg = tid >> 5;
   float m_row[4], l_row[4];
+  int lim_row[4];    // item tokens row rg + 8k sees (causal: its query's limit)
 #pragma unroll
-  for (int k = 0; k < 4; ++k) { m_row[k] = -INFINITY; l_row[k] = 0.f; }
+  for (int k = 0; k < 4; ++k) {
+    m_row[k] = -INFINITY;
+    l_row[k] = 0.f;
+    const int64_t v = (int64_t)it.vis0 + (rg + 8 * k) / g - it.tok_begin;
+    lim_row[k] = (int)std::min<int64_t>(it.tok_count, std::max<int64_t>(v, 0));
+  }
   // P.V-phase ownership: column d = tid % D, rows rgp + NRG*k
   const int d_own = tid % D, rgp = tid / D;
   float acc[RPT];
@@ -482,23 +495,23 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnArgs a) {
       vs[t][d] = vx;
     }
     __syncthreads();
-    const bool tvalid = (tb + t_own) < it.tok_count;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int r = rg + 8 * k;
       float sc = 0.f;
 #pragma unroll 8
       for (int d = 0; d < D; ++d) sc += qs[r][d] * ks[t_own * KST + d];
-      const float x = tvalid ? sc * a.scale_log2 : -INFINITY;
+      const float x = (tb + t_own) < lim_row[k] ? sc * a.scale_log2 : -INFINITY;
       float mx = x;
 #pragma unroll
       for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
       const float m_new = fmaxf(m_row[k], mx);
-      const float p = exp2f(x - m_new);
+      const float msafe = (m_new == -INFINITY) ? 0.f : m_new;   // a row with nothing seen yet
+      const float p = exp2f(x - msafe);
       float psum = p;
 #pragma unroll
       for (int o = 16; o > 0; o >>= 1) psum += __shfl_xor(psum, o, 64);
-      const float al = exp2f(m_row[k] - m_new);
+      const float al = exp2f(m_row[k] - msafe);
       l_row[k] = l_row[k] * al + psum;
       m_row[k] = m_new;
       psm[r][t_own] = p;
@@ -697,8 +710,25 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   for (int v : valid) valid_tokens += v;
   const int64_t es = (int64_t)dtype_size(dtype);
   double flops = 0.0;
-  for (const Group& gr : groups)
-    if (gr.kv_len > 0 && gr.q1 > gr.q0) flops += 4.0 * d * hq * (double)gr.kv_len * (gr.q1 - gr.q0);
+  // causal (BE_PLAN_CAUSAL): on the last level, query q0 + i of a group of n
+  // queries sees its first kv_len - n + i + 1 tokens (FlashInfer's alignment of
+  // the query block to the end of the keys; one query per group masks nothing)
+  const bool causal = (flags & BE_PLAN_CAUSAL) != 0;
+  auto is_causal = [&](const Group& gr) { return causal && gr.level == num_levels - 1 && gr.q1 - gr.q0 > 1; };
+  auto vis = [&](const Group& gr, int qi) -> int {
+    if (!is_causal(gr)) return gr.kv_len;
+    return std::max(0, std::min(gr.kv_len, gr.kv_len - (gr.q1 - gr.q0) + (qi - gr.q0) + 1));
+  };
+  bool any_causal = false;
+  for (const Group& gr : groups) {
+    if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
+    any_causal = any_causal || is_causal(gr);
+    if (is_causal(gr)) {
+      for (int qi = gr.q0; qi < gr.q1; ++qi) flops += 4.0 * d * hq * (double)vis(gr, qi);
+    } else {
+      flops += 4.0 * d * hq * (double)gr.kv_len * (gr.q1 - gr.q0);
+    }
+  }
 
   bool mfma = (dtype != BE_F32) && !(flags & BE_PLAN_FORCE_VALU);
   if (!mfma && g > kMaxRows) return fail(BE_ERR_UNSUPPORTED, "GQA group %d exceeds %d (VALU kernel)", g, kMaxRows);
@@ -715,7 +745,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
                "bad plan capacities (max_queries %d < %d queries?)", caps->max_queries, num_queries);
     if (mfma) rows_cap = std::min(rows_cap, tr);
   }
-  if (stream_eligible(dtype, d, g, page_size, flags) && (!caps || caps->tile_rows == 64)) {
+  if (!any_causal && stream_eligible(dtype, d, g, page_size, flags) && (!caps || caps->tile_rows == 64)) {
     memset(info, 0, sizeof(*info));
     const int rc = stream_plan(groups, levels, num_levels, total_pages, num_queries, hq, hkv, d, page_size,
                                num_pages, dtype, num_cus, flags, caps, out, cap, info);
@@ -756,12 +786,17 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
     return std::min(c, chunk_cap);
   };
 
-  // ---- per-query partial counts
+  // ---- per-query partial counts (a causal query tile stops at the chunk
+  // holding its last query's last visible token)
   std::vector<int> cnt(num_queries, 0);
   for (const Group& gr : groups) {
-    if (gr.kv_len <= 0) continue;
-    const int nch = (int)ceil_div(gr.kv_len, group_chunk(gr));
-    for (int qi = gr.q0; qi < gr.q1; ++qi) cnt[qi] += nch;
+    if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
+    const int64_t gchunk = group_chunk(gr);
+    for (int qa = gr.q0; qa < gr.q1; qa += q_tile) {
+      const int qn = std::min(q_tile, gr.q1 - qa);
+      const int nch = (int)ceil_div(vis(gr, qa + qn - 1), gchunk);
+      for (int qi = qa; qi < qa + qn; ++qi) cnt[qi] += nch;
+    }
   }
 
   // ---- items and partial rows
@@ -772,12 +807,18 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
     if (gr.kv_len <= 0 || gr.q1 <= gr.q0) continue;
     const int64_t gchunk = group_chunk(gr);
     for (int t0 = 0; t0 < gr.kv_len; t0 += (int)gchunk) {
-      const int tc = (int)std::min<int64_t>(gchunk, gr.kv_len - t0);
       for (int qa = gr.q0; qa < gr.q1; qa += q_tile) {
         const int qn = std::min(q_tile, gr.q1 - qa);
+        const int tile_vis = vis(gr, qa + qn - 1);     // the tile's last query sees the most
+        if (t0 >= tile_vis) continue;
+        const int tc = (int)std::min<int64_t>(gchunk, tile_vis - t0);
         bool direct = true;
         for (int qi = qa; qi < qa + qn; ++qi) direct = direct && (cnt[qi] == 1);
-        WorkItem w{qa, qn, gr.page_base, t0, tc, -1, 0, 0};
+        // vis0: tokens the item's first query sees (group token units, before
+        // clamping to [0, kv_len]: may be negative), query j of the item sees
+        // vis0 + j (the kernel clamps per row); kNoCausal without the mask
+        const int vis0 = gr.kv_len - (gr.q1 - gr.q0) + (qa - gr.q0) + 1;
+        WorkItem w{qa, qn, gr.page_base, t0, tc, -1, is_causal(gr) ? vis0 : kNoCausal, 0};
         if (!direct) {
           w.out_row = rows;
           for (int j = 0; j < qn; ++j) rows_of[qa + j].push_back(rows + j);

@@ -10,9 +10,11 @@ layer q/k/v projection, RoPE, append of the new K/V to the paged cache
 kernel) and attention is whatever ``attn(layer, q, kv_layer)`` the caller
 passes (the HIP cascade / flat wrappers).
 
-Prefill (prompt processing) is out of the hot path: causal attention is done
-in float32 with explicit matmuls (contiguous operands) and the prompt's K/V is
-scattered into its pages with one append per layer.
+Prefill (prompt processing) follows the reference's order
+(models/modeling_llama.py:213-283): the prompt's K/V is scattered into its
+pages with one append per layer, then causal paged prefill attention over
+those pages (``BatchPrefillWithPagedKVCacheWrapper``, HIP tile kernel with a
+per-row causal limit) planned once for all layers.
 """
 
 from __future__ import annotations
@@ -132,7 +134,15 @@ class LlamaDecoder:
         pages = torch.tensor([[p[i // ps] for i in range(s)] for p in page_ids], dtype=torch.int32,
                              device=self.device).reshape(-1)
         slots = (torch.arange(s, device=self.device, dtype=torch.int32) % ps).repeat(r)
-        causal = torch.full((s, s), float("-inf"), device=self.device).triu(1)
+        # causal paged prefill attention over the pages just written, planned
+        # once for every layer (models/modeling_llama.py:775-798)
+        from .attention import BatchPrefillWithPagedKVCacheWrapper
+        npg = -(-s // ps)
+        ws = torch.empty(256 << 20, dtype=torch.uint8, device=self.device)
+        pre = BatchPrefillWithPagedKVCacheWrapper(ws)
+        pre.plan([i * s for i in range(r + 1)], [i * npg for i in range(r + 1)],
+                 [p[j] for p in page_ids for j in range(npg)], [s - (npg - 1) * ps] * r, hq, hkv, d, ps,
+                 causal=True, q_data_type=self.dtype)
         x = F.embedding(input_ids, self.embed)
         for li, layer in enumerate(self.layers):
             h = self._rms(x, layer["ln1"])
@@ -141,13 +151,7 @@ class LlamaDecoder:
             k = self._rope(k, pos)
             page_table.write_blocks_vectorized(li, pages, k.reshape(r * s, hkv, d).contiguous(),
                                                v.reshape(r * s, hkv, d).contiguous(), slots)
-            # causal GQA attention in float32 (contiguous operands)
-            qf = q.float().permute(0, 2, 1, 3).contiguous()                                  # [R, Hq, S, D]
-            kf = k.float().repeat_interleave(hq // hkv, dim=2).permute(0, 2, 3, 1).contiguous()  # [R, Hq, D, S]
-            vf = v.float().repeat_interleave(hq // hkv, dim=2).permute(0, 2, 1, 3).contiguous()  # [R, Hq, S, D]
-            sc = torch.matmul(qf, kf) * (d ** -0.5) + causal
-            o = torch.matmul(torch.softmax(sc, dim=-1), vf)                                 # [R, Hq, S, D]
-            o = o.permute(0, 2, 1, 3).reshape(r, s, hq * d).to(self.dtype)
+            o = pre.run(q.reshape(r * s, hq, d), page_table.kv_cache_at_layer[li]).reshape(r, s, hq * d)
             x = x + F.linear(o, layer["wo"])
             x = self._mlp(layer, x)
         last = self._rms(x[:, -1], self.norm)

@@ -135,6 +135,10 @@ typedef struct be_level {
                                     lengths (no register-staged loop)                       */
 #define BE_PLAN_NO_WIDE 64       /* streaming kernel: no wide wave roles (32 rows per wave)
                                     and no 128-row segments for long many-query groups      */
+#define BE_PLAN_CAUSAL 128       /* causal groups on the last level: query q0 + i of a group
+                                    of n queries over kv_len tokens sees its first
+                                    kv_len - n + i + 1 tokens (FlashInfer's causal prefill
+                                    alignment; such plans run the tile / VALU kernels)     */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the

@@ -117,7 +117,7 @@ def merge_states(os_: Sequence[np.ndarray], lses: Sequence[np.ndarray]):
 
 
 def cascade_attention(q, kv_layer, qo_indptr_arr, kv_indptr_arr, kv_indices_arr,
-                      last_page_len_arr, page_size: int, sm_scale: float | None = None):
+                      last_page_len_arr, page_size: int, sm_scale: float | None = None, causal: bool = False):
     """Multi-level cascade decode attention, float64.
 
     For every level and every group gamma (queries qo_indptr[g]..qo_indptr[g+1],
@@ -125,13 +125,20 @@ def cascade_attention(q, kv_layer, qo_indptr_arr, kv_indptr_arr, kv_indices_arr,
     last_page_len[g]) computes the partial attention of the group's queries
     and merges the levels by log-sum-exp.  sm_scale defaults to D^-0.5
     (models/modeling_llama.py:304, 753).  Returns ``(o [N, Hq, D], lse [N, Hq])``.
+
+    ``causal`` masks the last level's groups as FlashInfer's causal prefill
+    does (the reference plans its prefill with causal=True,
+    models/modeling_llama.py:775-798): query i of a group of n queries over T
+    tokens sees the first T - n + i + 1 of them (the query block aligned to
+    the end of the keys; n == T is the plain lower-triangular mask).
     """
     qf = _as_f64(q)
     n, hq, d = qf.shape
     if sm_scale is None:
         sm_scale = d ** -0.5
     level_o, level_lse = [], []
-    for qo, kvp, kvi, lpl in zip(qo_indptr_arr, kv_indptr_arr, kv_indices_arr, last_page_len_arr):
+    n_levels = len(qo_indptr_arr)
+    for li, (qo, kvp, kvi, lpl) in enumerate(zip(qo_indptr_arr, kv_indptr_arr, kv_indices_arr, last_page_len_arr)):
         qo = [int(x) for x in qo]
         kvp = [int(x) for x in kvp]
         kvi = [int(x) for x in kvi]
@@ -141,6 +148,15 @@ def cascade_attention(q, kv_layer, qo_indptr_arr, kv_indptr_arr, kv_indices_arr,
         for gi in range(len(qo) - 1):
             pages = kvi[kvp[gi]:kvp[gi + 1]]
             k, v = gather_kv(kv_layer, pages, lpl[gi] if pages else 0, page_size)
+            nq = qo[gi + 1] - qo[gi]
+            if causal and li == n_levels - 1 and nq > 1:
+                t = k.shape[0]
+                for i in range(nq):
+                    vis = max(0, min(t, t - nq + i + 1))
+                    o_g, lse_g = partial_attention(qf[qo[gi] + i:qo[gi] + i + 1], k[:vis], v[:vis], sm_scale)
+                    o_l[qo[gi] + i] = o_g[0]
+                    lse_l[qo[gi] + i] = lse_g[0]
+                continue
             o_g, lse_g = partial_attention(qf[qo[gi]:qo[gi + 1]], k, v, sm_scale)
             o_l[qo[gi]:qo[gi + 1]] = o_g
             lse_l[qo[gi]:qo[gi + 1]] = lse_g

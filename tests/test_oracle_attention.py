@@ -120,3 +120,63 @@ def test_planted_head_mapping_mistake_is_caught():
     o_wrong, _ = oa.partial_attention(q, wrong_k, wrong_v, 0.3)   # g == 1 path
     o_right, _ = oa.partial_attention(q, k, v, 0.3)
     assert not np.allclose(o_wrong, o_right, atol=1e-6)
+
+
+def _one_request_levels(n_q, n_kv, page):
+    npg = -(-n_kv // page)
+    return ([[0, n_q]], [[0, npg]], [list(range(npg))], [[n_kv - (npg - 1) * page]]), npg
+
+
+def test_causal_prefill_equals_torch_sdpa_lower_triangle():
+    """qo_len == kv_len (a fresh prompt): the causal restatement is the plain
+    lower-triangular mask of torch's fp64 scaled_dot_product_attention."""
+    import torch
+    rng = np.random.default_rng(11)
+    page, hq, hkv, d, n = 4, 4, 2, 8, 13
+    levels, npg = _one_request_levels(n, n, page)
+    kv = rng.standard_normal((npg, 2, page, hkv, d))
+    q = rng.standard_normal((n, hq, d))
+    o, lse = oa.cascade_attention(q, kv, *levels, page, causal=True)
+    k, v = oa.gather_kv(kv, levels[2][0], levels[3][0][0], page)
+    qt = torch.from_numpy(q).permute(1, 0, 2)[None]                             # [1, Hq, n, D]
+    kt = torch.from_numpy(np.repeat(k, hq // hkv, axis=1)).permute(1, 0, 2)[None]
+    vt = torch.from_numpy(np.repeat(v, hq // hkv, axis=1)).permute(1, 0, 2)[None]
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True)[0].permute(1, 0, 2)
+    np.testing.assert_allclose(o, ref.numpy(), rtol=0, atol=1e-12)
+    assert np.isfinite(lse).all()
+
+
+def test_causal_block_aligned_to_the_end_of_the_keys():
+    """qo_len < kv_len (a prompt continuing cached tokens): query i of n sees
+    the first kv_len - n + i + 1 tokens -- the dense loop on each query's
+    visible prefix agrees, and the top-left alignment (i + 1 tokens) does not."""
+    rng = np.random.default_rng(12)
+    page, hq, hkv, d, n, t = 4, 2, 1, 4, 3, 9
+    levels, npg = _one_request_levels(n, t, page)
+    kv = rng.standard_normal((npg, 2, page, hkv, d))
+    q = rng.standard_normal((n, hq, d))
+    o, lse = oa.cascade_attention(q, kv, *levels, page, causal=True)
+    k, v = oa.gather_kv(kv, levels[2][0], levels[3][0][0], page)
+    for i in range(n):
+        oi, li = oa.reference_attention_dense(q[i:i + 1], k[:t - n + i + 1], v[:t - n + i + 1], d ** -0.5)
+        np.testing.assert_allclose(o[i:i + 1], oi, rtol=0, atol=1e-12)
+        np.testing.assert_allclose(lse[i:i + 1], li, rtol=0, atol=1e-12)
+    wrong, _ = oa.reference_attention_dense(q[:1], k[:1], v[:1], d ** -0.5)       # top-left: query 0 sees 1 token
+    assert np.abs(wrong - o[:1]).max() > 1e-3
+
+
+def test_causal_masks_only_the_last_level():
+    rng = np.random.default_rng(13)
+    page, hq, hkv, d = 4, 2, 1, 4
+    kv = rng.standard_normal((4, 2, page, hkv, d))
+    q = rng.standard_normal((2, hq, d))
+    levels = ([[0, 2], [0, 2]], [[0, 2], [0, 2]], [[0, 1], [2, 3]], [[4, 3]])
+    levels = (levels[0], levels[1], levels[2], [[4], [3]])
+    a = oa.cascade_attention(q, kv, *levels, page, causal=True)
+    # level 0 unmasked, level 1 causal: merge of the two computed separately
+    o0, l0 = oa.cascade_attention(q, kv, [levels[0][0]], [levels[1][0]], [levels[2][0]], [levels[3][0]], page)
+    o1, l1 = oa.cascade_attention(q, kv, [levels[0][1]], [levels[1][1]], [levels[2][1]], [levels[3][1]], page,
+                                  causal=True)
+    b = oa.merge_states([o0, o1], [l0, l1])
+    np.testing.assert_allclose(a[0], b[0], atol=1e-12)
+    np.testing.assert_allclose(a[1], b[1], atol=1e-12)
