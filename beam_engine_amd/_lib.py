@@ -68,7 +68,8 @@ class BeAttnPlanInfo(ctypes.Structure):
         ("flops", ctypes.c_double),
     ] + [(n, ctypes.c_int32) for n in ("num_wg", "off_wg", "off_records", "off_record_slots",
                                               "num_tails", "off_tails", "tail_waves",
-                                              "num_tail_items", "off_tail_items", "stream_loop")]
+                                              "num_tail_items", "off_tail_items", "stream_loop",
+                                              "off_seg_causal")]
 
 
 EXPORTS = (

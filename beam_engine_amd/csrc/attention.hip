@@ -745,7 +745,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
                "bad plan capacities (max_queries %d < %d queries?)", caps->max_queries, num_queries);
     if (mfma) rows_cap = std::min(rows_cap, tr);
   }
-  if (!any_causal && stream_eligible(dtype, d, g, page_size, flags) && (!caps || caps->tile_rows == 64)) {
+  if (!(any_causal && caps) && stream_eligible(dtype, d, g, page_size, flags) && (!caps || caps->tile_rows == 64)) {
     memset(info, 0, sizeof(*info));
     const int rc = stream_plan(groups, levels, num_levels, total_pages, num_queries, hq, hkv, d, page_size,
                                num_pages, dtype, num_cus, flags, caps, out, cap, info);

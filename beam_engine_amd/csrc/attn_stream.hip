@@ -69,6 +69,7 @@ constexpr int kStageBytes = 2 * kKvBytes + kQBytes;
 constexpr int kLdsStages = kRegStages * kStageBytes;   // the smaller of the two loops' stage buffers
 constexpr int kClassGeneric = 1;              // workgroup-table class: per-segment mode (else the mode 0 or 2)
 constexpr int kClassWide = 5;                 // workgroup-table class of the wide roles (32 rows per wave)
+constexpr int kNoCausalS = 0x3fffffff;        // segment causal base of a segment without the mask
 constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
 constexpr int kThreads = 64 * kWaves;
 constexpr int kSegCost = 4;                   // planner cost of a segment start, in quarter tiles
@@ -108,6 +109,7 @@ struct StreamArgs {
   float* part_lse;    // [slots, g]
   const int4* wg;     // per workgroup: first segment (item), segments (items), tiles, class
   const StreamSeg* segs;
+  const int32_t* seg_causal;   // per segment: tokens its first query sees (causal), or null
   const int32_t* titems;   // tail items [n][8]: query, KV head, first tail chunk, chunks, slot
   const int2* tails;
   const int32_t* pages;
@@ -237,7 +239,7 @@ __device__ __forceinline__ SegReg seg_reg(const StreamSeg& x) {
 template <typename T, int NSUB, int NMT>
 __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsigned char* vt, const v8s (&qf)[4],
                                              const uint32_t (&koff)[4], const uint32_t (&voff)[NMT], int tok_base,
-                                             int valid, int lg, float scale, float& m_run, float& l_run,
+                                             int vrow, int lg, float scale, float& m_run, float& l_run,
                                              v4f (&o_acc)[8]) {
   // all LDS operand reads first: the K fragments, then the V^T fragments
   // (independent of the scores, so their latency hides under the softmax)
@@ -262,12 +264,14 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[k][r] = acc[r] * scale;
   }
-  if (valid < kTok) {
+  // vrow: tokens of the tile this lane's row sees (the tile's valid tokens,
+  // fewer under a causal limit)
+  if (__builtin_amdgcn_ballot_w64(vrow < kTok) != 0) {
 #pragma unroll
     for (int k = 0; k < NSUB; ++k)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (tok_base + k * 16 + 4 * lg + r >= valid) x[k][r] = -INFINITY;
+        if (tok_base + k * 16 + 4 * lg + r >= vrow) x[k][r] = -INFINITY;
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -309,6 +313,13 @@ __device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsi
     }
     o_acc[mt] = o;
   }
+}
+
+// Tokens of a tile (valid of them, starting at group token tile_tok) that
+// row `row` of a segment sees when the segment's first query sees vis0 group
+// tokens and query j (row / g) sees vis0 + j; kNoCausalS leaves valid.
+__device__ __forceinline__ int row_limit(int valid, int vis0, int row, int g, int tile_tok) {
+  return min(valid, max(0, vis0 + row / g - tile_tok));
 }
 
 // Wide wave roles: one wave's share of a 64-token tile for two 16-row MFMA
@@ -474,7 +485,7 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
 // kClassWide: the wide roles (32 rows per wave, segments of up to 128 rows).
 template <typename T, int FM>
 __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
-                                                float* ml_lds, int n_segs, int n_tiles) {
+                                                const int* vis_lds, float* ml_lds, int n_segs, int n_tiles) {
   const int tid = threadIdx.x;
   const int w = rfl(tid >> 6);                        // wave index (uniform)
   const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
@@ -652,16 +663,17 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
     }
     if (act) {
       const int valid = min(kTok, sg.tok_count - c_t * kTok);
+      const int vr = row_limit(valid, vis_lds[c_s], 16 * rt + lc, g, sg.tok_begin + c_t * kTok);
       const unsigned char* kt = stage + sub0 * 4096;
       const unsigned char* vt = stage + kKvBytes + sub0 * 4096;
       if (mode == 0)
-        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, vr, lg, scale, m_run, l_run, o_acc);
       else if (mode == 1)
-        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, vr, lg, scale, m_run, l_run, o_acc);
       else if (mode == 2)
-        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, vr, lg, scale, m_run, l_run, o_acc);
       else
-        tile_compute<T, 4, 1>(kt, vt, qf, koff, voff1, 0, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 4, 1>(kt, vt, qf, koff, voff1, 0, vr, lg, scale, m_run, l_run, o_acc);
     }
 
     if (last) {
@@ -868,7 +880,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
 // set B (the loop is unrolled by two so that the sets are static).
 template <typename T, int FM>
 __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
-                                                 float* ml_lds, int n_segs, int n_tiles) {
+                                                 const int* vis_lds, float* ml_lds, int n_segs, int n_tiles) {
   typedef int v4i __attribute__((ext_vector_type(4)));
   const int tid = threadIdx.x;
   const int w = rfl(tid >> 6);                        // wave index (uniform)
@@ -1039,16 +1051,17 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
     }
     if (act) {
       const int valid = min(kTok, sg.tok_count - c_t * kTok);
+      const int vr = row_limit(valid, vis_lds[c_s], 16 * rt + lc, g, sg.tok_begin + c_t * kTok);
       const unsigned char* kt = stage + sub0 * 4096;
       const unsigned char* vt = stage + kKvBytes + sub0 * 4096;
       if (mode == 0)
-        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 2, 8>(kt, vt, qf, koff, voff8, sub0 * 16, vr, lg, scale, m_run, l_run, o_acc);
       else if (mode == 1)
-        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 2, 4>(kt, vt, qf, koff, voff4, sub0 * 16, vr, lg, scale, m_run, l_run, o_acc);
       else if (mode == 2)
-        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 1, 4>(kt, vt, qf, koff, voff4, sub0 * 16, vr, lg, scale, m_run, l_run, o_acc);
       else
-        tile_compute<T, 4, 1>(kt, vt, qf, koff, voff1, 0, valid, lg, scale, m_run, l_run, o_acc);
+        tile_compute<T, 4, 1>(kt, vt, qf, koff, voff1, 0, vr, lg, scale, m_run, l_run, o_acc);
     }
 
     if (last) {
@@ -1179,6 +1192,7 @@ template <typename T, bool REGS>
 __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char st_lds[(REGS ? kRegStages : kDmaStages) * kStageBytes];
   __shared__ StreamSeg seg_lds[kMaxSegs];
+  __shared__ int vis_lds[kMaxSegs];           // per segment: causal base, or kNoCausalS
   __shared__ float ml_lds[kWaves * 128];      // epilogue exchange of m and l
 
   const int tid = threadIdx.x;
@@ -1191,17 +1205,18 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
       const int* src = reinterpret_cast<const int*>(a.segs + wi.x);
       int* dst = reinterpret_cast<int*>(seg_lds);
       for (int i = tid; i < n_segs * 8; i += kThreads) dst[i] = src[i];
+      for (int i = tid; i < n_segs; i += kThreads) vis_lds[i] = a.seg_causal ? a.seg_causal[wi.x + i] : kNoCausalS;
     }
     __syncthreads();
     if constexpr (REGS) {
-      if (cls == 0) stream_body_regs<T, 0>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
-      else if (cls == 2) stream_body_regs<T, 2>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
-      else stream_body_regs<T, -1>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      if (cls == 0) stream_body_regs<T, 0>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == 2) stream_body_regs<T, 2>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else stream_body_regs<T, -1>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
     } else {
-      if (cls == 0) stream_body_dma<T, 0>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
-      else if (cls == 2) stream_body_dma<T, 2>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
-      else if (cls == kClassWide) stream_body_dma<T, kClassWide>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
-      else stream_body_dma<T, -1>(a, st_lds, seg_lds, ml_lds, n_segs, n_tiles);
+      if (cls == 0) stream_body_dma<T, 0>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == 2) stream_body_dma<T, 2>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == kClassWide) stream_body_dma<T, kClassWide>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else stream_body_dma<T, -1>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
     }
   }
 }
@@ -1377,6 +1392,13 @@ bool stream_eligible(int dtype, int head_dim, int group, int page_size, int flag
 int stream_plan(const std::vector<Group>& groups, const be_level* levels, int num_levels, int64_t total_pages,
                 int num_queries, int hq, int hkv, int d, int page_size, int num_pages, int dtype, int num_cus,
                 int flags, const be_plan_caps* caps, int32_t* out, int64_t cap, be_attn_plan_info* info) {
+  // causal groups (BE_PLAN_CAUSAL, last level, more than one query): query
+  // q0 + i of n sees the group's first kv_len - n + i + 1 tokens; such a
+  // group's tasks stop at their last query's last visible token and carry the
+  // unclamped count of their first query for the kernel's per-row limit
+  auto is_causal = [&](const Group& gr) {
+    return (flags & BE_PLAN_CAUSAL) && gr.level == num_levels - 1 && gr.q1 - gr.q0 > 1;
+  };
   (void)d;
   (void)num_pages;
   (void)dtype;
@@ -1403,7 +1425,9 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   if (!(flags & BE_PLAN_NO_TAIL) && page_size % 16 == 0 && g <= 16) {
     for (size_t gi = 0; gi < groups.size(); ++gi) {
       const Group& gr = groups[gi];
-      if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || gr.kv_len > kTailTokens || gr.q1 - gr.q0 > kTailQueries) continue;
+      if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || gr.kv_len > kTailTokens || gr.q1 - gr.q0 > kTailQueries ||
+          is_causal(gr))
+        continue;
       const int nch = (int)ceil_div(gr.kv_len, 16);
       bool fits = true;
       for (int qi = gr.q0; qi < gr.q1; ++qi) fits = fits && (int)tails_of[qi].size() + nch <= kTailChunks;
@@ -1438,22 +1462,32 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     }
     wide = tiles64 >= (int64_t)kWideMinRun * W;
   }
-  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc; };
+  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc, vis0; };
   std::vector<Task> tasks;
   int64_t total = 0;
+  bool any_causal = false;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
     const Group& gr = groups[gi];
     if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || is_tail[gi]) continue;
-    const int tiles = (int)ceil_div(gr.kv_len, kTok);
-    const bool w128 = wide && (gr.q1 - gr.q0) * g > kSegRows && tiles >= kWideMinTiles;
+    const bool cz = is_causal(gr);
+    any_causal = any_causal || cz;
+    const int tiles_all = (int)ceil_div(gr.kv_len, kTok);
+    const bool w128 = wide && !cz && (gr.q1 - gr.q0) * g > kSegRows && tiles_all >= kWideMinTiles;
     const int qt = w128 ? q_tile_w : q_tile;
     const int tc = w128 ? kWideTileCost : 4;
-    for (int qa = gr.q0; qa < gr.q1; qa += qt)
+    for (int qa = gr.q0; qa < gr.q1; qa += qt) {
+      const int qn = std::min(qt, gr.q1 - qa);
+      const int vis0 = cz ? gr.kv_len - (gr.q1 - gr.q0) + (qa - gr.q0) + 1 : kNoCausalS;
+      const int kv = cz ? std::max(0, std::min(gr.kv_len, vis0 + qn - 1)) : gr.kv_len;
+      if (kv <= 0) continue;                        // the tile's queries see nothing: zero records
+      const int tiles = (int)ceil_div(kv, kTok);
       for (int h = 0; h < hkv; ++h) {
-        tasks.push_back(Task{qa, std::min(qt, gr.q1 - qa), gr.page_base, gr.kv_len, h, tiles, tc});
+        tasks.push_back(Task{qa, qn, gr.page_base, kv, h, tiles, tc, vis0});
         total += tc * (int64_t)tiles + kSegCost;
       }
+    }
   }
+  std::vector<int32_t> seg_vis;                     // per segment: its task's vis0
 
   // ---- roles: with BE_PLAN_TAIL_ROLE the tail chunks run in tail-role
   // workgroups of this kernel (one wave per (query, KV head) item) while the
@@ -1525,6 +1559,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
           sgm.out_slot = -1;
           sgm.n_tiles = 0;
           segs.push_back(sgm);
+          seg_vis.push_back(t.vis0);
           wg[b].y += 1;
           used += kSegCost;
           open = true;
@@ -1670,9 +1705,11 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   const int64_t off_tails = off;  off += 2 * c_tails;
   const int64_t c_items = caps ? (int64_t)caps->max_merge : n_items;
   const int64_t off_items = off;  off += kRecWords * c_items;
+  const int64_t off_causal = off; off += any_causal ? c_segs : 0;
   off = ceil_div(off, 4) * 4;
   if (off > cap || off > INT32_MAX)
     return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  if (any_causal && n_segs) memcpy(out + off_causal, seg_vis.data(), n_segs * sizeof(int32_t));
   for (int i = 0; i < kPlanHeader; ++i) out[i] = 0;
   out[kHdrItems] = (int32_t)n_segs;
   out[kHdrMerge] = (int32_t)n_recs;
@@ -1707,6 +1744,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->partial_bytes = info->counter_offset;
   info->num_wg = W;
   info->off_wg = (int32_t)off_wg;
+  info->off_seg_causal = any_causal ? (int32_t)off_causal : 0;
   info->off_records = (int32_t)off_recs;
   info->off_record_slots = (int32_t)off_rslots;
   info->num_tails = (int32_t)n_tails;
@@ -1757,6 +1795,7 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
     a.part_o = part_o; a.part_lse = part_lse;
     a.wg = reinterpret_cast<const int4*>(plan + info->off_wg);
     a.segs = reinterpret_cast<const StreamSeg*>(plan + info->off_items);
+    a.seg_causal = info->off_seg_causal ? plan + info->off_seg_causal : nullptr;
     a.titems = plan + info->off_tail_items;
     a.tails = reinterpret_cast<const int2*>(plan + info->off_tails);
     a.pages = plan + info->off_pages;

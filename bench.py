@@ -38,7 +38,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (decode steps / attention reps)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="e2e",
-                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5"])
+                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-prefill"])
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
@@ -132,6 +132,59 @@ def attention_workload(args):
     return result, wl
 
 
+def prefill_workload(args):
+    """Causal paged prefill attention at the e2e prompt shape: 8 requests x
+    1024 tokens, 32 / 8 heads, head_dim 128, bf16, page 16, over 32 distinct
+    per-layer caches.  Compute-bound: value = TFLOP/s (4 D Hq sum of visible
+    tokens per launch), roofline against the bf16 MFMA peak."""
+    import torch
+    from beam_engine_amd import BatchPrefillWithPagedKVCacheWrapper
+    r, s, hq, hkv, d, ps = 8, 1024, 32, 8, 128, 16
+    steps = args.steps or 10
+    warmup = 3 if args.warmup is None else args.warmup
+    L = args.layers
+    dev = torch.device("cuda")
+    torch.manual_seed(0)
+    npg = s // ps
+    sc = 1.0 / math.sqrt(d)
+    kv = [torch.randn((r * npg, 2, ps, hkv, d), device=dev, dtype=torch.bfloat16).mul_(sc) for _ in range(L)]
+    qs = [torch.randn((r * s, hq, d), device=dev, dtype=torch.bfloat16).mul_(sc) for _ in range(L)]
+    outs = [torch.empty_like(q) for q in qs]
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    w = BatchPrefillWithPagedKVCacheWrapper(ws)
+    w.plan([i * s for i in range(r + 1)], [i * npg for i in range(r + 1)], list(range(r * npg)), [ps] * r,
+           hq, hkv, d, ps, causal=True, q_data_type=torch.bfloat16)
+    st = w.stats
+    for _ in range(warmup):
+        for l in range(L):
+            w.run(qs[l], kv[l], out=outs[l])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps * L)]
+    for i in range(steps * L):
+        evs[i][0].record(stream)
+        w.run(qs[i % L], kv[i % L], out=outs[i % L])
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    mean_us = sum(a.elapsed_time(b) for a, b in evs) * 1e3 / len(evs)
+    tflops = st.flops / (mean_us * 1e-6) / 1e12
+    gbs = st.bytes / (mean_us * 1e-6) / 1e9
+    return {
+        "metric": "prefill attention TFLOP/s (causal, paged)", "value": round(tflops, 2), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(mean_us * L / 1e3, 4),
+        "higher_is_better": True, "scaling": "strong", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1)/sqrt(D)",
+        "config": {"workload": "prefill attention, 8 x 1024-token prompts, Llama-3-8B layer shape, causal",
+                   "layers": L, "items": st.num_items, "flops_per_launch": st.flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": f"attn_{st.kernel}_kernel" + (" + tail_merge_kernel" if st.kernel == "stream" else
+                                                             " + merge_kernel"),
+                     "mean_launch_us": round(mean_us, 2),
+                     "hbm_gbs": round(gbs, 1)},
+    }
+
+
 # ---------------------------------------------------------------------- CPU baseline
 def cpu_baseline_attention(wl, alg_bytes):
     """The oracle (numpy float64 cascade attention + log-sum-exp merge) on one
@@ -161,6 +214,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         return 1
+    if args.workload == "attn-prefill":
+        print(json.dumps(prefill_workload(args)), flush=True)
+        return 0
     if args.workload.startswith("attn-"):
         if args.strategy not in ("cascade", "flat"):
             print(json.dumps({"error": "attention workloads take --strategy cascade or flat"}))

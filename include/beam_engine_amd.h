@@ -200,6 +200,8 @@ typedef struct be_attn_plan_info {
   int32_t num_tail_items;
   int32_t off_tail_items;
   int32_t stream_loop;     /* streaming kernel's loop: 0 direct global->LDS loads, 1 register-staged */
+  int32_t off_seg_causal;  /* causal plans: per segment, the tokens its first query sees (query j
+                              of the segment sees that + j); 0 when the plan has no causal group */
 } be_attn_plan_info;
 
 /* be_attn_plan (host only): validates the levels against num_queries,

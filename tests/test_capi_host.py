@@ -476,3 +476,44 @@ def test_stream_plan_tail_limits():
     # page sizes that are not a multiple of 16 never use tail chunks
     rc, info, buf, *_ = plan(levels, nq=5, hq=8, hkv=2, page=8, num_pages=nxt)
     assert rc == 0 and info.num_tails == 0
+
+
+@pytest.mark.parametrize("nq,nk,cus", [(200, 200, 256), (200, 700, 7), (9, 5, 3), (40, 40, 1)])
+def test_stream_plan_causal_groups(nq, nk, cus):
+    """BE_PLAN_CAUSAL on the streaming kernel: each 16-query tile (64 rows at
+    GQA 4) of a causal group is streamed over [0, its last query's visible
+    tokens) only, every segment carries its tile's first-query count (unclamped:
+    query j of the tile sees that + j), causal groups never become tail
+    chunks, and tiles whose queries see nothing get no segment."""
+    hq, hkv, page = 32, 8, 16
+    npg = -(-nk // page)
+    levels = [([0, nq], [0, npg], list(range(npg)), [nk - (npg - 1) * page])]
+    rc, info, buf, _lib, L = plan(levels, nq=nq, hq=hq, hkv=hkv, page=page, num_pages=npg, cus=cus, flags=128)
+    assert rc == 0, L.be_last_error()
+    assert info.kernel == 2 and info.off_seg_causal > 0 and info.num_tails == 0
+    wg, segs, recs, rslots, tails = decode_stream(info, buf)
+    vis = buf[info.off_seg_causal: info.off_seg_causal + info.num_items]
+    g, qt = hq // hkv, 64 // (hq // hkv)
+    covered = {}
+    for (q0, qn, pb, t0, tc, head, slot, nt), v in zip(segs, vis):
+        assert v == nk - nq + q0 + 1                     # first query's count, unclamped
+        assert qn == min(qt, nq - q0) and t0 % 64 == 0
+        covered.setdefault((int(q0), int(head)), []).append((int(t0), int(tc)))
+    for qa in range(0, nq, qt):
+        qn = min(qt, nq - qa)
+        last = max(0, min(nk, nk - nq + qa + qn))        # the tile's last query sees this many
+        for h in range(hkv):
+            got = sorted(covered.get((qa, h), []))
+            if last == 0:
+                assert not got
+                continue
+            assert got[0][0] == 0 and sum(tc for _, tc in got) == last
+            assert all(a + b == c for (a, b), (c, _) in zip(got, got[1:]))
+
+
+def test_causal_flag_without_multi_query_groups_changes_nothing():
+    levels = [([0, 1, 2], [0, 4, 8], list(range(8)), [16, 16])]
+    a = plan(levels, hq=32, hkv=8, page=16, num_pages=8)
+    b = plan(levels, hq=32, hkv=8, page=16, num_pages=8, flags=128)
+    assert a[0] == b[0] == 0 and b[1].off_seg_causal == 0
+    assert np.array_equal(a[2][: a[1].plan_ints], b[2][: b[1].plan_ints])
