@@ -17,6 +17,26 @@ namespace be {
 template <typename T>
 __device__ __forceinline__ float rnd(float x) { return to_f32(from_f32<T>(x)); }
 
+// Four consecutive 16-bit elements as one 8-byte access (the host checks the
+// alignment of every row these address).
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, T (&v)[4]) {
+  const u16x4 u = *reinterpret_cast<const u16x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint16_t b = u[e];
+    v[e] = __builtin_bit_cast(T, b);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const T (&v)[4]) {
+  u16x4 u;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) u[e] = __builtin_bit_cast(uint16_t, v[e]);
+  *reinterpret_cast<u16x4*>(p) = u;
+}
+
 // One thread per (candidate, head, 4 rotation pairs).  Heads [0, hq) are q,
 // [hq, hq + hkv) are k, [hq + hkv, hq + 2 hkv) are v (copied, not rotated).
 template <typename T>
@@ -36,24 +56,24 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const T* qkv, int64_t 
   const T* src = qkv + (int64_t)i * qkv_sn + (int64_t)h * d;
   const int j0 = qd * 4;
   T lo[4], hi[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    lo[e] = src[j0 + e];
-    hi[e] = src[half + j0 + e];
-  }
+  load4(src + j0, lo);
+  load4(src + half + j0, hi);
   if (h < hq + hkv) {
     const int64_t p = positions[i];
     if (p < 0 || p >= max_pos) {
       if (err && qd == 0 && h == 0) atomicAdd(err, 1);
       return;
     }
-    const T* c = cos_t + p * d;
-    const T* s = sin_t + p * d;
+    T cl[4], ch[4], sl[4], sh[4];
+    load4(cos_t + p * d + j0, cl);
+    load4(cos_t + p * d + half + j0, ch);
+    load4(sin_t + p * d + j0, sl);
+    load4(sin_t + p * d + half + j0, sh);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float xl = to_f32(lo[e]), xh = to_f32(hi[e]);
-      const float ol = rnd<T>(rnd<T>(xl * to_f32(c[j0 + e])) + rnd<T>(-xh * to_f32(s[j0 + e])));
-      const float oh = rnd<T>(rnd<T>(xh * to_f32(c[half + j0 + e])) + rnd<T>(xl * to_f32(s[half + j0 + e])));
+      const float ol = rnd<T>(rnd<T>(xl * to_f32(cl[e])) + rnd<T>(-xh * to_f32(sl[e])));
+      const float oh = rnd<T>(rnd<T>(xh * to_f32(ch[e])) + rnd<T>(xl * to_f32(sh[e])));
       lo[e] = from_f32<T>(ol);
       hi[e] = from_f32<T>(oh);
     }
@@ -71,11 +91,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const T* qkv, int64_t 
     const int kh = (h < hq + hkv) ? h - hq : h - hq - hkv;
     dst = kv + ((((int64_t)pg * 2 + kvsel) * page_size + sl) * hkv + kh) * d;
   }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    dst[j0 + e] = lo[e];
-    dst[half + j0 + e] = hi[e];
-  }
+  store4(dst + j0, lo);
+  store4(dst + half + j0, hi);
 }
 
 }  // namespace be
@@ -91,6 +108,10 @@ extern "C" int be_rope_qkv_append(const void* qkv, int64_t qkv_stride_n, int dty
   BE_REQUIRE(dtype == BE_F16 || dtype == BE_BF16, "rope append supports fp16 / bf16 storage");
   BE_REQUIRE(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 8 == 0, "bad head shape");
   BE_REQUIRE(qkv_stride_n >= (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim, "qkv row stride too small");
+  BE_REQUIRE(qkv_stride_n % 4 == 0 && (reinterpret_cast<uintptr_t>(qkv) & 7) == 0 &&
+                 (reinterpret_cast<uintptr_t>(cos_table) & 7) == 0 && (reinterpret_cast<uintptr_t>(sin_table) & 7) == 0 &&
+                 (reinterpret_cast<uintptr_t>(q_out) & 7) == 0 && (reinterpret_cast<uintptr_t>(kv_layer) & 7) == 0,
+             "qkv, tables, q_out and the cache must be 8-byte aligned with a qkv row stride that is a multiple of 4");
   BE_REQUIRE(num_pages > 0 && page_size > 0 && max_position > 0, "bad cache / table shape");
   const int64_t total = (int64_t)n * (num_qo_heads + 2 * num_kv_heads) * (head_dim / 8);
   const unsigned blocks = (unsigned)((total + 255) / 256);
