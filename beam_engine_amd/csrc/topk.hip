@@ -47,6 +47,7 @@ static TopkGeom topk_geom(int n_rows, int vocab, int k) {
   if (segs * k > kMaxRowCand) segs = kMaxRowCand / k;
   if (segs < 1) segs = 1;
   int seg_len = (vocab + segs - 1) / segs;
+  seg_len = (seg_len + 7) & ~7;                           // 16-byte segment starts for 16-bit logits
   segs = (vocab + seg_len - 1) / seg_len;
   return TopkGeom{segs, seg_len};
 }
@@ -65,6 +66,48 @@ template <> __device__ __forceinline__ float round_to<f16_t>(float x) { return (
 template <typename T>
 __device__ __forceinline__ float scaled(float x, float inv_temp) {
   return (inv_temp == 1.0f) ? x : round_to<T>(__fmul_rn(x, inv_temp));
+}
+
+constexpr int kPerThread = kMaxSegLen / kTopkThreads;   // logits per thread
+
+// Position inside the segment of a thread's j-th logit: chunks of 16 bytes
+// (8 bf16 / f16, 4 fp32), chunk c of thread t at c * 256 * V + t * V, so that
+// one 16-byte load per chunk covers the segment's kMaxSegLen positions once.
+template <typename T>
+__device__ __forceinline__ int seg_pos(int j) {
+  constexpr int V = 16 / (int)sizeof(T);
+  return (j / V) * (kTopkThreads * V) + (int)threadIdx.x * V + (j % V);
+}
+
+// The thread's logits of one segment (n valid positions from seg), scaled by
+// the temperature; positions >= n read as `fill`.  16-byte loads when the
+// segment start is 16-byte aligned (uniform over the workgroup), else one
+// load per logit.
+template <typename T>
+__device__ __forceinline__ void load_seg(const T* seg, int n, float inv_temp, float fill, float (&x)[kPerThread]) {
+  constexpr int V = 16 / (int)sizeof(T);
+  if ((reinterpret_cast<uintptr_t>(seg) & 15) == 0) {
+#pragma unroll
+    for (int c = 0; c < kPerThread / V; ++c) {
+      const int p0 = c * (kTopkThreads * V) + (int)threadIdx.x * V;
+      if (p0 + V <= n) {
+        const uint4 u = *reinterpret_cast<const uint4*>(seg + p0);
+        T t[V];
+        __builtin_memcpy(t, &u, 16);
+#pragma unroll
+        for (int e = 0; e < V; ++e) x[c * V + e] = scaled<T>(to_f32(t[e]), inv_temp);
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) x[c * V + e] = p0 + e < n ? scaled<T>(load_logit(seg + p0 + e), inv_temp) : fill;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const int p = seg_pos<T>(j);
+      x[j] = p < n ? scaled<T>(load_logit(seg + p), inv_temp) : fill;
+    }
+  }
 }
 
 __device__ __forceinline__ uint32_t fkey(float f) {
@@ -182,6 +225,94 @@ __device__ int block_select(const K* keys, int n, int k, int* out_pos, int* hist
   return k;
 }
 
+// block_select over keys held in registers by the segment kernel: the
+// thread's key j sits at segment position seg_pos<T>(j), present when that
+// position is < n.  Exact k largest, ties to the lowest position; writes
+// min(k, n) positions (unordered) to out_pos and their keys to out_key and
+// returns that count.  All 256 threads must call it.
+template <typename T>
+__device__ int block_select_regs(const uint32_t (&kr)[kPerThread], int n, int k, int* out_pos, uint32_t* out_key,
+                                 int* hist /*4*256*/, int* suf /*257*/, int* misc /*8*/) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const int tid = threadIdx.x, w = tid >> 6;
+  if (n <= k) {
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const int p = seg_pos<T>(j);
+      if (p < n) {
+        out_pos[p] = p;
+        out_key[p] = kr[j];
+      }
+    }
+    __syncthreads();
+    return n;
+  }
+  uint32_t prefix = 0, mask = 0;
+  int krem = k;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 4 * 256; i += kTopkThreads) hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j)
+      if (seg_pos<T>(j) < n && (kr[j] & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((kr[j] >> shift) & 255u)], 1);
+    __syncthreads();
+    suf[tid] = block_suffix_sum(hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid], misc + 4);
+    if (tid == 0) suf[256] = 0;
+    __syncthreads();
+    if (suf[tid] >= krem && suf[tid + 1] < krem) {   // unique digit
+      misc[0] = tid;
+      misc[1] = suf[tid + 1];
+    }
+    __syncthreads();
+    krem -= misc[1];
+    prefix |= ((uint32_t)misc[0]) << shift;
+    mask |= 255u << shift;
+    __syncthreads();
+  }
+  // keys > prefix: exactly k - krem of them; keys == prefix: the krem lowest
+  // positions, ranked chunk by chunk (chunk c of every thread precedes chunk
+  // c + 1 in position order; inside a chunk, threads in order)
+  if (tid == 0) misc[2] = 0;
+  __syncthreads();
+  const int ngt = k - krem;
+  int base = 0;
+#pragma unroll
+  for (int c = 0; c < kPerThread / V; ++c) {
+    int eq = 0;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int j = c * V + e;
+      if (seg_pos<T>(j) < n) {
+        if (kr[j] > prefix) {
+          const int at = atomicAdd(&misc[2], 1);
+          out_pos[at] = seg_pos<T>(j);
+          out_key[at] = kr[j];
+        } else if (kr[j] == prefix) {
+          ++eq;
+        }
+      }
+    }
+    const int incl = block_prefix_sum(eq, misc + 4);
+    const int chunk_total = misc[4] + misc[5] + misc[6] + misc[7];
+    int rank = base + incl - eq;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int j = c * V + e;
+      if (seg_pos<T>(j) < n && kr[j] == prefix) {
+        if (rank < krem) {
+          out_pos[ngt + rank] = seg_pos<T>(j);
+          out_key[ngt + rank] = prefix;
+        }
+        ++rank;
+      }
+    }
+    base += chunk_total;
+    __syncthreads();   // the wave totals are rewritten by the next chunk's scan
+  }
+  __syncthreads();
+  return k;
+}
+
 // ---------------------------------------------------------------- pass 1
 template <typename T>
 __global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logits, int64_t row_stride, int vocab,
@@ -190,23 +321,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logit
   __shared__ float redf[4];
   __shared__ double redd[4];
   const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
-  constexpr int kPer = kMaxSegLen / kTopkThreads;    // logits per thread, read once
+  constexpr int kPer = kPerThread;                   // logits per thread, read once
   const T* row = logits + (int64_t)r * row_stride;
-  const int b = s * seg_len, e = min(vocab, b + seg_len);
+  const int b = s * seg_len, n = min(vocab, b + seg_len) - b;
   float x[kPer];
+  load_seg<T>(row + b, n, inv_temp, -INFINITY, x);
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = b + threadIdx.x + j * kTopkThreads;
-    x[j] = i < e ? scaled<T>(load_logit(row + i), inv_temp) : -INFINITY;
-    m = fmaxf(m, x[j]);
-  }
+  for (int j = 0; j < kPer; ++j) m = fmaxf(m, x[j]);
   m = block_max(m, redf);
   double acc = 0.0;
   const double md = (double)m;
 #pragma unroll
   for (int j = 0; j < kPer; ++j)
-    if (b + threadIdx.x + j * kTopkThreads < e) acc += exp((double)x[j] - md);
+    if (seg_pos<T>(j) < n) acc += exp((double)x[j] - md);
   acc = block_sum_d(acc, redd);
   if (threadIdx.x == 0) {
     seg_max[(int64_t)r * segs + s] = m;
@@ -308,9 +436,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
                                                                    int seg_len, float inv_temp, int k,
                                                                    const float* seg_max, const double* seg_sum,
                                                                    float* cand_val, int32_t* cand_idx) {
-  constexpr int kPer = kMaxSegLen / kTopkThreads;    // keys per thread
-  __shared__ uint32_t keys[kMaxSegLen];
+  constexpr int kPer = kPerThread;                   // keys per thread (kept in registers)
   __shared__ int pos[kMaxK];
+  __shared__ uint32_t selkey[kMaxK];
   __shared__ int hist[4 * 256];
   __shared__ int suf[257];
   __shared__ int misc[8];
@@ -322,14 +450,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
   const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
   const T* row = logits + (int64_t)r * row_stride;
   const int b = s * seg_len, e = min(vocab, b + seg_len), n = e - b;
-  // this thread's logits (positions tid + 256 j), loaded before the row
+  // this thread's logits (positions seg_pos(j)), loaded before the row
   // normaliser so that the two latencies overlap
   float xs[kPer];
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = tid + j * kTopkThreads;
-    xs[j] = i < n ? scaled<T>(load_logit(row + b + i), inv_temp) : 0.f;
-  }
+  load_seg<T>(row + b, n, inv_temp, 0.f, xs);
   float m, L;
   if (tid == 0) misc[3] = 0;                         // candidate count
   row_norm_block(seg_max, seg_sum, r, segs, m, L, terms, mL);
@@ -338,12 +462,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
   uint32_t kmax = 0;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
-    const int i = tid + j * kTopkThreads;
+    const int i = seg_pos<T>(j);
     uint32_t key = 0;
-    if (i < n) {
-      key = fkey(logp_of<T>(xs[j], m, L));
-      keys[i] = key;
-    }
+    if (i < n) key = fkey(logp_of<T>(xs[j], m, L));
     kr[j] = key;
     kmax = key > kmax ? key : kmax;
   }
@@ -354,7 +475,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
   const uint32_t t0 = min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3]));
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
-    const int i = tid + j * kTopkThreads;
+    const int i = seg_pos<T>(j);
     if (i < n && kr[j] >= t0) {
       const int at = atomicAdd(&misc[3], 1);
       if (at < kTopkThreads) comp[at] = ((uint64_t)kr[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
@@ -364,18 +485,24 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
   const int total = misc[3];
   int cnt = k;
   if (n <= k || total > kTopkThreads) {
-    cnt = block_select<uint32_t>(keys, n, k, pos, hist, suf, misc);
+    cnt = block_select_regs<T>(kr, n, k, pos, selkey, hist, suf, misc);
   } else if (total <= 64) {
     if (w == 0) {
       const uint64_t v = wave_sort_desc<uint64_t>(lane < total ? comp[lane] : 0ull);
-      if (lane < k) pos[lane] = (int)(0xffffffffu - (uint32_t)v);
+      if (lane < k) {
+        pos[lane] = (int)(0xffffffffu - (uint32_t)v);
+        selkey[lane] = (uint32_t)(v >> 32);
+      }
     }
     __syncthreads();
   } else {
     const uint64_t v = tid < total ? comp[tid] : 0ull;
     __syncthreads();
     const uint64_t sorted = block_sort_desc<uint64_t>(v, comp);
-    if (tid < k) pos[tid] = (int)(0xffffffffu - (uint32_t)sorted);
+    if (tid < k) {
+      pos[tid] = (int)(0xffffffffu - (uint32_t)sorted);
+      selkey[tid] = (uint32_t)(sorted >> 32);
+    }
     __syncthreads();
   }
   float* cv = cand_val + ((int64_t)r * segs + s) * k;
@@ -385,7 +512,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* log
     const int p = pos[j];
     int rank = 0;
     for (int t = 0; t < cnt; ++t) rank += (pos[t] < p);
-    const uint32_t key = keys[p];
+    const uint32_t key = selkey[j];
     const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
     cv[rank] = __uint_as_float(u);
     ci[rank] = b + p;

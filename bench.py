@@ -38,7 +38,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (decode steps / attention reps)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="e2e",
-                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-prefill"])
+                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-prefill",
+                             "topk", "topk-c1"])
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
@@ -185,6 +186,63 @@ def prefill_workload(args):
     }
 
 
+def topk_workload(args):
+    """Beam selection (log_softmax + row top-2B + per-request top-B) on the GPU:
+    ``topk`` = the e2e step (8 requests x beam 16 rows of a 128256 vocabulary,
+    bf16 logits), ``topk-c1`` = config 1 (one request, beam 4, 32000, fp32).
+    Value = logits bytes / time (each logit is needed once); the CPU baseline
+    is the oracle's float64 selection on the same logits."""
+    import numpy as np
+    import torch
+    from beam_engine_amd.selection import beam_topk
+    c1 = args.workload == "topk-c1"
+    reqs, beam, vocab = (1, 4, 32000) if c1 else (8, 16, 128256)
+    dtype = torch.float32 if c1 else torch.bfloat16
+    n = reqs * beam
+    k = 2 * beam
+    steps = args.steps or 50
+    warmup = 5 if args.warmup is None else args.warmup
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(0)
+    # 32 distinct logit sets (the e2e working set is one [N, V] per step)
+    sets = [torch.randn((n, vocab), generator=g).to(dtype).to(dev) for _ in range(8)]
+    parents = torch.from_numpy(-np.random.default_rng(0).random(n))
+    rows = [beam] * reqs
+    for i in range(warmup):
+        beam_topk(sets[i % 8], k, parents, beam, request_rows=rows)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record(stream)
+        beam_topk(sets[i % 8], k, parents, beam, request_rows=rows)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    mean_us = sum(a.elapsed_time(b) for a, b in evs) * 1e3 / steps
+    byts = n * vocab * (4 if c1 else 2)
+    gbs = byts / (mean_us * 1e-6) / 1e9
+    result = {
+        "metric": "beam selection GB/s (logits bytes / time)", "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(mean_us / 1e3, 4), "higher_is_better": True,
+        "scaling": "strong", "vs_baseline": None, "dtype": "f32" if c1 else "bf16", "data": "synthetic N(0,1) logits",
+        "config": {"workload": f"beam selection, {reqs} request(s) x beam {beam}, vocab {vocab}, k {k}"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "topk_stats + topk_segment + topk_row + topk_global kernels",
+                     "bytes_per_launch": byts, "mean_launch_us": round(mean_us, 2)},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import topk as ot
+        x = sets[0][:beam].float().cpu().numpy()
+        t0 = time.perf_counter()
+        ot.beam_step(x, parents[:beam].tolist(), beam, "float32" if c1 else "bfloat16")
+        dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(beam * vocab * (4 if c1 else 2) / dt / 1e9, 4), "unit": "GB/s",
+                                  "cores": len(os.sched_getaffinity(0)), "kind": "port",
+                                  "sample": f"oracle selection (numpy float64) of one request ({beam} rows): {dt:.2f} s"}
+    return result
+
+
 # ---------------------------------------------------------------------- CPU baseline
 def cpu_baseline_attention(wl, alg_bytes):
     """The oracle (numpy float64 cascade attention + log-sum-exp merge) on one
@@ -214,6 +272,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device visible"}))
         return 1
+    if args.workload.startswith("topk"):
+        print(json.dumps(topk_workload(args)), flush=True)
+        return 0
     if args.workload == "attn-prefill":
         print(json.dumps(prefill_workload(args)), flush=True)
         return 0

@@ -104,7 +104,7 @@ def test_batched_requests_in_one_call():
         b += r
 
 
-@pytest.mark.parametrize("case", ["strided_best", "constant", "two_levels", "near_ties_bf16"])
+@pytest.mark.parametrize("case", ["strided_best", "chunk_best", "constant", "two_levels", "near_ties_bf16"])
 def test_segment_select_paths(case):
     """Logits that stress the per-segment selection: the best values all in
     one thread's stride (a single thread maximum among them), constant rows
@@ -117,6 +117,11 @@ def test_segment_select_paths(case):
         x = torch.randn((4, v), generator=g)
         x[:, ::256] += 8.0                       # every 256th token (one thread's stride per segment) is best
         logits = x.to(torch.bfloat16)
+    elif case == "chunk_best":
+        x = torch.randn((4, v), generator=g)
+        pos = torch.arange(v)
+        x[:, (pos % 2048) < 8] += 8.0            # one thread's 16-byte chunks of every segment are best
+        logits = x.to(torch.bfloat16)
     elif case == "constant":
         logits = torch.full((3, v), 0.5).to(torch.bfloat16)
     elif case == "two_levels":
@@ -128,3 +133,28 @@ def test_segment_select_paths(case):
     parents = [0.0, -0.25, -0.5, -0.75][: logits.shape[0]]
     compare(logits, parents, 16)
     compare(logits, parents, 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_unaligned_row_stride(dtype):
+    """Rows of a wider device tensor (row stride vocab + 3): segment starts
+    are not 16-byte aligned, so the kernels take their one-load-per-logit
+    path; the result is the same selection."""
+    from beam_engine_amd import beam_topk, decode_k
+    say(f"topk unaligned row stride {dtype}")
+    g = torch.Generator().manual_seed(5)
+    n, v, beam = 5, 32003, 4
+    wide = torch.randn((n, v + 3), generator=g).to(dtype)
+    logits = wide[:, :v]
+    k = decode_k(beam, v)
+    logp = ot.log_softmax_rows(logits.float().numpy(), DT[dtype], 1.0)
+    vals, idx = ot.row_topk(logp, k)
+    parents = [0.0, -0.5, -1.0, -0.25, -2.0]
+    _, flat = ot.select_global(parents, vals, idx, beam)
+    dev = wide.cuda()[:, :v]
+    assert dev.stride(0) == v + 3
+    rv, ri, (par, tok, sc) = beam_topk(dev, k, torch.tensor(parents, dtype=torch.float64), beam)
+    torch.cuda.synchronize()
+    assert np.array_equal(ri.cpu().numpy(), idx)
+    assert np.array_equal(rv.cpu().numpy().view(np.uint32), vals.view(np.uint32))
+    assert list(zip(par.tolist(), tok.tolist(), sc.tolist())) == flat
