@@ -19,6 +19,7 @@ per-row causal limit) planned once for all layers.
 
 from __future__ import annotations
 
+import gc
 import math
 from dataclasses import dataclass
 from typing import Callable, List, Optional
@@ -247,15 +248,26 @@ class GraphedDecoder:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self._pool = torch.cuda.graph_pool_handle()
-        x = None
-        for l in range(L + 1):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, pool=self._pool):
-                x, q, logits = self._segment(l, x)
-            self.graphs.append(g)
-            self.q.append(q)
-            if logits is not None:
-                self.logits = logits
+        # No automatic garbage collection inside a capture: a collected pinned
+        # host block or event is released with HIP calls that a capturing
+        # stream forbids, and that error inside a destructor aborts the
+        # process.  torch.cuda.graph still collects before each capture begins.
+        gc_on = gc.isenabled()
+        gc.collect()
+        gc.disable()
+        try:
+            x = None
+            for l in range(L + 1):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=self._pool):
+                    x, q, logits = self._segment(l, x)
+                self.graphs.append(g)
+                self.q.append(q)
+                if logits is not None:
+                    self.logits = logits
+        finally:
+            if gc_on:
+                gc.enable()
         torch.cuda.synchronize()
 
     def load_inputs(self, tok, pos, wpg, wps) -> None:
