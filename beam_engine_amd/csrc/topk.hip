@@ -326,15 +326,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logit
   const int b = s * seg_len, n = min(vocab, b + seg_len) - b;
   float x[kPer];
   load_seg<T>(row + b, n, inv_temp, -INFINITY, x);
-  float m = -INFINITY;
+  // each thread sums against its own maximum (no wait for the block's), then
+  // rescales by exp(m_t - m); a thread whose logits are all -inf adds 0
+  float mt = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) m = fmaxf(m, x[j]);
-  m = block_max(m, redf);
+  for (int j = 0; j < kPer; ++j) mt = fmaxf(mt, x[j]);
   double acc = 0.0;
-  const double md = (double)m;
+  if (mt != -INFINITY) {
+    const double md = (double)mt;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j)
-    if (seg_pos<T>(j) < n) acc += exp((double)x[j] - md);
+    for (int j = 0; j < kPer; ++j)
+      if (seg_pos<T>(j) < n) acc += exp((double)x[j] - md);
+  }
+  const float m = block_max(mt, redf);
+  if (mt != -INFINITY) acc *= exp((double)mt - (double)m);
   acc = block_sum_d(acc, redd);
   if (threadIdx.x == 0) {
     seg_max[(int64_t)r * segs + s] = m;

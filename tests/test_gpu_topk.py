@@ -158,3 +158,16 @@ def test_unaligned_row_stride(dtype):
     assert np.array_equal(ri.cpu().numpy(), idx)
     assert np.array_equal(rv.cpu().numpy().view(np.uint32), vals.view(np.uint32))
     assert list(zip(par.tolist(), tok.tolist(), sc.tolist())) == flat
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_masked_vocabulary_range(dtype):
+    """-inf over a range covering whole segments (a masked part of the
+    vocabulary): those segments add nothing to the row's exp-sum and the
+    selection equals the oracle's over the unmasked logits."""
+    say(f"topk masked vocabulary range {dtype}")
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn((3, 128256), generator=g)
+    x[:, 20000:60000] = float("-inf")
+    x[1, :100] = float("-inf")
+    compare(x.to(dtype), [0.0, -0.5, -1.0], 4)
