@@ -26,6 +26,7 @@ BE_PLAN_NO_REGS = 32
 BE_PLAN_NO_WIDE = 64
 BE_PLAN_CAUSAL = 128
 BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
+BE_TEMP_RECIPROCAL, BE_TEMP_DIVIDE = 0, 1
 
 _DTYPES = {torch.float32: BE_F32, torch.float16: BE_F16, torch.bfloat16: BE_BF16}
 
@@ -110,8 +111,8 @@ def load() -> ctypes.CDLL:
     lib.be_merge_states.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]
     lib.be_beam_topk_workspace_bytes.argtypes = [i32, i32, i32]
     lib.be_beam_topk_workspace_bytes.restype = i64
-    lib.be_beam_topk.argtypes = [vp, i32, i32, i32, i64, ctypes.c_float, i32, vp, i32, i32, vp, i32, vp, vp, vp,
-                                 vp, vp, vp, i64, vp]
+    lib.be_beam_topk.argtypes = [vp, i32, i32, i32, i64, ctypes.c_double, i32, i32, vp, i32, i32, vp, i32, vp, vp,
+                                 vp, vp, vp, vp, i64, vp]
     lib.be_diverse_select.argtypes = [vp, vp, i32, i32, vp, i32, vp, i32, i32, i32, ctypes.c_double, vp, vp, vp,
                                       vp]
     lib.be_trie_cascade.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, vp, i64, ctypes.POINTER(ctypes.c_int64)]

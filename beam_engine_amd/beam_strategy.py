@@ -67,7 +67,8 @@ class VanillaBeamSearchStrategy(BeamStrategy):
                 for i, inp in enumerate(new_candidates)]
 
     def select_from_logits(self, beam_state: BeamState, logits: torch.Tensor, temperature: float = 1.0,
-                           rows: Optional[Tuple[int, int]] = None) -> List[BeamGenerateResult]:
+                           rows: Optional[Tuple[int, int]] = None,
+                           temperature_mode: str = "reciprocal") -> List[BeamGenerateResult]:
         """GPU selection for the candidates ``rows = (begin, end)`` (default:
         all) of ``beam_state`` from their logits ``[end - begin, V]``."""
         cands = beam_state.candidates
@@ -77,7 +78,8 @@ class VanillaBeamSearchStrategy(BeamStrategy):
             return []
         k = decode_k(beam_state.beam_size, logits.shape[-1])
         parents = torch.tensor([c.score for c in sub], dtype=torch.float64)
-        _, _, (par, tok, sc) = beam_topk(logits, k, parents, beam_state.beam_size, temperature)
+        _, _, (par, tok, sc) = beam_topk(logits, k, parents, beam_state.beam_size, temperature,
+                                         temperature_mode=temperature_mode)
         par, tok, sc = par.tolist(), tok.tolist(), sc.tolist()
         per: List[List[BeamToken]] = [[] for _ in sub]
         for p, t, s in zip(par, tok, sc):
@@ -85,8 +87,8 @@ class VanillaBeamSearchStrategy(BeamStrategy):
                 per[p].append(BeamToken(token_id=t, accumulated_score=s))
         return [BeamGenerateResult(candidate=c, children=per[i]) for i, c in enumerate(sub)]
 
-    def select_batched(self, beam_state: BeamState, logits: torch.Tensor,
-                       temperature: float = 1.0) -> List[BeamGenerateResult]:
+    def select_batched(self, beam_state: BeamState, logits: torch.Tensor, temperature: float = 1.0,
+                       temperature_mode: str = "reciprocal") -> List[BeamGenerateResult]:
         """GPU selection for every request of a multi-request state in one
         call: candidates of one request are consecutive; ``logits [N, V]``."""
         cands = beam_state.candidates
@@ -100,7 +102,8 @@ class VanillaBeamSearchStrategy(BeamStrategy):
         k = decode_k(beam_state.beam_size, logits.shape[-1])
         parents = torch.tensor([c.score for c in cands], dtype=torch.float64)
         b = beam_state.beam_size
-        _, _, (par, tok, sc) = beam_topk(logits, k, parents, b, temperature, request_rows=rows, to_host=True)
+        _, _, (par, tok, sc) = beam_topk(logits, k, parents, b, temperature, request_rows=rows, to_host=True,
+                                         temperature_mode=temperature_mode)
         per: List[List[BeamToken]] = [[] for _ in cands]
         for p, t, s_ in zip(par.tolist(), tok.tolist(), sc.tolist()):
             if p >= 0:
@@ -223,7 +226,8 @@ class DiverseBeamSearchStrategy(BeamStrategy):
         return [BeamGenerateResult(candidate=c, children=per[i]) for i, c in enumerate(cands)]
 
     def select_from_logits(self, beam_state: BeamState, logits: torch.Tensor, temperature: float = 1.0,
-                           rows: Optional[Tuple[int, int]] = None) -> List[BeamGenerateResult]:
+                           rows: Optional[Tuple[int, int]] = None,
+                           temperature_mode: str = "reciprocal") -> List[BeamGenerateResult]:
         """Selection for the candidates ``rows = (begin, end)`` (default: all)
         of ``beam_state`` from their logits ``[end - begin, V]``."""
         cands = beam_state.candidates
@@ -232,7 +236,7 @@ class DiverseBeamSearchStrategy(BeamStrategy):
         if not sub:
             return []
         k = decode_k(beam_state.beam_size, logits.shape[-1])
-        vals, idx = beam_topk(logits, k, temperature=temperature)
+        vals, idx = beam_topk(logits, k, temperature=temperature, temperature_mode=temperature_mode)
         if self.diversity_type != "hamming":
             v, ix = vals.cpu().tolist(), idx.cpu().tolist()
             inputs = [BeamGenerateInput(c, [BeamTokenCandidate(int(t), float(x)) for t, x in zip(ix[r], v[r])])
@@ -243,8 +247,8 @@ class DiverseBeamSearchStrategy(BeamStrategy):
                                       self.diversity_penalty)
         return self._rows_to_results(sub, par, tok, sc)
 
-    def select_batched(self, beam_state: BeamState, logits: torch.Tensor,
-                       temperature: float = 1.0) -> List[BeamGenerateResult]:
+    def select_batched(self, beam_state: BeamState, logits: torch.Tensor, temperature: float = 1.0,
+                       temperature_mode: str = "reciprocal") -> List[BeamGenerateResult]:
         """Selection for every request of a multi-request state (its candidates
         consecutive per request; ``logits [N, V]``), each request on its own."""
         cands = beam_state.candidates
@@ -256,7 +260,8 @@ class DiverseBeamSearchStrategy(BeamStrategy):
                 e = b
                 while e < len(cands) and cands[e].request_id == cands[b].request_id:
                     e += 1
-                out += self.select_from_logits(beam_state, logits[b:e], temperature, rows=(b, e))
+                out += self.select_from_logits(beam_state, logits[b:e], temperature, rows=(b, e),
+                                               temperature_mode=temperature_mode)
                 b = e
             return out
         rows = []
@@ -265,7 +270,7 @@ class DiverseBeamSearchStrategy(BeamStrategy):
                 rows.append(0)
             rows[-1] += 1
         k = decode_k(beam_state.beam_size, logits.shape[-1])
-        vals, idx = beam_topk(logits, k, temperature=temperature)
+        vals, idx = beam_topk(logits, k, temperature=temperature, temperature_mode=temperature_mode)
         parents = torch.tensor([c.score for c in cands], dtype=torch.float64)
         par, tok, sc = diverse_select(vals, idx, parents, beam_state.beam_size, self.num_groups,
                                       self.diversity_penalty, request_rows=rows)

@@ -4,7 +4,12 @@
 // top-B of VanillaBeamSearchStrategy.select_candidates with float64 scores and
 // a stable sort (beam_strategy.py:433-488).  Floating-point contract (shared
 // with the CPU restatement used as test oracle):
-//   x'   = round_dtype(x * inv_temp)                   (only if inv_temp != 1)
+//   x'   = x                                           (temperature 1)
+//   x'   = round_dtype(x * fl32(1 / T))                (BE_TEMP_RECIPROCAL: torch's
+//          `logits / T` on a device tensor multiplies by the reciprocal of the
+//          double temperature rounded to float)
+//   x'   = round_dtype(x / T)                          (BE_TEMP_DIVIDE: correctly
+//          rounded division, torch's `logits / T` on a CPU tensor)
 //   m    = max_i x'_i
 //   S    = sum_i exp(fl64(x'_i - m))                    (float64)
 //   L    = fl32(ln S)
@@ -63,9 +68,18 @@ template <> __device__ __forceinline__ float round_to<bf16_t>(float x) {
 }
 template <> __device__ __forceinline__ float round_to<f16_t>(float x) { return (float)(_Float16)x; }
 
+// Temperature scaling: tdiv == 0 multiplies by t (the float reciprocal of the
+// temperature, computed on the host), tdiv == 1 divides by t (the temperature);
+// t == 1 leaves the logits unchanged in both modes.
+struct TempScale {
+  float t;
+  int tdiv;
+};
+
 template <typename T>
-__device__ __forceinline__ float scaled(float x, float inv_temp) {
-  return (inv_temp == 1.0f) ? x : round_to<T>(__fmul_rn(x, inv_temp));
+__device__ __forceinline__ float scaled(float x, TempScale ts) {
+  if (ts.t == 1.0f) return x;
+  return round_to<T>(ts.tdiv ? __fdiv_rn(x, ts.t) : __fmul_rn(x, ts.t));
 }
 
 constexpr int kPerThread = kMaxSegLen / kTopkThreads;   // logits per thread
@@ -84,7 +98,7 @@ __device__ __forceinline__ int seg_pos(int j) {
 // segment start is 16-byte aligned (uniform over the workgroup), else one
 // load per logit.
 template <typename T>
-__device__ __forceinline__ void load_seg(const T* seg, int n, float inv_temp, float fill, float (&x)[kPerThread]) {
+__device__ __forceinline__ void load_seg(const T* seg, int n, TempScale inv_temp, float fill, float (&x)[kPerThread]) {
   constexpr int V = 16 / (int)sizeof(T);
   if ((reinterpret_cast<uintptr_t>(seg) & 15) == 0) {
 #pragma unroll
@@ -316,7 +330,7 @@ __device__ int block_select_regs(const uint32_t (&kr)[kPerThread], int n, int k,
 // ---------------------------------------------------------------- pass 1
 template <typename T>
 __global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logits, int64_t row_stride, int vocab,
-                                                                 int seg_len, float inv_temp, float* seg_max,
+                                                                 int seg_len, TempScale inv_temp, float* seg_max,
                                                                  double* seg_sum) {
   __shared__ float redf[4];
   __shared__ double redd[4];
@@ -438,7 +452,7 @@ __device__ K wave_sort_desc(K v) {
 // all keys.
 template <typename T>
 __global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* logits, int64_t row_stride, int vocab,
-                                                                   int seg_len, float inv_temp, int k,
+                                                                   int seg_len, TempScale inv_temp, int k,
                                                                    const float* seg_max, const double* seg_sum,
                                                                    float* cand_val, int32_t* cand_idx) {
   constexpr int kPer = kPerThread;                   // keys per thread (kept in registers)
@@ -723,7 +737,8 @@ int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k) {
   return ns * 4 + ns * 8 + ns * k * 4 + ns * k * 4 + 256;
 }
 
-int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, float inv_temp, int k,
+int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, double temperature,
+                 int temp_mode, int k,
                  const double* parent_scores, int beam, int n_req, const int32_t* req_row_ptr, int max_req_rows,
                  float* row_vals, int32_t* row_idx, int32_t* out_parent, int32_t* out_token, double* out_score,
                  void* workspace, int64_t workspace_bytes, void* stream) {
@@ -733,7 +748,14 @@ int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t r
   BE_REQUIRE(k >= 1 && k <= vocab, "k = %d outside [1, vocab = %d]", k, vocab);
   if (k > be::kMaxK) return be::fail(BE_ERR_UNSUPPORTED, "k = %d exceeds %d", k, be::kMaxK);
   BE_REQUIRE(row_stride >= vocab, "row stride %lld < vocab %d", (long long)row_stride, vocab);
-  BE_REQUIRE(inv_temp > 0.f && isfinite(inv_temp), "inverse temperature must be positive and finite");
+  BE_REQUIRE(temperature > 0.0 && isfinite(temperature), "temperature must be positive and finite");
+  BE_REQUIRE(temp_mode == BE_TEMP_RECIPROCAL || temp_mode == BE_TEMP_DIVIDE, "unknown temperature mode %d",
+             temp_mode);
+  // reciprocal: the double reciprocal of the temperature rounded to float, the
+  // constant torch multiplies a device tensor by for `logits / temperature`;
+  // divide: the float temperature itself
+  const float tval = temp_mode == BE_TEMP_DIVIDE ? (float)temperature : (float)(1.0 / temperature);
+  const be::TempScale inv_temp{temperature == 1.0 ? 1.0f : tval, temp_mode == BE_TEMP_DIVIDE ? 1 : 0};
   BE_REQUIRE(beam >= 0, "beam must be >= 0");
   if (beam > 0) {
     BE_REQUIRE(parent_scores && out_parent && out_token && out_score, "null selection output");

@@ -48,7 +48,8 @@ class BatchedBeamSearch:
     def __init__(self, model, page_table: PageTable, beam_size: int,
                  strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
                  temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False,
-                 graphs: bool = False, eos_token_id: Optional[int] = None):
+                 graphs: bool = False, eos_token_id: Optional[int] = None, temperature_mode: str = "reciprocal",
+                 picker_costs: str = "mi355x"):
         if kernel_type not in ("cascade", "flat", "tree", "auto"):
             raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat', 'tree' or 'auto'.")
         self.model = model
@@ -57,6 +58,7 @@ class BatchedBeamSearch:
         self.strategy = strategy or VanillaBeamSearchStrategy()
         self.kernel_type = kernel_type
         self.temperature = temperature
+        self.temperature_mode = temperature_mode   # arithmetic of logits / T: see selection.beam_topk
         self.include_self = include_self
         self.eos_token_id = eos_token_id    # a pick of this token finishes its beam (off: None)
         self.device = page_table.device
@@ -66,6 +68,7 @@ class BatchedBeamSearch:
         self.flat = BatchDecodeWithPagedKVCacheWrapper(self.ws)
         self.last_attn = None
         self.picker = None
+        self.picker_costs = picker_costs    # "mi355x" fitted costs or "fasttree" (the reference's edge model)
         self.step_log: List[dict] = []
         self._staging = torch.empty(4 * 4096, dtype=torch.int64, pin_memory=True)
         self.attn_timer = None          # optional callable(layer, fn) used by benchmarks
@@ -85,8 +88,10 @@ class BatchedBeamSearch:
         logits = self.model.prefill(ids, self.pt, page_ids)
         results = []
         k = min(2 * self.beam_size, logits.shape[-1])
-        vals, idx = beam_topk(logits, k, temperature=self.temperature)
+        vals, idx = beam_topk(logits, k, temperature=self.temperature, temperature_mode=self.temperature_mode)
+        self.pt.stage_errors()
         vals, idx = vals[:, : self.beam_size].tolist(), idx[:, : self.beam_size].tolist()
+        self.pt.raise_staged_errors()          # the prompt's KV writes (ValueError on a bad page)
         for r, cand in enumerate(self.state.candidates):
             results.append(BeamGenerateResult(cand, [BeamToken(int(t), float(s)) for t, s in zip(idx[r], vals[r])]))
         self.state.add_filtered_results(results)
@@ -95,9 +100,10 @@ class BatchedBeamSearch:
     # ---------------------------------------------------------------- decode
     def _get_picker(self):
         if self.picker is None:
-            from .picker import StrategyPicker
+            from .picker import MI355X, StrategyPicker
             cfg = self.model.cfg
-            self.picker = StrategyPicker(cfg.num_attention_heads, cfg.num_key_value_heads, self.pt.page_size)
+            costs = "fasttree" if self.picker_costs == "fasttree" else MI355X
+            self.picker = StrategyPicker(cfg.num_attention_heads, cfg.num_key_value_heads, self.pt.page_size, costs)
         return self.picker
 
     def _plan(self, kind: str, levels=None):
@@ -134,7 +140,8 @@ class BatchedBeamSearch:
             levels, qids, wp, wpos, pos = st.step_metadata()
         else:
             if kind == "tree":
-                levels = st.tree_lists(self._get_picker().model.absorb)
+                p = self._get_picker()
+                levels = st.tree_lists((p.edges or p.model).absorb)
             elif kind == "auto":
                 plan = self._get_picker().choose(st)
                 kind, levels = plan.kind, plan.levels
@@ -166,6 +173,12 @@ class BatchedBeamSearch:
         self._select(logits)
         self.step_log.append({"n": n, "kind": kind})
 
+    def prepare_graphs(self) -> None:
+        """Capture the segment graphs now for the current candidate count (the
+        first decode step would otherwise capture them)."""
+        if self.graphs and hasattr(self.model, "decode") and self.state.candidates:
+            self._graph_ready(len(self.state.candidates))
+
     def _graph_ready(self, n: int) -> bool:
         """Capture the segment graphs once the candidate count is known (it
         stays B per request); a different count runs eagerly."""
@@ -177,7 +190,12 @@ class BatchedBeamSearch:
 
     def _select(self, logits: torch.Tensor) -> None:
         st = self.state
-        st.add_filtered_results(self.strategy.select_batched(st, logits, self.temperature), self.eos_token_id)
+        # the step's KV appends (and the previous step's fork copies) report
+        # out-of-pool entries at the selection's synchronisation
+        self.pt.stage_errors()
+        results = self.strategy.select_batched(st, logits, self.temperature, self.temperature_mode)
+        self.pt.raise_staged_errors()
+        st.add_filtered_results(results, self.eos_token_id)
 
     # ---------------------------------------------------------------- results
     def final_sequences(self, num_return: Optional[int] = None):

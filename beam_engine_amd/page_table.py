@@ -64,6 +64,10 @@ class PageTable:
                                    dtype=store_dtype, device=self.device)
         self.kv_cache_at_layer: List[torch.Tensor] = [self.kv_pool[l] for l in range(layer_num)]
         self.layer_stride_bytes = self.kv_pool.stride(0) * self.kv_pool.element_size()
+        # device count of append / copy entries the kernels skipped for naming a
+        # page, slot or position outside the pool (read by check_errors)
+        self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._err_host = torch.zeros(1, dtype=torch.int32, pin_memory=self.device.type == "cuda")
         logger.info("Initialized PageTable: %d layers, %d pages of size %d", layer_num, max_num_pages, page_size)
 
     # ------------------------------------------------------------ allocator
@@ -112,6 +116,31 @@ class PageTable:
     def num_free_pages(self) -> int:
         return len(self.free_pages)
 
+    # ------------------------------------------------------------ device errors
+    def stage_errors(self) -> None:
+        """Queue a copy of the device error count to the host on the current
+        stream; ``raise_staged_errors`` reads it after the caller's next
+        synchronisation (the decode step's selection), costing no extra wait."""
+        self._err_host.copy_(self._err, non_blocking=True)
+
+    def raise_staged_errors(self) -> None:
+        """Raise ValueError if the staged count is non-zero (the reference
+        raises ValueError for a write to a page it does not hold,
+        page_table.py:150-151); the device count is cleared first."""
+        bad = int(self._err_host[0])
+        if bad:
+            self._err.zero_()
+            self._err_host.zero_()
+            raise ValueError(f"{bad} KV append / copy entries named a page, slot or position outside the pool "
+                             f"({self.max_num_pages} pages of {self.page_size} slots) and were not written")
+
+    def check_errors(self) -> None:
+        """Synchronise the stream and raise ValueError if any append or copy
+        since the last check skipped an entry (see ``raise_staged_errors``)."""
+        self.stage_errors()
+        torch.cuda.current_stream(self.device).synchronize()
+        self.raise_staged_errors()
+
     # ------------------------------------------------------------ copies
     def copy_block(self, page_idx: int, length: int) -> int:
         """Allocate a page and copy the first ``length`` slots of K and V of
@@ -148,7 +177,7 @@ class PageTable:
         rc = lib.be_page_copy(self.kv_pool.data_ptr(), self.layer_stride_bytes, self.layer_num,
                               _lib.dtype_code(self.store_dtype), self.max_num_pages, self.page_size,
                               self.head_num, self.head_dim, dev[0].data_ptr(), dev[1].data_ptr(),
-                              dev[2].data_ptr(), len(todo), None, _lib.stream_ptr(self.device))
+                              dev[2].data_ptr(), len(todo), self._err.data_ptr(), _lib.stream_ptr(self.device))
         _lib.check(rc, "page copy")
         return len(todo)
 
@@ -176,7 +205,9 @@ class PageTable:
                                 kv_indptr: Optional[torch.Tensor] = None) -> None:
         """Append one token per candidate: ``kv[page_indices[i], :, indices[i]] = (keys[i], values[i])``
         (page_table.py:167-209).  ``batch_indices``/``kv_indptr`` are accepted
-        for signature compatibility (the reference passes the identity layout)."""
+        for signature compatibility (the reference passes the identity layout).
+        Entries outside the pool are skipped on the device and counted; the
+        next ``check_errors`` (the engine's per-step check) raises ValueError."""
         if layer < 0 or layer >= self.layer_num:
             raise ValueError(f"Layer {layer} out of range (max: {self.layer_num - 1})")
         n = keys.shape[0]
@@ -196,8 +227,8 @@ class PageTable:
         rc = lib.be_kv_append(self.kv_cache_at_layer[layer].data_ptr(), _lib.dtype_code(self.store_dtype),
                               self.max_num_pages, self.page_size, self.head_num, self.head_dim,
                               page_indices.data_ptr(), indices.data_ptr(), keys.data_ptr(), keys.stride(0),
-                              keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1), n, None,
-                              _lib.stream_ptr(self.device))
+                              keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1), n,
+                              self._err.data_ptr(), _lib.stream_ptr(self.device))
         _lib.check(rc, "kv append")
 
     def write_rope_qkv(self, layer: int, qkv: torch.Tensor, num_qo_heads: int, positions: torch.Tensor,
@@ -233,7 +264,8 @@ class PageTable:
                                     self.head_num, self.head_dim, positions.data_ptr(), cos.data_ptr(),
                                     sin.data_ptr(), cos.shape[0], q_out.data_ptr(),
                                     self.kv_cache_at_layer[layer].data_ptr(), self.max_num_pages, self.page_size,
-                                    page_indices.data_ptr(), indices.data_ptr(), None, _lib.stream_ptr(self.device))
+                                    page_indices.data_ptr(), indices.data_ptr(), self._err.data_ptr(),
+                                    _lib.stream_ptr(self.device))
         _lib.check(rc, "rope append")
         return q_out
 

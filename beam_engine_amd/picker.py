@@ -101,6 +101,36 @@ class CostModel:
         return absorb < split
 
 
+class FastTreeCostModel:
+    """The reference's own edge model (attention/fasttree/preparation.py:34-57,
+    constants of metadata.py:12-38): padded-tile work ``Cmm(nQ, nK) = alpha *
+    padQ * g * nK + beta * padK * nQ * g`` with query tiles (64 / g, 16 / g) and
+    KV tiles (32, 32) -- the second tile pair when the node has at most 16 / g
+    queries -- and a merge when SplitK (separate passes plus gamma per merged
+    query) costs more than SplitQ (the child re-reads the parent's KV).  Used
+    by ``StrategyPicker(costs="fasttree")`` to decide the tree's edges exactly
+    as the reference's FastTree preparation would, on this build's kernels."""
+
+    def __init__(self, num_qo_heads: int, num_kv_heads: int, alpha: float = 0.6, beta: float = 0.3,
+                 gamma: float = 0.1):
+        self.g = num_qo_heads // num_kv_heads
+        self.alpha, self.beta, self.gamma = alpha, beta, gamma
+        self.q_tiles = (64 // self.g, 16 // self.g)
+        self.kv_tiles = (32, 32)
+
+    def cmm(self, nq: int, nk: int) -> float:
+        ph = 0 if nq > self.q_tiles[1] else 1
+        tq, tk = self.q_tiles[ph], self.kv_tiles[ph]
+        pad_q = tq - ((nq - 1) % tq + 1)
+        pad_k = max(0, tk - nk)
+        return self.alpha * pad_q * self.g * nk + self.beta * pad_k * nq * self.g
+
+    def absorb(self, nq_cur: int, nq_child: int, len_parent: int, len_child: int) -> bool:
+        split_k = self.cmm(nq_cur, len_parent) + self.cmm(nq_child, len_child) + self.gamma * nq_child
+        split_q = self.cmm(nq_cur - nq_child, len_parent) + self.cmm(nq_child, len_child + len_parent)
+        return split_k > split_q
+
+
 @dataclass
 class Plan:
     kind: str                       # "flat", "split" or "tree"
@@ -154,8 +184,18 @@ class StrategyPicker:
     options are costed on the segment tree; only the chosen one is laid out
     as level arrays."""
 
-    def __init__(self, num_qo_heads: int, num_kv_heads: int, page_size: int, costs: KernelCosts = MI355X,
+    def __init__(self, num_qo_heads: int, num_kv_heads: int, page_size: int, costs=MI355X,
                  candidates=("flat", "split", "tree")):
+        """``costs``: ``KernelCosts`` (this build's fitted MI355X costs price
+        every option and decide the tree's edges) or ``"fasttree"`` (the tree's
+        edges decided by the reference's FastTree model, ``FastTreeCostModel``;
+        the options are still priced with the MI355X costs)."""
+        self.edges = None
+        if isinstance(costs, str):
+            if costs != "fasttree":
+                raise ValueError(f"unknown cost model {costs!r}")
+            self.edges = FastTreeCostModel(num_qo_heads, num_kv_heads)
+            costs = MI355X
         self.model = CostModel(num_qo_heads, num_kv_heads, page_size, costs)
         self.page_size = page_size
         self.candidates = tuple(candidates)
@@ -177,7 +217,7 @@ class StrategyPicker:
                 absorbed = set()
                 cost = decomposition_cost(m, segs, paths, absorbed, [sg[1] for sg in segs])
             else:
-                absorbed, teff = state.absorb_edges(segs, m.absorb)
+                absorbed, teff = state.absorb_edges(segs, (self.edges or m).absorb)
                 cost = decomposition_cost(m, segs, paths, absorbed, teff)
             out[kind] = (cost, absorbed)
         return segs, paths, out

@@ -51,11 +51,22 @@ def _staging(dev, name, n, dtype):
     return t[:n]
 
 
+TEMPERATURE_MODES = {"reciprocal": _lib.BE_TEMP_RECIPROCAL, "divide": _lib.BE_TEMP_DIVIDE}
+
+
 def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor] = None, beam: int = 0,
               temperature: float = 1.0, workspace: Optional[TopkWorkspace] = None,
-              request_rows: Optional[Sequence[int]] = None, to_host: bool = False):
+              request_rows: Optional[Sequence[int]] = None, to_host: bool = False,
+              temperature_mode: str = "reciprocal"):
     """Row top-k of log_softmax(logits / T) and, when ``beam > 0``, the top-``beam``
     of ``parent_scores[r] + logp`` (float64) within every request.
+
+    ``logits / T`` (beam.py:107, :270) has the arithmetic of ``temperature_mode``:
+    "reciprocal" multiplies by ``fl32(1.0 / T)`` (the reciprocal of the Python
+    float taken in double, rounded to float) -- what torch computes for a GPU
+    tensor divided by a Python float, i.e. the reference's own arithmetic --
+    and "divide" divides by ``fl32(T)`` with correct rounding, as torch does
+    for a CPU tensor.
 
     ``request_rows`` partitions the rows into consecutive requests (default:
     one request).  Returns ``(row_vals [N, k] f32, row_idx [N, k] i32)`` and, if
@@ -72,10 +83,13 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
     if logits.stride(1) != 1:
         logits = logits.contiguous()
     n, v = logits.shape
-    if temperature <= 0:
-        raise ValueError("temperature must be positive")
+    if not temperature > 0 or not np.isfinite(temperature):
+        raise ValueError("temperature must be positive and finite")
+    try:
+        tmode = TEMPERATURE_MODES[temperature_mode]
+    except KeyError:
+        raise ValueError(f"temperature_mode must be one of {sorted(TEMPERATURE_MODES)}") from None
     dev = logits.device
-    inv_t = 1.0 if temperature == 1.0 else float(torch.tensor(1.0 / temperature, dtype=torch.float32))
     ws = workspace or _default_ws.setdefault((dev.type, dev.index), TopkWorkspace(dev))
     need = lib.be_beam_topk_workspace_bytes(n, v, k)
     buf = ws.get(need)
@@ -111,7 +125,8 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
         outs = (torch.empty(n_req * beam, dtype=torch.int32, device=dev),
                 torch.empty(n_req * beam, dtype=torch.int32, device=dev),
                 torch.empty(n_req * beam, dtype=torch.float64, device=dev))
-    rc = lib.be_beam_topk(logits.data_ptr(), _lib.dtype_code(logits.dtype), n, v, logits.stride(0), inv_t, k,
+    rc = lib.be_beam_topk(logits.data_ptr(), _lib.dtype_code(logits.dtype), n, v, logits.stride(0),
+                          float(temperature), tmode, k,
                           _lib.ptr(ps), beam, n_req, _lib.ptr(ptr_dev), max_rows, row_vals.data_ptr(),
                           row_idx.data_ptr(), _lib.ptr(outs[0]), _lib.ptr(outs[1]), _lib.ptr(outs[2]),
                           buf.data_ptr(), buf.numel(), _lib.stream_ptr(dev))
@@ -152,10 +167,14 @@ def diverse_select(row_vals: torch.Tensor, row_idx: torch.Tensor, parent_scores:
     row_vals, row_idx = row_vals.contiguous(), row_idx.contiguous()
     if parent_scores.numel() != n:
         raise ValueError("parent_scores must have one entry per row")
-    if parent_scores.device.type == "cpu":
+    if parent_scores.device.type == "cpu" and to_host:
+        # the shared staging buffer is free again once this call synchronises
         host = _staging(dev, "dbs_parents", n, torch.float64)
         host.copy_(parent_scores.reshape(-1))
         ps = host.to(dev, non_blocking=True)
+    elif parent_scores.device.type == "cpu":
+        # no synchronisation at the end: a copy that completes before returning
+        ps = parent_scores.reshape(-1).to(dtype=torch.float64).to(dev)
     else:
         ps = parent_scores.to(dtype=torch.float64).contiguous()
     n_req, max_rows, ptr_dev = 1, n, None

@@ -1,10 +1,14 @@
 #!/usr/bin/env python3
 """Benchmark driver (one JSON line on stdout).
 
-Default workload ``e2e``: end-to-end batched beam search on a random-init
-Llama-3-8B-shaped decoder (8 requests x beam 16, 1024-token prompts); value = beam-decode tokens/s
-= sum over requests of beam width x decode steps / decode wall time.  A step
-is one decode step of all 8 requests x 16 beams.
+Default workload ``e2e`` (harness in ``bench_e2e.py``):
+end-to-end batched beam search on a random-init Llama-3-8B-shaped decoder
+(8 requests x beam 16, 1024-token prompts, 256 generated tokens); value =
+beam-decode tokens/s = 128 candidate tokens per step / step time over
+``--steps`` steps sampled evenly across the 256-step generation after
+``--warmup`` untimed steps.  A step is one decode step of all 8 requests x 16
+beams.  The flat strategy decodes the same prompts in the same process
+(``config.flat``, ``config.vs_flat``).
 
 Attention workloads (``--workload attn-c2|attn-ns|attn-c3|attn-c5|attn-c1``)
 time one decode-attention layer at a benchmark shape over 32 distinct per-layer
@@ -23,7 +27,6 @@ import argparse
 import json
 import math
 import os
-import platform
 import statistics
 import sys
 import time
@@ -48,6 +51,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true", help="e2e: launch every op eagerly (no HIP graphs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-flat", action="store_true", help="e2e: skip the flat-strategy run of the same prompts")
+    ap.add_argument("--picker-costs", default="mi355x", choices=["mi355x", "fasttree"],
+                    help="e2e tree / auto: edge decisions by the MI355X-fitted costs or the reference's FastTree model")
     ap.add_argument("--verbose", action="store_true")
     return ap.parse_args()
 
@@ -245,21 +251,24 @@ def topk_workload(args):
 
 # ---------------------------------------------------------------------- CPU baseline
 def cpu_baseline_attention(wl, alg_bytes):
-    """The oracle (numpy float64 cascade attention + log-sum-exp merge) on one
-    layer of the same workload, in GB/s of the same algorithmic bytes."""
-    import numpy as np
+    """The CPU restatement (torch float32 paged gather, per-level softmax
+    attention, log-sum-exp merge: BASELINE's CPU plan) on one layer of the
+    same workload, in GB/s of the same algorithmic bytes."""
+    import torch
+    from bench_e2e import cpu_model
     from oracle import attention as oa
     threads = len(os.sched_getaffinity(0))
-    rng = np.random.default_rng(0)
-    kv = rng.standard_normal((wl.num_pages, 2, wl.page, wl.hkv, wl.d)).astype(np.float32)
-    q = rng.standard_normal((wl.num_queries, wl.hq, wl.d)).astype(np.float32)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    kv = torch.randn((wl.num_pages, 2, wl.page, wl.hkv, wl.d), generator=g)
+    q = torch.randn((wl.num_queries, wl.hq, wl.d), generator=g)
     t0 = time.perf_counter()
-    oa.cascade_attention(q, kv, *wl.levels, wl.page, wl.d ** -0.5)
+    oa.cascade_attention_torch(q, kv, *wl.levels, wl.page, wl.d ** -0.5)
     dt = time.perf_counter() - t0
     gbs = alg_bytes / dt / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle cascade attention (numpy float64, BLAS threads = {threads}) over all "
-                      f"{wl.num_queries} queries of one layer: {dt:.2f} s; cpu {platform.processor() or platform.machine()}"}
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port", "cpu": cpu_model(),
+            "sample": f"torch float32 cascade attention on the host ({threads} threads) over all "
+                      f"{wl.num_queries} queries of one layer: {dt:.2f} s"}
 
 
 def main():
@@ -286,7 +295,7 @@ def main():
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = cpu_baseline_attention(wl, result["roofline"]["bytes_per_launch"])
     else:
-        from beam_engine_amd.e2e import run_e2e_bench
+        from bench_e2e import run_e2e_bench
         result = run_e2e_bench(args)
     print(json.dumps(result), flush=True)
     return 0

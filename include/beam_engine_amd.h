@@ -274,8 +274,16 @@ int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, cons
 
 /* ------------------------------------------------------------------ beam top-k
  * be_beam_topk: one decode-step selection over logits [n_rows, vocab]
- * (dtype, row stride in elements):
- *   x' = round_dtype(x * inv_temp)   (skipped when inv_temp == 1)
+ * (dtype, row stride in elements).  The reference scales by the temperature
+ * with `logits / temperature` when it is not 1 (src/beam_engine/beam.py:107,
+ * :270); temp_mode picks the arithmetic of that division:
+ *   BE_TEMP_RECIPROCAL  x' = round_dtype(x * fl32(1.0 / T)), the reciprocal taken in
+ *                       double and rounded to float -- what torch runs for a
+ *                       device tensor divided by a Python float (measured on
+ *                       MI355X; the reference's logits live on the GPU);
+ *   BE_TEMP_DIVIDE      x' = round_dtype(x / fl32(T)), correctly rounded in fp32 --
+ *                       torch's CPU tensor division;
+ * both leave x unchanged when T == 1.  Then
  *   logp = round_dtype(fl32(fl32(x' - max) - fl32(ln sum exp(x' - max))))
  *          with the exponential sum accumulated in float64;
  *   per row the k best (logp desc, index asc) -> row_vals/row_idx [n_rows, k];
@@ -289,9 +297,11 @@ int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, cons
  *   request (host-side pool capacity check).
  * All pointers are device pointers.  workspace must hold
  * be_beam_topk_workspace_bytes(n_rows, vocab, k) bytes. */
+#define BE_TEMP_RECIPROCAL 0
+#define BE_TEMP_DIVIDE 1
 int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k);
 int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride,
-                 float inv_temp, int k, const double* parent_scores, int beam, int n_req,
+                 double temperature, int temp_mode, int k, const double* parent_scores, int beam, int n_req,
                  const int32_t* req_row_ptr, int max_req_rows, float* row_vals, int32_t* row_idx,
                  int32_t* out_parent, int32_t* out_token, double* out_score, void* workspace,
                  int64_t workspace_bytes, void* stream);

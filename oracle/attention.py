@@ -195,3 +195,66 @@ def reference_attention_dense(q, k, v, sm_scale: float):
                 o[i, h, e] = sum(w[j] * v[j, h // g, e] for j in range(t)) / z
             lse[i, h] = m + math.log(z)
     return o, lse
+
+
+def cascade_attention_torch(q, kv_layer, qo_indptr_arr, kv_indptr_arr, kv_indices_arr, last_page_len_arr,
+                            page_size: int, sm_scale: float | None = None):
+    """The same multi-level cascade decode attention in torch float32 on the
+    CPU -- the form BASELINE's CPU plan times (paged gather, per-level softmax
+    attention with (o, lse), log-sum-exp merge), using torch's threads.
+
+    ``q [N, Hq, D]`` and ``kv_layer [P, 2, page, Hkv, D]`` are CPU tensors
+    (any float dtype, computed in float32).  Returns ``(o, lse)`` float32
+    tensors; pinned against ``cascade_attention`` (float64) in the tests."""
+    import torch
+    q = q.float()
+    kv = kv_layer
+    n, hq, d = q.shape
+    hkv = kv.shape[3]
+    g = hq // hkv
+    if sm_scale is None:
+        sm_scale = d ** -0.5
+    o_acc = torch.zeros((n, hq, d), dtype=torch.float32)
+    m_acc = torch.full((n, hq), NEG_INF, dtype=torch.float32)
+    z_acc = torch.zeros((n, hq), dtype=torch.float32)
+    slot_off = torch.arange(page_size)
+    k_flat = kv[:, 0].reshape(-1, hkv, d)         # [P * page, Hkv, D] (a copy of the K half)
+    v_flat = kv[:, 1].reshape(-1, hkv, d)
+    for qo, kvp, kvi, lpl in zip(qo_indptr_arr, kv_indptr_arr, kv_indices_arr, last_page_len_arr):
+        qo = [int(x) for x in qo]
+        kvp = [int(x) for x in kvp]
+        kvi_t = torch.as_tensor([int(x) for x in kvi], dtype=torch.long)
+        for gi in range(len(qo) - 1):
+            a, b = qo[gi], qo[gi + 1]
+            pages = kvi_t[kvp[gi]:kvp[gi + 1]]
+            if b <= a or pages.numel() == 0:
+                continue
+            t = (pages.numel() - 1) * page_size + int(lpl[gi])
+            if t <= 0:
+                continue
+            flat = (pages[:, None] * page_size + slot_off[None, :]).reshape(-1)[:t]
+            kk = k_flat.index_select(0, flat).float()                            # [T, Hkv, D]
+            vv = v_flat.index_select(0, flat).float()
+            qg = q[a:b].reshape(b - a, hkv, g, d).permute(1, 0, 2, 3).reshape(hkv, (b - a) * g, d)
+            s = torch.bmm(qg, kk.permute(1, 2, 0).contiguous()) * sm_scale    # [Hkv, nq*g, T]
+            m = s.amax(dim=2)
+            p = torch.exp(s - m[..., None])
+            z = p.sum(dim=2)
+            og = torch.bmm(p, vv.permute(1, 0, 2).contiguous())                # [Hkv, nq*g, D] unnormalised
+            og = og.reshape(hkv, b - a, g, d).permute(1, 0, 2, 3).reshape(b - a, hq, d)
+            m = m.reshape(hkv, b - a, g).permute(1, 0, 2).reshape(b - a, hq)
+            z = z.reshape(hkv, b - a, g).permute(1, 0, 2).reshape(b - a, hq)
+            # running log-sum-exp merge of this level's partial into the accumulator
+            m_old = m_acc[a:b]
+            m_new = torch.maximum(m_old, m)
+            c_old = torch.where(torch.isfinite(m_old), torch.exp(m_old - m_new), torch.zeros_like(m_old))
+            c_new = torch.exp(m - m_new)
+            o_acc[a:b] = o_acc[a:b] * c_old[..., None] + og * c_new[..., None]
+            z_acc[a:b] = z_acc[a:b] * c_old + z * c_new
+            m_acc[a:b] = m_new
+    ok = z_acc > 0
+    o = torch.where(ok[..., None], o_acc / torch.where(ok, z_acc, torch.ones_like(z_acc))[..., None],
+                    torch.zeros_like(o_acc))
+    lse = torch.where(ok, m_acc + torch.log(torch.where(ok, z_acc, torch.ones_like(z_acc))),
+                      torch.full_like(z_acc, NEG_INF))
+    return o, lse

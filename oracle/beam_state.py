@@ -72,6 +72,7 @@ class ONode:
 class OCand:
     node: ONode
     score: float
+    sequence: Optional[List[int]] = None    # a finished beam's own tokens (else read from the trie)
 
 
 @dataclass
@@ -88,6 +89,7 @@ class OracleBeamState:
         self.alloc = alloc
         self.root: Optional[ONode] = None
         self.candidates: List[OCand] = []
+        self.finished_candidates: List[OCand] = []
 
     # beam_state.py:76-98
     def add_root_sequence(self, seq: List[int]) -> List[ONode]:
@@ -236,8 +238,16 @@ class OracleBeamState:
         return out[::-1]
 
     def sequence(self, ci: int) -> List[int]:
+        return self.sequence_of(self.candidates[ci])
+
+    @staticmethod
+    def sequence_of(c: OCand) -> List[int]:
+        """Tokens root to leaf (beam_state.py:667-671); a finished beam that
+        keeps its own sequence returns that."""
+        if c.sequence is not None:
+            return list(c.sequence)
         seq: List[int] = []
-        n = self.candidates[ci].node
+        n = c.node
         while n is not None:
             seq = n.tokens + seq
             n = n.parent
@@ -245,9 +255,12 @@ class OracleBeamState:
 
     # beam_state.py:646-682
     def get_final_sequences(self, num_return: int, length_penalty: float = 1.0):
+        """Finished candidates first, then the live ones (:658); score divided
+        by len ** penalty unless the penalty is 0 or len <= 1 (:674-676); a
+        stable sort by that score, descending (:681), the first num_return."""
         out = []
-        for ci, c in enumerate(self.candidates):
-            seq = self.sequence(ci)
+        for c in self.finished_candidates + self.candidates:
+            seq = self.sequence_of(c)
             sc = c.score
             if length_penalty != 0 and len(seq) > 1:
                 sc = sc / (len(seq) ** length_penalty)

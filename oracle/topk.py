@@ -17,7 +17,20 @@ Floating-point contract restated here and implemented bit-for-bit by the GPU
 kernel (torch's own reduction order is unspecified, so this is the pinned
 form): for a row x (already in the logits dtype),
 
-    x'   = round_dtype(x * fl32(1/T))          only when T != 1
+    x'   = round_dtype(x * fl32(fl64(1 / T)))      only when T != 1, mode "reciprocal"
+    x'   = round_dtype(fl32(x / fl32(T)))          only when T != 1, mode "divide"
+
+``logits / temperature`` (beam.py:107, :270) runs on a GPU tensor in the
+reference; torch evaluates a tensor divided by a Python float on the GPU as a
+multiply by the scalar's reciprocal, taken in double and rounded to float
+(mode "reciprocal", the default), and on a CPU tensor as a correctly rounded
+division by the float temperature (mode "divide").  Both forms are pinned
+against torch itself: "divide" against torch's CPU division in the CPU
+tests, "reciprocal" against torch's GPU division in the GPU tests (at T = 1.1
+the two reciprocal roundings fl32(fl64(1 / T)) = 0x3F68BA2F and
+fl32(1 / fl32(T)) = 0x3F68BA2E differ; the GPU gives the former).  The rest
+of the row:
+
     m    = max(x')
     S    = sum_i exp(fl64(x'_i - m))            float64 accumulation
     L    = fl32(ln S)
@@ -56,12 +69,25 @@ def round_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(f"unsupported logits dtype {dtype}")
 
 
-def log_softmax_rows(logits: np.ndarray, dtype: str = "float32", temperature: float = 1.0) -> np.ndarray:
+def scale_temperature(x: np.ndarray, dtype: str, temperature: float, mode: str = "reciprocal") -> np.ndarray:
+    """``logits / temperature`` of beam.py:107, :270 (x already in the logits
+    dtype, held as float32) in the arithmetic of ``mode``; T == 1 is skipped as
+    the reference skips it."""
+    x = np.asarray(x, dtype=np.float32)
+    if temperature == 1.0:
+        return x
+    t = np.float32(temperature)
+    if mode == "reciprocal":
+        return round_dtype(x * np.float32(1.0 / float(temperature)), dtype)
+    if mode == "divide":
+        return round_dtype(x / t, dtype)
+    raise ValueError(f"unknown temperature mode {mode}")
+
+
+def log_softmax_rows(logits: np.ndarray, dtype: str = "float32", temperature: float = 1.0,
+                     temperature_mode: str = "reciprocal") -> np.ndarray:
     """Row log_softmax under the pinned contract above; returns float32 values."""
-    x = np.asarray(logits, dtype=np.float32)
-    if temperature != 1.0:
-        inv_t = np.float32(1.0 / temperature)
-        x = round_dtype(x * inv_t, dtype)
+    x = scale_temperature(logits, dtype, temperature, temperature_mode)
     m = x.max(axis=1, keepdims=True)
     s = np.exp(x.astype(np.float64) - m.astype(np.float64)).sum(axis=1, keepdims=True)
     lse_off = np.log(s).astype(np.float32)
@@ -110,9 +136,9 @@ def select_global(parent_scores, top_vals: np.ndarray, top_idx: np.ndarray, beam
 
 
 def beam_step(logits: np.ndarray, parent_scores, beam_size: int, dtype: str = "float32",
-              temperature: float = 1.0):
+              temperature: float = 1.0, temperature_mode: str = "reciprocal"):
     """One full decode-step selection: log_softmax -> row top-k -> global top-B."""
-    logp = log_softmax_rows(logits, dtype, temperature)
+    logp = log_softmax_rows(logits, dtype, temperature, temperature_mode)
     k = decode_k(beam_size, logp.shape[1])
     vals, idx = row_topk(logp, k)
     per_row, flat = select_global(parent_scores, vals, idx, beam_size)
@@ -120,9 +146,9 @@ def beam_step(logits: np.ndarray, parent_scores, beam_size: int, dtype: str = "f
 
 
 def prefill_select(logits_row: np.ndarray, beam_size: int, dtype: str = "float32",
-                   temperature: float = 1.0):
+                   temperature: float = 1.0, temperature_mode: str = "reciprocal"):
     """Prefill expansion (beam.py:105-141): first B of topk(min(2B, V)) of one row."""
-    logp = log_softmax_rows(np.asarray(logits_row)[None, :], dtype, temperature)
+    logp = log_softmax_rows(np.asarray(logits_row)[None, :], dtype, temperature, temperature_mode)
     k = min(beam_size * 2, logp.shape[1])
     vals, idx = row_topk(logp, k)
     b = min(beam_size, k)

@@ -10,7 +10,7 @@ from contextlib import contextmanager
 import pytest
 
 from beam_engine_amd.beam_state import (BeamCandidate, BeamGenerateResult, BeamState, BeamToken, TrieNode)
-from oracle.beam_state import OracleAllocator, OracleBeamState, OResult, build_tree
+from oracle.beam_state import OCand, OracleAllocator, OracleBeamState, OResult, build_tree
 from tests.conftest import load_fixtures
 
 FX = load_fixtures()
@@ -263,6 +263,7 @@ def test_eos_finishes_beams_without_pages(seed):
                  for ci, c in enumerate(o.candidates)]
         p.add_filtered_results(p_res, eos)
         o.add_filtered_results(o_res)
+        o.finished_candidates += [OCand(None, sc, sequence=seq) for seq, sc in expect_fin]
         got_fin = [(c.sequence, c.score) for c in p.finished_candidates[n_fin:]]
         assert got_fin == expect_fin and all(c.finished for c in p.finished_candidates)
         n_fin = len(p.finished_candidates)
@@ -274,6 +275,28 @@ def test_eos_finishes_beams_without_pages(seed):
             assert [tuple(x.tolist() for x in l) for l in nlv] == [tuple(l) for l in p._cascade_lists()]
     final = p.get_final_sequences(100)
     assert len(final) == len(p.finished_candidates) + len(p.candidates)
+    for pen in (1.0, 0.0, 0.5):
+        assert p.get_final_sequences(100, pen) == o.get_final_sequences(100, pen)
     # finished beams end with the token; live ones never carry it (an EOS pick never continues)
     assert n_fin > 0 and sum(seq[-1] == eos for seq, _ in final) == n_fin
     assert all(eos not in p.sequence(c) for c in p.candidates)
+
+
+def test_final_sequences_with_finished_hand_case():
+    """The product's get_final_sequences (beam_state.py:646-682) on the oracle's
+    hand case: finished candidates first in the pool, one read from the trie
+    and one with its own sequence; same order and scores as the oracle."""
+    from tests.test_oracle_beam_state import _final_ranking_case
+    o = _final_ranking_case()
+    pages = RecordingPages(8, 4)
+    st = BeamState(2, pages)
+    root = TrieNode([1, 2, 3, 4], 0)
+    a, b, c = TrieNode([5, 6], 1, root), TrieNode([7], 2, root), TrieNode([8], 3, root)
+    st.root = root
+    st.candidates = [BeamCandidate(a, -1.0), BeamCandidate(b, -0.6)]
+    st.finished_candidates = [BeamCandidate(c, -0.9, finished=True),
+                              BeamCandidate(b, -1.2, finished=True, sequence=[1, 2, 3, 4, 9, 0])]
+    for pen in (1.0, 0.0, 2.0):
+        assert st.get_final_sequences(4, pen) == o.get_final_sequences(4, pen)
+    assert [s for s, _ in st.get_final_sequences(4, 1.0)] == [[1, 2, 3, 4, 7], [1, 2, 3, 4, 5, 6], [1, 2, 3, 4, 8],
+                                                             [1, 2, 3, 4, 9, 0]]

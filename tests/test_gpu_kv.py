@@ -148,3 +148,33 @@ def test_rope_append_matches_eager_tensor_code():
     torch.cuda.synchronize()
     assert torch.equal(q_fused, q_ref)
     assert torch.equal(a.kv_pool, b.kv_pool)
+
+
+def test_page_table_raises_on_bad_page_ids():
+    """A bad page id or slot in write_blocks_vectorized / write_rope_qkv is
+    skipped on the device and counted; check_errors then raises ValueError (the
+    reference raises ValueError for a page it does not hold,
+    page_table.py:150-151).  Good entries are written; the count is cleared."""
+    say("page table: bad page ids raise ValueError")
+    from beam_engine_amd import PageTable
+    pt = PageTable(2, page_size=16, max_num_pages=8, head_num=2, head_dim=64, device="cuda",
+                   store_dtype=torch.bfloat16)
+    k = torch.ones((3, 2, 64), dtype=torch.bfloat16, device="cuda")
+    pages = torch.tensor([1, 8, 2], dtype=torch.int32, device="cuda")          # 8 >= 8 pages
+    slots = torch.tensor([0, 0, 3], dtype=torch.int32, device="cuda")
+    pt.write_blocks_vectorized(0, pages, k, k, slots)
+    with pytest.raises(ValueError, match="outside the pool"):
+        pt.check_errors()
+    assert torch.all(pt.kv_cache_at_layer[0][1, :, 0] == 1) and torch.all(pt.kv_cache_at_layer[0][2, :, 3] == 1)
+    pt.check_errors()                                                            # cleared: no raise
+    # a slot past the page and a bad page in the fused RoPE append
+    hq, d = 4, 64
+    qkv = torch.randn((2, (hq + 4) * d), device="cuda").to(torch.bfloat16)
+    cos = torch.ones((32, d), dtype=torch.bfloat16, device="cuda")
+    sin = torch.zeros((32, d), dtype=torch.bfloat16, device="cuda")
+    pos = torch.tensor([3, 4], dtype=torch.int64, device="cuda")
+    pt.write_rope_qkv(1, qkv, hq, pos, cos, sin, torch.tensor([0, -1], dtype=torch.int32, device="cuda"),
+                      torch.tensor([16, 1], dtype=torch.int32, device="cuda"))
+    with pytest.raises(ValueError):
+        pt.check_errors()
+    pt.check_errors()

@@ -26,16 +26,16 @@ def need_gpu():
 DT = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}
 
 
-def compare(logits, parents, beam, temperature=1.0):
+def compare(logits, parents, beam, temperature=1.0, mode="reciprocal"):
     from beam_engine_amd import beam_topk, decode_k
     n, v = logits.shape
     k = decode_k(beam, v)
     x = logits.float().numpy()
-    logp = ot.log_softmax_rows(x, DT[logits.dtype], temperature)
+    logp = ot.log_softmax_rows(x, DT[logits.dtype], temperature, mode)
     vals, idx = ot.row_topk(logp, k)
     _, flat = ot.select_global(parents, vals, idx, beam)
     rv, ri, (par, tok, sc) = beam_topk(logits.cuda(), k, torch.tensor(parents, dtype=torch.float64), beam,
-                                       temperature)
+                                       temperature, temperature_mode=mode)
     torch.cuda.synchronize()
     assert np.array_equal(ri.cpu().numpy(), idx), "row indices differ"
     assert np.array_equal(rv.cpu().numpy().view(np.uint32), vals.view(np.uint32)), "row values differ"
@@ -67,8 +67,41 @@ def test_ties_and_temperature(dtype):
     logits = torch.randint(-3, 4, (6, 5000), generator=g).to(torch.float32).to(dtype)   # massive ties
     parents = [0.0, 0.0, -1.0, -1.0, -2.0, 0.0]                                        # tied parents too
     compare(logits, parents, 4)
-    compare(logits, parents, 4, temperature=0.7)
+    for t in (0.7, 0.9, 1.1, 1.3):
+        compare(logits, parents, 4, temperature=t)
+        compare(logits, parents, 4, temperature=t, mode="divide")
     compare(logits, parents, 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("temperature", [0.7, 0.9, 1.1, 1.3])
+def test_temperature_matches_torch_division(dtype, temperature):
+    """The reference scales with ``logits / temperature`` on a GPU tensor
+    (beam.py:107, :270).  torch's device division equals the oracle's
+    "reciprocal" form bit for bit, and be_beam_topk with that mode selects
+    exactly what it selects from torch's divided logits at T = 1; the "divide"
+    mode does the same against torch's CPU division."""
+    from beam_engine_amd import beam_topk
+    say(f"topk temperature {temperature} vs torch division, {dtype}")
+    g = torch.Generator().manual_seed(21)
+    logits = (torch.randn((16, 50000), generator=g) * 3).to(dtype)
+    parents = torch.from_numpy(-np.random.default_rng(21).random(16))
+    dev = logits.cuda()
+    dev_div = dev / temperature                               # the reference's own expression
+    one = (torch.ones(1, device="cuda") / temperature).cpu().numpy()
+    torch.cuda.synchronize()
+    # torch's device division multiplies by the double reciprocal rounded to float
+    assert one.view(np.uint32)[0] == np.float32(1.0 / temperature).view(np.uint32)
+    ours = ot.scale_temperature(logits.float().numpy(), DT[dtype], temperature, "reciprocal")
+    assert np.array_equal(dev_div.float().cpu().numpy().view(np.uint32), ours.view(np.uint32)), \
+        "torch's device division differs from the reciprocal form"
+    for mode, pre in (("reciprocal", dev_div), ("divide", (logits / temperature).cuda())):
+        a = beam_topk(dev, 32, parents, 16, temperature, temperature_mode=mode)
+        b = beam_topk(pre, 32, parents, 16, 1.0)
+        torch.cuda.synchronize()
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]), mode
+        assert all(torch.equal(x, y) for x, y in zip(a[2], b[2])), mode
+        compare(logits, parents.tolist(), 16, temperature, mode)
 
 
 def test_prefill_single_row_and_small_vocab():

@@ -180,3 +180,27 @@ def test_causal_masks_only_the_last_level():
     b = oa.merge_states([o0, o1], [l0, l1])
     np.testing.assert_allclose(a[0], b[0], atol=1e-12)
     np.testing.assert_allclose(a[1], b[1], atol=1e-12)
+
+
+@pytest.mark.parametrize("name", ["cascade_md", "swapped", "uneven"])
+def test_torch_fp32_cascade_matches_fp64(name):
+    """The torch float32 CPU form (the CPU baseline's attention) equals the
+    float64 restatement within float32 rounding on the reference's trees,
+    with GQA and an empty group."""
+    import torch
+    from tests.conftest import load_fixtures
+    tree = load_fixtures()["trees"][name]
+    e = tree["expected"]
+    levels = [e["qo_indptr"], e["kv_indptr"], e["kv_indices"], e["last_page_len"]]
+    page = tree["page_size"]
+    n = e["qo_indptr"][0][-1]
+    npages = max(max(l) for l in e["kv_indices"] if l) + 2
+    g = torch.Generator().manual_seed(3)
+    kv = torch.randn((npages, 2, page, 2, 64), generator=g)
+    q = torch.randn((n, 8, 64), generator=g)
+    o64, lse64 = oa.cascade_attention(q, kv, *levels, page, 0.125)
+    o32, lse32 = oa.cascade_attention_torch(q, kv, *levels, page, 0.125)
+    np.testing.assert_allclose(o32.numpy(), o64, rtol=0, atol=1e-5)
+    fin = np.isfinite(lse64)
+    assert np.array_equal(fin, np.isfinite(lse32.numpy()))
+    np.testing.assert_allclose(lse32.numpy()[fin], lse64[fin], rtol=0, atol=1e-5)

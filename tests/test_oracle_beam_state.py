@@ -7,7 +7,7 @@ import random
 
 import pytest
 
-from oracle.beam_state import OracleAllocator, OracleBeamState, OResult, build_tree
+from oracle.beam_state import OCand, ONode, OracleAllocator, OracleBeamState, OResult, build_tree
 from tests.conftest import load_fixtures
 
 FX = load_fixtures()
@@ -149,3 +149,46 @@ def test_random_run_invariants(seed):
         # groups are contiguous candidate ranges covering all candidates
         for lv in range(len(qo)):
             assert qo[lv][0] == 0 and qo[lv][-1] == len(st.candidates)
+
+
+def _final_ranking_case():
+    """Page size 4: root [1, 2, 3, 4] with children A [5, 6], B [7], C [8];
+    live candidates A (score -1.0) and B (-0.6), finished F at C (-0.9) read
+    from the trie, and finished E with its own sequence [1, 2, 3, 4, 9, 0]
+    (score -1.2)."""
+    alloc = OracleAllocator(8, 4)
+    st = OracleBeamState(2, alloc)
+    root = ONode([1, 2, 3, 4], 0)
+    a, b, c = ONode([5, 6], 1, root), ONode([7], 2, root), ONode([8], 3, root)
+    st.root = root
+    st.candidates = [OCand(a, -1.0), OCand(b, -0.6)]
+    st.finished_candidates = [OCand(c, -0.9), OCand(b, -1.2, sequence=[1, 2, 3, 4, 9, 0])]
+    return st
+
+
+def test_final_sequences_hand_case_with_finished():
+    """beam_state.py:646-682 by hand.  Lengths: A 6, B 5, F 5, E 6.
+    Penalty 1: A -1/6 = -0.1667, B -0.6/5 = -0.12, F -0.9/5 = -0.18, E -1.2/6 = -0.2
+    -> B, A, F, E.  Penalty 0: B -0.6, F -0.9, A -1.0, E -1.2."""
+    st = _final_ranking_case()
+    got = st.get_final_sequences(4, 1.0)
+    assert [s for s, _ in got] == [[1, 2, 3, 4, 7], [1, 2, 3, 4, 5, 6], [1, 2, 3, 4, 8], [1, 2, 3, 4, 9, 0]]
+    assert [round(x, 6) for _, x in got] == [-0.12, round(-1 / 6, 6), -0.18, -0.2]
+    got0 = st.get_final_sequences(3, 0.0)
+    assert got0 == [([1, 2, 3, 4, 7], -0.6), ([1, 2, 3, 4, 8], -0.9), ([1, 2, 3, 4, 5, 6], -1.0)]
+
+
+def test_final_sequences_ties_keep_finished_first():
+    """Equal normalised scores keep pool order, finished candidates first
+    (:658, stable sort): F at -0.6 ties B at penalty 0; a one-token sequence
+    is not divided (len <= 1)."""
+    alloc = OracleAllocator(4, 4)
+    st = OracleBeamState(2, alloc)
+    root = ONode([1, 2, 3, 4], 0)
+    b = ONode([7], 1, root)
+    st.candidates = [OCand(b, -0.6)]
+    st.finished_candidates = [OCand(root, -0.6, sequence=[1, 2, 3, 4, 0])]
+    assert st.get_final_sequences(2, 0.0) == [([1, 2, 3, 4, 0], -0.6), ([1, 2, 3, 4, 7], -0.6)]
+    one = OracleBeamState(1, OracleAllocator(2, 4))
+    one.candidates = [OCand(ONode([5], 0), -0.7)]
+    assert one.get_final_sequences(1, 1.0) == [([5], -0.7)]

@@ -81,3 +81,57 @@ def test_bf16_logp_rounded_and_ties_by_index():
     for r in range(3):
         for j in range(31):
             assert v[r, j] > v[r, j + 1] or (v[r, j] == v[r, j + 1] and i[r, j] < i[r, j + 1])
+
+
+def _nearest_f32(q):
+    """The float32 nearest to the rational q (ties to even), from exact arithmetic."""
+    from fractions import Fraction
+    f = np.float32(float(q))
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        d = abs(Fraction(float(c)) - q)
+        if best is None or d < best[0] or (d == best[0] and (int(c.view(np.uint32)) & 1) == 0):
+            best = (d, c)
+    return best[1]
+
+
+@pytest.mark.parametrize("temperature", [0.7, 0.9, 1.1, 1.3])
+def test_temperature_reciprocal_constant(temperature):
+    """Mode "reciprocal" multiplies by fl32(fl64(1 / T)): the exact reciprocal
+    of the Python float rounded to double, then to float32 (two roundings, as
+    torch forms the constant for a GPU tensor divided by a Python float; the
+    GPU tests check torch's device division against it).  At T = 1.1 that is
+    0x3F68BA2F, whereas the float division 1.0f / fl32(1.1) gives 0x3F68BA2E --
+    a plausible restatement this test rejects."""
+    from fractions import Fraction
+    want = _nearest_f32(Fraction(float(1 / Fraction(temperature))))
+    got = ot.scale_temperature(np.array([1.0], dtype=np.float32), "float32", temperature, "reciprocal")[0]
+    assert got.view(np.uint32) == want.view(np.uint32)
+    if temperature == 1.1:
+        assert int(got.view(np.uint32)) == 0x3F68BA2F
+        assert int((np.float32(1) / np.float32(1.1)).view(np.uint32)) == 0x3F68BA2E
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("temperature", [0.7, 0.9, 1.1, 1.3])
+def test_temperature_divide_matches_torch_cpu(dtype, temperature):
+    """Mode "divide" equals torch's ``logits / T`` on a CPU tensor bit for
+    bit (float32 and bfloat16 logits); for float32 logits it differs from mode
+    "reciprocal" on a sizeable share of the values, so the two modes are
+    distinct arithmetic (after bfloat16 rounding they almost always agree)."""
+    tdt = {"float32": torch.float32, "bfloat16": torch.bfloat16}[dtype]
+    x = (torch.randn(200000, generator=torch.Generator().manual_seed(7)) * 3).to(tdt)
+    ref = (x / temperature).float().numpy()
+    ours = ot.scale_temperature(x.float().numpy(), dtype, temperature, "divide")
+    assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+    if dtype == "float32":
+        rec = ot.scale_temperature(x.float().numpy(), dtype, temperature, "reciprocal")
+        assert np.mean(rec != ours) > 0.01
+
+
+def test_temperature_one_is_skipped():
+    x = (np.random.default_rng(8).standard_normal(1000) * 3).astype(np.float32)
+    for mode in ("reciprocal", "divide"):
+        assert np.array_equal(ot.scale_temperature(x, "float32", 1.0, mode), x)
+    with pytest.raises(ValueError):
+        ot.scale_temperature(x, "float32", 0.5, "bogus")
