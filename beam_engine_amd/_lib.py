@@ -76,7 +76,7 @@ class BeAttnPlanInfo(ctypes.Structure):
 EXPORTS = (
     "be_version", "be_last_error", "be_kv_append", "be_rope_qkv_append", "be_page_copy", "be_attn_plan",
     "be_attn_run",
-    "be_merge_states", "be_beam_topk_workspace_bytes", "be_beam_topk", "be_trie_cascade",
+    "be_merge_states", "be_beam_topk_workspace_bytes", "be_beam_topk", "be_beam_topk_noalloc", "be_trie_cascade",
     "be_diverse_select",
 )
 
@@ -113,6 +113,8 @@ def load() -> ctypes.CDLL:
     lib.be_beam_topk_workspace_bytes.restype = i64
     lib.be_beam_topk.argtypes = [vp, i32, i32, i32, i64, ctypes.c_double, i32, i32, vp, i32, i32, vp, i32, vp, vp,
                                  vp, vp, vp, vp, i64, vp]
+    lib.be_beam_topk_noalloc.argtypes = [vp, i32, i32, i32, i64, ctypes.c_double, i32, i32, vp, i32, i32, vp, i32,
+                                         vp, vp, vp, vp, vp, vp]
     lib.be_diverse_select.argtypes = [vp, vp, i32, i32, vp, i32, vp, i32, i32, i32, ctypes.c_double, vp, vp, vp,
                                       vp]
     lib.be_trie_cascade.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, vp, i64, ctypes.POINTER(ctypes.c_int64)]

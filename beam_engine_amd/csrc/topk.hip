@@ -27,6 +27,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace be {
@@ -726,6 +728,52 @@ __global__ __launch_bounds__(kTopkThreads) void topk_diverse_kernel(int n_rows, 
   }
 }
 
+// ---------------------------------------------------------------- static scratch
+// Device scratch of be_beam_topk_noalloc: one copy per GPU, alive until the
+// process ends.  Host code never passes `topk_scratch` itself to a kernel (on
+// the host the name is only a stand-in for the symbol): its device address is
+// looked up once per device with hipGetSymbolAddress, with that device
+// current, and that address is what the kernels get.  Calls on one GPU share
+// the array, so calls that overlap on one GPU (different streams, or host
+// threads) race.  Every kernel writes the scratch words it reads before it
+// reads them, so nothing has to be cleared between calls.
+constexpr int64_t kTopkScratchBytes = 8ll << 20;
+static __device__ __align__(256) unsigned char topk_scratch[kTopkScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxScratchDevices] = {};
+
+static int topk_scratch_address(hipStream_t st, void** out) {
+  int dev = 0;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    BE_HIP_CHECK(hipStreamGetDevice(st, &d));
+    dev = (int)d;
+  } else {
+    BE_HIP_CHECK(hipGetDevice(&dev));
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(BE_ERR_UNSUPPORTED, "device %d beyond the %d this library tracks", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    int cur = 0;
+    BE_HIP_CHECK(hipGetDevice(&cur));
+    if (cur != dev) BE_HIP_CHECK(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(topk_scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e2 != hipSuccess) return fail(BE_ERR_HIP, "hipSetDevice(%d) failed: %s", cur, hipGetErrorString(e2));
+    }
+    if (e != hipSuccess || p == nullptr)
+      return fail(BE_ERR_HIP, "hipGetSymbolAddress(topk_scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return BE_OK;
+}
+
 }  // namespace be
 
 extern "C" {
@@ -737,8 +785,8 @@ int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k) {
   return ns * 4 + ns * 8 + ns * k * 4 + ns * k * 4 + 256;
 }
 
-int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, double temperature,
-                 int temp_mode, int k,
+static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, double temperature,
+                       int temp_mode, int k,
                  const double* parent_scores, int beam, int n_req, const int32_t* req_row_ptr, int max_req_rows,
                  float* row_vals, int32_t* row_idx, int32_t* out_parent, int32_t* out_token, double* out_score,
                  void* workspace, int64_t workspace_bytes, void* stream) {
@@ -806,6 +854,33 @@ int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t r
     BE_HIP_CHECK(hipGetLastError());
   }
   return BE_OK;
+}
+
+int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, double temperature,
+                 int temp_mode, int k, const double* parent_scores, int beam, int n_req, const int32_t* req_row_ptr,
+                 int max_req_rows, float* row_vals, int32_t* row_idx, int32_t* out_parent, int32_t* out_token,
+                 double* out_score, void* workspace, int64_t workspace_bytes, void* stream) {
+  return topk_launch(logits, dtype, n_rows, vocab, row_stride, temperature, temp_mode, k, parent_scores, beam, n_req,
+                     req_row_ptr, max_req_rows, row_vals, row_idx, out_parent, out_token, out_score, workspace,
+                     workspace_bytes, stream);
+}
+
+int be_beam_topk_noalloc(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride,
+                         double temperature, int temp_mode, int k, const double* parent_scores, int beam, int n_req,
+                         const int32_t* req_row_ptr, int max_req_rows, float* row_vals, int32_t* row_idx,
+                         int32_t* out_parent, int32_t* out_token, double* out_score, void* stream) {
+  const int64_t need = be_beam_topk_workspace_bytes(n_rows, vocab, k);
+  if (need > (int64_t)be::kTopkScratchBytes)
+    return be::fail(BE_ERR_CAPACITY,
+                    "be_beam_topk_noalloc: %d rows x %d logits with k = %d need %lld bytes of scratch, above the "
+                    "library's static %lld bytes (use be_beam_topk with a workspace)",
+                    n_rows, vocab, k, (long long)need, (long long)be::kTopkScratchBytes);
+  void* scratch_dev = nullptr;
+  const int rc = be::topk_scratch_address(reinterpret_cast<hipStream_t>(stream), &scratch_dev);
+  if (rc != BE_OK) return rc;
+  return topk_launch(logits, dtype, n_rows, vocab, row_stride, temperature, temp_mode, k, parent_scores, beam, n_req,
+                     req_row_ptr, max_req_rows, row_vals, row_idx, out_parent, out_token, out_score, scratch_dev,
+                     (int64_t)be::kTopkScratchBytes, stream);
 }
 
 int be_diverse_select(const float* row_vals, const int32_t* row_idx, int n_rows, int k, const double* parent_scores,

@@ -306,6 +306,23 @@ int be_beam_topk(const void* logits, int dtype, int n_rows, int vocab, int64_t r
                  int32_t* out_parent, int32_t* out_token, double* out_score, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* be_beam_topk_noalloc: be_beam_topk without a workspace argument and without
+ * any allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Its scratch is a static 8 MiB
+ * device array inside the library, one per GPU, held until the process ends
+ * (its address looked up once per device on the first call there).  Shapes
+ * whose be_beam_topk_workspace_bytes exceed 8 MiB are rejected with
+ * BE_ERR_CAPACITY (e.g. 128 rows of a 128256 vocabulary with k = 32 need
+ * 0.55 MB).  Every call on one GPU shares that scratch: calls that overlap on
+ * one GPU (other streams, other host threads) race and must be serialised by
+ * the caller.  Results are those of be_beam_topk with the same arguments. */
+int be_beam_topk_noalloc(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride,
+                         double temperature, int temp_mode, int k, const double* parent_scores, int beam,
+                         int n_req, const int32_t* req_row_ptr, int max_req_rows, float* row_vals,
+                         int32_t* row_idx, int32_t* out_parent, int32_t* out_token, double* out_score,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif
