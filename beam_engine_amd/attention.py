@@ -84,7 +84,7 @@ class PlanStats:
         self.num_items = int(info.num_items)
         self.num_part_rows = int(info.num_part_rows)
         self.num_merge = int(info.num_merge)
-        self.kernel = {0: "valu", 1: "tile", 2: "stream"}[int(info.kernel)]
+        self.kernel = {0: "valu", 1: "tile", 2: "stream", 3: "rows"}[int(info.kernel)]
         self.num_tails = int(info.num_tails) if self.kernel == "stream" else 0
         self.chunk_tokens = int(info.chunk_tokens)
 
@@ -116,6 +116,7 @@ class _PagedPlanner:
         self._tail_role = False       # streaming kernel: tail chunks in tail-role workgroups, not the merge kernel
         self._no_regs = False         # streaming kernel: direct-load loop in every workgroup
         self._no_wide = False         # streaming kernel: no wide (32-row) wave roles, no 128-row segments
+        self._rows = None             # row-block kernel: True forces it, False forbids it, None lets the planner pick
         self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
 
@@ -159,6 +160,8 @@ class _PagedPlanner:
             (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
             (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
             (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0) | \
+            (_lib.BE_PLAN_ROWS if self._rows is True else 0) | \
+            (_lib.BE_PLAN_NO_ROWS if self._rows is False else 0) | \
             (_lib.BE_PLAN_CAUSAL if causal else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()

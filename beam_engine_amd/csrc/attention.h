@@ -100,4 +100,23 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
                int64_t q_sh, const void* kv, void* out, int64_t o_sn, int64_t o_sh, float* lse, float sm_scale,
                int phases, hipStream_t st);
 
+// ---------------------------------------------------------------- row-block kernel
+// Writes the merge-free row-block plan (attn_rows.hip) for `groups` into
+// out[0..cap) and fills its layout fields of info (kernel 3).
+int rows_plan(const std::vector<Group>& groups, const be_level* levels, int num_levels, int64_t total_pages,
+              int num_queries, int hq, int hkv, int page_size, int num_cus, int32_t* out, int64_t cap,
+              be_attn_plan_info* info);
+
+// True when the row-block plan is expected to beat the streaming plan: every
+// block's passes re-read the groups it shares with other blocks (from L2),
+// so it pays where the streaming plan's fixed costs (partials, a second
+// kernel) dominate.
+bool rows_preferred(const std::vector<Group>& groups, int num_queries, int g, int num_cus);
+
+// Launches the row-block kernel of a kernel == 3 plan (phases & BE_RUN_ATTENTION;
+// it has no merge phase).
+int rows_run(const be_attn_plan_info* info, const int32_t* plan, const void* q, int64_t q_sn, int64_t q_sh,
+             const void* kv, void* out, int64_t o_sn, int64_t o_sh, float* lse, float sm_scale, int phases,
+             hipStream_t st);
+
 }  // namespace be

@@ -745,6 +745,29 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
                "bad plan capacities (max_queries %d < %d queries?)", caps->max_queries, num_queries);
     if (mfma) rows_cap = std::min(rows_cap, tr);
   }
+  // merge-free row blocks (decode plans, compact layout): forced by
+  // BE_PLAN_ROWS, else chosen when rows_preferred says so
+  bool rows_ok = false;
+  if (!any_causal && !caps && stream_eligible(dtype, d, g, page_size, flags) && g <= 16 &&
+      !(flags & BE_PLAN_NO_ROWS) && ((flags & BE_PLAN_ROWS) || rows_preferred(groups, num_queries, g, num_cus))) {
+    memset(info, 0, sizeof(*info));
+    const int rc = rows_plan(groups, levels, num_levels, total_pages, num_queries, hq, hkv, page_size, num_cus, out,
+                             cap, info);
+    if (rc != BE_OK && rc != BE_ERR_UNSUPPORTED) return rc;
+    rows_ok = rc == BE_OK;     // unsupported: a task exceeds the kernel's LDS tables
+  }
+  if (rows_ok) {
+    info->num_qo_heads = hq;
+    info->num_kv_heads = hkv;
+    info->head_dim = d;
+    info->page_size = page_size;
+    info->num_pages = num_pages;
+    info->dtype = dtype;
+    info->kv_bytes = valid_tokens * hkv * d * es * 2;
+    info->qo_bytes = (int64_t)num_queries * hq * d * es * 2;
+    info->flops = flops;
+    return BE_OK;
+  }
   if (!(any_causal && caps) && stream_eligible(dtype, d, g, page_size, flags) && (!caps || caps->tile_rows == 64)) {
     memset(info, 0, sizeof(*info));
     const int rc = stream_plan(groups, levels, num_levels, total_pages, num_queries, hq, hkv, d, page_size,
@@ -998,6 +1021,7 @@ int attn_run(const be_attn_plan_info* info, const int32_t* plan, void* partials,
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (info->kernel == 2)
     return stream_run(info, plan, partials, q, q_sn, q_sh, kv, out, o_sn, o_sh, lse, sm_scale, phases, st);
+  if (info->kernel == 3) return rows_run(info, plan, q, q_sn, q_sh, kv, out, o_sn, o_sh, lse, sm_scale, phases, st);
   const int64_t rows = info->part_rows_cap;
   AttnArgs a;
   a.q = q; a.q_sn = q_sn; a.q_sh = q_sh;

@@ -51,13 +51,12 @@
 #include <vector>
 
 #include "attention.h"
+#include "stream_device.h"
 
 namespace be {
 
 namespace stream {
 
-constexpr int kD = 128;                       // head_dim served
-constexpr int kTok = 64;                      // tokens per tile
 constexpr int kDmaStages = 3;                 // LDS stages of the direct-load loop
 constexpr int kRegStages = 2;                 // LDS stages of the register-staged loop
 constexpr int kRegsMinTiles = 8;              // launches whose largest run has this many tiles stage through registers
@@ -134,92 +133,6 @@ struct TailMergeArgs {
   float scale_log2;
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef __attribute__((address_space(3))) v4s* lds_v4s_t;
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_ptr_t)p;
-}
-
-// Direct global->LDS loads: lane l's bytes land at LDS byte address m0 + size * l
-// (lds must be wave-uniform).  They are issued from inline asm so that the
-// compiler's wait insertion does not treat every later LDS read as dependent
-// on them (it would wait for all outstanding loads); completion is tracked by
-// the explicit vmcnt waits.  Wait states: an M0 write needs one before an
-// LDS-DMA instruction reads it; an SGPR written by a VALU instruction
-// (readfirstlane) needs five before a vector memory instruction reads it.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(lds)
-               : "memory", "m0");
-}
-// SGPR base (wave-uniform) + 32-bit unsigned VGPR byte offset
-__device__ __forceinline__ void dma16_sv(uint64_t base, uint32_t voff, uint32_t lds) {
-  // readfirstlane returns int: zero-extend each half through uint32_t
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
-  const uint64_t sbase = ((uint64_t)hi << 32) | (uint64_t)lo;
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(sbase), "s"(lds)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :
-               : "v"(src), "s"(lds)
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] | expcnt 7 | lgkmcnt 15 | vmcnt[5:4] << 14).
-// n is the number of newer vector memory operations that may stay
-// outstanding; vmcnt retires operations in issue order.  Dispatched by a
-// binary tree of scalar branches (n is wave-uniform).
-#define BE_VMCNT(n) (((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
-template <int LO, int HI>
-__device__ __forceinline__ void wait_tree(int n) {
-  if constexpr (LO == HI) {
-    __builtin_amdgcn_s_waitcnt(BE_VMCNT(LO));
-  } else {
-    constexpr int MID = (LO + HI) / 2;
-    if (n <= MID) wait_tree<LO, MID>(n);
-    else wait_tree<MID + 1, HI>(n);
-  }
-}
-__device__ __forceinline__ void wait_vmcnt(int n) { wait_tree<0, 31>(n < 31 ? n : 31); }
-
-// Bare workgroup barrier (after explicit vmcnt waits for direct loads).
-__device__ __forceinline__ void lds_fence() {
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// Workgroup barrier after this wave's LDS writes have completed (s_waitcnt
-// lgkmcnt(0), then s_barrier; vector memory loads stay in flight).
-__device__ __forceinline__ void lds_sync() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-// Two floats -> two 16-bit values (round to nearest even) in one word.
-template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
-template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
-  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, bf2));
-}
-template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
-}
-template <typename T> __device__ __forceinline__ v4s pack4(float a, float b, float c, float d) {
-  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(v4s, (u2){pack2<T>(a, b), pack2<T>(c, d)});
-}
-
 // A segment record held in wave-uniform registers.
 struct SegReg {
   int q_begin, q_count, page_begin, tok_begin, tok_count, head, out_slot, n_tiles;
@@ -227,189 +140,6 @@ struct SegReg {
 __device__ __forceinline__ SegReg seg_reg(const StreamSeg& x) {
   return SegReg{rfl(x.q_begin), rfl(x.q_count), rfl(x.page_begin), rfl(x.tok_begin),
                 rfl(x.tok_count), rfl(x.head),   rfl(x.out_slot),   rfl(x.n_tiles)};
-}
-
-// One wave's share of a 64-token tile: rows 16 rt + (0..15) against NSUB
-// 16-token sub-tiles starting at kt / vt, for NMT head_dim tiles (voff).
-// Online softmax state (m_run, l_run over this wave's tokens, o_acc) is
-// updated in place; the rescale is skipped when no row's max rose.  P.V pairs
-// two sub-tiles per v_mfma_f32_16x16x32: lane group lg holds tokens 4 lg..+3
-// of both sub-tiles in the A (V^T) and B (P^T) operands alike, so the 32-wide
-// contraction pairs the same tokens.
-template <typename T, int NSUB, int NMT>
-__device__ __forceinline__ void tile_compute(const unsigned char* kt, const unsigned char* vt, const v8s (&qf)[4],
-                                             const uint32_t (&koff)[4], const uint32_t (&voff)[NMT], int tok_base,
-                                             int vrow, int lg, float scale, float& m_run, float& l_run,
-                                             v4f (&o_acc)[8]) {
-  // all LDS operand reads first: the K fragments, then the V^T fragments
-  // (independent of the scores, so their latency hides under the softmax)
-  v8s kf[NSUB][4];
-#pragma unroll
-  for (int k = 0; k < NSUB; ++k)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kf[k][ks] = *reinterpret_cast<const v8s*>(kt + k * 4096 + koff[ks]);
-  v4s vf[NMT][NSUB];
-#pragma unroll
-  for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k)
-      vf[mt][k] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + k * 4096 + voff[mt]));
-
-  float x[NSUB][4];
-#pragma unroll
-  for (int k = 0; k < NSUB; ++k) {
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma_qk<T>(kf[k][ks], qf[ks], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) x[k][r] = acc[r] * scale;
-  }
-  // vrow: tokens of the tile this lane's row sees (the tile's valid tokens,
-  // fewer under a causal limit)
-  if (__builtin_amdgcn_ballot_w64(vrow < kTok) != 0) {
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (tok_base + k * 16 + 4 * lg + r >= vrow) x[k][r] = -INFINITY;
-  }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < NSUB; ++k)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[k][r]);
-  mx = rows4_max(mx);
-  const float m_new = fmaxf(m_run, mx);
-  const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
-  if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
-    const float alpha = __builtin_amdgcn_exp2f(m_run - msafe);
-    l_run *= alpha;
-#pragma unroll
-    for (int mt = 0; mt < NMT; ++mt) o_acc[mt] *= alpha;
-  }
-  m_run = m_new;
-  v4s pf[NSUB];
-#pragma unroll
-  for (int k = 0; k < NSUB; ++k) {
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(x[k][r] - msafe);
-      l_run += p[r];
-    }
-    pf[k] = pack4<T>(p[0], p[1], p[2], p[3]);
-  }
-  // O^T tiles: lane (lg, lc) supplied V[16 sub + 4 lg + lc/4][16 mt + 4 (lc%4) .. +3]
-#pragma unroll
-  for (int mt = 0; mt < NMT; ++mt) {
-    v4f o = o_acc[mt];
-    if constexpr (NSUB == 1) {
-      o = mfma_pv<T>(vf[mt][0], pf[0], o);
-    } else {
-#pragma unroll
-      for (int k = 0; k < NSUB; k += 2)
-        o = mfma_qk<T>(__builtin_shufflevector(vf[mt][k], vf[mt][k + 1], 0, 1, 2, 3, 4, 5, 6, 7),
-                       __builtin_shufflevector(pf[k], pf[k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
-    }
-    o_acc[mt] = o;
-  }
-}
-
-// Tokens of a tile (valid of them, starting at group token tile_tok) that
-// row `row` of a segment sees when the segment's first query sees vis0 group
-// tokens and query j (row / g) sees vis0 + j; kNoCausalS leaves valid.
-__device__ __forceinline__ int row_limit(int valid, int vis0, int row, int g, int tile_tok) {
-  return min(valid, max(0, vis0 + row / g - tile_tok));
-}
-
-// Wide wave roles: one wave's share of a 64-token tile for two 16-row MFMA
-// tiles (32 rows) at once, so that every K and V^T fragment read from LDS
-// feeds both (half the LDS reads per row of tile_compute).  qf[r], m_run[r],
-// l_run[r] and o_acc[r] belong to row tile r; NSUB 16-token sub-tiles start
-// at kt / vt (tokens tok_base ..); all 8 head_dim tiles.
-template <typename T, int NSUB>
-__device__ __forceinline__ void tile_compute_w(const unsigned char* kt, const unsigned char* vt,
-                                               const v8s (&qf)[2][4], const uint32_t (&koff)[4],
-                                               const uint32_t (&voff)[8], int tok_base, int valid, int lg,
-                                               float scale, float (&m_run)[2], float (&l_run)[2],
-                                               v4f (&o_acc)[2][8]) {
-  v8s kf[NSUB][4];
-#pragma unroll
-  for (int k = 0; k < NSUB; ++k)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kf[k][ks] = *reinterpret_cast<const v8s*>(kt + k * 4096 + koff[ks]);
-  v4s vf[8][NSUB];
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k)
-      vf[mt][k] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + k * 4096 + voff[mt]));
-
-  float x[2][NSUB][4];
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k) {
-      v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) acc = mfma_qk<T>(kf[k][ks], qf[r][ks], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[r][k][i] = acc[i] * scale;
-    }
-  if (valid < tok_base + 16 * NSUB) {
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (tok_base + k * 16 + 4 * lg + i >= valid) {
-          x[0][k][i] = -INFINITY;
-          x[1][k][i] = -INFINITY;
-        }
-  }
-  v4s pf[2][NSUB];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, x[r][k][i]);
-    mx = rows4_max(mx);
-    const float m_new = fmaxf(m_run[r], mx);
-    const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run[r]) != 0) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run[r] - msafe);
-      l_run[r] *= alpha;
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) o_acc[r][mt] *= alpha;
-    }
-    m_run[r] = m_new;
-#pragma unroll
-    for (int k = 0; k < NSUB; ++k) {
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(x[r][k][i] - msafe);
-        l_run[r] += p[i];
-      }
-      pf[r][k] = pack4<T>(p[0], p[1], p[2], p[3]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-      v4f o = o_acc[r][mt];
-      if constexpr (NSUB == 1) {
-        o = mfma_pv<T>(vf[mt][0], pf[r][0], o);
-      } else {
-#pragma unroll
-        for (int k = 0; k < NSUB; k += 2)
-          o = mfma_qk<T>(__builtin_shufflevector(vf[mt][k], vf[mt][k + 1], 0, 1, 2, 3, 4, 5, 6, 7),
-                         __builtin_shufflevector(pf[r][k], pf[r][k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
-      }
-      o_acc[r][mt] = o;
-    }
 }
 
 // Online softmax of one (query, KV head) over its tail chunks c = first,

@@ -140,6 +140,12 @@ typedef struct be_level {
                                     kv_len - n + i + 1 tokens (FlashInfer's causal prefill
                                     alignment; such plans run the tile / VALU kernels)     */
 
+#define BE_PLAN_ROWS 256         /* decode plans: the merge-free row-block kernel (each workgroup
+                                    owns up to 16 rows -- queries x GQA heads of one KV head --
+                                    and all their groups on every level; no partials, one
+                                    kernel) whenever it applies                             */
+#define BE_PLAN_NO_ROWS 512      /* never the row-block kernel                               */
+
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the
  * live counts sit in a device header, and be_attn_run launches capacity-sized
@@ -158,7 +164,8 @@ typedef struct be_attn_plan_info {
   int32_t num_merge;       /* queries merged by the merge kernel               */
   int32_t num_queries;
   int32_t num_qo_heads, num_kv_heads, head_dim, page_size, num_pages, dtype;
-  int32_t kernel;          /* 0 = VALU, 1 = MFMA tile, 2 = MFMA streaming (persistent) */
+  int32_t kernel;          /* 0 = VALU, 1 = MFMA tile, 2 = MFMA streaming (persistent),
+                              3 = MFMA row blocks (one kernel, no merge)           */
   int32_t tile_rows;       /* rows (queries x GQA group) per MFMA tile: 16/32  */
   int32_t chunk_tokens;    /* split-K chunk length                             */
   int32_t plan_ints;       /* int32 words of the device plan                    */

@@ -517,3 +517,100 @@ def test_causal_flag_without_multi_query_groups_changes_nothing():
     b = plan(levels, hq=32, hkv=8, page=16, num_pages=8, flags=128)
     assert a[0] == b[0] == 0 and b[1].off_seg_causal == 0
     assert np.array_equal(a[2][: a[1].plan_ints], b[2][: b[1].plan_ints])
+
+
+# ---------------------------------------------------------------- row-block plans
+ROWS = 256     # BE_PLAN_ROWS
+
+
+def rows_coverage(levels, info, buf, nq, hq, hkv, page):
+    """Decode a row-block plan: for every (query, query head), the multiset of
+    (page, slot) keys its task's passes cover for it; and the workgroup order's
+    placement of tasks sharing a level-0 group on one XCD lane (id mod 8)."""
+    g = hq // hkv
+    tasks = buf[info.off_items: info.off_items + 8 * info.num_items].reshape(-1, 8)
+    pages = buf[info.off_pages:]
+    got = {}
+    for wg, (q0, n, p0, np_, head, nsub, _, _) in enumerate(tasks):
+        assert 1 <= n and n * g <= 16 and 0 <= head < hkv
+        subs = 0
+        for pi in range(p0, p0 + np_):
+            base, tokens, mask, sub = buf[info.off_merge_rows + 4 * pi: info.off_merge_rows + 4 * pi + 4]
+            assert tokens > 0 and sub == (tokens + 15) // 16
+            subs += sub
+            keys = [(int(pages[base + t // page]), t % page) for t in range(tokens)]
+            for r in range(n * g):
+                if (int(mask) >> r) & 1:
+                    qi, qh = q0 + r // g, head * g + r % g
+                    got.setdefault((qi, qh), []).extend(keys)
+        assert subs == nsub
+    return got
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 8), (8, 8), (16, 2)])
+def test_rows_plan_covers_each_query_groups_once(seed, hq, hkv):
+    """BE_PLAN_ROWS plans of random multi-request beam tries (page 16): every
+    (query, head) gets exactly the (page, slot) keys of its groups on every
+    level (once per level it appears in)."""
+    import random
+    from beam_engine_amd.beam_state import BeamGenerateResult, BeamState, BeamToken
+    from tests.test_beam_state_product import RecordingPages
+    rng = random.Random(seed)
+    page = 16
+    pages = RecordingPages(4000, page)
+    st = BeamState(4, pages)
+    for r in range(rng.randint(1, 3)):
+        st.add_root_sequence(list(range(rng.randint(1, 90))), request_id=r)
+    for step in range(rng.randint(5, 60)):
+        res = []
+        for rid in sorted({c.request_id for c in st.candidates}):
+            idx = [i for i, c in enumerate(st.candidates) if c.request_id == rid]
+            pool = sorted(((i, rng.randrange(50), st.candidates[i].score - rng.random()) for i in idx for _ in range(3)),
+                          key=lambda t: -t[2])
+            chosen, seen = [], set()
+            for i, t, s_ in pool:
+                if (i, t) not in seen and len(chosen) < 4:
+                    seen.add((i, t))
+                    chosen.append((i, t, s_))
+            res += [BeamGenerateResult(st.candidates[i], [BeamToken(t, s_) for ii, t, s_ in chosen if ii == i])
+                    for i in idx]
+        st.add_filtered_results(res)
+    levels = st._cascade_lists()
+    nq = len(st.candidates)
+    rc, info, buf, _lib, L = plan(levels, nq=nq, hq=hq, hkv=hkv, page=page, num_pages=4000, flags=ROWS)
+    if hq // hkv > 16:
+        assert info.kernel != 3
+        return
+    assert rc == 0 and info.kernel == 3
+    got = rows_coverage(levels, info, buf, nq, hq, hkv, page)
+    for qi in range(nq):
+        want = []
+        for qo, kvp, kvi, lpl in levels:
+            for j in range(len(qo) - 1):
+                if qo[j] <= qi < qo[j + 1]:
+                    npg = kvp[j + 1] - kvp[j]
+                    t = 0 if npg == 0 else (npg - 1) * page + lpl[j]
+                    want += [(kvi[kvp[j] + k // page], k % page) for k in range(t)]
+        for qh in range(hq):
+            assert sorted(got.get((qi, qh), [])) == sorted(want), (qi, qh)
+
+
+def test_rows_plan_places_shared_blocks_on_one_xcd_lane():
+    """8 requests x 16 beams over a shared prefix, g = 4: four blocks of four
+    queries per (request, KV head); the four tasks of each get workgroup ids
+    equal modulo 8 (one XCD)."""
+    qo0 = list(range(0, 129, 16))
+    kvp0 = [0] + [64 * (r + 1) for r in range(8)]
+    kvi0 = list(range(512))
+    lv0 = (qo0, kvp0, kvi0, [16] * 8)
+    lv1 = (list(range(129)), list(range(129)), list(range(512, 640)), [7] * 128)
+    rc, info, buf, _lib, L = plan([lv0, lv1], nq=128, hq=32, hkv=8, page=16, num_pages=640, flags=ROWS)
+    assert rc == 0 and info.kernel == 3 and info.num_items == 256
+    tasks = buf[info.off_items: info.off_items + 8 * 256].reshape(-1, 8)
+    lanes = {}
+    for wg, t in enumerate(tasks):
+        key = (int(t[0]) // 16, int(t[4]))          # (request, KV head)
+        lanes.setdefault(key, set()).add(wg % 8)
+        assert int(t[1]) == 4 and int(t[3]) == 5     # four queries: the prefix pass and four suffix passes
+    assert len(lanes) == 64 and all(len(v) == 1 for v in lanes.values())

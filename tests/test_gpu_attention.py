@@ -531,3 +531,63 @@ def test_stream_tail_role_without_streamed_groups(ws, cus):
     torch.cuda.synchronize()
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
+
+
+@pytest.mark.parametrize("case", ["trees", "ns", "g8_ragged", "tree_c3", "keyless"])
+def test_row_block_kernel(ws, case):
+    """The merge-free row-block kernel (BE_PLAN_ROWS) against the float64
+    oracle: the reference's trees at page 16 (scaled), the north-star shape
+    (queries subset), GQA 8 with ragged suffixes, the config-3 tree, and a
+    query without any keys (o = 0, lse = -inf)."""
+    say(f"row-block kernel {case}")
+    from beam_engine_amd.workloads import BUILDERS, shared_prefix
+    if case == "trees":
+        for name in ("cascade_md", "swapped", "uneven"):
+            e = FX["trees"][name]["expected"]
+            levels = (e["qo_indptr"], e["kv_indptr"], e["kv_indices"], e["last_page_len"])
+            npages = max(max(l) for l in e["kv_indices"] if l) + 1
+            # page 16 with each fixture page's tokens kept (last_page_len scaled by 4)
+            lv = (levels[0], levels[1], levels[2], [[min(16, 4 * x) for x in l] for l in levels[3]])
+            kv = make_pool(npages, 16, 2, 128, torch.bfloat16, 31, 128 ** -0.5)
+            q = make_q(levels[0][0][-1], 8, 128, torch.bfloat16, 32, 128 ** -0.5)
+            from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+            w = MultiLevelCascadeAttentionWrapper(len(lv[0]), ws)
+            w._rows = True
+            w.plan(*lv, 8, 2, 128, 16, q_data_type=torch.bfloat16)
+            assert w.stats.kernel == "rows"
+            out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
+            torch.cuda.synchronize()
+            ref_o, ref_lse = oa.cascade_attention(q, kv, *lv, 16, 128 ** -0.5)
+            check(out, lse, ref_o, ref_lse, torch.bfloat16)
+        return
+    if case == "keyless":
+        levels = ([[0, 2, 3]], [[0, 2, 2]], [[0, 1]], [[16, 0]])
+        kv = make_pool(4, 16, 8, 128, torch.bfloat16, 33, 128 ** -0.5)
+        q = make_q(3, 32, 128, torch.bfloat16, 34, 128 ** -0.5)
+        from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+        w = MultiLevelCascadeAttentionWrapper(1, ws)
+        w._rows = True
+        w.plan(*levels, 32, 8, 128, 16, q_data_type=torch.bfloat16)
+        out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
+        torch.cuda.synchronize()
+        ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, 16, 128 ** -0.5)
+        check(out, lse, ref_o, ref_lse, torch.bfloat16)
+        assert torch.all(out[2] == 0) and torch.all(torch.isinf(lse[2]))
+        return
+    wl = {"ns": lambda: BUILDERS["ns"](), "tree_c3": lambda: BUILDERS["c3"](),
+          "g8_ragged": lambda: shared_prefix("g8", 2, 8, 320, list(range(1, 17)), 64, 8, 128)}[case]()
+    kv = make_pool(wl.num_pages, wl.page, wl.hkv, wl.d, torch.bfloat16, 35, wl.d ** -0.5)
+    q = make_q(wl.num_queries, wl.hq, wl.d, torch.bfloat16, 36, wl.d ** -0.5)
+    from beam_engine_amd import MultiLevelCascadeAttentionWrapper
+    w = MultiLevelCascadeAttentionWrapper(len(wl.levels[0]), ws)
+    w._rows = True
+    w.plan(*wl.levels, wl.hq, wl.hkv, wl.d, wl.page, q_data_type=torch.bfloat16)
+    assert w.stats.kernel == "rows"
+    out, lse = w.run(q.cuda(), kv.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    sub = sorted({0, 1, wl.num_queries // 3, wl.num_queries // 2, wl.num_queries - 1})
+    kvp, kvi, lpl = wl.flat
+    ref_o, ref_lse = oa.paged_attention(q[sub], kv, [0] + list(np.cumsum([kvp[i + 1] - kvp[i] for i in sub])),
+                                        [p for i in sub for p in kvi[kvp[i]:kvp[i + 1]]], [lpl[i] for i in sub],
+                                        wl.page, wl.d ** -0.5)
+    check(out[sub], lse[sub], ref_o, ref_lse, torch.bfloat16)
