@@ -17,13 +17,17 @@
 // Order: within a row (logp desc, index asc); in the pool (total desc,
 // row*k + rank asc) with total = parent_score + (double)logp.
 //
-// Pass 1  grid (S, N): per segment max and float64 exp-sum.
-// Pass 2  grid (S, N): per segment, exact k best by radix select over the
-//         order-preserving uint32 key of logp, ties to the lowest index.
-// Pass 3  grid (N):    rank the row's S*k candidates -> sorted row top-k.
-// Pass 4  grid (1):    radix select the beam best of the N*k pool (uint64 key
-//         of the float64 total, ties to the lowest pool position), emitted in
-//         pool-position order = grouped by row, children in selection order.
+// Pass 1  grid (S, N): per segment max, float64 exp-sum and candidates -- the
+//         positions whose x' reaches a threshold that >= k of them reach,
+//         sorted -- with the largest x' below the threshold; the logits are
+//         read once.
+// Pass 2  grid (N):    the row's (m, L); the k best candidates by logp key,
+//         ranked by merging the sorted segment lists; a row where an outside
+//         value could tie the k-th is selected exactly over all its logits
+//         instead.
+// Pass 3  grid (R):    per request, the beam best of the row lists' pool by
+//         merge ranks, emitted in pool-position order = grouped by row,
+//         children in selection order.
 
 #include <math.h>
 
@@ -34,11 +38,19 @@
 namespace be {
 
 constexpr int kTopkThreads = 256;
-constexpr int kMaxSegLen = 8192;     // keys staged in LDS per segment
+constexpr int kMaxSegLen = 8192;     // logits per segment (32 per thread, in registers)
 constexpr int kMaxSegs = 64;
-constexpr int kMaxRowCand = 4096;    // S * k bound for pass 3
-constexpr int kMaxPool = 8192;       // N * k bound for pass 4
+constexpr int kMaxRowCand = 4096;    // candidates of one row (segments x cap), LDS in pass 2
+constexpr int kMaxPool = 8192;       // rows x k of one request, LDS in pass 3
+constexpr int kMaxPoolRows = 512;    // rows of one request
 constexpr int kMaxK = 256;
+
+// Candidate space per segment: 4k rounded up to a power of two, within [64, 256].
+inline int topk_cap(int k) {
+  int c = 64;
+  while (c < 4 * k && c < 256) c *= 2;
+  return c;
+}
 
 struct TopkGeom {
   int segs, seg_len;
@@ -51,7 +63,7 @@ static TopkGeom topk_geom(int n_rows, int vocab, int k) {
   const int by_k = (vocab + k - 1) / k;                   // every segment holds >= k elements
   if (segs > by_k) segs = by_k;
   if (segs > kMaxSegs) segs = kMaxSegs;
-  if (segs * k > kMaxRowCand) segs = kMaxRowCand / k;
+  if (segs * topk_cap(k) > kMaxRowCand) segs = kMaxRowCand / topk_cap(k);
   if (segs < 1) segs = 1;
   int seg_len = (vocab + segs - 1) / segs;
   seg_len = (seg_len + 7) & ~7;                           // 16-byte segment starts for 16-bit logits
@@ -95,36 +107,145 @@ __device__ __forceinline__ int seg_pos(int j) {
   return (j / V) * (kTopkThreads * V) + (int)threadIdx.x * V + (j % V);
 }
 
-// The thread's logits of one segment (n valid positions from seg), scaled by
-// the temperature; positions >= n read as `fill`.  16-byte loads when the
-// segment start is 16-byte aligned (uniform over the workgroup), else one
-// load per logit.
+// The thread's logits of one segment, temperature-scaled: 16-bit logits stay
+// in their storage format, two to a register (x' is rounded to that format, so
+// it is exact there), fp32 logits one to a register.  Positions >= n (past
+// the segment) read as 0xffff (16-bit: a NaN, whose order key is 0) or -inf
+// (fp32).
 template <typename T>
-__device__ __forceinline__ void load_seg(const T* seg, int n, TempScale inv_temp, float fill, float (&x)[kPerThread]) {
-  constexpr int V = 16 / (int)sizeof(T);
-  if ((reinterpret_cast<uintptr_t>(seg) & 15) == 0) {
+struct SegVals {
+  uint32_t w[kPerThread / 2];
+  __device__ __forceinline__ float at(int j) const {
+    const uint32_t u = w[j >> 1];
+    if constexpr (sizeof(T) == 2 && __is_same(T, bf16_t)) {
+      return __uint_as_float((j & 1) ? (u & 0xffff0000u) : (u << 16));
+    } else {
+      return (float)__builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? (u >> 16) : (u & 0xffffu)));
+    }
+  }
+};
+template <>
+struct SegVals<float> {
+  float x[kPerThread];
+  __device__ __forceinline__ float at(int j) const { return x[j]; }
+};
+
+template <typename T>
+__device__ __forceinline__ uint16_t bits_of(float x);
+template <> __device__ __forceinline__ uint16_t bits_of<bf16_t>(float x) { return f32_to_bf16_bits(x); }
+template <> __device__ __forceinline__ uint16_t bits_of<f16_t>(float x) {
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t raw_bits(const T* p) {
+  return __builtin_bit_cast(uint16_t, *p);
+}
+
+// Loads n valid positions from seg (16-byte loads when the segment start is
+// 16-byte aligned, uniform over the workgroup; else one load per logit).
+template <typename T>
+__device__ __forceinline__ void load_vals(const T* seg, int n, TempScale ts, SegVals<T>& v) {
+  constexpr int V = 8;                                 // 16-bit logits per 16 bytes
+  constexpr uint16_t kPast = 0xffff;                   // past the segment: a negative NaN pattern, key 0
+  const bool aligned = (reinterpret_cast<uintptr_t>(seg) & 15) == 0;
 #pragma unroll
-    for (int c = 0; c < kPerThread / V; ++c) {
-      const int p0 = c * (kTopkThreads * V) + (int)threadIdx.x * V;
-      if (p0 + V <= n) {
-        const uint4 u = *reinterpret_cast<const uint4*>(seg + p0);
-        T t[V];
-        __builtin_memcpy(t, &u, 16);
+  for (int c = 0; c < kPerThread / V; ++c) {
+    const int p0 = c * (kTopkThreads * V) + (int)threadIdx.x * V;
+    if (aligned && p0 + V <= n) {
+      const uint4 u = *reinterpret_cast<const uint4*>(seg + p0);
+      v.w[c * 4 + 0] = u.x;
+      v.w[c * 4 + 1] = u.y;
+      v.w[c * 4 + 2] = u.z;
+      v.w[c * 4 + 3] = u.w;
+    } else {
 #pragma unroll
-        for (int e = 0; e < V; ++e) x[c * V + e] = scaled<T>(to_f32(t[e]), inv_temp);
-      } else {
-#pragma unroll
-        for (int e = 0; e < V; ++e) x[c * V + e] = p0 + e < n ? scaled<T>(load_logit(seg + p0 + e), inv_temp) : fill;
+      for (int e = 0; e < V; e += 2) {
+        const uint32_t lo = p0 + e < n ? raw_bits(seg + p0 + e) : kPast;
+        const uint32_t hi = p0 + e + 1 < n ? raw_bits(seg + p0 + e + 1) : kPast;
+        v.w[c * 4 + e / 2] = lo | (hi << 16);
       }
     }
-  } else {
+  }
+  if (ts.t != 1.0f) {
 #pragma unroll
-    for (int j = 0; j < kPerThread; ++j) {
-      const int p = seg_pos<T>(j);
-      x[j] = p < n ? scaled<T>(load_logit(seg + p), inv_temp) : fill;
+    for (int i = 0; i < kPerThread / 2; ++i) {
+      const uint32_t u = v.w[i];
+      const uint32_t lo = (u & 0xffffu) == kPast ? kPast : bits_of<T>(scaled<T>(v.at(2 * i), ts));
+      const uint32_t hi = (u >> 16) == kPast ? kPast : bits_of<T>(scaled<T>(v.at(2 * i + 1), ts));
+      v.w[i] = lo | (hi << 16);
     }
   }
 }
+template <>
+__device__ __forceinline__ void load_vals<float>(const float* seg, int n, TempScale ts, SegVals<float>& v) {
+  constexpr int V = 4;
+  const bool aligned = (reinterpret_cast<uintptr_t>(seg) & 15) == 0;
+#pragma unroll
+  for (int c = 0; c < kPerThread / V; ++c) {
+    const int p0 = c * (kTopkThreads * V) + (int)threadIdx.x * V;
+    if (aligned && p0 + V <= n) {
+      const float4 u = *reinterpret_cast<const float4*>(seg + p0);
+      v.x[c * 4 + 0] = scaled<float>(u.x, ts);
+      v.x[c * 4 + 1] = scaled<float>(u.y, ts);
+      v.x[c * 4 + 2] = scaled<float>(u.z, ts);
+      v.x[c * 4 + 3] = scaled<float>(u.w, ts);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) v.x[c * 4 + e] = p0 + e < n ? scaled<float>(seg[p0 + e], ts) : -INFINITY;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- DPP wave scans
+// Inclusive scans over the 64 lanes of a wave on the VALU (no LDS): row_shr 1,
+// 2, 4, 8 within each 16-lane row, then row_bcast:15 and row_bcast:31 carry the
+// row totals upward; lane 63 ends with the whole wave's value.
+template <int CTRL, int ROWS, bool ZERO>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, ROWS, 0xf, ZERO);
+}
+
+__device__ __forceinline__ int wave_scan_add(int x) {
+  x += (int)dpp<0x111, 0xf, true>(0, x);
+  x += (int)dpp<0x112, 0xf, true>(0, x);
+  x += (int)dpp<0x114, 0xf, true>(0, x);
+  x += (int)dpp<0x118, 0xf, true>(0, x);
+  x += (int)dpp<0x142, 0xa, false>(0, x);
+  x += (int)dpp<0x143, 0xc, false>(0, x);
+  return x;
+}
+
+__device__ __forceinline__ uint32_t wave_scan_max(uint32_t x) {
+  x = max(x, dpp<0x111, 0xf, true>(0, x));
+  x = max(x, dpp<0x112, 0xf, true>(0, x));
+  x = max(x, dpp<0x114, 0xf, true>(0, x));
+  x = max(x, dpp<0x118, 0xf, true>(0, x));
+  x = max(x, dpp<0x142, 0xa, false>(0, x));
+  x = max(x, dpp<0x143, 0xc, false>(0, x));
+  return x;
+}
+
+template <int CTRL, int ROWS, bool ZERO>
+__device__ __forceinline__ double dpp_f64(double src) {
+  const uint64_t u = (uint64_t)__double_as_longlong(src);
+  const uint32_t lo = dpp<CTRL, ROWS, ZERO>(0, (uint32_t)u);
+  const uint32_t hi = dpp<CTRL, ROWS, ZERO>(0, (uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// A fixed order of additions: the sum does not depend on timing.
+__device__ __forceinline__ double wave_scan_add_f64(double x) {
+  x += dpp_f64<0x111, 0xf, true>(x);
+  x += dpp_f64<0x112, 0xf, true>(x);
+  x += dpp_f64<0x114, 0xf, true>(x);
+  x += dpp_f64<0x118, 0xf, true>(x);
+  x += dpp_f64<0x142, 0xa, false>(x);
+  x += dpp_f64<0x143, 0xc, false>(x);
+  return x;
+}
+
+__device__ __forceinline__ uint32_t lane63(uint32_t x) { return (uint32_t)__builtin_amdgcn_readlane((int)x, 63); }
 
 __device__ __forceinline__ uint32_t fkey(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -135,28 +256,29 @@ __device__ __forceinline__ uint64_t dkey(double f) {
   return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
 }
 
-__device__ __forceinline__ float block_max(float v, float* red) {
-  v = wave_max(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+// ---------------------------------------------------------------- 16-bit keys
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+typedef short v2i16 __attribute__((ext_vector_type(2)));
+
+// Order-preserving 16-bit keys of two packed 16-bit floats (bf16 or f16 bit
+// patterns): negative values get their bits inverted, the others the sign bit
+// set.  0xffff (a negative NaN pattern: positions past the segment) maps to 0,
+// below every other key.
+__device__ __forceinline__ uint32_t key16x2(uint32_t u) {
+  const v2i16 sgn = __builtin_bit_cast(v2i16, u) >> (v2i16){15, 15};   // 0xffff where negative
+  return u ^ (__builtin_bit_cast(uint32_t, sgn) | 0x80008000u);
 }
 
-__device__ __forceinline__ double block_sum_d(double v, double* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
+// The 32-bit key (fkey of the float value) of the 16-bit value with key k16.
+template <typename T>
+__device__ __forceinline__ uint32_t key32_of16(uint32_t k16) {
+  const uint16_t raw = (uint16_t)((k16 & 0x8000u) ? (k16 ^ 0x8000u) : (~k16 & 0xffffu));
+  return fkey(to_f32(__builtin_bit_cast(T, raw)));
 }
 
-// Block-wide inclusive scans of one int per thread: shuffles inside each wave,
-// then the wave totals through LDS (two barriers instead of a barrier pair per
-// doubling step).  Suffix: sum over threads >= tid; prefix: threads <= tid.
+// Block-wide inclusive suffix sum (over threads >= tid) of one int per
+// thread: shuffles inside each wave, then the wave totals through LDS (two
+// barriers instead of a barrier pair per doubling step).
 __device__ __forceinline__ int block_suffix_sum(int v, int* tot /*4*/) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
@@ -170,199 +292,6 @@ __device__ __forceinline__ int block_suffix_sum(int v, int* tot /*4*/) {
   __syncthreads();
   return v;
 }
-__device__ __forceinline__ int block_prefix_sum(int v, int* tot /*4*/) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o, 64);
-    if (lane >= o) v += u;
-  }
-  if (lane == 63) tot[w] = v;
-  __syncthreads();
-  for (int x = 0; x < w; ++x) v += tot[x];
-  __syncthreads();
-  return v;
-}
-
-// Exact block-wide selection of the k largest keys, ties broken by the lowest
-// position.  keys[0..n) live in LDS.  Writes min(k, n) positions (unordered)
-// to out_pos (LDS) and returns that count.  All 256 threads must call it.
-template <typename K>
-__device__ int block_select(const K* keys, int n, int k, int* out_pos, int* hist /*4*256*/,
-                            int* suf /*257*/, int* misc /*8*/) {
-  const int tid = threadIdx.x, w = tid >> 6;
-  if (n <= k) {
-    for (int i = tid; i < n; i += kTopkThreads) out_pos[i] = i;
-    __syncthreads();
-    return n;
-  }
-  K prefix = 0, mask = 0;
-  int krem = k;
-  for (int shift = (int)sizeof(K) * 8 - 8; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 4 * 256; i += kTopkThreads) hist[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += kTopkThreads) {
-      const K key = keys[i];
-      if ((key & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((key >> shift) & 255)], 1);
-    }
-    __syncthreads();
-    // suffix sums: suf[d] = #digits >= d
-    suf[tid] = block_suffix_sum(hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid], misc + 4);
-    if (tid == 0) suf[256] = 0;
-    __syncthreads();
-    if (suf[tid] >= krem && suf[tid + 1] < krem) {   // unique digit
-      misc[0] = tid;
-      misc[1] = suf[tid + 1];
-    }
-    __syncthreads();
-    const int digit = misc[0];
-    krem -= misc[1];
-    prefix |= ((K)digit) << shift;
-    mask |= ((K)255) << shift;
-    __syncthreads();
-  }
-  // keys > prefix: exactly k - krem of them; keys == prefix: the krem lowest positions
-  if (tid == 0) misc[2] = 0;
-  __syncthreads();
-  const int per = (n + kTopkThreads - 1) / kTopkThreads;
-  const int b = tid * per, e = min(n, b + per);
-  int eq = 0;
-  for (int i = b; i < e; ++i) {
-    const K key = keys[i];
-    if (key > prefix) out_pos[atomicAdd(&misc[2], 1)] = i;
-    else if (key == prefix) ++eq;
-  }
-  // exclusive scan of eq over threads (in position order)
-  int rank = block_prefix_sum(eq, misc + 4) - eq;
-  const int ngt = k - krem;
-  for (int i = b; i < e && rank < krem; ++i)
-    if (keys[i] == prefix) out_pos[ngt + rank++] = i;
-  __syncthreads();
-  return k;
-}
-
-// block_select over keys held in registers by the segment kernel: the
-// thread's key j sits at segment position seg_pos<T>(j), present when that
-// position is < n.  Exact k largest, ties to the lowest position; writes
-// min(k, n) positions (unordered) to out_pos and their keys to out_key and
-// returns that count.  All 256 threads must call it.
-template <typename T>
-__device__ int block_select_regs(const uint32_t (&kr)[kPerThread], int n, int k, int* out_pos, uint32_t* out_key,
-                                 int* hist /*4*256*/, int* suf /*257*/, int* misc /*8*/) {
-  constexpr int V = 16 / (int)sizeof(T);
-  const int tid = threadIdx.x, w = tid >> 6;
-  if (n <= k) {
-#pragma unroll
-    for (int j = 0; j < kPerThread; ++j) {
-      const int p = seg_pos<T>(j);
-      if (p < n) {
-        out_pos[p] = p;
-        out_key[p] = kr[j];
-      }
-    }
-    __syncthreads();
-    return n;
-  }
-  uint32_t prefix = 0, mask = 0;
-  int krem = k;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 4 * 256; i += kTopkThreads) hist[i] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kPerThread; ++j)
-      if (seg_pos<T>(j) < n && (kr[j] & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((kr[j] >> shift) & 255u)], 1);
-    __syncthreads();
-    suf[tid] = block_suffix_sum(hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid], misc + 4);
-    if (tid == 0) suf[256] = 0;
-    __syncthreads();
-    if (suf[tid] >= krem && suf[tid + 1] < krem) {   // unique digit
-      misc[0] = tid;
-      misc[1] = suf[tid + 1];
-    }
-    __syncthreads();
-    krem -= misc[1];
-    prefix |= ((uint32_t)misc[0]) << shift;
-    mask |= 255u << shift;
-    __syncthreads();
-  }
-  // keys > prefix: exactly k - krem of them; keys == prefix: the krem lowest
-  // positions, ranked chunk by chunk (chunk c of every thread precedes chunk
-  // c + 1 in position order; inside a chunk, threads in order)
-  if (tid == 0) misc[2] = 0;
-  __syncthreads();
-  const int ngt = k - krem;
-  int base = 0;
-#pragma unroll
-  for (int c = 0; c < kPerThread / V; ++c) {
-    int eq = 0;
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const int j = c * V + e;
-      if (seg_pos<T>(j) < n) {
-        if (kr[j] > prefix) {
-          const int at = atomicAdd(&misc[2], 1);
-          out_pos[at] = seg_pos<T>(j);
-          out_key[at] = kr[j];
-        } else if (kr[j] == prefix) {
-          ++eq;
-        }
-      }
-    }
-    const int incl = block_prefix_sum(eq, misc + 4);
-    const int chunk_total = misc[4] + misc[5] + misc[6] + misc[7];
-    int rank = base + incl - eq;
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const int j = c * V + e;
-      if (seg_pos<T>(j) < n && kr[j] == prefix) {
-        if (rank < krem) {
-          out_pos[ngt + rank] = seg_pos<T>(j);
-          out_key[ngt + rank] = prefix;
-        }
-        ++rank;
-      }
-    }
-    base += chunk_total;
-    __syncthreads();   // the wave totals are rewritten by the next chunk's scan
-  }
-  __syncthreads();
-  return k;
-}
-
-// ---------------------------------------------------------------- pass 1
-template <typename T>
-__global__ __launch_bounds__(kTopkThreads) void topk_stats_kernel(const T* logits, int64_t row_stride, int vocab,
-                                                                 int seg_len, TempScale inv_temp, float* seg_max,
-                                                                 double* seg_sum) {
-  __shared__ float redf[4];
-  __shared__ double redd[4];
-  const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
-  constexpr int kPer = kPerThread;                   // logits per thread, read once
-  const T* row = logits + (int64_t)r * row_stride;
-  const int b = s * seg_len, n = min(vocab, b + seg_len) - b;
-  float x[kPer];
-  load_seg<T>(row + b, n, inv_temp, -INFINITY, x);
-  // each thread sums against its own maximum (no wait for the block's), then
-  // rescales by exp(m_t - m); a thread whose logits are all -inf adds 0
-  float mt = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) mt = fmaxf(mt, x[j]);
-  double acc = 0.0;
-  if (mt != -INFINITY) {
-    const double md = (double)mt;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j)
-      if (seg_pos<T>(j) < n) acc += exp((double)x[j] - md);
-  }
-  const float m = block_max(mt, redf);
-  if (mt != -INFINITY) acc *= exp((double)mt - (double)m);
-  acc = block_sum_d(acc, redd);
-  if (threadIdx.x == 0) {
-    seg_max[(int64_t)r * segs + s] = m;
-    seg_sum[(int64_t)r * segs + s] = acc;
-  }
-}
-
 // Row max m and L = fl32(ln S) from the segment statistics, once per
 // workgroup: wave 0 takes one segment per lane (S_s exp(m_s - m) in
 // parallel), lane 0 adds the terms in segment order (a fixed float64 sum).
@@ -390,231 +319,712 @@ __device__ __forceinline__ float logp_of(float xs, float m, float L) {
   return round_to<T>(__fsub_rn(__fsub_rn(xs, m), L));
 }
 
-// ---------------------------------------------------------------- pass 2
-// Block-wide bitonic sort, descending, of one value per thread (256 values):
-// partners closer than 64 lanes exchange by shuffle, farther ones through LDS.
-template <typename K>
-__device__ K block_sort_desc(K v, K* xch) {
-  const int tid = threadIdx.x;
-#pragma unroll 1
-  for (int size = 2; size <= kTopkThreads; size <<= 1) {
-#pragma unroll 1
-    for (int j = size >> 1; j > 0; j >>= 1) {
-      K p;
-      if (j >= 64) {
-        xch[tid] = v;
-        __syncthreads();
-        p = xch[tid ^ j];
-        __syncthreads();
-      } else if constexpr (sizeof(K) == 8) {
-        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
-        p = ((K)hi << 32) | lo;
-      } else {
-        p = (K)__shfl_xor((int)v, j, 64);
-      }
-      const bool lower = (tid & j) == 0, first_half = (tid & size) == 0;
-      // descending blocks where first_half: the lower index keeps the larger value
-      v = (lower == first_half) ? (v > p ? v : p) : (v < p ? v : p);
-    }
-  }
-  return v;
+// ---------------------------------------------------------------- wave sort
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
 }
 
-// Wave-wide bitonic sort, descending, of one value per lane (64 values).
-template <typename K>
-__device__ K wave_sort_desc(K v) {
+// Wave-wide bitonic sort, descending, of NPL * 64 values: item q = e * 64 + lane
+// lives in v[e] of that lane.  Partners 64 or more items apart are in the
+// same lane (a register exchange), nearer ones in another lane (a shuffle).
+template <int NPL>
+__device__ __forceinline__ void wave_sort_desc_u64(uint64_t (&v)[NPL]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
+  for (int size = 2; size <= 64 * NPL; size <<= 1) {
 #pragma unroll
     for (int j = size >> 1; j > 0; j >>= 1) {
-      K p;
-      if constexpr (sizeof(K) == 8) {
-        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
-        p = ((K)hi << 32) | lo;
+      if (j >= 64) {
+        const int je = j >> 6;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) {
+          if ((e & je) == 0) {
+            // q & size does not depend on the lane: size > j >= 64
+            const bool first = ((e * 64) & size) == 0;
+            const uint64_t a = v[e], b = v[e | je];
+            const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+            v[e] = first ? hi : lo;
+            v[e | je] = first ? lo : hi;
+          }
+        }
       } else {
-        p = (K)__shfl_xor((int)v, j, 64);
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) {
+          const uint64_t p = shfl_xor_u64(v[e], j);
+          const int q = e * 64 + lane;
+          const bool lower = (q & j) == 0, first = (q & size) == 0;
+          // descending blocks where first: the lower item keeps the larger value
+          v[e] = (lower == first) ? (v[e] > p ? v[e] : p) : (v[e] < p ? v[e] : p);
+        }
       }
-      const bool lower = (lane & j) == 0, first_half = (lane & size) == 0;
-      v = (lower == first_half) ? (v > p ? v : p) : (v < p ? v : p);
     }
   }
-  return v;
 }
 
-// Per segment the exact k best logp (ties to the lowest index), emitted in
-// ascending index order.  Each wave sorts its 64 per-thread maxima; the
-// ceil(k/4)-th largest of every wave are, with the larger ones above them,
-// at least k distinct elements, so the smallest of the four is a lower bound
-// of the segment's k-th largest key.  The elements at or above it are
-// collected as (key, position) composites; up to 64 of them are sorted by one
-// wave, up to 256 by the workgroup, more fall back to the radix select over
-// all keys.
+// ---------------------------------------------------------------- float64 exp
+// e^d for d <= 0, accurate to about one ulp, without branches: Tang's
+// table-driven method.  k = rint(d 64 / ln 2), r = d - k ln2/64 (Cody-Waite,
+// hi part of 36 bits so k * hi is exact), e^r - 1 by its degree-5 Taylor
+// polynomial (|r| <= ln2/128: the first omitted term, r^6/720, is below
+// 4e-17), times 2^((k mod 64) / 64) from a 64-entry table and 2^floor(k / 64).
+// rint comes from adding 1.5 * 2^52 (k is then the low word of the sum) and
+// 2^floor(k / 64) from adding floor(k / 64) to the table entry's exponent, so
+// no rounding, conversion or ldexp instruction is needed.  d is clamped to
+// -708 first (fmax also maps NaN there), which keeps that exponent normal:
+// -inf, NaN and anything below give e^-708, nothing against the sums of at
+// least 1 these terms go into.
+constexpr double kInvLn2x64 = 0x1.71547652b82fep+6;
+constexpr double kLn2By64Hi = 0x1.62e42fefa0000p-7;
+constexpr double kLn2By64Lo = 0x1.cf79abc9e3b3ap-46;
+constexpr double kRoundShift = 0x1.8p52;
+
+__device__ __forceinline__ void exp_table_init(double* tab) {
+  if (threadIdx.x < 64) tab[threadIdx.x] = exp2((double)threadIdx.x / 64.0);
+}
+
+__device__ __forceinline__ double exp_neg(double d, const double* tab) {
+  const double dc = fmax(d, -708.0);
+  const double sh = fma(dc, kInvLn2x64, kRoundShift);
+  const int k = (int)(uint32_t)(uint64_t)__double_as_longlong(sh);
+  const double kf = sh - kRoundShift;
+  double r = fma(-kf, kLn2By64Hi, dc);
+  r = fma(-kf, kLn2By64Lo, r);
+  double p = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+  p = fma(r, p, 1.0 / 6.0);
+  p = fma(r, p, 0.5);
+  p = fma(r, p, 1.0);
+  p *= r;                                           // e^r - 1
+  const uint64_t tb = (uint64_t)__double_as_longlong(tab[k & 63]);
+  const uint32_t hi = (uint32_t)(tb >> 32) + ((uint32_t)(k >> 6) << 20);
+  const double t = __longlong_as_double((long long)(((uint64_t)hi << 32) | (uint32_t)tb));
+  return fma(t, p, t);
+}
+
+// ---------------------------------------------------------------- pass 1
+constexpr int kMaxCap = 256;
+
+// The segment's candidates (lc[0, total), composite keys) sorted descending by
+// wave 0 and written to out.
+template <int NPL>
+__device__ __forceinline__ void sort_out_candidates(const uint64_t* lc, int total, uint64_t* out) {
+  const int lane = threadIdx.x & 63;
+  uint64_t v[NPL];
+#pragma unroll
+  for (int e = 0; e < NPL; ++e) v[e] = e * 64 + lane < total ? lc[e * 64 + lane] : 0ull;
+  wave_sort_desc_u64<NPL>(v);
+#pragma unroll
+  for (int e = 0; e < NPL; ++e)
+    if (e * 64 + lane < total) out[e * 64 + lane] = v[e];
+}
+
+// Per (segment, row): the segment max m_s and S_s = sum exp(x' - m_s) in
+// float64 (x' the temperature-scaled logits; logits are read once), and the
+// segment's candidates: every position whose x' reaches a threshold tau that
+// at least k positions reach (the smallest of the four waves' ceil(k/4)-th
+// largest per-thread maximum, found bit by bit with ballots), as composite
+// keys (order-preserving key of x') << 32 | ~(vocabulary index), sorted
+// descending (x' descending, index ascending), plus the largest key below tau
+// (0 if none).  More than `cap` candidates is flagged (count -1).  logp is
+// monotone in x', so a row's best logp values are among its segments'
+// candidates unless a segment's largest outside value rounds to the same logp
+// as the row's k-th candidate -- pass 2 checks exactly that.
+//
+// Waves per SIMD the register budget allows: the kernel is latency-bound, so
+// more resident workgroups hide more of it.
+constexpr int kCandWavesPerSimd = 8;
+
+// One barrier exchanges the waves' maxima, float64 sums (each against its
+// wave's max) and thresholds; wave reductions and scans run on DPP; each wave
+// takes its candidates' LDS slots with one atomic add (their order there does
+// not matter: wave 0 sorts them).
+// The segment's float64 sum from the waves' sums (each against its wave's
+// max), its candidates sorted out by wave 0, and its statistics.
+__device__ __forceinline__ void finish_segment(const uint64_t* lc, int total, int cap, float m, const float* wmax,
+                                               const double* wsum, const double* tab, uint32_t bound, int64_t rs,
+                                               float* seg_max, double* seg_sum, int* seg_cnt, uint32_t* seg_bound,
+                                               uint64_t* cand) {
+  if (total <= cap && threadIdx.x < 64) {
+    uint64_t* out = cand + rs * cap;
+    if (total <= 64) sort_out_candidates<1>(lc, total, out);
+    else if (total <= 128) sort_out_candidates<2>(lc, total, out);
+    else sort_out_candidates<4>(lc, total, out);
+  }
+  if (threadIdx.x == 0) {
+    // the waves' sums rescaled to the segment max, in wave order
+    double sum = 0.0;
+    for (int q = 0; q < 4; ++q) sum += wsum[q] * exp_neg((double)wmax[q] - (double)m, tab);
+    seg_max[rs] = m;
+    seg_sum[rs] = sum;
+    seg_cnt[rs] = total <= cap ? total : -1;
+    seg_bound[rs] = bound;
+  }
+}
+
+// fp32 logits: 32-bit keys (one logit to a register: four waves per SIMD
+// leave it room without spills).
 template <typename T>
-__global__ __launch_bounds__(kTopkThreads) void topk_segment_kernel(const T* logits, int64_t row_stride, int vocab,
-                                                                   int seg_len, TempScale inv_temp, int k,
-                                                                   const float* seg_max, const double* seg_sum,
-                                                                   float* cand_val, int32_t* cand_idx) {
-  constexpr int kPer = kPerThread;                   // keys per thread (kept in registers)
-  __shared__ int pos[kMaxK];
-  __shared__ uint32_t selkey[kMaxK];
-  __shared__ int hist[4 * 256];
-  __shared__ int suf[257];
-  __shared__ int misc[8];
-  __shared__ uint64_t comp[kTopkThreads];
+__global__ __launch_bounds__(kTopkThreads, 4) void topk_cand_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                int seg_len, TempScale ts, int k, int cap,
+                                                                float* seg_max, double* seg_sum, int* seg_cnt,
+                                                                uint32_t* seg_bound, uint64_t* cand) {
+  __shared__ double tab[64];
+  __shared__ float wmax[4];
+  __shared__ double wsum[4];
   __shared__ uint32_t wtau[4];
-  __shared__ double terms[64];
-  __shared__ float mL[2];
+  __shared__ uint32_t wbelow[4];
+  __shared__ int ncand;
+  __shared__ uint64_t lc[kMaxCap];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
   const T* row = logits + (int64_t)r * row_stride;
-  const int b = s * seg_len, e = min(vocab, b + seg_len), n = e - b;
-  // this thread's logits (positions seg_pos(j)), loaded before the row
-  // normaliser so that the two latencies overlap
-  float xs[kPer];
-  load_seg<T>(row + b, n, inv_temp, 0.f, xs);
-  float m, L;
-  if (tid == 0) misc[3] = 0;                         // candidate count
-  row_norm_block(seg_max, seg_sum, r, segs, m, L, terms, mL);
-  // keys (real keys are > 0)
-  uint32_t kr[kPer];
+  const int b = s * seg_len, n = min(vocab, b + seg_len) - b;
+  exp_table_init(tab);
+  if (tid == 0) ncand = 0;
+  SegVals<T> x;
+  load_vals<T>(row + b, n, ts, x);
+  // key 0 marks positions past the segment (valid keys are >= fkey(-inf) > 0)
+  auto key_at = [&](int j) -> uint32_t { return seg_pos<T>(j) < n ? fkey(x.at(j)) : 0u; };
   uint32_t kmax = 0;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = seg_pos<T>(j);
-    uint32_t key = 0;
-    if (i < n) key = fkey(logp_of<T>(xs[j], m, L));
-    kr[j] = key;
-    kmax = key > kmax ? key : kmax;
+  for (int j = 0; j < kPerThread; ++j) kmax = max(kmax, key_at(j));
+  // the thread max: -inf when the thread holds no position or only -inf
+  const float mt = kmax > fkey(-INFINITY) ? __uint_as_float((kmax & 0x80000000u) ? (kmax & 0x7fffffffu) : ~kmax)
+                                          : -INFINITY;
+  // the wave's kw-th largest per-thread maximum, bit by bit
+  const int kw = (k + 3) >> 2;                         // <= 64
+  uint32_t pref = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t c = pref | (1u << bit);
+    if (__popcll(__builtin_amdgcn_ballot_w64(kmax >= c)) >= kw) pref = c;
   }
-  const int kw = (k + 3) >> 2;                       // <= 64
-  const uint32_t ws = wave_sort_desc<uint32_t>(kmax);
-  if (lane == kw - 1) wtau[w] = ws;
-  __syncthreads();
-  const uint32_t t0 = min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3]));
+  const uint32_t kwave = lane63(wave_scan_max(kmax));  // key of the wave max
+  __syncthreads();                                     // the exp table, ncand
+  // float64 sum against the thread's own max, then against the wave's
+  const double md = (double)mt;
+  double acc = 0.0;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = seg_pos<T>(j);
-    if (i < n && kr[j] >= t0) {
-      const int at = atomicAdd(&misc[3], 1);
-      if (at < kTopkThreads) comp[at] = ((uint64_t)kr[j] << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+  for (int j = 0; j < kPerThread; ++j) acc += exp_neg((double)x.at(j) - md, tab);
+  const float mw = kwave > fkey(-INFINITY)
+                       ? __uint_as_float((kwave & 0x80000000u) ? (kwave & 0x7fffffffu) : ~kwave)
+                       : -INFINITY;
+  acc = mt == -INFINITY ? 0.0 : acc * exp_neg(md - (double)mw, tab);
+  acc = wave_scan_add_f64(acc);
+  if (lane == 63) {
+    wmax[w] = mw;
+    wsum[w] = acc;
+    wtau[w] = pref;
+  }
+  __syncthreads();
+  const float m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const uint32_t tau = max(1u, min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3])));
+  int mine = 0;
+  uint32_t below = 0;
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const uint32_t key = key_at(j);
+    mine += key >= tau ? 1 : 0;
+    below = max(below, key < tau ? key : 0u);
+  }
+  const int incl = wave_scan_add(mine);
+  int wbase = 0;
+  if (lane == 63) wbase = atomicAdd(&ncand, incl);
+  int at = (int)lane63((uint32_t)wbase) + incl - mine;
+  if (mine > 0) {
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      const uint32_t key = key_at(j);
+      if (key >= tau) {
+        if (at < cap) lc[at] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(j));
+        ++at;
+      }
+    }
+  }
+  below = wave_scan_max(below);
+  if (lane == 63) wbelow[w] = below;
+  __syncthreads();
+  finish_segment(lc, ncand, cap, m, wmax, wsum, tab, max(max(wbelow[0], wbelow[1]), max(wbelow[2], wbelow[3])),
+                 (int64_t)r * segs + s, seg_max, seg_sum, seg_cnt, seg_bound, cand);
+}
+
+// 16-bit logits: packed 16-bit order keys, two to a register (packed u16 max,
+// saturating subtract and min count and compare two logits per instruction),
+// a 16-bit threshold search, and as the boundary key the value just below the
+// threshold (an upper bound of every outside value).
+template <typename T>
+__global__ __launch_bounds__(kTopkThreads, kCandWavesPerSimd) void topk_cand16_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                                  int seg_len, TempScale ts, int k, int cap,
+                                                                  float* seg_max, double* seg_sum, int* seg_cnt,
+                                                                  uint32_t* seg_bound, uint64_t* cand) {
+  __shared__ double tab[64];
+  __shared__ float wmax[4];
+  __shared__ double wsum[4];
+  __shared__ uint32_t wtau[4];
+  __shared__ int ncand;
+  __shared__ uint64_t lc[kMaxCap];
+  constexpr int kWords = kPerThread / 2;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int s = blockIdx.x, r = blockIdx.y, segs = gridDim.x;
+  const T* row = logits + (int64_t)r * row_stride;
+  const int b = s * seg_len, n = min(vocab, b + seg_len) - b;
+  exp_table_init(tab);
+  if (tid == 0) ncand = 0;
+  SegVals<T> x;
+  load_vals<T>(row + b, n, ts, x);
+  uint32_t kp[kWords];
+  v2u16 km2 = {0, 0};
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) {
+    kp[i] = key16x2(x.w[i]);
+    km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(v2u16, kp[i]));
+  }
+  const uint32_t kmax = max((uint32_t)km2.x, (uint32_t)km2.y);
+  const uint32_t kninf = key16x2(__is_same(T, bf16_t) ? 0xff80u : 0xfc00u) & 0xffffu;   // key of -inf
+  auto value_of = [&](uint32_t k16) -> float {
+    return k16 > kninf ? to_f32(__builtin_bit_cast(T, (uint16_t)((k16 & 0x8000u) ? (k16 ^ 0x8000u) : (~k16 & 0xffffu))))
+                       : -INFINITY;
+  };
+  const float mt = value_of(kmax);
+  // the wave's kw-th largest per-thread maximum, bit by bit
+  const int kw = (k + 3) >> 2;                         // <= 64
+  uint32_t pref = 0;
+  for (int bit = 15; bit >= 0; --bit) {
+    const uint32_t c = pref | (1u << bit);
+    if (__popcll(__builtin_amdgcn_ballot_w64(kmax >= c)) >= kw) pref = c;
+  }
+  const float mw = value_of(lane63(wave_scan_max(kmax)));
+  __syncthreads();                                     // the exp table, ncand
+  // float64 sum against the thread's own max, then against the wave's
+  // (positions past the segment read as NaN: exp_neg gives 0)
+  const double md = (double)mt;
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) acc += exp_neg((double)x.at(j) - md, tab);
+  acc = mt == -INFINITY ? 0.0 : acc * exp_neg(md - (double)mw, tab);
+  acc = wave_scan_add_f64(acc);
+  if (lane == 63) {
+    wmax[w] = mw;
+    wsum[w] = acc;
+    wtau[w] = pref;
+  }
+  __syncthreads();
+  const float m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const uint32_t tau = max(1u, min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3])));
+  // count of keys >= tau: min(sat(key - (tau - 1)), 1) per half
+  const v2u16 t1 = {(unsigned short)(tau - 1), (unsigned short)(tau - 1)};
+  const v2u16 one = {1, 1};
+  v2u16 c2 = {0, 0};
+#pragma unroll
+  for (int i = 0; i < kWords; ++i)
+    c2 += __builtin_elementwise_min(__builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, kp[i]), t1), one);
+  const int mine = (int)c2.x + (int)c2.y;
+  const int incl = wave_scan_add(mine);
+  int wbase = 0;
+  if (lane == 63) wbase = atomicAdd(&ncand, incl);
+  int at = (int)lane63((uint32_t)wbase) + incl - mine;
+  if (mine > 0) {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) {
+      const uint32_t lo = kp[i] & 0xffffu, hi = kp[i] >> 16;
+      if (max(lo, hi) >= tau) {
+        if (lo >= tau) {
+          if (at < cap) lc[at] = ((uint64_t)key32_of16<T>(lo) << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i));
+          ++at;
+        }
+        if (hi >= tau) {
+          if (at < cap)
+            lc[at] = ((uint64_t)key32_of16<T>(hi) << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i + 1));
+          ++at;
+        }
+      }
     }
   }
   __syncthreads();
-  const int total = misc[3];
-  int cnt = k;
-  if (n <= k || total > kTopkThreads) {
-    cnt = block_select_regs<T>(kr, n, k, pos, selkey, hist, suf, misc);
-  } else if (total <= 64) {
-    if (w == 0) {
-      const uint64_t v = wave_sort_desc<uint64_t>(lane < total ? comp[lane] : 0ull);
-      if (lane < k) {
-        pos[lane] = (int)(0xffffffffu - (uint32_t)v);
-        selkey[lane] = (uint32_t)(v >> 32);
+  finish_segment(lc, ncand, cap, m, wmax, wsum, tab, tau > 1 ? key32_of16<T>(tau - 1) : 0u,
+                 (int64_t)r * segs + s, seg_max, seg_sum, seg_cnt, seg_bound, cand);
+}
+
+// ---------------------------------------------------------------- selection helper
+// The k best of n items by (key desc, idx asc), keys and vocabulary indices
+// given by key_of(i) / idx_of(i), i < n (n >= k): a radix select of the k-th
+// largest key (4 passes of 8 bits), every item above it, and among the items
+// equal to it the lowest indices (a second radix select, over inverted
+// indices, only when the ties exceed what is needed).  Writes the k chosen
+// (key, idx) pairs to out_key / out_idx (LDS, unordered).  All threads call it.
+template <typename KeyF, typename IdxF>
+__device__ void select_k(KeyF key_of, IdxF idx_of, int n, int k, uint32_t* out_key, int32_t* out_idx,
+                         int* hist /*4*256*/, int* suf /*257*/, int* misc /*8*/) {
+  const int tid = threadIdx.x, w = tid >> 6;
+  auto radix = [&](auto val_of, auto live, int want, uint32_t& prefix_out) -> int {
+    // returns how many of the `want` remain at the selected value prefix_out
+    uint32_t prefix = 0, mask = 0;
+    int krem = want;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 4 * 256; i += kTopkThreads) hist[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < n; i += kTopkThreads) {
+        if (!live(i)) continue;
+        const uint32_t v = val_of(i);
+        if ((v & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((v >> shift) & 255u)], 1);
+      }
+      __syncthreads();
+      suf[tid] = block_suffix_sum(hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid], misc + 4);
+      if (tid == 0) suf[256] = 0;
+      __syncthreads();
+      if (suf[tid] >= krem && suf[tid + 1] < krem) {
+        misc[0] = tid;
+        misc[1] = suf[tid + 1];
+      }
+      __syncthreads();
+      krem -= misc[1];
+      prefix |= ((uint32_t)misc[0]) << shift;
+      mask |= 255u << shift;
+      __syncthreads();
+    }
+    prefix_out = prefix;
+    return krem;
+  };
+  uint32_t T;
+  const int krem = radix(key_of, [](int) { return true; }, k, T);
+  // items above T, and the count of ties
+  if (tid == 0) {
+    misc[2] = 0;
+    misc[3] = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += kTopkThreads) {
+    const uint32_t v = key_of(i);
+    if (v > T) {
+      const int at = atomicAdd(&misc[2], 1);
+      out_key[at] = v;
+      out_idx[at] = idx_of(i);
+    } else if (v == T) {
+      atomicAdd(&misc[3], 1);
+    }
+  }
+  __syncthreads();
+  const int ngt = k - krem, nties = misc[3];
+  if (nties == krem) {
+    if (tid == 0) misc[2] = ngt;
+    __syncthreads();
+    for (int i = tid; i < n; i += kTopkThreads)
+      if (key_of(i) == T) {
+        const int at = atomicAdd(&misc[2], 1);
+        out_key[at] = T;
+        out_idx[at] = idx_of(i);
+      }
+  } else {
+    // the krem lowest indices among the ties: largest inverted index
+    uint32_t I;
+    radix([&](int i) { return 0xffffffffu - (uint32_t)idx_of(i); }, [&](int i) { return key_of(i) == T; }, krem, I);
+    if (tid == 0) misc[2] = ngt;
+    __syncthreads();
+    for (int i = tid; i < n; i += kTopkThreads)
+      if (key_of(i) == T && 0xffffffffu - (uint32_t)idx_of(i) >= I) {
+        const int at = atomicAdd(&misc[2], 1);
+        out_key[at] = T;
+        out_idx[at] = idx_of(i);
+      }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------- pass 2
+// Per row: the row's (m, L) from the segment statistics, then the k best
+// candidates by (logp desc, index asc) from the segments' lists (sorted by
+// x' desc, index asc):
+//  1. the row's k best by x' -- every list entry is ranked by counting, in
+//     each other list, the entries above it (binary searches over the first
+//     k entries, sixteen lists at a time, with selects rather than branches
+//     so that their LDS reads overlap), list positions in chunks of 16 until
+//     no list has a further entry of rank < k;
+//  2. logp is monotone in x', so the k-th logp is the logp of the k-th x';
+//     the entries above it are selected, and from its tie group (every
+//     candidate with that logp, gathered wave by wave over the lists) the
+//     ones of lowest index;
+//  3. the k selected are ordered by (logp desc, index asc) by counting.
+// The candidates hold the row's k best unless a segment overflowed its
+// candidate space, the tie group overflows its LDS array, or a segment's
+// outside values (all at most its boundary key) reach the k-th logp; then the
+// row is selected exactly over all its logits.
+constexpr int kSlotsPerThread = kMaxRowCand / kTopkThreads;
+constexpr int kMaxTie = 512;
+
+template <typename T>
+__global__ __launch_bounds__(kTopkThreads) void topk_row_kernel(const T* logits, int64_t row_stride, int vocab,
+                                                               TempScale ts, int segs, int k, int cap,
+                                                               const float* seg_max, const double* seg_sum,
+                                                               const int* seg_cnt, const uint32_t* seg_bound,
+                                                               const uint64_t* cand, float* row_vals,
+                                                               int32_t* row_idx) {
+  __shared__ uint64_t la[kMaxRowCand];                 // x' composite keys, list after list
+  __shared__ uint64_t bx[kMaxK];                       // the k best by x' composite, in order
+  __shared__ uint64_t tg[kMaxTie];                     // the tie group (logp composite keys)
+  __shared__ uint64_t fin[kMaxK];                      // the k selected (logp composite keys)
+  __shared__ uint32_t skey[kMaxK];
+  __shared__ int32_t sidx[kMaxK];
+  __shared__ int hist[4 * 256];
+  __shared__ int suf[257];
+  __shared__ int misc[8];
+  __shared__ double terms[64];
+  __shared__ float mL[2];
+  __shared__ int off[kMaxSegs + 1];
+  __shared__ int more[kMaxK / 16];
+  __shared__ int flag, ntie, nfin;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = blockIdx.x;
+  const int64_t base = (int64_t)r * segs;
+  const int lcap = __ffs(cap) - 1;                     // cap is a power of two
+  const int nslots = segs << lcap;
+  // the row's candidate slots (segs lists of cap), loaded at once; slots past
+  // a list's count hold stale words and are not used
+  const uint64_t* blk = cand + base * cap;
+  uint64_t v[kSlotsPerThread];
+#pragma unroll
+  for (int u = 0; u < kSlotsPerThread; ++u)
+    if (u * kTopkThreads < nslots) v[u] = blk[min(u * kTopkThreads + tid, nslots - 1)];
+  if (tid < kMaxK / 16) more[tid] = 0;
+  if (tid == 0) {
+    ntie = 0;
+    nfin = 0;
+  }
+  if (tid < 64) {
+    const int c = tid < segs ? seg_cnt[base + tid] : 0;
+    int incl = c < 0 ? 0 : c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (tid >= o) incl += u;
+    }
+    if (tid < segs) off[tid + 1] = incl;
+    if (tid == 0) off[0] = 0;
+    const bool over = __builtin_amdgcn_ballot_w64(c < 0) != 0;
+    if (tid == 0) flag = over ? 1 : 0;
+  }
+  float m, L;
+  row_norm_block(seg_max, seg_sum, r, segs, m, L, terms, mL);   // (its barrier publishes the above)
+  auto key_of_x = [&](uint32_t xk) -> uint32_t {       // x' key -> logp key
+    const uint32_t u = (xk & 0x80000000u) ? (xk & 0x7fffffffu) : ~xk;
+    return fkey(logp_of<T>(__uint_as_float(u), m, L));
+  };
+  bool exact = flag != 0;
+  if (!exact) {
+#pragma unroll
+    for (int u = 0; u < kSlotsPerThread; ++u) {
+      const int f = u * kTopkThreads + tid, sg = f >> lcap, p = f & (cap - 1);
+      if (f < nslots) {
+        const int lo = off[sg];
+        if (p < off[sg + 1] - lo) la[lo + p] = v[u];
       }
     }
     __syncthreads();
-  } else {
-    const uint64_t v = tid < total ? comp[tid] : 0ull;
-    __syncthreads();
-    const uint64_t sorted = block_sort_desc<uint64_t>(v, comp);
-    if (tid < k) {
-      pos[tid] = (int)(0xffffffffu - (uint32_t)sorted);
-      selkey[tid] = (uint32_t)(sorted >> 32);
+    // 1. the k best by x'
+    int top = 1;
+    while (top * 2 <= k) top *= 2;
+    for (int c0 = 0; c0 < k; c0 += 16) {
+      for (int f = tid; f < segs * 16; f += kTopkThreads) {
+        const int sg = f >> 4, p = c0 + (f & 15);
+        const int lo = off[sg], len = off[sg + 1] - lo;
+        if (p >= len) continue;
+        const uint64_t key = la[lo + p];
+        int rank = p;
+        for (int l0 = 0; l0 < segs && rank < k; l0 += 16) {
+          int pos[16], bs[16], ln[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            const int l = l0 + u;
+            const bool use = (l < segs) & (l != sg);
+            const int o0 = off[min(l, segs)], o1 = off[min(l + 1, segs)];
+            bs[u] = use ? o0 : 0;
+            ln[u] = use ? min(o1 - o0, k) : 0;
+            pos[u] = 0;
+          }
+          for (int step = top; step > 0; step >>= 1) {
+            uint64_t y[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) y[u] = la[max(bs[u] + min(pos[u] + step, ln[u]) - 1, 0)];
+            // the sixteen reads are issued before any compare waits for one
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              const int c = pos[u] + step;
+              // bitwise & keeps the choice a select (a short-circuit && would let
+              // the compiler sink the read under a branch)
+              pos[u] = ((c <= ln[u]) & (y[u] > key)) ? c : pos[u];
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 16; ++u) rank += pos[u];
+        }
+        if (rank < k) {
+          bx[rank] = key;
+          if ((f & 15) == 15 && p + 1 < len) more[c0 >> 4] = 1;
+        }
+      }
+      __syncthreads();
+      if (!more[c0 >> 4]) break;
+    }
+    // 2. the k-th logp; the entries above it, and its tie group
+    const uint32_t kth = key_of_x((uint32_t)(bx[k - 1] >> 32));
+    for (int i = tid; i < k; i += kTopkThreads) {
+      const uint64_t x = bx[i];
+      const uint32_t lk = key_of_x((uint32_t)(x >> 32));
+      if (lk > kth) fin[atomicAdd(&nfin, 1)] = ((uint64_t)lk << 32) | (uint32_t)x;
+    }
+    for (int sg = w; sg < segs; sg += kTopkThreads / 64) {
+      const int lo = off[sg], len = off[sg + 1] - lo;
+      for (int p0 = 0; p0 < len; p0 += 64) {
+        const int p = p0 + lane;
+        const uint64_t x = p < len ? la[lo + p] : 0ull;
+        const uint32_t lk = p < len ? key_of_x((uint32_t)(x >> 32)) : 0u;
+        if (lk == kth && p < len) {
+          const int at = atomicAdd(&ntie, 1);
+          if (at < kMaxTie) tg[at] = ((uint64_t)lk << 32) | (uint32_t)x;
+        }
+        // the list is sorted: past its last entry at or above the k-th logp, stop
+        if (__builtin_amdgcn_ballot_w64(p < len && lk >= kth) != ~0ull) break;
+      }
+    }
+    if (tid < segs) {
+      const uint32_t bk = seg_bound[base + tid];
+      if (bk != 0 && key_of_x(bk) >= kth) atomicOr(&flag, 1);
     }
     __syncthreads();
+    exact = flag != 0 || ntie > kMaxTie;
+    if (!exact) {
+      const int above = nfin, g = ntie, need = k - above;
+      for (int i = tid; i < g; i += kTopkThreads) {
+        const uint64_t x = tg[i];
+        const uint32_t xi = ~(uint32_t)x;                // index
+        int rk = 0;
+        for (int j = 0; j < g; ++j) rk += (~(uint32_t)tg[j]) < xi ? 1 : 0;
+        if (rk < need) fin[above + rk] = x;
+      }
+      __syncthreads();
+      // 3. order by (logp desc, index asc)
+      for (int i = tid; i < k; i += kTopkThreads) {
+        const uint64_t x = fin[i];
+        int pos = 0;
+        for (int j = 0; j < k; ++j) pos += fin[j] > x ? 1 : 0;
+        const uint32_t ki = (uint32_t)(x >> 32);
+        const uint32_t u = (ki & 0x80000000u) ? (ki & 0x7fffffffu) : ~ki;
+        row_vals[(int64_t)r * k + pos] = __uint_as_float(u);
+        row_idx[(int64_t)r * k + pos] = (int32_t)~(uint32_t)x;
+      }
+      return;
+    }
   }
-  float* cv = cand_val + ((int64_t)r * segs + s) * k;
-  int32_t* ci = cand_idx + ((int64_t)r * segs + s) * k;
-  // emit in ascending vocabulary index, so that candidate order = index order
-  for (int j = tid; j < cnt; j += kTopkThreads) {
-    const int p = pos[j];
+  // every logit of the row (re-read from memory; rows here are rare)
+  const T* row = logits + (int64_t)r * row_stride;
+  select_k([&](int i) { return fkey(logp_of<T>(scaled<T>(load_logit(row + i), ts), m, L)); },
+           [&](int i) { return i; }, vocab, k, skey, sidx, hist, suf, misc);
+  // rank the k chosen by (key desc, idx asc)
+  for (int i = tid; i < k; i += kTopkThreads) {
+    const uint32_t ki = skey[i];
+    const int ii = sidx[i];
     int rank = 0;
-    for (int t = 0; t < cnt; ++t) rank += (pos[t] < p);
-    const uint32_t key = selkey[j];
-    const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
-    cv[rank] = __uint_as_float(u);
-    ci[rank] = b + p;
-  }
-  for (int j = cnt + tid; j < k; j += kTopkThreads) {
-    cv[j] = -INFINITY;
-    ci[j] = -1;   // empty slot (segment shorter than k)
+    for (int j = 0; j < k; ++j) rank += (skey[j] > ki) || (skey[j] == ki && sidx[j] < ii);
+    const uint32_t u = (ki & 0x80000000u) ? (ki & 0x7fffffffu) : ~ki;
+    row_vals[(int64_t)r * k + rank] = __uint_as_float(u);
+    row_idx[(int64_t)r * k + rank] = ii;
   }
 }
 
 // ---------------------------------------------------------------- pass 3
-// Candidates are segment-major and index-ascending inside a segment, so their
-// position order is vocabulary order: the radix select's lowest-position tie
-// rule is the lowest-index rule.  The k selected are then ranked among
-// themselves by (value desc, index asc).
-__global__ __launch_bounds__(kTopkThreads) void topk_row_kernel(int segs, int k, const float* cand_val,
-                                                               const int32_t* cand_idx, float* row_vals,
-                                                               int32_t* row_idx) {
-  __shared__ uint32_t keys[kMaxRowCand];
-  __shared__ int pos[kMaxK];
-  __shared__ int hist[4 * 256];
-  __shared__ int suf[257];
-  __shared__ int misc[8];
-  const int r = blockIdx.x;
-  const int c = segs * k;
-  const float* cv = cand_val + (int64_t)r * c;
-  const int32_t* ci = cand_idx + (int64_t)r * c;
-  for (int i = threadIdx.x; i < c; i += kTopkThreads) keys[i] = (ci[i] < 0) ? 0u : fkey(cv[i]);
-  __syncthreads();
-  const int cnt = block_select<uint32_t>(keys, c, k, pos, hist, suf, misc);
-  for (int i = threadIdx.x; i < cnt; i += kTopkThreads) {
-    const int p = pos[i];
-    const uint32_t kp = keys[p];
-    int rank = 0;
-    for (int j = 0; j < cnt; ++j) {
-      const uint32_t kj = keys[pos[j]];
-      rank += (kj > kp) || (kj == kp && pos[j] < p);
-    }
-    row_vals[(int64_t)r * k + rank] = cv[p];
-    row_idx[(int64_t)r * k + rank] = ci[p];
-  }
-}
-
-// ---------------------------------------------------------------- pass 4
-// grid.x = request; its rows are [req_row_ptr[r], req_row_ptr[r+1]) (all rows
-// when req_row_ptr is null).  Parents are emitted as global row indices.
-__global__ __launch_bounds__(kTopkThreads) void topk_global_kernel(int n_rows, int k, int beam,
-                                                                  const int32_t* req_row_ptr, const double* parent,
-                                                                  const float* row_vals, const int32_t* row_idx,
-                                                                  int32_t* out_parent, int32_t* out_token,
-                                                                  double* out_score) {
-  __shared__ uint64_t keys[kMaxPool];
-  __shared__ int pos[kMaxK];
-  __shared__ int hist[4 * 256];
-  __shared__ int suf[257];
-  __shared__ int misc[8];
-  const int req = blockIdx.x;
+// Per request: the beam best of its pool total = parent[r] + (double)row_vals[r, j]
+// by (total desc, pool position r * k + j asc), emitted grouped by row.  Each
+// row's list is sorted by logp desc (its totals do not increase along it), so
+// an entry's pool rank is its rank in its row plus, in every other row, the
+// entries that precede it (a binary search); entries j >= beam of a row
+// cannot be selected.
+__global__ __launch_bounds__(kTopkThreads) void topk_pool_kernel(int n_rows, int k, int beam, const int32_t* req_row_ptr,
+                                                                const double* parent, const float* row_vals,
+                                                                const int32_t* row_idx, int32_t* out_parent,
+                                                                int32_t* out_token, double* out_score) {
+  __shared__ double tot[kMaxPool];
+  __shared__ int sel[kMaxPoolRows];
+  __shared__ int first[kMaxPoolRows + 1];
+  const int tid = threadIdx.x, req = blockIdx.x;
   const int rb = req_row_ptr ? req_row_ptr[req] : 0;
   const int re = req_row_ptr ? req_row_ptr[req + 1] : n_rows;
   int32_t* op = out_parent + (int64_t)req * beam;
   int32_t* ot = out_token + (int64_t)req * beam;
   double* os = out_score + (int64_t)req * beam;
-  const bool ok = rb >= 0 && re <= n_rows && rb <= re && (int64_t)(re - rb) * k <= kMaxPool;
-  const int n = ok ? (re - rb) * k : 0;
-  for (int i = threadIdx.x; i < n; i += kTopkThreads) {
-    const int r = rb + i / k;
-    keys[i] = dkey(parent[r] + (double)row_vals[(int64_t)rb * k + i]);
+  const bool ok = rb >= 0 && re <= n_rows && rb <= re && (re - rb) <= kMaxPoolRows && (int64_t)(re - rb) * k <= kMaxPool;
+  const int nr = ok ? re - rb : 0;
+  const int n = nr * k;
+  // four entries per thread at a time, their loads issued together
+  for (int i0 = 0; i0 < n; i0 += 4 * kTopkThreads) {
+    double pv[4];
+    float rv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(i0 + u * kTopkThreads + tid, n - 1);
+      pv[u] = parent[rb + i / k];
+      rv[u] = row_vals[(int64_t)rb * k + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * kTopkThreads + tid;
+      if (i < n) tot[i] = pv[u] + (double)rv[u];
+    }
+  }
+  for (int i = tid; i < nr; i += kTopkThreads) sel[i] = 0;
+  __syncthreads();
+  const int jb = min(k, beam);                      // candidates per row
+  int top = 1;
+  while (top * 2 <= jb) top *= 2;
+  for (int e = tid; e < nr * jb; e += kTopkThreads) {
+    const int rr = e / jb, j = e - rr * jb;
+    const double t = tot[rr * k + j];
+    int rank = j;
+    // entries of row o before (rr, j): totals > t, or == t when o < rr -- a
+    // prefix of the row, counted over its first jb entries (a count of jb
+    // already puts the entry at rank >= beam); sixteen rows' binary searches
+    // at a time, with selects rather than branches so that their LDS reads
+    // overlap (bitwise & and | keep every read unconditional)
+    for (int o0 = 0; o0 < nr && rank < beam; o0 += 16) {
+      int pos[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) pos[u] = 0;
+      for (int step = top; step > 0; step >>= 1) {
+        double y[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int o = o0 + u, c = pos[u] + step;
+          const bool use = (o < nr) & (o != rr) & (c <= jb);
+          y[u] = tot[use ? o * k + c - 1 : 0];
+        }
+        // the sixteen reads above are issued before any compare waits for one
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int o = o0 + u, c = pos[u] + step;
+          const bool use = (o < nr) & (o != rr) & (c <= jb);
+          pos[u] = (use & ((y[u] > t) | ((y[u] == t) & (o < rr)))) ? c : pos[u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) rank += pos[u];
+    }
+    if (rank < beam) atomicAdd(&sel[rr], 1);
   }
   __syncthreads();
-  const int cnt = block_select<uint64_t>(keys, n, beam, pos, hist, suf, misc);
-  // emit in pool-position order: rows ascending, children in selection order
-  for (int i = threadIdx.x; i < cnt; i += kTopkThreads) {
-    const int p = pos[i];
-    int rank = 0;
-    for (int j = 0; j < cnt; ++j) rank += (pos[j] < p);
-    const int r = rb + p / k;
-    op[rank] = r;
-    ot[rank] = row_idx[(int64_t)rb * k + p];
-    os[rank] = parent[r] + (double)row_vals[(int64_t)rb * k + p];
+  if (tid == 0) {
+    first[0] = 0;
+    for (int i = 0; i < nr; ++i) first[i + 1] = first[i] + sel[i];
   }
-  for (int i = cnt + threadIdx.x; i < beam; i += kTopkThreads) {
+  __syncthreads();
+  for (int e = tid; e < nr * jb; e += kTopkThreads) {
+    const int rr = e / jb, j = e - rr * jb;
+    if (j < sel[rr]) {
+      const int at = first[rr] + j;
+      op[at] = rb + rr;
+      ot[at] = row_idx[(int64_t)(rb + rr) * k + j];
+      os[at] = tot[rr * k + j];
+    }
+  }
+  for (int i = first[nr] + tid; i < beam; i += kTopkThreads) {
     op[i] = -1;
     ot[i] = -1;
     os[i] = -INFINITY;
@@ -782,7 +1192,8 @@ int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k) {
   if (n_rows <= 0 || vocab <= 0 || k <= 0) return 0;
   const be::TopkGeom geo = be::topk_geom(n_rows, vocab, k);
   const int64_t ns = (int64_t)n_rows * geo.segs;
-  return ns * 4 + ns * 8 + ns * k * 4 + ns * k * 4 + 256;
+  // seg_sum f64, candidates (u64) x cap, seg_max f32, seg_cnt i32, seg_bound u32
+  return ns * 8 + ns * be::topk_cap(k) * 8 + ns * 4 + ns * 4 + ns * 4 + 256;
 }
 
 static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, double temperature,
@@ -812,45 +1223,49 @@ static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int
     if (beam > be::kMaxK) return be::fail(BE_ERR_UNSUPPORTED, "beam = %d exceeds %d", beam, be::kMaxK);
     const int rows = req_row_ptr ? max_req_rows : n_rows;
     BE_REQUIRE(rows >= 0 && rows <= n_rows, "max_req_rows outside [0, n_rows]");
-    if ((int64_t)rows * k > be::kMaxPool)
-      return be::fail(BE_ERR_UNSUPPORTED, "pool %d x %d exceeds %d entries", rows, k, be::kMaxPool);
+    if ((int64_t)rows * k > be::kMaxPool || rows > be::kMaxPoolRows)
+      return be::fail(BE_ERR_UNSUPPORTED, "pool %d x %d exceeds %d entries (or %d rows)", rows, k, be::kMaxPool,
+                      be::kMaxPoolRows);
   }
   const int64_t need = be_beam_topk_workspace_bytes(n_rows, vocab, k);
   if (!workspace || workspace_bytes < need)
     return be::fail(BE_ERR_CAPACITY, "top-k workspace needs %lld bytes", (long long)need);
   if (n_rows > 65535) return be::fail(BE_ERR_UNSUPPORTED, "n_rows %d exceeds 65535", n_rows);
   const be::TopkGeom geo = be::topk_geom(n_rows, vocab, k);
-  if (geo.seg_len > be::kMaxSegLen || geo.segs * k > be::kMaxRowCand)
+  const int cap = be::topk_cap(k);
+  if (geo.seg_len > be::kMaxSegLen || geo.segs * cap > be::kMaxRowCand)
     return be::fail(BE_ERR_UNSUPPORTED, "vocab %d with k %d needs segments of %d > %d logits", vocab, k, geo.seg_len,
                     be::kMaxSegLen);
   const int64_t ns = (int64_t)n_rows * geo.segs;
   char* ws = reinterpret_cast<char*>(workspace);
   double* seg_sum = reinterpret_cast<double*>(ws);
-  float* seg_max = reinterpret_cast<float*>(ws + ns * 8);
-  float* cand_val = reinterpret_cast<float*>(ws + ns * 12);
-  int32_t* cand_idx = reinterpret_cast<int32_t*>(ws + ns * 12 + ns * k * 4);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(ws + ns * 8);
+  char* tail = ws + ns * 8 + ns * cap * 8;
+  float* seg_max = reinterpret_cast<float*>(tail);
+  int* seg_cnt = reinterpret_cast<int*>(tail + ns * 4);
+  uint32_t* seg_bound = reinterpret_cast<uint32_t*>(tail + ns * 8);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(geo.segs, n_rows);
   switch (dtype) {
-#define BE_TOPK_CASE(DT, TY)                                                                                   \
-  case DT:                                                                                                     \
-    be::topk_stats_kernel<TY><<<grid, be::kTopkThreads, 0, st>>>(reinterpret_cast<const TY*>(logits), row_stride, \
-                                                                 vocab, geo.seg_len, inv_temp, seg_max, seg_sum); \
-    be::topk_segment_kernel<TY><<<grid, be::kTopkThreads, 0, st>>>(reinterpret_cast<const TY*>(logits),        \
-                                                                   row_stride, vocab, geo.seg_len, inv_temp, k,   \
-                                                                   seg_max, seg_sum, cand_val, cand_idx);       \
+#define BE_TOPK_CASE(DT, TY, CAND)                                                                                \
+  case DT:                                                                                                        \
+    be::CAND<TY><<<grid, be::kTopkThreads, 0, st>>>(reinterpret_cast<const TY*>(logits), row_stride, vocab,       \
+                                                   geo.seg_len, inv_temp, k, cap, seg_max, seg_sum, seg_cnt,      \
+                                                   seg_bound, cand);                                              \
+    be::topk_row_kernel<TY><<<n_rows, be::kTopkThreads, 0, st>>>(reinterpret_cast<const TY*>(logits), row_stride,  \
+                                                                 vocab, inv_temp, geo.segs, k, cap, seg_max,       \
+                                                                 seg_sum, seg_cnt, seg_bound, cand, row_vals,      \
+                                                                 row_idx);                                         \
     break;
-    BE_TOPK_CASE(BE_F32, float)
-    BE_TOPK_CASE(BE_F16, be::f16_t)
-    BE_TOPK_CASE(BE_BF16, be::bf16_t)
+    BE_TOPK_CASE(BE_F32, float, topk_cand_kernel)
+    BE_TOPK_CASE(BE_F16, be::f16_t, topk_cand16_kernel)
+    BE_TOPK_CASE(BE_BF16, be::bf16_t, topk_cand16_kernel)
 #undef BE_TOPK_CASE
   }
   BE_HIP_CHECK(hipGetLastError());
-  be::topk_row_kernel<<<n_rows, be::kTopkThreads, 0, st>>>(geo.segs, k, cand_val, cand_idx, row_vals, row_idx);
-  BE_HIP_CHECK(hipGetLastError());
   if (beam > 0) {
-    be::topk_global_kernel<<<n_req, be::kTopkThreads, 0, st>>>(n_rows, k, beam, req_row_ptr, parent_scores,
-                                                              row_vals, row_idx, out_parent, out_token, out_score);
+    be::topk_pool_kernel<<<n_req, be::kTopkThreads, 0, st>>>(n_rows, k, beam, req_row_ptr, parent_scores, row_vals,
+                                                            row_idx, out_parent, out_token, out_score);
     BE_HIP_CHECK(hipGetLastError());
   }
   return BE_OK;

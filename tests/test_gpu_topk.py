@@ -137,12 +137,17 @@ def test_batched_requests_in_one_call():
         b += r
 
 
-@pytest.mark.parametrize("case", ["strided_best", "chunk_best", "constant", "two_levels", "near_ties_bf16"])
+@pytest.mark.parametrize("case", ["strided_best", "chunk_best", "constant", "two_levels", "near_ties_bf16",
+                                  "few_finite", "large_magnitude", "mixed_offsets_f16"])
 def test_segment_select_paths(case):
     """Logits that stress the per-segment selection: the best values all in
     one thread's stride (a single thread maximum among them), constant rows
-    (every key tied: more candidates than threads), two value levels, and
-    bf16 logp values tied after rounding."""
+    (every key tied: more candidates than threads), two value levels, bf16
+    logp values tied after rounding (runs of equal logp from different
+    logits, reordered by index), rows with fewer finite logits than k (the
+    rest of the k are -inf, lowest indices first), and 16-bit logits of
+    large magnitude (maxima far from 0, rows whose halves sit hundreds
+    apart: float64 rescaling between threads, waves and segments)."""
     say(f"topk segment paths {case}")
     g = torch.Generator().manual_seed(11)
     v = 128256
@@ -160,6 +165,22 @@ def test_segment_select_paths(case):
     elif case == "two_levels":
         x = torch.zeros((3, v))
         x[:, torch.randperm(v, generator=g)[:40]] = 1.0
+        logits = x.to(torch.float16)
+    elif case == "few_finite":
+        x = torch.full((2, v), float("-inf"))
+        x[0, torch.randperm(v, generator=g)[:10]] = torch.randn(10, generator=g)
+        x[1, 70000:70005] = 1.0
+        logits = x.to(torch.bfloat16)
+    elif case == "large_magnitude":
+        x = torch.randn((3, v), generator=g)
+        x[0] *= 400.0                            # maxima far above 300
+        x[1] -= 900.0                            # every value far below -300
+        x[2] = x[2] * 3.0 + 310.0
+        logits = x.to(torch.bfloat16)
+    elif case == "mixed_offsets_f16":
+        x = torch.randn((3, v), generator=g) * 2.0
+        x[:, : v // 2] += 305.0                  # half the segments hundreds above the rest
+        x[1, v // 2:] += 296.0
         logits = x.to(torch.float16)
     else:
         logits = (torch.randn((4, v), generator=g) * 0.05).to(torch.bfloat16)
