@@ -79,7 +79,10 @@ EXPORTS = (
     "be_version", "be_last_error", "be_kv_append", "be_rope_qkv_append", "be_page_copy", "be_attn_plan",
     "be_attn_run",
     "be_merge_states", "be_beam_topk_workspace_bytes", "be_beam_topk", "be_beam_topk_noalloc", "be_trie_cascade",
-    "be_diverse_select",
+    "be_diverse_select", "be_pages_create", "be_pages_destroy", "be_pages_allocate", "be_pages_share",
+    "be_pages_release", "be_pages_reserve", "be_pages_num_free", "be_pages_ref_count", "be_pages_free_list",
+    "be_trie_create", "be_trie_destroy", "be_trie_add_root", "be_trie_apply", "be_trie_sizes",
+    "be_trie_candidates", "be_trie_export", "be_trie_metadata", "be_trie_plan",
 )
 
 _lib = None
@@ -120,8 +123,33 @@ def load() -> ctypes.CDLL:
     lib.be_diverse_select.argtypes = [vp, vp, i32, i32, vp, i32, vp, i32, i32, i32, ctypes.c_double, vp, vp, vp,
                                       vp]
     lib.be_trie_cascade.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, vp, i64, ctypes.POINTER(ctypes.c_int64)]
+    i32p, i64p = ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)
+    lib.be_pages_create.argtypes = [i32]
+    lib.be_pages_create.restype = vp
+    lib.be_pages_destroy.argtypes = [vp]
+    lib.be_pages_destroy.restype = None
+    lib.be_pages_allocate.argtypes = [vp, i32p]
+    lib.be_pages_share.argtypes = [vp, i32, i32p]
+    lib.be_pages_release.argtypes = [vp, i32, i32p]
+    lib.be_pages_reserve.argtypes = [vp, i32]
+    lib.be_pages_num_free.argtypes = [vp]
+    lib.be_pages_ref_count.argtypes = [vp, i32]
+    lib.be_pages_free_list.argtypes = [vp, vp, i32]
+    lib.be_trie_create.argtypes = [i32, vp]
+    lib.be_trie_create.restype = vp
+    lib.be_trie_destroy.argtypes = [vp]
+    lib.be_trie_destroy.restype = None
+    lib.be_trie_add_root.argtypes = [vp, vp, i32, i32, vp]
+    lib.be_trie_apply.argtypes = [vp, vp, vp, vp, i32, i32, vp, i32, i32p, i32p]
+    lib.be_trie_sizes.argtypes = [vp, vp, i64p]
+    lib.be_trie_candidates.argtypes = [vp, vp, vp, vp]
+    lib.be_trie_export.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.be_trie_metadata.argtypes = [vp, vp, i64, i64p]
+    lib.be_trie_plan.argtypes = [vp, i32, i32, i32, i32, i32, i32, ctypes.POINTER(BePlanCaps), vp, i64, i64p, vp,
+                                 i64, ctypes.POINTER(BeAttnPlanInfo), i32p]
     for name in EXPORTS:
-        if name not in ("be_version", "be_last_error", "be_beam_topk_workspace_bytes"):
+        if name not in ("be_version", "be_last_error", "be_beam_topk_workspace_bytes", "be_pages_create",
+                        "be_pages_destroy", "be_trie_create", "be_trie_destroy"):
             getattr(lib, name).restype = i32
     _lib = lib
     return lib

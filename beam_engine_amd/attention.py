@@ -153,16 +153,7 @@ class _PagedPlanner:
         if isinstance(q_data_type, str):
             q_data_type = getattr(torch, q_data_type)
         dt = _lib.dtype_code(q_data_type)
-        flags = (_lib.BE_PLAN_FORCE_VALU if self._force_valu else 0) | \
-            (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0) | \
-            (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0) | \
-            (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0) | \
-            (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
-            (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
-            (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0) | \
-            (_lib.BE_PLAN_ROWS if self._rows is True else 0) | \
-            (_lib.BE_PLAN_NO_ROWS if self._rows is False else 0) | \
-            (_lib.BE_PLAN_CAUSAL if causal else 0)
+        flags = self._plan_flags() | (_lib.BE_PLAN_CAUSAL if causal else 0)
         staging = _Staging.get(self._ws.device)
         info = _lib.BeAttnPlanInfo()
         cap = staging.buf.numel()
@@ -177,6 +168,23 @@ class _PagedPlanner:
                 continue
             _lib.check(rc, "attention plan")
             break
+        self._install_plan(info, buf, staging, max_page, head_dim, sm_scale, q_data_type)
+
+    def _plan_flags(self) -> int:
+        return (_lib.BE_PLAN_FORCE_VALU if self._force_valu else 0) | \
+            (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0) | \
+            (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0) | \
+            (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0) | \
+            (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
+            (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
+            (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0) | \
+            (_lib.BE_PLAN_ROWS if self._rows is True else 0) | \
+            (_lib.BE_PLAN_NO_ROWS if self._rows is False else 0)
+
+    def _install_plan(self, info, buf: torch.Tensor, staging: "_Staging", max_page: int, head_dim: int,
+                      sm_scale: Optional[float], q_data_type) -> None:
+        """Upload a plan written into the pinned staging ``buf`` to the
+        workspace (stream-ordered before the next run) and adopt it."""
         plan_bytes = int(info.plan_ints) * 4
         part_off = (plan_bytes + _WS_ALIGN - 1) // _WS_ALIGN * _WS_ALIGN
         need = part_off + int(info.partial_bytes)

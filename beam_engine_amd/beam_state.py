@@ -15,12 +15,18 @@ computed:
   every candidate carries its ``request_id``.
 * ``add_filtered_results`` defers the page fork copies of one step to a
   single batched launch (page ids are allocated in the reference's order).
+* ``NativeBeamState`` is the same state kept in native code (the trie and its
+  page allocator, ``be_beam_trie``): the decode loop applies each selection
+  and builds the next step's metadata without Python work per candidate;
+  the Python objects (``candidates``, nodes, ``sequence`` ...) are built
+  from it when read.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 import ctypes
+import logging
 from typing import Dict, List, Optional, Tuple
 
 import numpy as np
@@ -28,6 +34,8 @@ import torch
 
 from .kv_tree_node import KVTreeNode
 from .page_table import PageTable
+
+logger = logging.getLogger(__name__)
 
 
 class TrieNode:
@@ -145,6 +153,12 @@ class BeamState:
         self._tab: Optional[_NodeTable] = _NodeTable() if fast_metadata else None
         self._meta_buf = np.zeros(1 << 16, np.int32)
         self._meta_used = ctypes.c_int64(0)
+
+    def num_candidates(self) -> int:
+        return len(self.candidates)
+
+    def num_finished(self) -> int:
+        return len(self.finished_candidates)
 
     # ------------------------------------------------------------ building
     def add_root_sequence(self, sequence: List[int], request_id: int = 0) -> List[TrieNode]:
@@ -690,3 +704,248 @@ class BeamState:
             out.append((seq, sc))
         out.sort(key=lambda x: x[1], reverse=True)
         return out[:num_return]
+
+
+class _PageRef:
+    """A created page of ``NativeBeamState.add_root_sequence`` (its id)."""
+    __slots__ = ("page_id",)
+
+    def __init__(self, page_id: int):
+        self.page_id = page_id
+
+
+def _parse_metadata(buf: np.ndarray, n: int):
+    """Split be_trie_cascade's output words into (levels, query tokens, write
+    pages, write slots, positions)."""
+    nl, oc = int(buf[0]), int(buf[1])
+    levels = []
+    for lv in range(nl):
+        ng, oq, op, oi, ol = (int(x) for x in buf[2 + 5 * lv: 7 + 5 * lv])
+        levels.append((buf[oq: oq + ng + 1], buf[op: op + ng + 1], buf[oi: oi + int(buf[op + ng])],
+                       buf[ol: ol + ng]))
+    return levels, buf[oc: oc + n], buf[oc + n: oc + 2 * n], buf[oc + 2 * n: oc + 3 * n], \
+        buf[oc + 3 * n: oc + 4 * n]
+
+
+class NativeBeamState:
+    """``BeamState`` kept in native code: the trie, its candidates and the
+    page allocator of ``page_table`` live in ``be_beam_trie`` /
+    ``be_page_pool`` (the reference's BeamState.add_root_sequence and
+    add_filtered_results rules, beam_state.py:76-209, with pages from its
+    PageTable, page_table.py:77-124).  A decode step needs two native calls:
+    ``apply_selection`` with the selection arrays (prune, expand, fork copies
+    in one device launch) and ``step_metadata`` (the cascade arrays and the
+    candidates' inputs).
+
+    Everything else -- ``candidates``, ``finished_candidates``, ``root(s)``,
+    ``sequence``, ``get_final_sequences``, the Python metadata passes -- is
+    read from a ``BeamState`` built from the native state when first asked
+    for after a change (its nodes carry the same pages, tokens and order).
+    ``add_filtered_results`` takes results for the candidates of that view,
+    in its order, as ``BeamState.add_filtered_results`` does."""
+
+    def __init__(self, beam_size: int, page_table: PageTable):
+        from . import _lib
+        self._lib = lib = _lib.load()
+        self.beam_size = beam_size
+        self.page_table = page_table
+        self._h = lib.be_trie_create(int(page_table.page_size), page_table._pool)
+        if not self._h:
+            _lib.check(_lib.BE_ERR_INVALID, "beam trie")
+        self._sizes = np.zeros(5, np.int32)
+        self._ver = ctypes.c_int64(0)
+        self._mirror: Optional[BeamState] = None
+        self._mirror_ver = -1
+        self._meta_buf = np.zeros(1 << 16, np.int32)
+        self._meta_used = ctypes.c_int64(0)
+        self._copies = np.zeros(3 * 1024, np.int32)
+        self._ncopies = ctypes.c_int32(0)
+        self._warn = ctypes.c_int32(0)
+
+    def __del__(self):
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            self._lib.be_trie_destroy(h)
+
+    # ------------------------------------------------------------ native state
+    def _read_sizes(self) -> np.ndarray:
+        self._lib.be_trie_sizes(self._h, self._sizes.ctypes.data, ctypes.byref(self._ver))
+        return self._sizes
+
+    def num_candidates(self) -> int:
+        return int(self._read_sizes()[1])
+
+    def num_finished(self) -> int:
+        return int(self._read_sizes()[2])
+
+    def candidate_arrays(self) -> Tuple[np.ndarray, np.ndarray]:
+        """Each live candidate's request id (int32) and score (float64)."""
+        n = self.num_candidates()
+        req = np.zeros(n, np.int32)
+        score = np.zeros(n, np.float64)
+        self._lib.be_trie_candidates(self._h, None, req.ctypes.data, score.ctypes.data)
+        return req, score
+
+    def add_root_sequence(self, sequence: List[int], request_id: int = 0) -> List[_PageRef]:
+        """A prompt's pages and its candidate (beam_state.py:76-98); returns
+        the created pages in creation order."""
+        from . import _lib
+        toks = np.ascontiguousarray(sequence, dtype=np.int32)
+        ps = self.page_table.page_size
+        pages = np.zeros(max(1, -(-len(toks) // ps)), np.int32)
+        _lib.check(self._lib.be_trie_add_root(self._h, toks.ctypes.data, len(toks), int(request_id),
+                                              pages.ctypes.data), "add_root_sequence")
+        return [_PageRef(int(p)) for p in pages[: -(-len(toks) // ps)]]
+
+    def apply_selection(self, parent, token, score, eos_token_id: Optional[int] = None) -> int:
+        """One step's selection in emission order (entry e: parent candidate
+        index, -1 for an unused entry; token; accumulated score): the
+        reference's prune and expand rules, with this step's fork copies issued
+        in one launch.  Returns the number of fork copies."""
+        from . import _lib
+        par = np.ascontiguousarray(parent, dtype=np.int32)
+        tok = np.ascontiguousarray(token, dtype=np.int32)
+        sc = np.ascontiguousarray(score, dtype=np.float64)
+        n = len(par)
+        if len(tok) != n or len(sc) != n:
+            raise ValueError("parent, token and score must have one entry each")
+        if self._copies.size < 3 * n:
+            self._copies = np.zeros(6 * n, np.int32)
+        rc = self._lib.be_trie_apply(self._h, par.ctypes.data, tok.ctypes.data, sc.ctypes.data, n,
+                                     -1 if eos_token_id is None else int(eos_token_id), self._copies.ctypes.data,
+                                     self._copies.size // 3, ctypes.byref(self._ncopies), ctypes.byref(self._warn))
+        _lib.check(rc, "trie update")
+        if self._warn.value:
+            logger.warning("%d freed pages were not allocated", self._warn.value)
+        nc = int(self._ncopies.value)
+        if nc:
+            pt = self.page_table
+            if pt._defer:
+                pt._pending.extend(map(tuple, self._copies[: 3 * nc].reshape(nc, 3).tolist()))
+            else:
+                pt.copy_pages(self._copies[: 3 * nc].reshape(nc, 3))
+        return nc
+
+    def add_filtered_results(self, results: List[BeamGenerateResult], eos_token_id: Optional[int] = None) -> None:
+        """``BeamState.add_filtered_results`` for results on this state's
+        ``candidates`` (beam_state.py:101-209)."""
+        index = {id(c): i for i, c in enumerate(self.candidates)}
+        par, tok, sc = [], [], []
+        for r in results:
+            i = index.get(id(r.candidate))
+            if i is None:
+                raise ValueError("a result's candidate is not a live candidate of this state")
+            for ch in r.children:
+                par.append(i)
+                tok.append(ch.token_id)
+                sc.append(ch.accumulated_score)
+        self.apply_selection(par, tok, sc, eos_token_id)
+
+    def step_metadata(self):
+        """``BeamState.step_metadata`` from the native trie: (levels, query
+        tokens, write pages, write slots, positions)."""
+        from . import _lib
+        n = self.num_candidates()
+        while True:
+            buf = self._meta_buf
+            rc = self._lib.be_trie_metadata(self._h, buf.ctypes.data, buf.size, ctypes.byref(self._meta_used))
+            if rc == _lib.BE_ERR_CAPACITY:
+                self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
+                continue
+            _lib.check(rc, "trie cascade metadata")
+            break
+        return _parse_metadata(self._meta_buf[: int(self._meta_used.value)].copy(), n)
+
+    def plan_cascade(self, wrapper, num_qo_heads: int, num_kv_heads: int, head_dim: int, q_data_type):
+        """This step's cascade metadata and ``wrapper``'s plan of it in one
+        native call (``be_trie_plan``: the same plan as ``wrapper.plan`` of
+        ``step_metadata``'s levels with ``causal=True``), the plan uploaded
+        to the wrapper's workspace.  Returns the candidates' query tokens,
+        write pages, write slots and positions."""
+        from . import _lib
+        from .attention import _Staging, _num_cus
+        if isinstance(q_data_type, str):
+            q_data_type = getattr(torch, q_data_type)
+        staging = _Staging.get(wrapper._ws.device)
+        info = _lib.BeAttnPlanInfo()
+        max_page = ctypes.c_int32(-1)
+        caps = ctypes.byref(wrapper._caps) if wrapper._caps is not None else None
+        cap = staging.buf.numel()
+        while True:
+            buf = staging.acquire(cap)
+            meta = self._meta_buf
+            rc = self._lib.be_trie_plan(self._h, num_qo_heads, num_kv_heads, head_dim, _lib.dtype_code(q_data_type),
+                                        wrapper._plan_flags(), wrapper._num_cus or _num_cus(wrapper._ws.device), caps,
+                                        meta.ctypes.data, meta.size, ctypes.byref(self._meta_used), buf.data_ptr(),
+                                        buf.numel(), ctypes.byref(info), ctypes.byref(max_page))
+            if rc == _lib.BE_ERR_CAPACITY:
+                if int(self._meta_used.value) > meta.size:
+                    self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
+                else:
+                    cap = 2 * buf.numel()
+                continue
+            _lib.check(rc, "cascade plan")
+            break
+        wrapper.num_levels = int(self._meta_buf[0])
+        wrapper._install_plan(info, buf, staging, int(max_page.value), head_dim, None, q_data_type)
+        n = self.num_candidates()
+        oc = int(self._meta_buf[1])
+        m = self._meta_buf[oc: oc + 4 * n].copy()
+        return m[:n], m[n: 2 * n], m[2 * n: 3 * n], m[3 * n:]
+
+    # ------------------------------------------------------------ Python view
+    def python_state(self) -> BeamState:
+        """The state as ``BeamState`` objects (rebuilt after every change)."""
+        sz = self._read_sizes()
+        if self._mirror is not None and self._mirror_ver == self._ver.value:
+            return self._mirror
+        nn, nc, nf, nft, ps = (int(x) for x in sz)
+        parent = np.zeros(nn, np.int32)
+        page = np.zeros(nn, np.int32)
+        ntok = np.zeros(nn, np.int32)
+        alive = np.zeros(nn, np.uint8)
+        tokens = np.zeros(nn * ps, np.int32)
+        fin_req = np.zeros(nf, np.int32)
+        fin_score = np.zeros(nf, np.float64)
+        fin_off = np.zeros(nf + 1, np.int32)
+        fin_tok = np.zeros(nft, np.int32)
+        self._lib.be_trie_export(self._h, parent.ctypes.data, page.ctypes.data, ntok.ctypes.data, alive.ctypes.data,
+                                 tokens.ctypes.data, fin_req.ctypes.data, fin_score.ctypes.data, fin_off.ctypes.data,
+                                 fin_tok.ctypes.data)
+        cnode = np.zeros(nc, np.int32)
+        creq = np.zeros(nc, np.int32)
+        cscore = np.zeros(nc, np.float64)
+        self._lib.be_trie_candidates(self._h, cnode.ctypes.data, creq.ctypes.data, cscore.ctypes.data)
+        st = BeamState(self.beam_size, self.page_table)
+        tok2 = tokens.reshape(nn, ps) if nn else tokens.reshape(0, max(ps, 1))
+        nodes: List[Optional[TrieNode]] = [None] * nn
+        for i in range(nn):
+            if not alive[i]:
+                continue
+            p = int(parent[i])
+            node = TrieNode(tok2[i, : ntok[i]].tolist(), int(page[i]), nodes[p] if p >= 0 else None)
+            node.nid = i
+            nodes[i] = node
+            if p < 0:
+                st.roots.append(node)
+        st.root = st.roots[0] if st.roots else None
+        st.candidates = [BeamCandidate(nodes[int(nd)], float(s_), False, int(r))
+                         for nd, r, s_ in zip(cnode, creq, cscore)]
+        st.finished_candidates = [BeamCandidate(None, float(fin_score[f]), True, int(fin_req[f]),
+                                                fin_tok[fin_off[f]: fin_off[f + 1]].tolist()) for f in range(nf)]
+        self._mirror, self._mirror_ver = st, self._ver.value
+        return st
+
+    @property
+    def candidates(self) -> List[BeamCandidate]:
+        return self.python_state().candidates
+
+    @property
+    def finished_candidates(self) -> List[BeamCandidate]:
+        return self.python_state().finished_candidates
+
+    def __getattr__(self, name):
+        # the rest of BeamState's interface reads the Python view
+        if name.startswith("__") or name in ("_h", "_lib", "_mirror", "_sizes", "_ver"):
+            raise AttributeError(name)
+        return getattr(self.python_state(), name)

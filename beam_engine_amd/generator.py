@@ -38,10 +38,10 @@ import numpy as np
 import torch
 
 from .attention import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAttentionWrapper
-from .beam_state import BeamGenerateResult, BeamState, BeamToken
+from .beam_state import BeamGenerateResult, BeamState, BeamToken, NativeBeamState
 from .beam_strategy import VanillaBeamSearchStrategy
 from .page_table import PageTable
-from .selection import beam_topk
+from .selection import beam_topk, decode_k
 
 
 class BatchedBeamSearch:
@@ -49,7 +49,7 @@ class BatchedBeamSearch:
                  strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
                  temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False,
                  graphs: bool = False, eos_token_id: Optional[int] = None, temperature_mode: str = "reciprocal",
-                 picker_costs: str = "mi355x"):
+                 picker_costs: str = "mi355x", step_graph: bool = True):
         if kernel_type not in ("cascade", "flat", "tree", "auto"):
             raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat', 'tree' or 'auto'.")
         self.model = model
@@ -62,7 +62,11 @@ class BatchedBeamSearch:
         self.include_self = include_self
         self.eos_token_id = eos_token_id    # a pick of this token finishes its beam (off: None)
         self.device = page_table.device
-        self.state = BeamState(beam_size, page_table, fast_metadata=True)
+        # cascade decoding keeps the trie and its pages in native code (one call
+        # per selection, one for the metadata); the other kinds read the
+        # Python trie's passes every step and keep the Python state
+        self.state = NativeBeamState(beam_size, page_table) if kernel_type == "cascade" else \
+            BeamState(beam_size, page_table, fast_metadata=True)
         self.ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
         self.cascade = MultiLevelCascadeAttentionWrapper(1, self.ws)
         self.flat = BatchDecodeWithPagedKVCacheWrapper(self.ws)
@@ -73,7 +77,15 @@ class BatchedBeamSearch:
         self._staging = torch.empty(4 * 4096, dtype=torch.int64, pin_memory=True)
         self.attn_timer = None          # optional callable(layer, fn) used by benchmarks
         self.graphs = graphs            # capture the non-attention work of a step in HIP graphs
+        # cascade with graphs: the whole step, attention included, as one graph
+        # over a fixed-layout plan (a step whose plan does not fit that layout
+        # runs the per-layer graphs with eager attention)
+        self.step_graph = step_graph
+        self.step_graphed = False       # the last step ran as one graph
         self._gd = None
+        self._fixed = None              # the fixed-layout cascade wrapper of the step graph
+        self._fixed_key = None          # its launch shape (plan fields the captured launches read)
+        self._fixed_caps = None
 
     # ---------------------------------------------------------------- prefill
     @torch.no_grad()
@@ -127,36 +139,119 @@ class BatchedBeamSearch:
         self.last_attn = w
         return w
 
+    # ---------------------------------------------------------------- whole-step graph
+    _LAUNCH_FIELDS = ("kernel", "num_wg", "stream_loop", "tail_waves", "grid_merge", "static_layout", "off_wg",
+                      "off_items", "off_seg_causal", "off_tail_items", "off_tails", "off_pages", "off_records",
+                      "off_record_slots", "part_rows_cap", "dtype", "num_qo_heads", "num_kv_heads", "head_dim",
+                      "page_size", "plan_ints", "partial_bytes")
+
+    @classmethod
+    def _launch_key(cls, info):
+        return tuple(getattr(info, f) for f in cls._LAUNCH_FIELDS)
+
+    def _fixed_plan(self, levels, n: int):
+        """This step's cascade plan in the step graph's fixed layout, or None
+        when the step graph cannot run it (the per-layer path runs instead).
+        The first call sizes the layout from this step's plan with room to
+        grow and captures the graph; a plan beyond the layout re-sizes and
+        re-captures it."""
+        m = self.model
+        cfg = m.cfg
+        args = ([l[0] for l in levels], [l[1] for l in levels], [l[2] for l in levels], [l[3] for l in levels],
+                cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pt.page_size)
+        w = self._fixed
+        if w is not None:
+            w.num_levels = len(levels)
+            try:
+                w.plan(*args, causal=True, q_data_type=m.dtype)
+            except MemoryError:
+                w = None                            # outgrew the layout: re-size below
+            else:
+                if self._launch_key(w._info) == self._fixed_key:
+                    return w
+                return None
+        # size the layout: this step's compact plan, doubled, with margins
+        probe = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
+        probe.plan(*args, causal=True, q_data_type=m.dtype)
+        pi = probe._info
+        if pi.kernel != 2 or cfg.head_dim != 128:
+            self.step_graph = False                 # the fixed layout serves the streaming kernel only
+            return None
+        pages = sum(len(l[2]) for l in levels)
+        old = self._fixed_caps
+        grow = 2 if old is None else 4
+        caps = dict(max_items=grow * pi.num_items + 1024, max_queries=n,
+                    max_pages=grow * pages + 4096, max_merge=n * cfg.num_key_value_heads,
+                    max_merge_rows=grow * pi.num_part_rows + 1024, max_zero=n, tile_rows=64,
+                    max_tails=grow * pi.num_tails + 4096)
+        if old is not None:
+            caps = {k: max(v, old[k]) for k, v in caps.items()}
+        w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
+        w.use_fixed_layout(**caps)
+        try:
+            w.plan(*args, causal=True, q_data_type=m.dtype)
+        except (MemoryError, ValueError):
+            self.step_graph = False
+            return None
+        if w._info.kernel != 2:
+            self.step_graph = False
+            return None
+        self._fixed, self._fixed_caps, self._fixed_key = w, caps, self._launch_key(w._info)
+        self._gd.capture_step(lambda l, q, kv, out: w.run(q, kv, out=out))
+        return w
+
     @torch.no_grad()
     def step(self) -> None:
         st = self.state
-        n = len(st.candidates)
+        n = st.num_candidates()
         if n == 0:                  # every beam finished
             return
         kind = self.kernel_type
         levels = None
-        if kind == "cascade":
-            # the cascade arrays and the candidates' inputs from the native builder
-            levels, qids, wp, wpos, pos = st.step_metadata()
-        else:
-            if kind == "tree":
+        w = None
+        graphed = kind == "cascade" and self.graphs and self.step_graph and hasattr(self.model, "decode") and \
+            self._graph_ready(n)
+        if graphed and self._fixed is not None and isinstance(st, NativeBeamState):
+            # metadata and the fixed-layout plan in one native call
+            cfg = self.model.cfg
+            try:
+                qids, wp, wpos, pos = st.plan_cascade(self._fixed, cfg.num_attention_heads,
+                                                      cfg.num_key_value_heads, cfg.head_dim, self.model.dtype)
+            except MemoryError:
+                pass                                # beyond the layout: _fixed_plan re-sizes it
+            else:
+                if self._launch_key(self._fixed._info) == self._fixed_key:
+                    w = self.last_attn = self._fixed
+        if w is None:
+            if kind == "cascade":
+                # the cascade arrays and the candidates' inputs from the native builder
+                levels, qids, wp, wpos, pos = st.step_metadata()
+            elif kind == "tree":
                 p = self._get_picker()
                 levels = st.tree_lists((p.edges or p.model).absorb)
             elif kind == "auto":
                 plan = self._get_picker().choose(st)
                 kind, levels = plan.kind, plan.levels
-        w = self._plan(kind, levels)
+            if graphed:
+                w = self.last_attn = self._fixed_plan(levels, n)
+        self.step_graphed = w is not None
+        if w is None:
+            w = self._plan(kind, levels)
         if self.kernel_type != "cascade":
             qids = st.query_token_ids()
             wp, wpos = st.write_locations()
             pos = st.position_ids(reuse_annotation=True)     # _plan's metadata pass just ran
-        if self._staging.numel() < 4 * n:
-            self._staging = torch.empty(8 * n, dtype=torch.int64, pin_memory=True)
-        stg = self._staging[: 4 * n].view(4, n)
-        for i, v in enumerate((qids, wp, wpos, pos)):
-            stg[i] = torch.from_numpy(v) if isinstance(v, np.ndarray) else torch.tensor(v)
-        dev = stg.to(self.device, non_blocking=True)
-        tok, wpg, wps, psn = dev[0], dev[1].to(torch.int32), dev[2].to(torch.int32), dev[3]
+        graph_run = self.step_graphed or (self.graphs and hasattr(self.model, "decode") and self._graph_ready(n))
+        if graph_run:
+            self._gd.stage_inputs(qids, pos, wp, wpos)
+        else:
+            if self._staging.numel() < 4 * n:
+                self._staging = torch.empty(8 * n, dtype=torch.int64, pin_memory=True)
+            stg = self._staging[: 4 * n].view(4, n)
+            for i, v in enumerate((qids, wp, wpos, pos)):
+                stg[i] = torch.from_numpy(v) if isinstance(v, np.ndarray) else torch.tensor(v)
+            dev = stg.to(self.device, non_blocking=True)
+            tok, wpg, wps, psn = dev[0], dev[1].to(torch.int32), dev[2].to(torch.int32), dev[3]
 
         timer = self.attn_timer
 
@@ -165,8 +260,9 @@ class BatchedBeamSearch:
                 return w.run(q, kv, out=out)
             return timer(li, lambda between: w.run(q, kv, out=out, between=between), w)
 
-        if self.graphs and hasattr(self.model, "decode") and self._graph_ready(n):
-            self._gd.load_inputs(tok, psn, wpg, wps)
+        if self.step_graphed:
+            logits = self._gd.run_step()
+        elif graph_run:
             logits = self._gd.run(attn)
         else:
             logits = self.model.decode(tok, psn, wpg, wps, self.pt, attn)
@@ -174,10 +270,14 @@ class BatchedBeamSearch:
         self.step_log.append({"n": n, "kind": kind})
 
     def prepare_graphs(self) -> None:
-        """Capture the segment graphs now for the current candidate count (the
-        first decode step would otherwise capture them)."""
-        if self.graphs and hasattr(self.model, "decode") and self.state.candidates:
-            self._graph_ready(len(self.state.candidates))
+        """Capture the segment graphs (and, for cascade, the whole-step graph)
+        now for the current candidate count (the first decode step would
+        otherwise capture them)."""
+        n = self.state.num_candidates()
+        if self.graphs and hasattr(self.model, "decode") and n:
+            self._graph_ready(n)
+            if self.kernel_type == "cascade" and self.step_graph and self._fixed is None:
+                self._fixed_plan(self.state.step_metadata()[0], n)    # capture the whole-step graph too
 
     def _graph_ready(self, n: int) -> bool:
         """Capture the segment graphs once the candidate count is known (it
@@ -193,6 +293,19 @@ class BatchedBeamSearch:
         # the step's KV appends (and the previous step's fork copies) report
         # out-of-pool entries at the selection's synchronisation
         self.pt.stage_errors()
+        if isinstance(st, NativeBeamState) and type(self.strategy) is VanillaBeamSearchStrategy and \
+                "select_batched" not in vars(self.strategy):
+            # the selection arrays go straight to the native trie (no per-child objects)
+            req, score = st.candidate_arrays()
+            cut = np.flatnonzero(np.diff(req)) + 1
+            rows = np.diff(np.concatenate([[0], cut, [len(req)]])).tolist()
+            b = st.beam_size
+            _, _, (par, tok, sc) = beam_topk(logits, decode_k(b, logits.shape[-1]), torch.from_numpy(score), b,
+                                             self.temperature, request_rows=rows, to_host=True,
+                                             temperature_mode=self.temperature_mode)
+            self.pt.raise_staged_errors()
+            st.apply_selection(par.numpy(), tok.numpy(), sc.numpy(), self.eos_token_id)
+            return
         results = self.strategy.select_batched(st, logits, self.temperature, self.temperature_mode)
         self.pt.raise_staged_errors()
         st.add_filtered_results(results, self.eos_token_id)
@@ -206,7 +319,14 @@ class BatchedBeamSearch:
     def generate(self, prompts: Sequence[Sequence[int]], steps: int):
         self.prefill(prompts)
         for _ in range(steps):
-            if not self.state.candidates or self.strategy.should_stop(self.state, 1 << 30, 0):
+            st = self.state
+            if isinstance(st, NativeBeamState) and type(self.strategy) is VanillaBeamSearchStrategy:
+                # VanillaBeamSearchStrategy.should_stop without building the
+                # Python view: no live beam, or early stopping with beam_size
+                # finished ones (live beams are never finished)
+                if st.num_candidates() == 0 or (self.strategy.early_stopping and st.num_finished() >= st.beam_size):
+                    break
+            elif not st.candidates or self.strategy.should_stop(st, 1 << 30, 0):
                 break
             self.step()
         return self.final_sequences()

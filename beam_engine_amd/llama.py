@@ -198,22 +198,31 @@ class GraphedDecoder:
     of the current step, into a fixed output buffer.  Inputs (token ids,
     positions, write pages / slots) are copied into fixed device buffers
     before the replays; the graphs share one memory pool and are replayed in
-    capture order.
+    capture order.  ``capture_step`` also records the whole step, every
+    layer's attention included, as one graph for plans of a fixed layout.
     """
 
     def __init__(self, model: LlamaDecoder, page_table, n: int):
         cfg = model.cfg
         self.model, self.pt, self.n = model, page_table, n
         dev = model.device
-        self.tok = torch.zeros(n, dtype=torch.long, device=dev)
-        self.pos = torch.zeros(n, dtype=torch.long, device=dev)
-        self.wpg = torch.zeros(n, dtype=torch.int32, device=dev)
-        self.wps = torch.zeros(n, dtype=torch.int32, device=dev)
+        # inputs: token ids and positions (int64), write pages and slots (int32),
+        # each pair one device buffer filled from pinned staging by one copy
+        self._in64 = torch.zeros((2, n), dtype=torch.long, device=dev)
+        self._in32 = torch.zeros((2, n), dtype=torch.int32, device=dev)
+        self.tok, self.pos = self._in64[0], self._in64[1]
+        self.wpg, self.wps = self._in32[0], self._in32[1]
+        pin = dev.type == "cuda"
+        self._h64 = torch.zeros((2, n), dtype=torch.long, pin_memory=pin)
+        self._h32 = torch.zeros((2, n), dtype=torch.int32, pin_memory=pin)
         self.o = torch.zeros((n, cfg.num_attention_heads, cfg.head_dim), dtype=model.dtype, device=dev)
         self.graphs = []
         self.q = []
         self.logits = None
         self._pool = None
+        self.step_graph = None          # the whole step with its attention (capture_step)
+        self.step_q: List[torch.Tensor] = []
+        self.step_logits = None
         # page writes of the capture run go to a reserved page no candidate owns
         self._scratch_page = page_table.reserve_block(page_table.max_num_pages - 1)
 
@@ -269,6 +278,52 @@ class GraphedDecoder:
             if gc_on:
                 gc.enable()
         torch.cuda.synchronize()
+
+    @torch.no_grad()
+    def capture_step(self, attn_run: Callable) -> None:
+        """One graph of the whole step: every segment and, between them, each
+        layer's attention launched by ``attn_run(layer, q, kv_layer, out)`` --
+        the launch of a fixed-layout plan (same device plan address and launch
+        sizes for every step; the plan's contents are rewritten before each
+        replay).  Needs ``capture`` first (its warm-up and memory pool)."""
+        L = self.model.cfg.num_hidden_layers
+        self.step_graph, self.step_q, self.step_logits = None, [], None
+        gc_on = gc.isenabled()
+        gc.collect()
+        gc.disable()
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self._pool):
+                x = None
+                for l in range(L + 1):
+                    x, q, logits = self._segment(l, x)
+                    if q is not None:
+                        attn_run(l, q, self.pt.kv_cache_at_layer[l], self.o)
+                        self.step_q.append(q)
+            self.step_graph = g
+            self.step_logits = logits
+        finally:
+            if gc_on:
+                gc.enable()
+        torch.cuda.synchronize()
+
+    def run_step(self) -> torch.Tensor:
+        """Replay the whole-step graph (inputs and the attention plan loaded)."""
+        self.step_graph.replay()
+        return self.step_logits
+
+    def stage_inputs(self, tok, pos, wpg, wps) -> None:
+        """Host arrays of the step's inputs -> the graphs' input buffers (two
+        copies from pinned staging; the staging is rewritten only after the
+        step's selection has synchronised)."""
+        a = self._h64.numpy()
+        a[0] = tok
+        a[1] = pos
+        b = self._h32.numpy()
+        b[0] = wpg
+        b[1] = wps
+        self._in64.copy_(self._h64, non_blocking=True)
+        self._in32.copy_(self._h32, non_blocking=True)
 
     def load_inputs(self, tok, pos, wpg, wps) -> None:
         self.tok.copy_(tok, non_blocking=True)

@@ -6,7 +6,10 @@ Same constructor, attributes and methods.  MI355X-first differences:
   ``[L, P, 2, page_size, Hkv, D]``; ``kv_cache_at_layer[l]`` is the
   contiguous per-layer view with the reference's layout (page_table.py:62-72).
   A fork copy of every layer is then one kernel launch (``be_page_copy``).
-* The FIFO free list is a deque (O(1) ``pop(0)``) with the same order.
+* The allocator is native (``be_page_pool``): the same FIFO free list order,
+  O(1) allocate and free, shared with the native beam trie so that a decode
+  step's page bookkeeping needs no Python.  ``free_pages`` and
+  ``allocated_pages`` are read-only snapshots of it.
 * Pages carry a reference count: ``allocate_block`` sets it to 1,
   ``share_block`` adds a holder, ``free_block`` drops one and returns the page
   to the free list at zero.  With one holder per page (the reference's trie)
@@ -21,6 +24,7 @@ Same constructor, attributes and methods.  MI355X-first differences:
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import logging
 from collections import deque
 from typing import List, Optional, Tuple
@@ -54,10 +58,14 @@ class PageTable:
         self.device = torch.device(device) if device is not None else torch.device("cuda")
         self.store_dtype = store_dtype
 
-        self.free_pages = deque(range(max_num_pages))
-        self.allocated_pages = set()
-        self._refs = {}
+        lib = _lib.load()
+        self._lib = lib
+        self._pool = lib.be_pages_create(int(max_num_pages))
+        if not self._pool:
+            _lib.check(_lib.BE_ERR_INVALID, "page pool")
+        self._page_out = ctypes.c_int32(0)
         self._pending: List[Tuple[int, int, int]] = []
+        self._copy_host = self._copy_dev = self._copy_ev = None     # fork-copy lists' staging
         self._defer = 0
 
         self.kv_pool = torch.zeros((layer_num, max_num_pages, 2, page_size, head_num, head_dim),
@@ -71,50 +79,58 @@ class PageTable:
         logger.info("Initialized PageTable: %d layers, %d pages of size %d", layer_num, max_num_pages, page_size)
 
     # ------------------------------------------------------------ allocator
+    def __del__(self):
+        pool, self._pool = getattr(self, "_pool", None), None
+        if pool:
+            self._lib.be_pages_destroy(pool)
+
+    @property
+    def free_pages(self) -> deque:
+        """The free list, oldest page first (a snapshot)."""
+        n = self._lib.be_pages_num_free(self._pool)
+        out = np.zeros(max(n, 1), np.int32)
+        self._lib.be_pages_free_list(self._pool, out.ctypes.data, n)
+        return deque(out[:n].tolist())
+
+    @property
+    def allocated_pages(self) -> set:
+        """Pages with at least one holder (a snapshot)."""
+        free = set(self.free_pages)
+        return {p for p in range(self.max_num_pages) if p not in free}
+
     def allocate_block(self) -> int:
         """Pop the oldest free page (page_table.py:77-94)."""
-        if not self.free_pages:
+        rc = self._lib.be_pages_allocate(self._pool, ctypes.byref(self._page_out))
+        if rc == _lib.BE_ERR_CAPACITY:
             raise MemoryError("No free pages available")
-        page = self.free_pages.popleft()
-        self.allocated_pages.add(page)
-        self._refs[page] = 1
-        return page
+        _lib.check(rc, "allocate_block")
+        return int(self._page_out.value)
 
     def share_block(self, page_idx: int) -> int:
         """Add a holder to an allocated page; returns the new count."""
-        if page_idx not in self.allocated_pages:
-            raise ValueError(f"Page {page_idx} is not allocated")
-        self._refs[page_idx] += 1
-        return self._refs[page_idx]
+        cnt = ctypes.c_int32(0)
+        _lib.check(self._lib.be_pages_share(self._pool, int(page_idx), ctypes.byref(cnt)), "share_block")
+        return int(cnt.value)
 
     def ref_count(self, page_idx: int) -> int:
-        return self._refs.get(page_idx, 0)
+        return int(self._lib.be_pages_ref_count(self._pool, int(page_idx)))
 
     def free_block(self, page_idx: int) -> None:
         """Drop one holder; at zero the page goes to the back of the free list
         (page_table.py:110-124).  Freeing an unallocated page only warns."""
-        if page_idx not in self.allocated_pages:
+        state = ctypes.c_int32(0)
+        _lib.check(self._lib.be_pages_release(self._pool, int(page_idx), ctypes.byref(state)), "free_block")
+        if state.value < 0:
             logger.warning("Page %s is not allocated", page_idx)
-            return
-        self._refs[page_idx] -= 1
-        if self._refs[page_idx] > 0:
-            return
-        del self._refs[page_idx]
-        self.allocated_pages.remove(page_idx)
-        self.free_pages.append(page_idx)
 
     def reserve_block(self, page_idx: int) -> int:
         """Take one specific free page out of the free list (e.g. the last one,
         as a scratch slot) without changing the FIFO order of the others."""
-        if page_idx in self.allocated_pages:
-            raise ValueError(f"Page {page_idx} is already allocated")
-        self.free_pages.remove(page_idx)
-        self.allocated_pages.add(page_idx)
-        self._refs[page_idx] = 1
+        _lib.check(self._lib.be_pages_reserve(self._pool, int(page_idx)), "reserve_block")
         return page_idx
 
     def num_free_pages(self) -> int:
-        return len(self.free_pages)
+        return int(self._lib.be_pages_num_free(self._pool))
 
     # ------------------------------------------------------------ device errors
     def stage_errors(self) -> None:
@@ -171,8 +187,31 @@ class PageTable:
         if not self._pending:
             return 0
         todo, self._pending = self._pending, []
-        arr = torch.tensor(np.asarray(todo, dtype=np.int32).T.copy(), dtype=torch.int32)
-        dev = arr.to(self.device, non_blocking=False)
+        return self.copy_pages(np.asarray(todo, dtype=np.int32))
+
+    def copy_pages(self, copies: np.ndarray) -> int:
+        """Fork copies ``[n, 3]`` (source page, new page, tokens) in one
+        be_page_copy launch, now."""
+        todo = copies
+        n = len(todo)
+        if n == 0:
+            return 0
+        if self.device.type == "cuda":
+            # pinned staging, reused once the previous flush's copy has run
+            if self._copy_host is None or self._copy_host.shape[1] < n:
+                cap = max(256, 2 * n)
+                self._copy_host = torch.empty((3, cap), dtype=torch.int32, pin_memory=True)
+                self._copy_dev = torch.empty((3, cap), dtype=torch.int32, device=self.device)
+                self._copy_ev = None
+            if self._copy_ev is not None:
+                self._copy_ev.synchronize()
+            self._copy_host.numpy()[:, :n] = np.asarray(todo, dtype=np.int32).T
+            dev = self._copy_dev[:, :n]
+            dev.copy_(self._copy_host[:, :n], non_blocking=True)
+            self._copy_ev = torch.cuda.Event()
+            self._copy_ev.record()
+        else:
+            dev = torch.from_numpy(np.ascontiguousarray(np.asarray(todo, dtype=np.int32).T))
         lib = _lib.load()
         rc = lib.be_page_copy(self.kv_pool.data_ptr(), self.layer_stride_bytes, self.layer_num,
                               _lib.dtype_code(self.store_dtype), self.max_num_pages, self.page_size,
@@ -190,7 +229,7 @@ class PageTable:
             f"Cannot fit {key.shape[0]} tokens at index {index} in page size {self.page_size}"
         if layer >= self.layer_num:
             raise ValueError(f"Layer {layer} out of range (max: {self.layer_num - 1})")
-        if page_idx not in self.allocated_pages:
+        if self.ref_count(page_idx) == 0:
             raise ValueError(f"Page {page_idx} is not allocated")
         if index > self.page_size:
             raise ValueError(f"Index {index} exceeds page size {self.page_size}")

@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
+    ap.add_argument("--row-blocks", default="auto", choices=["auto", "on", "off"],
+                    help="attention: the row-block kernel (one launch, no partials) forced on or off")
     ap.add_argument("--selection", default="vanilla", choices=["vanilla", "diverse"],
                     help="e2e: beam selection (vanilla, or diverse beam search with 4 groups)")
     ap.add_argument("--layers", type=int, default=32)
@@ -85,6 +87,7 @@ def attention_workload(args):
     if args.strategy == "cascade":
         w = MultiLevelCascadeAttentionWrapper(len(wl.levels[0]), ws)
         w._fused_merge = args.fused_merge
+        w._rows = {"auto": None, "on": True, "off": False}[args.row_blocks]
         w.plan(*wl.levels, wl.hq, wl.hkv, wl.d, wl.page, q_data_type=dtype)
         alg_kv = w.stats.kv_bytes
     else:

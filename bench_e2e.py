@@ -15,9 +15,11 @@ is also timed (``generation_tokens_per_s``).  The flat strategy runs the same
 prompts through the same model in the same process, for the ratio.
 
 In every timed step one decode-attention launch -- that of layer (step mod
-32) -- is bracketed by two HIP events on the launch stream; the roofline
-reports the plan's algorithmic bytes against the mean duration of both
-kernels of a launch together.
+32) -- is bracketed by two HIP events on the launch stream: inside the step
+when its attention runs eagerly, or, when the step ran as one HIP graph,
+launched again right after the step (outside its timing) with the step's
+plan, queries and cache.  The roofline reports the plan's algorithmic bytes
+against the mean duration of both kernels of a launch together.
 
 The model's GEMMs are library calls outside the hot path; their library
 solutions come from the TunableOp results file ``bench_gemms.csv`` (timed
@@ -112,9 +114,7 @@ class AttnTimer:
         self.layers = layers
         self.layer = -1        # layer to time in the current step (-1: none)
 
-    def __call__(self, layer, run_fn, wrapper):
-        if layer != self.layer:
-            return run_fn(None)
+    def _bytes(self, wrapper):
         st = wrapper.stats
         self.kernels.add(st.kernel)
         if self.kind == "flat":
@@ -123,12 +123,37 @@ class AttnTimer:
             kv = int(round(st.flops / (4.0 * self.d * hq))) * self.hkv * self.d * self.es * 2
         else:
             kv = st.kv_bytes
+        return kv + st.qo_bytes, st.flops
+
+    def __call__(self, layer, run_fn, wrapper):
+        if layer != self.layer:
+            return run_fn(None)
+        byts, flops = self._bytes(wrapper)
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         out = run_fn(None)
         e.record()
-        self.records.append((s, e, kv + st.qo_bytes, st.flops))
+        self.records.append((s, e, byts, flops))
         return out
+
+    def after_step_graph(self, gen, layer):
+        """A step that ran as one graph: launch that layer's attention again,
+        right after the step and outside its timing, with the step's plan,
+        queries and cache (the same launch), into a scratch output."""
+        w = gen.last_attn
+        q = gen._gd.step_q[layer]
+        if getattr(self, "_scratch", None) is None or self._scratch.shape != q.shape:
+            self._scratch = torch.empty_like(q)
+        byts, flops = self._bytes(w)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # the device idles after the step: a short spin keeps it busy while the
+        # host enqueues the events and the launch, so the bracket holds the two
+        # kernels and not the host's launch latency
+        torch.cuda._sleep(200000)
+        s.record()
+        w.run(q, gen.pt.kv_cache_at_layer[layer], out=self._scratch)
+        e.record()
+        self.records.append((s, e, byts, flops))
 
     def summary(self):
         us, byts, flops = [], 0, 0.0
@@ -184,6 +209,8 @@ def generate(model, cfg, prompts, kind: str, timed, graphs: bool = True, selecti
             gen.step()
             torch.cuda.synchronize()
             per_step.append(time.perf_counter() - t0)
+            if gen.step_graphed:
+                timer.after_step_graph(gen, i % cfg.num_hidden_layers)
             timer.layer = -1
         else:
             gen.step()

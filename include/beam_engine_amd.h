@@ -29,6 +29,9 @@
  *                     (src/beam_engine/beam_strategy.py:173-312)
  *   be_trie_cascade   BeamState.get_cascade_input (src/beam_engine/beam_state.py:211-412) and the
  *                     per-step write locations / position ids (src/beam_engine/beam.py:180-221)
+ *   be_pages_*        PageTable.allocate_block / free_block (src/beam_engine/page_table.py:77-124)
+ *   be_trie_*         BeamState.add_root_sequence / add_filtered_results
+ *                     (src/beam_engine/beam_state.py:76-209)
  */
 #ifndef BEAM_ENGINE_AMD_H
 #define BEAM_ENGINE_AMD_H
@@ -255,6 +258,68 @@ int be_diverse_select(const float* row_vals, const int32_t* row_idx, int n_rows,
 int be_trie_cascade(const int32_t* parent, const int32_t* page, const int32_t* ntok, const int32_t* last_tok,
                     const uint8_t* alive, int num_nodes, const int32_t* leaves, int num_cands, int32_t* out,
                     int64_t out_capacity, int64_t* out_used);
+
+/* ------------------------------------------------------------------ page pool and beam trie (host only)
+ * be_page_pool replaces the reference PageTable's allocator
+ * (src/beam_engine/page_table.py:77-124): a FIFO free list (oldest free page
+ * first, freed pages to the back) with a holder count per page.
+ * be_pages_allocate fails with BE_ERR_CAPACITY ("No free pages available",
+ * the reference's MemoryError); be_pages_release drops one holder and puts
+ * the page back at zero, *state = 1 (freed), 0 (still held) or -1 (was not
+ * allocated: the reference only warns); be_pages_share adds a holder;
+ * be_pages_reserve takes one given free page out of the list; be_pages_free_list
+ * copies up to cap free pages in list order and returns the free count. */
+typedef struct be_page_pool be_page_pool;
+be_page_pool* be_pages_create(int num_pages);
+void be_pages_destroy(be_page_pool* pool);
+int be_pages_allocate(be_page_pool* pool, int32_t* page);
+int be_pages_share(be_page_pool* pool, int page, int32_t* count);
+int be_pages_release(be_page_pool* pool, int page, int32_t* state);
+int be_pages_reserve(be_page_pool* pool, int page);
+int be_pages_num_free(const be_page_pool* pool);
+int be_pages_ref_count(const be_page_pool* pool, int page);
+int be_pages_free_list(const be_page_pool* pool, int32_t* out, int cap);
+
+/* be_beam_trie replaces the reference BeamState's trie and its update
+ * (src/beam_engine/beam_state.py:76-209, add_root_sequence and
+ * add_filtered_results), with pages from a be_page_pool.
+ * be_trie_add_root: a prompt's pages (one per page_size tokens, written to
+ * pages_out) and its candidate (score 0).
+ * be_trie_apply: one step's selection in emission order -- entry e gives
+ * the parent candidate (-1: unused entry), the token and the accumulated
+ * score; a candidate's children are its entries in order.  Childless
+ * candidates are pruned first (leaf upward, freeing pages), then candidates
+ * are expanded in order by the reference's fork rules; the fork copies
+ * (source page, new page, tokens to copy) go to copies (3 words each, room
+ * for n_entries needed), *n_copies their count.  eos_token >= 0 finishes a
+ * beam on that token (kept with its whole sequence) instead of expanding it.
+ * *n_release_warnings counts frees of pages the pool did not hold.
+ * be_trie_sizes: [nodes, candidates, finished, finished tokens, page_size] and
+ * the state's version (bumped by every change).  be_trie_candidates /
+ * be_trie_export copy the candidates and the node table (parent, page,
+ * token count, alive, page_size tokens per node) and the finished beams
+ * (request, score, token offsets, tokens).  be_trie_metadata is
+ * be_trie_cascade over the trie. */
+typedef struct be_beam_trie be_beam_trie;
+be_beam_trie* be_trie_create(int page_size, be_page_pool* pool);
+void be_trie_destroy(be_beam_trie* trie);
+int be_trie_add_root(be_beam_trie* trie, const int32_t* tokens, int n, int request_id, int32_t* pages_out);
+int be_trie_apply(be_beam_trie* trie, const int32_t* sel_parent, const int32_t* sel_token, const double* sel_score,
+                  int n_entries, int eos_token, int32_t* copies, int copies_cap, int* n_copies,
+                  int* n_release_warnings);
+int be_trie_sizes(const be_beam_trie* trie, int32_t* out5, int64_t* version);
+int be_trie_candidates(const be_beam_trie* trie, int32_t* node, int32_t* request, double* score);
+int be_trie_export(const be_beam_trie* trie, int32_t* parent, int32_t* page, int32_t* ntok, uint8_t* alive,
+                   int32_t* tokens, int32_t* fin_req, double* fin_score, int32_t* fin_off, int32_t* fin_tokens);
+int be_trie_metadata(const be_beam_trie* trie, int32_t* out, int64_t out_capacity, int64_t* out_used);
+/* be_trie_plan: be_trie_metadata into meta, then be_attn_plan of its levels
+ * (the cascade wrapper's plan of the step: causal mask on the last level when
+ * a group there holds more than one query; num_pages from the largest page
+ * id named, returned in *max_page) -- a cascade decode step's host work in
+ * one call.  BE_ERR_CAPACITY for meta or host_plan as the two calls give it. */
+int be_trie_plan(const be_beam_trie* trie, int num_qo_heads, int num_kv_heads, int head_dim, int dtype, int flags,
+                 int num_cus, const be_plan_caps* caps, int32_t* meta, int64_t meta_capacity, int64_t* meta_used,
+                 int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info, int32_t* max_page);
 
 /* be_attn_run: o[i, h] = softmax(sm_scale * q[i, h] . K^T) V over query i's
  * groups on every level, merged by log-sum-exp; query head h reads KV head
