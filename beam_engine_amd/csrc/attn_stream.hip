@@ -40,10 +40,14 @@
 //    domain, fp32 accumulation, natural-log lse at the boundary.
 //  * A (query, KV head) covered by one segment is written as the final
 //    output; otherwise each segment writes a partial (o, lse) slot and a
-//    merge record combines the slots of the (query, KV head).  Outputs and
-//    slots are written with non-temporal stores: nothing in the launch reads
-//    them back, and the end-of-kernel write-back before the merge kernel then
-//    has little left to do (the gap between the two kernels halved on MI355X).
+//    merge record combines the slots of the (query, KV head).  A slot holds
+//    the normalised o in the KV's 16-bit type (the type FlashInfer's cascade
+//    merges its per-level outputs in) and the lse in fp32: half the bytes of
+//    fp32 slots, which the launch writes and reads back once each.  Outputs
+//    and slots are written with non-temporal stores: nothing in the launch
+//    reads them back, and the end-of-kernel write-back before the merge
+//    kernel then has little left to do (the gap between the two kernels
+//    halved on MI355X).
 
 #include <math.h>
 
@@ -104,7 +108,7 @@ struct StreamArgs {
   void* out;
   int64_t o_sn, o_sh;
   float* out_lse;
-  float* part_o;      // [slots, g, D]
+  void* part_o;       // [slots, g, D] in the KV's 16-bit type
   float* part_lse;    // [slots, g]
   const int4* wg;     // per workgroup: first segment (item), segments (items), tiles, class
   const StreamSeg* segs;
@@ -117,7 +121,7 @@ struct StreamArgs {
 };
 
 struct TailMergeArgs {
-  const float* part_o;
+  const void* part_o;        // [slots, g, D] in the KV's 16-bit type
   const float* part_lse;
   const int32_t* recs;       // [n][8]: query, KV head, first rec_slots entry, slots, first tail, tails, 0, 0
   const int32_t* rec_slots;
@@ -462,10 +466,13 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
             if (mt0 == 0 && lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
           } else {
             const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
-            float* op = a.part_o + slot * kD + d0;
+            T* op = reinterpret_cast<T*>(a.part_o) + slot * kD + d0;
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt)
-              if (mt < nmt) __builtin_nontemporal_store(o_acc[mt] * inv, reinterpret_cast<v4f*>(op + mt * 16));
+              if (mt < nmt)
+                __builtin_nontemporal_store(
+                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
+                    reinterpret_cast<v4s*>(op + mt * 16));
             if (mt0 == 0 && lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
           }
         }
@@ -576,10 +583,12 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
               if (lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
             } else {
               const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
-              float* op = a.part_o + slot * kD + d0;
+              T* op = reinterpret_cast<T*>(a.part_o) + slot * kD + d0;
 #pragma unroll
               for (int mt = 0; mt < 8; ++mt)
-                __builtin_nontemporal_store(o2[r][mt] * inv, reinterpret_cast<v4f*>(op + mt * 16));
+                __builtin_nontemporal_store(pack4<T>(o2[r][mt][0] * inv, o2[r][mt][1] * inv, o2[r][mt][2] * inv,
+                                                     o2[r][mt][3] * inv),
+                                            reinterpret_cast<v4s*>(op + mt * 16));
               if (lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
             }
           }
@@ -850,10 +859,13 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
             if (mt0 == 0 && lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
           } else {
             const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
-            float* op = a.part_o + slot * kD + d0;
+            T* op = reinterpret_cast<T*>(a.part_o) + slot * kD + d0;
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt)
-              if (mt < nmt) __builtin_nontemporal_store(o_acc[mt] * inv, reinterpret_cast<v4f*>(op + mt * 16));
+              if (mt < nmt)
+                __builtin_nontemporal_store(
+                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
+                    reinterpret_cast<v4s*>(op + mt * 16));
             if (mt0 == 0 && lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
           }
         }
@@ -899,9 +911,12 @@ __device__ __forceinline__ void tail_item(const StreamArgs& a, unsigned char* ar
   if (lc < g) {
     const float inv = 1.f / l;
     const int64_t sl = (int64_t)slot * g + lc;
-    float* op = a.part_o + sl * kD + 4 * lg;
+    T* op = reinterpret_cast<T*>(a.part_o) + sl * kD + 4 * lg;
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) __builtin_nontemporal_store(o_acc[mt] * inv, reinterpret_cast<v4f*>(op + 16 * mt));
+    for (int mt = 0; mt < 8; ++mt)
+      __builtin_nontemporal_store(
+          pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
+          reinterpret_cast<v4s*>(op + 16 * mt));
     if (lg == 0) __builtin_nontemporal_store((m_run + log2f(l)) * 0.69314718055994531f, a.part_lse + sl);
   }
 }
@@ -963,7 +978,7 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
 // Each wave keeps the K/V rows of its next two chunks in flight.  A record
 // with neither tail chunks nor slots writes o = 0 and lse = -inf.
 template <typename T, int WPR>
-__global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
+__global__ __launch_bounds__(256, 2) void tail_merge_kernel(TailMergeArgs m) {
   constexpr int RPB = 4 / WPR;                 // records per workgroup
   constexpr int RT = 64 * WPR;                 // threads per record
   constexpr int C4 = kD / 4;
@@ -974,22 +989,27 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
   const int rb = wv / WPR, sw = wv - rb * WPR;  // record of the workgroup, wave within the record
   const int rtid = tid - rb * RT;
   const int e = blockIdx.x * RPB + rb;
-  const int live = m.live ? *m.live : m.n_recs;
-  if (WPR == 4 && e >= live) return;           // (one record per workgroup: uniform)
-  const bool act = e < live;
+  // the record and the live count (fixed layouts) load together: a record
+  // within the launch's capacity is in bounds whether or not it is live
   int qi = 0, h = 0, s0 = 0, n = 0, t0 = 0, nt = 0;
-  if (act) {
+  if (e < m.n_recs) {
     const int32_t* rp = m.recs + (int64_t)e * kRecWords;
     qi = rfl(rp[0]); h = rfl(rp[1]); s0 = rfl(rp[2]); n = rfl(rp[3]); t0 = rfl(rp[4]);
     nt = min(rfl(rp[5]), kTailChunks);
   }
+  const int live = m.live ? *m.live : m.n_recs;
+  if (WPR == 4 && e >= live) return;           // (one record per workgroup: uniform)
+  const bool act = e < live;
+  if (!act) n = nt = 0;
   const int g = m.g;
   const int32_t* slots = m.rec_slots + s0;
   // every wave holds all tail entries and the first 64 slot ids, lane k entry k
   const int2 ent = lane < nt ? m.tails[t0 + lane] : int2{0, 0};
   const int sid = lane < n ? slots[lane] : -1;
 
-  auto load_batch = [&](int hh, int d4, int k0, int (&sl)[8], float (&lv)[8], v4f (&ov)[8]) {
+  // a batch of 8 slots of one (head, 4 columns) entry: o stays in its 16-bit
+  // form until folded
+  auto load_batch = [&](int hh, int d4, int k0, int (&sl)[8], float (&lv)[8], v4s (&ov)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       sl[j] = (k0 + j >= n) ? -1 : (k0 + j < 64) ? __builtin_amdgcn_readlane(sid, k0 + j) : slots[k0 + j];
@@ -998,13 +1018,22 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
       if (sl[j] >= 0) {
         const int64_t s = (int64_t)sl[j] * g + hh;
         lv[j] = m.part_lse[s];
-        ov[j] = *reinterpret_cast<const v4f*>(m.part_o + s * kD + 4 * d4);
+        ov[j] = *reinterpret_cast<const v4s*>(reinterpret_cast<const T*>(m.part_o) + s * kD + 4 * d4);
       } else {
         lv[j] = -INFINITY;
-        ov[j] = v4f{0.f, 0.f, 0.f, 0.f};
+        ov[j] = v4s{0, 0, 0, 0};
       }
     }
   };
+  // this thread's first entry (its only one for g <= 4 with two or more waves
+  // per record): its first slot batch loads now, beside the tail pass's K/V
+  // loads, instead of after it
+  const int ne = g * (kD / 4);
+  const int ca = rtid;
+  int sla[8];
+  float lva[8];
+  v4s ova[8];
+  if (ca < ne) load_batch(ca / (kD / 4), ca % (kD / 4), 0, sla, lva, ova);
 
   float* part = reinterpret_cast<float*>(&tl_lds[0][0]);       // after the tail pass: [4][16][kD]
   float m_run = -INFINITY, l_run = 0.f;
@@ -1037,7 +1066,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
   // one (head, 4 columns) entry: the waves' tail states from LDS, then the
   // partial slots in batches of 8 (the first batch loaded by the caller), then
   // the normalised output and lse
-  auto merge_entry = [&](int c, float (&lv0)[8], v4f (&ov0)[8]) {
+  auto merge_entry = [&](int c, float (&lv0)[8], v4s (&ov0)[8]) {
     const int hh = c / C4, d4 = c - hh * C4;
     const int head = h * g + hh;
     float M = -INFINITY, z = 0.f;
@@ -1063,7 +1092,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
       z = 1.f;
       acc = at * (1.f / zt);
     }
-    auto fold = [&](const float (&lv)[8], const v4f (&ov)[8]) {
+    auto fold = [&](const float (&lv)[8], const v4s (&ov)[8]) {
       float mx = M;
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lv[j]);
@@ -1075,7 +1104,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
         for (int j = 0; j < 8; ++j) {
           const float wgt = (lv[j] == -INFINITY) ? 0.f : expf(lv[j] - mx);
           z += wgt;
-          acc += ov[j] * wgt;
+          acc += unpack4<T>(ov[j]) * wgt;
         }
         M = mx;
       }
@@ -1084,7 +1113,7 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
     for (int k0 = 8; k0 < n; k0 += 8) {
       int sl[8];
       float lv[8];
-      v4f ov[8];
+      v4s ov[8];
       load_batch(hh, d4, k0, sl, lv, ov);
       fold(lv, ov);
     }
@@ -1094,14 +1123,15 @@ __global__ __launch_bounds__(256) void tail_merge_kernel(TailMergeArgs m) {
     if (d4 == 0 && m.out_lse)
       __builtin_nontemporal_store((z > 0.f) ? M + logf(z) : -INFINITY, m.out_lse + (int64_t)qi * m.hq + head);
   };
-  // a thread's entries two at a time: both first slot batches are loaded
-  // before either is folded, so their latencies overlap
-  const int ne = g * C4;
-  for (int c = rtid; c < ne; c += 2 * RT) {
+  // the first entry from its prefetched batch, then the others two at a time:
+  // both first slot batches are loaded before either is folded, so their
+  // latencies overlap
+  if (ca < ne) merge_entry(ca, lva, ova);
+  for (int c = rtid + RT; c < ne; c += 2 * RT) {
     const int c1 = c + RT;
     int sl0[8], sl1[8];
     float lv0[8], lv1[8];
-    v4f ov0[8], ov1[8];
+    v4s ov0[8], ov1[8];
     load_batch(c / C4, c % C4, 0, sl0, lv0, ov0);
     if (c1 < ne) load_batch(c1 / C4, c1 % C4, 0, sl1, lv1, ov1);
     merge_entry(c, lv0, ov0);
@@ -1469,7 +1499,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   info->grid_items = W;
   info->grid_merge = (int32_t)c_recs;
   info->part_rows_cap = (int32_t)c_slots;
-  info->counter_offset = ceil_div(c_slots * g * (kD + 1) * 4, 256) * 256;
+  info->counter_offset = ceil_div(c_slots * g * (kD * 2 + 4), 256) * 256;   // 16-bit o, fp32 lse
   info->counter_bytes = 0;
   info->partial_bytes = info->counter_offset;
   info->num_wg = W;
@@ -1517,8 +1547,10 @@ int stream_run(const be_attn_plan_info* info, const int32_t* plan, void* partial
              "q must be 16-byte aligned with strides that are multiples of 8 elements");
   BE_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7) == 0 && o_sn % 4 == 0 && o_sh % 4 == 0,
              "out must be 8-byte aligned with strides that are multiples of 4 elements");
-  float* part_o = reinterpret_cast<float*>(partials);
-  float* part_lse = part_o ? part_o + (int64_t)info->part_rows_cap * g * kD : nullptr;
+  void* part_o = partials;
+  float* part_lse = partials ? reinterpret_cast<float*>(static_cast<char*>(partials) +
+                                                        (int64_t)info->part_rows_cap * g * kD * 2)
+                             : nullptr;
   const int ps = info->page_size;
   if ((phases & BE_RUN_ATTENTION) && info->num_wg > 0 &&
       (info->static_layout || info->num_items > 0 || info->num_tail_items > 0)) {

@@ -98,6 +98,19 @@ template <typename T> __device__ __forceinline__ v4s pack4(float a, float b, flo
   return __builtin_bit_cast(v4s, (u2){pack2<T>(a, b), pack2<T>(c, d)});
 }
 
+// Four 16-bit values -> four floats (exact).
+template <typename T> __device__ __forceinline__ v4f unpack4(v4s x);
+template <> __device__ __forceinline__ v4f unpack4<bf16_t>(v4s x) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  const u2 w = __builtin_bit_cast(u2, x);
+  return v4f{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u), __uint_as_float(w[1] << 16),
+             __uint_as_float(w[1] & 0xffff0000u)};
+}
+template <> __device__ __forceinline__ v4f unpack4<f16_t>(v4s x) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  return __builtin_convertvector(__builtin_bit_cast(h4, x), v4f);
+}
+
 // One wave's share of a 64-token tile: rows 16 rt + (0..15) against NSUB
 // 16-token sub-tiles starting at kt / vt, for NMT head_dim tiles (voff).
 // Online softmax state (m_run, l_run over this wave's tokens, o_acc) is
