@@ -44,10 +44,10 @@
 //    the normalised o in the KV's 16-bit type (the type FlashInfer's cascade
 //    merges its per-level outputs in) and the lse in fp32: half the bytes of
 //    fp32 slots, which the launch writes and reads back once each.  Outputs
-//    and slots are written with non-temporal stores: nothing in the launch
-//    reads them back, and the end-of-kernel write-back before the merge
-//    kernel then has little left to do (the gap between the two kernels
-//    halved on MI355X).
+//    are written with non-temporal stores and slots written through to the
+//    device's point of coherence: nothing in the launch reads them back, and
+//    the end-of-kernel write-back before the merge kernel then has little
+//    left to do (the gap between the two kernels halved on MI355X).
 
 #include <math.h>
 
@@ -470,10 +470,9 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt)
               if (mt < nmt)
-                __builtin_nontemporal_store(
-                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
-                    reinterpret_cast<v4s*>(op + mt * 16));
-            if (mt0 == 0 && lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
+                store_wt(reinterpret_cast<v4s*>(op + mt * 16),
+                         pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv));
+            if (mt0 == 0 && lg == 0) store_wt(a.part_lse + slot, lse);
           }
         }
         ops += nmt;                                      // store instructions (lse not counted)
@@ -586,10 +585,9 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
               T* op = reinterpret_cast<T*>(a.part_o) + slot * kD + d0;
 #pragma unroll
               for (int mt = 0; mt < 8; ++mt)
-                __builtin_nontemporal_store(pack4<T>(o2[r][mt][0] * inv, o2[r][mt][1] * inv, o2[r][mt][2] * inv,
-                                                     o2[r][mt][3] * inv),
-                                            reinterpret_cast<v4s*>(op + mt * 16));
-              if (lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
+                store_wt(reinterpret_cast<v4s*>(op + mt * 16),
+                         pack4<T>(o2[r][mt][0] * inv, o2[r][mt][1] * inv, o2[r][mt][2] * inv, o2[r][mt][3] * inv));
+              if (lg == 0) store_wt(a.part_lse + slot, lse);
             }
           }
         }
@@ -863,10 +861,9 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt)
               if (mt < nmt)
-                __builtin_nontemporal_store(
-                    pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
-                    reinterpret_cast<v4s*>(op + mt * 16));
-            if (mt0 == 0 && lg == 0) __builtin_nontemporal_store(lse, a.part_lse + slot);
+                store_wt(reinterpret_cast<v4s*>(op + mt * 16),
+                         pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv));
+            if (mt0 == 0 && lg == 0) store_wt(a.part_lse + slot, lse);
           }
         }
       }
@@ -914,10 +911,9 @@ __device__ __forceinline__ void tail_item(const StreamArgs& a, unsigned char* ar
     T* op = reinterpret_cast<T*>(a.part_o) + sl * kD + 4 * lg;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
-      __builtin_nontemporal_store(
-          pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv),
-          reinterpret_cast<v4s*>(op + 16 * mt));
-    if (lg == 0) __builtin_nontemporal_store((m_run + log2f(l)) * 0.69314718055994531f, a.part_lse + sl);
+      store_wt(reinterpret_cast<v4s*>(op + 16 * mt),
+               pack4<T>(o_acc[mt][0] * inv, o_acc[mt][1] * inv, o_acc[mt][2] * inv, o_acc[mt][3] * inv));
+    if (lg == 0) store_wt(a.part_lse + sl, (m_run + log2f(l)) * 0.69314718055994531f);
   }
 }
 

