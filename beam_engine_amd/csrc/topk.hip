@@ -31,6 +31,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -70,6 +72,10 @@ static TopkGeom topk_geom(int n_rows, int vocab, int k) {
   segs = (vocab + seg_len - 1) / seg_len;
   return TopkGeom{segs, seg_len};
 }
+
+// Bytes of the arrival counters at the start of the workspace: one u32 per
+// row and one per request (at most 512 requests take the one-launch path).
+inline int64_t topk_counter_bytes(int n_rows) { return (((int64_t)n_rows + 512) * 4 + 255) / 256 * 256; }
 
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p) { return to_f32(*p); }
@@ -144,10 +150,52 @@ __device__ __forceinline__ uint16_t raw_bits(const T* p) {
 
 // Loads n valid positions from seg (16-byte loads when the segment start is
 // 16-byte aligned, uniform over the workgroup; else one load per logit).
+constexpr uint16_t kPast16 = 0xffff;                   // past the segment: a negative NaN pattern, key 0
+
+// The raw 16-bit logits of a segment (no temperature): only loads, so that a
+// caller can issue them ahead of their use.
+template <typename T>
+__device__ __forceinline__ void load_raw16(const T* seg, int n, SegVals<T>& v) {
+  constexpr int V = 8;
+  const bool aligned = (reinterpret_cast<uintptr_t>(seg) & 15) == 0;
+#pragma unroll
+  for (int c = 0; c < kPerThread / V; ++c) {
+    const int p0 = c * (kTopkThreads * V) + (int)threadIdx.x * V;
+    if (aligned && p0 + V <= n) {
+      const uint4 u = *reinterpret_cast<const uint4*>(seg + p0);
+      v.w[c * 4 + 0] = u.x;
+      v.w[c * 4 + 1] = u.y;
+      v.w[c * 4 + 2] = u.z;
+      v.w[c * 4 + 3] = u.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; e += 2) {
+        const uint32_t lo = p0 + e < n ? raw_bits(seg + p0 + e) : kPast16;
+        const uint32_t hi = p0 + e + 1 < n ? raw_bits(seg + p0 + e + 1) : kPast16;
+        v.w[c * 4 + e / 2] = lo | (hi << 16);
+      }
+    }
+  }
+}
+
+// Temperature scaling of raw 16-bit logits in place (past-the-segment
+// patterns stay).
+template <typename T>
+__device__ __forceinline__ void temp16(TempScale ts, SegVals<T>& v, int w0 = 0, int w1 = kPerThread / 2) {
+  if (ts.t == 1.0f) return;
+#pragma unroll
+  for (int i = w0; i < w1; ++i) {
+    const uint32_t u = v.w[i];
+    const uint32_t lo = (u & 0xffffu) == kPast16 ? kPast16 : bits_of<T>(scaled<T>(v.at(2 * i), ts));
+    const uint32_t hi = (u >> 16) == kPast16 ? kPast16 : bits_of<T>(scaled<T>(v.at(2 * i + 1), ts));
+    v.w[i] = lo | (hi << 16);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ void load_vals(const T* seg, int n, TempScale ts, SegVals<T>& v) {
   constexpr int V = 8;                                 // 16-bit logits per 16 bytes
-  constexpr uint16_t kPast = 0xffff;                   // past the segment: a negative NaN pattern, key 0
+  constexpr uint16_t kPast = kPast16;
   const bool aligned = (reinterpret_cast<uintptr_t>(seg) & 15) == 0;
 #pragma unroll
   for (int c = 0; c < kPerThread / V; ++c) {
@@ -1031,6 +1079,592 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pool_kernel(int n_rows, int
   }
 }
 
+// ---------------------------------------------------------------- two-kernel selection
+// The three passes above as two launches for 16-bit logits, with the same
+// results:
+//  * pass A (topk_units16_kernel): per (row, segment) unit the statistics and
+//    the candidates of pass 1, unsorted; a few workgroups per CU take the
+//    units in turn and load the next unit while computing the current one.
+//  * pass B (topk_rows16_kernel, one workgroup per row): the row's selection
+//    -- the k-th best logp among the candidates by a radix select on 16-bit
+//    logp keys over register-held candidates, the entries above it and its
+//    ties by lowest index, or the same exact fallback over all logits as
+//    pass 2 -- and, in the workgroup that completes a request's last row (an
+//    arrival counter per request), pass 3 for the request.
+// Every pass issues all of its loads before using any: one memory round trip
+// each.  The row lists go to the pool through agent-scope stores and loads
+// (written through to the device's point of coherence).
+// Arrival counters (u32 at the start of the workspace) are zero at rest: a
+// launch adds one per arrival (a plain atomic add) and the last arrival sets
+// the word back to zero, so every complete launch leaves them zero.  A
+// workspace must therefore hold zeros there before its first use (the Python
+// workspace is allocated zeroed; the static scratch of be_beam_topk_noalloc
+// starts zeroed).
+constexpr int kFusedRowCand = 2048;    // segs x cap of one row (register-held, 8 per thread)
+constexpr int kFusedPool = 512;        // rows x min(k, beam) of one request, in LDS
+constexpr int kFusedPoolRows = 256;
+constexpr int kFusedReqs = 512;
+constexpr int kFusedTie = 256;
+constexpr int kUnitWgPerCu = 4;        // pass A workgroups per CU (two units each at the e2e shape)
+constexpr int kUnitWavesPerSimd = 4;
+static_assert(kFusedReqs == 512, "topk_counter_bytes reserves one counter per request for 512 requests");
+static_assert(kFusedRowCand % kTopkThreads == 0, "row candidates are spread evenly over the threads");
+
+struct FusedTopkArgs {
+  const void* logits;
+  int64_t row_stride;
+  int vocab, seg_len, segs, n_rows, k, cap;
+  TempScale ts;
+  float* seg_max;
+  double* seg_sum;
+  int* seg_cnt;
+  uint32_t* seg_bound;
+  uint64_t* cand;
+  uint32_t* ctr;                       // n_rows row counters, then n_req request counters
+  float* row_vals;
+  int32_t* row_idx;
+  const double* parent;
+  int beam, n_req;
+  const int32_t* req_row_ptr;
+  int32_t* out_parent;
+  int32_t* out_token;
+  double* out_score;
+};
+
+// Stores written through to the device's coherence point and loads that read
+// there (agent scope): another workgroup of the same launch reads them after
+// an arrival counter says they are complete.
+__device__ __forceinline__ void st_wt(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_wt(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_wt(int32_t* p, int32_t v) { st_wt(reinterpret_cast<uint32_t*>(p), (uint32_t)v); }
+__device__ __forceinline__ void st_wt(float* p, float v) {
+  st_wt(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+__device__ __forceinline__ void st_wt(double* p, double v) {
+  st_wt(reinterpret_cast<uint64_t*>(p), (uint64_t)__double_as_longlong(v));
+}
+__device__ __forceinline__ uint64_t ld_co(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_co(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_co(const int32_t* p) { return (int32_t)ld_co(reinterpret_cast<const uint32_t*>(p)); }
+__device__ __forceinline__ float ld_co(const float* p) { return __uint_as_float(ld_co(reinterpret_cast<const uint32_t*>(p))); }
+__device__ __forceinline__ double ld_co(const double* p) {
+  return __longlong_as_double((long long)ld_co(reinterpret_cast<const uint64_t*>(p)));
+}
+
+// Counts one arrival on ctr and returns the count including it; the word
+// returns to zero when the count reaches total.
+__device__ __forceinline__ uint32_t arrive(uint32_t* ctr, uint32_t total) {
+  const uint32_t n = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  if (n >= total) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return n;
+}
+
+// The 16-bit order key of a 16-bit float pattern.
+__device__ __forceinline__ uint32_t key16_of_bits(uint32_t bits16) { return key16x2(bits16) & 0xffffu; }
+
+// x' of a 16-bit order key (keys at or below that of -inf give -inf).
+template <typename T>
+__device__ __forceinline__ float value_of_key16(uint32_t k16) {
+  const uint32_t kninf = key16_of_bits(__is_same(T, bf16_t) ? 0xff80u : 0xfc00u);
+  return k16 > kninf ? to_f32(__builtin_bit_cast(T, (uint16_t)((k16 & 0x8000u) ? (k16 ^ 0x8000u) : (~k16 & 0xffffu))))
+                     : -INFINITY;
+}
+
+// The 16-bit order key of logp(x') (logp is rounded to the logits' format).
+template <typename T>
+__device__ __forceinline__ uint32_t logp_key16(float xs, float m, float L) {
+  return key16_of_bits(bits_of<T>(logp_of<T>(xs, m, L)));
+}
+
+// Float64 sum of e^(x' - mh) over words [W0, W1) of a thread's logits, mh
+// their largest x'; NaN patterns (positions past the segment) give e^-708.  Four exps are interleaved at a time: enough
+// independent work per wave at eight waves per SIMD, within its register
+// budget.
+template <typename T, int W0, int W1>
+__device__ __forceinline__ double half_exp_sum(const SegVals<T>& x, const double* tab, float mh) {
+  double md = (double)mh;
+  double acc = 0.0;
+#pragma unroll
+  for (int j0 = 2 * W0; j0 < 2 * W1; j0 += 4) {
+#pragma unroll
+    for (int j = j0; j < j0 + 4; ++j) acc += exp_neg((double)x.at(j) - md, tab);
+    // the next group's arguments depend on this group's sum: the compiler
+    // cannot start every exp's range reduction at once (which spills)
+    asm volatile("" : "+v"(acc), "+v"(md));
+  }
+  return mh == -INFINITY ? 0.0 : acc;
+}
+
+// LDS of pass B.
+struct FusedLds {
+  float mL[2];
+  int flag, nabove, ntie, exact, req;
+  int off[kMaxSegs + 1];
+  uint32_t sbound[kMaxSegs];
+  int req_ptr[kFusedReqs + 1];
+  union {
+    struct {                                       // a row's selection
+      double terms[kMaxSegs];
+      int hist[256];
+      int suf[257];
+      int misc[8];
+      uint64_t fin[kMaxK];
+      uint64_t tg[kFusedTie];
+    } row;
+    struct {                                       // the exact fallback of a row
+      int hist[4 * 256];
+      int suf[257];
+      int misc[8];
+      uint32_t skey[kMaxK];
+      int32_t sidx[kMaxK];
+    } ex;
+    struct {                                       // a request's pool
+      double tot[kFusedPool];
+      int32_t idx[kFusedPool];
+      int sel[kFusedPoolRows];
+      int first[kFusedPoolRows + 1];
+    } pool;
+  } u;
+};
+
+// Row r's selection from its segments' statistics and candidates (every
+// thread of the workgroup; ends with a barrier).  Writes row_vals / row_idx
+// through to the device's point of coherence.
+template <typename T>
+__device__ void fused_row(const FusedTopkArgs& a, int r, FusedLds& sm) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int segs = a.segs, k = a.k, cap = a.cap;
+  const int64_t base = (int64_t)r * segs;
+  const int lcap = __ffs(cap) - 1;
+  const int nslots = segs << lcap;
+  // one round trip: the segments' statistics (wave 0), every candidate slot
+  // of the row (slots past a segment's count hold stale words: unused) and
+  // the request pointers (pass B's request lookup)
+  constexpr int kQ = kFusedRowCand / kTopkThreads;
+  uint64_t cv[kQ];
+  const uint64_t* blk = a.cand + base * cap;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) cv[q] = ld_co(blk + min(q * kTopkThreads + tid, nslots - 1));
+  float ms = -INFINITY;
+  double ss = 0.0;
+  int c = 0;
+  uint32_t bd = 0;
+  const int n_req = a.beam > 0 ? a.n_req : 0;
+  for (int i = tid; i <= n_req; i += kTopkThreads)
+    sm.req_ptr[i] = a.req_row_ptr ? a.req_row_ptr[i] : (i == 0 ? 0 : a.n_rows);
+  if (tid < 64) {
+    const int li = min(lane, segs - 1);
+    ms = ld_co(a.seg_max + base + li);
+    ss = ld_co(a.seg_sum + base + li);
+    c = ld_co(a.seg_cnt + base + li);
+    bd = ld_co(a.seg_bound + base + li);
+  }
+  if (tid < 64) {
+    const bool in = lane < segs;
+    if (!in) {
+      ms = -INFINITY;
+      ss = 0.0;
+      c = 0;
+    }
+    if (in) sm.sbound[lane] = bd;
+    const float mm = wave_max(ms);
+    sm.u.row.terms[lane] = in ? ss * exp((double)ms - (double)mm) : 0.0;
+    int incl = c < 0 ? 0 : c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    if (in) sm.off[lane + 1] = incl;
+    // an overflowed segment, or fewer candidates than k: the exact selection
+    const bool over = __builtin_amdgcn_ballot_w64(c < 0) != 0 || __shfl(incl, segs - 1, 64) < k;
+    if (lane == 0) {
+      sm.off[0] = 0;
+      sm.exact = over ? 1 : 0;
+      sm.nabove = 0;
+      sm.ntie = 0;
+      double S = 0.0;
+      for (int s = 0; s < segs; ++s) S += sm.u.row.terms[s];
+      sm.mL[0] = mm;
+      sm.mL[1] = (float)log(S);
+    }
+  }
+  __syncthreads();
+  const float m = sm.mL[0], L = sm.mL[1];
+  if (!sm.exact) {
+    // each valid candidate with the 16-bit key of its logp in bits 48..63
+    // (invalid slots: 0, below every valid key)
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const int f = q * kTopkThreads + tid, sg = min(f >> lcap, kMaxSegs - 1), p = f & (cap - 1);
+      const bool use = f < nslots && p < sm.off[sg + 1] - sm.off[sg];
+      const uint64_t cc = cv[q];
+      const uint32_t lk = logp_key16<T>(value_of_key16<T>((uint32_t)(cc >> 32) & 0xffffu), m, L);
+      cv[q] = use ? (cc | ((uint64_t)lk << 48)) : 0ull;
+    }
+    // the k-th largest logp key: two 8-bit radix passes over the valid entries
+    uint32_t K = 0;
+    int krem = k;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      sm.u.row.hist[tid] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) {
+        const uint32_t lk = (uint32_t)(cv[q] >> 48);
+        const bool valid = cv[q] != 0ull;
+        if (pass == 0) {
+          if (valid) atomicAdd(&sm.u.row.hist[lk >> 8], 1);
+        } else if (valid && (lk >> 8) == (K >> 8)) {
+          atomicAdd(&sm.u.row.hist[lk & 255u], 1);
+        }
+      }
+      __syncthreads();
+      sm.u.row.suf[tid] = block_suffix_sum(sm.u.row.hist[tid], sm.u.row.misc + 4);
+      if (tid == 0) sm.u.row.suf[256] = 0;
+      __syncthreads();
+      if (sm.u.row.suf[tid] >= krem && sm.u.row.suf[tid + 1] < krem) {
+        sm.u.row.misc[0] = tid;
+        sm.u.row.misc[1] = sm.u.row.suf[tid + 1];
+      }
+      __syncthreads();
+      K |= (uint32_t)sm.u.row.misc[0] << (pass == 0 ? 8 : 0);
+      krem -= sm.u.row.misc[1];
+      __syncthreads();
+    }
+    // the entries above the k-th logp, its tie group, and the segments' bounds
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const uint64_t cc = cv[q];
+      const uint32_t lk = (uint32_t)(cc >> 48);
+      const uint64_t e = ((uint64_t)lk << 32) | (uint32_t)cc;
+      if (cc != 0ull && lk > K) {
+        sm.u.row.fin[atomicAdd(&sm.nabove, 1)] = e;
+      } else if (cc != 0ull && lk == K) {
+        const int at = atomicAdd(&sm.ntie, 1);
+        if (at < kFusedTie) sm.u.row.tg[at] = e;
+      }
+    }
+    if (tid < segs) {
+      const uint32_t b = sm.sbound[tid];
+      if (b != 0 && logp_key16<T>(value_of_key16<T>(b), m, L) >= K) atomicOr(&sm.exact, 1);
+    }
+    __syncthreads();
+    if (!sm.exact && sm.ntie <= kFusedTie) {
+      const int above = sm.nabove, g = sm.ntie, need = k - above;
+      for (int i = tid; i < g; i += kTopkThreads) {
+        const uint64_t x = sm.u.row.tg[i];
+        const uint32_t xi = ~(uint32_t)x;
+        int rk = 0;
+        for (int j = 0; j < g; ++j) rk += (~(uint32_t)sm.u.row.tg[j]) < xi ? 1 : 0;
+        if (rk < need) sm.u.row.fin[above + rk] = x;
+      }
+      __syncthreads();
+      for (int i = tid; i < k; i += kTopkThreads) {
+        const uint64_t x = sm.u.row.fin[i];
+        int pos = 0;
+        for (int j = 0; j < k; ++j) pos += sm.u.row.fin[j] > x ? 1 : 0;
+        const uint32_t lk = (uint32_t)(x >> 32);
+        const uint16_t bits = (uint16_t)((lk & 0x8000u) ? (lk ^ 0x8000u) : (~lk & 0xffffu));
+        st_wt(a.row_vals + (int64_t)r * k + pos, to_f32(__builtin_bit_cast(T, bits)));
+        st_wt(a.row_idx + (int64_t)r * k + pos, (int32_t)~(uint32_t)x);
+      }
+      __syncthreads();
+      return;
+    }
+  }
+  __syncthreads();
+  // every logit of the row
+  const T* row = reinterpret_cast<const T*>(a.logits) + (int64_t)r * a.row_stride;
+  const TempScale ts = a.ts;
+  select_k([&](int i) { return fkey(logp_of<T>(scaled<T>(load_logit(row + i), ts), m, L)); },
+           [&](int i) { return i; }, a.vocab, k, sm.u.ex.skey, sm.u.ex.sidx, sm.u.ex.hist, sm.u.ex.suf,
+           sm.u.ex.misc);
+  for (int i = tid; i < k; i += kTopkThreads) {
+    const uint32_t ki = sm.u.ex.skey[i];
+    const int ii = sm.u.ex.sidx[i];
+    int rank = 0;
+    for (int j = 0; j < k; ++j) rank += (sm.u.ex.skey[j] > ki) || (sm.u.ex.skey[j] == ki && sm.u.ex.sidx[j] < ii);
+    const uint32_t uu = (ki & 0x80000000u) ? (ki & 0x7fffffffu) : ~ki;
+    st_wt(a.row_vals + (int64_t)r * k + rank, __uint_as_float(uu));
+    st_wt(a.row_idx + (int64_t)r * k + rank, (int32_t)ii);
+  }
+  __syncthreads();
+}
+
+// Pass 3 for request q (rows [rb, re)) from the row lists written by this
+// launch; only each row's first min(k, beam) entries can be chosen (every
+// thread; ends with a barrier).
+__device__ void fused_pool(const FusedTopkArgs& a, int rb, int re, int q, FusedLds& sm) {
+  const int tid = threadIdx.x, k = a.k, beam = a.beam;
+  int32_t* op = a.out_parent + (int64_t)q * beam;
+  int32_t* ot = a.out_token + (int64_t)q * beam;
+  double* os = a.out_score + (int64_t)q * beam;
+  const int nr = re - rb, jb = min(k, beam), n = nr * jb;
+  double* tot = sm.u.pool.tot;
+  {
+    constexpr int kQ = kFusedPool / kTopkThreads;
+    float rv[kQ];
+    int32_t ri[kQ];
+    double pv[kQ];
+#pragma unroll
+    for (int qq = 0; qq < kQ; ++qq) {
+      const int i = min(qq * kTopkThreads + tid, n - 1), rr = i / jb, j = i - rr * jb;
+      rv[qq] = ld_co(a.row_vals + (int64_t)(rb + rr) * k + j);
+      ri[qq] = ld_co(a.row_idx + (int64_t)(rb + rr) * k + j);
+      pv[qq] = a.parent[rb + rr];
+    }
+#pragma unroll
+    for (int qq = 0; qq < kQ; ++qq) {
+      const int i = qq * kTopkThreads + tid;
+      if (i < n) {
+        tot[i] = pv[qq] + (double)rv[qq];
+        sm.u.pool.idx[i] = ri[qq];
+      }
+    }
+  }
+  for (int i = tid; i < nr; i += kTopkThreads) sm.u.pool.sel[i] = 0;
+  __syncthreads();
+  int top = 1;
+  while (top * 2 <= jb) top *= 2;
+  for (int e = tid; e < n; e += kTopkThreads) {
+    const int rr = e / jb, j = e - rr * jb;
+    const double t = tot[e];
+    int rank = j;
+    // entries of row o before (rr, j): totals > t, or == t when o < rr (a
+    // prefix of the row; binary searches, eight rows at a time)
+    for (int o0 = 0; o0 < nr && rank < beam; o0 += 8) {
+      int pos[8];
+#pragma unroll
+      for (int uu = 0; uu < 8; ++uu) pos[uu] = 0;
+      for (int step = top; step > 0; step >>= 1) {
+        double y[8];
+#pragma unroll
+        for (int uu = 0; uu < 8; ++uu) {
+          const int o = o0 + uu, c = pos[uu] + step;
+          const bool use = (o < nr) & (o != rr) & (c <= jb);
+          y[uu] = tot[use ? o * jb + c - 1 : 0];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int uu = 0; uu < 8; ++uu) {
+          const int o = o0 + uu, c = pos[uu] + step;
+          const bool use = (o < nr) & (o != rr) & (c <= jb);
+          pos[uu] = (use & ((y[uu] > t) | ((y[uu] == t) & (o < rr)))) ? c : pos[uu];
+        }
+      }
+#pragma unroll
+      for (int uu = 0; uu < 8; ++uu) rank += pos[uu];
+    }
+    if (rank < beam) atomicAdd(&sm.u.pool.sel[rr], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    sm.u.pool.first[0] = 0;
+    for (int i = 0; i < nr; ++i) sm.u.pool.first[i + 1] = sm.u.pool.first[i] + sm.u.pool.sel[i];
+  }
+  __syncthreads();
+  for (int e = tid; e < n; e += kTopkThreads) {
+    const int rr = e / jb, j = e - rr * jb;
+    if (j < sm.u.pool.sel[rr]) {
+      const int at = sm.u.pool.first[rr] + j;
+      op[at] = rb + rr;
+      ot[at] = sm.u.pool.idx[e];
+      os[at] = tot[e];
+    }
+  }
+  for (int i = sm.u.pool.first[nr] + tid; i < beam; i += kTopkThreads) {
+    op[i] = -1;
+    ot[i] = -1;
+    os[i] = -INFINITY;
+  }
+  __syncthreads();
+}
+
+// Pass A: per (row, segment) unit the statistics and the unsorted candidates
+// (pass 1 without its sort).  G workgroups (a few per CU) take units
+// u = blockIdx.x + i G in turn; each issues the next unit's loads as soon as
+// the current unit's logits are in registers, so that the float64 exp-sums
+// (VALU-bound) run while the next logits stream in.  Within a unit, a
+// thread's two halves are summed in turn (each against its own maximum, then
+// rescaled).  SCALED: the temperature is not 1 (a separate instantiation keeps
+// the common path free of the scaling branches).
+template <typename T, bool SCALED>
+__global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_kernel(FusedTopkArgs a) {
+  __shared__ double tab[64];
+  __shared__ float wmax[4];
+  __shared__ double wsum[4];
+  __shared__ uint32_t wtau[4];
+  __shared__ int ncand;
+  __shared__ uint64_t lc[kMaxCap];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int segs = a.segs, k = a.k, cap = a.cap, seg_len = a.seg_len, vocab = a.vocab;
+  const int units = a.n_rows * segs;
+  const T* logits = reinterpret_cast<const T*>(a.logits);
+  constexpr int kWords = kPerThread / 2, kHalf = kWords / 2;
+  int u = blockIdx.x;
+  SegVals<T> x, xn;
+  if (u < units) {
+    const int r = u / segs, b = (u - r * segs) * seg_len;
+    load_raw16<T>(logits + (int64_t)r * a.row_stride + b, min(vocab, b + seg_len) - b, x);
+  }
+  exp_table_init(tab);
+  if (tid == 0) ncand = 0;
+  __syncthreads();                                     // the exp table, ncand
+  for (; u < units; u += gridDim.x) {
+    const int r = u / segs, s = u - r * segs;
+    const int b = s * seg_len;
+    if constexpr (SCALED) temp16<T>(a.ts, x);
+    // the largest x' of each half (fmaxf skips the NaN patterns of positions
+    // past the segment): this waits for the unit's logits
+    float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPerThread / 2; ++j) m0 = fmaxf(m0, x.at(j));
+#pragma unroll
+    for (int j = kPerThread / 2; j < kPerThread; ++j) m1 = fmaxf(m1, x.at(j));
+    // the next unit's loads, issued once this unit's logits are in registers
+    // (issued with them they would share the memory system and both arrive
+    // late together)
+    {
+      const int un = u + gridDim.x;
+      if (un < units) {
+        const int rn = un / segs, bn = (un - rn * segs) * seg_len;
+        asm volatile("" : "+v"(m0), "+v"(m1));
+        load_raw16<T>(logits + (int64_t)rn * a.row_stride + bn, min(vocab, bn + seg_len) - bn, xn);
+      }
+    }
+    const double acc0 = half_exp_sum<T, 0, kHalf>(x, tab, m0);
+    const double acc1 = half_exp_sum<T, kHalf, kWords>(x, tab, m1);
+    uint32_t kp[kWords];
+    v2u16 km2 = {0, 0};
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) {
+      kp[i] = key16x2(x.w[i]);
+      km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(v2u16, kp[i]));
+    }
+    const uint32_t kmax = max((uint32_t)km2.x, (uint32_t)km2.y);
+    const float mt = fmaxf(m0, m1);
+    // the wave's kw-th largest per-thread maximum, bit by bit
+    const int kw = (k + 3) >> 2;
+    uint32_t pref = 0;
+    for (int bit = 15; bit >= 0; --bit) {
+      const uint32_t c = pref | (1u << bit);
+      if (__popcll(__builtin_amdgcn_ballot_w64(kmax >= c)) >= kw) pref = c;
+    }
+    const float mw = value_of_key16<T>(lane63(wave_scan_max(kmax)));
+    // the two halves' sums against the thread max, then against the wave's
+    double acc = 0.0;
+    if (mt != -INFINITY) {
+      const double md = (double)mt;
+      acc = acc0 * exp_neg((double)m0 - md, tab) + acc1 * exp_neg((double)m1 - md, tab);
+      acc *= exp_neg(md - (double)mw, tab);
+    }
+    acc = wave_scan_add_f64(acc);
+    if (lane == 63) {
+      wmax[w] = mw;
+      wsum[w] = acc;
+      wtau[w] = pref;
+    }
+    __syncthreads();
+    const float m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const uint32_t tau = max(1u, min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3])));
+    const v2u16 t1 = {(unsigned short)(tau - 1), (unsigned short)(tau - 1)};
+    const v2u16 one = {1, 1};
+    v2u16 c2 = {0, 0};
+#pragma unroll
+    for (int i = 0; i < kWords; ++i)
+      c2 += __builtin_elementwise_min(__builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, kp[i]), t1), one);
+    const int mine = (int)c2.x + (int)c2.y;
+    const int incl = wave_scan_add(mine);
+    int wbase = 0;
+    if (lane == 63) wbase = atomicAdd(&ncand, incl);
+    int at = (int)lane63((uint32_t)wbase) + incl - mine;
+    if (mine > 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) {
+        const uint32_t lo = kp[i] & 0xffffu, hi = kp[i] >> 16;
+        if (max(lo, hi) >= tau) {
+          if (lo >= tau) {
+            if (at < cap) lc[at] = ((uint64_t)lo << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i));
+            ++at;
+          }
+          if (hi >= tau) {
+            if (at < cap) lc[at] = ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i + 1));
+            ++at;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int total = ncand;
+    const int64_t rs = (int64_t)r * segs + s;
+    for (int i = tid; i < min(total, cap); i += kTopkThreads) a.cand[rs * cap + i] = lc[i];
+    if (tid == 0) {
+      double sum = 0.0;
+      for (int q = 0; q < 4; ++q) sum += wsum[q] * exp_neg((double)wmax[q] - (double)m, tab);
+      a.seg_max[rs] = m;
+      a.seg_sum[rs] = sum;
+      a.seg_cnt[rs] = total <= cap ? total : -1;
+      a.seg_bound[rs] = tau > 1 ? tau - 1 : 0u;
+    }
+    __syncthreads();                                   // lc, ncand, wmax.. free again
+    if (tid == 0) ncand = 0;
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) x.w[i] = xn.w[i];
+  }
+}
+
+// Pass B: per row (one workgroup each) the selection from pass A's output;
+// the workgroup that completes a request's last row (an arrival counter per
+// request) runs pass 3 for it.
+template <typename T>
+__global__ __launch_bounds__(kTopkThreads) void topk_rows16_kernel(FusedTopkArgs a) {
+  __shared__ FusedLds sm;
+  const int tid = threadIdx.x, r = blockIdx.x;
+  const int n_req = a.beam > 0 ? a.n_req : 0;
+  // requests without rows (or with an invalid range) get empty selections
+  for (int q = r; q < n_req; q += gridDim.x) {
+    const int rb = a.req_row_ptr ? a.req_row_ptr[q] : 0, re = a.req_row_ptr ? a.req_row_ptr[q + 1] : a.n_rows;
+    if (!(rb >= 0 && re <= a.n_rows && rb < re))
+      for (int i = tid; i < a.beam; i += kTopkThreads) {
+        a.out_parent[(int64_t)q * a.beam + i] = -1;
+        a.out_token[(int64_t)q * a.beam + i] = -1;
+        a.out_score[(int64_t)q * a.beam + i] = -INFINITY;
+      }
+  }
+  fused_row<T>(a, r, sm);
+  if (n_req == 0) return;
+  // the row lists are complete before this row's arrival counts
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // the request holding row r: the last q with req_row_ptr[q] <= r
+  const int* rp = sm.req_ptr;
+  if (tid == 0) {
+    int lo = 0, hi = n_req;                            // the answer is in [lo, hi)
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (rp[mid] <= r) lo = mid;
+      else hi = mid;
+    }
+    const int rb = rp[lo], re = rp[lo + 1];
+    const bool ok = rb >= 0 && re <= a.n_rows && rb <= r && r < re;
+    sm.req = lo;
+    sm.flag = ok && arrive(a.ctr + lo, (uint32_t)(re - rb)) == (uint32_t)(re - rb);
+    sm.off[0] = rb;
+    sm.off[1] = re;
+  }
+  __syncthreads();
+  if (sm.flag) fused_pool(a, sm.off[0], sm.off[1], sm.req, sm);
+}
+
 // ---------------------------------------------------------------- diverse selection
 // Diverse beam search with the Hamming penalty (beam_strategy.py:173-312),
 // one workgroup per request over its pool of row top-k choices (row-major:
@@ -1145,8 +1779,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_diverse_kernel(int n_rows, 
 // looked up once per device with hipGetSymbolAddress, with that device
 // current, and that address is what the kernels get.  Calls on one GPU share
 // the array, so calls that overlap on one GPU (different streams, or host
-// threads) race.  Every kernel writes the scratch words it reads before it
-// reads them, so nothing has to be cleared between calls.
+// threads) race.  The one-launch selection's arrival counters at the start
+// of the array start zero (a device array without initialiser is zero-filled
+// when the code object loads) and every complete call leaves them zero; every
+// other scratch word is written before it is read.
 constexpr int64_t kTopkScratchBytes = 8ll << 20;
 static __device__ __align__(256) unsigned char topk_scratch[kTopkScratchBytes];
 
@@ -1184,6 +1820,30 @@ static int topk_scratch_address(hipStream_t st, void** out) {
   return BE_OK;
 }
 
+// Multiprocessor count of the stream's device (cached per device).
+static int g_cus[kMaxScratchDevices] = {};
+
+static int topk_device_cus(hipStream_t st, int* out) {
+  int dev = 0;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    BE_HIP_CHECK(hipStreamGetDevice(st, &d));
+    dev = (int)d;
+  } else {
+    BE_HIP_CHECK(hipGetDevice(&dev));
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(BE_ERR_UNSUPPORTED, "device %d beyond the %d this library tracks", dev, kMaxScratchDevices);
+  int n = __atomic_load_n(&g_cus[dev], __ATOMIC_RELAXED);
+  if (n <= 0) {
+    BE_HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    if (n <= 0) n = 1;
+    __atomic_store_n(&g_cus[dev], n, __ATOMIC_RELAXED);
+  }
+  *out = n;
+  return BE_OK;
+}
+
 }  // namespace be
 
 extern "C" {
@@ -1192,8 +1852,9 @@ int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k) {
   if (n_rows <= 0 || vocab <= 0 || k <= 0) return 0;
   const be::TopkGeom geo = be::topk_geom(n_rows, vocab, k);
   const int64_t ns = (int64_t)n_rows * geo.segs;
-  // seg_sum f64, candidates (u64) x cap, seg_max f32, seg_cnt i32, seg_bound u32
-  return ns * 8 + ns * be::topk_cap(k) * 8 + ns * 4 + ns * 4 + ns * 4 + 256;
+  // arrival counters (u32: one per row and per request), seg_sum f64,
+  // candidates (u64) x cap, seg_max f32, seg_cnt i32, seg_bound u32
+  return be::topk_counter_bytes(n_rows) + ns * 8 + ns * be::topk_cap(k) * 8 + ns * 4 + ns * 4 + ns * 4 + 256;
 }
 
 static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int64_t row_stride, double temperature,
@@ -1237,7 +1898,8 @@ static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int
     return be::fail(BE_ERR_UNSUPPORTED, "vocab %d with k %d needs segments of %d > %d logits", vocab, k, geo.seg_len,
                     be::kMaxSegLen);
   const int64_t ns = (int64_t)n_rows * geo.segs;
-  char* ws = reinterpret_cast<char*>(workspace);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
+  char* ws = reinterpret_cast<char*>(workspace) + be::topk_counter_bytes(n_rows);
   double* seg_sum = reinterpret_cast<double*>(ws);
   uint64_t* cand = reinterpret_cast<uint64_t*>(ws + ns * 8);
   char* tail = ws + ns * 8 + ns * cap * 8;
@@ -1245,6 +1907,54 @@ static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int
   int* seg_cnt = reinterpret_cast<int*>(tail + ns * 4);
   uint32_t* seg_bound = reinterpret_cast<uint32_t*>(tail + ns * 8);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // two launches for 16-bit logits whose row candidates and request pool fit
+  // pass B's registers and LDS arrays
+  const int pool_rows = beam > 0 ? (req_row_ptr ? max_req_rows : n_rows) : 0;
+  if (dtype != BE_F32 && geo.segs * cap <= be::kFusedRowCand && geo.segs <= be::kMaxSegs &&
+      (beam == 0 || (n_req <= be::kFusedReqs && pool_rows <= be::kFusedPoolRows &&
+                     (int64_t)pool_rows * std::min(k, beam) <= be::kFusedPool))) {
+    be::FusedTopkArgs fa{};
+    fa.logits = logits;
+    fa.row_stride = row_stride;
+    fa.vocab = vocab;
+    fa.seg_len = geo.seg_len;
+    fa.segs = geo.segs;
+    fa.n_rows = n_rows;
+    fa.k = k;
+    fa.cap = cap;
+    fa.ts = inv_temp;
+    fa.seg_max = seg_max;
+    fa.seg_sum = seg_sum;
+    fa.seg_cnt = seg_cnt;
+    fa.seg_bound = seg_bound;
+    fa.cand = cand;
+    fa.ctr = counters;
+    fa.row_vals = row_vals;
+    fa.row_idx = row_idx;
+    fa.parent = parent_scores;
+    fa.beam = beam;
+    fa.n_req = beam > 0 ? n_req : 0;
+    fa.req_row_ptr = req_row_ptr;
+    fa.out_parent = out_parent;
+    fa.out_token = out_token;
+    fa.out_score = out_score;
+    int cus = 0;
+    const int rc = be::topk_device_cus(st, &cus);
+    if (rc != BE_OK) return rc;
+    const int g_units = (int)std::min<int64_t>(ns, (int64_t)cus * be::kUnitWgPerCu);
+    const bool scaled = inv_temp.t != 1.0f;
+    if (dtype == BE_BF16) {
+      if (scaled) be::topk_units16_kernel<be::bf16_t, true><<<g_units, be::kTopkThreads, 0, st>>>(fa);
+      else be::topk_units16_kernel<be::bf16_t, false><<<g_units, be::kTopkThreads, 0, st>>>(fa);
+      be::topk_rows16_kernel<be::bf16_t><<<n_rows, be::kTopkThreads, 0, st>>>(fa);
+    } else {
+      if (scaled) be::topk_units16_kernel<be::f16_t, true><<<g_units, be::kTopkThreads, 0, st>>>(fa);
+      else be::topk_units16_kernel<be::f16_t, false><<<g_units, be::kTopkThreads, 0, st>>>(fa);
+      be::topk_rows16_kernel<be::f16_t><<<n_rows, be::kTopkThreads, 0, st>>>(fa);
+    }
+    BE_HIP_CHECK(hipGetLastError());
+    return BE_OK;
+  }
   const dim3 grid(geo.segs, n_rows);
   switch (dtype) {
 #define BE_TOPK_CASE(DT, TY, CAND)                                                                                \

@@ -19,15 +19,17 @@ from . import _lib
 
 
 class TopkWorkspace:
-    """Device scratch for be_beam_topk, grown on demand and reused."""
+    """Device scratch for be_beam_topk, grown on demand and reused.  It is
+    allocated zeroed: the kernel's arrival counters at its start must be zero
+    before the first call, and every call leaves them zero."""
 
     def __init__(self, device=None):
         self.device = torch.device(device) if device is not None else torch.device("cuda")
-        self.buf = torch.empty(0, dtype=torch.uint8, device=self.device)
+        self.buf = torch.zeros(0, dtype=torch.uint8, device=self.device)
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf.numel() < nbytes:
-            self.buf = torch.empty(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
+            self.buf = torch.zeros(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
         return self.buf
 
 

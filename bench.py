@@ -239,7 +239,7 @@ def topk_workload(args):
         "config": {"workload": f"beam selection, {reqs} request(s) x beam {beam}, vocab {vocab}, k {k}"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "topk_cand16 + topk_row + topk_pool kernels",
+                     "kernel": "topk_units16 + topk_rows16 kernels (16-bit logits)",
                      "bytes_per_launch": byts, "mean_launch_us": round(mean_us, 2)},
     }
     if not args.no_cpu_baseline:

@@ -225,3 +225,36 @@ def test_masked_vocabulary_range(dtype):
     x[:, 20000:60000] = float("-inf")
     x[1, :100] = float("-inf")
     compare(x.to(dtype), [0.0, -0.5, -1.0], 4)
+
+
+def test_workspace_shared_across_paths_and_empty_requests():
+    """One workspace across calls that take the two-kernel 16-bit path (its
+    per-request arrival counters must be back at zero after every call) and
+    the three-kernel path (fp32 logits, or a pool above 512 entries), with
+    requests that have no rows (their selections are empty: parent -1)."""
+    from beam_engine_amd import beam_topk
+    from beam_engine_amd.selection import TopkWorkspace
+    say("topk shared workspace, empty requests, both paths")
+    g = torch.Generator().manual_seed(12)
+    ws = TopkWorkspace(torch.device("cuda"))
+    cases = [([16, 0, 5, 16], torch.bfloat16, 16), ([3, 3], torch.float32, 4), ([0, 7, 0], torch.float16, 8),
+             ([32, 32], torch.bfloat16, 32), ([16, 0, 5, 16], torch.bfloat16, 16), ([1] * 40, torch.bfloat16, 1)]
+    for rows, dtype, beam in cases:
+        k = 2 * beam if beam > 1 else 1
+        logits = (torch.randn((sum(rows), 20000), generator=g) * 2).to(dtype)
+        parents = -torch.rand(sum(rows), generator=g, dtype=torch.float64) * 3
+        for _ in range(2):
+            _, _, (par, tok, sc) = beam_topk(logits.cuda(), k, parents, beam, request_rows=rows, workspace=ws)
+            torch.cuda.synchronize()
+            par, tok, sc = par.tolist(), tok.tolist(), sc.tolist()
+            b = 0
+            for q, r in enumerate(rows):
+                got = [(p - b, t, s) for p, t, s in zip(par[q * beam:(q + 1) * beam], tok[q * beam:(q + 1) * beam],
+                                                         sc[q * beam:(q + 1) * beam]) if p >= 0]
+                if r == 0:
+                    assert got == [] and par[q * beam:(q + 1) * beam] == [-1] * beam, f"{rows} request {q}"
+                else:
+                    x = logits[b:b + r].float().numpy()
+                    _, _, _, _, flat = ot.beam_step(x, parents[b:b + r].tolist(), beam, DT[dtype])
+                    assert got == flat, f"{rows} {dtype} request {q}"
+                b += r

@@ -39,7 +39,7 @@ def _call(lib, noalloc, logits, temperature, k, parents, beam, rows):
         rc = lib.be_beam_topk_noalloc(*common, _lib.stream_ptr(dev))
     else:
         need = lib.be_beam_topk_workspace_bytes(n, v, k)
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
         rc = lib.be_beam_topk(*common, ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "top-k")
     torch.cuda.synchronize()
