@@ -76,7 +76,8 @@ class BeAttnPlanInfo(ctypes.Structure):
 
 
 EXPORTS = (
-    "be_version", "be_last_error", "be_kv_append", "be_rope_qkv_append", "be_page_copy", "be_attn_plan",
+    "be_version", "be_last_error", "be_kv_append", "be_rope_qkv_append", "be_page_copy", "be_page_copy_counted",
+    "be_attn_plan",
     "be_attn_run",
     "be_merge_states", "be_beam_topk_workspace_bytes", "be_beam_topk", "be_beam_topk_noalloc", "be_trie_cascade",
     "be_diverse_select", "be_pages_create", "be_pages_destroy", "be_pages_allocate", "be_pages_share",
@@ -109,6 +110,7 @@ def load() -> ctypes.CDLL:
     lib.be_rope_qkv_append.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, i32, i32, vp, vp,
                                        vp, vp]
     lib.be_page_copy.argtypes = [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp]
+    lib.be_page_copy_counted.argtypes = [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp, vp]
     lib.be_attn_plan.argtypes = [ctypes.POINTER(BeLevel), i32, i32, i32, i32, i32, i32, i32, i32, i32, i32,
                                  ctypes.POINTER(BePlanCaps), vp, i64, ctypes.POINTER(BeAttnPlanInfo)]
     lib.be_attn_run.argtypes = [ctypes.POINTER(BeAttnPlanInfo), vp, vp, vp, i64, i64, vp, vp, i64, i64, vp,

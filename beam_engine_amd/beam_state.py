@@ -818,8 +818,12 @@ class NativeBeamState:
         if self._warn.value:
             logger.warning("%d freed pages were not allocated", self._warn.value)
         nc = int(self._ncopies.value)
-        if nc:
-            pt = self.page_table
+        pt = self.page_table
+        if pt.stage_copies_enabled:
+            # to the staged list: the next step (its graph, or its eager path
+            # first) performs them
+            pt.stage_copies(self._copies[: 3 * nc].reshape(nc, 3))
+        elif nc:
             if pt._defer:
                 pt._pending.extend(map(tuple, self._copies[: 3 * nc].reshape(nc, 3).tolist()))
             else:

@@ -666,6 +666,11 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
 
   // ---- validate levels, collect groups
   std::vector<Group> groups;
+  {
+    int64_t ng = 0;
+    for (int lv = 0; lv < num_levels; ++lv) ng += std::max(0, levels[lv].num_groups);
+    groups.reserve((size_t)ng);
+  }
   int64_t total_pages = 0;
   for (int lv = 0; lv < num_levels; ++lv) {
     const be_level& L = levels[lv];

@@ -1176,7 +1176,9 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // ---- tail chunks: groups of <= kTailTokens tokens and <= kTailQueries
   // queries are attended by the merge kernel, 16 tokens (one page) per chunk,
   // while each query holds at most kTailChunks of them
-  std::vector<std::vector<int2>> tails_of((size_t)num_queries);
+  // (per query as CSR: a first pass picks the groups and counts each query's
+  // chunks, a second lays them out in group order)
+  std::vector<int> tail_cnt((size_t)num_queries + 1, 0);
   std::vector<char> is_tail(groups.size(), 0);
   if (!(flags & BE_PLAN_NO_TAIL) && page_size % 16 == 0 && g <= 16) {
     for (size_t gi = 0; gi < groups.size(); ++gi) {
@@ -1186,18 +1188,31 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
         continue;
       const int nch = (int)ceil_div(gr.kv_len, 16);
       bool fits = true;
-      for (int qi = gr.q0; qi < gr.q1; ++qi) fits = fits && (int)tails_of[qi].size() + nch <= kTailChunks;
+      for (int qi = gr.q0; qi < gr.q1; ++qi) fits = fits && tail_cnt[qi] + nch <= kTailChunks;
       if (!fits) continue;
       is_tail[gi] = 1;
+      for (int qi = gr.q0; qi < gr.q1; ++qi) tail_cnt[qi] += nch;
+    }
+  }
+  std::vector<int> tail_beg((size_t)num_queries + 1, 0);
+  for (int qi = 0; qi < num_queries; ++qi) tail_beg[qi + 1] = tail_beg[qi] + tail_cnt[qi];
+  std::vector<int2> tails((size_t)tail_beg[num_queries]);
+  {
+    std::vector<int> fill(tail_beg.begin(), tail_beg.end() - 1);
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+      if (!is_tail[gi]) continue;
+      const Group& gr = groups[gi];
+      const int nch = (int)ceil_div(gr.kv_len, 16);
       for (int qi = gr.q0; qi < gr.q1; ++qi)
         for (int c = 0; c < nch; ++c) {
           const int tok0 = 16 * c;
           const int page = all_pages[(size_t)gr.page_base + tok0 / page_size];
           const int valid = std::min(16, gr.kv_len - tok0);
-          tails_of[qi].push_back(int2{page, (tok0 % page_size) | (valid << 16)});
+          tails[fill[qi]++] = int2{page, (tok0 % page_size) | (valid << 16)};
         }
     }
   }
+  auto n_tails_of = [&](int qi) { return tail_beg[qi + 1] - tail_beg[qi]; };
 
   // ---- tasks: (query tile of a group, KV head), in group order.  A long group
   // of more than 64 rows takes query tiles of up to 128 rows (wide roles), so
@@ -1253,7 +1268,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // bandwidth-bound on every CU, and a CU given to tail items costs them more
   // than the overlap saves on the ns and e2e shapes (measured on MI355X).
   int64_t tail_cost = 0;
-  for (int qi = 0; qi < num_queries; ++qi) tail_cost += (int64_t)tails_of[qi].size() * hkv * kTailUnit;
+  for (int qi = 0; qi < num_queries; ++qi) tail_cost += (int64_t)n_tails_of(qi) * hkv * kTailUnit;
   const bool tail_role = tail_cost > 0 && (flags & BE_PLAN_TAIL_ROLE) && (tasks.empty() || W >= 2);
   int W_t = 0;
   if (tail_role) {
@@ -1356,7 +1371,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   for (StreamSeg& s : segs) {
     bool direct = true;
     for (int j = 0; j < s.q_count; ++j)
-      direct = direct && cnt[(size_t)(s.q_begin + j) * hkv + s.head] == 1 && tails_of[s.q_begin + j].empty();
+      direct = direct && cnt[(size_t)(s.q_begin + j) * hkv + s.head] == 1 && n_tails_of(s.q_begin + j) == 0;
     if (!direct) {
       s.out_slot = n_slots;
       n_slots += s.q_count;
@@ -1368,7 +1383,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   if (tail_role) {
     int t0 = 0;
     for (int qi = 0; qi < num_queries; ++qi) {
-      const int nt = (int)tails_of[qi].size();
+      const int nt = n_tails_of(qi);
       for (int h = 0; h < hkv; ++h)
         for (int c = 0; c < nt; c += kItemChunks) {
           const int32_t it[kRecWords] = {qi, h, t0 + c, std::min(kItemChunks, nt - c), n_slots, 0, 0, 0};
@@ -1395,25 +1410,30 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     for (size_t i = 0; i < titems.size(); i += kRecWords)
       slot_ids[fill[(size_t)titems[i] * hkv + titems[i + 1]]++] = titems[i + 4];
   }
-  std::vector<int32_t> recs;
-  std::vector<int> rec_slots;
-  std::vector<int2> tails;
-  recs.reserve(nqh * kRecWords);
-  rec_slots.reserve(slot_ids.size());
+  // records (query, KV head) in query order; a record's slots are its CSR
+  // range of slot_ids, which is already in record order
+  std::vector<int32_t> recs(nqh * kRecWords);
+  int64_t n_recs = 0;
   for (int qi = 0; qi < num_queries; ++qi) {
-    const int t0 = (int)tails.size(), nt_q = (int)tails_of[qi].size();
+    const int t0 = tail_beg[qi], nt_q = n_tails_of(qi);
     const int nt = tail_role ? 0 : nt_q;                 // tail role: the chunks arrive as slots
-    tails.insert(tails.end(), tails_of[qi].begin(), tails_of[qi].end());
     for (int h = 0; h < hkv; ++h) {
       const size_t k = (size_t)qi * hkv + h;
       const int ns = sbeg[k + 1] - sbeg[k];
       if (cnt[k] == 1 && nt_q == 0 && ns == 0) continue;   // written directly
-      const int32_t r[kRecWords] = {qi, h, (int)rec_slots.size(), ns, t0, nt, 0, 0};
-      recs.insert(recs.end(), r, r + kRecWords);
-      rec_slots.insert(rec_slots.end(), slot_ids.begin() + sbeg[k], slot_ids.begin() + sbeg[k + 1]);
+      int32_t* r = recs.data() + n_recs * kRecWords;
+      r[0] = qi;
+      r[1] = h;
+      r[2] = sbeg[k];
+      r[3] = ns;
+      r[4] = t0;
+      r[5] = nt;
+      r[6] = 0;
+      r[7] = 0;
+      ++n_recs;
     }
   }
-  const int64_t n_recs = (int64_t)recs.size() / kRecWords;
+  const std::vector<int>& rec_slots = slot_ids;
   const int64_t n_tails = (int64_t)tails.size();
   const int64_t n_items = (int64_t)titems.size() / kRecWords;
   if (tail_role) {
@@ -1474,7 +1494,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   memcpy(out + off_wg, wg.data(), wg.size() * sizeof(int4));
   if (n_segs) memcpy(out + off_segs, segs.data(), n_segs * sizeof(StreamSeg));
   if (total_pages) memcpy(out + off_pages, all_pages.data(), total_pages * sizeof(int32_t));
-  if (!recs.empty()) memcpy(out + off_recs, recs.data(), recs.size() * sizeof(int32_t));
+  if (n_recs) memcpy(out + off_recs, recs.data(), n_recs * kRecWords * sizeof(int32_t));
   if (!rec_slots.empty()) memcpy(out + off_rslots, rec_slots.data(), rec_slots.size() * sizeof(int32_t));
   if (n_tails) memcpy(out + off_tails, tails.data(), n_tails * sizeof(int2));
   if (n_items) memcpy(out + off_items, titems.data(), titems.size() * sizeof(int32_t));

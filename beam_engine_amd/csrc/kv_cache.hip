@@ -60,12 +60,16 @@ __global__ __launch_bounds__(256) void kv_append_kernel(char* kv, int num_pages,
 }
 
 // grid.x = copy entry c, grid.y = layer * 2 + kv.  Copies len[c] * hkv * row
-// bytes (the first len slots are contiguous inside a page).
+// bytes (the first len slots are contiguous inside a page).  count (device,
+// optional): entries c >= *count are skipped (a launch of fixed size whose
+// live count is written on the device, e.g. inside a captured graph).
 __global__ __launch_bounds__(256) void page_copy_kernel(char* pool, int64_t layer_stride, int num_pages,
                                                        int page_size, int64_t slot_bytes,
                                                        const int32_t* src, const int32_t* dst,
-                                                       const int32_t* len, int vec, int32_t* err) {
+                                                       const int32_t* len, const int32_t* count, int vec,
+                                                       int32_t* err) {
   const int c = blockIdx.x;
+  if (count && c >= *count) return;
   const int layer = blockIdx.y >> 1, sel = blockIdx.y & 1;
   const int s = src[c], d = dst[c], l = len[c];
   if (s < 0 || s >= num_pages || d < 0 || d >= num_pages || l < 0 || l > page_size) {
@@ -127,9 +131,9 @@ int be_kv_append(void* kv_layer, int dtype, int num_pages, int page_size, int nu
   return BE_OK;
 }
 
-int be_page_copy(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int dtype, int num_pages,
-                 int page_size, int num_kv_heads, int head_dim, const int32_t* src, const int32_t* dst,
-                 const int32_t* len, int n, int32_t* err_count, void* stream) {
+static int page_copy_launch(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int dtype, int num_pages,
+                            int page_size, int num_kv_heads, int head_dim, const int32_t* src, const int32_t* dst,
+                            const int32_t* len, const int32_t* count, int n, int32_t* err_count, void* stream) {
   BE_REQUIRE(n >= 0 && num_layers >= 0, "negative count");
   if (n == 0 || num_layers == 0) return BE_OK;
   BE_REQUIRE(kv_pool && src && dst && len, "null pointer");
@@ -142,10 +146,25 @@ int be_page_copy(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int vec = ((slot_bytes & 15) == 0) && ((layer_stride_bytes & 15) == 0) && (((uintptr_t)kv_pool & 15) == 0);
   be::page_copy_kernel<<<dim3(n, num_layers * 2), 256, 0, st>>>(reinterpret_cast<char*>(kv_pool), layer_stride_bytes,
-                                                                num_pages, page_size, slot_bytes, src, dst, len, vec,
-                                                                err_count);
+                                                                num_pages, page_size, slot_bytes, src, dst, len, count,
+                                                                vec, err_count);
   BE_HIP_CHECK(hipGetLastError());
   return BE_OK;
+}
+
+int be_page_copy(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int dtype, int num_pages,
+                 int page_size, int num_kv_heads, int head_dim, const int32_t* src, const int32_t* dst,
+                 const int32_t* len, int n, int32_t* err_count, void* stream) {
+  return page_copy_launch(kv_pool, layer_stride_bytes, num_layers, dtype, num_pages, page_size, num_kv_heads,
+                          head_dim, src, dst, len, nullptr, n, err_count, stream);
+}
+
+int be_page_copy_counted(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int dtype, int num_pages,
+                         int page_size, int num_kv_heads, int head_dim, const int32_t* src, const int32_t* dst,
+                         const int32_t* len, const int32_t* count, int max_n, int32_t* err_count, void* stream) {
+  BE_REQUIRE(count, "null count");
+  return page_copy_launch(kv_pool, layer_stride_bytes, num_layers, dtype, num_pages, page_size, num_kv_heads,
+                          head_dim, src, dst, len, count, max_n, err_count, stream);
 }
 
 }  // extern "C"

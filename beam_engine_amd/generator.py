@@ -188,6 +188,10 @@ class BatchedBeamSearch:
             caps = {k: max(v, old[k]) for k, v in caps.items()}
         w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
         w.use_fixed_layout(**caps)
+        if isinstance(self.state, NativeBeamState) and not self.pt.stage_copies_enabled:
+            # from now on each selection's fork copies go to the staged list that
+            # the step graph's first part performs
+            self.pt.enable_staged_copies(2 * n)
         try:
             w.plan(*args, causal=True, q_data_type=m.dtype)
         except (MemoryError, ValueError):
@@ -235,6 +239,8 @@ class BatchedBeamSearch:
             if graphed:
                 w = self.last_attn = self._fixed_plan(levels, n)
         self.step_graphed = w is not None
+        if not self.step_graphed:
+            self.pt.run_staged_copies()     # an eager step performs the staged fork copies first
         if w is None:
             w = self._plan(kind, levels)
         if self.kernel_type != "cascade":
@@ -261,7 +267,7 @@ class BatchedBeamSearch:
             return timer(li, lambda between: w.run(q, kv, out=out, between=between), w)
 
         if self.step_graphed:
-            logits = self._gd.run_step()
+            logits = self._gd.run_step()     # the staged fork copies first, inside the graph
         elif graph_run:
             logits = self._gd.run(attn)
         else:
@@ -311,7 +317,12 @@ class BatchedBeamSearch:
         st.add_filtered_results(results, self.eos_token_id)
 
     # ---------------------------------------------------------------- results
+    def flush(self) -> None:
+        """Perform fork copies the last selection staged for a next step."""
+        self.pt.run_staged_copies()
+
     def final_sequences(self, num_return: Optional[int] = None):
+        self.flush()
         reqs = sorted({c.request_id for c in self.state.candidates})
         return {r: self.strategy.get_final_sequences(self.state, num_return, r) for r in reqs}
 
@@ -329,4 +340,5 @@ class BatchedBeamSearch:
             elif not st.candidates or self.strategy.should_stop(st, 1 << 30, 0):
                 break
             self.step()
+        self.flush()
         return self.final_sequences()

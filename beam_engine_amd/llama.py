@@ -281,11 +281,13 @@ class GraphedDecoder:
 
     @torch.no_grad()
     def capture_step(self, attn_run: Callable) -> None:
-        """One graph of the whole step: every segment and, between them, each
-        layer's attention launched by ``attn_run(layer, q, kv_layer, out)`` --
-        the launch of a fixed-layout plan (same device plan address and launch
-        sizes for every step; the plan's contents are rewritten before each
-        replay).  Needs ``capture`` first (its warm-up and memory pool)."""
+        """One graph of the whole step: the page table's staged fork copies
+        (when enabled: one counted launch over the list the last selection
+        staged), every segment and, between them, each layer's attention
+        launched by ``attn_run(layer, q, kv_layer, out)`` -- the launch of a
+        fixed-layout plan (same device plan address and launch sizes for every
+        step; the plan's contents are rewritten before each replay).  Needs
+        ``capture`` first (its warm-up and memory pool)."""
         L = self.model.cfg.num_hidden_layers
         self.step_graph, self.step_q, self.step_logits = None, [], None
         gc_on = gc.isenabled()
@@ -294,6 +296,8 @@ class GraphedDecoder:
         try:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=self._pool):
+                if self.pt.stage_copies_enabled:
+                    self.pt.record_staged_copies()
                 x = None
                 for l in range(L + 1):
                     x, q, logits = self._segment(l, x)
@@ -308,8 +312,10 @@ class GraphedDecoder:
         torch.cuda.synchronize()
 
     def run_step(self) -> torch.Tensor:
-        """Replay the whole-step graph (inputs and the attention plan loaded)."""
+        """Replay the whole-step graph (inputs and the attention plan loaded);
+        it performs the staged fork copies."""
         self.step_graph.replay()
+        self.pt.consume_staged_copies()
         return self.step_logits
 
     def stage_inputs(self, tok, pos, wpg, wps) -> None:

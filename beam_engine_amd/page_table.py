@@ -67,6 +67,13 @@ class PageTable:
         self._pending: List[Tuple[int, int, int]] = []
         self._copy_host = self._copy_dev = self._copy_ev = None     # fork-copy lists' staging
         self._defer = 0
+        # staged fork copies (stage_copies): a device list [count, src[m], dst[m], len[m]]
+        # and its pinned host twin, run by one counted launch (run_staged_copies),
+        # which a decode-step graph can hold
+        self._staged_dev = self._staged_host = None
+        self._staged_max = 0
+        self._staged_pending = False
+        self.stage_copies_enabled = False
 
         self.kv_pool = torch.zeros((layer_num, max_num_pages, 2, page_size, head_num, head_dim),
                                    dtype=store_dtype, device=self.device)
@@ -219,6 +226,69 @@ class PageTable:
                               dev[2].data_ptr(), len(todo), self._err.data_ptr(), _lib.stream_ptr(self.device))
         _lib.check(rc, "page copy")
         return len(todo)
+
+    # ------------------------------------------------------------ staged copies
+    def enable_staged_copies(self, max_copies: int) -> None:
+        """From now on ``stage_copies`` takes the fork copies of a trie update:
+        their list goes to a fixed device buffer, and ``run_staged_copies``
+        (eager) or a captured ``record_staged_copies`` launch (a graph replay)
+        performs them before anything reads the pages."""
+        if self.device.type != "cuda":
+            raise ValueError("staged copies need a HIP device")
+        if self._staged_dev is None or self._staged_max < max_copies:
+            self._staged_max = int(max_copies)
+            self._staged_dev = torch.zeros(1 + 3 * self._staged_max, dtype=torch.int32, device=self.device)
+            self._staged_host = torch.zeros(1 + 3 * self._staged_max, dtype=torch.int32, pin_memory=True)
+        self.stage_copies_enabled = True
+
+    def stage_copies(self, copies: np.ndarray) -> None:
+        """Write a step's fork copies ``[n, 3]`` (source page, new page, tokens)
+        into the staged list (one host-to-device copy, stream-ordered).  The
+        pinned twin is rewritten only after the stream has passed the previous
+        upload: callers stage once per decode step, after the step's
+        synchronising selection.  More copies than the list holds run now."""
+        n = len(copies)
+        if self._staged_pending:
+            self.run_staged_copies()           # an earlier list that no launch consumed yet
+        if n > self._staged_max:
+            self.copy_pages(copies)
+            n = 0
+        h = self._staged_host.numpy()
+        if n == 0 and h[0] == 0:
+            return                             # the device list already holds no copies
+        m = self._staged_max
+        h[0] = n
+        if n:
+            c = np.asarray(copies, dtype=np.int32)
+            h[1:1 + n] = c[:, 0]
+            h[1 + m:1 + m + n] = c[:, 1]
+            h[1 + 2 * m:1 + 2 * m + n] = c[:, 2]
+        self._staged_dev[: 1 + 3 * m].copy_(self._staged_host[: 1 + 3 * m], non_blocking=True)
+        self._staged_pending = n > 0
+
+    def record_staged_copies(self) -> None:
+        """Launch the counted copy of the staged list (inside a graph capture,
+        or eagerly): entries below the device count are copied."""
+        lib = _lib.load()
+        d = self._staged_dev
+        m = self._staged_max
+        base = d.data_ptr()
+        rc = lib.be_page_copy_counted(self.kv_pool.data_ptr(), self.layer_stride_bytes, self.layer_num,
+                                      _lib.dtype_code(self.store_dtype), self.max_num_pages, self.page_size,
+                                      self.head_num, self.head_dim, base + 4, base + 4 * (1 + m),
+                                      base + 4 * (1 + 2 * m), base, m, self._err.data_ptr(),
+                                      _lib.stream_ptr(self.device))
+        _lib.check(rc, "staged page copy")
+
+    def consume_staged_copies(self) -> None:
+        """A graph replay holding the counted launch ran the staged list."""
+        self._staged_pending = False
+
+    def run_staged_copies(self) -> None:
+        """Perform a staged list that no graph replay consumed (eager path)."""
+        if self._staged_pending:
+            self.record_staged_copies()
+            self._staged_pending = False
 
     # ------------------------------------------------------------ writes
     def write_block(self, layer: int, page_idx: int, key: torch.Tensor, value: torch.Tensor, index: int) -> None:

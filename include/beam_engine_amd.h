@@ -15,6 +15,7 @@
  *                     (src/beam_engine/models/modeling_llama.py:460-465, 506-514)
  *   be_page_copy      PageTable.copy_block's per-layer copy loop
  *                     (src/beam_engine/page_table.py:96-106), batched over forks and layers
+ *   be_page_copy_counted  the same with the copy count read on the device (graph capture)
  *   be_attn_plan      MultiLevelCascadeAttentionWrapper.plan
  *                     (src/beam_engine/models/modeling_llama.py:732-755) and the FastTree
  *                     host metadata pass (src/beam_engine/attention/fasttree/preparation.py:11-225)
@@ -87,6 +88,18 @@ int be_page_copy(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int 
                  int num_pages, int page_size, int num_kv_heads, int head_dim,
                  const int32_t* src, const int32_t* dst, const int32_t* len, int n,
                  int32_t* err_count, void* stream);
+
+/* be_page_copy_counted: be_page_copy over entries c < *count (count a device
+ * int32, read by the kernel) of arrays holding max_n entries: a launch whose
+ * size does not change with the number of copies, so that it can be captured
+ * in a HIP graph once and replayed with each step's copy list written into
+ * the same device arrays (the decode step's fork copies inside the step
+ * graph).  *count must lie in [0, max_n]; the same checks as be_page_copy.
+ * Replaces the same loop (page_table.py:96-106). */
+int be_page_copy_counted(void* kv_pool, int64_t layer_stride_bytes, int num_layers, int dtype,
+                         int num_pages, int page_size, int num_kv_heads, int head_dim,
+                         const int32_t* src, const int32_t* dst, const int32_t* len,
+                         const int32_t* count, int max_n, int32_t* err_count, void* stream);
 
 /* be_rope_qkv_append: decode-step rotary embedding fused with the append.
  * qkv is the fused projection [n, (Hq + 2 Hkv) * head_dim] (row stride in

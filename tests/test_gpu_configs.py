@@ -255,6 +255,8 @@ def test_config4_e2e_live_state():
         if (i + 1) % 10 == 0:
             say(f"config 4 e2e: step {i + 1}/40 trie replay equal")
     assert o_alloc.copies, "the run should fork partial pages"
+    # the last selection's fork copies (staged for a next step) into the pages
+    gen.flush()
     # one layer's attention at the live state, on the real pages
     st = gen.state
     lv = st._cascade_lists()

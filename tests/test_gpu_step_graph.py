@@ -119,6 +119,9 @@ def test_step_graph_logits_match_per_layer_path():
     for step in range(3):
         st = gen.state
         n = st.num_candidates()
+        # the previous selection's fork copies (staged for the step graph's first
+        # part) into the pages before either path reads them
+        gen.flush()
         levels, qids, wp, wpos, pos = st.step_metadata()
         dev = torch.device("cuda")
         tok = torch.from_numpy(np.asarray(qids, np.int64)).to(dev)
