@@ -84,6 +84,59 @@ def test_batched_page_copy_all_layers(dtype):
     assert torch.equal(pt.kv_pool, ref)
 
 
+def test_staged_copies_counted_launch_and_graph_replay():
+    """The staged fork-copy list: the counted launch copies exactly the
+    entries below the device count (the rest of the fixed arrays are stale
+    and untouched), eagerly and from one captured launch replayed with two
+    different lists; a bad page id is counted, not written."""
+    say("staged page copies: counted launch, graph replays")
+    from beam_engine_amd import PageTable
+    dt = torch.bfloat16
+    pt = PageTable(3, page_size=16, max_num_pages=40, head_num=2, head_dim=128, device="cuda", store_dtype=dt)
+    g = torch.Generator().manual_seed(9)
+    pt.kv_pool.copy_(torch.randn(pt.kv_pool.shape, generator=g).to(dt))
+    pt.enable_staged_copies(6)
+
+    def expect(base, copies):
+        ref = base.clone()
+        for s_, d_, n_ in copies:
+            ref[:, d_, :, :n_] = base[:, s_, :, :n_]
+        return ref
+
+    # eager: five entries staged, then three -- the arrays keep the stale fourth and fifth
+    pt.stage_copies(np.array([[1, 20, 5], [2, 21, 16], [3, 22, 1], [4, 23, 7], [5, 24, 3]]))
+    pt.run_staged_copies()
+    before = pt.kv_pool.clone()
+    cp = [[6, 25, 9], [7, 26, 16], [8, 27, 2]]
+    pt.stage_copies(np.array(cp))
+    pt.run_staged_copies()
+    torch.cuda.synchronize()
+    assert torch.equal(pt.kv_pool, expect(before, cp))
+    # one captured launch replayed with two lists
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph):
+            pt.record_staged_copies()
+    torch.cuda.current_stream().wait_stream(side)
+    for cp in ([[9, 28, 4], [10, 29, 11]], [[11, 30, 16], [12, 31, 6], [13, 32, 1], [14, 33, 15], [15, 34, 8]]):
+        torch.cuda.synchronize()
+        before = pt.kv_pool.clone()
+        pt.stage_copies(np.array(cp))
+        graph.replay()
+        pt.consume_staged_copies()
+        torch.cuda.synchronize()
+        assert torch.equal(pt.kv_pool, expect(before, cp)), cp
+    # a source page outside the pool is skipped and counted
+    before = pt.kv_pool.clone()
+    pt.stage_copies(np.array([[99, 35, 4], [16, 36, 4]]))
+    pt.run_staged_copies()
+    with pytest.raises(ValueError):
+        pt.check_errors()
+    assert torch.equal(pt.kv_pool, expect(before, [[16, 36, 4]]))
+
+
 def test_copy_block_errors():
     from beam_engine_amd import PageTable
     from beam_engine_amd.page_table import PageCopyError
