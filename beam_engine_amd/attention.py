@@ -116,6 +116,7 @@ class _PagedPlanner:
         self._tail_role = False       # streaming kernel: tail chunks in tail-role workgroups, not the merge kernel
         self._no_regs = False         # streaming kernel: direct-load loop in every workgroup
         self._no_wide = False         # streaming kernel: no wide (32-row) wave roles, no 128-row segments
+        self._no_wide256 = False      # streaming kernel: wide roles on 128-row segments only
         self._rows = None             # row-block kernel: True forces it, False forbids it, None lets the planner pick
         self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
@@ -178,6 +179,7 @@ class _PagedPlanner:
             (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
             (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
             (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0) | \
+            (_lib.BE_PLAN_NO_WIDE256 if self._no_wide256 else 0) | \
             (_lib.BE_PLAN_ROWS if self._rows is True else 0) | \
             (_lib.BE_PLAN_NO_ROWS if self._rows is False else 0)
 

@@ -72,6 +72,7 @@ constexpr int kStageBytes = 2 * kKvBytes + kQBytes;
 constexpr int kLdsStages = kRegStages * kStageBytes;   // the smaller of the two loops' stage buffers
 constexpr int kClassGeneric = 1;              // workgroup-table class: per-segment mode (else the mode 0 or 2)
 constexpr int kClassWide = 5;                 // workgroup-table class of the wide roles (32 rows per wave)
+constexpr int kClassWide256 = 6;              // ... of the 256-row wide roles (32 rows x all tokens per wave)
 constexpr int kNoCausalS = 0x3fffffff;        // segment causal base of a segment without the mask
 constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
 constexpr int kThreads = 64 * kWaves;
@@ -88,6 +89,8 @@ constexpr int kWideRows = 128;               // rows per segment of a long group
 constexpr int kWideMinTiles = 8;              // 128-row tasks for groups of at least this many tiles
 constexpr int kWideMinRun = 64;               // ... when the launch has this many 64-row tiles per workgroup
 constexpr int kWideTileCost = 6;              // planner cost of a 128-row tile (a 64-row tile is 4)
+constexpr int kWide256Rows = 256;             // rows per segment of the 256-row wide tasks
+constexpr int kWide256TileCost = 10;          // planner cost of a 256-row tile
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -216,7 +219,9 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
 // whose time is mostly the pipeline's fill and drain, and for the wide
 // roles).  Three LDS stages; iteration n waits for tile n, issues the loads
 // of tile n + 2 and computes tile n.  FM as for stream_body_regs, or
-// kClassWide: the wide roles (32 rows per wave, segments of up to 128 rows).
+// kClassWide: the wide roles (32 rows per wave, segments of up to 128 rows);
+// kClassWide256: the same with segments of up to 256 rows, every wave over
+// all 64 tokens of a tile.
 template <typename T, int FM>
 __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
                                                 const int* vis_lds, float* ml_lds, int n_segs, int n_tiles) {
@@ -305,7 +310,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
       }
     }
     int ops = 4;                                      // K/V loads per wave per tile
-    if (FM != kClassWide && l_t == 0) {             // wide roles: Q rows go to registers
+    if (FM != kClassWide && FM != kClassWide256 && l_t == 0) {   // wide roles: Q rows go to registers
       const int R = sg.q_count * g;
       const int nq = (R + 3) >> 2;                    // 1 KB loads of 4 rows
       for (int k = w; k < nq; k += kWaves) {
@@ -373,7 +378,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
     // part) collects the others at the end of the segment; mode 3 recomputes
     // the scores in every wave instead, which costs less than that exchange
     // when the segment is short.
-    if constexpr (FM != kClassWide) {
+    if constexpr (FM != kClassWide && FM != kClassWide256) {
     const SegReg& sg = c_sg;
     const int R = sg.q_count * g;
     const int NT = (R + 15) >> 4;
@@ -479,14 +484,16 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
       }
     }
     } else {
-    // ---- wide roles (FM == kClassWide, every segment of the workgroup; up to
-    // 128 rows): wave w takes rows 32 (w & 3) .. +31 as two 16-row MFMA tiles
+    // ---- wide roles (every segment of the workgroup).  kClassWide (up to 128
+    // rows): wave w takes rows 32 (w & 3) .. +31 as two 16-row MFMA tiles
     // sharing each K / V^T fragment read, and tokens 32 (w >> 2) .. +31 of the
-    // tile.  The w < 4 wave of each row group collects its partner's (m, l, o)
+    // tile; the w < 4 wave of each row group collects its partner's (m, l, o)
     // at the end of the segment, one row tile at a time through this stage.
-    // The segment's Q rows go global -> registers on its first tile (up to
-    // 32 KB, more than the stage's Q slot holds).
-    constexpr int TP = 2;                             // token parts
+    // kClassWide256 (up to 256 rows): wave w takes rows 32 w .. +31 and every
+    // token of the tile (two 32-token steps), so a tile is read once per 256
+    // rows and no wave hands over.  The segment's Q rows go global ->
+    // registers on its first tile (more than the stage's Q slot holds).
+    constexpr int TP = FM == kClassWide256 ? 1 : 2;   // token parts
     constexpr int RG = kWaves / TP;                   // 32-row groups
     constexpr int NSUB = 4 / TP;                      // 16-token sub-tiles per part
     const int rg = w % RG, tp = w / RG;
@@ -520,9 +527,17 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
     }
     if (act) {
       const int valid = min(kTok, sg.tok_count - c_t * kTok);
-      const int sub0 = tp * NSUB;
-      tile_compute_w<T, NSUB>(stage + sub0 * 4096, stage + kKvBytes + sub0 * 4096, qf2, koff, voff8, sub0 * 16,
-                              valid, lg, scale, m2, l2, o2);
+      if constexpr (TP == 1) {
+        // tokens 0..31, then 32..63 (the 16-token sub-tile pairs of tile_compute_w)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          tile_compute_w<T, 2>(stage + 2 * h * 4096, stage + kKvBytes + 2 * h * 4096, qf2, koff, voff8, 32 * h,
+                               valid, lg, scale, m2, l2, o2);
+      } else {
+        const int sub0 = tp * NSUB;
+        tile_compute_w<T, NSUB>(stage + sub0 * 4096, stage + kKvBytes + sub0 * 4096, qf2, koff, voff8, sub0 * 16,
+                                valid, lg, scale, m2, l2, o2);
+      }
     }
     if (last) {
       float l[2];
@@ -957,6 +972,8 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
       if (cls == 0) stream_body_dma<T, 0>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
       else if (cls == 2) stream_body_dma<T, 2>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
       else if (cls == kClassWide) stream_body_dma<T, kClassWide>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == kClassWide256)
+        stream_body_dma<T, kClassWide256>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
       else stream_body_dma<T, -1>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
     }
   }
@@ -1222,7 +1239,6 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // into registers, which drains the load pipeline once per segment, and the
   // direct-load loop it runs in fills and drains slower than the
   // register-staged one.)
-  const int q_tile_w = std::max(1, kWideRows / g);
   bool wide = !(flags & BE_PLAN_NO_WIDE) && !caps;
   if (wide) {
     int64_t tiles64 = 0;
@@ -1233,6 +1249,25 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     }
     wide = tiles64 >= (int64_t)kWideMinRun * W;
   }
+  auto wide_group = [&](size_t gi) {
+    const Group& gr = groups[gi];
+    return wide && !is_tail[gi] && gr.kv_len > 0 && gr.q1 > gr.q0 && !is_causal(gr) &&
+           (gr.q1 - gr.q0) * g > kSegRows && ceil_div(gr.kv_len, kTok) >= kWideMinTiles;
+  };
+  // 256-row tasks when every group that takes the wide roles has at least 256
+  // rows (no wave of a 256-row workgroup then idles on a short group's task)
+  bool wide256 = wide && !(flags & BE_PLAN_NO_WIDE256);
+  if (wide256) {
+    bool any = false;
+    for (size_t gi = 0; gi < groups.size() && wide256; ++gi)
+      if (wide_group(gi)) {
+        any = true;
+        wide256 = (groups[gi].q1 - groups[gi].q0) * g >= kWide256Rows;
+      }
+    wide256 = wide256 && any;
+  }
+  const int q_tile_w = std::max(1, (wide256 ? kWide256Rows : kWideRows) / g);
+  const int wide_cost = wide256 ? kWide256TileCost : kWideTileCost;
   struct Task { int q0, qn, page_base, kv_len, head, tiles, tc, vis0; };
   std::vector<Task> tasks;
   int64_t total = 0;
@@ -1242,10 +1277,9 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     if (gr.kv_len <= 0 || gr.q1 <= gr.q0 || is_tail[gi]) continue;
     const bool cz = is_causal(gr);
     any_causal = any_causal || cz;
-    const int tiles_all = (int)ceil_div(gr.kv_len, kTok);
-    const bool w128 = wide && !cz && (gr.q1 - gr.q0) * g > kSegRows && tiles_all >= kWideMinTiles;
+    const bool w128 = wide_group(gi);
     const int qt = w128 ? q_tile_w : q_tile;
-    const int tc = w128 ? kWideTileCost : 4;
+    const int tc = w128 ? wide_cost : 4;
     for (int qa = gr.q0; qa < gr.q1; qa += qt) {
       const int qn = std::min(qt, gr.q1 - qa);
       const int vis0 = cz ? gr.kv_len - (gr.q1 - gr.q0) + (qa - gr.q0) + 1 : kNoCausalS;
@@ -1359,7 +1393,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       const int md = nt >= 3 ? 0 : nt == 2 ? 1 : sgm.n_tiles >= kQuarterTiles ? 2 : 3;
       cls = cls == -2 ? md : cls == md ? cls : -1;
     }
-    wg[b].w = big ? kClassWide : (cls == 0 || cls == 2) ? cls : kClassGeneric;
+    wg[b].w = big ? (wide256 ? kClassWide256 : kClassWide) : (cls == 0 || cls == 2) ? cls : kClassGeneric;
     any_wide = any_wide || big;
   }
 

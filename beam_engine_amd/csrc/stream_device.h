@@ -261,7 +261,8 @@ __device__ __forceinline__ void tile_compute_w(const unsigned char* kt, const un
           x[1][k][i] = -INFINITY;
         }
   }
-  v4s pf[2][NSUB];
+  // row tile 0's softmax and P.V, then row tile 1's: row tile 1's softmax
+  // (VALU) issues while row tile 0's P.V MFMAs execute
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     float mx = -INFINITY;
@@ -279,6 +280,7 @@ __device__ __forceinline__ void tile_compute_w(const unsigned char* kt, const un
       for (int mt = 0; mt < 8; ++mt) o_acc[r][mt] *= alpha;
     }
     m_run[r] = m_new;
+    v4s pf[NSUB];
 #pragma unroll
     for (int k = 0; k < NSUB; ++k) {
       float p[4];
@@ -287,24 +289,22 @@ __device__ __forceinline__ void tile_compute_w(const unsigned char* kt, const un
         p[i] = __builtin_amdgcn_exp2f(x[r][k][i] - msafe);
         l_run[r] += p[i];
       }
-      pf[r][k] = pack4<T>(p[0], p[1], p[2], p[3]);
+      pf[k] = pack4<T>(p[0], p[1], p[2], p[3]);
     }
-  }
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       v4f o = o_acc[r][mt];
       if constexpr (NSUB == 1) {
-        o = mfma_pv<T>(vf[mt][0], pf[r][0], o);
+        o = mfma_pv<T>(vf[mt][0], pf[0], o);
       } else {
 #pragma unroll
         for (int k = 0; k < NSUB; k += 2)
           o = mfma_qk<T>(__builtin_shufflevector(vf[mt][k], vf[mt][k + 1], 0, 1, 2, 3, 4, 5, 6, 7),
-                         __builtin_shufflevector(pf[r][k], pf[r][k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
+                         __builtin_shufflevector(pf[k], pf[k + 1], 0, 1, 2, 3, 4, 5, 6, 7), o);
       }
       o_acc[r][mt] = o;
     }
+  }
 }
 
 }  // namespace stream

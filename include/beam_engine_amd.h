@@ -161,6 +161,8 @@ typedef struct be_level {
                                     and all their groups on every level; no partials, one
                                     kernel) whenever it applies                             */
 #define BE_PLAN_NO_ROWS 512      /* never the row-block kernel                               */
+#define BE_PLAN_NO_WIDE256 1024  /* streaming kernel: wide roles on 128-row segments only    */
+                                 /* (no 256-row segments for groups of >= 256 rows)         */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the

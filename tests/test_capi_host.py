@@ -244,8 +244,8 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             assert s0 == istart and tiles == 0
             istart += ns
             continue
-        # wave-role mode 0 / 2, per segment (1), wide roles over up to 128 rows (5)
-        assert cls in (0, 1, 2, 5)
+        # wave-role mode 0 / 2, per segment (1), wide roles over up to 128 (5) or 256 rows (6)
+        assert cls in (0, 1, 2, 5, 6)
         if ns:
             assert s0 == start
             assert tiles == segs[s0:s0 + ns, 7].sum()
@@ -253,6 +253,8 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             rows = segs[s0:s0 + ns, 1] * g
             if cls == 5:
                 assert (rows > 64).any() and (rows <= 128).all()
+            elif cls == 6:
+                assert (rows > 64).any() and (rows <= 256).all()
             else:
                 assert (rows <= 64).all()
         start += ns
@@ -260,7 +262,7 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
     # 64-aligned start; tail chunks: up to 16 tokens of one page), page by page
     seen = [[Counter() for _ in range(hkv)] for _ in range(nq)]
     for q0, qn, pb, t0, tc, head, slot, nt in segs:
-        assert tc > 0 and qn > 0 and qn * g <= 128 and t0 % 64 == 0 and nt == -(-tc // 64)
+        assert tc > 0 and qn > 0 and qn * g <= 256 and t0 % 64 == 0 and nt == -(-tc // 64)
         keys = [(int(pages[pb + t // page]), t % page) for t in range(t0, t0 + tc)]
         for q in range(q0, q0 + qn):
             seen[q][head].update(keys)
@@ -309,7 +311,8 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
     # the loop: register-staged when the longest run reaches 8 tiles (never for fixed layouts
     # nor with wide-role workgroups, which run in the direct-load loop)
     assert info.stream_loop == (1 if int(wg[wg[:, 3] != TAIL_ROLE, 2].max(initial=0)) >= 8
-                                and not info.static_layout and not (wg[:, 3] == 5).any() else 0)
+                                and not info.static_layout and not ((wg[:, 3] == 5) | (wg[:, 3] == 6)).any()
+                                else 0)
     return wg, segs, recs, rslots
 
 
@@ -360,12 +363,14 @@ def test_stream_plan_balances_tiles_across_workgroups(cus):
     assert info.num_merge == 32 * hkv           # every (query, head) merges prefix and suffix
 
 
-@pytest.mark.parametrize("beams,cus", [(32, 256), (32, 5), (18, 4), (64, 13), (64, 5), (10, 5)])
+@pytest.mark.parametrize("beams,cus", [(32, 256), (32, 5), (18, 4), (64, 13), (64, 5), (10, 5), (80, 5)])
 def test_stream_plan_wide_roles(beams, cus):
-    """Long groups of more than 64 rows go to 128-row segments in wide-role
-    workgroups (class 5) when the launch gives every workgroup a long run (at
-    least 64 tiles of 64 rows each); BE_PLAN_NO_WIDE keeps 64-row segments;
-    every (query, KV head) still sees exactly its tokens."""
+    """Long groups of more than 64 rows go to wide-role workgroups when the
+    launch gives every workgroup a long run (at least 64 tiles of 64 rows
+    each): 256-row segments (class 6) when every such group has at least 256
+    rows, else 128-row segments (class 5); BE_PLAN_NO_WIDE256 keeps the
+    128-row ones, BE_PLAN_NO_WIDE 64-row segments; every (query, KV head)
+    still sees exactly its tokens."""
     hq, hkv, page = 32, 8, 16
     pre, suf = 96, 3                            # 1536-token prefix, 48-token suffixes
     qo0, kvp0, kvi0 = [0, beams], [0, pre], list(range(pre))
@@ -376,16 +381,20 @@ def test_stream_plan_wide_roles(beams, cus):
     g = hq // hkv
     tiles64 = (pre * page // 64) * -(-beams * g // 64) * hkv
     expect = beams * g > 64 and tiles64 >= 64 * cus
-    for flags in (0, 64):
+    for flags in (0, 64, 1024):
         rc, info, buf, _lib, L = plan(levels, nq=beams, hq=hq, hkv=hkv, page=page, num_pages=pre + beams * suf,
                                       cus=cus, flags=flags)
         assert rc == 0, L.be_last_error()
         wg, segs, recs, rslots = check_stream_plan(levels, beams, hq, hkv, page, info, buf)
         rows = segs[:, 1] * g
-        if flags or not expect:
-            assert (rows <= 64).all() and not (wg[:, 3] == 5).any()
+        if flags == 64 or not expect:
+            assert (rows <= 64).all() and not ((wg[:, 3] == 5) | (wg[:, 3] == 6)).any()
+        elif beams * g >= 256 and flags == 0:
+            assert rows.max() > 128 and rows.max() <= 256 and (wg[:, 3] == 6).any() and not (wg[:, 3] == 5).any()
+            assert info.stream_loop == 0
         else:
-            assert rows.max() > 64 and (wg[:, 3] == 5).any() and info.stream_loop == 0
+            assert rows.max() > 64 and rows.max() <= 128 and (wg[:, 3] == 5).any() and not (wg[:, 3] == 6).any()
+            assert info.stream_loop == 0
 
 
 def test_stream_plan_zero_records_for_keyless_queries():

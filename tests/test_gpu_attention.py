@@ -46,11 +46,12 @@ def make_q(n, hq, d, dtype, seed, scale=1.0):
 
 
 def run_cascade(ws, q, kv, levels, page, force_valu=False, return_lse=True, fused_merge=False, tile_kernel=False,
-                num_cus=None, no_regs=False, no_wide=False):
+                num_cus=None, no_regs=False, no_wide=False, no_wide256=False):
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper
     w = MultiLevelCascadeAttentionWrapper(len(levels[0]), ws)
     w._no_regs = no_regs
     w._no_wide = no_wide
+    w._no_wide256 = no_wide256
     w._force_valu = force_valu
     w._fused_merge = fused_merge
     w._tile_kernel = tile_kernel
@@ -345,21 +346,23 @@ def test_stream_and_tile_kernels(ws, shape, kernel, num_cus):
     if kernel != "tile":
         info = w._info
         wg = w._plan_dev[info.off_wg: info.off_wg + 4 * info.num_wg].view(-1, 4).cpu()
-        wide = bool(((wg[:, 3] == 4) | (wg[:, 3] == 5)).any())
+        wide = bool(((wg[:, 3] == 4) | (wg[:, 3] == 5) | (wg[:, 3] == 6)).any())
         assert info.stream_loop == (1 if kernel == "stream" and int(wg[:, 2].max()) >= 8 and not wide else 0)
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
 
 
-@pytest.mark.parametrize("case", ["rows72", "rows100", "rows128", "rows256_g8", "mixed"])
+@pytest.mark.parametrize("case", ["rows72", "rows100", "rows128", "rows256_g8", "rows512_g8", "rows296_g8", "mixed"])
 @pytest.mark.parametrize("cus", [None, 4, 7, 13])
 def test_stream_wide_roles(ws, case, cus):
-    """Wide wave roles (32 rows per wave, 128-row segments of long groups of
-    more than 64 rows) against the oracle and against the plan without them,
-    with ragged token counts (partial last tiles, split segments), row counts
-    that leave row groups empty, and shorter groups in the same launch.  They
-    apply when every workgroup's run is long (few CUs here); with all 256 CUs
-    the same shapes take 64-row segments."""
+    """Wide wave roles (32 rows per wave: 128-row segments of long groups of
+    more than 64 rows, or 256-row segments, every wave over all tokens, when
+    every such group has at least 256 rows) against the oracle and against the
+    plans without them, with ragged token counts (partial last tiles, split
+    segments), row counts that leave row groups empty (296 rows: a 40-row
+    remainder segment), and shorter groups in the same launch.  They apply
+    when every workgroup's run is long (few CUs here); with all 256 CUs the
+    same shapes take 64-row segments."""
     say(f"wide roles {case} cus={cus}")
     page, hkv, d = 16, 8, 128
     hq = 64 if case.endswith("g8") else 32
@@ -394,11 +397,24 @@ def test_stream_wide_roles(ws, case, cus):
     wg = w._plan_dev[info.off_wg: info.off_wg + 4 * info.num_wg].view(-1, 4).cpu()
     tiles64 = sum(-(-p // 64) * -(-b * g // 64) * hkv for b, p in zip(beams, prefixes))
     expect = any(b * g > 64 for b in beams) and tiles64 >= 64 * info.num_wg
-    assert bool((wg[:, 3] == 5).any()) == expect
+    w256 = expect and all(b * g >= 256 for b in beams if b * g > 64)
+    if w.stats.kernel != "stream":
+        # more segments than a workgroup's table holds (512 rows of 1-query suffix
+        # groups over 4 CUs): the planner falls back to the tile kernel
+        assert cus is not None and cus <= 4
+        expect = w256 = False
+    assert bool((wg[:, 3] == 5).any()) == (expect and not w256)
+    assert bool((wg[:, 3] == 6).any()) == w256
     ref_o, ref_lse = oa.cascade_attention(q, kv, *levels, page, d ** -0.5)
     check(out, lse, ref_o, ref_lse, torch.bfloat16)
     (out2, lse2), _ = run_cascade(ws, q, kv, levels, page, num_cus=cus, no_wide=True)
     torch.testing.assert_close(out.float(), out2.float(), rtol=2e-2, atol=1e-2)
+    if w256:
+        (out3, lse3), w3 = run_cascade(ws, q, kv, levels, page, num_cus=cus, no_wide256=True)
+        i3 = w3._info
+        wg3 = w3._plan_dev[i3.off_wg: i3.off_wg + 4 * i3.num_wg].view(-1, 4).cpu()
+        assert (wg3[:, 3] == 5).any() and not (wg3[:, 3] == 6).any()
+        torch.testing.assert_close(out.float(), out3.float(), rtol=2e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
