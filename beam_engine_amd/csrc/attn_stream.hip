@@ -353,6 +353,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
   v8s qf[4];
   float m2[2] = {-INFINITY, -INFINITY}, l2[2] = {0.f, 0.f};   // wide roles
   v4f o2[2][8];
+  v4f lw[2];                                                    // 256-row wide roles: row sums
   v8s qf2[2][4];
   int st_c = 0, st_l = 2;            // stages of the computed and the next loaded tile
 
@@ -507,6 +508,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
       for (int r = 0; r < 2; ++r) {
         m2[r] = -INFINITY;
         l2[r] = 0.f;
+        lw[r] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) o2[r][mt] = v4f{0.f, 0.f, 0.f, 0.f};
       }
@@ -528,11 +530,7 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
     if (act) {
       const int valid = min(kTok, sg.tok_count - c_t * kTok);
       if constexpr (TP == 1) {
-        // tokens 0..31, then 32..63 (the 16-token sub-tile pairs of tile_compute_w)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          tile_compute_w<T, 2>(stage + 2 * h * 4096, stage + kKvBytes + 2 * h * 4096, qf2, koff, voff8, 32 * h,
-                               valid, lg, scale, m2, l2, o2);
+        tile_compute_w64<T>(stage, stage + kKvBytes, qf2, koff, voff8, valid, lg, scale, m2, lw, o2);
       } else {
         const int sub0 = tp * NSUB;
         tile_compute_w<T, NSUB>(stage + sub0 * 4096, stage + kKvBytes + sub0 * 4096, qf2, koff, voff8, sub0 * 16,
@@ -543,8 +541,8 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
       float l[2];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        l[r] = l2[r];
-        l[r] = rows4_sum(l[r]);
+        // (256-row roles: every lane's l is the whole row's, from the MFMA pipe)
+        l[r] = TP == 1 ? lw[r][0] : rows4_sum(l2[r]);
       }
       // (TP - 1) * RG = 4 waves hand over 8 KB each per row tile (32 KB of the stage's 48)
 #pragma unroll

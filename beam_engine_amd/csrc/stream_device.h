@@ -307,5 +307,95 @@ __device__ __forceinline__ void tile_compute_w(const unsigned char* kt, const un
   }
 }
 
+// The 256-row wide roles' step: one wave's two 16-row MFMA tiles (32 rows)
+// against a whole 64-token tile.  The scores of all 64 tokens come first (K
+// fragments read in two 32-token halves to bound the registers), then one
+// softmax step per row tile (one max reduction and one rescale check per
+// tile), then P.V in two halves.  The scale enters the exponent as one FMA
+// (p = 2^(s x - m) with m kept in the scaled domain), and the row sums l come
+// from the MFMA pipe: a ones operand in place of V^T gives sum_t P[row][t] in
+// every lane of the row (of the same 16-bit P that P.V uses), accumulated and
+// rescaled like o.
+template <typename T>
+__device__ __forceinline__ void tile_compute_w64(const unsigned char* kt, const unsigned char* vt,
+                                                 const v8s (&qf)[2][4], const uint32_t (&koff)[4],
+                                                 const uint32_t (&voff)[8], int valid, int lg, float scale,
+                                                 float (&m_run)[2], v4f (&l_acc)[2], v4f (&o_acc)[2][8]) {
+  float x[2][4][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v8s kf[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        kf[k][ks] = *reinterpret_cast<const v8s*>(kt + (2 * h + k) * 4096 + koff[ks]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma_qk<T>(kf[k][ks], qf[r][ks], acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[r][2 * h + k][i] = acc[i];
+      }
+  }
+  if (valid < kTok) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (k * 16 + 4 * lg + i >= valid) {
+          x[0][k][i] = -INFINITY;
+          x[1][k][i] = -INFINITY;
+        }
+  }
+  v4s pf[2][4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mx = fmaxf(mx, fmaxf(fmaxf(x[r][k][0], x[r][k][1]), fmaxf(x[r][k][2], x[r][k][3])));
+    mx = rows4_max(mx) * scale;                       // the scaled (log2-domain) max; scale > 0
+    const float m_new = fmaxf(m_run[r], mx);
+    const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run[r]) != 0) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run[r] - msafe);
+      l_acc[r] *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) o_acc[r][mt] *= alpha;
+    }
+    m_run[r] = m_new;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[r][k][i], scale, -msafe));
+      pf[r][k] = pack4<T>(p[0], p[1], p[2], p[3]);
+    }
+  }
+  constexpr short kOne = __is_same(T, bf16_t) ? (short)0x3F80 : (short)0x3C00;   // 1.0 in T
+  const v8s ones = {kOne, kOne, kOne, kOne, kOne, kOne, kOne, kOne};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v4s vf[8][2];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        vf[mt][k] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)(vt + (2 * h + k) * 4096 + voff[mt]));
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const v8s pp = __builtin_shufflevector(pf[r][2 * h], pf[r][2 * h + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      l_acc[r] = mfma_qk<T>(ones, pp, l_acc[r]);
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+        o_acc[r][mt] = mfma_qk<T>(__builtin_shufflevector(vf[mt][0], vf[mt][1], 0, 1, 2, 3, 4, 5, 6, 7), pp,
+                                  o_acc[r][mt]);
+    }
+  }
+}
+
 }  // namespace stream
 }  // namespace be
