@@ -75,7 +75,10 @@ static TopkGeom topk_geom(int n_rows, int vocab, int k) {
 
 // Bytes of the arrival counters at the start of the workspace: one u32 per
 // row and one per request (at most 512 requests take the one-launch path).
-inline int64_t topk_counter_bytes(int n_rows) { return (((int64_t)n_rows + 512) * 4 + 255) / 256 * 256; }
+// Counter words at the start of the workspace: one arrival counter per request
+// (at most 512 requests take the two-launch path).
+constexpr int kTopkCounterWords = 512;
+inline int64_t topk_counter_bytes(int) { return ((int64_t)kTopkCounterWords * 4 + 255) / 256 * 256; }
 
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p) { return to_f32(*p); }
@@ -325,9 +328,11 @@ __device__ __forceinline__ uint32_t key32_of16(uint32_t k16) {
 }
 
 // Block-wide inclusive suffix sum (over threads >= tid) of one int per
-// thread: shuffles inside each wave, then the wave totals through LDS (two
-// barriers instead of a barrier pair per doubling step).
-__device__ __forceinline__ int block_suffix_sum(int v, int* tot /*4*/) {
+// thread of an NT-thread block: shuffles inside each wave, then the wave
+// totals through LDS (two barriers instead of a barrier pair per doubling
+// step).  tot holds NT / 64 ints.
+template <int NT = kTopkThreads>
+__device__ __forceinline__ int block_suffix_sum(int v, int* tot) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -336,7 +341,7 @@ __device__ __forceinline__ int block_suffix_sum(int v, int* tot /*4*/) {
   }
   if (lane == 0) tot[w] = v;
   __syncthreads();
-  for (int x = w + 1; x < 4; ++x) v += tot[x];
+  for (int x = w + 1; x < NT / 64; ++x) v += tot[x];
   __syncthreads();
   return v;
 }
@@ -700,27 +705,29 @@ __global__ __launch_bounds__(kTopkThreads, kCandWavesPerSimd) void topk_cand16_k
 // equal to it the lowest indices (a second radix select, over inverted
 // indices, only when the ties exceed what is needed).  Writes the k chosen
 // (key, idx) pairs to out_key / out_idx (LDS, unordered).  All threads call it.
-template <typename KeyF, typename IdxF>
+template <int NT = kTopkThreads, typename KeyF, typename IdxF>
 __device__ void select_k(KeyF key_of, IdxF idx_of, int n, int k, uint32_t* out_key, int32_t* out_idx,
-                         int* hist /*4*256*/, int* suf /*257*/, int* misc /*8*/) {
+                         int* hist /*4*256*/, int* suf /*257*/, int* misc /*4 + NT/64*/) {
   const int tid = threadIdx.x, w = tid >> 6;
   auto radix = [&](auto val_of, auto live, int want, uint32_t& prefix_out) -> int {
     // returns how many of the `want` remain at the selected value prefix_out
     uint32_t prefix = 0, mask = 0;
     int krem = want;
     for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid; i < 4 * 256; i += kTopkThreads) hist[i] = 0;
+      for (int i = tid; i < 4 * 256; i += NT) hist[i] = 0;
       __syncthreads();
-      for (int i = tid; i < n; i += kTopkThreads) {
+      for (int i = tid; i < n; i += NT) {
         if (!live(i)) continue;
         const uint32_t v = val_of(i);
-        if ((v & mask) == prefix) atomicAdd(&hist[w * 256 + (int)((v >> shift) & 255u)], 1);
+        if ((v & mask) == prefix) atomicAdd(&hist[(w & 3) * 256 + (int)((v >> shift) & 255u)], 1);
       }
       __syncthreads();
-      suf[tid] = block_suffix_sum(hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid], misc + 4);
+      const int hv = tid < 256 ? hist[tid] + hist[256 + tid] + hist[512 + tid] + hist[768 + tid] : 0;
+      const int sv = block_suffix_sum<NT>(hv, misc + 4);
+      if (tid < 256) suf[tid] = sv;
       if (tid == 0) suf[256] = 0;
       __syncthreads();
-      if (suf[tid] >= krem && suf[tid + 1] < krem) {
+      if (tid < 256 && suf[tid] >= krem && suf[tid + 1] < krem) {
         misc[0] = tid;
         misc[1] = suf[tid + 1];
       }
@@ -741,7 +748,7 @@ __device__ void select_k(KeyF key_of, IdxF idx_of, int n, int k, uint32_t* out_k
     misc[3] = 0;
   }
   __syncthreads();
-  for (int i = tid; i < n; i += kTopkThreads) {
+  for (int i = tid; i < n; i += NT) {
     const uint32_t v = key_of(i);
     if (v > T) {
       const int at = atomicAdd(&misc[2], 1);
@@ -756,7 +763,7 @@ __device__ void select_k(KeyF key_of, IdxF idx_of, int n, int k, uint32_t* out_k
   if (nties == krem) {
     if (tid == 0) misc[2] = ngt;
     __syncthreads();
-    for (int i = tid; i < n; i += kTopkThreads)
+    for (int i = tid; i < n; i += NT)
       if (key_of(i) == T) {
         const int at = atomicAdd(&misc[2], 1);
         out_key[at] = T;
@@ -768,7 +775,7 @@ __device__ void select_k(KeyF key_of, IdxF idx_of, int n, int k, uint32_t* out_k
     radix([&](int i) { return 0xffffffffu - (uint32_t)idx_of(i); }, [&](int i) { return key_of(i) == T; }, krem, I);
     if (tid == 0) misc[2] = ngt;
     __syncthreads();
-    for (int i = tid; i < n; i += kTopkThreads)
+    for (int i = tid; i < n; i += NT)
       if (key_of(i) == T && 0xffffffffu - (uint32_t)idx_of(i) >= I) {
         const int at = atomicAdd(&misc[2], 1);
         out_key[at] = T;
@@ -1083,32 +1090,42 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pool_kernel(int n_rows, int
 // The three passes above as two launches for 16-bit logits, with the same
 // results:
 //  * pass A (topk_units16_kernel): per (row, segment) unit the statistics and
-//    the candidates of pass 1, unsorted; a few workgroups per CU take the
-//    units in turn and load the next unit while computing the current one.
-//  * pass B (topk_rows16_kernel, one workgroup per row): the row's selection
-//    -- the k-th best logp among the candidates by a radix select on 16-bit
-//    logp keys over register-held candidates, the entries above it and its
-//    ties by lowest index, or the same exact fallback over all logits as
-//    pass 2 -- and, in the workgroup that completes a request's last row (an
-//    arrival counter per request), pass 3 for the request.
-// Every pass issues all of its loads before using any: one memory round trip
-// each.  The row lists go to the pool through agent-scope stores and loads
-// (written through to the device's point of coherence).
-// Arrival counters (u32 at the start of the workspace) are zero at rest: a
-// launch adds one per arrival (a plain atomic add) and the last arrival sets
-// the word back to zero, so every complete launch leaves them zero.  A
-// workspace must therefore hold zeros there before its first use (the Python
-// workspace is allocated zeroed; the static scratch of be_beam_topk_noalloc
-// starts zeroed).
-constexpr int kFusedRowCand = 2048;    // segs x cap of one row (register-held, 8 per thread)
+//    the candidates of pass 1, unsorted.  A few workgroups per CU take units
+//    in turn and load the next unit while computing the current one (a
+//    counter handing out units measured far slower: every workgroup's claims
+//    queue on one device-scope atomic).  A wave sums e^x' against
+//    0, so that no maximum is needed first and each 16-byte chunk of logits is
+//    summed as it lands; only a wave whose largest x' lies outside
+//    [-600, 600] sums against that maximum instead, and the unit records it.
+//  * pass B (topk_rows16_kernel, one workgroup of sixteen waves per row): the
+//    row's log-sum-exp from the unit sums; the k-th largest x' among the
+//    candidates by a radix select over their 16-bit keys, run while wave 0
+//    takes the logarithm (logp is non-decreasing in x', so the k-th largest
+//    logp is the logp of the k-th largest x'); the entries above that logp and
+//    its ties of lowest index, ordered by counting; or the exact selection
+//    over all logits.  The workgroup that completes a request's last row (an
+//    arrival counter per request) then runs pass 3 for the request.
+// Row lists go to the pool through agent-scope stores and loads (written
+// through to the device's point of coherence).
+// Arrival counters (u32 at the start of the workspace, one per request) are
+// zero at rest: a launch adds one per arrival and the last arrival sets the
+// word back to zero, so every complete launch leaves them zero.  A workspace must therefore hold zeros
+// there before its first use (the Python workspace is allocated zeroed; the
+// static scratch of be_beam_topk_noalloc starts zeroed).
+constexpr int kFusedRowCand = 2048;    // segs x cap of one row (two per pass-B thread)
 constexpr int kFusedPool = 512;        // rows x min(k, beam) of one request, in LDS
 constexpr int kFusedPoolRows = 256;
 constexpr int kFusedReqs = 512;
 constexpr int kFusedTie = 256;
-constexpr int kUnitWgPerCu = 4;        // pass A workgroups per CU (two units each at the e2e shape)
+constexpr int kUnitWgPerCu = 4;        // pass A workgroups per CU
 constexpr int kUnitWavesPerSimd = 4;
-static_assert(kFusedReqs == 512, "topk_counter_bytes reserves one counter per request for 512 requests");
-static_assert(kFusedRowCand % kTopkThreads == 0, "row candidates are spread evenly over the threads");
+constexpr int kRowThreads = 1024;      // pass B workgroup
+constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kRowCandPer = kFusedRowCand / kRowThreads;
+constexpr int kPoolSurv = 32;           // pool entries ranked exactly after the sample bound
+static_assert(kFusedReqs <= kTopkCounterWords, "topk_counter_bytes reserves one counter per request");
+static_assert(kFusedRowCand % kRowThreads == 0, "row candidates are spread evenly over the threads");
+static_assert(kFusedPool <= kRowThreads, "one pool entry per pass-B thread");
 
 struct FusedTopkArgs {
   const void* logits;
@@ -1118,9 +1135,9 @@ struct FusedTopkArgs {
   float* seg_max;
   double* seg_sum;
   int* seg_cnt;
-  uint32_t* seg_bound;
+  uint32_t* seg_bound;                 // bits 0..15: boundary key; bit 31: the sum is against seg_max, not 0
   uint64_t* cand;
-  uint32_t* ctr;                       // n_rows row counters, then n_req request counters
+  uint32_t* ctr;                       // one arrival counter per request
   float* row_vals;
   int32_t* row_idx;
   const double* parent;
@@ -1134,9 +1151,6 @@ struct FusedTopkArgs {
 // Stores written through to the device's coherence point and loads that read
 // there (agent scope): another workgroup of the same launch reads them after
 // an arrival counter says they are complete.
-__device__ __forceinline__ void st_wt(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_wt(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1144,20 +1158,11 @@ __device__ __forceinline__ void st_wt(int32_t* p, int32_t v) { st_wt(reinterpret
 __device__ __forceinline__ void st_wt(float* p, float v) {
   st_wt(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
 }
-__device__ __forceinline__ void st_wt(double* p, double v) {
-  st_wt(reinterpret_cast<uint64_t*>(p), (uint64_t)__double_as_longlong(v));
-}
-__device__ __forceinline__ uint64_t ld_co(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ uint32_t ld_co(const uint32_t* p) {
   return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ int32_t ld_co(const int32_t* p) { return (int32_t)ld_co(reinterpret_cast<const uint32_t*>(p)); }
 __device__ __forceinline__ float ld_co(const float* p) { return __uint_as_float(ld_co(reinterpret_cast<const uint32_t*>(p))); }
-__device__ __forceinline__ double ld_co(const double* p) {
-  return __longlong_as_double((long long)ld_co(reinterpret_cast<const uint64_t*>(p)));
-}
 
 // Counts one arrival on ctr and returns the count including it; the word
 // returns to zero when the count reaches total.
@@ -1170,12 +1175,16 @@ __device__ __forceinline__ uint32_t arrive(uint32_t* ctr, uint32_t total) {
 // The 16-bit order key of a 16-bit float pattern.
 __device__ __forceinline__ uint32_t key16_of_bits(uint32_t bits16) { return key16x2(bits16) & 0xffffu; }
 
+// The 16-bit float pattern of a 16-bit order key.
+__device__ __forceinline__ uint16_t bits_of_key16(uint32_t k16) {
+  return (uint16_t)((k16 & 0x8000u) ? (k16 ^ 0x8000u) : (~k16 & 0xffffu));
+}
+
 // x' of a 16-bit order key (keys at or below that of -inf give -inf).
 template <typename T>
 __device__ __forceinline__ float value_of_key16(uint32_t k16) {
   const uint32_t kninf = key16_of_bits(__is_same(T, bf16_t) ? 0xff80u : 0xfc00u);
-  return k16 > kninf ? to_f32(__builtin_bit_cast(T, (uint16_t)((k16 & 0x8000u) ? (k16 ^ 0x8000u) : (~k16 & 0xffffu))))
-                     : -INFINITY;
+  return k16 > kninf ? to_f32(__builtin_bit_cast(T, bits_of_key16(k16))) : -INFINITY;
 }
 
 // The 16-bit order key of logp(x') (logp is rounded to the logits' format).
@@ -1184,374 +1193,150 @@ __device__ __forceinline__ uint32_t logp_key16(float xs, float m, float L) {
   return key16_of_bits(bits_of<T>(logp_of<T>(xs, m, L)));
 }
 
-// Float64 sum of e^(x' - mh) over words [W0, W1) of a thread's logits, mh
-// their largest x'; NaN patterns (positions past the segment) give e^-708.  Four exps are interleaved at a time: enough
-// independent work per wave at eight waves per SIMD, within its register
-// budget.
+// ---------------------------------------------------------------- float64 exp, 256-entry table
+// e^d for d in [-708, 708] (callers clamp), Tang's method as exp_neg with a
+// 256-entry table: k = rint(d 256 / ln 2), r = d - k ln2/256 (Cody-Waite; the
+// high part has 32 significant bits, so k times it is exact for |k| < 2^21),
+// e^r - 1 by its degree-4 Taylor polynomial (|r| <= ln2/512: the first omitted
+// term, r^5/120, is below 4e-17), times 2^((k mod 256) / 256) from the table
+// and 2^floor(k / 256) added to the entry's exponent.
+constexpr double kInvLn2x256 = 0x1.71547652b82fep+8;
+constexpr double kLn2By256Hi = 0x1.62e42feep-9;
+constexpr double kLn2By256Lo = 0x1.a39ef35793c76p-41;
+
+__device__ __forceinline__ void exp_table256_init(double* tab) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = exp2((double)i / 256.0);
+}
+
+__device__ __forceinline__ double exp_t256(double d, const double* tab) {
+  const double sh = fma(d, kInvLn2x256, kRoundShift);
+  const int k = (int)(uint32_t)(uint64_t)__double_as_longlong(sh);
+  const double kf = sh - kRoundShift;
+  double r = fma(-kf, kLn2By256Hi, d);
+  r = fma(-kf, kLn2By256Lo, r);
+  double p = fma(r, 1.0 / 24.0, 1.0 / 6.0);
+  p = fma(r, p, 0.5);
+  p = fma(r, p, 1.0);
+  p *= r;                                           // e^r - 1
+  const uint64_t tb = (uint64_t)__double_as_longlong(tab[k & 255]);
+  const uint32_t hi = (uint32_t)(tb >> 32) + ((uint32_t)(k >> 8) << 20);
+  const double t = __longlong_as_double((long long)(((uint64_t)hi << 32) | (uint32_t)tb));
+  return fma(t, p, t);
+}
+
+// acc + the float64 sum of e^x' over words [W0, W1) of a thread's logits,
+// against 0.  x' below -650 (and -inf, and the NaN patterns past the segment)
+// count as e^-650: nothing against a sum that an x' of at least -600 adds e^-600
+// to.  Four exps at a time, each group's arguments chained to the previous
+// group's sum, so that the compiler cannot start every range reduction at once
+// (which spills).
 template <typename T, int W0, int W1>
-__device__ __forceinline__ double half_exp_sum(const SegVals<T>& x, const double* tab, float mh) {
-  double md = (double)mh;
-  double acc = 0.0;
+__device__ __forceinline__ double exp_sum0(SegVals<T>& x, const double* tab, double acc) {
 #pragma unroll
-  for (int j0 = 2 * W0; j0 < 2 * W1; j0 += 4) {
+  for (int i = W0; i < W1; i += 2) {
+    asm volatile("" : "+v"(acc), "+v"(x.w[i]), "+v"(x.w[i + 1]));
 #pragma unroll
-    for (int j = j0; j < j0 + 4; ++j) acc += exp_neg((double)x.at(j) - md, tab);
-    // the next group's arguments depend on this group's sum: the compiler
-    // cannot start every exp's range reduction at once (which spills)
-    asm volatile("" : "+v"(acc), "+v"(md));
+    for (int j = 2 * i; j < 2 * i + 4; ++j) acc += exp_t256((double)fmaxf(x.at(j), -650.0f), tab);
   }
-  return mh == -INFINITY ? 0.0 : acc;
+  return acc;
 }
 
-// LDS of pass B.
-struct FusedLds {
-  float mL[2];
-  int flag, nabove, ntie, exact, req;
-  int off[kMaxSegs + 1];
-  uint32_t sbound[kMaxSegs];
-  int req_ptr[kFusedReqs + 1];
-  union {
-    struct {                                       // a row's selection
-      double terms[kMaxSegs];
-      int hist[256];
-      int suf[257];
-      int misc[8];
-      uint64_t fin[kMaxK];
-      uint64_t tg[kFusedTie];
-    } row;
-    struct {                                       // the exact fallback of a row
-      int hist[4 * 256];
-      int suf[257];
-      int misc[8];
-      uint32_t skey[kMaxK];
-      int32_t sidx[kMaxK];
-    } ex;
-    struct {                                       // a request's pool
-      double tot[kFusedPool];
-      int32_t idx[kFusedPool];
-      int sel[kFusedPoolRows];
-      int first[kFusedPoolRows + 1];
-    } pool;
-  } u;
-};
-
-// Row r's selection from its segments' statistics and candidates (every
-// thread of the workgroup; ends with a barrier).  Writes row_vals / row_idx
-// through to the device's point of coherence.
-template <typename T>
-__device__ void fused_row(const FusedTopkArgs& a, int r, FusedLds& sm) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int segs = a.segs, k = a.k, cap = a.cap;
-  const int64_t base = (int64_t)r * segs;
-  const int lcap = __ffs(cap) - 1;
-  const int nslots = segs << lcap;
-  // one round trip: the segments' statistics (wave 0), every candidate slot
-  // of the row (slots past a segment's count hold stale words: unused) and
-  // the request pointers (pass B's request lookup)
-  constexpr int kQ = kFusedRowCand / kTopkThreads;
-  uint64_t cv[kQ];
-  const uint64_t* blk = a.cand + base * cap;
+// The float64 sum of e^(x' - mw) over a thread's logits given as 16-bit keys
+// (0 when mw is -inf): the sum of a wave whose largest x', mw, lies outside
+// [-600, 600].
+template <typename T, int NW>
+__device__ __forceinline__ double exp_sum_keys(const uint32_t (&kp)[NW], float mw, const double* tab) {
+  double acc = 0.0, md = (double)mw;
 #pragma unroll
-  for (int q = 0; q < kQ; ++q) cv[q] = ld_co(blk + min(q * kTopkThreads + tid, nslots - 1));
-  float ms = -INFINITY;
-  double ss = 0.0;
-  int c = 0;
-  uint32_t bd = 0;
-  const int n_req = a.beam > 0 ? a.n_req : 0;
-  for (int i = tid; i <= n_req; i += kTopkThreads)
-    sm.req_ptr[i] = a.req_row_ptr ? a.req_row_ptr[i] : (i == 0 ? 0 : a.n_rows);
-  if (tid < 64) {
-    const int li = min(lane, segs - 1);
-    ms = ld_co(a.seg_max + base + li);
-    ss = ld_co(a.seg_sum + base + li);
-    c = ld_co(a.seg_cnt + base + li);
-    bd = ld_co(a.seg_bound + base + li);
+  for (int i = 0; i < NW; ++i) {
+    uint32_t u = kp[i];
+    asm volatile("" : "+v"(acc), "+v"(u));
+    acc += exp_t256(fmax((double)value_of_key16<T>(u & 0xffffu) - md, -700.0), tab);
+    acc += exp_t256(fmax((double)value_of_key16<T>(u >> 16) - md, -700.0), tab);
   }
-  if (tid < 64) {
-    const bool in = lane < segs;
-    if (!in) {
-      ms = -INFINITY;
-      ss = 0.0;
-      c = 0;
-    }
-    if (in) sm.sbound[lane] = bd;
-    const float mm = wave_max(ms);
-    sm.u.row.terms[lane] = in ? ss * exp((double)ms - (double)mm) : 0.0;
-    int incl = c < 0 ? 0 : c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += v;
-    }
-    if (in) sm.off[lane + 1] = incl;
-    // an overflowed segment, or fewer candidates than k: the exact selection
-    const bool over = __builtin_amdgcn_ballot_w64(c < 0) != 0 || __shfl(incl, segs - 1, 64) < k;
-    if (lane == 0) {
-      sm.off[0] = 0;
-      sm.exact = over ? 1 : 0;
-      sm.nabove = 0;
-      sm.ntie = 0;
-      double S = 0.0;
-      for (int s = 0; s < segs; ++s) S += sm.u.row.terms[s];
-      sm.mL[0] = mm;
-      sm.mL[1] = (float)log(S);
-    }
-  }
-  __syncthreads();
-  const float m = sm.mL[0], L = sm.mL[1];
-  if (!sm.exact) {
-    // each valid candidate with the 16-bit key of its logp in bits 48..63
-    // (invalid slots: 0, below every valid key)
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const int f = q * kTopkThreads + tid, sg = min(f >> lcap, kMaxSegs - 1), p = f & (cap - 1);
-      const bool use = f < nslots && p < sm.off[sg + 1] - sm.off[sg];
-      const uint64_t cc = cv[q];
-      const uint32_t lk = logp_key16<T>(value_of_key16<T>((uint32_t)(cc >> 32) & 0xffffu), m, L);
-      cv[q] = use ? (cc | ((uint64_t)lk << 48)) : 0ull;
-    }
-    // the k-th largest logp key: two 8-bit radix passes over the valid entries
-    uint32_t K = 0;
-    int krem = k;
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-      sm.u.row.hist[tid] = 0;
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < kQ; ++q) {
-        const uint32_t lk = (uint32_t)(cv[q] >> 48);
-        const bool valid = cv[q] != 0ull;
-        if (pass == 0) {
-          if (valid) atomicAdd(&sm.u.row.hist[lk >> 8], 1);
-        } else if (valid && (lk >> 8) == (K >> 8)) {
-          atomicAdd(&sm.u.row.hist[lk & 255u], 1);
-        }
-      }
-      __syncthreads();
-      sm.u.row.suf[tid] = block_suffix_sum(sm.u.row.hist[tid], sm.u.row.misc + 4);
-      if (tid == 0) sm.u.row.suf[256] = 0;
-      __syncthreads();
-      if (sm.u.row.suf[tid] >= krem && sm.u.row.suf[tid + 1] < krem) {
-        sm.u.row.misc[0] = tid;
-        sm.u.row.misc[1] = sm.u.row.suf[tid + 1];
-      }
-      __syncthreads();
-      K |= (uint32_t)sm.u.row.misc[0] << (pass == 0 ? 8 : 0);
-      krem -= sm.u.row.misc[1];
-      __syncthreads();
-    }
-    // the entries above the k-th logp, its tie group, and the segments' bounds
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const uint64_t cc = cv[q];
-      const uint32_t lk = (uint32_t)(cc >> 48);
-      const uint64_t e = ((uint64_t)lk << 32) | (uint32_t)cc;
-      if (cc != 0ull && lk > K) {
-        sm.u.row.fin[atomicAdd(&sm.nabove, 1)] = e;
-      } else if (cc != 0ull && lk == K) {
-        const int at = atomicAdd(&sm.ntie, 1);
-        if (at < kFusedTie) sm.u.row.tg[at] = e;
-      }
-    }
-    if (tid < segs) {
-      const uint32_t b = sm.sbound[tid];
-      if (b != 0 && logp_key16<T>(value_of_key16<T>(b), m, L) >= K) atomicOr(&sm.exact, 1);
-    }
-    __syncthreads();
-    if (!sm.exact && sm.ntie <= kFusedTie) {
-      const int above = sm.nabove, g = sm.ntie, need = k - above;
-      for (int i = tid; i < g; i += kTopkThreads) {
-        const uint64_t x = sm.u.row.tg[i];
-        const uint32_t xi = ~(uint32_t)x;
-        int rk = 0;
-        for (int j = 0; j < g; ++j) rk += (~(uint32_t)sm.u.row.tg[j]) < xi ? 1 : 0;
-        if (rk < need) sm.u.row.fin[above + rk] = x;
-      }
-      __syncthreads();
-      for (int i = tid; i < k; i += kTopkThreads) {
-        const uint64_t x = sm.u.row.fin[i];
-        int pos = 0;
-        for (int j = 0; j < k; ++j) pos += sm.u.row.fin[j] > x ? 1 : 0;
-        const uint32_t lk = (uint32_t)(x >> 32);
-        const uint16_t bits = (uint16_t)((lk & 0x8000u) ? (lk ^ 0x8000u) : (~lk & 0xffffu));
-        st_wt(a.row_vals + (int64_t)r * k + pos, to_f32(__builtin_bit_cast(T, bits)));
-        st_wt(a.row_idx + (int64_t)r * k + pos, (int32_t)~(uint32_t)x);
-      }
-      __syncthreads();
-      return;
-    }
-  }
-  __syncthreads();
-  // every logit of the row
-  const T* row = reinterpret_cast<const T*>(a.logits) + (int64_t)r * a.row_stride;
-  const TempScale ts = a.ts;
-  select_k([&](int i) { return fkey(logp_of<T>(scaled<T>(load_logit(row + i), ts), m, L)); },
-           [&](int i) { return i; }, a.vocab, k, sm.u.ex.skey, sm.u.ex.sidx, sm.u.ex.hist, sm.u.ex.suf,
-           sm.u.ex.misc);
-  for (int i = tid; i < k; i += kTopkThreads) {
-    const uint32_t ki = sm.u.ex.skey[i];
-    const int ii = sm.u.ex.sidx[i];
-    int rank = 0;
-    for (int j = 0; j < k; ++j) rank += (sm.u.ex.skey[j] > ki) || (sm.u.ex.skey[j] == ki && sm.u.ex.sidx[j] < ii);
-    const uint32_t uu = (ki & 0x80000000u) ? (ki & 0x7fffffffu) : ~ki;
-    st_wt(a.row_vals + (int64_t)r * k + rank, __uint_as_float(uu));
-    st_wt(a.row_idx + (int64_t)r * k + rank, (int32_t)ii);
-  }
-  __syncthreads();
-}
-
-// Pass 3 for request q (rows [rb, re)) from the row lists written by this
-// launch; only each row's first min(k, beam) entries can be chosen (every
-// thread; ends with a barrier).
-__device__ void fused_pool(const FusedTopkArgs& a, int rb, int re, int q, FusedLds& sm) {
-  const int tid = threadIdx.x, k = a.k, beam = a.beam;
-  int32_t* op = a.out_parent + (int64_t)q * beam;
-  int32_t* ot = a.out_token + (int64_t)q * beam;
-  double* os = a.out_score + (int64_t)q * beam;
-  const int nr = re - rb, jb = min(k, beam), n = nr * jb;
-  double* tot = sm.u.pool.tot;
-  {
-    constexpr int kQ = kFusedPool / kTopkThreads;
-    float rv[kQ];
-    int32_t ri[kQ];
-    double pv[kQ];
-#pragma unroll
-    for (int qq = 0; qq < kQ; ++qq) {
-      const int i = min(qq * kTopkThreads + tid, n - 1), rr = i / jb, j = i - rr * jb;
-      rv[qq] = ld_co(a.row_vals + (int64_t)(rb + rr) * k + j);
-      ri[qq] = ld_co(a.row_idx + (int64_t)(rb + rr) * k + j);
-      pv[qq] = a.parent[rb + rr];
-    }
-#pragma unroll
-    for (int qq = 0; qq < kQ; ++qq) {
-      const int i = qq * kTopkThreads + tid;
-      if (i < n) {
-        tot[i] = pv[qq] + (double)rv[qq];
-        sm.u.pool.idx[i] = ri[qq];
-      }
-    }
-  }
-  for (int i = tid; i < nr; i += kTopkThreads) sm.u.pool.sel[i] = 0;
-  __syncthreads();
-  int top = 1;
-  while (top * 2 <= jb) top *= 2;
-  for (int e = tid; e < n; e += kTopkThreads) {
-    const int rr = e / jb, j = e - rr * jb;
-    const double t = tot[e];
-    int rank = j;
-    // entries of row o before (rr, j): totals > t, or == t when o < rr (a
-    // prefix of the row; binary searches, eight rows at a time)
-    for (int o0 = 0; o0 < nr && rank < beam; o0 += 8) {
-      int pos[8];
-#pragma unroll
-      for (int uu = 0; uu < 8; ++uu) pos[uu] = 0;
-      for (int step = top; step > 0; step >>= 1) {
-        double y[8];
-#pragma unroll
-        for (int uu = 0; uu < 8; ++uu) {
-          const int o = o0 + uu, c = pos[uu] + step;
-          const bool use = (o < nr) & (o != rr) & (c <= jb);
-          y[uu] = tot[use ? o * jb + c - 1 : 0];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int uu = 0; uu < 8; ++uu) {
-          const int o = o0 + uu, c = pos[uu] + step;
-          const bool use = (o < nr) & (o != rr) & (c <= jb);
-          pos[uu] = (use & ((y[uu] > t) | ((y[uu] == t) & (o < rr)))) ? c : pos[uu];
-        }
-      }
-#pragma unroll
-      for (int uu = 0; uu < 8; ++uu) rank += pos[uu];
-    }
-    if (rank < beam) atomicAdd(&sm.u.pool.sel[rr], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    sm.u.pool.first[0] = 0;
-    for (int i = 0; i < nr; ++i) sm.u.pool.first[i + 1] = sm.u.pool.first[i] + sm.u.pool.sel[i];
-  }
-  __syncthreads();
-  for (int e = tid; e < n; e += kTopkThreads) {
-    const int rr = e / jb, j = e - rr * jb;
-    if (j < sm.u.pool.sel[rr]) {
-      const int at = sm.u.pool.first[rr] + j;
-      op[at] = rb + rr;
-      ot[at] = sm.u.pool.idx[e];
-      os[at] = tot[e];
-    }
-  }
-  for (int i = sm.u.pool.first[nr] + tid; i < beam; i += kTopkThreads) {
-    op[i] = -1;
-    ot[i] = -1;
-    os[i] = -INFINITY;
-  }
-  __syncthreads();
+  return mw == -INFINITY ? 0.0 : acc;
 }
 
 // Pass A: per (row, segment) unit the statistics and the unsorted candidates
-// (pass 1 without its sort).  G workgroups (a few per CU) take units
-// u = blockIdx.x + i G in turn; each issues the next unit's loads as soon as
-// the current unit's logits are in registers, so that the float64 exp-sums
-// (VALU-bound) run while the next logits stream in.  Within a unit, a
-// thread's two halves are summed in turn (each against its own maximum, then
-// rescaled).  SCALED: the temperature is not 1 (a separate instantiation keeps
-// the common path free of the scaling branches).
+// (pass 1 without its sort).  G workgroups (a few per CU) take their units in
+// turn; each issues the next unit's loads as soon as the current unit's
+// logits are in registers, so that the float64 exp-sums (VALU-bound) run while the next
+// logits stream in.  SCALED: the temperature is not 1 (a separate
+// instantiation keeps the common path free of the scaling code).
 template <typename T, bool SCALED>
 __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_kernel(FusedTopkArgs a) {
-  __shared__ double tab[64];
+  __shared__ double tab[256];
   __shared__ float wmax[4];
   __shared__ double wsum[4];
   __shared__ uint32_t wtau[4];
+  __shared__ int wslow[4];
   __shared__ int ncand;
   __shared__ uint64_t lc[kMaxCap];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int segs = a.segs, k = a.k, cap = a.cap, seg_len = a.seg_len, vocab = a.vocab;
   const int units = a.n_rows * segs;
+  const int G = gridDim.x;
   const T* logits = reinterpret_cast<const T*>(a.logits);
-  constexpr int kWords = kPerThread / 2, kHalf = kWords / 2;
-  int u = blockIdx.x;
+  constexpr int kWords = kPerThread / 2;
+  // 16-bit keys of -600 and 600: a wave sums against 0 when its largest x' lies between them
+  const uint32_t klo = key16_of_bits(bits_of<T>(-600.0f)), khi = key16_of_bits(bits_of<T>(600.0f));
+  // Units go out by columns: with G = 4C workgroups, workgroups col, col + C,
+  // col + 2C and col + 3C share the units col, col + C, col + 2C, ..., taking
+  // 3 : 2 : 2 : 1 of them in workgroup order.  The dispatcher places one
+  // workgroup of each quarter of the grid on every CU, in order, and a CU
+  // issues its oldest workgroup first: equal shares left the last quarter
+  // finishing far behind the first (measured).  Otherwise every G-th unit.
+  const bool quarters = (G & 3) == 0;
+  const int C = quarters ? G / 4 : G;
+  const int qtr = blockIdx.x / C, col = blockIdx.x - qtr * C;
+  const int ncol = (units - col + C - 1) / C;          // units col + i C below units
+  constexpr int kShare[5] = {0, 3, 5, 7, 8};           // cumulative eighths of a column
+  const int i0 = quarters ? ncol * kShare[qtr] / 8 : 0;
+  const int i1 = quarters ? ncol * kShare[qtr + 1] / 8 : ncol;
   SegVals<T> x, xn;
-  if (u < units) {
+  if (i0 < i1) {
+    const int u = col + i0 * C;
     const int r = u / segs, b = (u - r * segs) * seg_len;
     load_raw16<T>(logits + (int64_t)r * a.row_stride + b, min(vocab, b + seg_len) - b, x);
   }
-  exp_table_init(tab);
   if (tid == 0) ncand = 0;
+  exp_table256_init(tab);
   __syncthreads();                                     // the exp table, ncand
-  for (; u < units; u += gridDim.x) {
+  for (int i = i0; i < i1; ++i) {
+    const int u = col + i * C;
+    const int un = i + 1 < i1 ? u + C : units;
     const int r = u / segs, s = u - r * segs;
     const int b = s * seg_len;
-    if constexpr (SCALED) temp16<T>(a.ts, x);
-    // the largest x' of each half (fmaxf skips the NaN patterns of positions
-    // past the segment): this waits for the unit's logits
-    float m0 = -INFINITY, m1 = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kPerThread / 2; ++j) m0 = fmaxf(m0, x.at(j));
-#pragma unroll
-    for (int j = kPerThread / 2; j < kPerThread; ++j) m1 = fmaxf(m1, x.at(j));
-    // the next unit's loads, issued once this unit's logits are in registers
-    // (issued with them they would share the memory system and both arrive
-    // late together)
-    {
-      const int un = u + gridDim.x;
-      if (un < units) {
-        const int rn = un / segs, bn = (un - rn * segs) * seg_len;
-        asm volatile("" : "+v"(m0), "+v"(m1));
-        load_raw16<T>(logits + (int64_t)rn * a.row_stride + bn, min(vocab, bn + seg_len) - bn, xn);
-      }
+    // the sum against 0, a 16-byte chunk (4 words) at a time as it lands
+    double acc = 0.0;
+    if constexpr (SCALED) temp16<T>(a.ts, x, 0, 4);
+    acc = exp_sum0<T, 0, 4>(x, tab, acc);
+    if constexpr (SCALED) temp16<T>(a.ts, x, 4, 8);
+    acc = exp_sum0<T, 4, 8>(x, tab, acc);
+    if constexpr (SCALED) temp16<T>(a.ts, x, 8, 12);
+    acc = exp_sum0<T, 8, 12>(x, tab, acc);
+    // the last chunk has landed (the asm reads it): the next unit's loads
+    // (issued with this unit's they would share the memory system and both
+    // arrive late together)
+    asm volatile("" : "+v"(x.w[12]), "+v"(x.w[13]), "+v"(x.w[14]), "+v"(x.w[15]));
+    if (un < units) {
+      const int rn = un / segs, bn = (un - rn * segs) * seg_len;
+      load_raw16<T>(logits + (int64_t)rn * a.row_stride + bn, min(vocab, bn + seg_len) - bn, xn);
     }
-    const double acc0 = half_exp_sum<T, 0, kHalf>(x, tab, m0);
-    const double acc1 = half_exp_sum<T, kHalf, kWords>(x, tab, m1);
-    uint32_t kp[kWords];
+    if constexpr (SCALED) temp16<T>(a.ts, x, 12, 16);
+    acc = exp_sum0<T, 12, 16>(x, tab, acc);
+    // 16-bit order keys in place of the logits
     v2u16 km2 = {0, 0};
 #pragma unroll
     for (int i = 0; i < kWords; ++i) {
-      kp[i] = key16x2(x.w[i]);
-      km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(v2u16, kp[i]));
+      x.w[i] = key16x2(x.w[i]);
+      km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(v2u16, x.w[i]));
     }
     const uint32_t kmax = max((uint32_t)km2.x, (uint32_t)km2.y);
-    const float mt = fmaxf(m0, m1);
+    const uint32_t wk = lane63(wave_scan_max(kmax));
+    const float mw = value_of_key16<T>(wk);
+    const bool slow = wk > khi || wk < klo;              // wave-uniform
+    if (slow) acc = exp_sum_keys<T, kWords>(x.w, mw, tab);
     // the wave's kw-th largest per-thread maximum, bit by bit
     const int kw = (k + 3) >> 2;
     uint32_t pref = 0;
@@ -1559,19 +1344,12 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
       const uint32_t c = pref | (1u << bit);
       if (__popcll(__builtin_amdgcn_ballot_w64(kmax >= c)) >= kw) pref = c;
     }
-    const float mw = value_of_key16<T>(lane63(wave_scan_max(kmax)));
-    // the two halves' sums against the thread max, then against the wave's
-    double acc = 0.0;
-    if (mt != -INFINITY) {
-      const double md = (double)mt;
-      acc = acc0 * exp_neg((double)m0 - md, tab) + acc1 * exp_neg((double)m1 - md, tab);
-      acc *= exp_neg(md - (double)mw, tab);
-    }
     acc = wave_scan_add_f64(acc);
     if (lane == 63) {
       wmax[w] = mw;
       wsum[w] = acc;
       wtau[w] = pref;
+      wslow[w] = slow ? 1 : 0;
     }
     __syncthreads();
     const float m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
@@ -1581,7 +1359,7 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     v2u16 c2 = {0, 0};
 #pragma unroll
     for (int i = 0; i < kWords; ++i)
-      c2 += __builtin_elementwise_min(__builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, kp[i]), t1), one);
+      c2 += __builtin_elementwise_min(__builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, x.w[i]), t1), one);
     const int mine = (int)c2.x + (int)c2.y;
     const int incl = wave_scan_add(mine);
     int wbase = 0;
@@ -1590,7 +1368,7 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     if (mine > 0) {
 #pragma unroll
       for (int i = 0; i < kWords; ++i) {
-        const uint32_t lo = kp[i] & 0xffffu, hi = kp[i] >> 16;
+        const uint32_t lo = x.w[i] & 0xffffu, hi = x.w[i] >> 16;
         if (max(lo, hi) >= tau) {
           if (lo >= tau) {
             if (at < cap) lc[at] = ((uint64_t)lo << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i));
@@ -1608,12 +1386,21 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     const int64_t rs = (int64_t)r * segs + s;
     for (int i = tid; i < min(total, cap); i += kTopkThreads) a.cand[rs * cap + i] = lc[i];
     if (tid == 0) {
+      // the waves' sums against one reference: 0, or the unit's max when a wave
+      // summed against a max above 600 (or every wave against its own)
+      float ref = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ref = fmaxf(ref, wslow[q] ? wmax[q] : 0.0f);
       double sum = 0.0;
-      for (int q = 0; q < 4; ++q) sum += wsum[q] * exp_neg((double)wmax[q] - (double)m, tab);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float rq = wslow[q] ? wmax[q] : 0.0f;
+        if (wsum[q] != 0.0) sum += rq == ref ? wsum[q] : wsum[q] * exp_t256(fmax((double)rq - (double)ref, -700.0), tab);
+      }
       a.seg_max[rs] = m;
       a.seg_sum[rs] = sum;
       a.seg_cnt[rs] = total <= cap ? total : -1;
-      a.seg_bound[rs] = tau > 1 ? tau - 1 : 0u;
+      a.seg_bound[rs] = (tau > 1 ? tau - 1 : 0u) | (ref == 0.0f ? 0u : 0x80000000u);
     }
     __syncthreads();                                   // lc, ncand, wmax.. free again
     if (tid == 0) ncand = 0;
@@ -1622,47 +1409,474 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
   }
 }
 
-// Pass B: per row (one workgroup each) the selection from pass A's output;
-// the workgroup that completes a request's last row (an arrival counter per
-// request) runs pass 3 for it.
+// LDS of pass B.
+struct RowLds {
+  float m, L;
+  int exact, nabove, ntie, flag, req, rb, re, bin, rem, lo, shift, nsurv;
+  double pt;
+  int ppos;
+  int off[kMaxSegs + 1];
+  uint32_t sbound[kMaxSegs];
+  int hist[2][256];
+  int req_ptr[kFusedReqs + 1];
+  uint64_t fin[kMaxK];
+  uint64_t tg[kFusedTie];
+  double ptot[kFusedPool];
+  int32_t pidx[kFusedPool];
+  int sel[kFusedPoolRows];
+  int first[kFusedPoolRows + 1];
+  int surv[kPoolSurv];
+  // the exact selection over all logits
+  int xhist[4 * 256];
+  int xsuf[257];
+  int xmisc[4 + kRowWaves];
+  uint32_t skey[kMaxK];
+  int32_t sidx[kMaxK];
+};
+
+// Inclusive sums within each 32-lane half of a wave (DPP; lane 31 and lane 63
+// end with their half's total).
+__device__ __forceinline__ int half_wave_scan_add(int x) {
+  x += (int)dpp<0x111, 0xf, true>(0, x);
+  x += (int)dpp<0x112, 0xf, true>(0, x);
+  x += (int)dpp<0x114, 0xf, true>(0, x);
+  x += (int)dpp<0x118, 0xf, true>(0, x);
+  x += (int)dpp<0x142, 0xa, false>(0, x);
+  return x;
+}
+
+// One wave: the bin b of hist (256 bins) with suffix(b) >= want > suffix(b + 1),
+// suffix(b) counting the entries in bins >= b, and suffix(b + 1) (wave-uniform).
+// Lane l holds bins 255 - 4l down to 252 - 4l, so that the inclusive scan over
+// lanes is the suffix over bins.  want must not exceed the total.
+__device__ __forceinline__ void wave_find_bin(const int* hist, int want, int& bin, int& above) {
+  const int lane = threadIdx.x & 63;
+  const int b0 = 255 - 4 * lane;
+  const int h[4] = {hist[b0], hist[b0 - 1], hist[b0 - 2], hist[b0 - 3]};
+  const int incl = wave_scan_add(h[0] + h[1] + h[2] + h[3]);
+  int c = incl - (h[0] + h[1] + h[2] + h[3]);          // entries in bins above b0
+  int fb = -1, fa = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (c < want && c + h[q] >= want) {
+      fb = b0 - q;
+      fa = c;
+    }
+    c += h[q];
+  }
+  const uint64_t hit = __builtin_amdgcn_ballot_w64(fb >= 0);
+  const int src = hit ? (int)__builtin_ctzll(hit) : 0;
+  bin = __builtin_amdgcn_readlane(fb, src);
+  above = __builtin_amdgcn_readlane(fa, src);
+}
+
+// Rank by descending key of each of n <= 32 keys in LDS: thread t compares key
+// t >> 5 with key t & 31 and the 32 lanes of a key add their comparisons.
+// Returns the rank in the lane with (t & 31) == 31 of each key below n, -1
+// elsewhere (every thread of the block calls it).
+__device__ __forceinline__ int rank32_desc(const uint64_t* v, int n) {
+  const int t = threadIdx.x, i = t >> 5, j = t & 31;
+  const int c = half_wave_scan_add((i < n && j < n && v[j] > v[i]) ? 1 : 0);
+  return (j == 31 && i < n) ? c : -1;
+}
+
+// Writes the k entries of fin (composite keys: logp key << 32 | ~index) to row
+// r's lists in rank order (every thread of the block calls it).
 template <typename T>
-__global__ __launch_bounds__(kTopkThreads) void topk_rows16_kernel(FusedTopkArgs a) {
-  __shared__ FusedLds sm;
-  const int tid = threadIdx.x, r = blockIdx.x;
+__device__ __forceinline__ void store_row(const FusedTopkArgs& a, int r, const uint64_t* fin) {
+  const int k = a.k;
+  auto put = [&](uint64_t x, int pos) {
+    st_wt(a.row_vals + (int64_t)r * k + pos, to_f32(__builtin_bit_cast(T, bits_of_key16((uint32_t)(x >> 32)))));
+    st_wt(a.row_idx + (int64_t)r * k + pos, (int32_t)~(uint32_t)x);
+  };
+  if (k <= 32) {
+    const int pos = rank32_desc(fin, k);
+    if (pos >= 0) put(fin[threadIdx.x >> 5], pos);
+  } else {
+    for (int i = threadIdx.x; i < k; i += kRowThreads) {
+      const uint64_t x = fin[i];
+      int pos = 0;
+      for (int j = 0; j < k; ++j) pos += fin[j] > x ? 1 : 0;
+      put(x, pos);
+    }
+  }
+}
+
+// Row max m and L = fl32(ln S), S = sum over the row of e^(x' - m), from the
+// unit statistics held by wave 0 (lane s < segs: unit s's max, sum and
+// whether the sum is against that max rather than 0).  Wave 0 only.
+__device__ __forceinline__ void row_log_sum(bool in, float mu, double su, bool against_max, RowLds& sm) {
+  const float mm = wave_max(mu);
+  const float ref = !in ? -INFINITY : against_max ? mu : 0.0f;
+  const float R = wave_max(ref);
+  const double t = su != 0.0 ? su * exp((double)ref - (double)R) : 0.0;
+  const double B = __shfl(wave_scan_add_f64(t), 63, 64);
+  if ((threadIdx.x & 63) == 0) {
+    sm.m = mm;
+    sm.L = (float)(log(B) + ((double)R - (double)mm));
+  }
+}
+
+// Pass 3 for request q (rows [rb, re)) from the row lists written by this
+// launch; only each row's first min(k, beam) entries can be chosen (every
+// thread of the block; ends with a barrier).  An entry's rank is its position
+// in its row plus, in every other row, the entries before it in the order
+// (total desc, pool position asc) -- a prefix of that row, found by binary
+// search; P adjacent threads share an entry, each taking every P-th row.
+__device__ void fused_pool(const FusedTopkArgs& a, int rb, int re, int q, RowLds& sm) {
+  const int tid = threadIdx.x, k = a.k, beam = a.beam;
+  int32_t* op = a.out_parent + (int64_t)q * beam;
+  int32_t* ot = a.out_token + (int64_t)q * beam;
+  double* os = a.out_score + (int64_t)q * beam;
+  const int nr = re - rb, jb = min(k, beam), n = nr * jb;
+  if (tid < n) {
+    const int rr = tid / jb, j = tid - rr * jb;
+    const float rv = ld_co(a.row_vals + (int64_t)(rb + rr) * k + j);
+    const int32_t ri = ld_co(a.row_idx + (int64_t)(rb + rr) * k + j);
+    sm.ptot[tid] = a.parent[rb + rr] + (double)rv;
+    sm.pidx[tid] = ri;
+  }
+  for (int i = tid; i < nr; i += kRowThreads) sm.sel[i] = 0;
+  __syncthreads();
+  // A bound on the beam-th best: the beam-th best (rank beam - 1) of a sample,
+  // each row's first ns entries.  Every entry of the top beam is at or before
+  // it (beam sampled entries are), so only those -- per row a prefix -- need
+  // exact ranks, and their ranks among themselves are their ranks in the pool.
+  const int ns = nr <= kPoolSurv ? min(jb, kPoolSurv / nr) : 0;
+  const int nsamp = nr * ns;
+  int S = kPoolSurv + 1;                               // survivors; above kPoolSurv: rank every entry
+  if (nsamp >= beam) {
+    {
+      const int i = tid >> 5, jj = tid & 31;
+      const int pi = i < nsamp ? (i / ns) * jb + i % ns : 0;
+      int c = 0;
+      if (i < nsamp && jj < nsamp) {
+        const int pj = (jj / ns) * jb + jj % ns;
+        const double ti = sm.ptot[pi], tj = sm.ptot[pj];
+        c = (tj > ti || (tj == ti && pj < pi)) ? 1 : 0;
+      }
+      c = half_wave_scan_add(c);
+      if (jj == 31 && i < nsamp && c == beam - 1) {
+        sm.pt = sm.ptot[pi];
+        sm.ppos = pi;
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // the prefix of row tid at or before the bound, by binary search
+      const double pt = sm.pt;
+      const int ppos = sm.ppos;
+      int c = 0;
+      if (tid < nr) {
+        int lo = 0, hi = jb;                           // entries [0, lo) qualify, [hi, jb) do not
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1, pm = tid * jb + mid;
+          const double y = sm.ptot[pm];
+          if (y > pt || (y == pt && pm <= ppos)) lo = mid + 1;
+          else hi = mid;
+        }
+        c = lo;
+      }
+      const int incl = wave_scan_add(c);
+      const int tot = __builtin_amdgcn_readlane(incl, 63);
+      if (tot <= kPoolSurv)
+        for (int j2 = 0; j2 < c; ++j2) sm.surv[incl - c + j2] = tid * jb + j2;
+      if (tid == 0) sm.nsurv = tot;
+    }
+    __syncthreads();
+    S = sm.nsurv;
+  }
+  if (S <= kPoolSurv) {
+    // the survivors' ranks: thread t compares survivor t >> 5 with survivor t & 31
+    const int i = tid >> 5, jj = tid & 31;
+    const int pi = i < S ? sm.surv[i] : 0;
+    int c = 0;
+    if (i < S && jj < S) {
+      const int pj = sm.surv[jj];
+      const double ti = sm.ptot[pi], tj = sm.ptot[pj];
+      c = (tj > ti || (tj == ti && pj < pi)) ? 1 : 0;
+    }
+    c = half_wave_scan_add(c);
+    if (jj == 31 && i < S && c < beam) atomicAdd(&sm.sel[pi / jb], 1);
+  } else {
+    // every entry's rank: P adjacent threads share an entry, each taking every
+    // P-th row, and add their counts
+    const int P = n <= kRowThreads / 8 ? 8 : n <= kRowThreads / 4 ? 4 : 2;
+    const int e = tid / P, part = tid - e * P;
+    int cnt = 0;
+    int rr = 0, j = 0;
+    if (e < n) {
+      rr = e / jb;
+      j = e - rr * jb;
+      const double t = sm.ptot[e];
+      int top = 1;
+      while (top * 2 <= jb) top *= 2;
+      for (int o0 = part; o0 < nr; o0 += 4 * P) {
+        int pos[4] = {0, 0, 0, 0};
+        for (int step = top; step > 0; step >>= 1) {
+          double y[4];
+#pragma unroll
+          for (int uu = 0; uu < 4; ++uu) {
+            const int o = o0 + uu * P, c = pos[uu] + step;
+            const bool use = (o < nr) & (o != rr) & (c <= jb);
+            y[uu] = sm.ptot[use ? o * jb + c - 1 : 0];
+          }
+#pragma unroll
+          for (int uu = 0; uu < 4; ++uu) {
+            const int o = o0 + uu * P, c = pos[uu] + step;
+            const bool use = (o < nr) & (o != rr) & (c <= jb);
+            pos[uu] = (use & ((y[uu] > t) | ((y[uu] == t) & (o < rr)))) ? c : pos[uu];
+          }
+        }
+        cnt += pos[0] + pos[1] + pos[2] + pos[3];
+      }
+    }
+    for (int sft = 1; sft < P; sft <<= 1) cnt += __shfl_xor(cnt, sft, 64);
+    if (e < n && part == 0 && j + cnt < beam) atomicAdd(&sm.sel[rr], 1);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // exclusive prefix of the rows' selection counts, four rows per lane
+    int v[4], s4 = 0;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int i = 4 * tid + qq;
+      v[qq] = i < nr ? sm.sel[i] : 0;
+      s4 += v[qq];
+    }
+    const int incl = wave_scan_add(s4);
+    int base = incl - s4;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int i = 4 * tid + qq;
+      if (i < nr) sm.first[i] = base;
+      base += v[qq];
+    }
+    if (tid == 63) sm.first[nr] = incl;
+  }
+  __syncthreads();
+  if (tid < n) {
+    const int r2 = tid / jb, j2 = tid - r2 * jb;
+    if (j2 < sm.sel[r2]) {
+      const int at = sm.first[r2] + j2;
+      op[at] = rb + r2;
+      ot[at] = sm.pidx[tid];
+      os[at] = sm.ptot[tid];
+    }
+  }
+  for (int i = sm.first[nr] + tid; i < beam; i += kRowThreads) {
+    op[i] = -1;
+    ot[i] = -1;
+    os[i] = -INFINITY;
+  }
+  __syncthreads();
+}
+
+// Pass B: per row (one workgroup of sixteen waves each) the selection from
+// pass A's output; the workgroup that completes a request's last row (an
+// arrival counter per request) runs pass 3 for it.
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void topk_rows16_kernel(FusedTopkArgs a) {
+  __shared__ RowLds sm;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = blockIdx.x;
+  const int segs = a.segs, k = a.k, cap = a.cap;
   const int n_req = a.beam > 0 ? a.n_req : 0;
+  const int64_t base = (int64_t)r * segs;
+  const int lcap = __ffs(cap) - 1;                     // cap is a power of two
+  const int nslots = segs << lcap;
   // requests without rows (or with an invalid range) get empty selections
   for (int q = r; q < n_req; q += gridDim.x) {
     const int rb = a.req_row_ptr ? a.req_row_ptr[q] : 0, re = a.req_row_ptr ? a.req_row_ptr[q + 1] : a.n_rows;
     if (!(rb >= 0 && re <= a.n_rows && rb < re))
-      for (int i = tid; i < a.beam; i += kTopkThreads) {
+      for (int i = tid; i < a.beam; i += kRowThreads) {
         a.out_parent[(int64_t)q * a.beam + i] = -1;
         a.out_token[(int64_t)q * a.beam + i] = -1;
         a.out_score[(int64_t)q * a.beam + i] = -INFINITY;
       }
   }
-  fused_row<T>(a, r, sm);
+  // one round trip: every candidate slot of the row (slots past a unit's count
+  // hold stale words: unused), the unit statistics (wave 0), the request
+  // pointers
+  uint64_t cv[kRowCandPer];
+  const uint64_t* blk = a.cand + base * cap;
+#pragma unroll
+  for (int q = 0; q < kRowCandPer; ++q) cv[q] = blk[min(q * kRowThreads + tid, nslots - 1)];
+  for (int i = tid; i <= n_req; i += kRowThreads)
+    sm.req_ptr[i] = a.req_row_ptr ? a.req_row_ptr[i] : (i == 0 ? 0 : a.n_rows);
+  float mu = -INFINITY;
+  double su = 0.0;
+  bool against_max = false;
+  const bool in = lane < segs;
+  if (w == 0) {
+    const int li = min(lane, segs - 1);
+    mu = a.seg_max[base + li];
+    su = a.seg_sum[base + li];
+    const int c = a.seg_cnt[base + li];
+    const uint32_t bd = a.seg_bound[base + li];
+    if (!in) {
+      mu = -INFINITY;
+      su = 0.0;
+    }
+    against_max = in && (bd >> 31) != 0;
+    if (in) sm.sbound[lane] = bd & 0xffffu;
+    const int incl = wave_scan_add(in && c > 0 ? c : 0);
+    if (in) sm.off[lane + 1] = incl;
+    // the radix select's key range: the k-th largest x' key is at least the
+    // threshold of any unit holding k candidates (all its candidates reach
+    // it), and at most the row max's key
+    const uint32_t tau = (bd & 0xffffu) + 1u;
+    const uint32_t lo = wave_scan_max(in && c >= k ? tau : 1u);
+    const uint32_t hi = wave_scan_max(in ? key16_of_bits(bits_of<T>(mu)) : 0u);
+    const uint32_t lo63 = lane63(lo), hi63 = max(lane63(hi), lo63);
+    int shift = 0;
+    while (((hi63 - lo63) >> shift) >= 256u) ++shift;
+    // an overflowed unit, or fewer candidates than k: the exact selection
+    const bool over = __builtin_amdgcn_ballot_w64(in && c < 0) != 0 ||
+                      __builtin_amdgcn_readlane(incl, segs - 1) < k;
+    if (lane == 0) {
+      sm.off[0] = 0;
+      sm.exact = over ? 1 : 0;
+      sm.nabove = 0;
+      sm.ntie = 0;
+      sm.req = -1;
+      sm.lo = (int)lo63;
+      sm.shift = shift;
+    }
+  }
+  if (tid < 256) {
+    sm.hist[0][tid] = 0;
+    sm.hist[1][tid] = 0;
+  }
+  __syncthreads();
+  // the request holding row r (wave 3): the last q with req_ptr[q] <= r
+  if (w == 3 && n_req > 0) {
+    int best = -1;
+    for (int q = lane; q < n_req; q += 64)
+      if (sm.req_ptr[q] <= r) best = q;
+    best = (int)wave_scan_max((uint32_t)(best + 1)) - 1;
+    if (lane == 63) {
+      const int rb = best >= 0 ? sm.req_ptr[best] : 0, re = best >= 0 ? sm.req_ptr[best + 1] : 0;
+      const bool ok = best >= 0 && rb >= 0 && re <= a.n_rows && rb <= r && r < re;
+      sm.req = ok ? best : -1;
+      sm.rb = rb;
+      sm.re = re;
+    }
+  }
+  const bool exact0 = sm.exact != 0;
+  // the candidates' x' keys (0 for slots past their unit's count)
+  uint32_t xk[kRowCandPer];
+#pragma unroll
+  for (int q = 0; q < kRowCandPer; ++q) {
+    const int f = q * kRowThreads + tid, sg = min(f >> lcap, kMaxSegs - 1), p = f & (cap - 1);
+    const bool use = f < nslots && p < sm.off[sg + 1] - sm.off[sg];
+    xk[q] = use ? (uint32_t)(cv[q] >> 32) & 0xffffu : 0u;
+  }
+  if (!exact0) {
+    // the k-th largest x' key: radix passes over the keys' offsets from lo
+    // (one pass when the range spans at most 256 keys), while wave 0 takes
+    // the row's log-sum-exp
+    const uint32_t lo = (uint32_t)sm.lo;
+    const int shift = sm.shift;
+#pragma unroll
+    for (int q = 0; q < kRowCandPer; ++q)
+      if (xk[q] >= lo && xk[q] != 0) atomicAdd(&sm.hist[0][(xk[q] - lo) >> shift], 1);
+    if (w == 0) row_log_sum(in, mu, su, against_max, sm);
+    __syncthreads();
+    if (w == 1) {
+      int bin, above;
+      wave_find_bin(sm.hist[0], k, bin, above);
+      if (lane == 0) {
+        sm.bin = shift == 0 ? (int)lo + bin : bin;
+        sm.rem = k - above;
+      }
+    }
+    __syncthreads();
+    if (shift > 0) {
+      const uint32_t hb = (uint32_t)sm.bin;
+#pragma unroll
+      for (int q = 0; q < kRowCandPer; ++q)
+        if (xk[q] >= lo && xk[q] != 0 && ((xk[q] - lo) >> shift) == hb)
+          atomicAdd(&sm.hist[1][(xk[q] - lo) & ((1u << shift) - 1u)], 1);
+      __syncthreads();
+      if (w == 1) {
+        int bin, above;
+        wave_find_bin(sm.hist[1], sm.rem, bin, above);
+        if (lane == 0) sm.bin = (int)(lo + (hb << shift) + (uint32_t)bin);
+      }
+      __syncthreads();
+    }
+  } else {
+    if (w == 0) row_log_sum(in, mu, su, against_max, sm);
+    __syncthreads();
+  }
+  const float m = sm.m, L = sm.L;
+  bool done = false;
+  if (!exact0) {
+    // the k-th logp; the entries above it, its tie group, and the units' bounds
+    const uint32_t K = logp_key16<T>(value_of_key16<T>((uint32_t)sm.bin), m, L);
+#pragma unroll
+    for (int q = 0; q < kRowCandPer; ++q) {
+      if (xk[q] == 0) continue;
+      const uint32_t lk = logp_key16<T>(value_of_key16<T>(xk[q]), m, L);
+      const uint64_t e = ((uint64_t)lk << 32) | (uint32_t)cv[q];
+      if (lk > K) {
+        sm.fin[atomicAdd(&sm.nabove, 1)] = e;
+      } else if (lk == K) {
+        const int at = atomicAdd(&sm.ntie, 1);
+        if (at < kFusedTie) sm.tg[at] = e;
+      }
+    }
+    if (tid < segs) {
+      const uint32_t bd = sm.sbound[tid];
+      if (bd != 0 && logp_key16<T>(value_of_key16<T>(bd), m, L) >= K) atomicOr(&sm.exact, 1);
+    }
+    __syncthreads();
+    if (!sm.exact && sm.ntie <= kFusedTie) {
+      // the need lowest indices of the tie group (largest composite keys)
+      const int above = sm.nabove, g = sm.ntie, need = k - above;
+      if (g <= 32) {
+        const int rk = rank32_desc(sm.tg, g);
+        if (rk >= 0 && rk < need) sm.fin[above + rk] = sm.tg[tid >> 5];
+      } else {
+        for (int i = tid; i < g; i += kRowThreads) {
+          const uint64_t x = sm.tg[i];
+          int rk = 0;
+          for (int jj = 0; jj < g; ++jj) rk += sm.tg[jj] > x ? 1 : 0;
+          if (rk < need) sm.fin[above + rk] = x;
+        }
+      }
+      __syncthreads();
+      store_row<T>(a, r, sm.fin);
+      done = true;
+    }
+  }
+  if (!done) {
+    // every logit of the row
+    __syncthreads();
+    const T* row = reinterpret_cast<const T*>(a.logits) + (int64_t)r * a.row_stride;
+    const TempScale ts = a.ts;
+    select_k<kRowThreads>([&](int i) { return fkey(logp_of<T>(scaled<T>(load_logit(row + i), ts), m, L)); },
+                          [&](int i) { return i; }, a.vocab, k, sm.skey, sm.sidx, sm.xhist, sm.xsuf, sm.xmisc);
+    for (int i = tid; i < k; i += kRowThreads) {
+      const uint32_t ki = sm.skey[i];
+      const int ii = sm.sidx[i];
+      int rank = 0;
+      for (int jj = 0; jj < k; ++jj) rank += (sm.skey[jj] > ki) || (sm.skey[jj] == ki && sm.sidx[jj] < ii);
+      const uint32_t uu = (ki & 0x80000000u) ? (ki & 0x7fffffffu) : ~ki;
+      st_wt(a.row_vals + (int64_t)r * k + rank, __uint_as_float(uu));
+      st_wt(a.row_idx + (int64_t)r * k + rank, (int32_t)ii);
+    }
+  }
   if (n_req == 0) return;
   // the row lists are complete before this row's arrival counts
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // the request holding row r: the last q with req_row_ptr[q] <= r
-  const int* rp = sm.req_ptr;
   if (tid == 0) {
-    int lo = 0, hi = n_req;                            // the answer is in [lo, hi)
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (rp[mid] <= r) lo = mid;
-      else hi = mid;
-    }
-    const int rb = rp[lo], re = rp[lo + 1];
-    const bool ok = rb >= 0 && re <= a.n_rows && rb <= r && r < re;
-    sm.req = lo;
-    sm.flag = ok && arrive(a.ctr + lo, (uint32_t)(re - rb)) == (uint32_t)(re - rb);
-    sm.off[0] = rb;
-    sm.off[1] = re;
+    const int q = sm.req;
+    sm.flag = q >= 0 && arrive(a.ctr + q, (uint32_t)(sm.re - sm.rb)) == (uint32_t)(sm.re - sm.rb);
   }
   __syncthreads();
-  if (sm.flag) fused_pool(a, sm.off[0], sm.off[1], sm.req, sm);
+  if (sm.flag) fused_pool(a, sm.rb, sm.re, sm.req, sm);
 }
 
 // ---------------------------------------------------------------- diverse selection
@@ -1946,11 +2160,11 @@ static int topk_launch(const void* logits, int dtype, int n_rows, int vocab, int
     if (dtype == BE_BF16) {
       if (scaled) be::topk_units16_kernel<be::bf16_t, true><<<g_units, be::kTopkThreads, 0, st>>>(fa);
       else be::topk_units16_kernel<be::bf16_t, false><<<g_units, be::kTopkThreads, 0, st>>>(fa);
-      be::topk_rows16_kernel<be::bf16_t><<<n_rows, be::kTopkThreads, 0, st>>>(fa);
+      be::topk_rows16_kernel<be::bf16_t><<<n_rows, be::kRowThreads, 0, st>>>(fa);
     } else {
       if (scaled) be::topk_units16_kernel<be::f16_t, true><<<g_units, be::kTopkThreads, 0, st>>>(fa);
       else be::topk_units16_kernel<be::f16_t, false><<<g_units, be::kTopkThreads, 0, st>>>(fa);
-      be::topk_rows16_kernel<be::f16_t><<<n_rows, be::kTopkThreads, 0, st>>>(fa);
+      be::topk_rows16_kernel<be::f16_t><<<n_rows, be::kRowThreads, 0, st>>>(fa);
     }
     BE_HIP_CHECK(hipGetLastError());
     return BE_OK;

@@ -258,3 +258,38 @@ def test_workspace_shared_across_paths_and_empty_requests():
                     _, _, _, _, flat = ot.beam_step(x, parents[b:b + r].tolist(), beam, DT[dtype])
                     assert got == flat, f"{rows} {dtype} request {q}"
                 b += r
+
+
+def test_pool_bound_and_full_ranking():
+    """The pool's sample bound (the beam-th best of each row's first entries):
+    a request whose best entries all sit in one row (more than 32 entries reach
+    the bound, so every entry is ranked), a request of 48 rows (too many to
+    sample: every entry is ranked), rows with one far outlier (their keys span
+    more than 256 values: two radix passes), and identical rows under equal
+    parents (totals tied across rows, ordered by pool position)."""
+    from beam_engine_amd import beam_topk
+    say("topk pool bound, full ranking, wide key range, tied totals")
+    g = torch.Generator().manual_seed(31)
+    rows = [16, 48, 8]
+    v = 50000
+    x = torch.randn((sum(rows), v), generator=g)
+    x[16:64, 997::4999] = 50.0                     # one outlier every 4999 logits
+    x[64:72] = x[64]                               # identical rows
+    logits = x.to(torch.bfloat16)
+    parents = -torch.rand(sum(rows), generator=g, dtype=torch.float64) * 3
+    parents[:16] = -100.0
+    parents[3] = 0.0                               # one dominant row
+    parents[64:72] = -1.0
+    for beam in (16, 4):
+        k = 2 * beam
+        _, _, (par, tok, sc) = beam_topk(logits.cuda(), k, parents, beam, request_rows=rows)
+        torch.cuda.synchronize()
+        par, tok, sc = par.tolist(), tok.tolist(), sc.tolist()
+        b = 0
+        for q, r in enumerate(rows):
+            got = [(p - b, t, s) for p, t, s in zip(par[q * beam:(q + 1) * beam], tok[q * beam:(q + 1) * beam],
+                                                     sc[q * beam:(q + 1) * beam]) if p >= 0]
+            _, _, _, _, flat = ot.beam_step(logits[b:b + r].float().numpy(), parents[b:b + r].tolist(), beam,
+                                            "bfloat16")
+            assert got == flat, f"beam {beam} request {q}"
+            b += r
