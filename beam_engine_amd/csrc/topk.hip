@@ -1224,19 +1224,37 @@ __device__ __forceinline__ double exp_t256(double d, const double* tab) {
   return fma(t, p, t);
 }
 
+// Two packed 16-bit logits with every negative value below -648 (bf16) or
+// -650 (f16) -- and -inf and the negative NaN patterns, past-the-segment
+// positions among them -- replaced by that value: one unsigned 16-bit min,
+// since negative patterns order by magnitude above 0x8000.
+template <typename T>
+__device__ __forceinline__ uint32_t clamp_low16(uint32_t u) {
+  constexpr unsigned short kLow = __is_same(T, bf16_t) ? 0xc422 : 0xe114;
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(v2u16, u), (v2u16){kLow, kLow}));
+}
+
+template <typename T>
+__device__ __forceinline__ float half_value(uint32_t u, int hi) {
+  if constexpr (__is_same(T, bf16_t)) return __uint_as_float(hi ? (u & 0xffff0000u) : (u << 16));
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (u >> 16) : (u & 0xffffu)));
+}
+
 // acc + the float64 sum of e^x' over words [W0, W1) of a thread's logits,
-// against 0.  x' below -650 (and -inf, and the NaN patterns past the segment)
-// count as e^-650: nothing against a sum that an x' of at least -600 adds e^-600
-// to.  Four exps at a time, each group's arguments chained to the previous
-// group's sum, so that the compiler cannot start every range reduction at once
-// (which spills).
+// against 0.  x' below about -650 (and -inf, and the NaN patterns past the
+// segment) count as e^-650: nothing against a sum that an x' of at least -600
+// adds e^-600 to (a positive NaN stays NaN, but its key puts the wave on the
+// sum against its max).  Four exps at a time, each group's arguments chained
+// to the previous group's sum, so that the compiler cannot start every range
+// reduction at once (which spills).
 template <typename T, int W0, int W1>
 __device__ __forceinline__ double exp_sum0(SegVals<T>& x, const double* tab, double acc) {
 #pragma unroll
   for (int i = W0; i < W1; i += 2) {
     asm volatile("" : "+v"(acc), "+v"(x.w[i]), "+v"(x.w[i + 1]));
+    const uint32_t c[2] = {clamp_low16<T>(x.w[i]), clamp_low16<T>(x.w[i + 1])};
 #pragma unroll
-    for (int j = 2 * i; j < 2 * i + 4; ++j) acc += exp_t256((double)fmaxf(x.at(j), -650.0f), tab);
+    for (int j = 0; j < 4; ++j) acc += exp_t256((double)half_value<T>(c[j >> 1], j & 1), tab);
   }
   return acc;
 }
@@ -1502,19 +1520,27 @@ __device__ __forceinline__ void store_row(const FusedTopkArgs& a, int r, const u
   }
 }
 
-// Row max m and L = fl32(ln S), S = sum over the row of e^(x' - m), from the
-// unit statistics held by wave 0 (lane s < segs: unit s's max, sum and
-// whether the sum is against that max rather than 0).  Wave 0 only.
-__device__ __forceinline__ void row_log_sum(bool in, float mu, double su, bool against_max, RowLds& sm) {
-  const float mm = wave_max(mu);
+// The row max mm and S e^-(R - mm) = B, S = sum over the row of e^(x' - mm),
+// from the unit statistics held by wave 0 (lane s < segs: unit s's max, sum
+// and whether the sum is against that max rather than 0; R the largest
+// reference).  Wave 0 only; every lane ends with the same values.
+__device__ __forceinline__ void row_sum(bool in, float mu, double su, bool against_max, float& mm, float& R,
+                                        double& B) {
+  mm = wave_max(mu);
   const float ref = !in ? -INFINITY : against_max ? mu : 0.0f;
-  const float R = wave_max(ref);
-  const double t = su != 0.0 ? su * exp((double)ref - (double)R) : 0.0;
-  const double B = __shfl(wave_scan_add_f64(t), 63, 64);
-  if ((threadIdx.x & 63) == 0) {
-    sm.m = mm;
-    sm.L = (float)(log(B) + ((double)R - (double)mm));
+  double t = su;
+  if (__builtin_amdgcn_ballot_w64(against_max) == 0) {
+    R = __builtin_amdgcn_ballot_w64(in) != 0 ? 0.0f : -INFINITY;
+  } else {
+    R = wave_max(ref);
+    t = su != 0.0 ? su * exp((double)ref - (double)R) : 0.0;
   }
+  B = __shfl(wave_scan_add_f64(t), 63, 64);
+}
+
+// L = fl32(ln S) from row_sum's values.
+__device__ __forceinline__ float row_log(float mm, float R, double B) {
+  return (float)(log(B) + ((double)R - (double)mm));
 }
 
 // Pass 3 for request q (rows [rb, re)) from the row lists written by this
@@ -1703,8 +1729,8 @@ __global__ __launch_bounds__(kRowThreads) void topk_rows16_kernel(FusedTopkArgs 
   for (int q = 0; q < kRowCandPer; ++q) cv[q] = blk[min(q * kRowThreads + tid, nslots - 1)];
   for (int i = tid; i <= n_req; i += kRowThreads)
     sm.req_ptr[i] = a.req_row_ptr ? a.req_row_ptr[i] : (i == 0 ? 0 : a.n_rows);
-  float mu = -INFINITY;
-  double su = 0.0;
+  float mu = -INFINITY, mm_row = -INFINITY, R_row = 0.0f;
+  double su = 0.0, B_row = 0.0;
   bool against_max = false;
   const bool in = lane < segs;
   if (w == 0) {
@@ -1733,6 +1759,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_rows16_kernel(FusedTopkArgs 
     // an overflowed unit, or fewer candidates than k: the exact selection
     const bool over = __builtin_amdgcn_ballot_w64(in && c < 0) != 0 ||
                       __builtin_amdgcn_readlane(incl, segs - 1) < k;
+    row_sum(in, mu, su, against_max, mm_row, R_row, B_row);
     if (lane == 0) {
       sm.off[0] = 0;
       sm.exact = over ? 1 : 0;
@@ -1780,8 +1807,11 @@ __global__ __launch_bounds__(kRowThreads) void topk_rows16_kernel(FusedTopkArgs 
 #pragma unroll
     for (int q = 0; q < kRowCandPer; ++q)
       if (xk[q] >= lo && xk[q] != 0) atomicAdd(&sm.hist[0][(xk[q] - lo) >> shift], 1);
-    if (w == 0) row_log_sum(in, mu, su, against_max, sm);
     __syncthreads();
+    if (w == 0 && lane == 0) {
+      sm.m = mm_row;
+      sm.L = row_log(mm_row, R_row, B_row);
+    }
     if (w == 1) {
       int bin, above;
       wave_find_bin(sm.hist[0], k, bin, above);
@@ -1806,7 +1836,10 @@ __global__ __launch_bounds__(kRowThreads) void topk_rows16_kernel(FusedTopkArgs 
       __syncthreads();
     }
   } else {
-    if (w == 0) row_log_sum(in, mu, su, against_max, sm);
+    if (w == 0 && lane == 0) {
+      sm.m = mm_row;
+      sm.L = row_log(mm_row, R_row, B_row);
+    }
     __syncthreads();
   }
   const float m = sm.m, L = sm.L;
