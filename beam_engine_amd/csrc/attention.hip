@@ -699,7 +699,10 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   }
 
   // ---- algorithmic bytes: distinct (page, head) valid tokens, plus Q and O
-  std::vector<int> valid(num_pages, 0);
+  // (a per-thread table of the pool's pages, zero between calls: only the
+  // referenced entries are set, summed and cleared)
+  static thread_local std::vector<int> valid;
+  if ((int)valid.size() < num_pages) valid.assign((size_t)num_pages, 0);
   for (int lv = 0; lv < num_levels; ++lv) {
     const be_level& L = levels[lv];
     for (int j = 0; j < L.num_groups; ++j) {
@@ -712,7 +715,14 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
     }
   }
   int64_t valid_tokens = 0;
-  for (int v : valid) valid_tokens += v;
+  for (int lv = 0; lv < num_levels; ++lv) {
+    const be_level& L = levels[lv];
+    const int np = L.num_groups ? L.kv_indptr[L.num_groups] : 0;
+    for (int i = 0; i < np; ++i) {
+      valid_tokens += valid[L.kv_indices[i]];
+      valid[L.kv_indices[i]] = 0;
+    }
+  }
   const int64_t es = (int64_t)dtype_size(dtype);
   double flops = 0.0;
   // causal (BE_PLAN_CAUSAL): on the last level, query q0 + i of a group of n

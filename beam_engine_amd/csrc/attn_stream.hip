@@ -1336,7 +1336,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     for (size_t ti = 0; ti < tasks.size(); ++ti) {
       const Task& t = tasks[ti];
       bool open = false;                 // a segment of this task is open in workgroup b
-      for (int tile = 0; tile < t.tiles; ++tile) {
+      for (int tile = 0; tile < t.tiles;) {
         if (first) {
           open_wg(ti, tile);
           first = false;
@@ -1367,11 +1367,21 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
           used += kSegCost;
           open = true;
         }
+        // this tile joins, and with it every following tile of the task that
+        // passes the same test (tile j more joins while used + (j - 1) tc +
+        // tc / 2 <= share; the last workgroup takes all)
+        int take = t.tiles - tile;
+        if (b != W_s - 1) {
+          const int64_t slack = share - (used + t.tc) - t.tc / 2;
+          const int64_t more = slack < 0 ? 0 : slack / t.tc + 1;
+          take = (int)std::min<int64_t>(take, 1 + more);
+        }
         StreamSeg& cur = segs.back();
-        cur.n_tiles += 1;
+        cur.n_tiles += take;
         cur.tok_count = std::min(t.kv_len - cur.tok_begin, cur.n_tiles * kTok);
-        wg[b].z += 1;
-        used += t.tc;
+        wg[b].z += take;
+        used += (int64_t)take * t.tc;
+        tile += take;
       }
     }
   }
@@ -1395,16 +1405,33 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     any_wide = any_wide || big;
   }
 
-  // ---- partial slots and merge records per (query, KV head)
-  std::vector<int> cnt((size_t)num_queries * hkv, 0);
-  for (const StreamSeg& s : segs)
-    for (int j = 0; j < s.q_count; ++j) cnt[(size_t)(s.q_begin + j) * hkv + s.head] += 1;
+  // ---- partial slots and merge records per (query, KV head).  Per KV head
+  // (head-major rows of num_queries + 1): cnt, the segments covering each
+  // query, from a difference array over the segments' query ranges; a segment
+  // is written directly when every query it covers has one segment and no tail
+  // chunks (a prefix count of the queries that fail this)
+  const size_t nq1 = (size_t)num_queries + 1;
+  std::vector<int> cnt((size_t)hkv * nq1, 0);
+  for (const StreamSeg& s : segs) {
+    cnt[(size_t)s.head * nq1 + s.q_begin] += 1;
+    cnt[(size_t)s.head * nq1 + s.q_begin + s.q_count] -= 1;
+  }
+  std::vector<int> undirect((size_t)hkv * nq1, 0);
+  for (int h = 0; h < hkv; ++h) {
+    int* c = cnt.data() + (size_t)h * nq1;
+    int* u = undirect.data() + (size_t)h * nq1;
+    int run = 0;
+    for (int qi = 0; qi < num_queries; ++qi) {
+      run += c[qi];
+      c[qi] = run;
+      u[qi + 1] = u[qi] + ((run != 1 || n_tails_of(qi) != 0) ? 1 : 0);
+    }
+  }
+  auto cnt_of = [&](int qi, int h) { return cnt[(size_t)h * nq1 + qi]; };
   int n_slots = 0;
   for (StreamSeg& s : segs) {
-    bool direct = true;
-    for (int j = 0; j < s.q_count; ++j)
-      direct = direct && cnt[(size_t)(s.q_begin + j) * hkv + s.head] == 1 && n_tails_of(s.q_begin + j) == 0;
-    if (!direct) {
+    const int* u = undirect.data() + (size_t)s.head * nq1;
+    if (u[s.q_begin + s.q_count] != u[s.q_begin]) {
       s.out_slot = n_slots;
       n_slots += s.q_count;
     }
@@ -1428,9 +1455,22 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // slot ids per (query, KV head) as CSR: count, prefix, fill in segment order
   const size_t nqh = (size_t)num_queries * hkv;
   std::vector<int> sbeg(nqh + 1, 0);
-  for (const StreamSeg& s : segs)
-    if (s.out_slot >= 0)
-      for (int j = 0; j < s.q_count; ++j) sbeg[(size_t)(s.q_begin + j) * hkv + s.head + 1] += 1;
+  {
+    // slot-bearing segments per (query, KV head): a difference array per head
+    std::fill(undirect.begin(), undirect.end(), 0);
+    for (const StreamSeg& s : segs)
+      if (s.out_slot >= 0) {
+        undirect[(size_t)s.head * nq1 + s.q_begin] += 1;
+        undirect[(size_t)s.head * nq1 + s.q_begin + s.q_count] -= 1;
+      }
+    for (int h = 0; h < hkv; ++h) {
+      int run = 0;
+      for (int qi = 0; qi < num_queries; ++qi) {
+        run += undirect[(size_t)h * nq1 + qi];
+        sbeg[(size_t)qi * hkv + h + 1] = run;
+      }
+    }
+  }
   for (size_t i = 0; i < titems.size(); i += kRecWords) sbeg[(size_t)titems[i] * hkv + titems[i + 1] + 1] += 1;
   for (size_t k = 0; k < nqh; ++k) sbeg[k + 1] += sbeg[k];
   std::vector<int> slot_ids((size_t)sbeg[nqh]);
@@ -1452,7 +1492,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     for (int h = 0; h < hkv; ++h) {
       const size_t k = (size_t)qi * hkv + h;
       const int ns = sbeg[k + 1] - sbeg[k];
-      if (cnt[k] == 1 && nt_q == 0 && ns == 0) continue;   // written directly
+      if (cnt_of(qi, h) == 1 && nt_q == 0 && ns == 0) continue;   // written directly
       int32_t* r = recs.data() + n_recs * kRecWords;
       r[0] = qi;
       r[1] = h;
