@@ -120,6 +120,8 @@ class _PagedPlanner:
         self._rows = None             # row-block kernel: True forces it, False forbids it, None lets the planner pick
         self._num_cus: Optional[int] = None   # planner's CU count (default: the device's)
         self._caps: Optional[_lib.BePlanCaps] = None
+        self._views_key = None          # (plan bytes, workspace bytes) of the cached workspace views
+        self._views = (None, None)
 
     # ---------------------------------------------------------------- plan
     def _plan_levels(self, qo: Sequence, kvp: Sequence, kvi: Sequence, lpl: Sequence, num_qo_heads: int,
@@ -183,22 +185,31 @@ class _PagedPlanner:
             (_lib.BE_PLAN_ROWS if self._rows is True else 0) | \
             (_lib.BE_PLAN_NO_ROWS if self._rows is False else 0)
 
-    def _install_plan(self, info, buf: torch.Tensor, staging: "_Staging", max_page: int, head_dim: int,
-                      sm_scale: Optional[float], q_data_type) -> None:
+    def _install_plan(self, info, buf: torch.Tensor, staging: Optional["_Staging"], max_page: int, head_dim: int,
+                      sm_scale: Optional[float], q_data_type, upload: bool = True) -> None:
         """Upload a plan written into the pinned staging ``buf`` to the
-        workspace (stream-ordered before the next run) and adopt it."""
+        workspace (stream-ordered before the next run) and adopt it.
+        ``upload=False``: the caller copies ``buf`` to the workspace's first
+        ``plan_ints`` words itself, before the next run."""
         plan_bytes = int(info.plan_ints) * 4
         part_off = (plan_bytes + _WS_ALIGN - 1) // _WS_ALIGN * _WS_ALIGN
         need = part_off + int(info.partial_bytes)
         if need > self._ws.numel():
             raise MemoryError(f"attention plan needs {need} workspace bytes, buffer has {self._ws.numel()}")
-        ws_i32 = self._ws[:plan_bytes].view(torch.int32)
-        ws_i32.copy_(buf[: info.plan_ints], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        staging.event = ev
+        key = (plan_bytes, need)
+        if self._views_key != key:
+            # the workspace views of this plan size (a fixed layout keeps them)
+            self._views_key = key
+            self._views = (self._ws[:plan_bytes].view(torch.int32),
+                           self._ws[part_off:need] if info.partial_bytes else None)
+        ws_i32 = self._views[0]
+        if upload:
+            ws_i32.copy_(buf[: info.plan_ints], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            staging.event = ev
         self._plan_dev = ws_i32
-        self._partials = self._ws[part_off:need] if info.partial_bytes else None
+        self._partials = self._views[1]
         if info.counter_bytes:
             c0 = part_off + int(info.counter_offset)
             self._ws[c0:c0 + int(info.counter_bytes)].zero_()

@@ -860,23 +860,27 @@ class NativeBeamState:
             break
         return _parse_metadata(self._meta_buf[: int(self._meta_used.value)].copy(), n)
 
-    def plan_cascade(self, wrapper, num_qo_heads: int, num_kv_heads: int, head_dim: int, q_data_type):
+    def plan_cascade(self, wrapper, num_qo_heads: int, num_kv_heads: int, head_dim: int, q_data_type,
+                     host_plan: Optional[torch.Tensor] = None):
         """This step's cascade metadata and ``wrapper``'s plan of it in one
         native call (``be_trie_plan``: the same plan as ``wrapper.plan`` of
         ``step_metadata``'s levels with ``causal=True``), the plan uploaded
         to the wrapper's workspace.  Returns the candidates' query tokens,
-        write pages, write slots and positions."""
+        write pages, write slots and positions.  ``host_plan`` (pinned int32):
+        the plan is written there and not uploaded -- the caller copies its
+        first ``wrapper._info.plan_ints`` words to the workspace's start before
+        the next run (a plan beyond it raises MemoryError)."""
         from . import _lib
         from .attention import _Staging, _num_cus
         if isinstance(q_data_type, str):
             q_data_type = getattr(torch, q_data_type)
-        staging = _Staging.get(wrapper._ws.device)
+        staging = None if host_plan is not None else _Staging.get(wrapper._ws.device)
         info = _lib.BeAttnPlanInfo()
         max_page = ctypes.c_int32(-1)
         caps = ctypes.byref(wrapper._caps) if wrapper._caps is not None else None
-        cap = staging.buf.numel()
+        cap = host_plan.numel() if host_plan is not None else staging.buf.numel()
         while True:
-            buf = staging.acquire(cap)
+            buf = host_plan if host_plan is not None else staging.acquire(cap)
             meta = self._meta_buf
             rc = self._lib.be_trie_plan(self._h, num_qo_heads, num_kv_heads, head_dim, _lib.dtype_code(q_data_type),
                                         wrapper._plan_flags(), wrapper._num_cus or _num_cus(wrapper._ws.device), caps,
@@ -885,13 +889,18 @@ class NativeBeamState:
             if rc == _lib.BE_ERR_CAPACITY:
                 if int(self._meta_used.value) > meta.size:
                     self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
+                elif host_plan is not None or buf.numel() >= (1 << 26):
+                    # a full caller buffer, or a plan beyond the fixed layout's
+                    # capacities (which no buffer size cures): MemoryError
+                    _lib.check(rc, "cascade plan")
                 else:
                     cap = 2 * buf.numel()
                 continue
             _lib.check(rc, "cascade plan")
             break
         wrapper.num_levels = int(self._meta_buf[0])
-        wrapper._install_plan(info, buf, staging, int(max_page.value), head_dim, None, q_data_type)
+        wrapper._install_plan(info, buf, staging, int(max_page.value), head_dim, None, q_data_type,
+                              upload=host_plan is None)
         n = self.num_candidates()
         oc = int(self._meta_buf[1])
         m = self._meta_buf[oc: oc + 4 * n].copy()

@@ -44,6 +44,13 @@ from .page_table import PageTable
 from .selection import beam_topk, decode_k
 
 
+# Bytes reserved in front of the attention workspace for a graphed step's
+# upload header (inputs and staged copy list: 48 bytes per candidate and some
+# alignment), and of the pinned twin's plan area (a fixed-layout plan).
+_STEP_HEADER_BYTES = 1 << 20
+_STEP_PLAN_BYTES = 8 << 20
+
+
 class BatchedBeamSearch:
     def __init__(self, model, page_table: PageTable, beam_size: int,
                  strategy: Optional[VanillaBeamSearchStrategy] = None, kernel_type: str = "cascade",
@@ -67,7 +74,17 @@ class BatchedBeamSearch:
         # Python trie's passes every step and keep the Python state
         self.state = NativeBeamState(beam_size, page_table) if kernel_type == "cascade" else \
             BeamState(beam_size, page_table, fast_metadata=True)
-        self.ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
+        # The wrappers' workspace (an attention plan at its start) follows a
+        # reserved region whose last bytes hold the graphed step's inputs and
+        # staged fork-copy list: header and plan are contiguous, so a graphed
+        # step uploads all of its host data with one copy from a pinned twin
+        self._hdr = _STEP_HEADER_BYTES
+        self.ws_all = torch.empty(self._hdr + workspace_bytes, dtype=torch.uint8, device=self.device)
+        self.ws = self.ws_all[self._hdr:]
+        self._hblock: Optional[torch.Tensor] = None   # pinned twin of ws_all[hdr - header : hdr + plan]
+        self._hb = 0                                  # the graphed step's header bytes
+        self._up_key, self._up = None, None           # (bytes, (device, host) views) of the step upload
+        self._host_plan: Optional[torch.Tensor] = None   # the pinned twin's plan area (int32)
         self.cascade = MultiLevelCascadeAttentionWrapper(1, self.ws)
         self.flat = BatchDecodeWithPagedKVCacheWrapper(self.ws)
         self.last_attn = None
@@ -190,8 +207,12 @@ class BatchedBeamSearch:
         w.use_fixed_layout(**caps)
         if isinstance(self.state, NativeBeamState) and not self.pt.stage_copies_enabled:
             # from now on each selection's fork copies go to the staged list that
-            # the step graph's first part performs
-            self.pt.enable_staged_copies(2 * n)
+            # the step graph's first part performs (in the upload header when
+            # there is one)
+            if self._gd.copy_list is not None:
+                self.pt.enable_staged_copies(2 * n, *self._gd.copy_list)
+            else:
+                self.pt.enable_staged_copies(2 * n)
         try:
             w.plan(*args, causal=True, q_data_type=m.dtype)
         except (MemoryError, ValueError):
@@ -215,17 +236,22 @@ class BatchedBeamSearch:
         w = None
         graphed = kind == "cascade" and self.graphs and self.step_graph and hasattr(self.model, "decode") and \
             self._graph_ready(n)
+        upload = False                  # one copy uploads the header and the plan
         if graphed and self._fixed is not None and isinstance(st, NativeBeamState):
-            # metadata and the fixed-layout plan in one native call
+            # metadata and the fixed-layout plan in one native call, the plan
+            # written straight into the upload block's pinned twin
             cfg = self.model.cfg
+            host_plan = self._host_plan
             try:
                 qids, wp, wpos, pos = st.plan_cascade(self._fixed, cfg.num_attention_heads,
-                                                      cfg.num_key_value_heads, cfg.head_dim, self.model.dtype)
+                                                      cfg.num_key_value_heads, cfg.head_dim, self.model.dtype,
+                                                      host_plan=host_plan)
             except MemoryError:
                 pass                                # beyond the layout: _fixed_plan re-sizes it
             else:
                 if self._launch_key(self._fixed._info) == self._fixed_key:
                     w = self.last_attn = self._fixed
+                    upload = host_plan is not None
         if w is None:
             if kind == "cascade":
                 # the cascade arrays and the candidates' inputs from the native builder
@@ -249,7 +275,16 @@ class BatchedBeamSearch:
             pos = st.position_ids(reuse_annotation=True)     # _plan's metadata pass just ran
         graph_run = self.step_graphed or (self.graphs and hasattr(self.model, "decode") and self._graph_ready(n))
         if graph_run:
-            self._gd.stage_inputs(qids, pos, wp, wpos)
+            self._gd.stage_inputs(qids, pos, wp, wpos, upload=not upload)
+        if upload:
+            nb = self._hb + 4 * int(w._info.plan_ints)
+            if self._up_key != nb:
+                self._up_key = nb
+                self._up = (self.ws_all[self._hdr - self._hb: self._hdr - self._hb + nb], self._hblock[:nb])
+            self._up[0].copy_(self._up[1], non_blocking=True)
+            self.pt.staged_uploaded()
+        elif self.step_graphed:
+            self.pt.upload_staged()          # the step graph's first node reads the device list
         else:
             if self._staging.numel() < 4 * n:
                 self._staging = torch.empty(8 * n, dtype=torch.int64, pin_memory=True)
@@ -290,7 +325,14 @@ class BatchedBeamSearch:
         stays B per request); a different count runs eagerly."""
         from .llama import GraphedDecoder
         if self._gd is None:
-            self._gd = GraphedDecoder(self.model, self.pt, n)
+            header = None
+            hb = GraphedDecoder.header_bytes(n)
+            if self.device.type == "cuda" and self.kernel_type == "cascade" and self.step_graph and hb <= self._hdr:
+                self._hb = hb
+                self._hblock = torch.zeros(hb + _STEP_PLAN_BYTES, dtype=torch.uint8, pin_memory=True)
+                self._host_plan = self._hblock[hb:].view(torch.int32)
+                header = (self.ws_all[self._hdr - hb: self._hdr], self._hblock[:hb])
+            self._gd = GraphedDecoder(self.model, self.pt, n, header=header)
             self._gd.capture()
         return self._gd.n == n
 

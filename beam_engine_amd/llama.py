@@ -187,6 +187,10 @@ class LlamaDecoder:
         return F.linear(self._rms(x, self.norm), self.lm_head)
 
 
+def _align(nbytes: int, to: int = 256) -> int:
+    return (nbytes + to - 1) // to * to
+
+
 class GraphedDecoder:
     """Decode forward with the non-attention work captured as HIP graphs.
 
@@ -202,19 +206,42 @@ class GraphedDecoder:
     layer's attention included, as one graph for plans of a fixed layout.
     """
 
-    def __init__(self, model: LlamaDecoder, page_table, n: int):
+    @staticmethod
+    def header_bytes(n: int) -> int:
+        """Bytes of a step-upload header for n candidates: the inputs (two
+        int64 and two int32 rows) and a staged fork-copy list of 2n entries."""
+        return _align(16 * n) + _align(8 * n) + _align(4 * (1 + 6 * n))
+
+    def __init__(self, model: LlamaDecoder, page_table, n: int, header=None):
         cfg = model.cfg
         self.model, self.pt, self.n = model, page_table, n
         dev = model.device
         # inputs: token ids and positions (int64), write pages and slots (int32),
-        # each pair one device buffer filled from pinned staging by one copy
-        self._in64 = torch.zeros((2, n), dtype=torch.long, device=dev)
-        self._in32 = torch.zeros((2, n), dtype=torch.int32, device=dev)
+        # each pair one device buffer filled from pinned staging by one copy.
+        # ``header``: (device, pinned host) uint8 views of header_bytes(n) at
+        # the head of a step-upload block; the inputs and the staged copy list
+        # then live there, and the block's owner uploads them with the plan
+        self.header = header
+        pin = dev.type == "cuda"
+        if header is not None:
+            hd, hh = header
+            o32 = _align(16 * n)
+            self._in64 = hd[: 16 * n].view(torch.long).view(2, n)
+            self._in32 = hd[o32: o32 + 8 * n].view(torch.int32).view(2, n)
+            self._h64 = hh[: 16 * n].view(torch.long).view(2, n)
+            self._h32 = hh[o32: o32 + 8 * n].view(torch.int32).view(2, n)
+            ocp = o32 + _align(8 * n)
+            self.copy_list = (hd[ocp: ocp + 4 * (1 + 6 * n)].view(torch.int32),
+                              hh[ocp: ocp + 4 * (1 + 6 * n)].view(torch.int32))
+        else:
+            self._in64 = torch.zeros((2, n), dtype=torch.long, device=dev)
+            self._in32 = torch.zeros((2, n), dtype=torch.int32, device=dev)
+            self._h64 = torch.zeros((2, n), dtype=torch.long, pin_memory=pin)
+            self._h32 = torch.zeros((2, n), dtype=torch.int32, pin_memory=pin)
+            self.copy_list = None
         self.tok, self.pos = self._in64[0], self._in64[1]
         self.wpg, self.wps = self._in32[0], self._in32[1]
-        pin = dev.type == "cuda"
-        self._h64 = torch.zeros((2, n), dtype=torch.long, pin_memory=pin)
-        self._h32 = torch.zeros((2, n), dtype=torch.int32, pin_memory=pin)
+        self._np = (self._h64.numpy(), self._h32.numpy())     # numpy views of the pinned staging
         self.o = torch.zeros((n, cfg.num_attention_heads, cfg.head_dim), dtype=model.dtype, device=dev)
         self.graphs = []
         self.q = []
@@ -318,18 +345,19 @@ class GraphedDecoder:
         self.pt.consume_staged_copies()
         return self.step_logits
 
-    def stage_inputs(self, tok, pos, wpg, wps) -> None:
+    def stage_inputs(self, tok, pos, wpg, wps, upload: bool = True) -> None:
         """Host arrays of the step's inputs -> the graphs' input buffers (two
         copies from pinned staging; the staging is rewritten only after the
-        step's selection has synchronised)."""
-        a = self._h64.numpy()
+        step's selection has synchronised).  ``upload=False``: only the pinned
+        staging is written; the header's owner uploads it."""
+        a, b = self._np
         a[0] = tok
         a[1] = pos
-        b = self._h32.numpy()
         b[0] = wpg
         b[1] = wps
-        self._in64.copy_(self._h64, non_blocking=True)
-        self._in32.copy_(self._h32, non_blocking=True)
+        if upload:
+            self._in64.copy_(self._h64, non_blocking=True)
+            self._in32.copy_(self._h32, non_blocking=True)
 
     def load_inputs(self, tok, pos, wpg, wps) -> None:
         self.tok.copy_(tok, non_blocking=True)

@@ -73,6 +73,8 @@ class PageTable:
         self._staged_dev = self._staged_host = None
         self._staged_max = 0
         self._staged_pending = False
+        self._staged_external = False   # the list's buffers are a caller's, who uploads them
+        self._staged_dirty = False      # the pinned list is newer than the device list
         self.stage_copies_enabled = False
 
         self.kv_pool = torch.zeros((layer_num, max_num_pages, 2, page_size, head_num, head_dim),
@@ -228,17 +230,35 @@ class PageTable:
         return len(todo)
 
     # ------------------------------------------------------------ staged copies
-    def enable_staged_copies(self, max_copies: int) -> None:
+    def enable_staged_copies(self, max_copies: int, dev: Optional[torch.Tensor] = None,
+                             host: Optional[torch.Tensor] = None) -> None:
         """From now on ``stage_copies`` takes the fork copies of a trie update:
         their list goes to a fixed device buffer, and ``run_staged_copies``
         (eager) or a captured ``record_staged_copies`` launch (a graph replay)
-        performs them before anything reads the pages."""
+        performs them before anything reads the pages.  ``dev`` / ``host``
+        (int32, ``1 + 3 * max_copies`` words, the host one pinned): buffers of
+        the caller, who uploads the host list with the rest of a step's data
+        and then calls ``staged_uploaded``; ``upload_staged`` uploads it alone."""
         if self.device.type != "cuda":
             raise ValueError("staged copies need a HIP device")
-        if self._staged_dev is None or self._staged_max < max_copies:
+        if (dev is None) != (host is None):
+            raise ValueError("give both the device and the pinned host list, or neither")
+        if dev is not None:
+            words = 1 + 3 * int(max_copies)
+            if dev.dtype != torch.int32 or host.dtype != torch.int32 or dev.numel() < words or host.numel() < words:
+                raise ValueError(f"staged-copy buffers must be int32 with {words} words")
+            self.run_staged_copies()
+            self._staged_max = int(max_copies)
+            self._staged_dev, self._staged_host = dev, host
+            self._staged_host.zero_()
+            self._staged_dev.zero_()
+            self._staged_external = True
+            self._staged_dirty = False
+        elif self._staged_dev is None or self._staged_max < max_copies:
             self._staged_max = int(max_copies)
             self._staged_dev = torch.zeros(1 + 3 * self._staged_max, dtype=torch.int32, device=self.device)
             self._staged_host = torch.zeros(1 + 3 * self._staged_max, dtype=torch.int32, pin_memory=True)
+            self._staged_external = False
         self.stage_copies_enabled = True
 
     def stage_copies(self, copies: np.ndarray) -> None:
@@ -263,13 +283,29 @@ class PageTable:
             h[1:1 + n] = c[:, 0]
             h[1 + m:1 + m + n] = c[:, 1]
             h[1 + 2 * m:1 + 2 * m + n] = c[:, 2]
-        self._staged_dev[: 1 + 3 * m].copy_(self._staged_host[: 1 + 3 * m], non_blocking=True)
+        if self._staged_external:
+            self._staged_dirty = True          # the caller's step upload carries it
+        else:
+            self._staged_dev[: 1 + 3 * m].copy_(self._staged_host[: 1 + 3 * m], non_blocking=True)
         self._staged_pending = n > 0
+
+    def staged_uploaded(self) -> None:
+        """The caller's step upload copied the pinned list to the device list."""
+        self._staged_dirty = False
+
+    def upload_staged(self) -> None:
+        """Upload the pinned list alone if it is newer than the device list."""
+        if self._staged_dirty:
+            m = self._staged_max
+            self._staged_dev[: 1 + 3 * m].copy_(self._staged_host[: 1 + 3 * m], non_blocking=True)
+            self._staged_dirty = False
 
     def record_staged_copies(self) -> None:
         """Launch the counted copy of the staged list (inside a graph capture,
         or eagerly): entries below the device count are copied."""
         lib = _lib.load()
+        if not torch.cuda.is_current_stream_capturing():
+            self.upload_staged()
         d = self._staged_dev
         m = self._staged_max
         base = d.data_ptr()

@@ -53,6 +53,28 @@ def _staging(dev, name, n, dtype):
     return t[:n]
 
 
+_dev_outs = {}
+
+
+def _selection_block(dev, m: int):
+    """Device block (cached per device) holding a selection's parent (i32),
+    token (i32) and score (f64) arrays back to back, and its pinned twin: one
+    copy brings all three to the host.  Only for calls that synchronise before
+    returning copies of the host views."""
+    key = (dev.type, dev.index)
+    a = (4 * m + 7) // 8 * 8
+    nbytes = 2 * a + 8 * m
+    blk = _dev_outs.get(key)
+    if blk is None or blk[0].numel() < nbytes:
+        blk = _dev_outs[key] = (torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=dev),
+                                torch.empty(max(nbytes, 4096), dtype=torch.uint8, pin_memory=True))
+    d, h = blk
+
+    def views(t):
+        return (t[:4 * m].view(torch.int32), t[a:a + 4 * m].view(torch.int32), t[2 * a:2 * a + 8 * m].view(torch.float64))
+    return d[:nbytes], h[:nbytes], views(d), views(h)
+
+
 TEMPERATURE_MODES = {"reciprocal": _lib.BE_TEMP_RECIPROCAL, "divide": _lib.BE_TEMP_DIVIDE}
 
 
@@ -124,9 +146,12 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
                     _row_ptrs.clear()
                 ptr_dev = _row_ptrs[key] = torch.tensor(
                     np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)).to(dev)
-        outs = (torch.empty(n_req * beam, dtype=torch.int32, device=dev),
-                torch.empty(n_req * beam, dtype=torch.int32, device=dev),
-                torch.empty(n_req * beam, dtype=torch.float64, device=dev))
+        if to_host:
+            blk_dev, blk_host, outs, outs_host = _selection_block(dev, n_req * beam)
+        else:
+            outs = (torch.empty(n_req * beam, dtype=torch.int32, device=dev),
+                    torch.empty(n_req * beam, dtype=torch.int32, device=dev),
+                    torch.empty(n_req * beam, dtype=torch.float64, device=dev))
     rc = lib.be_beam_topk(logits.data_ptr(), _lib.dtype_code(logits.dtype), n, v, logits.stride(0),
                           float(temperature), tmode, k,
                           _lib.ptr(ps), beam, n_req, _lib.ptr(ptr_dev), max_rows, row_vals.data_ptr(),
@@ -135,15 +160,9 @@ def beam_topk(logits: torch.Tensor, k: int, parent_scores: Optional[torch.Tensor
     _lib.check(rc, "beam top-k")
     if beam > 0:
         if to_host:
-            m = outs[0].numel()
-            hp = _staging(dev, "parent", m, torch.int32)
-            ht = _staging(dev, "token", m, torch.int32)
-            hs = _staging(dev, "score", m, torch.float64)
-            hp.copy_(outs[0], non_blocking=True)
-            ht.copy_(outs[1], non_blocking=True)
-            hs.copy_(outs[2], non_blocking=True)
+            blk_host.copy_(blk_dev, non_blocking=True)
             torch.cuda.current_stream(dev).synchronize()
-            outs = (hp.clone(), ht.clone(), hs.clone())
+            outs = tuple(t.clone() for t in outs_host)
         return row_vals, row_idx, outs
     return row_vals, row_idx
 
