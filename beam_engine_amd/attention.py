@@ -67,11 +67,19 @@ class _Staging:
         return self.buf
 
 
+_cus_by_dev = {}
+
+
 def _num_cus(device: torch.device) -> int:
-    try:
-        return int(torch.cuda.get_device_properties(device).multi_processor_count)
-    except Exception:   # noqa: BLE001 - properties are a sizing hint only
-        return 256
+    key = (device.type, device.index)
+    n = _cus_by_dev.get(key)
+    if n is None:
+        try:
+            n = int(torch.cuda.get_device_properties(device).multi_processor_count)
+        except Exception:   # noqa: BLE001 - properties are a sizing hint only
+            n = 256
+        _cus_by_dev[key] = n
+    return n
 
 
 class PlanStats:

@@ -757,8 +757,10 @@ class NativeBeamState:
         self._mirror: Optional[BeamState] = None
         self._mirror_ver = -1
         self._meta_buf = np.zeros(1 << 16, np.int32)
+        self._meta_ptr = (None, 0)          # (buffer, its address) for the planner call
         self._meta_used = ctypes.c_int64(0)
         self._copies = np.zeros(3 * 1024, np.int32)
+        self._copies_ptr = (None, 0)        # (buffer, its address) for the trie update call
         self._ncopies = ctypes.c_int32(0)
         self._warn = ctypes.c_int32(0)
 
@@ -803,16 +805,23 @@ class NativeBeamState:
         reference's prune and expand rules, with this step's fork copies issued
         in one launch.  Returns the number of fork copies."""
         from . import _lib
-        par = np.ascontiguousarray(parent, dtype=np.int32)
-        tok = np.ascontiguousarray(token, dtype=np.int32)
-        sc = np.ascontiguousarray(score, dtype=np.float64)
-        n = len(par)
-        if len(tok) != n or len(sc) != n:
+        arrs = []
+        for x, dt, tdt in ((parent, np.int32, torch.int32), (token, np.int32, torch.int32),
+                           (score, np.float64, torch.float64)):
+            if isinstance(x, torch.Tensor) and x.device.type == "cpu" and x.dtype == tdt and x.is_contiguous():
+                arrs.append((x.numel(), x.data_ptr(), x))       # the selection's host tensors as they are
+            else:
+                a = np.ascontiguousarray(x, dtype=dt)
+                arrs.append((len(a), a.ctypes.data, a))
+        n = arrs[0][0]
+        if arrs[1][0] != n or arrs[2][0] != n:
             raise ValueError("parent, token and score must have one entry each")
         if self._copies.size < 3 * n:
             self._copies = np.zeros(6 * n, np.int32)
-        rc = self._lib.be_trie_apply(self._h, par.ctypes.data, tok.ctypes.data, sc.ctypes.data, n,
-                                     -1 if eos_token_id is None else int(eos_token_id), self._copies.ctypes.data,
+        if self._copies_ptr[0] is not self._copies:
+            self._copies_ptr = (self._copies, self._copies.ctypes.data)
+        rc = self._lib.be_trie_apply(self._h, arrs[0][1], arrs[1][1], arrs[2][1], n,
+                                     -1 if eos_token_id is None else int(eos_token_id), self._copies_ptr[1],
                                      self._copies.size // 3, ctypes.byref(self._ncopies), ctypes.byref(self._warn))
         _lib.check(rc, "trie update")
         if self._warn.value:
@@ -882,9 +891,11 @@ class NativeBeamState:
         while True:
             buf = host_plan if host_plan is not None else staging.acquire(cap)
             meta = self._meta_buf
+            if self._meta_ptr[0] is not meta:
+                self._meta_ptr = (meta, meta.ctypes.data)
             rc = self._lib.be_trie_plan(self._h, num_qo_heads, num_kv_heads, head_dim, _lib.dtype_code(q_data_type),
                                         wrapper._plan_flags(), wrapper._num_cus or _num_cus(wrapper._ws.device), caps,
-                                        meta.ctypes.data, meta.size, ctypes.byref(self._meta_used), buf.data_ptr(),
+                                        self._meta_ptr[1], meta.size, ctypes.byref(self._meta_used), buf.data_ptr(),
                                         buf.numel(), ctypes.byref(info), ctypes.byref(max_page))
             if rc == _lib.BE_ERR_CAPACITY:
                 if int(self._meta_used.value) > meta.size:
@@ -901,7 +912,7 @@ class NativeBeamState:
         wrapper.num_levels = int(self._meta_buf[0])
         wrapper._install_plan(info, buf, staging, int(max_page.value), head_dim, None, q_data_type,
                               upload=host_plan is None)
-        n = self.num_candidates()
+        n = int(info.num_queries)                      # one query per candidate
         oc = int(self._meta_buf[1])
         m = self._meta_buf[oc: oc + 4 * n].copy()
         return m[:n], m[n: 2 * n], m[2 * n: 3 * n], m[3 * n:]

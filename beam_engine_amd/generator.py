@@ -352,7 +352,7 @@ class BatchedBeamSearch:
                                              self.temperature, request_rows=rows, to_host=True,
                                              temperature_mode=self.temperature_mode)
             self.pt.raise_staged_errors()
-            st.apply_selection(par.numpy(), tok.numpy(), sc.numpy(), self.eos_token_id)
+            st.apply_selection(par, tok, sc, self.eos_token_id)
             return
         results = self.strategy.select_batched(st, logits, self.temperature, self.temperature_mode)
         self.pt.raise_staged_errors()

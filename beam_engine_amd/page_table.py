@@ -85,6 +85,7 @@ class PageTable:
         # page, slot or position outside the pool (read by check_errors)
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._err_host = torch.zeros(1, dtype=torch.int32, pin_memory=self.device.type == "cuda")
+        self._err_np = self._err_host.numpy()     # its numpy view (a cheap read after each synchronisation)
         logger.info("Initialized PageTable: %d layers, %d pages of size %d", layer_num, max_num_pages, page_size)
 
     # ------------------------------------------------------------ allocator
@@ -152,7 +153,7 @@ class PageTable:
         """Raise ValueError if the staged count is non-zero (the reference
         raises ValueError for a write to a page it does not hold,
         page_table.py:150-151); the device count is cleared first."""
-        bad = int(self._err_host[0])
+        bad = int(self._err_np[0])
         if bad:
             self._err.zero_()
             self._err_host.zero_()
