@@ -233,6 +233,12 @@ class GraphedDecoder:
             ocp = o32 + _align(8 * n)
             self.copy_list = (hd[ocp: ocp + 4 * (1 + 6 * n)].view(torch.int32),
                               hh[ocp: ocp + 4 * (1 + 6 * n)].view(torch.int32))
+            # the header is carved from uninitialised memory: valid inputs (token
+            # 0, position 0) until the first step stages its own
+            self._in64.zero_()
+            self._in32.zero_()
+            self._h64.zero_()
+            self._h32.zero_()
         else:
             self._in64 = torch.zeros((2, n), dtype=torch.long, device=dev)
             self._in32 = torch.zeros((2, n), dtype=torch.int32, device=dev)
@@ -272,7 +278,10 @@ class GraphedDecoder:
     @torch.no_grad()
     def capture(self) -> None:
         L = self.model.cfg.num_hidden_layers
-        # capture-time writes land in a scratch slot; real steps overwrite the inputs
+        # the warm-up pass below reads the inputs: token 0 at position 0, its
+        # writes landing in a scratch slot; real steps overwrite the inputs
+        self.tok.zero_()
+        self.pos.zero_()
         self.wpg.fill_(self._scratch_page)
         self.wps.zero_()
         side = torch.cuda.Stream()

@@ -23,6 +23,8 @@ class _Stream:
 def _decoder(layers, seen, fail_at=None):
     gd = llama.GraphedDecoder.__new__(llama.GraphedDecoder)
     gd.model = SimpleNamespace(cfg=SimpleNamespace(num_hidden_layers=layers))
+    gd.tok = torch.full((4,), 7, dtype=torch.long)
+    gd.pos = torch.full((4,), 9, dtype=torch.long)
     gd.wpg = torch.zeros(4, dtype=torch.int32)
     gd.wps = torch.zeros(4, dtype=torch.int32)
     gd._scratch_page = 3
@@ -57,6 +59,8 @@ def test_capture_disables_automatic_gc(monkeypatch):
     # three warm-up segments with collection on, three captured with it off
     assert seen == [True] * 3 + [False] * 3
     assert gc.isenabled() and len(gd.graphs) == 3 and gd.wpg.tolist() == [3] * 4
+    # the warm-up pass reads valid inputs: token 0 at position 0
+    assert gd.tok.tolist() == [0] * 4 and gd.pos.tolist() == [0] * 4
 
 
 def test_capture_restores_gc_after_an_error(monkeypatch):

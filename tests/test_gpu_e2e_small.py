@@ -210,3 +210,41 @@ def test_eos_finishes_beams_and_decoding_continues():
     assert gen.state.finished_candidates and all(c.sequence[-1] == eos for c in gen.state.finished_candidates)
     assert min(counts) < 8 and counts[0] == 8
     assert all(eos not in gen.state.sequence(c)[18:] for c in gen.state.candidates)
+
+
+def test_graphed_decoder_inputs_start_valid_on_reused_memory():
+    """The graphed decoder's input buffers are carved from the generator's
+    workspace (torch.empty).  Memory the caching allocator hands back holds
+    earlier contents: the buffers must still read token 0 at position 0 for
+    the capture's warm-up pass, and the graphed steps must match the eager
+    ones.  The workspace's block is first filled with 0x7f bytes and freed,
+    so that the generator reuses it."""
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    say("graphed decoder on reused workspace memory")
+    from beam_engine_amd import PageTable
+    from beam_engine_amd.generator import BatchedBeamSearch, _STEP_HEADER_BYTES
+    from beam_engine_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(num_hidden_layers=2, hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
+                      head_dim=128, intermediate_size=512, vocab_size=700, max_position_embeddings=512)
+    ws_bytes = 8 << 20
+    runs = []
+    for graphs in (False, True):
+        junk = torch.full((_STEP_HEADER_BYTES + ws_bytes,), 0x7F, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        del junk
+        model = LlamaDecoder(cfg, "cuda", torch.bfloat16, seed=12)
+        pt = PageTable(2, page_size=16, max_num_pages=256, head_num=2, head_dim=128, device="cuda",
+                       store_dtype=torch.bfloat16)
+        gen = BatchedBeamSearch(model, pt, 4, kernel_type="cascade", graphs=graphs, workspace_bytes=ws_bytes)
+        gen.prefill([list(range(3, 40)), list(range(50, 87))])
+        runs.append(gen)
+    ge, gg = runs
+    for step in range(6):
+        ge.step()
+        gg.step()
+        torch.cuda.synchronize()
+        assert [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in ge.state.candidates] == \
+            [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in gg.state.candidates], f"step {step}"
+    assert gg._gd is not None
