@@ -1290,6 +1290,8 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
   __shared__ int wslow[4];
   __shared__ int ncand;
   __shared__ uint64_t lc[kMaxCap];
+  __shared__ uint4 kst[kPerThread / 8 * kTopkThreads];   // a unit's keys, for the candidate pass
+  static_assert(sizeof(T) == 2 && kPerThread == 32, "16 words of two 16-bit logits per thread");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int segs = a.segs, k = a.k, cap = a.cap, seg_len = a.seg_len, vocab = a.vocab;
   const int units = a.n_rows * segs;
@@ -1374,29 +1376,34 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     const uint32_t tau = max(1u, min(min(wtau[0], wtau[1]), min(wtau[2], wtau[3])));
     const v2u16 t1 = {(unsigned short)(tau - 1), (unsigned short)(tau - 1)};
     const v2u16 one = {1, 1};
-    v2u16 c2 = {0, 0};
+    // one bit per key >= tau: bit i for the low half of word i, bit 16 + i for
+    // its high half
+    uint32_t cm = 0;
 #pragma unroll
     for (int i = 0; i < kWords; ++i)
-      c2 += __builtin_elementwise_min(__builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, x.w[i]), t1), one);
-    const int mine = (int)c2.x + (int)c2.y;
+      cm |= __builtin_bit_cast(uint32_t, __builtin_elementwise_min(
+                __builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, x.w[i]), t1), one)) << i;
+    const int mine = __popc(cm);
     const int incl = wave_scan_add(mine);
     int wbase = 0;
     if (lane == 63) wbase = atomicAdd(&ncand, incl);
     int at = (int)lane63((uint32_t)wbase) + incl - mine;
-    if (mine > 0) {
+    if (__builtin_amdgcn_ballot_w64(mine > 0)) {
+      // the keys go through LDS so that a thread visits only its set bits (a
+      // register cannot be indexed per lane); each thread reads back its own
+      // words only
 #pragma unroll
-      for (int i = 0; i < kWords; ++i) {
-        const uint32_t lo = x.w[i] & 0xffffu, hi = x.w[i] >> 16;
-        if (max(lo, hi) >= tau) {
-          if (lo >= tau) {
-            if (at < cap) lc[at] = ((uint64_t)lo << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i));
-            ++at;
-          }
-          if (hi >= tau) {
-            if (at < cap) lc[at] = ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)(b + seg_pos<T>(2 * i + 1));
-            ++at;
-          }
-        }
+      for (int c = 0; c < kWords / 4; ++c)
+        kst[c * kTopkThreads + tid] = make_uint4(x.w[4 * c], x.w[4 * c + 1], x.w[4 * c + 2], x.w[4 * c + 3]);
+      const uint16_t* kh = reinterpret_cast<const uint16_t*>(kst);
+      while (cm) {
+        const int j = __builtin_ctz(cm), i = j & 15, h = j >> 4;
+        cm &= cm - 1;
+        const int q = (i >> 2) * kTopkThreads + tid;       // the word's 16-byte chunk
+        const uint32_t key = kh[q * 8 + (i & 3) * 2 + h];
+        // position (i >> 2) * 256 * 8 + tid * 8 + 2 (i & 3) + h, as seg_pos(2 i + h)
+        if (at < cap) lc[at] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)(b + q * 8 + (i & 3) * 2 + h);
+        ++at;
       }
     }
     __syncthreads();
