@@ -152,10 +152,11 @@ __device__ __forceinline__ SegReg seg_reg(const StreamSeg& x) {
 // Online softmax of one (query, KV head) over its tail chunks c = first,
 // first + stride, ... < nt (16 tokens of one page each; ent: lane k holds
 // chunk k's page id and in-page offset | valid << 16).  K and V rows go from
-// global memory through registers (two chunks in flight) into the wave's 8 KB
-// LDS area and the streaming tile step, rows = the g query heads of the KV
-// head.  A token in two groups counts twice, as two merged groups would count it.
-template <typename T>
+// global memory through registers (NB chunks in flight, 32 VGPRs each) into
+// the wave's 8 KB LDS area and the streaming tile step, rows = the g query
+// heads of the KV head.  A token in two groups counts twice, as two merged
+// groups would count it.
+template <typename T, int NB = 2>
 __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t q_sh, const void* kv, int ps, int hkv,
                                             int g, int qi, int h, int2 ent, int nt, int first, int stride,
                                             unsigned char* area, float scale, float& m_run, float& l_run,
@@ -180,7 +181,7 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
   }
   // rows 4 i + lg of chunk c, 16-byte column slot lc holding global column lc ^ row,
   // into register buffer b
-  v4i kr[2][4], vr[2][4];
+  v4i kr[NB][4], vr[NB][4];
   auto load = [&](int c, int b) {
     const int page = __builtin_amdgcn_readlane(ent.x, c);
     const int ov = __builtin_amdgcn_readlane(ent.y, c);
@@ -194,7 +195,7 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
       vr[b][i] = *reinterpret_cast<const v4i*>(src + plane);
     }
   };
-  // chunk c from buffer b to LDS, chunk c + 2 stride into buffer b, then compute c
+  // chunk c from buffer b to LDS, chunk c + NB stride into buffer b, then compute c
   auto step = [&](int c, int b) {
     const int valid = __builtin_amdgcn_readlane(ent.y, c) >> 16;
 #pragma unroll
@@ -203,14 +204,16 @@ __device__ __forceinline__ void tail_chunks(const void* q, int64_t q_sn, int64_t
       *reinterpret_cast<v4i*>(kt + r * 256 + lc * 16) = kr[b][i];
       *reinterpret_cast<v4i*>(vt + r * 256 + lc * 16) = vr[b][i];
     }
-    if (c + 2 * stride < nt) load(c + 2 * stride, b);
+    if (c + NB * stride < nt) load(c + NB * stride, b);
     tile_compute<T, 1, 8>(kt, vt, qf, koff, voff8, 0, valid, lg, scale, m_run, l_run, o_acc);
   };
-  if (first < nt) load(first, 0);
-  if (first + stride < nt) load(first + stride, 1);
-  for (int c = first; c < nt; c += 2 * stride) {
-    step(c, 0);
-    if (c + stride < nt) step(c + stride, 1);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    if (first + b * stride < nt) load(first + b * stride, b);
+  for (int c = first; c < nt; c += NB * stride) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      if (c + b * stride < nt) step(c + b * stride, b);
   }
 }
 
@@ -988,6 +991,7 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
 // by log-sum-exp with a running max, one (head, 4 columns) entry per thread.
 // Each wave keeps the K/V rows of its next two chunks in flight.  A record
 // with neither tail chunks nor slots writes o = 0 and lse = -inf.
+constexpr int kTailDepth = 2;                  // tail chunks in flight per wave (3 measured slower)
 template <typename T, int WPR>
 __global__ __launch_bounds__(256, 2) void tail_merge_kernel(TailMergeArgs m) {
   constexpr int RPB = 4 / WPR;                 // records per workgroup
@@ -1052,7 +1056,7 @@ __global__ __launch_bounds__(256, 2) void tail_merge_kernel(TailMergeArgs m) {
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) o_acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
   if (nt > 0) {
-    tail_chunks<T>(m.q, m.q_sn, m.q_sh, m.kv, m.page_size, m.hkv, g, qi, h, ent, nt, sw, WPR, tl_lds[wv],
+    tail_chunks<T, kTailDepth>(m.q, m.q_sn, m.q_sh, m.kv, m.page_size, m.hkv, g, qi, h, ent, nt, sw, WPR, tl_lds[wv],
                    m.scale_log2, m_run, l_run, o_acc);
     float l = l_run;
     l = rows4_sum(l);
