@@ -59,6 +59,8 @@ CASES = {
     "more_queries_than_keys": ([8], [5], 8, 8, 128, 4),
     "g8_page4": ([129, 77], [129, 200], 64, 8, 128, 4),
     "mha_d64": ([96, 31], [96, 31], 8, 8, 64, 16),
+    # a long prompt at every storage type, fp32 included (the VALU kernel's long causal path)
+    "long_mha_d64": ([1000], [1000], 8, 8, 64, 16),
 }
 
 
@@ -68,8 +70,9 @@ CASES = {
 def test_prefill_wrapper_causal(ws, dtype, case, cus):
     from beam_engine_amd import BatchPrefillWithPagedKVCacheWrapper
     q_lens, kv_lens, hq, hkv, d, page = CASES[case]
-    if dtype == torch.float32 and max(q_lens) > 300:
-        pytest.skip("fp32 VALU kernel: long prompts checked at 16-bit storage")
+    if dtype == torch.float32 and max(q_lens) > 300 and hq * d > 512:
+        pytest.skip("fp32 VALU kernel: long prompts at 32 heads x 128 are slow there; "
+                    "its long causal path runs in long_mha_d64")
     print(f"[case] prefill {case} {dtype} cus={cus}", flush=True)
     (qo, kvp, kvi, lpl), pages = _levels(q_lens, kv_lens, page)
     g = torch.Generator().manual_seed(7)
