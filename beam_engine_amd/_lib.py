@@ -76,6 +76,19 @@ class BeAttnPlanInfo(ctypes.Structure):
                                               "off_seg_causal")]
 
 
+BE_KIND_CASCADE, BE_KIND_FLAT, BE_KIND_SPLIT, BE_KIND_TREE, BE_KIND_AUTO = 0, 1, 2, 3, 4
+BE_EDGES_FITTED, BE_EDGES_FASTTREE = 0, 1
+KIND_CODES = {"cascade": BE_KIND_CASCADE, "flat": BE_KIND_FLAT, "split": BE_KIND_SPLIT, "tree": BE_KIND_TREE,
+              "auto": BE_KIND_AUTO}
+KIND_NAMES = {v: k for k, v in KIND_CODES.items()}
+
+
+class BeTreeModel(ctypes.Structure):
+    _fields_ = [("tile_nt", ctypes.c_double * 4)] + [
+        (n, ctypes.c_double) for n in ("seg", "slot", "tail", "fixed", "alpha", "beta", "gamma")] + [
+        (n, ctypes.c_int32) for n in ("num_qo_heads", "num_kv_heads", "edge_model", "reserved")]
+
+
 EXPORTS = (
     "be_version", "be_last_error", "be_kv_append", "be_rope_qkv_append", "be_page_copy", "be_page_copy_counted",
     "be_attn_plan",
@@ -84,7 +97,8 @@ EXPORTS = (
     "be_diverse_select", "be_pages_create", "be_pages_destroy", "be_pages_allocate", "be_pages_share",
     "be_pages_release", "be_pages_reserve", "be_pages_num_free", "be_pages_ref_count", "be_pages_free_list",
     "be_trie_create", "be_trie_destroy", "be_trie_add_root", "be_trie_apply", "be_trie_sizes",
-    "be_trie_candidates", "be_trie_export", "be_trie_metadata", "be_trie_plan",
+    "be_trie_candidates", "be_trie_export", "be_trie_metadata", "be_trie_plan", "be_trie_levels",
+    "be_trie_plan_kind", "be_trie_metadata_kind",
 )
 
 _lib = None
@@ -150,6 +164,12 @@ def load() -> ctypes.CDLL:
     lib.be_trie_metadata.argtypes = [vp, vp, i64, i64p]
     lib.be_trie_plan.argtypes = [vp, i32, i32, i32, i32, i32, i32, ctypes.POINTER(BePlanCaps), vp, i64, i64p, vp,
                                  i64, ctypes.POINTER(BeAttnPlanInfo), i32p]
+    lib.be_trie_levels.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, ctypes.POINTER(BeTreeModel), vp,
+                                   i64, i64p, i32p, vp]
+    lib.be_trie_metadata_kind.argtypes = [vp, i32, i32, ctypes.POINTER(BeTreeModel), vp, i64, i64p, i32p, vp]
+    lib.be_trie_plan_kind.argtypes = [vp, i32, i32, ctypes.POINTER(BeTreeModel), i32, i32, i32, i32, i32, i32,
+                                      ctypes.POINTER(BePlanCaps), vp, i64, i64p, vp, i64,
+                                      ctypes.POINTER(BeAttnPlanInfo), i32p, i32p, vp]
     for name in EXPORTS:
         if name not in ("be_version", "be_last_error", "be_beam_topk_workspace_bytes", "be_pages_create",
                         "be_pages_destroy", "be_trie_create", "be_trie_destroy"):

@@ -430,14 +430,16 @@ class BeamState:
         return levels, buf[oc: oc + n], buf[oc + n: oc + 2 * n], buf[oc + 2 * n: oc + 3 * n], \
             buf[oc + 3 * n: oc + 4 * n]
 
-    def segment_tree(self):
+    def segment_tree(self, include_self: bool = False):
         """The live trie's segments (the cascade's groups: unbranched page
         chains between branch points), parents before children.
 
         Returns ``(segs, paths)``: ``segs[i] = [pages, tokens, parent index or
         -1, candidate indices below it, child indices]`` (a candidate's own
-        leaf segment excludes its newest token, the cascade convention) and
-        ``paths[q]`` = the segment indices of candidate q's path, top down."""
+        leaf segment excludes its newest token, the cascade convention, unless
+        ``include_self``: FastTree's req_to_token covers the whole path,
+        beam_state.py:512-564) and ``paths[q]`` = the segment indices of
+        candidate q's path, top down."""
         self._annotate()
         ps = self.page_table.page_size
         index: Dict[int, int] = {}
@@ -451,7 +453,7 @@ class BeamState:
                 i = index.get(id(rep))
                 if i is None:
                     pages = self._seg_pages(rep)
-                    last = max(0, len(rep.tokens) - 1) if rep is leaf else len(rep.tokens)
+                    last = max(0, len(rep.tokens) - 1) if rep is leaf and not include_self else len(rep.tokens)
                     i = index[id(rep)] = len(segs)
                     segs.append([pages, (len(pages) - 1) * ps + last, parent, [], []])
                     if parent >= 0:
@@ -482,63 +484,11 @@ class BeamState:
         return absorbed, teff
 
     def tree_levels(self, segs, paths, absorbed):
-        """Level arrays of a decomposition: a segment's pass reads its own
-        pages after those of the ancestors it absorbed and serves the
-        candidates below it that no absorbing child covers; a candidate's
-        passes along its path are its levels 0, 1, ...  Candidates served at
-        a level by one segment but not contiguous in candidate order get one
-        group per run; candidates without a pass at a level get empty
-        groups."""
-        ps = self.page_table.page_size
-        pages_eff: Dict[int, List[int]] = {}
+        """Level arrays of a decomposition (``decomposition_levels`` at this
+        state's page size)."""
+        return decomposition_levels(segs, paths, absorbed, self.page_table.page_size)
 
-        def eff(k):
-            p = pages_eff.get(k)
-            if p is None:
-                p = segs[k][0]
-                if k in absorbed:
-                    p = eff(segs[k][2]) + p
-                pages_eff[k] = p
-            return p
-        per_level: List[Dict[int, List[int]]] = []
-        for qi, keys in enumerate(paths):
-            lv = 0
-            for j, k in enumerate(keys):
-                if j + 1 < len(keys) and keys[j + 1] in absorbed:
-                    continue
-                if lv == len(per_level):
-                    per_level.append({})
-                per_level[lv].setdefault(k, []).append(qi)
-                lv += 1
-        n = len(paths)
-        levels = []
-        for groups in per_level:
-            runs = []
-            for k, qs in groups.items():
-                start = prev = qs[0]
-                for q in qs[1:]:
-                    if q != prev + 1:
-                        runs.append((start, prev + 1, k))
-                        start = q
-                    prev = q
-                runs.append((start, prev + 1, k))
-            runs.sort()
-            qo, kvp, kvi, lpl = [0], [0], [], []
-            for q0, q1, k in runs:
-                if q0 > qo[-1]:                      # candidates without a pass here
-                    qo.append(q0); kvp.append(len(kvi)); lpl.append(0)
-                pages = eff(k)
-                tok = len(pages) * ps - (ps * len(segs[k][0]) - segs[k][1])
-                kvi.extend(pages)
-                kvp.append(len(kvi))
-                lpl.append(tok - (len(pages) - 1) * ps if pages else 0)
-                qo.append(q1)
-            if qo[-1] < n:
-                qo.append(n); kvp.append(len(kvi)); lpl.append(0)
-            levels.append((qo, kvp, kvi, lpl))
-        return levels
-
-    def tree_lists(self, absorb):
+    def tree_lists(self, absorb, include_self: bool = False):
         """Exact path attention as levels of shared passes (the decomposition of
         FastTree's preparation, attention/fasttree/preparation.py:60-105, over
         the cascade's segments instead of single pages): every candidate
@@ -548,7 +498,7 @@ class BeamState:
         last_page_len)] per level."""
         if not self.candidates:
             return []
-        segs, paths = self.segment_tree()
+        segs, paths = self.segment_tree(include_self)
         absorbed, _ = self.absorb_edges(segs, absorb)
         return self.tree_levels(segs, paths, absorbed)
 
@@ -704,6 +654,64 @@ class BeamState:
             out.append((seq, sc))
         out.sort(key=lambda x: x[1], reverse=True)
         return out[:num_return]
+
+
+def decomposition_levels(segs, paths, absorbed, page_size: int):
+    """Level arrays of a decomposition: a segment's pass reads its own
+    pages after those of the ancestors it absorbed and serves the
+    candidates below it that no absorbing child covers; a candidate's
+    passes along its path are its levels 0, 1, ...  Candidates served at
+    a level by one segment but not contiguous in candidate order get one
+    group per run; candidates without a pass at a level get empty
+    groups."""
+    ps = page_size
+    pages_eff: Dict[int, List[int]] = {}
+
+    def eff(k):
+        p = pages_eff.get(k)
+        if p is None:
+            p = segs[k][0]
+            if k in absorbed:
+                p = eff(segs[k][2]) + p
+            pages_eff[k] = p
+        return p
+    per_level: List[Dict[int, List[int]]] = []
+    for qi, keys in enumerate(paths):
+        lv = 0
+        for j, k in enumerate(keys):
+            if j + 1 < len(keys) and keys[j + 1] in absorbed:
+                continue
+            if lv == len(per_level):
+                per_level.append({})
+            per_level[lv].setdefault(k, []).append(qi)
+            lv += 1
+    n = len(paths)
+    levels = []
+    for groups in per_level:
+        runs = []
+        for k, qs in groups.items():
+            start = prev = qs[0]
+            for q in qs[1:]:
+                if q != prev + 1:
+                    runs.append((start, prev + 1, k))
+                    start = q
+                prev = q
+            runs.append((start, prev + 1, k))
+        runs.sort()
+        qo, kvp, kvi, lpl = [0], [0], [], []
+        for q0, q1, k in runs:
+            if q0 > qo[-1]:                      # candidates without a pass here
+                qo.append(q0); kvp.append(len(kvi)); lpl.append(0)
+            pages = eff(k)
+            tok = len(pages) * ps - (ps * len(segs[k][0]) - segs[k][1])
+            kvi.extend(pages)
+            kvp.append(len(kvi))
+            lpl.append(tok - (len(pages) - 1) * ps if pages else 0)
+            qo.append(q1)
+        if qo[-1] < n:
+            qo.append(n); kvp.append(len(kvi)); lpl.append(0)
+        levels.append((qo, kvp, kvi, lpl))
+    return levels
 
 
 class _PageRef:
@@ -869,6 +877,31 @@ class NativeBeamState:
             break
         return _parse_metadata(self._meta_buf[: int(self._meta_used.value)].copy(), n)
 
+    def step_levels(self, kind: str = "cascade", include_self: bool = False, model=None):
+        """One strategy's levels and the candidates' inputs from the native
+        trie (``be_trie_levels``): ``kind`` "cascade" (``step_metadata``),
+        "flat", "split", "tree" or "auto" (``model``: a ``be_tree_model``,
+        ``StrategyPicker.tree_model()``).  Returns ``(levels, query tokens,
+        write pages, write slots, positions, kind built, option costs)``; the
+        costs (flat, split, tree) are given for "auto" only."""
+        from . import _lib
+        n = self.num_candidates()
+        chosen = ctypes.c_int32(-1)
+        costs = np.full(3, np.nan)
+        pm = ctypes.byref(model) if model is not None else None
+        while True:
+            buf = self._meta_buf
+            rc = self._lib.be_trie_metadata_kind(self._h, _lib.KIND_CODES[kind], int(include_self), pm,
+                                                 buf.ctypes.data, buf.size, ctypes.byref(self._meta_used),
+                                                 ctypes.byref(chosen), costs.ctypes.data)
+            if rc == _lib.BE_ERR_CAPACITY and int(self._meta_used.value) > buf.size:
+                self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
+                continue
+            _lib.check(rc, f"{kind} levels")
+            break
+        out = _parse_metadata(self._meta_buf[: int(self._meta_used.value)].copy(), n)
+        return out + (_lib.KIND_NAMES[int(chosen.value)], costs if kind == "auto" else None)
+
     def plan_cascade(self, wrapper, num_qo_heads: int, num_kv_heads: int, head_dim: int, q_data_type,
                      host_plan: Optional[torch.Tensor] = None):
         """This step's cascade metadata and ``wrapper``'s plan of it in one
@@ -879,6 +912,16 @@ class NativeBeamState:
         the plan is written there and not uploaded -- the caller copies its
         first ``wrapper._info.plan_ints`` words to the workspace's start before
         the next run (a plan beyond it raises MemoryError)."""
+        return self.plan_kind(wrapper, "cascade", num_qo_heads, num_kv_heads, head_dim, q_data_type,
+                              host_plan=host_plan)[:4]
+
+    def plan_kind(self, wrapper, kind: str, num_qo_heads: int, num_kv_heads: int, head_dim: int, q_data_type,
+                  include_self: bool = False, model=None, host_plan: Optional[torch.Tensor] = None):
+        """``plan_cascade`` for any strategy kind (``be_trie_plan_kind``: the
+        levels of ``step_levels(kind, include_self, model)`` and ``wrapper``'s
+        plan of them, causal only for "cascade").  Returns the candidates'
+        query tokens, write pages, write slots and positions, the kind built
+        and, for "auto", the modelled flat / split / tree costs."""
         from . import _lib
         from .attention import _Staging, _num_cus
         if isinstance(q_data_type, str):
@@ -886,28 +929,36 @@ class NativeBeamState:
         staging = None if host_plan is not None else _Staging.get(wrapper._ws.device)
         info = _lib.BeAttnPlanInfo()
         max_page = ctypes.c_int32(-1)
+        chosen = ctypes.c_int32(-1)
+        costs = self._costs_buf = getattr(self, "_costs_buf", None)
+        if costs is None:
+            costs = self._costs_buf = np.full(3, np.nan)
         caps = ctypes.byref(wrapper._caps) if wrapper._caps is not None else None
+        pm = ctypes.byref(model) if model is not None else None
+        code = _lib.KIND_CODES[kind]
         cap = host_plan.numel() if host_plan is not None else staging.buf.numel()
         while True:
             buf = host_plan if host_plan is not None else staging.acquire(cap)
             meta = self._meta_buf
             if self._meta_ptr[0] is not meta:
                 self._meta_ptr = (meta, meta.ctypes.data)
-            rc = self._lib.be_trie_plan(self._h, num_qo_heads, num_kv_heads, head_dim, _lib.dtype_code(q_data_type),
-                                        wrapper._plan_flags(), wrapper._num_cus or _num_cus(wrapper._ws.device), caps,
-                                        self._meta_ptr[1], meta.size, ctypes.byref(self._meta_used), buf.data_ptr(),
-                                        buf.numel(), ctypes.byref(info), ctypes.byref(max_page))
+            rc = self._lib.be_trie_plan_kind(self._h, code, int(include_self), pm, num_qo_heads, num_kv_heads,
+                                             head_dim, _lib.dtype_code(q_data_type), wrapper._plan_flags(),
+                                             wrapper._num_cus or _num_cus(wrapper._ws.device), caps,
+                                             self._meta_ptr[1], meta.size, ctypes.byref(self._meta_used),
+                                             buf.data_ptr(), buf.numel(), ctypes.byref(info), ctypes.byref(max_page),
+                                             ctypes.byref(chosen), costs.ctypes.data)
             if rc == _lib.BE_ERR_CAPACITY:
                 if int(self._meta_used.value) > meta.size:
                     self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
                 elif host_plan is not None or buf.numel() >= (1 << 26):
                     # a full caller buffer, or a plan beyond the fixed layout's
                     # capacities (which no buffer size cures): MemoryError
-                    _lib.check(rc, "cascade plan")
+                    _lib.check(rc, f"{kind} plan")
                 else:
                     cap = 2 * buf.numel()
                 continue
-            _lib.check(rc, "cascade plan")
+            _lib.check(rc, f"{kind} plan")
             break
         wrapper.num_levels = int(self._meta_buf[0])
         wrapper._install_plan(info, buf, staging, int(max_page.value), head_dim, None, q_data_type,
@@ -915,7 +966,8 @@ class NativeBeamState:
         n = int(info.num_queries)                      # one query per candidate
         oc = int(self._meta_buf[1])
         m = self._meta_buf[oc: oc + 4 * n].copy()
-        return m[:n], m[n: 2 * n], m[2 * n: 3 * n], m[3 * n:]
+        return (m[:n], m[n: 2 * n], m[2 * n: 3 * n], m[3 * n:], _lib.KIND_NAMES[int(chosen.value)],
+                costs.copy() if kind == "auto" else None)
 
     # ------------------------------------------------------------ Python view
     def python_state(self) -> BeamState:

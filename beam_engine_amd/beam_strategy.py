@@ -128,6 +128,13 @@ class VanillaBeamSearchStrategy(BeamStrategy):
             num_return = beam_state.beam_size
         return beam_state.get_final_sequences(num_return, self.length_penalty, request_id)
 
+    def finalize_scores(self, candidates: List[BeamCandidate], step: int) -> List[Tuple[BeamCandidate, float]]:
+        """(candidate, score / step^length_penalty) pairs, highest first, the
+        length being the ``step`` the caller passes (beam_strategy.py:539-552;
+        unchanged when the penalty is 0 or step <= 1; ties keep input order)."""
+        scored = [(c, self._apply_length_penalty(c.score, step)) for c in candidates]
+        return sorted(scored, key=lambda x: x[1], reverse=True)
+
 
 class DiverseBeamSearchStrategy(BeamStrategy):
     """Diverse beam search (beam_strategy.py:60-400; Vijayakumar et al. 2018).

@@ -28,8 +28,12 @@
 //    first child appends to the original page.  A child whose token is the
 //    end-of-sequence id (when one is given) finishes its beam instead, with
 //    its whole sequence kept.
+//    A selection whose expansion needs more pages than the pool holds after
+//    the prune fails (BE_ERR_CAPACITY) before the trie or the pool changes.
 //  * be_trie_metadata: the cascade arrays and per-candidate inputs of the
-//    live trie (be_trie_cascade over the node table).
+//    live trie (be_trie_cascade over the node table); be_trie_plan /
+//    be_trie_plan_kind: a strategy's levels (be_trie_levels) and their
+//    attention plan in one call.
 
 #include <cstring>
 #include <new>
@@ -290,7 +294,44 @@ int be_trie_apply(be_beam_trie* t, const int32_t* sel_parent, const int32_t* sel
   }
   // end-of-sequence picks finish their beams (the other children go on)
   std::vector<int> live_cnt((size_t)nc, 0);
-  for (int i = 0; i < nc; ++i) {
+  for (int i = 0; i < nc; ++i)
+    for (int q = cnt[i]; q < cnt[i + 1]; ++q)
+      if (!(eos_token >= 0 && sel_token[kids[q]] == eos_token)) live_cnt[i] += 1;
+  // The pages the expansion takes (a single child on a full page: one; m
+  // children on a full page: m; on a partial page: m - 1 copies) against the
+  // free list after the prune (pages whose last holder the prune releases,
+  // found on a copy of the child counts): a selection the pool cannot hold
+  // fails here, before anything changes.
+  {
+    int64_t need = 0;
+    for (int i = 0; i < nc; ++i) {
+      const int m = live_cnt[i];
+      if (m == 0) continue;
+      const int node = t->cand_node[i];
+      need += m == 1 ? (t->ntok[node] < ps ? 0 : 1) : (t->ntok[node] == ps ? m : m - 1);
+    }
+    int64_t avail = t->pool->count;
+    if (need > avail) {
+      std::vector<int32_t> kc(t->nchild);
+      std::vector<uint8_t> gone(t->alive.size(), 0);
+      for (int i = 0; i < nc && need > avail; ++i) {
+        if (live_cnt[i] > 0) continue;
+        int node = t->cand_node[i];
+        while (node >= 0 && t->alive[node] && !gone[node] && kc[node] == 0) {
+          gone[node] = 1;
+          const int32_t pg = t->page[node];
+          if (pg >= 0 && pg < t->pool->num_pages && t->pool->refs[pg] == 1) ++avail;
+          const int par = t->parent[node];
+          if (par >= 0) kc[par] -= 1;
+          node = par;
+        }
+      }
+    }
+    if (need > avail)
+      return be::fail(BE_ERR_CAPACITY, "No free pages available (the step needs %lld, %lld free after pruning)",
+                      (long long)need, (long long)avail);
+  }
+  for (int i = 0; i < nc; ++i)
     for (int q = cnt[i]; q < cnt[i + 1]; ++q) {
       const int e = kids[q];
       if (eos_token >= 0 && sel_token[e] == eos_token) {
@@ -300,11 +341,8 @@ int be_trie_apply(be_beam_trie* t, const int32_t* sel_parent, const int32_t* sel
         t->fin_tokens.push_back(sel_token[e]);
         t->fin_off.push_back((int32_t)t->fin_tokens.size());
         kids[q] = -1;
-      } else {
-        live_cnt[i] += 1;
       }
     }
-  }
   // prune: leaf upward while childless, candidates in order
   int warnings = 0;
   for (int i = 0; i < nc; ++i) {
@@ -318,6 +356,7 @@ int be_trie_apply(be_beam_trie* t, const int32_t* sel_parent, const int32_t* sel
       node = par;
     }
   }
+  t->version += 1;                 // the state has changed from here on
   // expand, candidates in order
   std::vector<int32_t> nn, nr;
   std::vector<double> nsc;
@@ -436,6 +475,15 @@ int be_trie_metadata(const be_beam_trie* t, int32_t* out, int64_t out_capacity, 
                          out_used);
 }
 
+// One strategy's levels of the live trie, as be_trie_levels lays them out.
+int be_trie_metadata_kind(const be_beam_trie* t, int kind, int include_self, const be_tree_model* model, int32_t* out,
+                          int64_t out_capacity, int64_t* out_used, int32_t* chosen, double* option_costs) {
+  BE_REQUIRE(t, "null trie");
+  return be_trie_levels(t->parent.data(), t->page.data(), t->ntok.data(), t->last.data(), t->alive.data(),
+                        (int)t->parent.size(), t->cand_node.data(), (int)t->cand_node.size(), t->page_size, kind,
+                        include_self, model, out, out_capacity, out_used, chosen, option_costs);
+}
+
 // The step's metadata (into meta, as be_trie_metadata) and the cascade
 // attention plan of its levels (be_attn_plan into host_plan): the per-step
 // host work of a cascade decode step in one call.  The last level's groups
@@ -445,8 +493,24 @@ int be_trie_metadata(const be_beam_trie* t, int32_t* out, int64_t out_capacity, 
 int be_trie_plan(const be_beam_trie* t, int num_qo_heads, int num_kv_heads, int head_dim, int dtype, int flags,
                  int num_cus, const be_plan_caps* caps, int32_t* meta, int64_t meta_capacity, int64_t* meta_used,
                  int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info, int32_t* max_page) {
+  return be_trie_plan_kind(t, BE_KIND_CASCADE, 0, nullptr, num_qo_heads, num_kv_heads, head_dim, dtype, flags,
+                           num_cus, caps, meta, meta_capacity, meta_used, host_plan, host_plan_capacity, info,
+                           max_page, nullptr, nullptr);
+}
+
+// be_trie_plan for any strategy kind: the levels of be_trie_levels, then
+// the attention plan of those levels.
+int be_trie_plan_kind(const be_beam_trie* t, int kind, int include_self, const be_tree_model* model,
+                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype, int flags, int num_cus,
+                      const be_plan_caps* caps, int32_t* meta, int64_t meta_capacity, int64_t* meta_used,
+                      int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info, int32_t* max_page,
+                      int32_t* chosen, double* option_costs) {
   BE_REQUIRE(t && meta_used && info && max_page, "null argument");
-  const int rc = be_trie_metadata(t, meta, meta_capacity, meta_used);
+  int32_t used_kind = kind;
+  const int rc = be_trie_levels(t->parent.data(), t->page.data(), t->ntok.data(), t->last.data(), t->alive.data(),
+                                (int)t->parent.size(), t->cand_node.data(), (int)t->cand_node.size(), t->page_size,
+                                kind, include_self, model, meta, meta_capacity, meta_used, &used_kind, option_costs);
+  if (chosen) *chosen = used_kind;
   if (rc != BE_OK) return rc;
   const int nl = meta[0];
   const int nc = (int)t->cand_node.size();
@@ -460,7 +524,7 @@ int be_trie_plan(const be_beam_trie* t, int num_qo_heads, int num_kv_heads, int 
     const int32_t* kvp = meta + rec[2];
     const int32_t* kvi = meta + rec[3];
     for (int32_t i = 0; i < kvp[ng]; ++i) mp = kvi[i] > mp ? kvi[i] : mp;
-    if (l == nl - 1)
+    if (l == nl - 1 && used_kind == BE_KIND_CASCADE)
       for (int gi = 0; gi < ng; ++gi)
         if (meta[rec[1] + gi + 1] - meta[rec[1] + gi] > 1) mask = true;
   }

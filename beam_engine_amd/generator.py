@@ -13,16 +13,24 @@ requests decoded together in one forward per step:
   selection per request (log_softmax + top-2B + global top-B), trie update
   with the step's fork copies in one launch.
 
-``kernel_type``: "cascade" (per-level groups of the reference's
-get_cascade_input), "flat" (each candidate's whole path, the baseline),
-"tree" (the path attention as shared passes over trie segments, each edge
-absorbed or split by the MI355X cost model, as FastTree's preparation decides
-them, attention/fasttree/preparation.py:60-105) or "auto" (per step, the
-cheaper of flat, fully split and tree under that model).  "flat", "tree" and
-"auto" give every candidate its path tokens exactly once; "cascade" keeps the
-reference's repetition of a shallow candidate's leaf group on deeper levels.
-``include_self`` False follows the reference's cascade convention (a query
-does not attend to the K/V it appends in the same step, beam_state.py:347-354).
+``kernel_type``: the reference's two (beam.py:20, 191-206) and three more --
+"cascade" (per-level groups of the reference's get_cascade_input),
+"fasttree" (the reference's FastTree strategy: each candidate attends its
+whole root-to-leaf path, its newest token included as FastTree's
+req_to_token includes it, beam_state.py:512-564, decomposed into shared passes
+over trie segments with each edge absorbed or split by FastTree's own cost
+model, attention/fasttree/preparation.py:34-88), "flat" (each candidate's whole
+path, the baseline), "split" (one pass per trie segment, merged), "tree" (the fasttree decomposition with each edge decided
+by this build's fitted MI355X costs, or FastTree's with
+``picker_costs="fasttree"``) or "auto" (per step, the cheapest of flat, fully
+split and tree under the fitted costs: the per-step picker).  Every kind's
+metadata and attention plan come from the native trie in one call
+(``be_trie_plan_kind``) and every kind runs as the whole-step graph.  "flat",
+"tree", "auto" and "fasttree" give every candidate its path tokens exactly
+once; "cascade" keeps the reference's repetition of a shallow candidate's leaf
+group on deeper levels.  ``include_self`` False follows the reference's
+cascade convention (a query does not attend to the K/V it appends in the same
+step, beam_state.py:347-354); "fasttree" always includes it.
 ``eos_token_id`` (off by default, as in the reference, which never finishes a
 beam): a pick of that token finishes its beam (``state.finished_candidates``)
 and the request continues with its other beams; steps whose candidate count
@@ -57,8 +65,12 @@ class BatchedBeamSearch:
                  temperature: float = 1.0, workspace_bytes: int = 256 << 20, include_self: bool = False,
                  graphs: bool = False, eos_token_id: Optional[int] = None, temperature_mode: str = "reciprocal",
                  picker_costs: str = "mi355x", step_graph: bool = True):
-        if kernel_type not in ("cascade", "flat", "tree", "auto"):
-            raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'flat', 'tree' or 'auto'.")
+        if kernel_type not in ("cascade", "fasttree", "flat", "split", "tree", "auto"):
+            raise ValueError(f"Unknown kernel_type: {kernel_type}. Must be 'cascade', 'fasttree', 'flat', 'split', "
+                             "'tree' or 'auto'.")
+        if kernel_type == "cascade" and include_self:
+            raise NotImplementedError("include_self with the cascade levels (their last level excludes the newest "
+                                      "token, beam_state.py:343-356)")
         self.model = model
         self.pt = page_table
         self.beam_size = beam_size
@@ -66,14 +78,13 @@ class BatchedBeamSearch:
         self.kernel_type = kernel_type
         self.temperature = temperature
         self.temperature_mode = temperature_mode   # arithmetic of logits / T: see selection.beam_topk
-        self.include_self = include_self
+        # the reference's FastTree attends the whole path, the query's own new token included
+        self.include_self = include_self or kernel_type == "fasttree"
         self.eos_token_id = eos_token_id    # a pick of this token finishes its beam (off: None)
         self.device = page_table.device
-        # cascade decoding keeps the trie and its pages in native code (one call
-        # per selection, one for the metadata); the other kinds read the
-        # Python trie's passes every step and keep the Python state
-        self.state = NativeBeamState(beam_size, page_table) if kernel_type == "cascade" else \
-            BeamState(beam_size, page_table, fast_metadata=True)
+        # the trie and its pages live in native code: one call per selection,
+        # one for the step's metadata and attention plan (any strategy kind)
+        self.state = NativeBeamState(beam_size, page_table)
         # The wrappers' workspace (an attention plan at its start) follows a
         # reserved region whose last bytes hold the graphed step's inputs and
         # staged fork-copy list: header and plan are contiguous, so a graphed
@@ -89,7 +100,10 @@ class BatchedBeamSearch:
         self.flat = BatchDecodeWithPagedKVCacheWrapper(self.ws)
         self.last_attn = None
         self.picker = None
-        self.picker_costs = picker_costs    # "mi355x" fitted costs or "fasttree" (the reference's edge model)
+        # "mi355x" fitted costs or "fasttree" (the reference's edge model) for
+        # the tree's edges; the "fasttree" kind always takes FastTree's model
+        self.picker_costs = "fasttree" if kernel_type == "fasttree" else picker_costs
+        self._model = None                  # the picker's costs as the native planner's be_tree_model
         self.step_log: List[dict] = []
         self._staging = torch.empty(4 * 4096, dtype=torch.int64, pin_memory=True)
         self.attn_timer = None          # optional callable(layer, fn) used by benchmarks
@@ -99,6 +113,7 @@ class BatchedBeamSearch:
         # runs the per-layer graphs with eager attention)
         self.step_graph = step_graph
         self.step_graphed = False       # the last step ran as one graph
+        self.graphed_steps = 0          # decode steps that ran as one graph
         self._gd = None
         self._fixed = None              # the fixed-layout cascade wrapper of the step graph
         self._fixed_key = None          # its launch shape (plan fields the captured launches read)
@@ -109,6 +124,8 @@ class BatchedBeamSearch:
     def prefill(self, prompts: Sequence[Sequence[int]]) -> torch.Tensor:
         if len({len(p) for p in prompts}) != 1:
             raise ValueError("batched prefill needs prompts of equal length")
+        for p in prompts:
+            self._check_tokens(p)
         page_ids = []
         for r, p in enumerate(prompts):
             nodes = self.state.add_root_sequence(list(p), request_id=r)
@@ -126,6 +143,15 @@ class BatchedBeamSearch:
         self.state.add_filtered_results(results)
         return logits
 
+    def _check_tokens(self, ids) -> None:
+        """Token ids outside the vocabulary raise here: the embedding lookup
+        on the device would read out of bounds."""
+        a = np.asarray(ids)
+        vocab = self.model.cfg.vocab_size
+        if a.size and (int(a.min()) < 0 or int(a.max()) >= vocab):
+            bad = a[(a < 0) | (a >= vocab)]
+            raise ValueError(f"token id {int(bad[0])} is outside the vocabulary [0, {vocab})")
+
     # ---------------------------------------------------------------- decode
     def _get_picker(self):
         if self.picker is None:
@@ -135,24 +161,25 @@ class BatchedBeamSearch:
             self.picker = StrategyPicker(cfg.num_attention_heads, cfg.num_key_value_heads, self.pt.page_size, costs)
         return self.picker
 
-    def _plan(self, kind: str, levels=None):
+    def _native_kind(self):
+        """(kind code name for be_trie_plan_kind, its be_tree_model or None)."""
+        kind = self.kernel_type
+        if kind == "cascade":
+            return "cascade", None
+        if kind in ("flat", "split"):
+            return kind, None
+        if self._model is None:
+            self._model = self._get_picker().tree_model()
+        return ("tree" if kind == "fasttree" else kind), self._model
+
+    def _plan(self, levels, causal: bool):
+        """An eager plan of ``levels`` on a workspace wrapper."""
         m = self.model
         cfg = m.cfg
-        st = self.state
-        if kind != "flat" or levels is not None:
-            if levels is None:
-                levels = st._cascade_lists()
-            if self.include_self:
-                raise NotImplementedError("include_self with cascade or tree levels")
-            w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
-            w.plan([l[0] for l in levels], [l[1] for l in levels], [l[2] for l in levels], [l[3] for l in levels],
-                   cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pt.page_size,
-                   causal=kind == "cascade", q_data_type=m.dtype)
-        else:
-            kvp, kvi, lpl = st.flat_lists(self.include_self)
-            w = self.flat
-            w.plan(kvp, kvi, lpl, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
-                   self.pt.page_size, q_data_type=m.dtype)
+        w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
+        w.plan([l[0] for l in levels], [l[1] for l in levels], [l[2] for l in levels], [l[3] for l in levels],
+               cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, self.pt.page_size,
+               causal=causal, q_data_type=m.dtype)
         self.last_attn = w
         return w
 
@@ -166,7 +193,7 @@ class BatchedBeamSearch:
     def _launch_key(cls, info):
         return tuple(getattr(info, f) for f in cls._LAUNCH_FIELDS)
 
-    def _fixed_plan(self, levels, n: int):
+    def _fixed_plan(self, levels, n: int, causal: bool = True):
         """This step's cascade plan in the step graph's fixed layout, or None
         when the step graph cannot run it (the per-layer path runs instead).
         The first call sizes the layout from this step's plan with room to
@@ -180,7 +207,7 @@ class BatchedBeamSearch:
         if w is not None:
             w.num_levels = len(levels)
             try:
-                w.plan(*args, causal=True, q_data_type=m.dtype)
+                w.plan(*args, causal=causal, q_data_type=m.dtype)
             except MemoryError:
                 w = None                            # outgrew the layout: re-size below
             else:
@@ -189,7 +216,7 @@ class BatchedBeamSearch:
                 return None
         # size the layout: this step's compact plan, doubled, with margins
         probe = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
-        probe.plan(*args, causal=True, q_data_type=m.dtype)
+        probe.plan(*args, causal=causal, q_data_type=m.dtype)
         pi = probe._info
         if pi.kernel != 2 or cfg.head_dim != 128:
             self.step_graph = False                 # the fixed layout serves the streaming kernel only
@@ -205,7 +232,7 @@ class BatchedBeamSearch:
             caps = {k: max(v, old[k]) for k, v in caps.items()}
         w = MultiLevelCascadeAttentionWrapper(len(levels), self.ws)
         w.use_fixed_layout(**caps)
-        if isinstance(self.state, NativeBeamState) and not self.pt.stage_copies_enabled:
+        if not self.pt.stage_copies_enabled:
             # from now on each selection's fork copies go to the staged list that
             # the step graph's first part performs (in the upload header when
             # there is one)
@@ -214,7 +241,7 @@ class BatchedBeamSearch:
             else:
                 self.pt.enable_staged_copies(2 * n)
         try:
-            w.plan(*args, causal=True, q_data_type=m.dtype)
+            w.plan(*args, causal=causal, q_data_type=m.dtype)
         except (MemoryError, ValueError):
             self.step_graph = False
             return None
@@ -231,21 +258,22 @@ class BatchedBeamSearch:
         n = st.num_candidates()
         if n == 0:                  # every beam finished
             return
-        kind = self.kernel_type
-        levels = None
+        nkind, model = self._native_kind()
+        causal = nkind == "cascade"
+        inc = self.include_self
+        cfg = self.model.cfg
         w = None
-        graphed = kind == "cascade" and self.graphs and self.step_graph and hasattr(self.model, "decode") and \
-            self._graph_ready(n)
+        built, costs = nkind, None
+        graphed = self.graphs and self.step_graph and hasattr(self.model, "decode") and self._graph_ready(n)
         upload = False                  # one copy uploads the header and the plan
-        if graphed and self._fixed is not None and isinstance(st, NativeBeamState):
+        if graphed and self._fixed is not None:
             # metadata and the fixed-layout plan in one native call, the plan
             # written straight into the upload block's pinned twin
-            cfg = self.model.cfg
             host_plan = self._host_plan
             try:
-                qids, wp, wpos, pos = st.plan_cascade(self._fixed, cfg.num_attention_heads,
-                                                      cfg.num_key_value_heads, cfg.head_dim, self.model.dtype,
-                                                      host_plan=host_plan)
+                qids, wp, wpos, pos, built, costs = st.plan_kind(
+                    self._fixed, nkind, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                    self.model.dtype, include_self=inc, model=model, host_plan=host_plan)
             except MemoryError:
                 pass                                # beyond the layout: _fixed_plan re-sizes it
             else:
@@ -253,26 +281,15 @@ class BatchedBeamSearch:
                     w = self.last_attn = self._fixed
                     upload = host_plan is not None
         if w is None:
-            if kind == "cascade":
-                # the cascade arrays and the candidates' inputs from the native builder
-                levels, qids, wp, wpos, pos = st.step_metadata()
-            elif kind == "tree":
-                p = self._get_picker()
-                levels = st.tree_lists((p.edges or p.model).absorb)
-            elif kind == "auto":
-                plan = self._get_picker().choose(st)
-                kind, levels = plan.kind, plan.levels
+            levels, qids, wp, wpos, pos, built, costs = st.step_levels(nkind, inc, model)
             if graphed:
-                w = self.last_attn = self._fixed_plan(levels, n)
+                w = self.last_attn = self._fixed_plan(levels, n, causal)
         self.step_graphed = w is not None
+        self.graphed_steps += int(self.step_graphed)
         if not self.step_graphed:
             self.pt.run_staged_copies()     # an eager step performs the staged fork copies first
-        if w is None:
-            w = self._plan(kind, levels)
-        if self.kernel_type != "cascade":
-            qids = st.query_token_ids()
-            wp, wpos = st.write_locations()
-            pos = st.position_ids(reuse_annotation=True)     # _plan's metadata pass just ran
+            w = self._plan(levels, causal)
+        self._check_tokens(qids)
         graph_run = self.step_graphed or (self.graphs and hasattr(self.model, "decode") and self._graph_ready(n))
         if graph_run:
             self._gd.stage_inputs(qids, pos, wp, wpos, upload=not upload)
@@ -308,17 +325,22 @@ class BatchedBeamSearch:
         else:
             logits = self.model.decode(tok, psn, wpg, wps, self.pt, attn)
         self._select(logits)
-        self.step_log.append({"n": n, "kind": kind})
+        entry = {"n": n, "kind": built if self.kernel_type == "auto" else self.kernel_type}
+        if costs is not None:
+            entry["costs"] = {"flat": float(costs[0]), "split": float(costs[1]), "tree": float(costs[2])}
+        self.step_log.append(entry)
 
     def prepare_graphs(self) -> None:
-        """Capture the segment graphs (and, for cascade, the whole-step graph)
-        now for the current candidate count (the first decode step would
-        otherwise capture them)."""
+        """Capture the segment graphs and the whole-step graph now for the
+        current candidate count (the first decode step would otherwise
+        capture them)."""
         n = self.state.num_candidates()
         if self.graphs and hasattr(self.model, "decode") and n:
             self._graph_ready(n)
-            if self.kernel_type == "cascade" and self.step_graph and self._fixed is None:
-                self._fixed_plan(self.state.step_metadata()[0], n)    # capture the whole-step graph too
+            if self.step_graph and self._fixed is None:
+                nkind, model = self._native_kind()
+                levels = self.state.step_levels(nkind, self.include_self, model)[0]
+                self._fixed_plan(levels, n, nkind == "cascade")    # capture the whole-step graph too
 
     def _graph_ready(self, n: int) -> bool:
         """Capture the segment graphs once the candidate count is known (it
@@ -327,7 +349,7 @@ class BatchedBeamSearch:
         if self._gd is None:
             header = None
             hb = GraphedDecoder.header_bytes(n)
-            if self.device.type == "cuda" and self.kernel_type == "cascade" and self.step_graph and hb <= self._hdr:
+            if self.device.type == "cuda" and self.step_graph and hb <= self._hdr:
                 self._hb = hb
                 self._hblock = torch.zeros(hb + _STEP_PLAN_BYTES, dtype=torch.uint8, pin_memory=True)
                 self._host_plan = self._hblock[hb:].view(torch.int32)
@@ -341,8 +363,7 @@ class BatchedBeamSearch:
         # the step's KV appends (and the previous step's fork copies) report
         # out-of-pool entries at the selection's synchronisation
         self.pt.stage_errors()
-        if isinstance(st, NativeBeamState) and type(self.strategy) is VanillaBeamSearchStrategy and \
-                "select_batched" not in vars(self.strategy):
+        if type(self.strategy) is VanillaBeamSearchStrategy and "select_batched" not in vars(self.strategy):
             # the selection arrays go straight to the native trie (no per-child objects)
             req, score = st.candidate_arrays()
             cut = np.flatnonzero(np.diff(req)) + 1
@@ -373,7 +394,7 @@ class BatchedBeamSearch:
         self.prefill(prompts)
         for _ in range(steps):
             st = self.state
-            if isinstance(st, NativeBeamState) and type(self.strategy) is VanillaBeamSearchStrategy:
+            if type(self.strategy) is VanillaBeamSearchStrategy:
                 # VanillaBeamSearchStrategy.should_stop without building the
                 # Python view: no live beam, or early stopping with beam_size
                 # finished ones (live beams are never finished)

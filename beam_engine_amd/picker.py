@@ -202,8 +202,24 @@ class StrategyPicker:
         self.last: Optional[Plan] = None
         self.history: List[str] = []
 
-    def _options(self, state: BeamState):
-        segs, paths = state.segment_tree()
+    def tree_model(self):
+        """These costs and edge decisions as the native planner's model
+        (``be_tree_model``: ``be_trie_levels`` / ``be_trie_plan_kind`` decide
+        the same edges and price the same options)."""
+        from . import _lib
+        c = self.model.c
+        m = _lib.BeTreeModel()
+        for i, v in enumerate(c.tile_nt):
+            m.tile_nt[i] = v
+        m.seg, m.slot, m.tail, m.fixed = c.seg, c.slot, c.tail, c.fixed
+        ft = self.edges if self.edges is not None else FastTreeCostModel(self.model.g * self.model.hkv, self.model.hkv)
+        m.alpha, m.beta, m.gamma = ft.alpha, ft.beta, ft.gamma
+        m.num_qo_heads, m.num_kv_heads = self.model.g * self.model.hkv, self.model.hkv
+        m.edge_model = _lib.BE_EDGES_FASTTREE if self.edges is not None else _lib.BE_EDGES_FITTED
+        return m
+
+    def _options(self, state: BeamState, include_self: bool = False):
+        segs, paths = state.segment_tree(include_self)
         m = self.model
         out = {}
         for kind in self.candidates:
@@ -222,11 +238,11 @@ class StrategyPicker:
             out[kind] = (cost, absorbed)
         return segs, paths, out
 
-    def costs(self, state: BeamState) -> Dict[str, float]:
-        return {k: v[0] for k, v in self._options(state)[2].items()}
+    def costs(self, state: BeamState, include_self: bool = False) -> Dict[str, float]:
+        return {k: v[0] for k, v in self._options(state, include_self)[2].items()}
 
-    def choose(self, state: BeamState) -> Plan:
-        segs, paths, opts = self._options(state)
+    def choose(self, state: BeamState, include_self: bool = False) -> Plan:
+        segs, paths, opts = self._options(state, include_self)
         kind = min(opts, key=lambda k: opts[k][0])
         plan = Plan(kind, state.tree_levels(segs, paths, opts[kind][1]), opts[kind][0],
                     {k: v[0] for k, v in opts.items()})

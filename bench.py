@@ -43,7 +43,7 @@ def parse():
     ap.add_argument("--workload", default="e2e",
                     choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-prefill",
                              "topk", "topk-c1"])
-    ap.add_argument("--strategy", default="cascade", choices=["cascade", "flat", "tree", "auto"],
+    ap.add_argument("--strategy", default="cascade", choices=["cascade", "fasttree", "flat", "split", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
     ap.add_argument("--row-blocks", default="auto", choices=["auto", "on", "off"],

@@ -347,8 +347,9 @@ def run_e2e_bench(args):
                "generation_tokens_per_s": n * DECODE_STEPS / wall, "generation_s": wall,
                "att": timer.summary(), "kernels": sorted(timer.kernels),
                "final_sequences": sum(len(v) for v in finals.values()),
-               "picker": ({k: gen.picker.history.count(k) for k in sorted(set(gen.picker.history))}
-                          if gen.picker is not None else None)}
+               "picker": ({k: sum(1 for e in gen.step_log if e["kind"] == k)
+                           for k in sorted({e["kind"] for e in gen.step_log})} if strategy == "auto" else None),
+               "graphed_steps": gen.graphed_steps}
         log(f"{strategy}: {len(per)} sampled steps -> {res['tokens_per_s']:.1f} tokens/s, whole decode "
             f"{res['generation_tokens_per_s']:.1f} tokens/s; attention {res['att']['mean_pair_us']:.1f} us per "
             f"launch, {res['att']['gbs']:.0f} GB/s")

@@ -17,10 +17,20 @@
  *                     (src/beam_engine/page_table.py:96-106), batched over forks and layers
  *   be_page_copy_counted  the same with the copy count read on the device (graph capture)
  *   be_attn_plan      MultiLevelCascadeAttentionWrapper.plan
- *                     (src/beam_engine/models/modeling_llama.py:732-755) and the FastTree
- *                     host metadata pass (src/beam_engine/attention/fasttree/preparation.py:11-225)
- *   be_attn_run       MultiLevelCascadeAttentionWrapper.run (models/modeling_llama.py:362) and
- *                     fasttree_decode (src/beam_engine/attention/fasttree/kernel.py:288-348)
+ *                     (src/beam_engine/models/modeling_llama.py:732-755); over the levels of
+ *                     be_trie_levels it is also the vnode layout step of FastTree's
+ *                     prepare_fasttree_metadata_for_paged_cache
+ *                     (src/beam_engine/attention/fasttree/preparation.py:107-225)
+ *   be_attn_run       MultiLevelCascadeAttentionWrapper.run (models/modeling_llama.py:362); on a
+ *                     plan of FastTree levels, fasttree_decode's two stages
+ *                     (src/beam_engine/attention/fasttree/kernel.py:288-348), reading the paged
+ *                     cache in place of the K / V copies of models/modeling_llama.py:369-425
+ *   be_trie_levels    FastTree's per-edge SplitQ / SplitK decision over the trie
+ *                     (src/beam_engine/attention/fasttree/preparation.py:34-105) with its inputs
+ *                     (BeamState.get_fasttree_input, src/beam_engine/beam_state.py:414-633), the
+ *                     flat / split / per-step-picked decompositions, and the cascade levels
+ *   be_trie_plan_kind the per-step metadata + plan of either reference kernel_type
+ *                     (src/beam_engine/beam.py:168-206; models/modeling_llama.py:732-773)
  *   be_merge_states   the log-sum-exp merge inside the cascade wrapper and FastTree stage 2
  *                     (src/beam_engine/attention/fasttree/kernel.py:188-285)
  *   be_beam_topk      log_softmax + per-row topk (src/beam_engine/beam.py:269-276, prefill
@@ -274,6 +284,47 @@ int be_trie_cascade(const int32_t* parent, const int32_t* page, const int32_t* n
                     const uint8_t* alive, int num_nodes, const int32_t* leaves, int num_cands, int32_t* out,
                     int64_t out_capacity, int64_t* out_used);
 
+/* Strategy kinds of be_trie_levels / be_trie_plan_kind. */
+#define BE_KIND_CASCADE 0  /* the reference's cascade levels (be_trie_cascade)                  */
+#define BE_KIND_FLAT 1     /* one pass per candidate over its whole path                        */
+#define BE_KIND_SPLIT 2    /* one pass per trie segment, merged                                  */
+#define BE_KIND_TREE 3     /* each edge absorbed or split by the cost model's edge decision      */
+#define BE_KIND_AUTO 4     /* the cheapest of flat, split and tree under the fitted costs        */
+#define BE_EDGES_FITTED 0  /* edge decisions by this build's fitted kernel costs                 */
+#define BE_EDGES_FASTTREE 1 /* edge decisions by FastTree's padded-tile model (preparation.py:34-57) */
+
+/* Kernel costs (microseconds per layer, the whole GPU) and the edge model of
+ * the tree decompositions: tile_nt[i] one 64-token tile of one KV head with
+ * i + 1 16-row MFMA tiles filled, seg a segment start, slot a partial slot
+ * and its merge, tail a 16-token tail chunk, fixed a step's launches; alpha,
+ * beta, gamma FastTree's Cmm constants (metadata.py:12-17). */
+typedef struct be_tree_model {
+  double tile_nt[4];
+  double seg, slot, tail, fixed;
+  double alpha, beta, gamma;
+  int32_t num_qo_heads, num_kv_heads;
+  int32_t edge_model;
+  int32_t reserved;
+} be_tree_model;
+
+/* be_trie_levels (host only): the levels of one strategy for the live trie,
+ * laid out as be_trie_cascade lays them out (with the same candidate block).
+ * BE_KIND_CASCADE is be_trie_cascade (include_self must be 0).  The other
+ * kinds attend every candidate to its root-to-leaf path exactly once --
+ * with its newest token when include_self is set (FastTree's req_to_token
+ * covers the whole path, beam_state.py:512-564), without it otherwise (the
+ * cascade convention) -- as passes over the trie's segments: flat absorbs
+ * every edge, split none, tree decides each edge top down with the model
+ * (FastTree's rule, attention/fasttree/preparation.py:60-105), auto builds the
+ * cheapest of the three under the fitted costs.  model is needed for
+ * BE_KIND_TREE and BE_KIND_AUTO.  *chosen receives the kind built;
+ * option_costs (3 doubles, optional) the modelled flat / split / tree costs
+ * under BE_KIND_AUTO. */
+int be_trie_levels(const int32_t* parent, const int32_t* page, const int32_t* ntok, const int32_t* last_tok,
+                   const uint8_t* alive, int num_nodes, const int32_t* leaves, int num_cands, int page_size, int kind,
+                   int include_self, const be_tree_model* model, int32_t* out, int64_t out_capacity,
+                   int64_t* out_used, int32_t* chosen, double* option_costs);
+
 /* ------------------------------------------------------------------ page pool and beam trie (host only)
  * be_page_pool replaces the reference PageTable's allocator
  * (src/beam_engine/page_table.py:77-124): a FIFO free list (oldest free page
@@ -327,6 +378,10 @@ int be_trie_candidates(const be_beam_trie* trie, int32_t* node, int32_t* request
 int be_trie_export(const be_beam_trie* trie, int32_t* parent, int32_t* page, int32_t* ntok, uint8_t* alive,
                    int32_t* tokens, int32_t* fin_req, double* fin_score, int32_t* fin_off, int32_t* fin_tokens);
 int be_trie_metadata(const be_beam_trie* trie, int32_t* out, int64_t out_capacity, int64_t* out_used);
+/* be_trie_metadata_kind: be_trie_levels over the trie (any strategy kind). */
+int be_trie_metadata_kind(const be_beam_trie* trie, int kind, int include_self, const be_tree_model* model,
+                          int32_t* out, int64_t out_capacity, int64_t* out_used, int32_t* chosen,
+                          double* option_costs);
 /* be_trie_plan: be_trie_metadata into meta, then be_attn_plan of its levels
  * (the cascade wrapper's plan of the step: causal mask on the last level when
  * a group there holds more than one query; num_pages from the largest page
@@ -335,6 +390,18 @@ int be_trie_metadata(const be_beam_trie* trie, int32_t* out, int64_t out_capacit
 int be_trie_plan(const be_beam_trie* trie, int num_qo_heads, int num_kv_heads, int head_dim, int dtype, int flags,
                  int num_cus, const be_plan_caps* caps, int32_t* meta, int64_t meta_capacity, int64_t* meta_used,
                  int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info, int32_t* max_page);
+/* be_trie_plan_kind: be_trie_plan for any strategy kind -- be_trie_levels
+ * over the trie into meta, then be_attn_plan of its levels (the causal mask
+ * only for BE_KIND_CASCADE, as be_trie_plan decides it; the other kinds'
+ * multi-query groups are shared segments, not causal blocks).  Replaces the
+ * reference's per-step dispatch on kernel_type (beam.py:168-206) with
+ * get_cascade_input or get_fasttree_input + prepare_fasttree_metadata_for_paged_cache
+ * (attention/fasttree/preparation.py:11-225) and the wrapper's plan. */
+int be_trie_plan_kind(const be_beam_trie* trie, int kind, int include_self, const be_tree_model* model,
+                      int num_qo_heads, int num_kv_heads, int head_dim, int dtype, int flags, int num_cus,
+                      const be_plan_caps* caps, int32_t* meta, int64_t meta_capacity, int64_t* meta_used,
+                      int32_t* host_plan, int64_t host_plan_capacity, be_attn_plan_info* info, int32_t* max_page,
+                      int32_t* chosen, double* option_costs);
 
 /* be_attn_run: o[i, h] = softmax(sm_scale * q[i, h] . K^T) V over query i's
  * groups on every level, merged by log-sum-exp; query head h reads KV head

@@ -300,3 +300,18 @@ def test_final_sequences_with_finished_hand_case():
         assert st.get_final_sequences(4, pen) == o.get_final_sequences(4, pen)
     assert [s for s, _ in st.get_final_sequences(4, 1.0)] == [[1, 2, 3, 4, 7], [1, 2, 3, 4, 5, 6], [1, 2, 3, 4, 8],
                                                              [1, 2, 3, 4, 9, 0]]
+
+
+def test_finalize_scores_hand_case():
+    """VanillaBeamSearchStrategy.finalize_scores (beam_strategy.py:539-552):
+    score / step^penalty, highest first, input order kept on ties; penalty 0
+    or step <= 1 leaves the scores alone."""
+    from beam_engine_amd.beam_state import BeamCandidate
+    from beam_engine_amd.beam_strategy import VanillaBeamSearchStrategy
+    a, b, c = BeamCandidate(None, -4.0), BeamCandidate(None, -2.0), BeamCandidate(None, -4.0)
+    got = VanillaBeamSearchStrategy(length_penalty=1.0).finalize_scores([a, b, c], 4)
+    assert [(x is y, s) for (x, s), y in zip(got, [b, a, c])] == [(True, -0.5), (True, -1.0), (True, -1.0)]
+    got = VanillaBeamSearchStrategy(length_penalty=2.0).finalize_scores([a, b], 2)
+    assert [s for _, s in got] == [-0.5, -1.0]
+    assert [s for _, s in VanillaBeamSearchStrategy(length_penalty=0.0).finalize_scores([a, b], 9)] == [-2.0, -4.0]
+    assert [s for _, s in VanillaBeamSearchStrategy().finalize_scores([a, b], 1)] == [-2.0, -4.0]

@@ -623,3 +623,31 @@ def test_rows_plan_places_shared_blocks_on_one_xcd_lane():
         lanes.setdefault(key, set()).add(wg % 8)
         assert int(t[1]) == 4 and int(t[3]) == 5     # four queries: the prefix pass and four suffix passes
     assert len(lanes) == 64 and all(len(v) == 1 for v in lanes.values())
+
+
+def test_generator_rejects_out_of_vocabulary_token_ids():
+    """Token ids outside the vocabulary raise ValueError on the host before
+    anything reaches the device embedding: prompts before the trie or the
+    pool change, and every step's staged ids (``_check_tokens``)."""
+    import types
+
+    import numpy as np
+    import torch
+    from beam_engine_amd import PageTable
+    from beam_engine_amd.beam_state import NativeBeamState
+    from beam_engine_amd.generator import BatchedBeamSearch
+    from beam_engine_amd.llama import LlamaConfig
+
+    cfg = LlamaConfig(num_hidden_layers=1, hidden_size=64, num_attention_heads=2, num_key_value_heads=1,
+                      head_dim=32, intermediate_size=64, vocab_size=100, max_position_embeddings=64)
+    pt = PageTable(1, page_size=4, max_num_pages=16, head_num=1, head_dim=32, device="cpu",
+                   store_dtype=torch.float32)
+    gen = types.SimpleNamespace(model=types.SimpleNamespace(cfg=cfg), state=NativeBeamState(2, pt))
+    gen._check_tokens = lambda ids: BatchedBeamSearch._check_tokens(gen, ids)
+    for bad in ([[1, 2, 100]], [[-1, 2, 3]], [[1, 2, 3], [4, 5, 1000]]):
+        with pytest.raises(ValueError, match="outside the vocabulary"):
+            BatchedBeamSearch.prefill(gen, bad)
+    assert gen.state.num_candidates() == 0 and pt.num_free_pages() == 16
+    gen._check_tokens(np.array([0, 99]))
+    with pytest.raises(ValueError, match="token id 100"):
+        gen._check_tokens(np.array([5, 100, 7]))

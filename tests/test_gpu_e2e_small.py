@@ -21,7 +21,7 @@ def say(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("kind", ["cascade", "flat", "tree", "auto"])
+@pytest.mark.parametrize("kind", ["cascade", "fasttree", "flat", "split", "tree", "auto"])
 def test_tiny_llama_beam_search_matches_oracle(kind):
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
@@ -58,7 +58,15 @@ def test_tiny_llama_beam_search_matches_oracle(kind):
             ref, _ = oa.cascade_attention(q, kv, [l[0] for l in lv], [l[1] for l in lv], [l[2] for l in lv],
                                           [l[3] for l in lv], 4, 128 ** -0.5)
         else:
-            kvp, kvi, lpl = gen.state.flat_lists()
+            # every other kind attends each candidate's whole path once (the
+            # oracle replay's pages; "fasttree" with the newest token, as the
+            # reference's req_to_token covers it)
+            inc = kind == "fasttree"
+            kvp, kvi, lpl = [0], [], []
+            for ci, c in enumerate(o.candidates):
+                kvi.extend(o.path_pages(ci))
+                kvp.append(len(kvi))
+                lpl.append(len(c.node.tokens) - (0 if inc else 1))
             ref, _ = oa.paged_attention(q, kv, kvp, kvi, lpl, 4, 128 ** -0.5)
         np.testing.assert_allclose(out.float().cpu().numpy(), ref, rtol=2e-2, atol=1e-2)
         checks["attn"] += 1
@@ -112,6 +120,8 @@ def test_tiny_llama_beam_search_matches_oracle(kind):
         gen.step()
     assert checks["attn"] == 10 * cfg.num_hidden_layers
     assert o_alloc.copies, "the run should have forked partial pages"
+    if kind == "auto":
+        say(f"auto picks: {[e['kind'] for e in gen.step_log]}")
 
 
 def test_graph_replays_match_eager_steps():
@@ -212,16 +222,18 @@ def test_eos_finishes_beams_and_decoding_continues():
     assert all(eos not in gen.state.sequence(c)[18:] for c in gen.state.candidates)
 
 
-def test_graphed_decoder_inputs_start_valid_on_reused_memory():
+@pytest.mark.parametrize("kind", ["cascade", "fasttree", "flat", "auto"])
+def test_graphed_decoder_inputs_start_valid_on_reused_memory(kind):
     """The graphed decoder's input buffers are carved from the generator's
     workspace (torch.empty).  Memory the caching allocator hands back holds
     earlier contents: the buffers must still read token 0 at position 0 for
     the capture's warm-up pass, and the graphed steps must match the eager
     ones.  The workspace's block is first filled with 0x7f bytes and freed,
-    so that the generator reuses it."""
+    so that the generator reuses it.  Every strategy kind runs its steps as
+    the whole-step graph (native plan into the fixed layout)."""
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
-    say("graphed decoder on reused workspace memory")
+    say(f"graphed decoder on reused workspace memory ({kind})")
     from beam_engine_amd import PageTable
     from beam_engine_amd.generator import BatchedBeamSearch, _STEP_HEADER_BYTES
     from beam_engine_amd.llama import LlamaConfig, LlamaDecoder
@@ -237,7 +249,7 @@ def test_graphed_decoder_inputs_start_valid_on_reused_memory():
         model = LlamaDecoder(cfg, "cuda", torch.bfloat16, seed=12)
         pt = PageTable(2, page_size=16, max_num_pages=256, head_num=2, head_dim=128, device="cuda",
                        store_dtype=torch.bfloat16)
-        gen = BatchedBeamSearch(model, pt, 4, kernel_type="cascade", graphs=graphs, workspace_bytes=ws_bytes)
+        gen = BatchedBeamSearch(model, pt, 4, kernel_type=kind, graphs=graphs, workspace_bytes=ws_bytes)
         gen.prefill([list(range(3, 40)), list(range(50, 87))])
         runs.append(gen)
     ge, gg = runs
@@ -248,3 +260,5 @@ def test_graphed_decoder_inputs_start_valid_on_reused_memory():
         assert [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in ge.state.candidates] == \
             [(c.trie_node.page_id, c.trie_node.tokens, c.score) for c in gg.state.candidates], f"step {step}"
     assert gg._gd is not None
+    say(f"{kind}: {gg.graphed_steps} of 6 steps as one graph; kinds {[e['kind'] for e in gg.step_log]}")
+    assert gg.graphed_steps >= 5 and ge.graphed_steps == 0

@@ -128,7 +128,7 @@ def test_step_graph_logits_match_per_layer_path():
         psn = torch.from_numpy(np.asarray(pos, np.int64)).to(dev)
         wpg = torch.from_numpy(np.asarray(wp, np.int32)).to(dev)
         wps = torch.from_numpy(np.asarray(wpos, np.int32)).to(dev)
-        w = gen._plan("cascade", levels)
+        w = gen._plan(levels, True)
         gen._gd.load_inputs(tok, psn, wpg, wps)
         want = gen._gd.run(lambda l, q, kv, out=None: w.run(q, kv, out=out)).float().clone()
         wf = gen._fixed_plan(levels, n)

@@ -200,3 +200,211 @@ def test_trie_plan_equals_attn_plan_of_its_metadata(caps):
     assert bytes(info_a) == bytes(info_b)
     assert info_a.kernel == 2 and info_a.static_layout == int(caps)
     assert np.array_equal(plan_a[: info_a.plan_ints], plan_b[: info_b.plan_ints])
+
+
+def _py_levels(st, kind, include_self, picker):
+    """The Python restatement's levels of one strategy (BeamState.segment_tree /
+    absorb_edges / tree_levels, StrategyPicker.choose)."""
+    if kind == "auto":
+        plan = picker.choose(st, include_self)
+        return plan.levels, plan.kind, [plan.costs["flat"], plan.costs["split"], plan.costs["tree"]]
+    segs, paths = st.segment_tree(include_self)
+    if kind == "flat":
+        absorbed = set(k for k, sg in enumerate(segs) if sg[2] >= 0)
+    elif kind == "split":
+        absorbed = set()
+    else:
+        absorbed, _ = st.absorb_edges(segs, (picker.edges or picker.model).absorb)
+    return st.tree_levels(segs, paths, absorbed), kind, None
+
+
+@pytest.mark.parametrize("page_size,hq,hkv,edges,seed", [(4, 32, 8, "mi355x", 11), (16, 32, 8, "fasttree", 12),
+                                                         (16, 64, 8, "mi355x", 13), (8, 8, 8, "fasttree", 14),
+                                                         (16, 32, 8, "mi355x", 15)])
+def test_native_levels_match_python_decompositions(page_size, hq, hkv, edges, seed):
+    """be_trie_levels (flat, split, tree, auto; with and without each
+    candidate's newest token) gives the Python restatement's level arrays,
+    kind and modelled option costs exactly, on random multi-request tries."""
+    from beam_engine_amd.picker import MI355X, StrategyPicker
+    rng_a, rng_b = random.Random(seed), random.Random(seed)
+    beam = 8
+    pa, pb = make_pt(8192, page_size), make_pt(8192, page_size)
+    a = BeamState(beam, pa, fast_metadata=True)
+    b = NativeBeamState(beam, pb)
+    rp = random.Random(seed + 7)
+    for r in range(3):
+        p = [rp.randrange(1000) for _ in range(rp.choice([3, 17, 70, 200]))]
+        a.add_root_sequence(list(p), request_id=r)
+        b.add_root_sequence(list(p), request_id=r)
+    first = [BeamToken(100 + j, -0.1 * j) for j in range(beam)]
+    a.add_filtered_results([BeamGenerateResult(c, first) for c in a.candidates])
+    b.add_filtered_results([BeamGenerateResult(c, first) for c in b.candidates])
+    picker = StrategyPicker(hq, hkv, page_size, "fasttree" if edges == "fasttree" else MI355X)
+    model = picker.tree_model()
+    checked = 0
+    for step in range(40):
+        a.add_filtered_results(random_results(a, rng_a, beam))
+        b.add_filtered_results(random_results(b, rng_b, beam))
+        if step % 3:
+            continue
+        for kind in ("flat", "split", "tree", "auto"):
+            for inc in (False, True):
+                want, want_kind, want_costs = _py_levels(a, kind, inc, picker)
+                levels, qids, wp, ws, pos, got_kind, got_costs = b.step_levels(kind, inc, model)
+                assert got_kind == want_kind, (step, kind, inc)
+                assert len(levels) == len(want), (step, kind, inc)
+                for lg, lw in zip(levels, want):
+                    for xg, xw in zip(lg, lw):
+                        assert np.array_equal(np.asarray(xg), np.asarray(xw, dtype=np.int32)), (step, kind, inc)
+                if want_costs is not None:
+                    assert list(got_costs) == want_costs, (step, kind, inc)
+                assert list(qids) == a.query_token_ids()
+                assert (list(wp), list(ws)) == tuple(map(list, a.write_locations()))
+                assert list(pos) == a.position_ids()
+                if kind == "flat":
+                    kvp, kvi, lpl = a.flat_lists(inc)
+                    assert list(levels[0][0]) == list(range(len(lpl) + 1))
+                    assert (list(levels[0][1]), list(levels[0][2]), list(levels[0][3])) == (kvp, kvi, lpl)
+                checked += 1
+    assert checked >= 8 * 10
+
+
+def test_trie_plan_kind_equals_attn_plan_of_its_levels():
+    """be_trie_plan_kind writes the plan be_attn_plan gives for the levels of
+    be_trie_metadata_kind (no causal mask outside the cascade kind)."""
+    import ctypes
+    from beam_engine_amd import _lib
+    from beam_engine_amd.beam_state import _parse_metadata
+    from beam_engine_amd.picker import StrategyPicker
+    lib = _lib.load()
+    rng = random.Random(21)
+    pt = make_pt(8192, 16)
+    st = NativeBeamState(8, pt)
+    for r in range(3):
+        st.add_root_sequence([rng.randrange(1000) for _ in range(150 + 40 * r)], request_id=r)
+    st.add_filtered_results([BeamGenerateResult(c, [BeamToken(100 + j, -0.1 * j) for j in range(8)])
+                             for c in st.candidates])
+    for _ in range(25):
+        st.add_filtered_results(random_results(st, rng, 8))
+    n = st.num_candidates()
+    hq, hkv, d = 32, 8, 128
+    model = StrategyPicker(hq, hkv, 16, "fasttree").tree_model()
+    for kind in ("flat", "split", "tree", "auto"):
+        meta = np.zeros(1 << 18, np.int32)
+        used = ctypes.c_int64(0)
+        plan_a = np.zeros(1 << 21, np.int32)
+        info_a = _lib.BeAttnPlanInfo()
+        mp, chosen = ctypes.c_int32(0), ctypes.c_int32(-1)
+        _lib.check(lib.be_trie_plan_kind(st._h, _lib.KIND_CODES[kind], 1, ctypes.byref(model), hq, hkv, d,
+                                         _lib.BE_BF16, 0, 256, None, meta.ctypes.data, meta.size, ctypes.byref(used),
+                                         plan_a.ctypes.data, plan_a.size, ctypes.byref(info_a), ctypes.byref(mp),
+                                         ctypes.byref(chosen), None), "trie plan")
+        levels, *_ = _parse_metadata(meta[: used.value].copy(), n)
+        ref = st.step_levels(kind, True, model)
+        assert ref[5] == _lib.KIND_NAMES[chosen.value]
+        for lg, lw in zip(levels, ref[0]):
+            for xg, xw in zip(lg, lw):
+                assert np.array_equal(xg, xw)
+        arr = (_lib.BeLevel * len(levels))()
+        keep = []
+        for i, (qo, kvp, kvi, lpl) in enumerate(levels):
+            qo, kvp, kvi, lpl = (np.ascontiguousarray(x, np.int32) for x in (qo, kvp, kvi, lpl))
+            keep += [qo, kvp, kvi, lpl]
+            arr[i] = _lib.BeLevel(qo.ctypes.data, kvp.ctypes.data, kvi.ctypes.data if len(kvi) else 0,
+                                  lpl.ctypes.data, len(qo) - 1)
+        max_page = max(int(np.max(l[2])) for l in levels if len(l[2]))
+        plan_b = np.zeros_like(plan_a)
+        info_b = _lib.BeAttnPlanInfo()
+        _lib.check(lib.be_attn_plan(arr, len(levels), n, hq, hkv, d, 16, max_page + 1, _lib.BE_BF16, 0, 256, None,
+                                    plan_b.ctypes.data, plan_b.size, ctypes.byref(info_b)), "attention plan")
+        assert bytes(info_a) == bytes(info_b)
+        assert np.array_equal(plan_a[: info_a.plan_ints], plan_b[: info_b.plan_ints])
+
+
+def test_trie_apply_fails_before_changing_state_when_pages_run_out():
+    """A selection whose expansion needs more pages than the pool holds after
+    the prune raises MemoryError and leaves the trie, its candidates, the
+    free list and the version as they were; the same selection succeeds once
+    the pool has room (pages the prune frees count as room)."""
+    pt = make_pt(10, 4)
+    st = NativeBeamState(4, pt)
+    st.add_root_sequence([1, 2, 3, 4], request_id=0)         # one full page
+    st.add_root_sequence([5, 6], request_id=1)               # one partial page
+    before = (snapshot(st), list(pt.free_pages), int(st._read_sizes()[0]))
+    ver = st._ver.value
+    # candidate 0 forks 4 ways on a full page (4 pages), candidate 1 forks 4
+    # ways on a partial page (3 copies): 7 pages, 8 free -> fine; take 2 first
+    held = [pt.allocate_block(), pt.allocate_block()]
+    par = [0, 0, 0, 0, 1, 1, 1, 1]
+    tok = [10, 11, 12, 13, 20, 21, 22, 23]
+    sc = [-0.1 * i for i in range(8)]
+    with pytest.raises(MemoryError):
+        st.apply_selection(par, tok, sc)
+    assert (snapshot(st), list(pt.free_pages), int(st._read_sizes()[0])) == \
+        (before[0], list(pt.free_pages), before[2])
+    assert st._ver.value == ver and pt._pending == []
+    pt.free_block(held[0])
+    st.apply_selection(par, tok, sc)                         # 7 pages needed, 7 free
+    assert len(st.candidates) == 8 and pt.num_free_pages() == 0
+    # the prune's pages count: no page is free, the first candidate (one
+    # token on its page) forks 4 ways (3 copies) and the other 7 die, freeing
+    # 7 pages first
+    st.apply_selection([0, 0, 0, 0], [30, 31, 32, 33], [-1.0, -1.1, -1.2, -1.3])
+    assert len(st.candidates) == 4 and pt.num_free_pages() == 4
+
+
+@pytest.mark.parametrize("page_size,hq,hkv,seed", [(4, 32, 8, 31), (16, 32, 8, 32), (16, 64, 8, 33)])
+def test_fasttree_boundary_levels_equal_native_fasttree_kind(page_size, hq, hkv, seed):
+    """The reference's FastTree call path -- BeamState.get_fasttree_input ->
+    prepare_fasttree_metadata_for_paged_cache -- plans the same levels as the
+    engine's native "fasttree" kind (be_trie_levels with FastTree's edges and
+    each candidate's newest token) on the same trie, and those attend each
+    candidate to exactly its req_to_token row: per level, every query's pages
+    and token counts, concatenated, give its whole path."""
+    from beam_engine_amd.fasttree import fasttree_levels
+    from beam_engine_amd.picker import StrategyPicker
+    rng_a, rng_b = random.Random(seed), random.Random(seed)
+    beam = 8
+    pa, pb = make_pt(8192, page_size), make_pt(8192, page_size)
+    a = BeamState(beam, pa, fast_metadata=True)
+    b = NativeBeamState(beam, pb)
+    rp = random.Random(seed + 3)
+    for r in range(3):
+        p = [rp.randrange(1000) for _ in range(rp.choice([5, 40, 130]))]
+        a.add_root_sequence(list(p), request_id=r)
+        b.add_root_sequence(list(p), request_id=r)
+    first = [BeamToken(100 + j, -0.1 * j) for j in range(beam)]
+    a.add_filtered_results([BeamGenerateResult(c, first) for c in a.candidates])
+    b.add_filtered_results([BeamGenerateResult(c, first) for c in b.candidates])
+    model = StrategyPicker(hq, hkv, page_size, "fasttree").tree_model()
+    for step in range(30):
+        a.add_filtered_results(random_results(a, rng_a, beam))
+        b.add_filtered_results(random_results(b, rng_b, beam))
+        tree_nodes, req_to_token, qids, wp, wpos = a.get_fasttree_input()
+        n = len(a.candidates)
+        got = fasttree_levels(tree_nodes, req_to_token, n, hq, hkv, page_size)
+        want = b.step_levels("tree", True, model)[0]
+        assert len(got) == len(want), step
+        for lg, lw in zip(got, want):
+            for xg, xw in zip(lg, lw):
+                assert np.array_equal(np.asarray(xg, np.int32), np.asarray(xw)), step
+        # every query's slots over the levels = its req_to_token row
+        rtt = req_to_token.cpu().numpy()
+        for ci in range(n):
+            slots = []
+            for qo, kvp, kvi, lpl in got:
+                j = int(np.searchsorted(qo, ci, side="right")) - 1
+                pages = kvi[kvp[j]: kvp[j + 1]]
+                for t, pg in enumerate(pages):
+                    cnt = page_size if t + 1 < len(pages) else lpl[j]
+                    slots.extend(pg * page_size + i for i in range(cnt))
+            length = sum(len(x.tokens) for x in _path(a.candidates[ci].trie_node))
+            assert sorted(slots) == sorted(rtt[ci, :length].tolist()), (step, ci)
+
+
+def _path(node):
+    out = []
+    while node is not None:
+        out.append(node)
+        node = node.parent
+    return out[::-1]
