@@ -218,8 +218,9 @@ class StrategyPicker:
         m.edge_model = _lib.BE_EDGES_FASTTREE if self.edges is not None else _lib.BE_EDGES_FITTED
         return m
 
-    def _options(self, state: BeamState, include_self: bool = False):
-        segs, paths = state.segment_tree(include_self)
+    def options(self, segs, paths):
+        """Modelled cost and absorbed edge set of every candidate option
+        (flat, split, tree) of a segment tree (``BeamState.segment_tree``)."""
         m = self.model
         out = {}
         for kind in self.candidates:
@@ -233,19 +234,26 @@ class StrategyPicker:
                 absorbed = set()
                 cost = decomposition_cost(m, segs, paths, absorbed, [sg[1] for sg in segs])
             else:
-                absorbed, teff = state.absorb_edges(segs, (self.edges or m).absorb)
+                absorbed, teff = BeamState.absorb_edges(segs, (self.edges or m).absorb)
                 cost = decomposition_cost(m, segs, paths, absorbed, teff)
             out[kind] = (cost, absorbed)
-        return segs, paths, out
+        return out
 
-    def costs(self, state: BeamState, include_self: bool = False) -> Dict[str, float]:
-        return {k: v[0] for k, v in self._options(state, include_self)[2].items()}
-
-    def choose(self, state: BeamState, include_self: bool = False) -> Plan:
-        segs, paths, opts = self._options(state, include_self)
+    def choose_segments(self, segs, paths) -> Plan:
+        """``choose`` on a segment tree given directly."""
+        from .beam_state import decomposition_levels
+        opts = self.options(segs, paths)
         kind = min(opts, key=lambda k: opts[k][0])
-        plan = Plan(kind, state.tree_levels(segs, paths, opts[kind][1]), opts[kind][0],
+        plan = Plan(kind, decomposition_levels(segs, paths, opts[kind][1], self.page_size), opts[kind][0],
                     {k: v[0] for k, v in opts.items()})
         self.last = plan
         self.history.append(kind)
         return plan
+
+    def costs(self, state: BeamState, include_self: bool = False) -> Dict[str, float]:
+        segs, paths = state.segment_tree(include_self)
+        return {k: v[0] for k, v in self.options(segs, paths).items()}
+
+    def choose(self, state: BeamState, include_self: bool = False) -> Plan:
+        segs, paths = state.segment_tree(include_self)
+        return self.choose_segments(segs, paths)

@@ -29,6 +29,50 @@ class Workload:
     note: str = ""
     tokens_per_query: List[int] = field(default_factory=list)
 
+    def segment_tree(self):
+        """(segs, paths) as ``BeamState.segment_tree`` gives them, read off
+        the cascade levels (each group is one segment, its parent the group
+        one level up holding its queries; every query has a group on every
+        level here)."""
+        qo_arr, kvp_arr, kvi_arr, lpl_arr = self.levels
+        segs, paths = [], [[] for _ in range(self.num_queries)]
+        prev_of = [-1] * self.num_queries
+        for qo, kvp, kvi, lpl in zip(qo_arr, kvp_arr, kvi_arr, lpl_arr):
+            for j in range(len(qo) - 1):
+                pages = list(kvi[kvp[j]: kvp[j + 1]])
+                qs = list(range(qo[j], qo[j + 1]))
+                parent = prev_of[qs[0]]
+                if any(prev_of[q] != parent for q in qs):
+                    raise ValueError("a group's queries have different parents")
+                k = len(segs)
+                segs.append([pages, (len(pages) - 1) * self.page + int(lpl[j]), parent, qs, []])
+                if parent >= 0:
+                    segs[parent][4].append(k)
+                for q in qs:
+                    paths[q].append(k)
+                    prev_of[q] = k
+        return segs, paths
+
+    def decomposition(self, kind: str):
+        """Level arrays of one exact path decomposition of the workload:
+        "flat", "split", "tree" (the fitted MI355X edge model), "fasttree"
+        (FastTree's edge model) or "auto" (the picker's choice)."""
+        from .beam_state import BeamState, decomposition_levels
+        from .picker import MI355X, StrategyPicker
+        segs, paths = self.segment_tree()
+        picker = StrategyPicker(self.hq, self.hkv, self.page, "fasttree" if kind == "fasttree" else MI355X)
+        if kind == "auto":
+            return picker.choose_segments(segs, paths).levels
+        if kind == "flat":
+            absorbed = set(k for k, sg in enumerate(segs) if sg[2] >= 0)
+        elif kind == "split":
+            absorbed = set()
+        elif kind in ("tree", "fasttree"):
+            absorbed, _ = BeamState.absorb_edges(segs, (picker.edges or picker.model).absorb)
+        else:
+            raise ValueError(f"unknown decomposition {kind!r}")
+        return decomposition_levels(segs, paths, absorbed, self.page)
+
 
 class _Pages:
     def __init__(self):
@@ -122,10 +166,45 @@ def config3():
                     [4096 + 256 + 128 + 96] * 32)
 
 
+def e2e_step():
+    """The decode attention of one config-4 step (8 requests x beam 16, 32/8
+    heads, D 128, bf16, page 16) at the trie's typical mid-run structure:
+    each request's 16 beams share a 1136-token prefix (the 1024-token prompt
+    and the generated tokens all beams agree on), then branch into groups of
+    1, 1, 2, 3, 1 and 8 beams over one 16-token page each, and every beam ends
+    in a private page holding 8 tokens (three cascade levels)."""
+    page = 16
+    alloc = _Pages()
+    split = [1, 1, 2, 3, 1, 8]
+    lv = [([0], [0], [], []) for _ in range(3)]
+    paths = []
+
+    def add(level, pages, last, nq):
+        qo, kvp, kvi, lpl = lv[level]
+        kvi.extend(pages)
+        kvp.append(len(kvi))
+        lpl.append(last)
+        qo.append(qo[-1] + nq)
+    for r in range(8):
+        pre, last0 = alloc.take(1136, page)
+        add(0, pre, last0, 16)
+        for nb in split:
+            mid, last1 = alloc.take(16, page)
+            add(1, mid, last1, nb)
+            for _ in range(nb):
+                leaf, last2 = alloc.take(8, page)
+                add(2, leaf, last2, 1)
+                paths.append((pre + mid + leaf, last2))
+    levels = tuple([l[i] for l in lv] for i in range(4))
+    return Workload("e2e", 32, 8, 128, page, 128, alloc.next, levels, _flat_from_paths(paths),
+                    "config-4 step: 8 req x beam 16, 32/8 heads, D128, bf16, prefix 1136, branch pages of 16, "
+                    "leaf pages of 8", [1136 + 16 + 8] * 128)
+
+
 def config1():
     """CPU-path shape: 1 request x beam 4, prefix 512, suffix 32, 8/8 heads, D 64, fp32, page 16."""
     return shared_prefix("c1", 1, 4, 512, [32] * 4, 8, 8, 64,
                          note="1 req x beam 4, 8/8 heads, D64, fp32, page 16, prefix 512, suffix 32")
 
 
-BUILDERS = {"c1": config1, "c2": config2, "c3": config3, "c5": config5, "ns": north_star}
+BUILDERS = {"c1": config1, "c2": config2, "c3": config3, "c5": config5, "ns": north_star, "e2e": e2e_step}

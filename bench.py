@@ -41,11 +41,16 @@ def parse():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (decode steps / attention reps)")
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="e2e",
-                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-prefill",
+                    choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-e2e", "attn-prefill",
                              "topk", "topk-c1"])
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "fasttree", "flat", "split", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
+    ap.add_argument("--plan-cus", type=int, default=None,
+                    help="attention workloads: plan for this many CUs (workgroups of the streaming kernel)")
+    ap.add_argument("--plan-opts", default="",
+                    help="attention workloads: comma-separated planner switches (no_tail, tail_role, no_regs, "
+                         "no_wide, no_wide256, tile_kernel)")
     ap.add_argument("--row-blocks", default="auto", choices=["auto", "on", "off"],
                     help="attention: the row-block kernel (one launch, no partials) forced on or off")
     ap.add_argument("--selection", default="vanilla", choices=["vanilla", "diverse"],
@@ -84,17 +89,30 @@ def attention_workload(args):
     qs = [torch.randn((wl.num_queries, wl.hq, wl.d), device=dev, dtype=dtype).mul_(scale) for _ in range(L)]
     outs = [torch.empty_like(q) for q in qs]
     ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-    if args.strategy == "cascade":
-        w = MultiLevelCascadeAttentionWrapper(len(wl.levels[0]), ws)
+    def tune(w):
         w._fused_merge = args.fused_merge
         w._rows = {"auto": None, "on": True, "off": False}[args.row_blocks]
+        w._num_cus = args.plan_cus
+        for opt in filter(None, args.plan_opts.split(",")):
+            if opt not in ("no_tail", "tail_role", "no_regs", "no_wide", "no_wide256", "tile_kernel"):
+                raise SystemExit(f"unknown --plan-opts entry {opt!r}")
+            setattr(w, "_" + opt, True)
+        return w
+    if args.strategy == "cascade":
+        w = tune(MultiLevelCascadeAttentionWrapper(len(wl.levels[0]), ws))
         w.plan(*wl.levels, wl.hq, wl.hkv, wl.d, wl.page, q_data_type=dtype)
         alg_kv = w.stats.kv_bytes
-    else:
-        w = BatchDecodeWithPagedKVCacheWrapper(ws)
-        w._fused_merge = args.fused_merge
+    elif args.strategy == "flat":
+        w = tune(BatchDecodeWithPagedKVCacheWrapper(ws))
         w.plan(*wl.flat, wl.hq, wl.hkv, wl.d, wl.page, q_data_type=dtype)
         alg_kv = sum(wl.tokens_per_query) * wl.hkv * wl.d * es * 2     # flat scored by its own path bytes
+    else:
+        # the exact path decompositions of the workload's segment tree
+        lv = wl.decomposition(args.strategy)
+        w = tune(MultiLevelCascadeAttentionWrapper(len(lv), ws))
+        w.plan([l[0] for l in lv], [l[1] for l in lv], [l[2] for l in lv], [l[3] for l in lv], wl.hq, wl.hkv, wl.d,
+               wl.page, q_data_type=dtype)
+        alg_kv = w.stats.kv_bytes
     st = w.stats
     alg = alg_kv + st.qo_bytes
     for _ in range(warmup):
@@ -293,9 +311,6 @@ def main():
         print(json.dumps(prefill_workload(args)), flush=True)
         return 0
     if args.workload.startswith("attn-"):
-        if args.strategy not in ("cascade", "flat"):
-            print(json.dumps({"error": "attention workloads take --strategy cascade or flat"}))
-            return 2
         result, wl = attention_workload(args)
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = cpu_baseline_attention(wl, result["roofline"]["bytes_per_launch"])

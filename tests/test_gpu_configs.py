@@ -191,12 +191,15 @@ def test_config5_trie_every_strategy(ws):
 
 
 def test_config4_e2e_live_state():
-    """Config 4 end to end for 40 decode steps with HIP graphs: the trie is
+    """Config 4 end to end, all 256 decode steps with HIP graphs: the trie is
     replayed on the oracle with the engine's own selections (page ids,
     candidates, fork copies, free list identical at every step); the
-    selection of steps 0, 13 and 39 is checked bit for bit against the oracle
-    on the same logits; then layer 5's cascade attention at the live state is
-    checked against the oracle on the real pages."""
+    selections of steps 0, 13, 39, 97, 163 and 255 are checked bit for bit
+    against the oracle on the same logits; the final ranking of every request
+    (beam_state.py:646-682) equals the oracle's; then layer 5's cascade
+    attention at the live state after step 256 (beam suffixes past 128 tokens,
+    leaf groups on the streaming kernel) is checked against the oracle on the
+    real pages."""
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     from beam_engine_amd import MultiLevelCascadeAttentionWrapper, PageTable
@@ -217,10 +220,18 @@ def test_config4_e2e_live_state():
     o = OracleBeamState(beam, o_alloc)
     for p in prompts:
         o.add_root_sequence(p)
+
+    def root_of(node):
+        while node.parent is not None:
+            node = node.parent
+        return node
+    # request r's root page node (each request's candidates stay below it)
+    request_of_root = {id(root_of(o.candidates[r].node)): r for r in range(n_req)}
     # the graph capture reserves the pool's last page as its scratch slot
     o_alloc.free_pages.remove(pages - 1)
     step = {"i": 0}
-    check_steps = {0, 13, 39}
+    check_steps = {0, 13, 39, 97, 163, 255}
+    steps = 256
     real_select = gen.strategy.select_batched
 
     def select(state, logits, temperature, mode):
@@ -245,16 +256,26 @@ def test_config4_e2e_live_state():
     lg = logits.float().cpu().numpy()
     o.add_filtered_results([OResult(o.candidates[r], ot.prefill_select(lg[r], beam, "bfloat16"))
                             for r in range(n_req)])
-    say("config 4 e2e: prefill done; decoding 40 steps")
-    for i in range(40):
+    say(f"config 4 e2e: prefill done; decoding {steps} steps")
+    for i in range(steps):
         gen.step()
         got = [(c.trie_node.page_id, list(c.trie_node.tokens), c.score) for c in gen.state.candidates]
         want = [(c.node.page_id, c.node.tokens, c.score) for c in o.candidates]
         assert got == want, f"trie differs after step {i}"
         assert list(pt.free_pages) == list(o_alloc.free_pages), f"free list differs after step {i}"
-        if (i + 1) % 10 == 0:
-            say(f"config 4 e2e: step {i + 1}/40 trie replay equal")
-    assert o_alloc.copies, "the run should fork partial pages"
+        if (i + 1) % 32 == 0:
+            say(f"config 4 e2e: step {i + 1}/{steps} trie replay equal")
+    assert step["i"] == steps and o_alloc.copies, "the run should fork partial pages"
+    # the final ranking of every request against the oracle's
+    finals = gen.final_sequences()
+    for r in range(n_req):
+        sub = OracleBeamState.__new__(OracleBeamState)
+        sub.finished_candidates = []
+        sub.candidates = [c for c in o.candidates if request_of_root[id(root_of(c.node))] == r]
+        want = sub.get_final_sequences(beam, 1.0)
+        assert [(list(sq), sc) for sq, sc in finals[r]] == [(list(sq), sc) for sq, sc in want], f"request {r}"
+        assert len(want[0][0]) == 1024 + steps + 1
+    say("config 4 e2e: final sequences of the 8 requests equal the oracle's")
     # the last selection's fork copies (staged for a next step) into the pages
     gen.flush()
     # one layer's attention at the live state, on the real pages
@@ -277,4 +298,4 @@ def test_config4_e2e_live_state():
     np.testing.assert_allclose(out.float().cpu().numpy(), ref_o, **TOL)
     fin = np.isfinite(ref_lse)
     np.testing.assert_allclose(lse.cpu().numpy()[fin], ref_lse[fin], rtol=2e-3, atol=2e-3)
-    say(f"config 4 e2e: layer 5 attention at step 40 equal ({len(lv)} levels, {n} candidates)")
+    say(f"config 4 e2e: layer 5 attention after step {steps} equal ({len(lv)} levels, {n} candidates)")

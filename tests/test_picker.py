@@ -176,7 +176,8 @@ def test_segment_tree_costs_match_the_level_arrays(seed):
     arrays they cost the same (up to candidates split into several runs)."""
     st, page = random_state(seed)
     pk = StrategyPicker(32, 8, page)
-    segs, paths, opts = pk._options(st)
+    segs, paths = st.segment_tree()
+    opts = pk.options(segs, paths)
     for kind, (cost, absorbed) in opts.items():
         levels = st.tree_levels(segs, paths, absorbed)
         lv_cost, _ = plan_cost(pk.model, levels, page)
