@@ -80,6 +80,15 @@ static TopkGeom topk_geom(int n_rows, int vocab, int k) {
 constexpr int kTopkCounterWords = 512;
 inline int64_t topk_counter_bytes(int) { return ((int64_t)kTopkCounterWords * 4 + 255) / 256 * 256; }
 
+// The hand-off from the rows pass's row workgroups to a request's pool pass
+// (below) rests on how gfx942 / gfx950 treat agent-scope relaxed accesses:
+// stores written through to the device's point of coherence (sc1), loads that
+// read there, and in-order completion of a wave's vector memory operations
+// before s_waitcnt vmcnt(0) returns.  Another target would need its own check.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__) && !defined(__gfx942__)
+#error "topk.hip's cross-workgroup hand-off is written for gfx942 / gfx950"
+#endif
+
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p) { return to_f32(*p); }
 
@@ -1108,10 +1117,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pool_kernel(int n_rows, int
 // Row lists go to the pool through agent-scope stores and loads (written
 // through to the device's point of coherence).
 // Arrival counters (u32 at the start of the workspace, one per request) are
-// zero at rest: a launch adds one per arrival and the last arrival sets the
-// word back to zero, so every complete launch leaves them zero.  A workspace must therefore hold zeros
-// there before its first use (the Python workspace is allocated zeroed; the
-// static scratch of be_beam_topk_noalloc starts zeroed).
+// set to zero by the units pass's first workgroup, so the rows pass of every
+// call starts from zero whatever the workspace held (a launch also leaves
+// them zero: the last arrival resets its word).
 constexpr int kFusedRowCand = 2048;    // segs x cap of one row (two per pass-B thread)
 constexpr int kFusedPool = 512;        // rows x min(k, beam) of one request, in LDS
 constexpr int kFusedPoolRows = 256;
@@ -1298,6 +1306,10 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
   const int G = gridDim.x;
   const T* logits = reinterpret_cast<const T*>(a.logits);
   constexpr int kWords = kPerThread / 2;
+  // the rows pass's arrival counters start every call at zero (it runs after
+  // this kernel), whatever the workspace held
+  if (blockIdx.x == 0)
+    for (int i = tid; i < a.n_req; i += kTopkThreads) st_wt(a.ctr + i, 0u);
   // 16-bit keys of -600 and 600: a wave sums against 0 when its largest x' lies between them
   const uint32_t klo = key16_of_bits(bits_of<T>(-600.0f)), khi = key16_of_bits(bits_of<T>(600.0f));
   // Units go out by columns: with G = 4C workgroups, workgroups col, col + C,

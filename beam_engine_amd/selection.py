@@ -19,9 +19,9 @@ from . import _lib
 
 
 class TopkWorkspace:
-    """Device scratch for be_beam_topk, grown on demand and reused.  It is
-    allocated zeroed: the kernel's arrival counters at its start must be zero
-    before the first call, and every call leaves them zero."""
+    """Device scratch for be_beam_topk, grown on demand and reused (the call
+    clears the arrival counters at its start, so the contents need no
+    initialisation)."""
 
     def __init__(self, device=None):
         self.device = torch.device(device) if device is not None else torch.device("cuda")
