@@ -85,7 +85,8 @@ KIND_NAMES = {v: k for k, v in KIND_CODES.items()}
 
 class BeTreeModel(ctypes.Structure):
     _fields_ = [("tile_nt", ctypes.c_double * 4)] + [
-        (n, ctypes.c_double) for n in ("seg", "slot", "tail", "fixed", "alpha", "beta", "gamma")] + [
+        (n, ctypes.c_double) for n in ("seg", "slot", "tail", "fixed", "alpha", "beta", "gamma", "tile_w128",
+                                       "tile_w256")] + [
         (n, ctypes.c_int32) for n in ("num_qo_heads", "num_kv_heads", "edge_model", "reserved")]
 
 
@@ -98,7 +99,7 @@ EXPORTS = (
     "be_pages_release", "be_pages_reserve", "be_pages_num_free", "be_pages_ref_count", "be_pages_free_list",
     "be_trie_create", "be_trie_destroy", "be_trie_add_root", "be_trie_apply", "be_trie_sizes",
     "be_trie_candidates", "be_trie_export", "be_trie_metadata", "be_trie_plan", "be_trie_levels",
-    "be_trie_plan_kind", "be_trie_metadata_kind",
+    "be_trie_plan_kind", "be_trie_metadata_kind", "be_read_probe",
 )
 
 _lib = None
@@ -166,6 +167,7 @@ def load() -> ctypes.CDLL:
                                  i64, ctypes.POINTER(BeAttnPlanInfo), i32p]
     lib.be_trie_levels.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, ctypes.POINTER(BeTreeModel), vp,
                                    i64, i64p, i32p, vp]
+    lib.be_read_probe.argtypes = [vp, i64, i64, i64, i64, i32, vp, i32, vp]
     lib.be_trie_metadata_kind.argtypes = [vp, i32, i32, ctypes.POINTER(BeTreeModel), vp, i64, i64p, i32p, vp]
     lib.be_trie_plan_kind.argtypes = [vp, i32, i32, ctypes.POINTER(BeTreeModel), i32, i32, i32, i32, i32, i32,
                                       ctypes.POINTER(BePlanCaps), vp, i64, i64p, vp, i64,

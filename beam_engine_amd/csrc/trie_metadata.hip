@@ -156,6 +156,7 @@ void chain_pages(const TrieWalk& w, const int32_t* parent, const int32_t* page, 
 
 // ---------------------------------------------------------------- costs
 constexpr int kTileTokens = 64, kSegRows = 64, kTailTokens = 128, kTailQueries = 4, kTailChunk = 16;
+constexpr int64_t kWideMinTiles = 8, kWideMinTiles64 = 64 * 256;
 
 struct Costs {
   const be_tree_model* m;
@@ -170,6 +171,16 @@ struct Costs {
     const int64_t tiles = (tokens + kTileTokens - 1) / kTileTokens;
     int64_t rows = nq * g;
     double cost = 0.0;
+    if (rows > kSegRows && tiles >= kWideMinTiles && (rows + kSegRows - 1) / kSegRows * tiles * hkv >= kWideMinTiles64) {
+      // the planner's wide segments: 256 rows when the group has that many, else 128
+      const int64_t wr = rows >= 256 ? 256 : 128;
+      const double coef = rows >= 256 ? m->tile_w256 : m->tile_w128;
+      while (rows > 0) {
+        rows -= std::min<int64_t>(rows, wr);
+        cost += (double)tiles * coef + m->seg;
+      }
+      return cost * hkv;
+    }
     while (rows > 0) {
       const int64_t r = std::min<int64_t>(rows, kSegRows);
       cost += (double)tiles * m->tile_nt[std::min<int64_t>(4, (r + 15) / 16) - 1] + m->seg;

@@ -39,17 +39,21 @@ SEG_ROWS = 64             # rows (queries x GQA heads) per streaming segment
 TAIL_TOKENS = 128         # tail pass: groups of at most this many tokens ...
 TAIL_QUERIES = 4          # ... and at most this many queries
 TAIL_CHUNK = 16
+WIDE_MIN_TILES = 8        # groups of more than 64 rows take wide (128 / 256-row) segments from this many tiles ...
+WIDE_MIN_TILES64 = 64 * 256   # ... when the group alone has 64 tiles of 64 rows per workgroup of an MI355X
 
 
 @dataclass(frozen=True)
 class KernelCosts:
     """Machine time (us per layer, the whole GPU) of one unit of work."""
-    tile_nt: Tuple[float, float, float, float] = (0.005995, 0.006132, 0.006983, 0.007661)
+    tile_nt: Tuple[float, float, float, float] = (0.005513, 0.006248, 0.006062, 0.006575)
     """one 64-token tile of one KV head, by 16-row MFMA tiles filled (1, 2, 3, 4)"""
-    seg: float = 0.012804           # a segment start (Q rows, epilogue) of one KV head
-    slot: float = 0.003339          # a partial slot of one (query, KV head) and its merge
-    tail: float = 0.001222          # a 16-token tail chunk of one (query, KV head)
-    fixed: float = 8.559           # both launches, prologue and the merge of a step
+    seg: float = 0.007044           # a segment start (Q rows, epilogue) of one KV head
+    slot: float = 0.0               # a partial slot of one (query, KV head) and its merge (the fit finds it free)
+    tail: float = 0.001332          # a 16-token tail chunk of one (query, KV head)
+    fixed: float = 12.584           # both launches, prologue and the merge of a step
+    tile_w128: float = 0.007958     # one 64-token tile of a 128-row wide segment, one KV head
+    tile_w256: float = 0.014145     # one 64-token tile of a 256-row wide segment, one KV head
 
 
 MI355X = KernelCosts()
@@ -84,6 +88,14 @@ class CostModel:
         tiles = math.ceil(tokens / TILE_TOKENS)
         rows = nq * self.g
         cost = 0.0
+        if rows > SEG_ROWS and tiles >= WIDE_MIN_TILES and \
+                math.ceil(rows / SEG_ROWS) * tiles * self.hkv >= WIDE_MIN_TILES64:
+            # the planner's wide segments: 256 rows when the group has that many, else 128
+            wr, coef = (256, c.tile_w256) if rows >= 256 else (128, c.tile_w128)
+            while rows > 0:
+                rows -= min(rows, wr)
+                cost += tiles * coef + c.seg
+            return cost * self.hkv
         while rows > 0:
             r = min(rows, SEG_ROWS)
             cost += tiles * c.tile_nt[min(4, math.ceil(r / 16)) - 1] + c.seg
@@ -212,6 +224,7 @@ class StrategyPicker:
         for i, v in enumerate(c.tile_nt):
             m.tile_nt[i] = v
         m.seg, m.slot, m.tail, m.fixed = c.seg, c.slot, c.tail, c.fixed
+        m.tile_w128, m.tile_w256 = c.tile_w128, c.tile_w256
         ft = self.edges if self.edges is not None else FastTreeCostModel(self.model.g * self.model.hkv, self.model.hkv)
         m.alpha, m.beta, m.gamma = ft.alpha, ft.beta, ft.gamma
         m.num_qo_heads, m.num_kv_heads = self.model.g * self.model.hkv, self.model.hkv

@@ -53,14 +53,15 @@ class Workload:
                     prev_of[q] = k
         return segs, paths
 
-    def decomposition(self, kind: str):
+    def decomposition(self, kind: str, costs=None):
         """Level arrays of one exact path decomposition of the workload:
-        "flat", "split", "tree" (the fitted MI355X edge model), "fasttree"
-        (FastTree's edge model) or "auto" (the picker's choice)."""
+        "flat", "split", "tree" (the fitted MI355X edge model, or ``costs``),
+        "fasttree" (FastTree's edge model) or "auto" (the picker's choice)."""
         from .beam_state import BeamState, decomposition_levels
         from .picker import MI355X, StrategyPicker
         segs, paths = self.segment_tree()
-        picker = StrategyPicker(self.hq, self.hkv, self.page, "fasttree" if kind == "fasttree" else MI355X)
+        picker = StrategyPicker(self.hq, self.hkv, self.page,
+                                "fasttree" if kind == "fasttree" else (costs if costs is not None else MI355X))
         if kind == "auto":
             return picker.choose_segments(segs, paths).levels
         if kind == "flat":

@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="e2e",
                     choices=["e2e", "attn-c1", "attn-c2", "attn-ns", "attn-c3", "attn-c5", "attn-e2e", "attn-prefill",
-                             "topk", "topk-c1"])
+                             "topk", "topk-c1", "read-ns"])
     ap.add_argument("--strategy", default="cascade", choices=["cascade", "fasttree", "flat", "split", "tree", "auto"],
                     help="attention workloads: cascade or flat; e2e: also tree / auto (cost-model picker)")
     ap.add_argument("--fused-merge", action="store_true", help="merge split-K partials inside the attention kernel")
@@ -272,6 +272,63 @@ def topk_workload(args):
     return result
 
 
+def read_ceiling_workload(args):
+    """The read ceiling the attention roofline is read against: one launch of
+    a plain read kernel (``be_read_probe``) over one north-star layer's K/V
+    (3072 pages of [2, 16, 8, 128] bf16 = 201 MB) per call, 32 distinct layers,
+    HIP events around each launch as the attention workloads time theirs.
+    Two access patterns -- the layer as one contiguous range, and one KV head's
+    256-byte rows at a 2 KB stride at a time (the decode kernels' pattern) --
+    over a sweep of grid sizes; value = the best per-launch GB/s."""
+    import torch
+    from beam_engine_amd import _lib
+    lib = _lib.load()
+    P, page, hkv, d = 3072, 16, 8, 128
+    L = args.layers
+    steps = args.steps or 10
+    warmup = 3 if args.warmup is None else args.warmup
+    dev = torch.device("cuda")
+    layers = [torch.empty((P, 2, page, hkv, d), dtype=torch.bfloat16, device=dev).fill_(0.5) for _ in range(L)]
+    nbytes = layers[0].numel() * 2
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    patterns = {"contiguous": (nbytes // 256, nbytes // 256, 256, 0, 256),
+                "per KV head": (P * 2 * page * hkv, P * 2 * page, hkv * d * 2, d * 2, d * 2)}
+    results = []
+    for name, (rows, inner, istr, ostr, rb) in patterns.items():
+        for grid in (256, 1024, 2048, 4096, 8192, 16384):
+            def launch(l):
+                _lib.check(lib.be_read_probe(layers[l].data_ptr(), rows, inner, istr, ostr, rb, sink.data_ptr(),
+                                             grid, stream.cuda_stream), "read probe")
+            for _ in range(warmup):
+                for l in range(L):
+                    launch(l)
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(steps * L)]
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(evs):
+                a.record(stream)
+                launch(i % L)
+                b.record(stream)
+            torch.cuda.synchronize()
+            us = sum(a.elapsed_time(b) for a, b in evs) * 1e3 / len(evs)
+            results.append({"pattern": name, "grid": grid, "us": round(us, 2),
+                            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)})
+            log(f"read probe {name} grid {grid}: {us:.2f} us per launch, {results[-1]['gbs']} GB/s")
+    best = max(results, key=lambda r: r["gbs"])
+    return {
+        "metric": "HBM read ceiling GB/s (one launch over one north-star layer's K/V)", "value": best["gbs"],
+        "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(best["us"] * L / 1e3, 4), "higher_is_better": True, "scaling": "strong",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "read ceiling: be_read_probe over 3072 pages x [2, 16, 8, 128] bf16 (201 MB) per launch",
+                   "layers": L, "bytes_per_launch": nbytes, "sweep": results},
+        "roofline": {"bound": "hbm", "achieved": best["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(best["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "read_probe_kernel",
+                     "bytes_per_launch": nbytes, "mean_launch_us": best["us"]},
+    }
+
+
 # ---------------------------------------------------------------------- CPU baseline
 def cpu_baseline_attention(wl, alg_bytes):
     """The CPU restatement (torch float32 paged gather, per-level softmax
@@ -306,6 +363,9 @@ def main():
         return 1
     if args.workload.startswith("topk"):
         print(json.dumps(topk_workload(args)), flush=True)
+        return 0
+    if args.workload == "read-ns":
+        print(json.dumps(read_ceiling_workload(args)), flush=True)
         return 0
     if args.workload == "attn-prefill":
         print(json.dumps(prefill_workload(args)), flush=True)

@@ -188,7 +188,8 @@ typedef struct be_plan_caps {
 /* Filled by be_attn_plan; passed back to be_attn_run unchanged. */
 typedef struct be_attn_plan_info {
   int32_t num_items;       /* work items (grid.x of the attention kernel)      */
-  int32_t num_part_rows;   /* partial rows, each [Hq, D] fp32 + [Hq] fp32 lse  */
+  int32_t num_part_rows;   /* partial rows: tile kernel [Hq, D] fp32 + [Hq] fp32 lse each;
+                              streaming kernel (slots) [g, D] in the KV's 16-bit type + [g] fp32 lse */
   int32_t num_merge;       /* queries merged by the merge kernel               */
   int32_t num_queries;
   int32_t num_qo_heads, num_kv_heads, head_dim, page_size, num_pages, dtype;
@@ -296,12 +297,16 @@ int be_trie_cascade(const int32_t* parent, const int32_t* page, const int32_t* n
 /* Kernel costs (microseconds per layer, the whole GPU) and the edge model of
  * the tree decompositions: tile_nt[i] one 64-token tile of one KV head with
  * i + 1 16-row MFMA tiles filled, seg a segment start, slot a partial slot
- * and its merge, tail a 16-token tail chunk, fixed a step's launches; alpha,
- * beta, gamma FastTree's Cmm constants (metadata.py:12-17). */
+ * and its merge, tail a 16-token tail chunk, fixed a step's launches,
+ * tile_w128 / tile_w256 a tile of the wide segments a group of more than 64
+ * rows takes when it has at least 8 tiles and 64 x 256 tiles of 64 rows over
+ * its KV heads; alpha, beta, gamma FastTree's Cmm constants
+ * (metadata.py:12-17). */
 typedef struct be_tree_model {
   double tile_nt[4];
   double seg, slot, tail, fixed;
   double alpha, beta, gamma;
+  double tile_w128, tile_w256;   /* a 64-token tile of a 128 / 256-row wide segment, one KV head */
   int32_t num_qo_heads, num_kv_heads;
   int32_t edge_model;
   int32_t reserved;
@@ -450,7 +455,15 @@ int be_merge_states(const float* o_a, const float* lse_a, const float* o_b, cons
  *   out_score (double) [n_req * beam].  max_req_rows bounds the rows of any
  *   request (host-side pool capacity check).
  * All pointers are device pointers.  workspace must hold
- * be_beam_topk_workspace_bytes(n_rows, vocab, k) bytes. */
+ * be_beam_topk_workspace_bytes(n_rows, vocab, k) bytes; its contents need no
+ * initialisation (the call clears the per-request arrival counters at its
+ * start), and calls that share one workspace must be stream-ordered.
+ * Parity contract: the exponential sum is accumulated in float64 in a
+ * reduction order of this library's own; L = fl32(ln S) then equals the
+ * float64 oracle's whenever ln S lies more than ~1e-13 (relative) from an
+ * fp32 rounding boundary -- torch's fp32 log_softmax agrees with this
+ * contract to about 4e-6, so a near-tie whose order the fp32 rounding of L
+ * decides may rank differently from the reference's GPU. */
 #define BE_TEMP_RECIPROCAL 0
 #define BE_TEMP_DIVIDE 1
 int64_t be_beam_topk_workspace_bytes(int n_rows, int vocab, int k);
@@ -476,6 +489,20 @@ int be_beam_topk_noalloc(const void* logits, int dtype, int n_rows, int vocab, i
                          int n_req, const int32_t* req_row_ptr, int max_req_rows, float* row_vals,
                          int32_t* row_idx, int32_t* out_parent, int32_t* out_token, double* out_score,
                          void* stream);
+
+/* ------------------------------------------------------------------ measurement
+ * be_read_probe: no counterpart in the reference -- the roofline measurement's
+ * read ceiling.  Reads rows of row_bytes (16 bytes times a power of two, at
+ * most 32 KiB) once with 16-byte loads, row r at base + (r % inner) * inner_stride + (r / inner) *
+ * outer_stride bytes, over grid workgroups of 256 threads, and writes one
+ * fold of the data per workgroup to sink[grid] (device uint32) so that no load
+ * is dead.  One KV head's rows of a layer [P, 2, page, Hkv, D] at a time:
+ * inner = P * 2 * page, inner_stride = Hkv * D * es, outer_stride = D * es,
+ * row_bytes = D * es; a contiguous read: inner = rows, inner_stride =
+ * row_bytes.  bench.py --workload read-ns times it over the north-star
+ * layer. */
+int be_read_probe(const void* base, int64_t rows, int64_t inner, int64_t inner_stride, int64_t outer_stride,
+                  int row_bytes, uint32_t* sink, int grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -408,3 +408,38 @@ def _path(node):
         out.append(node)
         node = node.parent
     return out[::-1]
+
+
+def test_native_costs_price_wide_segments_like_python():
+    """On a trie whose shared prompts are long enough for the planner's wide
+    segments (2 requests x 64 beams, GQA 8, 16384-token prompts), the native
+    option costs equal the Python picker's (wide pricing included)."""
+    from beam_engine_amd.picker import MI355X, StrategyPicker
+    rng_a, rng_b = random.Random(71), random.Random(71)
+    pa, pb = make_pt(8192, 16), make_pt(8192, 16)
+    a = BeamState(64, pa, fast_metadata=True)
+    b = NativeBeamState(64, pb)
+    for r in range(2):
+        a.add_root_sequence(list(range(16384)), request_id=r)
+        b.add_root_sequence(list(range(16384)), request_id=r)
+    first = [BeamToken(100 + j, -0.01 * j) for j in range(64)]
+    a.add_filtered_results([BeamGenerateResult(c, first) for c in a.candidates])
+    b.add_filtered_results([BeamGenerateResult(c, first) for c in b.candidates])
+    for _ in range(20):
+        a.add_filtered_results(random_results(a, rng_a, 64))
+        b.add_filtered_results(random_results(b, rng_b, 64))
+    picker = StrategyPicker(64, 8, 16, MI355X)
+    plan = picker.choose(a)
+    got = b.step_levels("auto", False, picker.tree_model())
+    assert got[5] == plan.kind and list(got[6]) == [plan.costs["flat"], plan.costs["split"], plan.costs["tree"]]
+    segs, _ = a.segment_tree()
+    root = max(segs, key=lambda sg: sg[1])
+    assert picker.model.group(len(root[3]), root[1]) < 0.9 * CostModelNoWide(picker).group(len(root[3]), root[1])
+
+
+def CostModelNoWide(picker):
+    """The same costs with the wide segments priced as 64-row ones."""
+    from dataclasses import replace
+    from beam_engine_amd.picker import CostModel
+    c = picker.model.c
+    return CostModel(64, 8, 16, replace(c, tile_w128=c.tile_nt[3] * 2, tile_w256=c.tile_nt[3] * 4))

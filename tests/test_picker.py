@@ -143,6 +143,16 @@ def test_cost_model_prices_tail_stream_and_rows():
     assert m.group(16, 64) == 8 * (4.0 + 10.0)                # 64 rows: a full segment
     assert m.group(20, 64) == 8 * (4.0 + 10.0 + 1.0 + 10.0)   # 80 rows: 64 + 16
     assert CostModel(32, 8, 8, c).group(2, 40) == 8 * (1.0 + 10.0)   # page 8: no tail pass
+    # wide segments: more than 64 rows, at least 8 tiles, and 64 x 256 tiles of
+    # 64 rows over the KV heads (the planner's 128- / 256-row tasks)
+    cw = KernelCosts(tile_nt=(1.0, 2.0, 3.0, 4.0), seg=10.0, slot=0.5, tail=0.25, fixed=0.0, tile_w128=6.0,
+                     tile_w256=9.0)
+    m8 = CostModel(64, 8, 16, cw)
+    assert m8.group(64, 16384) == 8 * (256 * 9.0 + 10.0) * 2        # 512 rows: two 256-row segments
+    assert m8.group(40, 16384 * 2) == 8 * (512 * 9.0 + 10.0 + 512 * 9.0 + 10.0)   # 320 rows: 256 + 64
+    assert m8.group(24, 16384 * 3) == 8 * (768 * 6.0 + 10.0) * 2    # 192 rows: two 128-row segments
+    assert m8.group(64, 8192) == 8 * (128 * 4.0 + 10.0) * 8         # 8 x 128 x 8 tiles64: below the bar
+    assert CostModel(32, 8, 16, cw).group(16, 1 << 20) == 8 * ((1 << 14) * 4.0 + 10.0)   # 64 rows: never wide
     # absorbing a short parent into a single child saves a pass and a slot
     assert m.absorb(1, 1, 16, 16)
     # a long parent shared by many queries stays a separate pass
@@ -159,7 +169,8 @@ def test_picker_prefers_shared_passes_for_a_shared_prefix_and_flat_without_shari
     plan = pk.choose(st)
     assert plan.kind in ("split", "tree")
     costs = pk.costs(st)
-    assert costs["flat"] > 2 * min(costs["split"], costs["tree"])
+    fixed = pk.model.c.fixed                  # both launches: paid by every option
+    assert costs["flat"] - fixed > 2 * (min(costs["split"], costs["tree"]) - fixed)
     assert plan.cost == min(costs.values()) and plan.costs == costs
     # one candidate per request: nothing is shared, every decomposition is one pass per query
     st2 = BeamState(1, RecordingPages(20000, page))
