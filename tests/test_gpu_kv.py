@@ -62,25 +62,32 @@ def test_append_skips_out_of_range_entries():
     assert torch.all(kv[1, :, 0] == 1) and torch.count_nonzero(kv) == 2 * 2 * 64
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_batched_page_copy_all_layers(dtype):
-    say(f"page copy {dtype}")
+@pytest.mark.parametrize("dtype,page,heads,dim", [(torch.float32, 8, 2, 64), (torch.bfloat16, 8, 2, 64),
+                                                   (torch.bfloat16, 16, 8, 256), (torch.float32, 16, 8, 128)])
+def test_batched_page_copy_all_layers(dtype, page, heads, dim):
+    """Batched fork copies over every layer; the larger shapes give page planes
+    of 64 KB, more than one batch of loads per workgroup."""
+    say(f"page copy {dtype} page={page} heads={heads} dim={dim}")
     from beam_engine_amd import PageTable
-    pt = PageTable(4, page_size=8, max_num_pages=32, head_num=2, head_dim=64, device="cuda", store_dtype=dtype)
+    pt = PageTable(4, page_size=page, max_num_pages=32, head_num=heads, head_dim=dim, device="cuda",
+                   store_dtype=dtype)
     g = torch.Generator().manual_seed(2)
     pt.kv_pool.copy_(torch.randn(pt.kv_pool.shape, generator=g).to(dtype))
     for _ in range(10):
         pt.allocate_block()
     before = pt.kv_pool.clone()
+    n1, n2 = 5, page - 1
     with pt.defer_copies():
-        a = pt.copy_block(3, 5)
-        b = pt.copy_block(7, 8)
+        a = pt.copy_block(3, n1)
+        b = pt.copy_block(7, page)
         c = pt.copy_block(3, 0)
-    assert (a, b, c) == (10, 11, 12)
+        e = pt.copy_block(9, n2)
+    assert (a, b, c, e) == (10, 11, 12, 13)
     torch.cuda.synchronize()
     ref = before.clone()
-    ref[:, a, :, :5] = before[:, 3, :, :5]
-    ref[:, b, :, :8] = before[:, 7, :, :8]
+    ref[:, a, :, :n1] = before[:, 3, :, :n1]
+    ref[:, b, :, :page] = before[:, 7, :, :page]
+    ref[:, e, :, :n2] = before[:, 9, :, :n2]
     assert torch.equal(pt.kv_pool, ref)
 
 
@@ -174,9 +181,12 @@ def test_fork_trace_moves_page_contents():
         assert list(pt.free_pages) == step.get("expect_free_list", list(pt.free_pages))
 
 
-def test_rope_append_matches_eager_tensor_code():
-    """be_rope_qkv_append is bit-identical to the eager HF-style RoPE + append."""
-    say("rope append vs eager")
+@pytest.mark.parametrize("pad", [0, 4])
+def test_rope_append_matches_eager_tensor_code(pad):
+    """be_rope_qkv_append is bit-identical to the eager HF-style RoPE + append,
+    on a contiguous projection (pad 0) and on a row view 8 bytes past a 16-byte
+    boundary with a row stride of 4 mod 8 elements (pad 4)."""
+    say(f"rope append vs eager pad={pad}")
     from beam_engine_amd import PageTable
     from beam_engine_amd.llama import LlamaConfig, LlamaDecoder
     cfg = LlamaConfig(num_hidden_layers=1, hidden_size=256, num_attention_heads=8, num_key_value_heads=2,
@@ -184,7 +194,8 @@ def test_rope_append_matches_eager_tensor_code():
     m = LlamaDecoder(cfg, "cuda", torch.bfloat16, seed=1)
     g = torch.Generator().manual_seed(5)
     n = 37
-    qkv = (torch.randn((n, (8 + 4) * 128), generator=g) * 2).to(torch.bfloat16).cuda()
+    full = (torch.randn((n, (8 + 4) * 128 + pad), generator=g) * 2).to(torch.bfloat16).cuda()
+    qkv = full[:, pad:]
     pos = torch.randint(0, 2048, (n,), generator=g).cuda()
     pages = torch.randperm(64, generator=g)[:n].to(torch.int32).cuda()
     slots = torch.randint(0, 16, (n,), generator=g, dtype=torch.int32).cuda()
