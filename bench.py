@@ -70,6 +70,23 @@ def log(msg):
 
 
 # ---------------------------------------------------------------------- attention
+def attention_traffic(name, args):
+    """HBM bytes per launch measured by rocprofv3 counter runs of the same
+    workload (profiles/attn_traffic.json, cascade plans with default options),
+    or (None, None)."""
+    if args.strategy != "cascade" or args.plan_opts or args.plan_cus or args.fused_merge or args.row_blocks != "auto":
+        return None, None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "attn_traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f).get(f"attn-{name}:cascade")
+    except (OSError, ValueError):
+        return None, None
+    if not entry:
+        return None, None
+    return int(entry["traffic_bytes_per_launch"]), entry["source"]
+
+
 def attention_workload(args):
     import torch
     from beam_engine_amd import BatchDecodeWithPagedKVCacheWrapper, MultiLevelCascadeAttentionWrapper
@@ -140,8 +157,9 @@ def attention_workload(args):
     layer_us = statistics.median([a.elapsed_time(b) * 1e3 / L for a, b in loop])
     gbs = alg / (mean_us * 1e-6) / 1e9
     tflops = st.flops / (mean_us * 1e-6) / 1e12
+    traffic, traffic_src = attention_traffic(wl.name, args)
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
             "kernel": f"attn_{st.kernel}_kernel" + ("" if st.num_merge == 0 or args.fused_merge else
                                                     " + tail_merge_kernel" if st.kernel == "stream" else " + merge_kernel"),
             "bytes_per_launch": alg, "mean_launch_us": round(mean_us, 2), "median_launch_us": round(med_us, 2),
