@@ -90,7 +90,13 @@ constexpr int kWideMinTiles = 8;              // 128-row tasks for groups of at 
 constexpr int kWideMinRun = 64;               // ... when the launch has this many 64-row tiles per workgroup
 constexpr int kWideTileCost = 6;              // planner cost of a 128-row tile (a 64-row tile is 4)
 constexpr int kWide256Rows = 256;             // rows per segment of the 256-row wide tasks
-constexpr int kWide256TileCost = 10;          // planner cost of a 256-row tile
+// planner cost of a 256-row tile.  Such a tile's step is bound by MFMA and
+// LDS, not by its bytes: beside 64-row and shorter segments in one launch
+// (config 5's long suffixes) it runs at about 1.5x, not 2.5x, a 16-row tile's
+// time on MI355X, and the 2.5x weight left those workgroups finishing 80 us
+// after the wide ones (286.8 -> 240.7 us per launch, 238-244 over four suffix
+// seeds, with 6)
+constexpr int kWide256TileCost = 6;
 
 struct StreamSeg {
   int32_t q_begin;     // first query

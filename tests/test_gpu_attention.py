@@ -411,9 +411,14 @@ def test_stream_wide_roles(ws, case, cus):
     torch.testing.assert_close(out.float(), out2.float(), rtol=2e-2, atol=1e-2)
     if w256:
         (out3, lse3), w3 = run_cascade(ws, q, kv, levels, page, num_cus=cus, no_wide256=True)
-        i3 = w3._info
-        wg3 = w3._plan_dev[i3.off_wg: i3.off_wg + 4 * i3.num_wg].view(-1, 4).cpu()
-        assert (wg3[:, 3] == 5).any() and not (wg3[:, 3] == 6).any()
+        if w3.stats.kernel == "stream":
+            i3 = w3._info
+            wg3 = w3._plan_dev[i3.off_wg: i3.off_wg + 4 * i3.num_wg].view(-1, 4).cpu()
+            assert (wg3[:, 3] == 5).any() and not (wg3[:, 3] == 6).any()
+        else:
+            # 128-row segments need more of them per workgroup than 256-row ones:
+            # on 4 CUs that plan can exceed the table where the 256-row plan fits
+            assert cus is not None and cus <= 4
         torch.testing.assert_close(out.float(), out3.float(), rtol=2e-2, atol=1e-2)
 
 
