@@ -46,14 +46,14 @@ WIDE_MIN_TILES64 = 64 * 256   # ... when the group alone has 64 tiles of 64 rows
 @dataclass(frozen=True)
 class KernelCosts:
     """Machine time (us per layer, the whole GPU) of one unit of work."""
-    tile_nt: Tuple[float, float, float, float] = (0.005513, 0.006248, 0.006062, 0.006575)
+    tile_nt: Tuple[float, float, float, float] = (0.005547, 0.006147, 0.005959, 0.006624)
     """one 64-token tile of one KV head, by 16-row MFMA tiles filled (1, 2, 3, 4)"""
-    seg: float = 0.007044           # a segment start (Q rows, epilogue) of one KV head
+    seg: float = 0.007042           # a segment start (Q rows, epilogue) of one KV head
     slot: float = 0.0               # a partial slot of one (query, KV head) and its merge (the fit finds it free)
-    tail: float = 0.001332          # a 16-token tail chunk of one (query, KV head)
-    fixed: float = 12.584           # both launches, prologue and the merge of a step
-    tile_w128: float = 0.007958     # one 64-token tile of a 128-row wide segment, one KV head
-    tile_w256: float = 0.014145     # one 64-token tile of a 256-row wide segment, one KV head
+    tail: float = 0.001355          # a 16-token tail chunk of one (query, KV head)
+    fixed: float = 12.925           # both launches, prologue and the merge of a step
+    tile_w128: float = 0.007982     # one 64-token tile of a 128-row wide segment, one KV head
+    tile_w256: float = 0.01313      # one 64-token tile of a 256-row wide segment, one KV head
 
 
 MI355X = KernelCosts()
