@@ -73,6 +73,7 @@ constexpr int kLdsStages = kRegStages * kStageBytes;   // the smaller of the two
 constexpr int kClassGeneric = 1;              // workgroup-table class: per-segment mode (else the mode 0 or 2)
 constexpr int kClassWide = 5;                 // workgroup-table class of the wide roles (32 rows per wave)
 constexpr int kClassWide256 = 6;              // ... of the 256-row wide roles (32 rows x all tokens per wave)
+constexpr int kClassWide256Dma = 7;           // ... the same through the direct-load loop (BE_PLAN_NO_REGS)
 constexpr int kNoCausalS = 0x3fffffff;        // segment causal base of a segment without the mask
 constexpr int kWaves = 8;                     // 2 per SIMD; each head_dim half gets 4
 constexpr int kThreads = 64 * kWaves;
@@ -153,6 +154,36 @@ struct SegReg {
 __device__ __forceinline__ SegReg seg_reg(const StreamSeg& x) {
   return SegReg{rfl(x.q_begin), rfl(x.q_count), rfl(x.page_begin), rfl(x.tok_begin),
                 rfl(x.tok_count), rfl(x.head),   rfl(x.out_slot),   rfl(x.n_tiles)};
+}
+
+// The end of a wide role's 16-row tile: lane holds O^T[d = 16 mt + 4 lg + i]
+// [row] of segment row `row` (< rows), normalised by l, with m in the log2
+// domain; to the final output or the segment's partial slot.
+template <typename T>
+__device__ __forceinline__ void wide_store(const StreamArgs& a, const SegReg& sg, int row, int lg, float m, float l,
+                                           const v4f (&o)[8]) {
+  const int g = a.g;
+  const int j = row / g, hh = row - j * g, head = sg.head * g + hh;
+  const int qi = sg.q_begin + j;
+  const float inv = (l > 0.f) ? 1.f / l : 0.f;
+  const float lse = (l > 0.f) ? (m + log2f(l)) * 0.69314718055994531f : -INFINITY;
+  const int d0 = 4 * lg;
+  if (sg.out_slot < 0) {
+    T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh + d0;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+      __builtin_nontemporal_store(pack4<T>(o[mt][0] * inv, o[mt][1] * inv, o[mt][2] * inv, o[mt][3] * inv),
+                                  reinterpret_cast<v4s*>(op + mt * 16));
+    if (lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
+  } else {
+    const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
+    T* op = reinterpret_cast<T*>(a.part_o) + slot * kD + d0;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+      store_wt(reinterpret_cast<v4s*>(op + mt * 16),
+               pack4<T>(o[mt][0] * inv, o[mt][1] * inv, o[mt][2] * inv, o[mt][3] * inv));
+    if (lg == 0) store_wt(a.part_lse + slot, lse);
+  }
 }
 
 // Online softmax of one (query, KV head) over its tail chunks c = first,
@@ -584,34 +615,10 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
         }
       }
       if (tp == 0 && act) {
-        // lane holds O^T[d = 16 mt + 4 lg + i][row = 32 rg + 16 r + lc]
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int row = 32 * rg + 16 * r + lc;
-          if (row < R) {
-            const int j = row / g, hh = row - j * g, head = sg.head * g + hh;
-            const int qi = sg.q_begin + j;
-            const float inv = (l[r] > 0.f) ? 1.f / l[r] : 0.f;
-            const float lse = (l[r] > 0.f) ? (m2[r] + log2f(l[r])) * 0.69314718055994531f : -INFINITY;
-            const int d0 = 4 * lg;
-            if (sg.out_slot < 0) {
-              T* op = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_sn + (int64_t)head * a.o_sh + d0;
-#pragma unroll
-              for (int mt = 0; mt < 8; ++mt)
-                __builtin_nontemporal_store(pack4<T>(o2[r][mt][0] * inv, o2[r][mt][1] * inv, o2[r][mt][2] * inv,
-                                                     o2[r][mt][3] * inv),
-                                            reinterpret_cast<v4s*>(op + mt * 16));
-              if (lg == 0 && a.out_lse) __builtin_nontemporal_store(lse, a.out_lse + (int64_t)qi * a.hq + head);
-            } else {
-              const int64_t slot = (int64_t)(sg.out_slot + j) * g + hh;
-              T* op = reinterpret_cast<T*>(a.part_o) + slot * kD + d0;
-#pragma unroll
-              for (int mt = 0; mt < 8; ++mt)
-                store_wt(reinterpret_cast<v4s*>(op + mt * 16),
-                         pack4<T>(o2[r][mt][0] * inv, o2[r][mt][1] * inv, o2[r][mt][2] * inv, o2[r][mt][3] * inv));
-              if (lg == 0) store_wt(a.part_lse + slot, lse);
-            }
-          }
+          if (row < R) wide_store<T>(a, sg, row, lg, m2[r], l[r], o2[r]);
         }
         // row tile 2 rg always has a stored row (32 rg < R): its 8 stores are
         // certain; the second tile's and the lse stores are not counted, which
@@ -627,9 +634,17 @@ __device__ __forceinline__ void stream_body_dma(const StreamArgs& a, unsigned ch
 }
 
 // The loop of one workgroup over its segments' tiles (the planner's choice
-// for workgroups of at least kRegsMinTiles tiles).  FM >= 0: every segment of
-// the workgroup takes wave-role mode FM (the planner marks such workgroups),
-// so the per-tile mode dispatch folds away; FM < 0: mode per segment.
+// for workgroups of at least kRegsMinTiles tiles, and for the 256-row wide
+// roles).  FM >= 0: every segment of the workgroup takes wave-role mode FM
+// (the planner marks such workgroups), so the per-tile mode dispatch folds
+// away; FM < 0: mode per segment; FM == kClassWide256: the 256-row wide
+// roles (wave w takes rows 32 w .. +31 over every token of a tile; the
+// segment's Q rows go global -> registers on its first tile).  The 256-row
+// step reads each 32 KB tile 8 times from LDS; beside it, direct
+// global -> LDS loads slowed the step by about a third on MI355X, loads into
+// registers stored by ds_write by about a tenth (the step with LDS-resident
+// tiles: 2.0 us per tile alone, 2.7-2.9 with direct loads, 2.2 through
+// registers).
 //
 // K, V and Q rows travel global memory -> registers -> LDS.  Two register
 // sets hold tiles n + 1 and n + 2 in flight while tile n is computed from one
@@ -641,6 +656,7 @@ template <typename T, int FM>
 __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned char* st_lds, StreamSeg* seg_lds,
                                                  const int* vis_lds, float* ml_lds, int n_segs, int n_tiles) {
   typedef int v4i __attribute__((ext_vector_type(4)));
+  constexpr bool W256 = FM == kClassWide256;
   const int tid = threadIdx.x;
   const int w = rfl(tid >> 6);                        // wave index (uniform)
   const int lane = tid & 63, lg = lane >> 4, lc = lane & 15;
@@ -731,9 +747,10 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
       r.k[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(kb + off[i]));
       r.v[i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(kb + off[i] + plane * 2));
     }
+    r.nq = 0;
+    if constexpr (!W256) {
     const int R = sg.q_count * g;
     const int nblk = (live && l_t == 0) ? (R + 3) >> 2 : 0;   // 1 KB blocks of 4 rows due with this tile
-    r.nq = 0;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int k = w + kWaves * j;
@@ -746,6 +763,7 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
       r.q[j] = *reinterpret_cast<const v4i*>(reinterpret_cast<const T*>(a.q) + qoff);
       if (k < nblk) r.nq = j + 1;
     }
+    }
     if (live) advance(l_s, l_t, l_sg);
   };
   // store a tile's registers into stage st (lane l's 16 bytes at block + 16 l)
@@ -756,9 +774,11 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
       *reinterpret_cast<v4i*>(stage + (2 * w + i) * 1024 + lane * 16) = r.k[i];
       *reinterpret_cast<v4i*>(stage + kKvBytes + (2 * w + i) * 1024 + lane * 16) = r.v[i];
     }
+    if constexpr (!W256) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      if (j < r.nq) *reinterpret_cast<v4i*>(stage + 2 * kKvBytes + (w + kWaves * j) * 1024 + lane * 16) = r.q[j];
+      for (int j = 0; j < 2; ++j)
+        if (j < r.nq) *reinterpret_cast<v4i*>(stage + 2 * kKvBytes + (w + kWaves * j) * 1024 + lane * 16) = r.q[j];
+    }
   };
 
   // ---- prologue: tiles 0 and 1 into A and B, tile 0 stored, tile 2 into A
@@ -772,10 +792,53 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
   float m_run = -INFINITY, l_run = 0.f;
   v4f o_acc[8];
   v8s qf[4];
+  float m2[2] = {-INFINITY, -INFINITY};               // 256-row wide roles: two 16-row tiles per wave
+  v4f lw[2], o2[2][8];
+  v8s qf2[2][4];
 
   // iteration n: compute n, store tile n + 1 (set nx), reload nx with tile n + 3
   auto iteration = [&](int n, Regs& nx) {
     const int page = (n + 3 < n_tiles) ? page_id() : 0;
+
+    if constexpr (W256) {
+      const SegReg& sg = c_sg;
+      const int R = sg.q_count * g;
+      const bool act = 32 * w < R;
+      const unsigned char* stage = st_lds + (n & 1) * kStageBytes;
+      if (c_t == 0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          m2[r] = -INFINITY;
+          lw[r] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt) o2[r][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+        if (act) {
+          // rows past the segment's last re-read it (their results are never stored)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = min(32 * w + 16 * r + lc, R - 1);
+            const int j = row / g, hh = row - j * g;
+            const T* src = reinterpret_cast<const T*>(a.q) + (int64_t)(sg.q_begin + j) * a.q_sn +
+                           (int64_t)(sg.head * g + hh) * a.q_sh;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qf2[r][ks] = *reinterpret_cast<const v8s*>(src + 8 * (4 * ks + lg));
+          }
+        }
+      }
+      if (act) {
+        const int valid = min(kTok, sg.tok_count - c_t * kTok);
+        tile_compute_w64<T>(stage, stage + kKvBytes, qf2, koff, voff8, valid, lg, scale, m2, lw, o2);
+        if (c_t == sg.n_tiles - 1) {
+          // every lane's l is the whole row's (row sums from the MFMA pipe)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = 32 * w + 16 * r + lc;
+            if (row < R) wide_store<T>(a, sg, row, lg, m2[r], lw[r][0], o2[r]);
+          }
+        }
+      }
+    } else {
 
     // ---- compute tile n.  Wave roles by the segment's row tiles (NT):
     //   NT >= 3: row tile w & 3, token half w >> 2, all head_dim        (mode 0)
@@ -890,6 +953,7 @@ __device__ __forceinline__ void stream_body_regs(const StreamArgs& a, unsigned c
         }
       }
     }
+    }
     advance(c_s, c_t, c_sg);
     if (n + 1 < n_tiles) store(nx, (n + 1) & 1);
     load(nx, n + 3 < n_tiles, page);
@@ -980,6 +1044,8 @@ __global__ __launch_bounds__(kThreads) void attn_stream_kernel(StreamArgs a) {
       else if (cls == 2) stream_body_dma<T, 2>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
       else if (cls == kClassWide) stream_body_dma<T, kClassWide>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
       else if (cls == kClassWide256)
+        stream_body_regs<T, kClassWide256>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
+      else if (cls == kClassWide256Dma)
         stream_body_dma<T, kClassWide256>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
       else stream_body_dma<T, -1>(a, st_lds, seg_lds, vis_lds, ml_lds, n_segs, n_tiles);
     }
@@ -1411,7 +1477,8 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       const int md = nt >= 3 ? 0 : nt == 2 ? 1 : sgm.n_tiles >= kQuarterTiles ? 2 : 3;
       cls = cls == -2 ? md : cls == md ? cls : -1;
     }
-    wg[b].w = big ? (wide256 ? kClassWide256 : kClassWide) : (cls == 0 || cls == 2) ? cls : kClassGeneric;
+    wg[b].w = big ? (wide256 ? ((flags & BE_PLAN_NO_REGS) ? kClassWide256Dma : kClassWide256) : kClassWide)
+                  : (cls == 0 || cls == 2) ? cls : kClassGeneric;
     any_wide = any_wide || big;
   }
 

@@ -158,7 +158,8 @@ typedef struct be_level {
                                     workgroups of the persistent kernel rather than in the
                                     merge kernel                                            */
 #define BE_PLAN_NO_REGS 32       /* streaming kernel: the direct-load loop whatever the runs'
-                                    lengths (no register-staged loop)                       */
+                                    lengths and roles (no register-staged loop; the 256-row
+                                    wide roles otherwise stage through registers)           */
 #define BE_PLAN_NO_WIDE 64       /* streaming kernel: no wide wave roles (32 rows per wave)
                                     and no 128-row segments for long many-query groups      */
 #define BE_PLAN_CAUSAL 128       /* causal groups on the last level: query q0 + i of a group

@@ -244,8 +244,9 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             assert s0 == istart and tiles == 0
             istart += ns
             continue
-        # wave-role mode 0 / 2, per segment (1), wide roles over up to 128 (5) or 256 rows (6)
-        assert cls in (0, 1, 2, 5, 6)
+        # wave-role mode 0 / 2, per segment (1), wide roles over up to 128 (5) or 256 rows (6;
+        # 7: the same through the direct-load loop)
+        assert cls in (0, 1, 2, 5, 6, 7)
         if ns:
             assert s0 == start
             assert tiles == segs[s0:s0 + ns, 7].sum()
@@ -253,7 +254,7 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
             rows = segs[s0:s0 + ns, 1] * g
             if cls == 5:
                 assert (rows > 64).any() and (rows <= 128).all()
-            elif cls == 6:
+            elif cls in (6, 7):
                 assert (rows > 64).any() and (rows <= 256).all()
             else:
                 assert (rows <= 64).all()

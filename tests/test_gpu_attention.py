@@ -420,6 +420,13 @@ def test_stream_wide_roles(ws, case, cus):
             # on 4 CUs that plan can exceed the table where the 256-row plan fits
             assert cus is not None and cus <= 4
         torch.testing.assert_close(out.float(), out3.float(), rtol=2e-2, atol=1e-2)
+        # the 256-row roles through the direct-load loop (class 7) instead of registers
+        (out4, lse4), w4 = run_cascade(ws, q, kv, levels, page, num_cus=cus, no_regs=True)
+        i4 = w4._info
+        wg4 = w4._plan_dev[i4.off_wg: i4.off_wg + 4 * i4.num_wg].view(-1, 4).cpu()
+        assert (wg4[:, 3] == 7).any() and not (wg4[:, 3] == 6).any()
+        check(out4, lse4, ref_o, ref_lse, torch.bfloat16)
+        torch.testing.assert_close(out.float(), out4.float(), rtol=2e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
