@@ -1342,7 +1342,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   }
   const int q_tile_w = std::max(1, (wide256 ? kWide256Rows : kWideRows) / g);
   const int wide_cost = wide256 ? kWide256TileCost : kWideTileCost;
-  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc, vis0; };
+  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc, vis0, grp; bool wide; };
   std::vector<Task> tasks;
   int64_t total = 0;
   bool any_causal = false;
@@ -1361,7 +1361,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       if (kv <= 0) continue;                        // the tile's queries see nothing: zero records
       const int tiles = (int)ceil_div(kv, kTok);
       for (int h = 0; h < hkv; ++h) {
-        tasks.push_back(Task{qa, qn, gr.page_base, kv, h, tiles, tc, vis0});
+        tasks.push_back(Task{qa, qn, gr.page_base, kv, h, tiles, tc, vis0, (int)gi, w128});
         total += tc * (int64_t)tiles + kSegCost;
       }
     }
@@ -1389,77 +1389,180 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   }
   const int W_s = W - W_t;                              // streaming workgroups: [0, W_s)
 
-  // ---- balanced contiguous runs over the streaming workgroups.  Costs: 4 per
-  // tile, kSegCost per segment start.  When workgroup b opens, its share is the
-  // remaining cost (tiles, task starts, and one split per remaining workgroup
-  // boundary) over the remaining workgroups; a tile joins b unless it would
-  // overshoot that share by more than half its cost.
+  // ---- balanced contiguous runs.  A run's share is, when it opens, the
+  // remaining cost (tiles, task starts, and one split per remaining run
+  // boundary) over the remaining runs; a tile joins the run unless it would
+  // overshoot that share by more than half its cost.  balance() walks the
+  // tasks of `list` in order, each costing mult x (tc per tile + kSegCost per
+  // segment start), over n_runs runs, calling piece(run, list entry, first
+  // tile, tiles, new segment) for every piece; segs_of(run) is the run's
+  // segment count so far (at most kMaxSegs).
   std::vector<StreamSeg> segs;
   std::vector<int4> wg(W, int4{0, 0, 0, 0});
-  std::vector<int64_t> suffix(tasks.size() + 1, 0);     // cost of tasks[i..] as whole segments
-  for (size_t i = tasks.size(); i-- > 0;)
-    suffix[i] = suffix[i + 1] + tasks[i].tc * (int64_t)tasks[i].tiles + kSegCost;
-  {
+  auto balance = [&](const std::vector<int>& list, int n_runs, int mult, auto&& piece, auto&& segs_of) -> bool {
+    std::vector<int64_t> suffix(list.size() + 1, 0);
+    for (size_t i = list.size(); i-- > 0;)
+      suffix[i] = suffix[i + 1] + mult * (tasks[list[i]].tc * (int64_t)tasks[list[i]].tiles + kSegCost);
+    const int64_t sc = (int64_t)mult * kSegCost;
     int b = 0;
     int64_t used = 0, share = 0;
-    auto open_wg = [&](size_t ti, int tile) {
-      const int64_t rem = suffix[ti + 1] + tasks[ti].tc * (int64_t)(tasks[ti].tiles - tile) + kSegCost +
-                          (int64_t)(W_s - 1 - b) * kSegCost;
-      share = ceil_div(rem, W_s - b);
+    auto open_run = [&](size_t li, int tile) {
+      const Task& t = tasks[list[li]];
+      const int64_t rem = suffix[li + 1] + mult * (t.tc * (int64_t)(t.tiles - tile)) + sc + (int64_t)(n_runs - 1 - b) * sc;
+      share = ceil_div(rem, n_runs - b);
       used = 0;
     };
     bool first = true;
-    for (size_t ti = 0; ti < tasks.size(); ++ti) {
-      const Task& t = tasks[ti];
-      bool open = false;                 // a segment of this task is open in workgroup b
+    for (size_t li = 0; li < list.size(); ++li) {
+      const Task& t = tasks[list[li]];
+      const int64_t tc = (int64_t)mult * t.tc;
+      bool open = false;                 // a segment of this task is open in run b
       for (int tile = 0; tile < t.tiles;) {
         if (first) {
-          open_wg(ti, tile);
+          open_run(li, tile);
           first = false;
         }
         for (;;) {
-          const int64_t c = t.tc + (open ? 0 : kSegCost);
-          const bool room = used + c / 2 <= share && (open || wg[b].y < kMaxSegs);
-          if (room || b == W_s - 1) break;
+          const int64_t c = tc + (open ? 0 : sc);
+          const bool room = used + c / 2 <= share && (open || segs_of(b) < kMaxSegs);
+          if (room || b == n_runs - 1) break;
           ++b;
           open = false;
-          open_wg(ti, tile);
+          open_run(li, tile);
         }
-        if (!open) {
-          if (wg[b].y >= kMaxSegs) return BE_ERR_UNSUPPORTED;
-          if (wg[b].y == 0) wg[b].x = (int)segs.size();
-          StreamSeg sgm;
-          sgm.q_begin = t.q0;
-          sgm.q_count = t.qn;
-          sgm.page_begin = t.page_base;
-          sgm.tok_begin = tile * kTok;
-          sgm.tok_count = 0;
-          sgm.head = t.head;
-          sgm.out_slot = -1;
-          sgm.n_tiles = 0;
-          segs.push_back(sgm);
-          seg_vis.push_back(t.vis0);
-          wg[b].y += 1;
-          used += kSegCost;
+        const bool fresh = !open;
+        if (fresh) {
+          if (segs_of(b) >= kMaxSegs) return false;
+          used += sc;
           open = true;
         }
         // this tile joins, and with it every following tile of the task that
         // passes the same test (tile j more joins while used + (j - 1) tc +
-        // tc / 2 <= share; the last workgroup takes all)
+        // tc / 2 <= share; the last run takes all)
         int take = t.tiles - tile;
-        if (b != W_s - 1) {
-          const int64_t slack = share - (used + t.tc) - t.tc / 2;
-          const int64_t more = slack < 0 ? 0 : slack / t.tc + 1;
+        if (b != n_runs - 1) {
+          const int64_t slack = share - (used + tc) - tc / 2;
+          const int64_t more = slack < 0 ? 0 : slack / tc + 1;
           take = (int)std::min<int64_t>(take, 1 + more);
         }
-        StreamSeg& cur = segs.back();
-        cur.n_tiles += take;
-        cur.tok_count = std::min(t.kv_len - cur.tok_begin, cur.n_tiles * kTok);
-        wg[b].z += take;
-        used += (int64_t)take * t.tc;
+        piece(b, (int)li, tile, take, fresh);
+        used += (int64_t)take * tc;
         tile += take;
       }
     }
+    return true;
+  };
+  // one piece of task ti in workgroup b (b's segments are appended together)
+  auto put = [&](int b, int ti, int tile, int take, bool fresh) {
+    const Task& t = tasks[ti];
+    if (fresh) {
+      if (wg[b].y == 0) wg[b].x = (int)segs.size();
+      StreamSeg sgm;
+      sgm.q_begin = t.q0;
+      sgm.q_count = t.qn;
+      sgm.page_begin = t.page_base;
+      sgm.tok_begin = tile * kTok;
+      sgm.tok_count = 0;
+      sgm.head = t.head;
+      sgm.out_slot = -1;
+      sgm.n_tiles = 0;
+      segs.push_back(sgm);
+      seg_vis.push_back(t.vis0);
+      wg[b].y += 1;
+    }
+    StreamSeg& cur = segs.back();
+    cur.n_tiles += take;
+    cur.tok_count = std::min(t.kv_len - cur.tok_begin, cur.n_tiles * kTok);
+    wg[b].z += take;
+  };
+
+  // Sibling sets: the k query tiles of one wide group and KV head read the
+  // same K/V tiles.  With every wide group split into the same k >= 2 tiles,
+  // the sets are balanced as units over virtual runs, and virtual run v puts
+  // sibling s in workgroup (v / 8) 8 k + 8 s + v % 8: the k workgroups of a
+  // piece share an XCD (workgroups are dispatched to the 8 XCDs round-robin)
+  // and read each tile at about the same time, so one of them fetches it from
+  // HBM and the others find it in that XCD's L2 (config 5 with 1-token
+  // suffixes on MI355X: 181-187 us per launch with the siblings aligned, 197
+  // with them on different XCDs).  The other tasks fill the other workgroups.
+  std::vector<std::vector<int>> sets;               // task indices, sibling order
+  {
+    std::vector<int> set_of(groups.size() * (size_t)hkv, -1);
+    for (size_t ti = 0; ti < tasks.size(); ++ti) {
+      const Task& t = tasks[ti];
+      if (!t.wide) continue;
+      int& si = set_of[(size_t)t.grp * hkv + t.head];
+      if (si < 0) {
+        si = (int)sets.size();
+        sets.emplace_back();
+      }
+      sets[si].push_back((int)ti);
+    }
+  }
+  int k_sib = sets.empty() ? 0 : (int)sets[0].size();
+  for (const auto& st : sets)
+    if ((int)st.size() != k_sib) k_sib = 0;
+  const int v_max = k_sib >= 2 ? 8 * (W_s / (8 * k_sib)) : 0;
+  if (v_max > 0) {
+    std::vector<int> wide_list, narrow_list;
+    for (const auto& st : sets) wide_list.push_back(st[0]);
+    int64_t wide_sum = 0, narrow_sum = 0;
+    for (size_t ti = 0; ti < tasks.size(); ++ti) {
+      const int64_t c = tasks[ti].tc * (int64_t)tasks[ti].tiles + kSegCost;
+      if (tasks[ti].wide) wide_sum += c;
+      else {
+        narrow_sum += c;
+        narrow_list.push_back((int)ti);
+      }
+    }
+    // virtual runs: the split that best evens the two sides' cost per workgroup
+    int V = v_max;
+    if (!narrow_list.empty()) {
+      V = 1;
+      int64_t best = INT64_MAX;
+      for (int v = 1; v <= v_max && W_s - v * k_sib >= 1; ++v) {
+        const int64_t a = ceil_div(wide_sum, (int64_t)v * k_sib), c = ceil_div(narrow_sum, (int64_t)(W_s - v * k_sib));
+        if (std::max(a, c) < best) {
+          best = std::max(a, c);
+          V = v;
+        }
+      }
+    }
+    auto slot = [&](int v, int sib) { return (v / 8) * 8 * k_sib + 8 * sib + (v % 8); };
+    struct Piece { int set, tile, take; };
+    std::vector<std::vector<Piece>> vpieces(V);
+    const bool ok = balance(
+        wide_list, V, k_sib,
+        [&](int v, int li, int tile, int take, bool fresh) {
+          if (fresh) vpieces[v].push_back(Piece{li, tile, 0});
+          vpieces[v].back().take += take;
+        },
+        [&](int v) { return (int)vpieces[v].size(); });
+    if (!ok) return BE_ERR_UNSUPPORTED;
+    std::vector<char> taken(W_s, 0);
+    for (int v = 0; v < V; ++v)
+      for (int sib = 0; sib < k_sib; ++sib) {
+        const int b = slot(v, sib);
+        taken[b] = 1;
+        for (const Piece& pc : vpieces[v]) put(b, sets[pc.set][sib], pc.tile, pc.take, true);
+      }
+    std::vector<int> free_wg;
+    for (int b = 0; b < W_s; ++b)
+      if (!taken[b]) free_wg.push_back(b);
+    if (!narrow_list.empty()) {
+      const bool ok2 = balance(
+          narrow_list, (int)free_wg.size(), 1,
+          [&](int r, int li, int tile, int take, bool fresh) { put(free_wg[r], narrow_list[li], tile, take, fresh); },
+          [&](int r) { return wg[free_wg[r]].y; });
+      if (!ok2) return BE_ERR_UNSUPPORTED;
+    }
+  } else {
+    std::vector<int> all(tasks.size());
+    for (size_t ti = 0; ti < tasks.size(); ++ti) all[ti] = (int)ti;
+    const bool ok = balance(
+        all, W_s, 1, [&](int b, int li, int tile, int take, bool fresh) { put(b, li, tile, take, fresh); },
+        [&](int b) { return wg[b].y; });
+    if (!ok) return BE_ERR_UNSUPPORTED;
   }
 
   // ---- class per workgroup: the wave-role mode every segment of the

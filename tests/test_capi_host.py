@@ -230,14 +230,16 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
     g = hq // hkv
     items = decode_tail_items(info, buf)
     TAIL_ROLE = 8
-    # workgroup table: contiguous segment runs with their tile totals, then the tail-role
-    # workgroups' contiguous item runs
+    # workgroup table: segment runs with their tile totals that together partition the
+    # segment list (workgroups of sibling query tiles are placed 8 apart, so the runs need
+    # not follow the workgroup order), then the tail-role workgroups' contiguous item runs
     role = wg[:, 3] == TAIL_ROLE
     assert wg[~role, 1].sum() == info.num_items and wg[role, 1].sum() == info.num_tail_items
     if role.any():
         first = int(np.argmax(role))
         assert role[first:].all()                          # tail roles are the last workgroups
-    start = istart = 0
+    istart = 0
+    covered = np.zeros(len(segs), dtype=bool)
     seg_cls = np.full(len(segs), -1)
     for b, (s0, ns, tiles, cls) in enumerate(wg):
         if cls == TAIL_ROLE:
@@ -248,7 +250,8 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
         # 7: the same through the direct-load loop)
         assert cls in (0, 1, 2, 5, 6, 7)
         if ns:
-            assert s0 == start
+            assert not covered[s0:s0 + ns].any()
+            covered[s0:s0 + ns] = True
             assert tiles == segs[s0:s0 + ns, 7].sum()
             seg_cls[s0:s0 + ns] = cls
             rows = segs[s0:s0 + ns, 1] * g
@@ -258,7 +261,7 @@ def check_stream_plan(levels, nq, hq, hkv, page, info, buf):
                 assert (rows > 64).any() and (rows <= 256).all()
             else:
                 assert (rows <= 64).all()
-        start += ns
+    assert covered.all()
     # coverage: every (query, KV head) sees exactly its tokens (segments: whole tiles from a
     # 64-aligned start; tail chunks: up to 16 tokens of one page), page by page
     seen = [[Counter() for _ in range(hkv)] for _ in range(nq)]
@@ -396,6 +399,45 @@ def test_stream_plan_wide_roles(beams, cus):
         else:
             assert rows.max() > 64 and rows.max() <= 128 and (wg[:, 3] == 5).any() and not (wg[:, 3] == 6).any()
             assert info.stream_loop == 0
+
+
+@pytest.mark.parametrize("beams,cus", [(64, 256), (64, 64), (96, 256), (64, 20)])
+def test_stream_plan_pairs_sibling_query_tiles(beams, cus):
+    """A wide group split into several 256-row query tiles reads the same K/V
+    tiles once per query tile: the planner balances each (group, KV head) set
+    of sibling tiles as one unit and puts sibling s of virtual run v in
+    workgroup (v // 8) 8 k + 8 s + v % 8, so that the k workgroups of a piece
+    share an XCD and the same tile range.  Config-5-like shape: 2 requests,
+    GQA 8, a long prefix, 1..4-token suffixes (tail pass)."""
+    hq, hkv, page = 64, 8, 16
+    pre = 512                                   # 8192-token prefix per request
+    qo0, kvp0, kvi0, lpl0 = [0, beams, 2 * beams], [0, pre, 2 * pre], list(range(2 * pre)), [16, 16]
+    rng = np.random.default_rng(beams + cus)
+    suf = rng.integers(1, 5, size=2 * beams)
+    qo1 = list(range(2 * beams + 1))
+    kvp1 = list(range(2 * beams + 1))
+    kvi1 = list(range(2 * pre, 2 * pre + 2 * beams))
+    levels = [(qo0, kvp0, kvi0, lpl0), (qo1, kvp1, kvi1, [int(x) for x in suf])]
+    rc, info, buf, _lib, L = plan(levels, nq=2 * beams, hq=hq, hkv=hkv, page=page,
+                                  num_pages=2 * pre + 2 * beams, cus=cus)
+    assert rc == 0, L.be_last_error()
+    wg, segs, recs, rslots = check_stream_plan(levels, 2 * beams, hq, hkv, page, info, buf)
+    g = hq // hkv
+    k = -(-beams * g // 256)                    # 256-row query tiles per (request, KV head)
+    wide = np.flatnonzero(wg[:, 3] == 6)
+    if 8 * (cus // (8 * k)) == 0:               # fewer than 8 k workgroups: no pairing
+        return
+    assert len(wide) > 0 and len(wide) % k == 0
+    for b in wide:
+        sib = int(b) % (8 * k) // 8             # sibling index of workgroup b
+        group = [int(b) + 8 * (s - sib) for s in range(k)]
+        assert all(wg[x, 3] == 6 for x in group), (b, group)
+        runs = [segs[wg[x, 0]: wg[x, 0] + wg[x, 1]] for x in group]
+        for r in runs[1:]:
+            # same KV head, pages and tile ranges; different query tiles
+            assert len(r) == len(runs[0])
+            assert (r[:, [2, 3, 4, 5, 7]] == runs[0][:, [2, 3, 4, 5, 7]]).all()
+            assert (r[:, 0] != runs[0][:, 0]).all()
 
 
 def test_stream_plan_zero_records_for_keyless_queries():
