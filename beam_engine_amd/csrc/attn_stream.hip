@@ -1342,7 +1342,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   }
   const int q_tile_w = std::max(1, (wide256 ? kWide256Rows : kWideRows) / g);
   const int wide_cost = wide256 ? kWide256TileCost : kWideTileCost;
-  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc, vis0, grp; bool wide; };
+  struct Task { int q0, qn, page_base, kv_len, head, tiles, tc, vis0, grp; };
   std::vector<Task> tasks;
   int64_t total = 0;
   bool any_causal = false;
@@ -1361,7 +1361,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       if (kv <= 0) continue;                        // the tile's queries see nothing: zero records
       const int tiles = (int)ceil_div(kv, kTok);
       for (int h = 0; h < hkv; ++h) {
-        tasks.push_back(Task{qa, qn, gr.page_base, kv, h, tiles, tc, vis0, (int)gi, w128});
+        tasks.push_back(Task{qa, qn, gr.page_base, kv, h, tiles, tc, vis0, (int)gi});
         total += tc * (int64_t)tiles + kSegCost;
       }
     }
@@ -1476,9 +1476,9 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     wg[b].z += take;
   };
 
-  // Sibling sets: the k query tiles of one wide group and KV head read the
-  // same K/V tiles.  With every wide group split into the same k >= 2 tiles,
-  // the sets are balanced as units over virtual runs, and virtual run v puts
+  // Sibling sets: the k query tiles of one group and KV head read the same
+  // K/V tiles.  When every group split into several tiles has the same k, its
+  // sets are balanced as units over virtual runs, and virtual run v puts
   // sibling s in workgroup (v / 8) 8 k + 8 s + v % 8: the k workgroups of a
   // piece share an XCD (workgroups are dispatched to the 8 XCDs round-robin)
   // and read each tile at about the same time, so one of them fetches it from
@@ -1486,42 +1486,57 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // suffixes on MI355X: 181-187 us per launch with the siblings aligned, 197
   // with them on different XCDs).  The other tasks fill the other workgroups.
   std::vector<std::vector<int>> sets;               // task indices, sibling order
+  std::vector<char> in_set(tasks.size(), 0);
+  int k_sib = 0;
   {
+    std::vector<std::vector<int>> all;
     std::vector<int> set_of(groups.size() * (size_t)hkv, -1);
     for (size_t ti = 0; ti < tasks.size(); ++ti) {
       const Task& t = tasks[ti];
-      if (!t.wide) continue;
       int& si = set_of[(size_t)t.grp * hkv + t.head];
       if (si < 0) {
-        si = (int)sets.size();
-        sets.emplace_back();
+        si = (int)all.size();
+        all.emplace_back();
       }
-      sets[si].push_back((int)ti);
+      all[si].push_back((int)ti);
     }
+    for (auto& st : all) {
+      if (st.size() < 2) continue;
+      // siblings of a causal group see different token counts: not paired
+      bool same = true;
+      for (int ti : st) same = same && tasks[ti].tiles == tasks[st[0]].tiles && tasks[ti].vis0 == kNoCausalS;
+      if (!same) continue;
+      if (k_sib == 0) k_sib = (int)st.size();
+      if ((int)st.size() != k_sib) {
+        k_sib = -1;
+        break;
+      }
+      sets.push_back(st);
+    }
+    if (k_sib < 2) sets.clear();
+    for (const auto& st : sets)
+      for (int ti : st) in_set[ti] = 1;
   }
-  int k_sib = sets.empty() ? 0 : (int)sets[0].size();
-  for (const auto& st : sets)
-    if ((int)st.size() != k_sib) k_sib = 0;
   const int v_max = k_sib >= 2 ? 8 * (W_s / (8 * k_sib)) : 0;
   if (v_max > 0) {
-    std::vector<int> wide_list, narrow_list;
-    for (const auto& st : sets) wide_list.push_back(st[0]);
-    int64_t wide_sum = 0, narrow_sum = 0;
+    std::vector<int> set_list, rest_list;
+    for (const auto& st : sets) set_list.push_back(st[0]);
+    int64_t set_sum = 0, rest_sum = 0;
     for (size_t ti = 0; ti < tasks.size(); ++ti) {
       const int64_t c = tasks[ti].tc * (int64_t)tasks[ti].tiles + kSegCost;
-      if (tasks[ti].wide) wide_sum += c;
+      if (in_set[ti]) set_sum += c;
       else {
-        narrow_sum += c;
-        narrow_list.push_back((int)ti);
+        rest_sum += c;
+        rest_list.push_back((int)ti);
       }
     }
     // virtual runs: the split that best evens the two sides' cost per workgroup
     int V = v_max;
-    if (!narrow_list.empty()) {
+    if (!rest_list.empty()) {
       V = 1;
       int64_t best = INT64_MAX;
       for (int v = 1; v <= v_max && W_s - v * k_sib >= 1; ++v) {
-        const int64_t a = ceil_div(wide_sum, (int64_t)v * k_sib), c = ceil_div(narrow_sum, (int64_t)(W_s - v * k_sib));
+        const int64_t a = ceil_div(set_sum, (int64_t)v * k_sib), c = ceil_div(rest_sum, (int64_t)(W_s - v * k_sib));
         if (std::max(a, c) < best) {
           best = std::max(a, c);
           V = v;
@@ -1532,7 +1547,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     struct Piece { int set, tile, take; };
     std::vector<std::vector<Piece>> vpieces(V);
     const bool ok = balance(
-        wide_list, V, k_sib,
+        set_list, V, k_sib,
         [&](int v, int li, int tile, int take, bool fresh) {
           if (fresh) vpieces[v].push_back(Piece{li, tile, 0});
           vpieces[v].back().take += take;
@@ -1549,10 +1564,10 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     std::vector<int> free_wg;
     for (int b = 0; b < W_s; ++b)
       if (!taken[b]) free_wg.push_back(b);
-    if (!narrow_list.empty()) {
+    if (!rest_list.empty()) {
       const bool ok2 = balance(
-          narrow_list, (int)free_wg.size(), 1,
-          [&](int r, int li, int tile, int take, bool fresh) { put(free_wg[r], narrow_list[li], tile, take, fresh); },
+          rest_list, (int)free_wg.size(), 1,
+          [&](int r, int li, int tile, int take, bool fresh) { put(free_wg[r], rest_list[li], tile, take, fresh); },
           [&](int r) { return wg[free_wg[r]].y; });
       if (!ok2) return BE_ERR_UNSUPPORTED;
     }

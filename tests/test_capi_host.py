@@ -440,6 +440,39 @@ def test_stream_plan_pairs_sibling_query_tiles(beams, cus):
             assert (r[:, 0] != runs[0][:, 0]).all()
 
 
+@pytest.mark.parametrize("cus", [256, 24, 40])
+def test_stream_plan_pairs_narrow_sibling_tiles(cus):
+    """The same placement for a group cut into 64-row query tiles (config 3's
+    root: 32 beams x GQA 4 = 128 rows, two tiles) beside single-tile groups:
+    each root segment of query tile 1 lies in the workgroup 8 after its tile-0
+    twin (same KV head, tokens and tiles), and the single-tile groups fill the
+    other workgroups (on at least 17 workgroups: fewer give every workgroup
+    64 root tiles, and the root takes the 128-row wide roles instead)."""
+    hq, hkv, page, beams = 32, 8, 16, 32
+    root = 256                                  # 4096-token root
+    qo0, kvp0, kvi0 = [0, beams], [0, root], list(range(root))
+    # level 1: two branches of 16 beams, 8 pages each; level 2: 2-token leaves
+    qo1, kvp1 = [0, 16, 32], [0, 8, 16]
+    kvi1 = list(range(root, root + 16))
+    qo2 = list(range(beams + 1))
+    kvp2 = list(range(beams + 1))
+    kvi2 = list(range(root + 16, root + 16 + beams))
+    levels = [(qo0, kvp0, kvi0, [16]), (qo1, kvp1, kvi1, [16, 16]), (qo2, kvp2, kvi2, [2] * beams)]
+    rc, info, buf, _lib, L = plan(levels, nq=beams, hq=hq, hkv=hkv, page=page, num_pages=root + 16 + beams,
+                                  cus=cus, flags=8)
+    assert rc == 0, L.be_last_error()
+    wg, segs, recs, rslots = check_stream_plan(levels, beams, hq, hkv, page, info, buf)
+    seg_wg = np.empty(len(segs), dtype=np.int64)
+    for b, (s0, ns, tiles, cls) in enumerate(wg):
+        seg_wg[s0:s0 + ns] = b
+    rootseg = segs[:, 2] == 0                   # segments of the root group (page list from 0)
+    a = {(int(x[5]), int(x[3]), int(x[7])): int(seg_wg[i]) for i, x in enumerate(segs) if rootseg[i] and x[0] == 0}
+    b16 = {(int(x[5]), int(x[3]), int(x[7])): int(seg_wg[i]) for i, x in enumerate(segs) if rootseg[i] and x[0] == 16}
+    assert len(a) > 0 and a.keys() == b16.keys()
+    for key, b0 in a.items():
+        assert b16[key] == b0 + 8 and b0 % 16 < 8, (key, b0, b16[key])
+
+
 def test_stream_plan_zero_records_for_keyless_queries():
     levels = [([0, 1, 2], [0, 1, 2], [0, 1], [3, 0])]
     rc, info, buf, *_ = plan(levels, nq=3, page=16, num_pages=2)
