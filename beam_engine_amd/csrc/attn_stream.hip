@@ -98,6 +98,12 @@ constexpr int kWide256Rows = 256;             // rows per segment of the 256-row
 // after the wide ones (286.8 -> 240.7 us per launch, 238-244 over four suffix
 // seeds, with 6)
 constexpr int kWide256TileCost = 6;
+// planner cost of a 256-row segment start (a second segment in a workgroup:
+// its epilogue, the next segment's Q rows, the pipeline across the switch).
+// Measured on MI355X at config 5: such workgroups ended 9 us (about 3.4
+// 256-row tiles) after one-segment ones at the cost of 4; with 24, 1.5-2%
+// shorter launches over four suffix seeds (20 and 28 within 0.5%)
+constexpr int kWide256SegCost = 24;
 
 struct StreamSeg {
   int32_t q_begin;     // first query
@@ -1394,16 +1400,18 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // boundary) over the remaining runs; a tile joins the run unless it would
   // overshoot that share by more than half its cost.  balance() walks the
   // tasks of `list` in order, each costing mult x (tc per tile + kSegCost per
-  // segment start), over n_runs runs, calling piece(run, list entry, first
-  // tile, tiles, new segment) for every piece; segs_of(run) is the run's
-  // segment count so far (at most kMaxSegs).
+  // segment start; seg for the sibling sets of 256-row tasks), over n_runs
+  // runs, calling piece(run, list entry, first tile, tiles, new segment) for
+  // every piece; segs_of(run) is the run's segment count so far (at most
+  // kMaxSegs).
   std::vector<StreamSeg> segs;
   std::vector<int4> wg(W, int4{0, 0, 0, 0});
-  auto balance = [&](const std::vector<int>& list, int n_runs, int mult, auto&& piece, auto&& segs_of) -> bool {
+  auto balance = [&](const std::vector<int>& list, int n_runs, int mult, int seg, auto&& piece,
+                     auto&& segs_of) -> bool {
     std::vector<int64_t> suffix(list.size() + 1, 0);
     for (size_t i = list.size(); i-- > 0;)
-      suffix[i] = suffix[i + 1] + mult * (tasks[list[i]].tc * (int64_t)tasks[list[i]].tiles + kSegCost);
-    const int64_t sc = (int64_t)mult * kSegCost;
+      suffix[i] = suffix[i + 1] + mult * (tasks[list[i]].tc * (int64_t)tasks[list[i]].tiles + seg);
+    const int64_t sc = (int64_t)mult * seg;
     int b = 0;
     int64_t used = 0, share = 0;
     auto open_run = [&](size_t li, int tile) {
@@ -1522,9 +1530,10 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     std::vector<int> set_list, rest_list;
     for (const auto& st : sets) set_list.push_back(st[0]);
     int64_t set_sum = 0, rest_sum = 0;
+    const int set_seg = wide256 && tasks[set_list[0]].tc == kWide256TileCost ? kWide256SegCost : kSegCost;
     for (size_t ti = 0; ti < tasks.size(); ++ti) {
       const int64_t c = tasks[ti].tc * (int64_t)tasks[ti].tiles + kSegCost;
-      if (in_set[ti]) set_sum += c;
+      if (in_set[ti]) set_sum += c - kSegCost + set_seg;
       else {
         rest_sum += c;
         rest_list.push_back((int)ti);
@@ -1547,7 +1556,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     struct Piece { int set, tile, take; };
     std::vector<std::vector<Piece>> vpieces(V);
     const bool ok = balance(
-        set_list, V, k_sib,
+        set_list, V, k_sib, set_seg,
         [&](int v, int li, int tile, int take, bool fresh) {
           if (fresh) vpieces[v].push_back(Piece{li, tile, 0});
           vpieces[v].back().take += take;
@@ -1566,7 +1575,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
       if (!taken[b]) free_wg.push_back(b);
     if (!rest_list.empty()) {
       const bool ok2 = balance(
-          rest_list, (int)free_wg.size(), 1,
+          rest_list, (int)free_wg.size(), 1, kSegCost,
           [&](int r, int li, int tile, int take, bool fresh) { put(free_wg[r], rest_list[li], tile, take, fresh); },
           [&](int r) { return wg[free_wg[r]].y; });
       if (!ok2) return BE_ERR_UNSUPPORTED;
@@ -1575,7 +1584,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     std::vector<int> all(tasks.size());
     for (size_t ti = 0; ti < tasks.size(); ++ti) all[ti] = (int)ti;
     const bool ok = balance(
-        all, W_s, 1, [&](int b, int li, int tile, int take, bool fresh) { put(b, li, tile, take, fresh); },
+        all, W_s, 1, kSegCost, [&](int b, int li, int tile, int take, bool fresh) { put(b, li, tile, take, fresh); },
         [&](int b) { return wg[b].y; });
     if (!ok) return BE_ERR_UNSUPPORTED;
   }
