@@ -86,7 +86,7 @@ KIND_NAMES = {v: k for k, v in KIND_CODES.items()}
 class BeTreeModel(ctypes.Structure):
     _fields_ = [("tile_nt", ctypes.c_double * 4)] + [
         (n, ctypes.c_double) for n in ("seg", "slot", "tail", "fixed", "alpha", "beta", "gamma", "tile_w128",
-                                       "tile_w256")] + [
+                                       "tile_w256", "tile_sib")] + [
         (n, ctypes.c_int32) for n in ("num_qo_heads", "num_kv_heads", "edge_model", "reserved")]
 
 

@@ -181,10 +181,14 @@ struct Costs {
       }
       return cost * hkv;
     }
+    // a group's second and later 64-row query tiles read their K/V from the
+    // L2 the first one filled (the planner places them on one XCD)
+    bool first = true;
     while (rows > 0) {
       const int64_t r = std::min<int64_t>(rows, kSegRows);
-      cost += (double)tiles * m->tile_nt[std::min<int64_t>(4, (r + 15) / 16) - 1] + m->seg;
+      cost += (double)tiles * (first ? m->tile_nt[std::min<int64_t>(4, (r + 15) / 16) - 1] : m->tile_sib) + m->seg;
       rows -= r;
+      first = false;
     }
     return cost * hkv;
   }

@@ -46,14 +46,18 @@ WIDE_MIN_TILES64 = 64 * 256   # ... when the group alone has 64 tiles of 64 rows
 @dataclass(frozen=True)
 class KernelCosts:
     """Machine time (us per layer, the whole GPU) of one unit of work."""
-    tile_nt: Tuple[float, float, float, float] = (0.005547, 0.006147, 0.005959, 0.006624)
+    tile_nt: Tuple[float, float, float, float] = (0.005529, 0.006238, 0.006042, 0.006733)
     """one 64-token tile of one KV head, by 16-row MFMA tiles filled (1, 2, 3, 4)"""
-    seg: float = 0.007042           # a segment start (Q rows, epilogue) of one KV head
+    seg: float = 0.00772            # a segment start (Q rows, epilogue) of one KV head
     slot: float = 0.0               # a partial slot of one (query, KV head) and its merge (the fit finds it free)
-    tail: float = 0.001355          # a 16-token tail chunk of one (query, KV head)
-    fixed: float = 12.925           # both launches, prologue and the merge of a step
-    tile_w128: float = 0.007982     # one 64-token tile of a 128-row wide segment, one KV head
-    tile_w256: float = 0.01313      # one 64-token tile of a 256-row wide segment, one KV head
+    tail: float = 0.001361          # a 16-token tail chunk of one (query, KV head)
+    fixed: float = 12.81            # both launches, prologue and the merge of a step
+    tile_w128: float = 0.008359     # one 64-token tile of a 128-row wide segment, one KV head
+    tile_w256: float = 0.011972     # one 64-token tile of a 256-row wide segment, one KV head
+    tile_sib: float = 0.004888
+    """one 64-token tile of a group's second or later 64-row query tile, one KV head: the planner
+    places a group's query tiles of one KV head on one XCD at the same tile range, so their K/V
+    comes from the L2 the first tile's reads filled"""
 
 
 MI355X = KernelCosts()
@@ -96,10 +100,12 @@ class CostModel:
                 rows -= min(rows, wr)
                 cost += tiles * coef + c.seg
             return cost * self.hkv
+        first = True
         while rows > 0:
             r = min(rows, SEG_ROWS)
-            cost += tiles * c.tile_nt[min(4, math.ceil(r / 16)) - 1] + c.seg
+            cost += tiles * (c.tile_nt[min(4, math.ceil(r / 16)) - 1] if first else c.tile_sib) + c.seg
             rows -= r
+            first = False
         return cost * self.hkv
 
     def slots(self, nq: int) -> float:
@@ -224,7 +230,7 @@ class StrategyPicker:
         for i, v in enumerate(c.tile_nt):
             m.tile_nt[i] = v
         m.seg, m.slot, m.tail, m.fixed = c.seg, c.slot, c.tail, c.fixed
-        m.tile_w128, m.tile_w256 = c.tile_w128, c.tile_w256
+        m.tile_w128, m.tile_w256, m.tile_sib = c.tile_w128, c.tile_w256, c.tile_sib
         ft = self.edges if self.edges is not None else FastTreeCostModel(self.model.g * self.model.hkv, self.model.hkv)
         m.alpha, m.beta, m.gamma = ft.alpha, ft.beta, ft.gamma
         m.num_qo_heads, m.num_kv_heads = self.model.g * self.model.hkv, self.model.hkv

@@ -13,6 +13,7 @@ and solves a non-negative least-squares fit of
     us per layer = fixed + sum_nt tile_nt * tiles(nt) + seg * segments
                    + slot * extra passes + tail * tail chunks
                    + tile_w128 * wide tiles (128 rows) + tile_w256 * wide tiles (256 rows)
+                   + tile_sib * tiles of a group's second and later 64-row query tiles
 
 The features are the cost model's own counts (``picker.plan_cost`` under a
 unit cost per term), so the fit prices exactly what ``picker.CostModel``
@@ -39,7 +40,8 @@ import numpy as np
 from .picker import MI355X, CostModel, KernelCosts, StrategyPicker, plan_cost
 
 D, PAGE = 128, 16
-TERMS = ("fixed", "tile_nt0", "tile_nt1", "tile_nt2", "tile_nt3", "seg", "slot", "tail", "tile_w128", "tile_w256")
+TERMS = ("fixed", "tile_nt0", "tile_nt1", "tile_nt2", "tile_nt3", "seg", "slot", "tail", "tile_w128", "tile_w256",
+         "tile_sib")
 
 
 def levels_of(spec):
@@ -61,7 +63,8 @@ def levels_of(spec):
 
 
 def _unit(term: str) -> KernelCosts:
-    zero = dict(tile_nt=(0.0, 0.0, 0.0, 0.0), seg=0.0, slot=0.0, tail=0.0, fixed=0.0, tile_w128=0.0, tile_w256=0.0)
+    zero = dict(tile_nt=(0.0, 0.0, 0.0, 0.0), seg=0.0, slot=0.0, tail=0.0, fixed=0.0, tile_w128=0.0, tile_w256=0.0,
+                tile_sib=0.0)
     if term.startswith("tile_nt"):
         t = [0.0] * 4
         t[int(term[-1])] = 1.0
@@ -79,7 +82,7 @@ def features(levels, hq: int, hkv: int):
 def costs_of(coef) -> KernelCosts:
     c = [round(float(x), 6) for x in coef]
     return KernelCosts(tile_nt=tuple(c[1:5]), seg=c[5], slot=c[6], tail=c[7], fixed=round(float(coef[0]), 3),
-                       tile_w128=c[8], tile_w256=c[9])
+                       tile_w128=c[8], tile_w256=c[9], tile_sib=c[10])
 
 
 def sweep():
@@ -101,6 +104,11 @@ def sweep():
         for nq in (1, 2, 4):
             for tok in (16, 48, 64):
                 add(f"g{g}: 512 x ({nq}q, {tok}) tail", hq, [[(nq, tok)] * 512])
+        # groups of two and four 64-row query tiles (the siblings read their K/V from L2)
+        for nq in (128 // g, 256 // g):
+            for tok in (256, 1024, 4096):
+                n = max(4, min(512, int(4e6 // (tok * nq * 4))))
+                add(f"g{g}: {n} x ({nq}q, {tok})", hq, [[(nq, tok)] * n])
     for n, suf in ((64, 16), (64, 128), (128, 32)):
         add(f"g4: 8 x (16q, 1024) + {n} x (1q, {suf})", 32, [[(16, 1024)] * 8, [(1, suf)] * 128])
     add("g4: 8 x (16q, 1024) + 128 x (1q, 16) + 128 x (1q, 16)", 32,

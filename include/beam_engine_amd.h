@@ -308,6 +308,8 @@ typedef struct be_tree_model {
   double seg, slot, tail, fixed;
   double alpha, beta, gamma;
   double tile_w128, tile_w256;   /* a 64-token tile of a 128 / 256-row wide segment, one KV head */
+  double tile_sib;               /* a 64-token tile of a group's second or later 64-row query tile, one
+                                    KV head (its K/V comes from the L2 its first tile's reads filled) */
   int32_t num_qo_heads, num_kv_heads;
   int32_t edge_model;
   int32_t reserved;

@@ -133,7 +133,7 @@ def test_oracle_attention_of_tree_levels_equals_flat(seed):
 
 
 def test_cost_model_prices_tail_stream_and_rows():
-    c = KernelCosts(tile_nt=(1.0, 2.0, 3.0, 4.0), seg=10.0, slot=0.5, tail=0.25, fixed=0.0)
+    c = KernelCosts(tile_nt=(1.0, 2.0, 3.0, 4.0), seg=10.0, slot=0.5, tail=0.25, fixed=0.0, tile_sib=0.75)
     m = CostModel(32, 8, 16, c)
     assert m.group(0, 100) == 0 and m.group(3, 0) == 0
     assert m.group(2, 40) == 2 * 8 * 3 * 0.25                 # tail: 3 chunks x 2 queries x 8 heads
@@ -141,17 +141,19 @@ def test_cost_model_prices_tail_stream_and_rows():
     assert m.group(5, 65) == 8 * (2 * 2.0 + 10.0)             # 20 rows: two 16-row tiles, 2 tiles
     assert m.group(1, 129) == 8 * (3 * 1.0 + 10.0)            # 4 rows: one 16-row tile, 3 tiles
     assert m.group(16, 64) == 8 * (4.0 + 10.0)                # 64 rows: a full segment
-    assert m.group(20, 64) == 8 * (4.0 + 10.0 + 1.0 + 10.0)   # 80 rows: 64 + 16
+    assert m.group(20, 64) == 8 * (4.0 + 10.0 + 0.75 + 10.0)  # 80 rows: 64 + a 16-row sibling tile
+    assert m.group(64, 128) == 8 * (2 * 4.0 + 10.0 + 3 * (2 * 0.75 + 10.0))   # 256 rows: 1 + 3 siblings
     assert CostModel(32, 8, 8, c).group(2, 40) == 8 * (1.0 + 10.0)   # page 8: no tail pass
     # wide segments: more than 64 rows, at least 8 tiles, and 64 x 256 tiles of
     # 64 rows over the KV heads (the planner's 128- / 256-row tasks)
     cw = KernelCosts(tile_nt=(1.0, 2.0, 3.0, 4.0), seg=10.0, slot=0.5, tail=0.25, fixed=0.0, tile_w128=6.0,
-                     tile_w256=9.0)
+                     tile_w256=9.0, tile_sib=4.0)
     m8 = CostModel(64, 8, 16, cw)
     assert m8.group(64, 16384) == 8 * (256 * 9.0 + 10.0) * 2        # 512 rows: two 256-row segments
     assert m8.group(40, 16384 * 2) == 8 * (512 * 9.0 + 10.0 + 512 * 9.0 + 10.0)   # 320 rows: 256 + 64
     assert m8.group(24, 16384 * 3) == 8 * (768 * 6.0 + 10.0) * 2    # 192 rows: two 128-row segments
     assert m8.group(64, 8192) == 8 * (128 * 4.0 + 10.0) * 8         # 8 x 128 x 8 tiles64: below the bar
+                                                                    # (tile_sib = tile_nt[3] here)
     assert CostModel(32, 8, 16, cw).group(16, 1 << 20) == 8 * ((1 << 14) * 4.0 + 10.0)   # 64 rows: never wide
     # absorbing a short parent into a single child saves a pass and a slot
     assert m.absorb(1, 1, 16, 16)
