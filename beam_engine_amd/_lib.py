@@ -28,6 +28,7 @@ BE_PLAN_CAUSAL = 128
 BE_PLAN_ROWS = 256
 BE_PLAN_NO_ROWS = 512
 BE_PLAN_NO_WIDE256 = 1024
+BE_PLAN_NO_TAIL_ROLE = 2048
 BE_RUN_ATTENTION, BE_RUN_MERGE = 1, 2
 BE_TEMP_RECIPROCAL, BE_TEMP_DIVIDE = 0, 1
 

@@ -121,7 +121,8 @@ class _PagedPlanner:
         self._fused_merge = False
         self._tile_kernel = False     # force the per-(item, head) tile kernel over the streaming kernel
         self._no_tail = False         # streaming kernel: keep short groups in whole tiles, no tail chunks
-        self._tail_role = False       # streaming kernel: tail chunks in tail-role workgroups, not the merge kernel
+        self._tail_role = None        # streaming kernel: tail chunks in tail-role workgroups (True), in the merge
+                                      # kernel (False), or as the planner decides (None)
         self._no_regs = False         # streaming kernel: direct-load loop in every workgroup
         self._no_wide = False         # streaming kernel: no wide (32-row) wave roles, no 128-row segments
         self._no_wide256 = False      # streaming kernel: wide roles on 128-row segments only
@@ -174,9 +175,11 @@ class _PagedPlanner:
                                   max(max_page + 1, 1), dt, flags, self._num_cus or _num_cus(self._ws.device),
                                   ctypes.byref(self._caps) if self._caps is not None else None,
                                   buf.data_ptr(), buf.numel(), ctypes.byref(info))
-            if rc == _lib.BE_ERR_CAPACITY:
-                cap = 2 * buf.numel()
+            if rc == _lib.BE_ERR_CAPACITY and info.plan_ints > buf.numel():
+                cap = max(int(info.plan_ints), 2 * buf.numel())
                 continue
+            # (a capacity error with plan_ints 0 is a fixed layout's, which no
+            # buffer size cures: MemoryError)
             _lib.check(rc, "attention plan")
             break
         self._install_plan(info, buf, staging, max_page, head_dim, sm_scale, q_data_type)
@@ -186,7 +189,8 @@ class _PagedPlanner:
             (_lib.BE_PLAN_FUSED_MERGE if self._fused_merge else 0) | \
             (_lib.BE_PLAN_TILE_KERNEL if self._tile_kernel else 0) | \
             (_lib.BE_PLAN_NO_TAIL if self._no_tail else 0) | \
-            (_lib.BE_PLAN_TAIL_ROLE if self._tail_role else 0) | \
+            (_lib.BE_PLAN_TAIL_ROLE if self._tail_role is True else 0) | \
+            (_lib.BE_PLAN_NO_TAIL_ROLE if self._tail_role is False else 0) | \
             (_lib.BE_PLAN_NO_REGS if self._no_regs else 0) | \
             (_lib.BE_PLAN_NO_WIDE if self._no_wide else 0) | \
             (_lib.BE_PLAN_NO_WIDE256 if self._no_wide256 else 0) | \

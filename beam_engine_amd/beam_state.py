@@ -951,12 +951,12 @@ class NativeBeamState:
             if rc == _lib.BE_ERR_CAPACITY:
                 if int(self._meta_used.value) > meta.size:
                     self._meta_buf = np.zeros(2 * int(self._meta_used.value), np.int32)
-                elif host_plan is not None or buf.numel() >= (1 << 26):
-                    # a full caller buffer, or a plan beyond the fixed layout's
-                    # capacities (which no buffer size cures): MemoryError
-                    _lib.check(rc, f"{kind} plan")
+                elif host_plan is None and info.plan_ints > buf.numel():
+                    cap = max(int(info.plan_ints), 2 * buf.numel())
                 else:
-                    cap = 2 * buf.numel()
+                    # a full caller buffer, or a plan beyond the fixed layout's
+                    # capacities (plan_ints 0: no buffer size cures it): MemoryError
+                    _lib.check(rc, f"{kind} plan")
                 continue
             _lib.check(rc, f"{kind} plan")
             break

@@ -654,6 +654,7 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
               int page_size, int num_pages, int dtype, int flags, int num_cus, const be_plan_caps* caps,
               int32_t* out, int64_t cap, be_attn_plan_info* info) {
   BE_REQUIRE(info != nullptr && out != nullptr, "null plan buffer or info");
+  memset(info, 0, sizeof(*info));
   BE_REQUIRE(num_levels >= 0 && (num_levels == 0 || levels != nullptr), "bad levels");
   BE_REQUIRE(num_queries >= 0, "num_queries must be >= 0");
   BE_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "num_qo_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
@@ -909,7 +910,10 @@ int attn_plan(const be_level* levels, int num_levels, int num_queries, int hq, i
   const int64_t off_zq = off;       off += c_zero;
   const int64_t off_zp = off;       off += c_zero + 1;
   off = ceil_div(off, 4) * 4;
-  if (off > cap || off > INT32_MAX) return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  if (off > cap || off > INT32_MAX) {
+    info->plan_ints = (int32_t)std::min<int64_t>(off, INT32_MAX);   // the words needed (0: a capacity of caps)
+    return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  }
   for (int i = 0; i < kPlanHeader; ++i) out[i] = 0;
   out[kHdrItems] = (int32_t)n_items;
   out[kHdrMerge] = (int32_t)merge_q.size();

@@ -381,8 +381,11 @@ int rows_plan(const std::vector<Group>& groups, const be_level* levels, int num_
   const int64_t off_tasks = off;  off += n_tasks * kTaskWords;
   const int64_t off_passes = off; off += (int64_t)passes.size();
   const int64_t off_pages = off;  off += total_pages;
-  if (off > cap) return fail(BE_ERR_CAPACITY, "rows plan needs %lld int32 words, buffer holds %lld", (long long)off,
-                             (long long)cap);
+  if (off > cap) {
+    info->plan_ints = (int32_t)std::min<int64_t>(off, INT32_MAX);   // the words needed
+    return fail(BE_ERR_CAPACITY, "rows plan needs %lld int32 words, buffer holds %lld", (long long)off,
+                (long long)cap);
+  }
   memset(out, 0, kPlanHeader * sizeof(int32_t));
   out[kHdrItems] = (int32_t)n_tasks;
   for (int x = 0; x < kXcd; ++x)

@@ -85,6 +85,7 @@ constexpr int kTailChunks = 64;               // 16-token tail chunks per query 
 constexpr int kRecWords = 8;                  // int32 words per merge record (and per tail item)
 constexpr int kTailRole = 8;                  // workgroup-table class of a workgroup that runs tail items
 constexpr int kTailUnit = 1;                  // planner cost of one tail chunk of one KV head (a tile is 4)
+constexpr int kTailRoleChunks = 2;            // tail chunks per query up to which the tail role is the default
 constexpr int kItemChunks = 4;                // tail chunks per tail item (tail role and tail queue)
 constexpr int kWideRows = 128;               // rows per segment of a long group's wide-128 tasks
 constexpr int kWideMinTiles = 8;              // 128-row tasks for groups of at least this many tiles
@@ -1374,16 +1375,29 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   }
   std::vector<int32_t> seg_vis;                     // per segment: its task's vis0
 
-  // ---- roles: with BE_PLAN_TAIL_ROLE the tail chunks run in tail-role
-  // workgroups of this kernel (one wave per (query, KV head) item) while the
-  // other workgroups stream; the split follows the planner costs (4 per tile,
-  // kSegCost per segment start, kTailUnit per chunk of one KV head).  By
-  // default the merge kernel attends them: the streaming workgroups are
-  // bandwidth-bound on every CU, and a CU given to tail items costs them more
-  // than the overlap saves on the ns and e2e shapes (measured on MI355X).
-  int64_t tail_cost = 0;
-  for (int qi = 0; qi < num_queries; ++qi) tail_cost += (int64_t)n_tails_of(qi) * hkv * kTailUnit;
-  const bool tail_role = tail_cost > 0 && (flags & BE_PLAN_TAIL_ROLE) && (tasks.empty() || W >= 2);
+  // ---- roles: the tail chunks run either in tail-role workgroups of this
+  // kernel (one wave per (query, KV head) item) while the other workgroups
+  // stream -- the split following the planner costs (4 per tile, kSegCost per
+  // segment start, kTailUnit per chunk of one KV head) -- and the merge
+  // kernel then only merges, or in the merge kernel, fused with the merge.
+  // The launch shares HBM either way; what decides is the merge kernel.  With
+  // many chunks per query (long short-group suffixes) its tail pass streams
+  // them at the streaming kernel's rate and the tail role's extra merge-only
+  // pass costs more than the overlap saves (MI355X: north-star 48.4 vs 51.8
+  // us per launch, config 2 21.9 vs 22.7, 8 chunks per query); with few it is
+  // a latency-bound stub and the tail role wins (e2e step 24.95 vs 23.0, 1.5
+  // per query; config 5 205.3 vs 202.1, 1.2).  So by default: the tail role
+  // when a compact plan with streamed groups has at most kTailRoleChunks per
+  // query.  Fixed layouts keep the tail pass: their tail items' partial slots
+  // outgrew the step graph's layout and its re-captures cost the config-4
+  // decode 1.6% per step, against 0.7 us per attention launch saved.
+  // BE_PLAN_TAIL_ROLE forces the tail role, BE_PLAN_NO_TAIL_ROLE forbids it.
+  int64_t tail_cost = 0, tail_chunks = 0;
+  for (int qi = 0; qi < num_queries; ++qi) tail_chunks += n_tails_of(qi);
+  tail_cost = tail_chunks * hkv * kTailUnit;
+  const bool auto_tail = !caps && !tasks.empty() && !(flags & BE_PLAN_NO_TAIL_ROLE) &&
+                         tail_chunks <= (int64_t)kTailRoleChunks * num_queries;
+  const bool tail_role = tail_cost > 0 && ((flags & BE_PLAN_TAIL_ROLE) || auto_tail) && (tasks.empty() || W >= 2);
   int W_t = 0;
   if (tail_role) {
     if (tasks.empty()) {
@@ -1759,8 +1773,10 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   const int64_t off_items = off;  off += kRecWords * c_items;
   const int64_t off_causal = off; off += any_causal ? c_segs : 0;
   off = ceil_div(off, 4) * 4;
-  if (off > cap || off > INT32_MAX)
+  if (off > cap || off > INT32_MAX) {
+    info->plan_ints = (int32_t)std::min<int64_t>(off, INT32_MAX);   // the words needed (0: a capacity of caps)
     return fail(BE_ERR_CAPACITY, "plan needs %lld int32 words, buffer holds %lld", (long long)off, (long long)cap);
+  }
   if (any_causal && n_segs) memcpy(out + off_causal, seg_vis.data(), n_segs * sizeof(int32_t));
   for (int i = 0; i < kPlanHeader; ++i) out[i] = 0;
   out[kHdrItems] = (int32_t)n_segs;

@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--plan-cus", type=int, default=None,
                     help="attention workloads: plan for this many CUs (workgroups of the streaming kernel)")
     ap.add_argument("--plan-opts", default="",
-                    help="attention workloads: comma-separated planner switches (no_tail, tail_role, no_regs, "
+                    help="attention workloads: comma-separated planner switches (no_tail, tail_role, no_tail_role, no_regs, "
                          "no_wide, no_wide256, tile_kernel)")
     ap.add_argument("--row-blocks", default="auto", choices=["auto", "on", "off"],
                     help="attention: the row-block kernel (one launch, no partials) forced on or off")
@@ -111,9 +111,12 @@ def attention_workload(args):
         w._rows = {"auto": None, "on": True, "off": False}[args.row_blocks]
         w._num_cus = args.plan_cus
         for opt in filter(None, args.plan_opts.split(",")):
-            if opt not in ("no_tail", "tail_role", "no_regs", "no_wide", "no_wide256", "tile_kernel"):
+            if opt not in ("no_tail", "tail_role", "no_tail_role", "no_regs", "no_wide", "no_wide256", "tile_kernel"):
                 raise SystemExit(f"unknown --plan-opts entry {opt!r}")
-            setattr(w, "_" + opt, True)
+            if opt == "no_tail_role":
+                w._tail_role = False
+            else:
+                setattr(w, "_" + opt, True)
         return w
     if args.strategy == "cascade":
         w = tune(MultiLevelCascadeAttentionWrapper(len(wl.levels[0]), ws))
