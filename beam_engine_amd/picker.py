@@ -46,15 +46,15 @@ WIDE_MIN_TILES64 = 64 * 256   # ... when the group alone has 64 tiles of 64 rows
 @dataclass(frozen=True)
 class KernelCosts:
     """Machine time (us per layer, the whole GPU) of one unit of work."""
-    tile_nt: Tuple[float, float, float, float] = (0.005529, 0.006238, 0.006042, 0.006733)
+    tile_nt: Tuple[float, float, float, float] = (0.005492, 0.006099, 0.005898, 0.006712)
     """one 64-token tile of one KV head, by 16-row MFMA tiles filled (1, 2, 3, 4)"""
-    seg: float = 0.00772            # a segment start (Q rows, epilogue) of one KV head
+    seg: float = 0.007525           # a segment start (Q rows, epilogue) of one KV head
     slot: float = 0.0               # a partial slot of one (query, KV head) and its merge (the fit finds it free)
-    tail: float = 0.001361          # a 16-token tail chunk of one (query, KV head)
-    fixed: float = 12.81            # both launches, prologue and the merge of a step
-    tile_w128: float = 0.008359     # one 64-token tile of a 128-row wide segment, one KV head
-    tile_w256: float = 0.011972     # one 64-token tile of a 256-row wide segment, one KV head
-    tile_sib: float = 0.004888
+    tail: float = 0.001363          # a 16-token tail chunk of one (query, KV head)
+    fixed: float = 12.914           # both launches, prologue and the merge of a step
+    tile_w128: float = 0.008329     # one 64-token tile of a 128-row wide segment, one KV head
+    tile_w256: float = 0.011948     # one 64-token tile of a 256-row wide segment, one KV head
+    tile_sib: float = 0.004881
     """one 64-token tile of a group's second or later 64-row query tile, one KV head: the planner
     places a group's query tiles of one KV head on one XCD at the same tile range, so their K/V
     comes from the L2 the first tile's reads filled"""
