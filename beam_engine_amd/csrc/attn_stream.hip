@@ -1386,16 +1386,14 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // pass costs more than the overlap saves (MI355X: north-star 48.4 vs 51.8
   // us per launch, config 2 21.9 vs 22.7, 8 chunks per query); with few it is
   // a latency-bound stub and the tail role wins (e2e step 24.95 vs 23.0, 1.5
-  // per query; config 5 205.3 vs 202.1, 1.2).  So by default: the tail role
-  // when a compact plan with streamed groups has at most kTailRoleChunks per
-  // query.  Fixed layouts keep the tail pass: their tail items' partial slots
-  // outgrew the step graph's layout and its re-captures cost the config-4
-  // decode 1.6% per step, against 0.7 us per attention launch saved.
-  // BE_PLAN_TAIL_ROLE forces the tail role, BE_PLAN_NO_TAIL_ROLE forbids it.
+  // per query; config 5 205.3 vs 202.1, 1.2; in a fixed layout the e2e step
+  // 25.1 vs 23.3).  So by default: the tail role when a plan with streamed
+  // groups has at most kTailRoleChunks per query.  BE_PLAN_TAIL_ROLE forces
+  // it, BE_PLAN_NO_TAIL_ROLE forbids it.
   int64_t tail_cost = 0, tail_chunks = 0;
   for (int qi = 0; qi < num_queries; ++qi) tail_chunks += n_tails_of(qi);
   tail_cost = tail_chunks * hkv * kTailUnit;
-  const bool auto_tail = !caps && !tasks.empty() && !(flags & BE_PLAN_NO_TAIL_ROLE) &&
+  const bool auto_tail = !tasks.empty() && !(flags & BE_PLAN_NO_TAIL_ROLE) &&
                          tail_chunks <= (int64_t)kTailRoleChunks * num_queries;
   const bool tail_role = tail_cost > 0 && ((flags & BE_PLAN_TAIL_ROLE) || auto_tail) && (tasks.empty() || W >= 2);
   int W_t = 0;
@@ -1749,7 +1747,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   const int64_t n_segs = (int64_t)segs.size();
   if (caps) {
     if (n_segs > caps->max_items || total_pages > caps->max_pages || n_recs > caps->max_merge ||
-        n_slots > caps->max_merge_rows || n_tails > caps->max_tails || n_items > caps->max_merge)
+        n_slots > caps->max_merge_rows || n_tails > caps->max_tails || n_items > caps->max_tails)
       return fail(BE_ERR_CAPACITY,
                   "plan exceeds its fixed capacities: segments %lld/%d pages %lld/%d records %lld/%d slots %d/%d "
                   "tail chunks %lld/%d",
@@ -1769,7 +1767,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   const int64_t off_rslots = off; off += c_slots;
   off = ceil_div(off, 2) * 2;
   const int64_t off_tails = off;  off += 2 * c_tails;
-  const int64_t c_items = caps ? (int64_t)caps->max_merge : n_items;
+  const int64_t c_items = caps ? (int64_t)caps->max_tails : n_items;   // an item holds >= 1 tail chunk
   const int64_t off_items = off;  off += kRecWords * c_items;
   const int64_t off_causal = off; off += any_causal ? c_segs : 0;
   off = ceil_div(off, 4) * 4;

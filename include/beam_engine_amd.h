@@ -157,8 +157,7 @@ typedef struct be_level {
 #define BE_PLAN_TAIL_ROLE 16     /* streaming kernel: attend tail chunks in tail-role
                                     workgroups of the persistent kernel rather than in the
                                     merge kernel, whatever their count (by default: when a
-                                    compact plan with streamed groups has at most 2 per
-                                    query; fixed layouts keep them in the merge kernel)    */
+                                    plan with streamed groups has at most 2 per query)      */
 #define BE_PLAN_NO_REGS 32       /* streaming kernel: the direct-load loop whatever the runs'
                                     lengths and roles (no register-staged loop; the 256-row
                                     wide roles otherwise stage through registers)           */
@@ -186,7 +185,7 @@ typedef struct be_level {
 typedef struct be_plan_caps {
   int32_t max_items, max_queries, max_pages, max_merge, max_merge_rows, max_zero;
   int32_t tile_rows;       /* fixed rows per workgroup tile: 16, 32, 64 or 128 */
-  int32_t max_tails;       /* streaming kernel: tail chunk entries              */
+  int32_t max_tails;       /* streaming kernel: tail chunk entries (and tail-role items) */
 } be_plan_caps;
 
 /* Filled by be_attn_plan; passed back to be_attn_run unchanged. */
