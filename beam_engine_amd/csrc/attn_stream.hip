@@ -1505,6 +1505,14 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // HBM and the others find it in that XCD's L2 (config 5 with 1-token
   // suffixes on MI355X: 181-187 us per launch with the siblings aligned, 197
   // with them on different XCDs).  The other tasks fill the other workgroups.
+  // Runs that are not sibling sets take the workgroups XCD by XCD (0, 8, 16,
+  // ..., then 1, 9, ...): consecutive runs, which hold the pieces of one split
+  // task, then share an XCD, and the pieces after the first find the task's
+  // query rows in that XCD's L2.
+  std::vector<int> xcd_order;
+  xcd_order.reserve(W_s);
+  for (int x = 0; x < 8; ++x)
+    for (int b = x; b < W_s; b += 8) xcd_order.push_back(b);
   std::vector<std::vector<int>> sets;               // task indices, sibling order
   std::vector<char> in_set(tasks.size(), 0);
   int k_sib = 0;
@@ -1583,7 +1591,7 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
         for (const Piece& pc : vpieces[v]) put(b, sets[pc.set][sib], pc.tile, pc.take, true);
       }
     std::vector<int> free_wg;
-    for (int b = 0; b < W_s; ++b)
+    for (int b : xcd_order)
       if (!taken[b]) free_wg.push_back(b);
     if (!rest_list.empty()) {
       const bool ok2 = balance(
@@ -1596,8 +1604,9 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
     std::vector<int> all(tasks.size());
     for (size_t ti = 0; ti < tasks.size(); ++ti) all[ti] = (int)ti;
     const bool ok = balance(
-        all, W_s, 1, kSegCost, [&](int b, int li, int tile, int take, bool fresh) { put(b, li, tile, take, fresh); },
-        [&](int b) { return wg[b].y; });
+        all, W_s, 1, kSegCost,
+        [&](int r, int li, int tile, int take, bool fresh) { put(xcd_order[r], li, tile, take, fresh); },
+        [&](int r) { return wg[xcd_order[r]].y; });
     if (!ok) return BE_ERR_UNSUPPORTED;
   }
 
