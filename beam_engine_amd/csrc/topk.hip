@@ -1130,7 +1130,8 @@ constexpr int kUnitWavesPerSimd = 4;
 constexpr int kRowThreads = 1024;      // pass B workgroup
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kRowCandPer = kFusedRowCand / kRowThreads;
-constexpr int kPoolSurv = 32;           // pool entries ranked exactly after the sample bound
+constexpr int kPoolSurv = 64;           // pool entries ranked pairwise (16 threads each) after the sample bound
+static_assert(kPoolSurv * 16 == kRowThreads, "pairwise pool ranks: 16 threads per entry");
 static_assert(kFusedReqs <= kTopkCounterWords, "topk_counter_bytes reserves one counter per request");
 static_assert(kFusedRowCand % kRowThreads == 0, "row candidates are spread evenly over the threads");
 static_assert(kFusedPool <= kRowThreads, "one pool entry per pass-B thread");
@@ -1471,13 +1472,19 @@ struct RowLds {
   int32_t sidx[kMaxK];
 };
 
-// Inclusive sums within each 32-lane half of a wave (DPP; lane 31 and lane 63
-// end with their half's total).
-__device__ __forceinline__ int half_wave_scan_add(int x) {
+// Inclusive sums within each 16-lane DPP row of a wave (lanes 15, 31, 47 and
+// 63 end with their row's total).
+__device__ __forceinline__ int row16_scan_add(int x) {
   x += (int)dpp<0x111, 0xf, true>(0, x);
   x += (int)dpp<0x112, 0xf, true>(0, x);
   x += (int)dpp<0x114, 0xf, true>(0, x);
   x += (int)dpp<0x118, 0xf, true>(0, x);
+  return x;
+}
+// Inclusive sums within each 32-lane half of a wave (DPP; lane 31 and lane 63
+// end with their half's total).
+__device__ __forceinline__ int half_wave_scan_add(int x) {
+  x = row16_scan_add(x);
   x += (int)dpp<0x142, 0xa, false>(0, x);
   return x;
 }
@@ -1587,21 +1594,34 @@ __device__ void fused_pool(const FusedTopkArgs& a, int rb, int re, int q, RowLds
   // each row's first ns entries.  Every entry of the top beam is at or before
   // it (beam sampled entries are), so only those -- per row a prefix -- need
   // exact ranks, and their ranks among themselves are their ranks in the pool.
-  const int ns = nr <= kPoolSurv ? min(jb, kPoolSurv / nr) : 0;
+  // (ns a power of two, so that a sample's pool position is a shift and a mask)
+  const int ns_max = nr <= kPoolSurv ? min(jb, kPoolSurv / nr) : 0;
+  const int lns = ns_max > 0 ? 31 - __builtin_clz(ns_max) : 0;
+  const int ns = ns_max > 0 ? 1 << lns : 0;
   const int nsamp = nr * ns;
+  auto samp_pos = [&](int i) { return (i >> lns) * jb + (i & (ns - 1)); };
   int S = kPoolSurv + 1;                               // survivors; above kPoolSurv: rank every entry
   if (nsamp >= beam) {
     {
-      const int i = tid >> 5, jj = tid & 31;
-      const int pi = i < nsamp ? (i / ns) * jb + i % ns : 0;
+      // sample i = tid >> 4 against samples (tid & 15) + 16 u, summed over the
+      // 16 lanes of its DPP row
+      const int i = tid >> 4, j0 = tid & 15;
+      const int pi = i < nsamp ? samp_pos(i) : 0;
       int c = 0;
-      if (i < nsamp && jj < nsamp) {
-        const int pj = (jj / ns) * jb + jj % ns;
-        const double ti = sm.ptot[pi], tj = sm.ptot[pj];
-        c = (tj > ti || (tj == ti && pj < pi)) ? 1 : 0;
+      if (i < nsamp) {
+        const double ti = sm.ptot[pi];
+#pragma unroll
+        for (int u = 0; u < kPoolSurv / 16; ++u) {
+          const int jj = j0 + 16 * u;
+          if (jj < nsamp) {
+            const int pj = samp_pos(jj);
+            const double tj = sm.ptot[pj];
+            c += (tj > ti || (tj == ti && pj < pi)) ? 1 : 0;
+          }
+        }
       }
-      c = half_wave_scan_add(c);
-      if (jj == 31 && i < nsamp && c == beam - 1) {
+      c = row16_scan_add(c);
+      if (j0 == 15 && i < nsamp && c == beam - 1) {
         sm.pt = sm.ptot[pi];
         sm.ppos = pi;
       }
@@ -1632,17 +1652,24 @@ __device__ void fused_pool(const FusedTopkArgs& a, int rb, int re, int q, RowLds
     S = sm.nsurv;
   }
   if (S <= kPoolSurv) {
-    // the survivors' ranks: thread t compares survivor t >> 5 with survivor t & 31
-    const int i = tid >> 5, jj = tid & 31;
+    // the survivors' ranks: survivor t >> 4 against survivors (t & 15) + 16 u
+    const int i = tid >> 4, j0 = tid & 15;
     const int pi = i < S ? sm.surv[i] : 0;
     int c = 0;
-    if (i < S && jj < S) {
-      const int pj = sm.surv[jj];
-      const double ti = sm.ptot[pi], tj = sm.ptot[pj];
-      c = (tj > ti || (tj == ti && pj < pi)) ? 1 : 0;
+    if (i < S) {
+      const double ti = sm.ptot[pi];
+#pragma unroll
+      for (int u = 0; u < kPoolSurv / 16; ++u) {
+        const int jj = j0 + 16 * u;
+        if (jj < S) {
+          const int pj = sm.surv[jj];
+          const double tj = sm.ptot[pj];
+          c += (tj > ti || (tj == ti && pj < pi)) ? 1 : 0;
+        }
+      }
     }
-    c = half_wave_scan_add(c);
-    if (jj == 31 && i < S && c < beam) atomicAdd(&sm.sel[pi / jb], 1);
+    c = row16_scan_add(c);
+    if (j0 == 15 && i < S && c < beam) atomicAdd(&sm.sel[pi / jb], 1);
   } else {
     // every entry's rank: P adjacent threads share an entry, each taking every
     // P-th row, and add their counts
