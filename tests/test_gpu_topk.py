@@ -138,7 +138,8 @@ def test_batched_requests_in_one_call():
 
 
 @pytest.mark.parametrize("case", ["strided_best", "chunk_best", "constant", "two_levels", "near_ties_bf16",
-                                  "few_finite", "large_magnitude", "mixed_offsets_f16"])
+                                  "few_finite", "large_magnitude", "mixed_offsets_f16", "tiny_values_bf16",
+                                  "zero_runs_bf16"])
 def test_segment_select_paths(case):
     """Logits that stress the per-segment selection: the best values all in
     one thread's stride (a single thread maximum among them), constant rows
@@ -176,6 +177,23 @@ def test_segment_select_paths(case):
         x[0] *= 400.0                            # maxima far above 300
         x[1] -= 900.0                            # every value far below -300
         x[2] = x[2] * 3.0 + 310.0
+        logits = x.to(torch.bfloat16)
+    elif case == "tiny_values_bf16":
+        # zeros and values below 2^-22 in magnitude scattered among N(0, 1): the
+        # waves holding them sum against their own max, beside waves with a larger one
+        x = torch.randn((4, v), generator=g)
+        pos = torch.randperm(v, generator=g)[:300]
+        x[:, pos[:100]] = 0.0
+        x[:, pos[100:200]] = 3.0e-8
+        x[:, pos[200:]] = -1.0e-9
+        x[1, :2048] = 0.0                        # whole waves of zeros
+        logits = x.to(torch.bfloat16)
+    elif case == "zero_runs_bf16":
+        x = torch.zeros((3, v))
+        x[:, torch.randperm(v, generator=g)[:40]] = 1.0
+        x[1] = torch.randn(v, generator=g) * 0.25
+        x[1, 50000:90000] = 0.0
+        x[2, :8016] = -2.0
         logits = x.to(torch.bfloat16)
     elif case == "mixed_offsets_f16":
         x = torch.randn((3, v), generator=g) * 2.0
