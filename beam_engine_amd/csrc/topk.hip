@@ -36,7 +36,6 @@
 #include <mutex>
 
 #include "common.h"
-#include "topk_exp_tables.h"
 
 namespace be {
 
@@ -1269,50 +1268,6 @@ __device__ __forceinline__ double exp_sum0(SegVals<T>& x, const double* tab, dou
   return acc;
 }
 
-// acc + the float64 sum of e^x' over words [W0, W1) of a thread's bf16 logits
-// (no temperature: x' is the bf16 value itself), against 0, from two factor
-// tables in LDS: x = (-1)^s 2^(E-127) (1 + m/128) splits exactly into
-// 2^(E-127) (1 + mh/8) and 2^(E-127) ml/128 (mh, ml: the mantissa's top 3 and
-// low 4 bits), so e^x = ta[r][mh] * tb[r][ml] with row r = E - kExpTabE0 + 32 s
-// (each entry the float64 nearest to its exact value; the product is within 2
-// ulps of e^x).  The index arithmetic runs on both halves of a word at once
-// (packed 16-bit operations).  Exponents are clamped to the tables' rows, and
-// emin keeps the smallest one seen: a wave holding an x' below 2^-22 in
-// magnitude (zero among them) sums against its maximum instead.  x' below
-// about -648 is clamped there as in exp_sum0 (e^-648 is a normal float64);
-// rows up to |x'| < 1024 hold e^x' of up to +inf, for x' that put the wave on
-// the sum against its maximum anyway.
-template <int W0, int W1>
-__device__ __forceinline__ double exp_sum0_tab(SegVals<bf16_t>& x, const double* ta, const double* tb, double acc,
-                                               v2u16& emin) {
-  const v2u16 e_lo = {kExpTabE0, kExpTabE0};
-  const v2u16 e_hi = {kExpTabE0 + kExpTabNE - 1, kExpTabE0 + kExpTabNE - 1};
-  // rows are addressed from exponent kExpTabE0: offsets start at kExpTabE0 rows
-  const char* pa = reinterpret_cast<const char*>(ta) - kExpTabE0 * 64;
-  const char* pb = reinterpret_cast<const char*>(tb) - kExpTabE0 * 128;
-#pragma unroll
-  for (int i = W0; i < W1; ++i) {
-    // two words (eight table reads) at a time, each pair's arguments chained to
-    // the previous pair's sum, so that the compiler does not issue every read
-    // at once (which spills)
-    if (((i - W0) & 1) == 0) asm volatile("" : "+v"(acc), "+v"(x.w[i]), "+v"(x.w[i + 1]));
-    const uint32_t c = clamp_low16<bf16_t>(x.w[i]);
-    const v2u16 e = __builtin_bit_cast(v2u16, (c >> 7) & 0x00ff00ffu);
-    emin = __builtin_elementwise_min(emin, e);
-    const v2u16 row = __builtin_elementwise_min(__builtin_elementwise_max(e, e_lo), e_hi) +
-                      __builtin_bit_cast(v2u16, (c >> 10) & 0x00200020u);   // + 32 for x' < 0
-    const v2u16 oa = row * (v2u16){64, 64} + __builtin_bit_cast(v2u16, (c >> 1) & 0x00380038u);
-    const v2u16 ob = row * (v2u16){128, 128} + __builtin_bit_cast(v2u16, (c << 3) & 0x00780078u);
-    const double a0 = *reinterpret_cast<const double*>(pa + oa.x);
-    const double a1 = *reinterpret_cast<const double*>(pa + oa.y);
-    const double b0 = *reinterpret_cast<const double*>(pb + ob.x);
-    const double b1 = *reinterpret_cast<const double*>(pb + ob.y);
-    acc += a0 * b0;
-    acc += a1 * b1;
-  }
-  return acc;
-}
-
 // The float64 sum of e^(x' - mw) over a thread's logits given as 16-bit keys
 // (0 when mw is -inf): the sum of a wave whose largest x', mw, lies outside
 // [-600, 600].
@@ -1337,10 +1292,6 @@ __device__ __forceinline__ double exp_sum_keys(const uint32_t (&kp)[NW], float m
 // instantiation keeps the common path free of the scaling code).
 template <typename T, bool SCALED>
 __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_kernel(FusedTopkArgs a) {
-  // unscaled bf16 logits: e^x' from the factor tables (exp_sum0_tab)
-  constexpr bool kTab = __is_same(T, bf16_t) && !SCALED;
-  constexpr int kTabA = sizeof(kExpTabA) / sizeof(double), kTabB = sizeof(kExpTabB) / sizeof(double);
-  __shared__ double etab[kTab ? kTabA + kTabB : 1];
   __shared__ double tab[256];
   __shared__ float wmax[4];
   __shared__ double wsum[4];
@@ -1383,9 +1334,7 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
   }
   if (tid == 0) ncand = 0;
   exp_table256_init(tab);
-  if constexpr (kTab)
-    for (int i = tid; i < kTabA + kTabB; i += kTopkThreads) etab[i] = i < kTabA ? kExpTabA[i] : kExpTabB[i - kTabA];
-  __syncthreads();                                     // the exp tables, ncand
+  __syncthreads();                                     // the exp table, ncand
   for (int i = i0; i < i1; ++i) {
     const int u = col + i * C;
     const int un = i + 1 < i1 ? u + C : units;
@@ -1393,19 +1342,12 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     const int b = s * seg_len;
     // the sum against 0, a 16-byte chunk (4 words) at a time as it lands
     double acc = 0.0;
-    v2u16 emin = {0xffff, 0xffff};
-    if constexpr (kTab) {
-      acc = exp_sum0_tab<0, 4>(x, etab, etab + kTabA, acc, emin);
-      acc = exp_sum0_tab<4, 8>(x, etab, etab + kTabA, acc, emin);
-      acc = exp_sum0_tab<8, 12>(x, etab, etab + kTabA, acc, emin);
-    } else {
-      if constexpr (SCALED) temp16<T>(a.ts, x, 0, 4);
-      acc = exp_sum0<T, 0, 4>(x, tab, acc);
-      if constexpr (SCALED) temp16<T>(a.ts, x, 4, 8);
-      acc = exp_sum0<T, 4, 8>(x, tab, acc);
-      if constexpr (SCALED) temp16<T>(a.ts, x, 8, 12);
-      acc = exp_sum0<T, 8, 12>(x, tab, acc);
-    }
+    if constexpr (SCALED) temp16<T>(a.ts, x, 0, 4);
+    acc = exp_sum0<T, 0, 4>(x, tab, acc);
+    if constexpr (SCALED) temp16<T>(a.ts, x, 4, 8);
+    acc = exp_sum0<T, 4, 8>(x, tab, acc);
+    if constexpr (SCALED) temp16<T>(a.ts, x, 8, 12);
+    acc = exp_sum0<T, 8, 12>(x, tab, acc);
     // the last chunk has landed (the asm reads it): the next unit's loads
     // (issued with this unit's they would share the memory system and both
     // arrive late together)
@@ -1414,12 +1356,8 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
       const int rn = un / segs, bn = (un - rn * segs) * seg_len;
       load_raw16<T>(logits + (int64_t)rn * a.row_stride + bn, min(vocab, bn + seg_len) - bn, xn);
     }
-    if constexpr (kTab) {
-      acc = exp_sum0_tab<12, 16>(x, etab, etab + kTabA, acc, emin);
-    } else {
-      if constexpr (SCALED) temp16<T>(a.ts, x, 12, 16);
-      acc = exp_sum0<T, 12, 16>(x, tab, acc);
-    }
+    if constexpr (SCALED) temp16<T>(a.ts, x, 12, 16);
+    acc = exp_sum0<T, 12, 16>(x, tab, acc);
     // 16-bit order keys in place of the logits
     v2u16 km2 = {0, 0};
 #pragma unroll
@@ -1430,9 +1368,7 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     const uint32_t kmax = max((uint32_t)km2.x, (uint32_t)km2.y);
     const uint32_t wk = lane63(wave_scan_max(kmax));
     const float mw = value_of_key16<T>(wk);
-    // (a wave holding an x' below the factor tables' exponents: against its max too)
-    const bool slow = wk > khi || wk < klo ||
-                      (kTab && __builtin_amdgcn_ballot_w64(min((uint32_t)emin.x, (uint32_t)emin.y) < kExpTabE0) != 0);
+    const bool slow = wk > khi || wk < klo;              // wave-uniform
     if (slow) acc = exp_sum_keys<T, kWords>(x.w, mw, tab);
     // the wave's kw-th largest per-thread maximum, bit by bit
     const int kw = (k + 3) >> 2;
@@ -1488,14 +1424,11 @@ __global__ __launch_bounds__(kTopkThreads, kUnitWavesPerSimd) void topk_units16_
     const int64_t rs = (int64_t)r * segs + s;
     for (int i = tid; i < min(total, cap); i += kTopkThreads) a.cand[rs * cap + i] = lc[i];
     if (tid == 0) {
-      // the waves' sums against one reference: 0, or the unit's max m when a
-      // wave summed against a positive max (one above 600, or a wave holding a
-      // value below the factor tables' exponents) or every wave against its
-      // own; the unit records which (bit 31 of its bound word: against m)
+      // the waves' sums against one reference: 0, or the unit's max when a wave
+      // summed against a max above 600 (or every wave against its own)
       float ref = -INFINITY;
 #pragma unroll
       for (int q = 0; q < 4; ++q) ref = fmaxf(ref, wslow[q] ? wmax[q] : 0.0f);
-      if (ref != 0.0f) ref = m;
       double sum = 0.0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
