@@ -1387,14 +1387,20 @@ int stream_plan(const std::vector<Group>& groups, const be_level* levels, int nu
   // us per launch, config 2 21.9 vs 22.7, 8 chunks per query); with few it is
   // a latency-bound stub and the tail role wins (e2e step 24.95 vs 23.0, 1.5
   // per query; config 5 205.3 vs 202.1, 1.2; in a fixed layout the e2e step
-  // 25.1 vs 23.3).  So by default: the tail role when a plan with streamed
-  // groups has at most kTailRoleChunks per query.  BE_PLAN_TAIL_ROLE forces
-  // it, BE_PLAN_NO_TAIL_ROLE forbids it.
-  int64_t tail_cost = 0, tail_chunks = 0;
+  // 25.1 vs 23.3).  When the tail chunks are as much work as most of the
+  // streamed tiles, running them beside the stream rather than after it wins
+  // too (config 3: tail chunks 0.82 of the streamed tokens, 25.25 vs 26.0 us;
+  // north-star and config 2, 0.5 of them: 52.1 vs 49.9 and 23.1 vs 22.2).  So
+  // by default: the tail role when a plan with streamed groups has at most
+  // kTailRoleChunks per query, or tail work of at least two thirds of its
+  // streamed tiles' (in the planner's units: 1 per chunk and KV head, 4 per
+  // 64-token tile).  BE_PLAN_TAIL_ROLE forces it, BE_PLAN_NO_TAIL_ROLE forbids it.
+  int64_t tail_cost = 0, tail_chunks = 0, tile_cost = 0;
   for (int qi = 0; qi < num_queries; ++qi) tail_chunks += n_tails_of(qi);
   tail_cost = tail_chunks * hkv * kTailUnit;
+  for (const Task& t : tasks) tile_cost += 4 * (int64_t)t.tiles;
   const bool auto_tail = !tasks.empty() && !(flags & BE_PLAN_NO_TAIL_ROLE) &&
-                         tail_chunks <= (int64_t)kTailRoleChunks * num_queries;
+                         (tail_chunks <= (int64_t)kTailRoleChunks * num_queries || 3 * tail_cost >= 2 * tile_cost);
   const bool tail_role = tail_cost > 0 && ((flags & BE_PLAN_TAIL_ROLE) || auto_tail) && (tasks.empty() || W >= 2);
   int W_t = 0;
   if (tail_role) {

@@ -13,6 +13,7 @@ from tests.conftest import ROOT
 
 HEADER = os.path.join(ROOT, "include", "beam_engine_amd.h")
 TILE = 4      # BE_PLAN_TILE_KERNEL
+_NO_TAIL_ROLE = 2048   # BE_PLAN_NO_TAIL_ROLE
 
 
 def declared_functions():
@@ -326,14 +327,16 @@ def test_stream_plan_cascade_coverage_and_records():
               ([0, 1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 3, 4, 5, 6, 7, 8, 9],
                [10, 11, 12, 13, 14, 15, 16, 17, 18], [1, 1, 1, 0, 0, 3, 3, 3])]
     # (the streaming kernel takes page sizes that are multiples of 16)
-    for flags in (0, 8, 16):
+    # tail chunks in the merge kernel (no tail role), no tail pass, the tail role
+    for flags in (_NO_TAIL_ROLE, 8, 16, 0):
         rc, info, buf, _lib, L = plan(levels, hq=8, hkv=2, page=16, num_pages=19, flags=flags)
         assert rc == 0, L.be_last_error()
         check_stream_plan(levels, 8, 8, 2, 16, info, buf)
         valid = 3 * 16 + 1 + 3 * (16 + 1) + (1 + 16 + 1 + 1 + 0 + 0 + 3 + 3 + 3)
         assert info.kv_bytes == valid * 2 * 128 * 2 * 2
         assert (info.num_tails > 0) == (flags != 8)
-        assert (info.num_tail_items > 0) == (flags == 16)
+        # by default the tail role too: here the tail chunks outweigh the streamed tiles
+        assert (info.num_tail_items > 0) == (flags in (16, 0))
         assert buf[4] == info.num_tail_items                     # header: tail item count
     rc, info, *_ = plan(levels, hq=8, hkv=2, page=4, num_pages=19)
     assert rc == 0 and info.kernel == 1                 # page 4: the tile kernel
