@@ -22,8 +22,8 @@ Here:
   and lays the decomposition out as levels of shared passes, planned once for
   every layer of the step (``be_attn_plan``).  Each candidate attends every
   token of its root-to-leaf path once -- the tokens its ``req_to_token`` row
-  lists, its newest one included -- which is FastTree's intent
-  (SURVEY B.5); the reference's own metadata reads ``seqlen`` as a node's own
+  lists, its newest one included -- which is FastTree's intent (every
+  token of the path once); the reference's own metadata reads ``seqlen`` as a node's own
   length and starts only from node 0, which breaks deeper trees and forests.
 * ``fasttree_decode(q, paged_kv_cache, o, metadata)`` runs the plan on the
   layer's paged cache (``kv_cache_at_layer[layer]``) in place: no K / V

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark driver (one JSON line on stdout).
 
-Default workload ``e2e`` (harness in ``bench_e2e.py``):
+Default workload ``e2e`` (benchmark config 4, harness in ``bench_e2e.py``):
 end-to-end batched beam search on a random-init Llama-3-8B-shaped decoder
 (8 requests x beam 16, 1024-token prompts, 256 generated tokens); value =
 beam-decode tokens/s = 128 candidate tokens per step / step time over
@@ -353,7 +353,7 @@ def read_ceiling_workload(args):
 # ---------------------------------------------------------------------- CPU baseline
 def cpu_baseline_attention(wl, alg_bytes):
     """The CPU restatement (torch float32 paged gather, per-level softmax
-    attention, log-sum-exp merge: BASELINE's CPU plan) on one layer of the
+    attention, log-sum-exp merge: the reference's CPU path) on one layer of the
     same workload, in GB/s of the same algorithmic bytes."""
     import torch
     from bench_e2e import cpu_model

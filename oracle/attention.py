@@ -200,7 +200,7 @@ def reference_attention_dense(q, k, v, sm_scale: float):
 def cascade_attention_torch(q, kv_layer, qo_indptr_arr, kv_indptr_arr, kv_indices_arr, last_page_len_arr,
                             page_size: int, sm_scale: float | None = None):
     """The same multi-level cascade decode attention in torch float32 on the
-    CPU -- the form BASELINE's CPU plan times (paged gather, per-level softmax
+    CPU -- the form the bench's CPU baseline times (paged gather, per-level softmax
     attention with (o, lse), log-sum-exp merge), using torch's threads.
 
     ``q [N, Hq, D]`` and ``kv_layer [P, 2, page, Hkv, D]`` are CPU tensors

@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE configurations' full sizes (bf16, page 16):
+"""GPU parity at the benchmark configurations' full sizes (bf16, page 16):
 
 * the north-star shape (8 requests x beam 16, 32/8 heads, 4096-token prefix,
   128-token suffixes) and config 5 (2 x 64 beams, 64/8 heads, 32768-token

@@ -3,8 +3,8 @@ entry points: ``BeamState.get_fasttree_input()`` (beam_state.py:566-633) ->
 ``prepare_fasttree_metadata_for_paged_cache`` (preparation.py:11-225) ->
 ``fasttree_decode`` (kernel.py:288-348) per layer.  Every candidate's output
 must equal the float64 oracle's attention over the slots its ``req_to_token``
-row lists (its whole root-to-leaf path, the newest token included: SURVEY
-B.5), for multi-request forests grown by random selections (branch points at
+row lists (its whole root-to-leaf path once, the newest token included),
+for multi-request forests grown by random selections (branch points at
 every depth, dead branches, private suffixes of many lengths).
 
 Tolerance (bf16 storage against the float64 oracle): 2e-2 relative, 1e-2
