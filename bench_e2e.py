@@ -1,4 +1,4 @@
-"""End-to-end beam-search benchmark harness, used by bench.py.
+"""End-to-end beam-search benchmark harness (benchmark config 4), used by bench.py.
 
 Random-init Llama-3-8B-shaped decoder (32 layers, hidden 4096, 32/8 heads,
 head_dim 128, FFN 14336, vocab 128256, bf16 weights ~ N(0, 0.02)), 8 requests
@@ -236,7 +236,7 @@ def cpu_model() -> str:
 
 def cpu_baseline_e2e(gen: BatchedBeamSearch, budget_s: float = 25.0):
     """The CPU restatement (oracle/) of the hot path on one decode step at the
-    generation's final beam state, in the form BASELINE's CPU plan names:
+    generation's final beam state, in the form the reference's CPU path takes:
     torch float32 cascade attention on the host for every layer (the state's
     real pages and index arrays; layer 0's K/V stand in for each layer's, with
     distinct queries), the cascade metadata restatement, and the vanilla
