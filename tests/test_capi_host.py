@@ -730,3 +730,25 @@ def test_generator_rejects_out_of_vocabulary_token_ids():
     gen._check_tokens(np.array([0, 99]))
     with pytest.raises(ValueError, match="token id 100"):
         gen._check_tokens(np.array([5, 100, 7]))
+
+
+@pytest.mark.parametrize("name, tail_role", [("e2e_step", True), ("config2", False), ("config3", True),
+                                             ("north_star", False), ("config5", True)])
+def test_stream_plan_tail_role_default_on_benchmark_shapes(name, tail_role):
+    """The planner's default for who attends the tail chunks, at the benchmark
+    shapes: tail-role workgroups of the streaming launch when the chunks
+    average at most 2 per query (e2e step 1.5, config 5 1.2) or are at least
+    two thirds of the streamed tiles' work (config 3: 14 chunks per query, 0.82
+    of it); the tail-and-merge kernel otherwise (config 2 and the north-star:
+    8 per query, half of it)."""
+    from beam_engine_amd import workloads
+    wl = getattr(workloads, name)()
+    levels = [tuple(wl.levels[j][i] for j in range(4)) for i in range(len(wl.levels[0]))]
+    rc, info, buf, _lib, L = plan(levels, nq=wl.num_queries, hq=wl.hq, hkv=wl.hkv, page=wl.page,
+                                  num_pages=wl.num_pages, cus=256)
+    assert rc == 0, L.be_last_error()
+    wg, segs, recs, rslots, tails = decode_stream(info, buf)
+    assert (info.num_tail_items > 0) == tail_role
+    assert ((wg[:, 3] == 8).any()) == tail_role              # class 8: tail-role workgroups
+    if tail_role:
+        assert (recs[:, 5] == 0).all()                 # the merge kernel only merges
