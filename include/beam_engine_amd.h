@@ -157,7 +157,8 @@ typedef struct be_level {
 #define BE_PLAN_TAIL_ROLE 16     /* streaming kernel: attend tail chunks in tail-role
                                     workgroups of the persistent kernel rather than in the
                                     merge kernel, whatever their count (by default: when a
-                                    plan with streamed groups has at most 2 per query)      */
+                                    plan with streamed groups has at most 2 per query, or
+                                    tail work of at least two thirds of its streamed tiles') */
 #define BE_PLAN_NO_REGS 32       /* streaming kernel: the direct-load loop whatever the runs'
                                     lengths and roles (no register-staged loop; the 256-row
                                     wide roles otherwise stage through registers)           */
@@ -174,8 +175,8 @@ typedef struct be_level {
                                     kernel) whenever it applies                             */
 #define BE_PLAN_NO_ROWS 512      /* never the row-block kernel                               */
 #define BE_PLAN_NO_WIDE256 1024  /* streaming kernel: wide roles on 128-row segments only    */
-#define BE_PLAN_NO_TAIL_ROLE 2048 /* streaming kernel: tail chunks always in the merge kernel */
                                  /* (no 256-row segments for groups of >= 256 rows)         */
+#define BE_PLAN_NO_TAIL_ROLE 2048 /* streaming kernel: tail chunks always in the merge kernel */
 
 /* Fixed-capacity plan layout (for HIP-graph capture): every region of the
  * device plan sits at an offset that depends only on these capacities, the
